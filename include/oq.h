@@ -1,0 +1,165 @@
+/*
+ * oq.h -- C ABI of the MI355X (gfx950) quantized-weight matrix library (liboq.so).
+ *
+ * Plain pointers and sizes only.  "dev" pointers are device (HBM) addresses; "host" pointers
+ * are ordinary host memory (an mmap'd GGUF payload is fine).  Every entry point returns an
+ * oq_status; the text of the last failure on a context is available from oq_last_error().
+ *
+ * Each declaration names the reference interface it replaces (paths are relative to the
+ * reference engine's source tree).  The reference's quantized path is a set of free
+ * functions in oracle::backend::cpu (include/oracle/backend/cpu/quantized_reference.hpp:10-27)
+ * over oracle::model::GgufTensorView (include/oracle/model/mapped_gguf.hpp:18-41) and the
+ * GGML layout registry (include/oracle/model/ggml_type.hpp:9-24).  The C++ adapter in
+ * oracle_amd/host/ maps those signatures, and their exceptions, onto this ABI.
+ *
+ * Threading: one oq_context owns one HIP stream on one device and is not thread-safe.
+ * Weights are immutable after upload and may be used from any context on the same device.
+ * All compute entry points are asynchronous on the context's stream; oq_synchronize() waits.
+ */
+#ifndef OQ_H
+#define OQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum oq_status {
+    OQ_OK = 0,
+    OQ_INVALID_ARGUMENT = -1, /* reference: std::invalid_argument */
+    OQ_OUT_OF_RANGE = -2,     /* reference: std::out_of_range */
+    OQ_OVERFLOW = -3,         /* reference: std::overflow_error */
+    OQ_UNSUPPORTED_TYPE = -4, /* reference: std::runtime_error("unsupported GGML tensor type") */
+    OQ_DEVICE_ERROR = -5,     /* HIP runtime failure */
+    OQ_OUT_OF_MEMORY = -6,    /* device allocation failure */
+    OQ_LOGIC_ERROR = -7       /* reference: std::logic_error (bad row geometry) */
+} oq_status;
+
+/* GGML type ids, as registered in the reference (src/model/ggml_type.cpp:12-54) */
+enum {
+    OQ_TYPE_F32 = 0,
+    OQ_TYPE_F16 = 1,
+    OQ_TYPE_Q8_0 = 8,
+    OQ_TYPE_Q4_K = 12,
+    OQ_TYPE_Q5_K = 13,
+    OQ_TYPE_Q6_K = 14,
+    OQ_TYPE_Q8_K = 15,
+    OQ_TYPE_BF16 = 30
+};
+
+typedef struct oq_context oq_context;
+typedef struct oq_weight oq_weight;
+typedef struct oq_graph oq_graph;
+
+/* ------------------------------------------------------------------ registry */
+
+/* Replaces oracle::model::ggml_type_layout (src/model/ggml_type.cpp:62-75).  Returns
+   OQ_UNSUPPORTED_TYPE for unknown, deprecated and removed ids (the reference returns nullptr).
+   Any output pointer may be NULL.  *name points at static storage. */
+int oq_type_layout(uint32_t type, uint64_t* block_elements, uint64_t* bytes_per_block,
+                   int* quantized, const char** name);
+
+/* Replaces oracle::model::ggml_row_byte_size (src/model/ggml_type.cpp:77-94): unknown type ->
+   OQ_UNSUPPORTED_TYPE, zero elements -> OQ_INVALID_ARGUMENT, ragged row -> OQ_UNSUPPORTED_TYPE
+   (the reference throws std::runtime_error for both), overflow -> OQ_OVERFLOW. */
+int oq_row_byte_size(uint64_t row_elements, uint32_t type, uint64_t* out);
+
+/* 1 if the device path decodes/multiplies this type: f32, f16, bf16, q8_0, q4_K, q5_K, q6_K.
+   This is the reference decoder whitelist (src/model/storage_decode.cpp:192-193) plus q4_K. */
+int oq_type_supported(uint32_t type);
+
+/* ------------------------------------------------------------------ context */
+
+/* No reference counterpart (the reference is CPU-only; backend choice by name happens in
+   src/runtime/engine.cpp:62-72).  Creates a context on HIP device `device` with its own stream. */
+int oq_context_create(int device, oq_context** out);
+void oq_context_destroy(oq_context* ctx);
+/* Text of the last failure on ctx (or of the last failed oq_context_create when ctx is NULL). */
+const char* oq_last_error(const oq_context* ctx);
+int oq_synchronize(oq_context* ctx);
+/* The context's hipStream_t, for callers that interleave their own work. */
+void* oq_context_stream(oq_context* ctx);
+
+/* Device memory helpers (so callers need no other GPU runtime). */
+int oq_device_alloc(oq_context* ctx, uint64_t bytes, void** out_dev);
+int oq_device_free(oq_context* ctx, void* dev);
+int oq_copy_to_device(oq_context* ctx, void* dst_dev, const void* src_host, uint64_t bytes);
+int oq_copy_to_host(oq_context* ctx, void* dst_host, const void* src_dev, uint64_t bytes);
+int oq_copy_device(oq_context* ctx, void* dst_dev, const void* src_dev, uint64_t bytes);
+
+/* ------------------------------------------------------------------ weights */
+
+/* One-time upload of a rank-2 GGML tensor: ne0 = K (contiguous, GGUF dimensions[0]),
+   ne1 = N rows (dimensions[1]), `host_bytes` = GgufTensorView::bytes() (zero-copy: the mmap
+   pointer is copied straight to HBM).  Validates exactly what reference_storage_matvec
+   validates before its loop (src/backend/cpu/quantized_reference.cpp:134-153) plus the decoder
+   whitelist (src/model/storage_decode.cpp:192-193, extended by q4_K).  Q8_0 and Q6_K rows are
+   re-laid out on the device into aligned planes; the values they decode to are unchanged. */
+int oq_weight_upload(oq_context* ctx, uint32_t type, uint64_t ne0, uint64_t ne1,
+                     const void* host_bytes, uint64_t nbytes, oq_weight** out);
+/* Same, from bytes already in device memory (e.g. a whole GGUF payload uploaded once). */
+int oq_weight_upload_device(oq_context* ctx, uint32_t type, uint64_t ne0, uint64_t ne1,
+                            const void* dev_bytes, uint64_t nbytes, oq_weight** out);
+void oq_weight_release(oq_weight* w);
+int oq_weight_info(const oq_weight* w, uint32_t* type, uint64_t* ne0, uint64_t* ne1,
+                   uint64_t* device_bytes);
+
+/* ------------------------------------------------------------------ decode */
+
+/* Replaces oracle::backend::cpu::reference_decode_mapped_tensor
+   (src/backend/cpu/quantized_reference.cpp:85-105) and, row by row, oracle::model::
+   decode_storage_row (src/model/storage_decode.cpp:244-294): rows [row0, row0+nrows) of w
+   decoded to F32 into out_dev[nrows][ne0].  Bit-identical to the reference's decode.
+   row0 + nrows > ne1 -> OQ_OUT_OF_RANGE (make_storage_row_view(tensor,row),
+   src/model/storage_decode.cpp:223-225). */
+int oq_dequantize_rows(oq_context* ctx, const oq_weight* w, uint64_t row0, uint64_t nrows,
+                       float* out_dev);
+
+/* ------------------------------------------------------------------ activations */
+
+/* F32 -> GGML block_q8_K {f32 d; i8 qs[256]; i16 bsums[16]} (292 B per 256 values).  The
+   reference registers the layout only (src/model/ggml_type.cpp:28); this is GGML's
+   quantize_row_q8_K: bit-identical to it for finite inputs (an all-zero block gets d = 0 and
+   zero bsums).  x_dev is [m][k], q8k_dev receives m*k/256 blocks.  k % 256 != 0 ->
+   OQ_INVALID_ARGUMENT. */
+int oq_quantize_q8k(oq_context* ctx, const float* x_dev, uint64_t m, uint64_t k, void* q8k_dev);
+
+/* ------------------------------------------------------------------ products */
+
+/* Replaces oracle::backend::cpu::reference_mapped_tensor_matvec / reference_storage_matvec
+   (src/backend/cpu/quantized_reference.cpp:107-162): y_dev[n] = row_n(w) . x for n < ne1.
+   x_dev holds ne0 F32 values, y_dev ne1.  q4_K / q5_K / q6_K weights quantize x to Q8_K on the
+   device and use integer dots (GGML vec_dot_qX_K_q8_K semantics); q8_0 and plain types use the
+   F32 activation directly.  Result within 1e-4 * sum_k |w_k x_k| of the reference's F32 dot. */
+int oq_matvec(oq_context* ctx, const oq_weight* w, const float* x_dev, float* y_dev);
+
+/* As oq_matvec for K-quant weights, with activations already in Q8_K blocks (ne0/256 blocks). */
+int oq_matvec_q8k(oq_context* ctx, const oq_weight* w, const void* q8k_dev, float* y_dev);
+
+/* M activation rows: x_dev [m][ne0] -> y_dev [m][ne1].  The reference has no M>1 kernel; its
+   multi-token evaluation is M independent matvecs (src/runtime/qwen35_target_multi.cpp:14-25),
+   which is the semantics here.  Small m streams the weights once with register reuse;
+   m >= 16 on q4_K uses matrix cores (fp16 MFMA on exact small-integer tiles). */
+int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x_dev, float* y_dev);
+int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q8k_dev,
+                  float* y_dev);
+
+/* ------------------------------------------------------------------ timing / graphs */
+
+/* HIP events on the context's stream, for timing the kernels launched there. */
+int oq_timer_start(oq_context* ctx);
+int oq_timer_stop(oq_context* ctx, float* elapsed_ms); /* waits for the stop event */
+
+/* Capture every oq_* launch on ctx between begin and end into a replayable HIP graph. */
+int oq_capture_begin(oq_context* ctx);
+int oq_capture_end(oq_context* ctx, oq_graph** out);
+int oq_graph_launch(oq_context* ctx, oq_graph* g);
+void oq_graph_destroy(oq_graph* g);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

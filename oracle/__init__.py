@@ -1,0 +1,252 @@
+"""ORACLE -- test infrastructure, not product code.
+
+ctypes view of the CPU restatement (liboracle.so, built from oracle.c) and, where it was built
+from the reference's own sources, of the reference's quantized path (_ref/libref.so).  Only the
+tests, the smoke check and the CPU-baseline leg of the benchmark use this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_LIB = HERE / "liboracle.so"
+REF_LIB = HERE / "_ref" / "libref.so"
+REFERENCE_TREE = Path("/root/reference")
+
+_P = C.c_void_p
+_U64 = C.c_uint64
+_U32 = C.c_uint32
+_F = C.POINTER(C.c_float)
+_D = C.POINTER(C.c_double)
+
+_ORC_SIGS = [
+    ("orc_last_error", C.c_char_p, []),
+    ("orc_type_layout", C.c_int, [_U32, C.POINTER(_U64), C.POINTER(_U64), C.POINTER(C.c_int), C.POINTER(C.c_char_p)]),
+    ("orc_row_byte_size", C.c_int, [_U64, _U32, C.POINTER(_U64)]),
+    ("orc_f16_to_f32", C.c_float, [C.c_uint16]),
+    ("orc_bf16_to_f32", C.c_float, [C.c_uint16]),
+    ("orc_check_row", C.c_int, [_U32, _U64, _U64]),
+    ("orc_decode_row", C.c_int, [_U32, _U64, _P, _U64, _P]),
+    ("orc_storage_dot", C.c_int, [_U32, _U64, _P, _U64, _P, _F]),
+    ("orc_storage_matvec", C.c_int, [_U32, _U64, _U64, _P, _U64, _P, _P]),
+    ("orc_storage_matvec_mt", C.c_int, [_U32, _U64, _U64, _P, _U64, _P, _P, C.c_int]),
+    ("orc_storage_matmul_mt", C.c_int, [_U32, _U64, _U64, _P, _U64, _U64, _P, _P, C.c_int]),
+    ("orc_storage_dot_stats", C.c_int, [_U32, _U64, _P, _U64, _P, _D, _D]),
+    ("orc_storage_matvec_stats", C.c_int, [_U32, _U64, _U64, _P, _U64, _P, _P, _P, C.c_int]),
+    ("orc_quantize_row_q8_k", C.c_int, [_P, _U64, _P]),
+    ("orc_dequantize_row_q8_k", C.c_int, [_P, _U64, _P]),
+    ("orc_vec_dot_q8_k", C.c_int, [_U32, _U64, _P, _P, _F]),
+    ("orc_fnv1a64", _U64, [_P, _U64]),
+]
+
+_REF_SIGS = [
+    ("ref_last_error", C.c_char_p, []),
+    ("ref_f16_to_f32", C.c_float, [C.c_uint16]),
+    ("ref_bf16_to_f32", C.c_float, [C.c_uint16]),
+    ("ref_type_layout", C.c_int, [_U32, C.POINTER(_U64), C.POINTER(_U64), C.POINTER(C.c_int), C.c_char_p, C.c_int]),
+    ("ref_row_byte_size", C.c_int, [_U64, _U32, C.POINTER(_U64)]),
+    ("ref_decode_row", C.c_int, [_U32, _U64, _P, _U64, _P, _U64]),
+    ("ref_storage_dot", C.c_int, [_U32, _U64, _P, _U64, _P, _U64, _F]),
+    ("ref_storage_matvec", C.c_int, [_U32, _U64, _U64, _P, _U64, _P, _U64, _P, _U64]),
+    ("ref_mapped_tensor_matvec", C.c_int, [_U32, _U64, _U64, _P, _U64, _P, _U64, _P, _U64]),
+    ("ref_storage_matvec_rows", C.c_int, [_U32, _U64, _P, _U64, _U64, _U64, _P, _P]),
+]
+
+
+class OracleError(Exception):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+def build(reference: bool = True) -> None:
+    """Compile liboracle.so and, when the reference tree is present, _ref/libref.so."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "all"], check=True)
+    if reference and REFERENCE_TREE.exists():
+        subprocess.run(["make", "-s", "-C", str(HERE), "ref", f"REF={REFERENCE_TREE}"], check=True)
+
+
+def _bind(path: Path, sigs) -> C.CDLL:
+    lib = C.CDLL(str(path))
+    for name, res, args in sigs:
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_orc = None
+_ref = None
+
+
+def lib() -> C.CDLL:
+    global _orc
+    if _orc is None:
+        if not ORACLE_LIB.exists():
+            build(reference=False)
+        _orc = _bind(ORACLE_LIB, _ORC_SIGS)
+    return _orc
+
+
+def ref_available() -> bool:
+    return REF_LIB.exists()
+
+
+def ref() -> C.CDLL:
+    global _ref
+    if _ref is None:
+        if not REF_LIB.exists():
+            raise FileNotFoundError(f"{REF_LIB} not built (needs the reference tree at build time)")
+        _ref = _bind(REF_LIB, _REF_SIGS)
+    return _ref
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data if a.size else None
+
+
+def _chk(rc: int, which: C.CDLL, err_fn: str) -> None:
+    if rc != 0:
+        raise OracleError(rc, getattr(which, err_fn)().decode(errors="replace"))
+
+
+# ---------------------------------------------------------------- restatement wrappers
+
+def decode_row(type_id: int, n: int, data: np.ndarray) -> np.ndarray:
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    _chk(lib().orc_decode_row(type_id, n, _ptr(d), d.nbytes, _ptr(out)), lib(), "orc_last_error")
+    return out
+
+
+def decode_matrix(type_id: int, cols: int, rows: int, data: np.ndarray) -> np.ndarray:
+    d = np.ascontiguousarray(data, dtype=np.uint8).reshape(rows, -1)
+    return np.stack([decode_row(type_id, cols, d[r]) for r in range(rows)])
+
+
+def storage_dot(type_id: int, n: int, data: np.ndarray, x: np.ndarray) -> float:
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    out = C.c_float()
+    _chk(lib().orc_storage_dot(type_id, n, _ptr(d), d.nbytes, _ptr(xv), C.byref(out)), lib(), "orc_last_error")
+    return out.value
+
+
+def storage_matvec(type_id: int, rows: int, cols: int, data: np.ndarray, x: np.ndarray,
+                   threads: int = 1) -> np.ndarray:
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(rows, dtype=np.float32)
+    if threads <= 1:
+        rc = lib().orc_storage_matvec(type_id, rows, cols, _ptr(d), d.nbytes, _ptr(xv), _ptr(y))
+    else:
+        rc = lib().orc_storage_matvec_mt(type_id, rows, cols, _ptr(d), d.nbytes, _ptr(xv), _ptr(y), threads)
+    _chk(rc, lib(), "orc_last_error")
+    return y
+
+
+def storage_matmul(type_id: int, rows: int, cols: int, data: np.ndarray, x: np.ndarray,
+                   threads: int = 1) -> np.ndarray:
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    m = xv.size // cols
+    y = np.empty((m, rows), dtype=np.float32)
+    _chk(lib().orc_storage_matmul_mt(type_id, rows, cols, _ptr(d), d.nbytes, m, _ptr(xv), _ptr(y), threads),
+         lib(), "orc_last_error")
+    return y
+
+
+def matvec_stats(type_id: int, rows: int, cols: int, data: np.ndarray, x: np.ndarray,
+                 threads: int = 8) -> tuple[np.ndarray, np.ndarray]:
+    """(double-precision dot, sum |w x|) per row, the tolerance normaliser."""
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    dot = np.empty(rows, dtype=np.float64)
+    ab = np.empty(rows, dtype=np.float64)
+    _chk(lib().orc_storage_matvec_stats(type_id, rows, cols, _ptr(d), d.nbytes, _ptr(xv), _ptr(dot), _ptr(ab),
+                                        threads), lib(), "orc_last_error")
+    return dot, ab
+
+
+def quantize_q8k(x: np.ndarray) -> np.ndarray:
+    xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(xv.size // 256 * 292, dtype=np.uint8)
+    _chk(lib().orc_quantize_row_q8_k(_ptr(xv), xv.size, _ptr(out)), lib(), "orc_last_error")
+    return out
+
+
+def dequantize_q8k(blocks: np.ndarray, k: int) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.empty(k, dtype=np.float32)
+    _chk(lib().orc_dequantize_row_q8_k(_ptr(b), k, _ptr(out)), lib(), "orc_last_error")
+    return out
+
+
+def vec_dot_q8k(type_id: int, k: int, wrow: np.ndarray, q8k: np.ndarray) -> float:
+    w = np.ascontiguousarray(wrow, dtype=np.uint8)
+    q = np.ascontiguousarray(q8k, dtype=np.uint8)
+    out = C.c_float()
+    _chk(lib().orc_vec_dot_q8_k(type_id, k, _ptr(w), _ptr(q), C.byref(out)), lib(), "orc_last_error")
+    return out.value
+
+
+def fnv1a64(data) -> int:
+    a = np.ascontiguousarray(np.frombuffer(memoryview(data).cast("B"), dtype=np.uint8))
+    return int(lib().orc_fnv1a64(_ptr(a), a.nbytes))
+
+
+def f16_to_f32(bits: int) -> float:
+    return lib().orc_f16_to_f32(bits)
+
+
+def check_row(type_id: int, n: int, nbytes: int) -> int:
+    return lib().orc_check_row(type_id, n, nbytes)
+
+
+def row_byte_size(n: int, type_id: int) -> int:
+    out = C.c_uint64()
+    _chk(lib().orc_row_byte_size(n, type_id, C.byref(out)), lib(), "orc_last_error")
+    return out.value
+
+
+# ---------------------------------------------------------------- compiled-reference wrappers
+
+def ref_decode_row(type_id: int, n: int, data: np.ndarray) -> np.ndarray:
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    _chk(ref().ref_decode_row(type_id, n, _ptr(d), d.nbytes, _ptr(out), n), ref(), "ref_last_error")
+    return out
+
+
+def ref_storage_dot(type_id: int, n: int, data: np.ndarray, x: np.ndarray) -> float:
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    out = C.c_float()
+    _chk(ref().ref_storage_dot(type_id, n, _ptr(d), d.nbytes, _ptr(xv), xv.size, C.byref(out)), ref(),
+         "ref_last_error")
+    return out.value
+
+
+def ref_storage_matvec(type_id: int, rows: int, cols: int, data: np.ndarray, x: np.ndarray) -> np.ndarray:
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(rows, dtype=np.float32)
+    _chk(ref().ref_storage_matvec(type_id, rows, cols, _ptr(d), d.nbytes, _ptr(xv), xv.size, _ptr(y), rows),
+         ref(), "ref_last_error")
+    return y
+
+
+def ref_status(fn: str, *args) -> int:
+    return getattr(ref(), fn)(*args)
+
+
+def default_threads() -> int:
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        return os.cpu_count() or 1

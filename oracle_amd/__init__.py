@@ -1,0 +1,296 @@
+"""oracle_amd -- MI355X (gfx950) quantized-weight matrix path.
+
+Python view of liboq.so's C ABI (include/oq.h), used by the tests and the benchmark.  The
+production host side is the C++20 adapter in oracle_amd/host/, which mirrors the reference's
+oracle::backend::cpu quantized functions.  Errors surface as the reference's exception kinds:
+
+    std::invalid_argument -> InvalidArgument (ValueError)
+    std::out_of_range     -> OutOfRange (IndexError)
+    std::overflow_error   -> Overflow (OverflowError)
+    std::runtime_error    -> UnsupportedType (RuntimeError)   [unregistered / ragged type]
+    std::logic_error      -> LogicError
+    HIP failures          -> DeviceError / DeviceOutOfMemory
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+
+TYPE_F32 = 0
+TYPE_F16 = 1
+TYPE_Q8_0 = 8
+TYPE_Q4_K = 12
+TYPE_Q5_K = 13
+TYPE_Q6_K = 14
+TYPE_Q8_K = 15
+TYPE_BF16 = 30
+QK_K = 256
+Q8K_BLOCK_BYTES = 292
+
+
+class OqError(Exception):
+    code = 0
+
+
+class InvalidArgument(OqError, ValueError):
+    code = _lib.OQ_INVALID_ARGUMENT
+
+
+class OutOfRange(OqError, IndexError):
+    code = _lib.OQ_OUT_OF_RANGE
+
+
+class Overflow(OqError, OverflowError):
+    code = _lib.OQ_OVERFLOW
+
+
+class UnsupportedType(OqError, RuntimeError):
+    code = _lib.OQ_UNSUPPORTED_TYPE
+
+
+class DeviceError(OqError, RuntimeError):
+    code = _lib.OQ_DEVICE_ERROR
+
+
+class DeviceOutOfMemory(DeviceError):
+    code = _lib.OQ_OUT_OF_MEMORY
+
+
+class LogicError(OqError):
+    code = _lib.OQ_LOGIC_ERROR
+
+
+_BY_CODE = {cls.code: cls for cls in (InvalidArgument, OutOfRange, Overflow, UnsupportedType,
+                                      DeviceError, DeviceOutOfMemory, LogicError)}
+
+
+def _check(rc: int, ctx_handle=None) -> None:
+    if rc == _lib.OQ_OK:
+        return
+    lib = _lib.load()
+    msg = lib.oq_last_error(ctx_handle).decode(errors="replace")
+    raise _BY_CODE.get(rc, OqError)(msg)
+
+
+# ---------------------------------------------------------------- registry
+
+@dataclass(frozen=True)
+class GgmlTypeLayout:
+    """Mirror of oracle::model::GgmlTypeLayout (include/oracle/model/ggml_type.hpp:9-15)."""
+    type: int
+    name: str
+    block_elements: int
+    bytes_per_block: int
+    quantized: bool
+
+
+def ggml_type_layout(type_id: int) -> GgmlTypeLayout | None:
+    """ggml_type_layout (src/model/ggml_type.cpp:69-75): None for unknown/removed ids."""
+    lib = _lib.load()
+    be, bpb, q = C.c_uint64(), C.c_uint64(), C.c_int()
+    name = C.c_char_p()
+    if lib.oq_type_layout(type_id, C.byref(be), C.byref(bpb), C.byref(q), C.byref(name)) != 0:
+        return None
+    return GgmlTypeLayout(type_id, name.value.decode(), be.value, bpb.value, bool(q.value))
+
+
+def ggml_row_byte_size(row_elements: int, type_id: int) -> int:
+    """ggml_row_byte_size (src/model/ggml_type.cpp:77-94), same error kinds."""
+    lib = _lib.load()
+    out = C.c_uint64()
+    _check(lib.oq_row_byte_size(row_elements, type_id, C.byref(out)))
+    return out.value
+
+
+def type_supported(type_id: int) -> bool:
+    return bool(_lib.load().oq_type_supported(type_id))
+
+
+# ---------------------------------------------------------------- device objects
+
+class DeviceBuffer:
+    """Device (HBM) allocation owned by a Context."""
+
+    def __init__(self, ctx: "Context", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        ctx._call(ctx.lib.oq_device_alloc, ctx.h, self.nbytes, C.byref(p))
+        self.ptr = p.value
+
+    def upload(self, arr: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(arr)
+        if a.nbytes > self.nbytes:
+            raise InvalidArgument("host array larger than device buffer")
+        self.ctx._call(self.ctx.lib.oq_copy_to_device, self.ctx.h, self.ptr, a.ctypes.data, a.nbytes)
+        return self
+
+    def download(self, dtype, count: int | None = None) -> np.ndarray:
+        dt = np.dtype(dtype)
+        n = self.nbytes // dt.itemsize if count is None else count
+        out = np.empty(n, dtype=dt)
+        self.ctx._call(self.ctx.lib.oq_copy_to_host, self.ctx.h, out.ctypes.data, self.ptr, out.nbytes)
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            self.ctx._call(self.ctx.lib.oq_device_free, self.ctx.h, self.ptr)
+            self.ptr = None
+
+
+class Weight:
+    """A GGML tensor uploaded once to HBM (oq_weight)."""
+
+    def __init__(self, ctx: "Context", handle: int, type_id: int, ne0: int, ne1: int):
+        self.ctx, self.h = ctx, handle
+        self.type, self.ne0, self.ne1 = type_id, ne0, ne1
+
+    @property
+    def device_bytes(self) -> int:
+        db = C.c_uint64()
+        _check(self.ctx.lib.oq_weight_info(self.h, None, None, None, C.byref(db)))
+        return db.value
+
+    def release(self) -> None:
+        if self.h:
+            self.ctx.lib.oq_weight_release(self.h)
+            self.h = None
+
+
+class Graph:
+    def __init__(self, ctx: "Context", handle: int):
+        self.ctx, self.h = ctx, handle
+
+    def launch(self) -> None:
+        self.ctx._call(self.ctx.lib.oq_graph_launch, self.ctx.h, self.h)
+
+    def destroy(self) -> None:
+        if self.h:
+            self.ctx.lib.oq_graph_destroy(self.h)
+            self.h = None
+
+
+class Context:
+    """One device + one HIP stream (oq_context)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = _lib.load()
+        h = C.c_void_p()
+        _check(self.lib.oq_context_create(device, C.byref(h)))
+        self.h = h.value
+
+    def _call(self, fn, *args) -> None:
+        _check(fn(*args), self.h)
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.oq_context_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # memory
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, arr: np.ndarray) -> DeviceBuffer:
+        a = np.ascontiguousarray(arr)
+        return DeviceBuffer(self, max(a.nbytes, 1)).upload(a)
+
+    def sync(self) -> None:
+        self._call(self.lib.oq_synchronize, self.h)
+
+    # weights
+    def upload(self, type_id: int, ne0: int, ne1: int, data) -> Weight:
+        buf = np.frombuffer(data, dtype=np.uint8) if not isinstance(data, np.ndarray) else data
+        buf = np.ascontiguousarray(buf)
+        h = C.c_void_p()
+        self._call(self.lib.oq_weight_upload, self.h, type_id, ne0, ne1,
+                   buf.ctypes.data if buf.size else None, buf.nbytes, C.byref(h))
+        return Weight(self, h.value, type_id, ne0, ne1)
+
+    def upload_from_device(self, type_id: int, ne0: int, ne1: int, buf: DeviceBuffer, nbytes: int) -> Weight:
+        h = C.c_void_p()
+        self._call(self.lib.oq_weight_upload_device, self.h, type_id, ne0, ne1, buf.ptr, nbytes, C.byref(h))
+        return Weight(self, h.value, type_id, ne0, ne1)
+
+    # compute (device buffers in, device buffers out; asynchronous on the context stream)
+    def dequantize_rows(self, w: Weight, row0: int, nrows: int, out: DeviceBuffer) -> None:
+        self._call(self.lib.oq_dequantize_rows, self.h, w.h, row0, nrows, out.ptr if out else None)
+
+    def quantize_q8k(self, x: DeviceBuffer, m: int, k: int, out: DeviceBuffer) -> None:
+        self._call(self.lib.oq_quantize_q8k, self.h, x.ptr, m, k, out.ptr)
+
+    def matvec(self, w: Weight, x: DeviceBuffer, y: DeviceBuffer) -> None:
+        self._call(self.lib.oq_matvec, self.h, w.h, x.ptr, y.ptr)
+
+    def matvec_q8k(self, w: Weight, q8k: DeviceBuffer, y: DeviceBuffer) -> None:
+        self._call(self.lib.oq_matvec_q8k, self.h, w.h, q8k.ptr, y.ptr)
+
+    def matmul(self, w: Weight, m: int, x: DeviceBuffer, y: DeviceBuffer) -> None:
+        self._call(self.lib.oq_matmul, self.h, w.h, m, x.ptr, y.ptr)
+
+    def matmul_q8k(self, w: Weight, m: int, q8k: DeviceBuffer, y: DeviceBuffer) -> None:
+        self._call(self.lib.oq_matmul_q8k, self.h, w.h, m, q8k.ptr, y.ptr)
+
+    # timing / graphs
+    def timer_start(self) -> None:
+        self._call(self.lib.oq_timer_start, self.h)
+
+    def timer_stop(self) -> float:
+        ms = C.c_float()
+        self._call(self.lib.oq_timer_stop, self.h, C.byref(ms))
+        return ms.value
+
+    def capture_begin(self) -> None:
+        self._call(self.lib.oq_capture_begin, self.h)
+
+    def capture_end(self) -> Graph:
+        g = C.c_void_p()
+        self._call(self.lib.oq_capture_end, self.h, C.byref(g))
+        return Graph(self, g.value)
+
+
+# ---------------------------------------------------------------- reference-shaped helpers
+
+def storage_matvec(ctx: Context, type_id: int, rows: int, cols: int, matrix: np.ndarray,
+                   vector: np.ndarray) -> np.ndarray:
+    """reference_storage_matvec (src/backend/cpu/quantized_reference.cpp:128-162) on the GPU:
+    host bytes and host F32 vector in, host F32 output back (upload included)."""
+    vec = np.ascontiguousarray(vector, dtype=np.float32)
+    if rows == 0 or cols == 0:
+        raise InvalidArgument("reference matvec dimensions must be non-zero")
+    if vec.size != cols:
+        raise InvalidArgument("reference matvec vector length mismatch")
+    w = ctx.upload(type_id, cols, rows, matrix)
+    try:
+        xb = ctx.to_device(vec)
+        yb = ctx.alloc(rows * 4)
+        ctx.matvec(w, xb, yb)
+        y = yb.download(np.float32, rows)
+        xb.free()
+        yb.free()
+        return y
+    finally:
+        w.release()
+
+
+def decode_rows(ctx: Context, type_id: int, cols: int, rows: int, data: np.ndarray) -> np.ndarray:
+    """reference_decode_mapped_tensor (src/backend/cpu/quantized_reference.cpp:85-105) on the GPU."""
+    w = ctx.upload(type_id, cols, rows, data)
+    try:
+        out = ctx.alloc(rows * cols * 4)
+        ctx.dequantize_rows(w, 0, rows, out)
+        r = out.download(np.float32, rows * cols)
+        out.free()
+        return r.reshape(rows, cols)
+    finally:
+        w.release()

@@ -1,0 +1,80 @@
+"""ctypes binding of liboq.so (include/oq.h).
+
+The library is built in-tree by oracle_amd/build.py.  Loading never falls back to anything:
+a missing or unloadable liboq.so raises immediately.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "liboq.so"
+
+OQ_OK = 0
+OQ_INVALID_ARGUMENT = -1
+OQ_OUT_OF_RANGE = -2
+OQ_OVERFLOW = -3
+OQ_UNSUPPORTED_TYPE = -4
+OQ_DEVICE_ERROR = -5
+OQ_OUT_OF_MEMORY = -6
+OQ_LOGIC_ERROR = -7
+
+# (name, restype, argtypes) for every entry point declared in include/oq.h
+_P = C.c_void_p
+_U64 = C.c_uint64
+_U32 = C.c_uint32
+SIGNATURES = [
+    ("oq_type_layout", C.c_int, [_U32, C.POINTER(_U64), C.POINTER(_U64), C.POINTER(C.c_int), C.POINTER(C.c_char_p)]),
+    ("oq_row_byte_size", C.c_int, [_U64, _U32, C.POINTER(_U64)]),
+    ("oq_type_supported", C.c_int, [_U32]),
+    ("oq_context_create", C.c_int, [C.c_int, C.POINTER(_P)]),
+    ("oq_context_destroy", None, [_P]),
+    ("oq_last_error", C.c_char_p, [_P]),
+    ("oq_synchronize", C.c_int, [_P]),
+    ("oq_context_stream", _P, [_P]),
+    ("oq_device_alloc", C.c_int, [_P, _U64, C.POINTER(_P)]),
+    ("oq_device_free", C.c_int, [_P, _P]),
+    ("oq_copy_to_device", C.c_int, [_P, _P, _P, _U64]),
+    ("oq_copy_to_host", C.c_int, [_P, _P, _P, _U64]),
+    ("oq_copy_device", C.c_int, [_P, _P, _P, _U64]),
+    ("oq_weight_upload", C.c_int, [_P, _U32, _U64, _U64, _P, _U64, C.POINTER(_P)]),
+    ("oq_weight_upload_device", C.c_int, [_P, _U32, _U64, _U64, _P, _U64, C.POINTER(_P)]),
+    ("oq_weight_release", None, [_P]),
+    ("oq_weight_info", C.c_int, [_P, C.POINTER(_U32), C.POINTER(_U64), C.POINTER(_U64), C.POINTER(_U64)]),
+    ("oq_dequantize_rows", C.c_int, [_P, _P, _U64, _U64, _P]),
+    ("oq_quantize_q8k", C.c_int, [_P, _P, _U64, _U64, _P]),
+    ("oq_matvec", C.c_int, [_P, _P, _P, _P]),
+    ("oq_matvec_q8k", C.c_int, [_P, _P, _P, _P]),
+    ("oq_matmul", C.c_int, [_P, _P, _U64, _P, _P]),
+    ("oq_matmul_q8k", C.c_int, [_P, _P, _U64, _P, _P]),
+    ("oq_timer_start", C.c_int, [_P]),
+    ("oq_timer_stop", C.c_int, [_P, C.POINTER(C.c_float)]),
+    ("oq_capture_begin", C.c_int, [_P]),
+    ("oq_capture_end", C.c_int, [_P, C.POINTER(_P)]),
+    ("oq_graph_launch", C.c_int, [_P, _P]),
+    ("oq_graph_destroy", None, [_P]),
+]
+
+_lib: C.CDLL | None = None
+
+
+def load() -> C.CDLL:
+    """Load liboq.so and attach prototypes; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python oracle_amd/build.py` "
+            "(or __graft_entry__.build()); there is no fallback path")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, res, args in SIGNATURES:
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def exported_symbols() -> list[str]:
+    return [name for name, _, _ in SIGNATURES]

@@ -1,0 +1,481 @@
+// C ABI of liboq.so (declared in include/oq.h): contexts, one-time weight upload, argument
+// validation with the reference's error kinds, and dispatch to the gfx950 kernels.
+//
+// Validation mirrors what the reference checks before it writes anything
+// (src/backend/cpu/quantized_reference.cpp:134-153, src/model/ggml_type.cpp:77-94,
+// src/model/storage_decode.cpp:182-198): the first failing check decides the status.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "../../include/oq.h"
+#include "oq_internal.h"
+
+struct oq_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    std::string error;
+    bool capturing = false;
+    void* scratch = nullptr;  // Q8_K staging for the un-fused and MFMA paths
+    uint64_t scratch_bytes = 0;
+};
+
+struct oq_weight {
+    oq::DeviceMatrix m{};
+    void* owned = nullptr;
+    uint64_t device_bytes = 0;
+    int device = 0;
+};
+
+struct oq_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+struct Layout {
+    const char* name;
+    uint32_t block_elements;
+    uint32_t bytes_per_block;
+    int quantized;
+};
+
+// GGML on-disk layouts by type id (the reference keeps the same table, src/model/ggml_type.cpp
+// :12-54; ids with zero geometry are deprecated or removed and count as unregistered).
+constexpr Layout kLayouts[] = {
+    {"f32", 1, 4, 0},          {"f16", 1, 2, 0},           {"q4_0", 32, 18, 1},
+    {"q4_1", 32, 20, 1},       {"deprecated_q4_2", 0, 0, 0}, {"deprecated_q4_3", 0, 0, 0},
+    {"q5_0", 32, 22, 1},       {"q5_1", 32, 24, 1},        {"q8_0", 32, 34, 1},
+    {"q8_1", 32, 36, 1},       {"q2_K", 256, 84, 1},       {"q3_K", 256, 110, 1},
+    {"q4_K", 256, 144, 1},     {"q5_K", 256, 176, 1},      {"q6_K", 256, 210, 1},
+    {"q8_K", 256, 292, 1},     {"iq2_xxs", 256, 66, 1},    {"iq2_xs", 256, 74, 1},
+    {"iq3_xxs", 256, 98, 1},   {"iq1_s", 256, 50, 1},      {"iq4_nl", 32, 18, 1},
+    {"iq3_s", 256, 110, 1},    {"iq2_s", 256, 82, 1},      {"iq4_xs", 256, 136, 1},
+    {"i8", 1, 1, 0},           {"i16", 1, 2, 0},           {"i32", 1, 4, 0},
+    {"i64", 1, 8, 0},          {"f64", 1, 8, 0},           {"iq1_m", 256, 56, 1},
+    {"bf16", 1, 2, 0},         {"removed_q4_0_4_4", 0, 0, 0}, {"removed_q4_0_4_8", 0, 0, 0},
+    {"removed_q4_0_8_8", 0, 0, 0}, {"tq1_0", 256, 54, 1},  {"tq2_0", 256, 66, 1},
+    {"removed_iq4_nl_4_4", 0, 0, 0}, {"removed_iq4_nl_4_8", 0, 0, 0},
+    {"removed_iq4_nl_8_8", 0, 0, 0}, {"mxfp4", 32, 17, 1}, {"nvfp4", 64, 36, 1},
+    {"q1_0", 128, 18, 1},      {"q2_0", 64, 18, 1},
+};
+constexpr uint32_t kLayoutCount = sizeof(kLayouts) / sizeof(kLayouts[0]);
+
+const Layout* layout_of(uint32_t type) {
+    if (type >= kLayoutCount) return nullptr;
+    const Layout& l = kLayouts[type];
+    return (l.block_elements == 0 || l.bytes_per_block == 0) ? nullptr : &l;
+}
+
+bool is_kquant(uint32_t t) { return t == OQ_TYPE_Q4_K || t == OQ_TYPE_Q5_K || t == OQ_TYPE_Q6_K; }
+
+int fail(oq_context* ctx, int code, const std::string& msg) {
+    if (ctx) ctx->error = msg;
+    else g_error = msg;
+    return code;
+}
+
+int hip_fail(oq_context* ctx, hipError_t e, const char* what) {
+    const int code = e == hipErrorOutOfMemory ? OQ_OUT_OF_MEMORY : OQ_DEVICE_ERROR;
+    return fail(ctx, code, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define OQ_HIP(ctx, expr, what)                         \
+    do {                                                \
+        hipError_t e_ = (expr);                         \
+        if (e_ != hipSuccess) return hip_fail(ctx, e_, what); \
+    } while (0)
+
+// ggml_row_byte_size (src/model/ggml_type.cpp:77-94)
+int row_bytes(oq_context* ctx, uint64_t k, uint32_t type, uint64_t* out) {
+    const Layout* l = layout_of(type);
+    if (!l) return fail(ctx, OQ_UNSUPPORTED_TYPE, "unsupported GGML tensor type: " + std::to_string(type));
+    if (k == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "GGML tensor row must contain at least one element");
+    if (k % l->block_elements != 0) {
+        return fail(ctx, OQ_UNSUPPORTED_TYPE,
+                    "GGML tensor row length " + std::to_string(k) + " is not divisible by block size " +
+                        std::to_string(l->block_elements) + " for type " + l->name);
+    }
+    const uint64_t blocks = k / l->block_elements;
+    if (blocks != 0 && l->bytes_per_block > UINT64_MAX / blocks) {
+        return fail(ctx, OQ_OVERFLOW, "GGML row byte size overflow");
+    }
+    *out = blocks * l->bytes_per_block;
+    return OQ_OK;
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_weight(oq_context* ctx, const oq_weight* w) {
+    if (!w || !w->m.base) return fail(ctx, OQ_INVALID_ARGUMENT, "null weight");
+    if (w->device != ctx->device) return fail(ctx, OQ_INVALID_ARGUMENT, "weight lives on another device");
+    return OQ_OK;
+}
+
+int ensure_scratch(oq_context* ctx, uint64_t bytes) {
+    if (ctx->scratch_bytes >= bytes) return OQ_OK;
+    if (ctx->capturing) {
+        return fail(ctx, OQ_INVALID_ARGUMENT,
+                    "activation staging buffer must be sized before graph capture (run the call once first)");
+    }
+    if (ctx->scratch) {
+        OQ_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        OQ_HIP(ctx, hipFree(ctx->scratch), "hipFree");
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+    }
+    OQ_HIP(ctx, hipMalloc(&ctx->scratch, bytes), "hipMalloc(activation staging)");
+    ctx->scratch_bytes = bytes;
+    return OQ_OK;
+}
+
+bool env_flag(const char* name, bool fallback) {
+    const char* v = getenv(name);
+    return v ? atoi(v) != 0 : fallback;
+}
+
+int upload_common(oq_context* ctx, uint32_t type, uint64_t ne0, uint64_t ne1, const void* bytes,
+                  uint64_t nbytes, bool from_device, oq_weight** out) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (!out) return fail(ctx, OQ_INVALID_ARGUMENT, "null output handle");
+    *out = nullptr;
+    if (ne0 == 0 || ne1 == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "reference matvec dimensions must be non-zero");
+    uint64_t rb = 0;
+    if (int rc = row_bytes(ctx, ne0, type, &rb)) return rc;
+    if (rb > UINT64_MAX / ne1) return fail(ctx, OQ_OVERFLOW, "reference matvec matrix size overflow");
+    if (nbytes != rb * ne1) return fail(ctx, OQ_INVALID_ARGUMENT, "reference matvec matrix byte size mismatch");
+    if (!oq_type_supported(type)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "storage decoder does not support GGML type " + std::to_string(type));
+    }
+    if (!bytes) return fail(ctx, OQ_INVALID_ARGUMENT, "null tensor bytes");
+    if (ctx->capturing) return fail(ctx, OQ_INVALID_ARGUMENT, "weights cannot be uploaded during graph capture");
+
+    const uint64_t pitch = oq::device_pitch(type, ne0);
+    if (pitch != 0 && ne1 > UINT64_MAX / pitch) return fail(ctx, OQ_OVERFLOW, "device matrix size overflow");
+    const uint64_t dbytes = pitch * ne1;
+    OQ_HIP(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    void* dst = nullptr;
+    OQ_HIP(ctx, hipMalloc(&dst, dbytes), "hipMalloc(weight)");
+    auto cleanup = [&](int rc) {
+        (void)hipFree(dst);
+        return rc;
+    };
+    const bool identity = pitch == rb && type != OQ_TYPE_Q6_K && type != OQ_TYPE_Q8_0;
+    hipError_t e = hipSuccess;
+    if (identity) {
+        e = hipMemcpyAsync(dst, bytes, nbytes, from_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                           ctx->stream);
+    } else {
+        const void* src = bytes;
+        void* staging = nullptr;
+        if (!from_device) {
+            e = hipMalloc(&staging, nbytes);
+            if (e == hipSuccess) e = hipMemcpyAsync(staging, bytes, nbytes, hipMemcpyHostToDevice, ctx->stream);
+            src = staging;
+        }
+        if (e == hipSuccess) e = hipMemsetAsync(dst, 0, dbytes, ctx->stream);
+        if (e == hipSuccess)
+            e = oq::launch_relayout(type, ne0, ne1, static_cast<const uint8_t*>(src),
+                                    static_cast<uint8_t*>(dst), pitch, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (staging) (void)hipFree(staging);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return cleanup(hip_fail(ctx, e, "weight upload"));
+    oq_weight* w = new oq_weight;
+    w->m.type = type;
+    w->m.k = ne0;
+    w->m.n = ne1;
+    w->m.pitch = pitch;
+    w->m.base = static_cast<const uint8_t*>(dst);
+    w->owned = dst;
+    w->device_bytes = dbytes;
+    w->device = ctx->device;
+    *out = w;
+    return OQ_OK;
+}
+
+int launch_rc(oq_context* ctx, hipError_t e, const char* what) {
+    return e == hipSuccess ? OQ_OK : hip_fail(ctx, e, what);
+}
+
+}  // namespace
+
+extern "C" {
+
+int oq_type_layout(uint32_t type, uint64_t* block_elements, uint64_t* bytes_per_block, int* quantized,
+                   const char** name) {
+    const Layout* l = layout_of(type);
+    if (!l) return fail(nullptr, OQ_UNSUPPORTED_TYPE, "unsupported GGML tensor type: " + std::to_string(type));
+    if (block_elements) *block_elements = l->block_elements;
+    if (bytes_per_block) *bytes_per_block = l->bytes_per_block;
+    if (quantized) *quantized = l->quantized;
+    if (name) *name = l->name;
+    return OQ_OK;
+}
+
+int oq_row_byte_size(uint64_t row_elements, uint32_t type, uint64_t* out) {
+    if (!out) return fail(nullptr, OQ_INVALID_ARGUMENT, "null output");
+    return row_bytes(nullptr, row_elements, type, out);
+}
+
+int oq_type_supported(uint32_t t) {
+    return t == OQ_TYPE_F32 || t == OQ_TYPE_F16 || t == OQ_TYPE_BF16 || t == OQ_TYPE_Q8_0 ||
+           t == OQ_TYPE_Q4_K || t == OQ_TYPE_Q5_K || t == OQ_TYPE_Q6_K;
+}
+
+int oq_context_create(int device, oq_context** out) {
+    if (!out) return fail(nullptr, OQ_INVALID_ARGUMENT, "null output handle");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail(nullptr, e, "hipGetDeviceCount");
+    if (device < 0 || device >= count) {
+        return fail(nullptr, OQ_OUT_OF_RANGE, "device ordinal " + std::to_string(device) + " out of range");
+    }
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
+    oq_context* ctx = new oq_context;
+    ctx->device = device;
+    e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->t0);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->t1);
+    if (e != hipSuccess) {
+        const int rc = hip_fail(nullptr, e, "context creation");
+        oq_context_destroy(ctx);
+        return rc;
+    }
+    *out = ctx;
+    return OQ_OK;
+}
+
+void oq_context_destroy(oq_context* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->t0) (void)hipEventDestroy(ctx->t0);
+    if (ctx->t1) (void)hipEventDestroy(ctx->t1);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+const char* oq_last_error(const oq_context* ctx) { return ctx ? ctx->error.c_str() : g_error.c_str(); }
+
+int oq_synchronize(oq_context* ctx) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    OQ_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return OQ_OK;
+}
+
+void* oq_context_stream(oq_context* ctx) { return ctx ? ctx->stream : nullptr; }
+
+int oq_device_alloc(oq_context* ctx, uint64_t bytes, void** out) {
+    if (!ctx || !out) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    OQ_HIP(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    OQ_HIP(ctx, hipMalloc(out, bytes ? bytes : 1), "hipMalloc");
+    return OQ_OK;
+}
+
+int oq_device_free(oq_context* ctx, void* p) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (p) {
+        OQ_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        OQ_HIP(ctx, hipFree(p), "hipFree");
+    }
+    return OQ_OK;
+}
+
+int oq_copy_to_device(oq_context* ctx, void* dst, const void* src, uint64_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    OQ_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpy H2D");
+    OQ_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return OQ_OK;
+}
+
+int oq_copy_to_host(oq_context* ctx, void* dst, const void* src, uint64_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    OQ_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpy D2H");
+    OQ_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return OQ_OK;
+}
+
+int oq_copy_device(oq_context* ctx, void* dst, const void* src, uint64_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    OQ_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream), "hipMemcpy D2D");
+    return OQ_OK;
+}
+
+int oq_weight_upload(oq_context* ctx, uint32_t type, uint64_t ne0, uint64_t ne1, const void* host_bytes,
+                     uint64_t nbytes, oq_weight** out) {
+    return upload_common(ctx, type, ne0, ne1, host_bytes, nbytes, false, out);
+}
+
+int oq_weight_upload_device(oq_context* ctx, uint32_t type, uint64_t ne0, uint64_t ne1, const void* dev_bytes,
+                            uint64_t nbytes, oq_weight** out) {
+    return upload_common(ctx, type, ne0, ne1, dev_bytes, nbytes, true, out);
+}
+
+void oq_weight_release(oq_weight* w) {
+    if (!w) return;
+    if (w->owned) {
+        (void)hipSetDevice(w->device);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(w->owned);
+    }
+    delete w;
+}
+
+int oq_weight_info(const oq_weight* w, uint32_t* type, uint64_t* ne0, uint64_t* ne1, uint64_t* device_bytes) {
+    if (!w) return fail(nullptr, OQ_INVALID_ARGUMENT, "null weight");
+    if (type) *type = w->m.type;
+    if (ne0) *ne0 = w->m.k;
+    if (ne1) *ne1 = w->m.n;
+    if (device_bytes) *device_bytes = w->device_bytes;
+    return OQ_OK;
+}
+
+int oq_dequantize_rows(oq_context* ctx, const oq_weight* w, uint64_t row0, uint64_t nrows, float* out) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (int rc = check_weight(ctx, w)) return rc;
+    if (row0 > w->m.n || nrows > w->m.n - row0) {
+        return fail(ctx, OQ_OUT_OF_RANGE, "GGUF tensor row index exceeds row count");
+    }
+    if (nrows == 0) return OQ_OK;
+    if (!out) return fail(ctx, OQ_INVALID_ARGUMENT, "null output");
+    return launch_rc(ctx, oq::launch_dequantize(w->m, row0, nrows, out, ctx->stream), "dequantize");
+}
+
+int oq_quantize_q8k(oq_context* ctx, const float* x, uint64_t m, uint64_t k, void* q8k) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (m == 0 || k == 0 || k % oq::kQK != 0) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Q8_K quantization needs m > 0 rows of a multiple of 256 values");
+    }
+    if (!x || !q8k) return fail(ctx, OQ_INVALID_ARGUMENT, "null buffer");
+    if (!aligned(x, 16) || !aligned(q8k, 4)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "activations must be 16-byte aligned and Q8_K blocks 4-byte aligned");
+    }
+    return launch_rc(ctx, oq::launch_quantize_q8k(x, m, k, static_cast<uint8_t*>(q8k), ctx->stream),
+                     "quantize_q8k");
+}
+
+int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, float* y) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (int rc = check_weight(ctx, w)) return rc;
+    if (m == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "matmul batch must be non-zero");
+    if (m > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "matmul batch too large");
+    if (!x || !y) return fail(ctx, OQ_INVALID_ARGUMENT, "null buffer");
+    const uint32_t t = w->m.type;
+    const bool vec_loads = is_kquant(t) || t == OQ_TYPE_Q8_0;
+    if ((vec_loads && !aligned(x, 16)) || !aligned(x, 4) || !aligned(y, 4)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "activation / output buffers are misaligned");
+    }
+    if (is_kquant(t)) {
+        const uint64_t q8bytes = m * (w->m.k / oq::kQK) * oq::kQ8KBytes;
+        const bool mfma = m >= 16 && oq::gemm_mfma_supported(w->m, (int)m);
+        const bool fused = env_flag("OQ_FUSED_QUANT", true);
+        if (mfma || !fused) {
+            if (int rc = ensure_scratch(ctx, q8bytes)) return rc;
+            uint8_t* q8 = static_cast<uint8_t*>(ctx->scratch);
+            hipError_t e = oq::launch_quantize_q8k(x, m, w->m.k, q8, ctx->stream);
+            if (e == hipSuccess) {
+                e = mfma ? oq::launch_gemm_q4k_mfma(w->m, (int)m, q8, y, ctx->stream)
+                         : oq::launch_gemv_kquant(w->m, (int)m, nullptr, q8, y, ctx->stream);
+            }
+            return launch_rc(ctx, e, "matmul");
+        }
+        return launch_rc(ctx, oq::launch_gemv_kquant(w->m, (int)m, x, nullptr, y, ctx->stream), "matmul");
+    }
+    return launch_rc(ctx, oq::launch_gemv_f32act(w->m, (int)m, x, y, ctx->stream), "matmul");
+}
+
+int oq_matvec(oq_context* ctx, const oq_weight* w, const float* x, float* y) {
+    return oq_matmul(ctx, w, 1, x, y);
+}
+
+int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q8k, float* y) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (int rc = check_weight(ctx, w)) return rc;
+    if (!is_kquant(w->m.type)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Q8_K activations need a q4_K, q5_K or q6_K weight");
+    }
+    if (m == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "matmul batch must be non-zero");
+    if (m > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "matmul batch too large");
+    if (!q8k || !y) return fail(ctx, OQ_INVALID_ARGUMENT, "null buffer");
+    if (!aligned(q8k, 4) || !aligned(y, 4)) return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer");
+    const uint8_t* q8 = static_cast<const uint8_t*>(q8k);
+    if (m >= 16 && oq::gemm_mfma_supported(w->m, (int)m)) {
+        return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, q8, y, ctx->stream), "matmul_q8k");
+    }
+    return launch_rc(ctx, oq::launch_gemv_kquant(w->m, (int)m, nullptr, q8, y, ctx->stream), "matmul_q8k");
+}
+
+int oq_matvec_q8k(oq_context* ctx, const oq_weight* w, const void* q8k, float* y) {
+    return oq_matmul_q8k(ctx, w, 1, q8k, y);
+}
+
+int oq_timer_start(oq_context* ctx) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    OQ_HIP(ctx, hipEventRecord(ctx->t0, ctx->stream), "hipEventRecord");
+    return OQ_OK;
+}
+
+int oq_timer_stop(oq_context* ctx, float* ms) {
+    if (!ctx || !ms) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    OQ_HIP(ctx, hipEventRecord(ctx->t1, ctx->stream), "hipEventRecord");
+    OQ_HIP(ctx, hipEventSynchronize(ctx->t1), "hipEventSynchronize");
+    OQ_HIP(ctx, hipEventElapsedTime(ms, ctx->t0, ctx->t1), "hipEventElapsedTime");
+    return OQ_OK;
+}
+
+int oq_capture_begin(oq_context* ctx) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (ctx->capturing) return fail(ctx, OQ_INVALID_ARGUMENT, "capture already active");
+    OQ_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    ctx->capturing = true;
+    return OQ_OK;
+}
+
+int oq_capture_end(oq_context* ctx, oq_graph** out) {
+    if (!ctx || !out) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (!ctx->capturing) return fail(ctx, OQ_INVALID_ARGUMENT, "no capture active");
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    OQ_HIP(ctx, hipStreamEndCapture(ctx->stream, &g), "hipStreamEndCapture");
+    hipGraphExec_t ex = nullptr;
+    hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return hip_fail(ctx, e, "hipGraphInstantiate");
+    }
+    oq_graph* gr = new oq_graph;
+    gr->graph = g;
+    gr->exec = ex;
+    *out = gr;
+    return OQ_OK;
+}
+
+int oq_graph_launch(oq_context* ctx, oq_graph* g) {
+    if (!ctx || !g) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    OQ_HIP(ctx, hipGraphLaunch(g->exec, ctx->stream), "hipGraphLaunch");
+    return OQ_OK;
+}
+
+void oq_graph_destroy(oq_graph* g) {
+    if (!g) return;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
+}  // extern "C"

@@ -1,0 +1,134 @@
+// Device helpers shared by the gfx950 kernels: exact GGML scalar decodes, the K-quant
+// scale/min unpack, wave64 reductions and the Q8_K block quantizer.
+//
+// Everything here that feeds a bit-exact output (dequantized rows, Q8_K blocks) is compiled
+// with FP contraction off, so a*b - c*d stays two roundings as in the reference's scalar C++.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "oq_internal.h"
+
+#define OQ_DEVICE __device__ __forceinline__
+
+namespace oq {
+
+// ------------------------------------------------------------------ scalars
+
+OQ_DEVICE float bits_f32(uint32_t u) { return __uint_as_float(u); }
+
+// Exact binary16 -> binary32 that keeps NaN payloads bit for bit (the hardware conversion
+// quiets signalling NaNs; the reference's f16_to_f32, src/model/storage_decode.cpp:150-176,
+// does not).  Subnormals: value = mantissa * 2^-24, exact in F32.
+OQ_DEVICE float f16_bits_to_f32(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t em = h & 0x7FFFu;
+    if (em >= 0x7C00u) return bits_f32(sign | 0x7F800000u | ((em & 0x3FFu) << 13));
+    if (em >= 0x0400u) return bits_f32(sign | ((em << 13) + (112u << 23)));
+    return bits_f32(sign | __float_as_uint((float)em * 5.9604644775390625e-08f));
+}
+
+OQ_DEVICE float bf16_bits_to_f32(uint32_t h) { return bits_f32(h << 16); }
+
+// byte `idx` (0..11) of the 12-byte K-quant scale array held in three dwords
+OQ_DEVICE uint32_t byte_of3(uint32_t p0, uint32_t p1, uint32_t p2, uint32_t idx) {
+    const uint32_t w = idx < 4 ? p0 : (idx < 8 ? p1 : p2);
+    return (w >> (8u * (idx & 3u))) & 0xFFu;
+}
+
+// K-quant 6-bit (scale, min) pair j of 8 (src/model/storage_decode.cpp:44-61): pairs 0..3 are
+// the low six bits of bytes j and j+4; pairs 4..7 take a low nibble from byte j+4 and their two
+// high bits from bits 6..7 of bytes j-4 (scale) and j (min).
+OQ_DEVICE void scale_min_k4(uint32_t j, uint32_t p0, uint32_t p1, uint32_t p2, uint32_t& sc,
+                            uint32_t& mn) {
+    if (j < 4) {
+        sc = byte_of3(p0, p1, p2, j) & 63u;
+        mn = byte_of3(p0, p1, p2, j + 4) & 63u;
+    } else {
+        const uint32_t b4 = byte_of3(p0, p1, p2, j + 4);
+        sc = (b4 & 15u) | ((byte_of3(p0, p1, p2, j - 4) >> 6) << 4);
+        mn = (b4 >> 4) | ((byte_of3(p0, p1, p2, j) >> 6) << 4);
+    }
+}
+
+// ------------------------------------------------------------------ wave64 reductions
+
+OQ_DEVICE float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+OQ_DEVICE float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+OQ_DEVICE int wave_min_int(int v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = min(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// sum over aligned groups of 4 lanes
+OQ_DEVICE int quad_sum_int(int v) {
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    return v;
+}
+
+// ------------------------------------------------------------------ Q8_K
+
+// Result of quantizing one 256-value block with one wave: lane l owns values 4l..4l+3.
+struct Q8KLane {
+    uint32_t qword;  // the lane's four int8 quants, little-endian
+    int quad_bsum;   // sum of the 16 quants of bsums group l/4 (same in the 4 lanes of a quad)
+    float d;         // block scale (wave-uniform)
+};
+
+// GGML quantize_row_q8_K on one block, wave-parallel.  amax = max |x|; `max` is x at the
+// FIRST index reaching amax (a strict > scan keeps the first); amax == 0 gives d = 0, q = 0.
+// iscale = -127/max (correctly rounded division), q = min(127, rne(iscale*x)), d = 1/iscale.
+// Identical bits to the sequential algorithm for finite x.
+OQ_DEVICE Q8KLane quantize_q8k_block_wave(float4 v, int lane) {
+#pragma clang fp contract(off)
+    const float a0 = fabsf(v.x), a1 = fabsf(v.y), a2 = fabsf(v.z), a3 = fabsf(v.w);
+    const float lane_max = fmaxf(fmaxf(a0, a1), fmaxf(a2, a3));
+    const float amax = wave_max(lane_max);
+    Q8KLane r;
+    if (amax == 0.0f) {
+        r.qword = 0u;
+        r.quad_bsum = 0;
+        r.d = 0.0f;
+        return r;
+    }
+    int first = 1 << 30;
+    if (a3 == amax) first = 4 * lane + 3;
+    if (a2 == amax) first = 4 * lane + 2;
+    if (a1 == amax) first = 4 * lane + 1;
+    if (a0 == amax) first = 4 * lane + 0;
+    const int idx = wave_min_int(first);
+    const int owner = idx >> 2, sub = idx & 3;
+    float mine = sub == 0 ? v.x : (sub == 1 ? v.y : (sub == 2 ? v.z : v.w));
+    const float maxv = __shfl(mine, owner, 64);
+    const float iscale = -127.0f / maxv;
+    const float vals[4] = {v.x, v.y, v.z, v.w};
+    uint32_t word = 0;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float t = iscale * vals[i];
+        int q = (int)__builtin_rintf(t);
+        q = q < 127 ? q : 127;
+        s += q;
+        word |= ((uint32_t)q & 0xFFu) << (8 * i);
+    }
+    r.qword = word;
+    r.quad_bsum = quad_sum_int(s);
+    r.d = 1.0f / iscale;
+    return r;
+}
+
+}  // namespace oq

@@ -1,0 +1,55 @@
+// Internal interfaces between the C ABI (oq_api.cpp) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace oq {
+
+constexpr int kQK = 256;          // K-quant super-block
+constexpr int kQ4KBytes = 144;    // {f16 d, f16 dmin, u8 scales[12], u8 qs[128]}
+constexpr int kQ5KBytes = 176;    // {d, dmin, scales[12], qh[32], qs[128]}
+constexpr int kQ6KBytes = 210;    // {ql[128], qh[64], i8 sc[16], f16 d}
+constexpr int kQ80Bytes = 34;     // {f16 d, i8 qs[32]}
+constexpr int kQ8KBytes = 292;    // {f32 d, i8 qs[256], i16 bsums[16]}
+
+// How a weight's rows sit in HBM.  Every row starts at a multiple of `pitch` bytes from
+// `base`, and `pitch` is a multiple of 16 so rows can be streamed with 128-bit loads.
+//   q4_K, q5_K : native GGML blocks (144 / 176 B are multiples of 16)
+//   q6_K       : per-row planes  ql[nsb][128] | qh[nsb][64] | sc[nsb][16] | d[nsb] (f16)
+//   q8_0       : per-row planes  qs[nb][32] | d[nb] (f16)
+//   f32/f16/bf16: native
+struct DeviceMatrix {
+    uint32_t type;
+    uint64_t k;      // elements per row (GGUF dimensions[0])
+    uint64_t n;      // rows (GGUF dimensions[1])
+    uint64_t pitch;  // device bytes per row
+    const uint8_t* base;
+};
+
+uint64_t device_pitch(uint32_t type, uint64_t k);
+
+// ---- oq_decode.hip
+hipError_t launch_relayout(uint32_t type, uint64_t k, uint64_t n, const uint8_t* src,
+                           uint8_t* dst, uint64_t pitch, hipStream_t s);
+hipError_t launch_dequantize(const DeviceMatrix& w, uint64_t row0, uint64_t nrows, float* out,
+                             hipStream_t s);
+hipError_t launch_quantize_q8k(const float* x, uint64_t m, uint64_t k, uint8_t* q8k,
+                               hipStream_t s);
+
+// ---- oq_gemv.hip  (m activation rows, small m: weights streamed once, reuse in registers)
+// K-quant weights against Q8_K activations given as blocks (q8k) or as F32 (x, quantized in
+// the prologue of every workgroup into LDS; bit-identical to launch_quantize_q8k).
+hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k,
+                              float* y, hipStream_t s);
+// q8_0 / f32 / f16 / bf16 weights against F32 activations
+hipError_t launch_gemv_f32act(const DeviceMatrix& w, int m, const float* x, float* y,
+                              hipStream_t s);
+int gemv_max_m();
+
+// ---- oq_gemm.hip  (m >= 16, q4_K on fp16 MFMA)
+hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const uint8_t* q8k, float* y,
+                                hipStream_t s);
+bool gemm_mfma_supported(const DeviceMatrix& w, int m);
+
+}  // namespace oq

@@ -1,0 +1,97 @@
+"""Seeded synthetic GGML tensors and activations for the quantized matrix workloads.
+
+Distributions (per workload definition):
+  q8_0 : d = fp16(|N(0, 0.02)| / 127), q ~ U{-127..127}
+  q4_K : d, dmin = fp16(|N(0, 0.02)| / 63); 8 scales and 8 mins ~ U{0..63} packed in GGML's
+         12-byte K-quant form; 4-bit q ~ U{0..15}
+  q5_K : as q4_K with a fifth bit ~ U{0,1} (32-byte qh plane)
+  q6_K : d = fp16(|N(0, 0.02)| / 63); sc ~ U{-32..31} (int8); 6-bit q ~ U{0..63} split into the
+         ql (low nibble) and qh (two high bits) planes
+  activations x ~ N(0, 1) in F32
+numpy's PCG64 generator makes every stream reproducible from its seed on any platform.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+Q4_K, Q5_K, Q6_K, Q8_0 = 12, 13, 14, 8
+
+
+def _f16_bits(v: np.ndarray) -> np.ndarray:
+    return v.astype(np.float16).view(np.uint16)
+
+
+def _u16_bytes(bits: np.ndarray) -> np.ndarray:
+    return bits.astype("<u2").view(np.uint8).reshape(-1, 2)
+
+
+def pack_scale_min_k4(sc: np.ndarray, mn: np.ndarray) -> np.ndarray:
+    """Inverse of the K-quant 6-bit (scale, min) unpack: (nb, 8) x2 -> (nb, 12) bytes.
+    Pairs 0..3 occupy the low six bits of bytes 0..3 / 4..7; pairs 4..7 keep their low nibbles
+    in bytes 8..11 (scale low, min high) and their top two bits in bits 6..7 of bytes 0..7."""
+    sc = sc.astype(np.uint8)
+    mn = mn.astype(np.uint8)
+    p = np.empty((sc.shape[0], 12), dtype=np.uint8)
+    p[:, 0:4] = sc[:, 0:4] | ((sc[:, 4:8] >> 4) << 6)
+    p[:, 4:8] = mn[:, 0:4] | ((mn[:, 4:8] >> 4) << 6)
+    p[:, 8:12] = (sc[:, 4:8] & 15) | ((mn[:, 4:8] & 15) << 4)
+    return p
+
+
+def _scale(rng: np.random.Generator, nb: int, div: float) -> np.ndarray:
+    return _f16_bits(np.abs(rng.normal(0.0, 0.02, nb)) / div)
+
+
+def q4_k(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    assert cols % 256 == 0
+    nb = rows * cols // 256
+    d = _u16_bytes(_scale(rng, nb, 63.0))
+    dmin = _u16_bytes(_scale(rng, nb, 63.0))
+    sc = rng.integers(0, 64, (nb, 8), dtype=np.uint8)
+    mn = rng.integers(0, 64, (nb, 8), dtype=np.uint8)
+    qs = np.frombuffer(rng.bytes(nb * 128), dtype=np.uint8).reshape(nb, 128)
+    return np.concatenate([d, dmin, pack_scale_min_k4(sc, mn), qs], axis=1).reshape(-1)
+
+
+def q5_k(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    assert cols % 256 == 0
+    nb = rows * cols // 256
+    d = _u16_bytes(_scale(rng, nb, 63.0))
+    dmin = _u16_bytes(_scale(rng, nb, 63.0))
+    sc = rng.integers(0, 64, (nb, 8), dtype=np.uint8)
+    mn = rng.integers(0, 64, (nb, 8), dtype=np.uint8)
+    qh = np.frombuffer(rng.bytes(nb * 32), dtype=np.uint8).reshape(nb, 32)
+    qs = np.frombuffer(rng.bytes(nb * 128), dtype=np.uint8).reshape(nb, 128)
+    return np.concatenate([d, dmin, pack_scale_min_k4(sc, mn), qh, qs], axis=1).reshape(-1)
+
+
+def q6_k(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    assert cols % 256 == 0
+    nb = rows * cols // 256
+    ql = np.frombuffer(rng.bytes(nb * 128), dtype=np.uint8).reshape(nb, 128)
+    qh = np.frombuffer(rng.bytes(nb * 64), dtype=np.uint8).reshape(nb, 64)
+    sc = rng.integers(-32, 32, (nb, 16), dtype=np.int8).view(np.uint8)
+    d = _u16_bytes(_scale(rng, nb, 63.0))
+    return np.concatenate([ql, qh, sc, d], axis=1).reshape(-1)
+
+
+def q8_0(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    assert cols % 32 == 0
+    nb = rows * cols // 32
+    d = _u16_bytes(_scale(rng, nb, 127.0))
+    q = rng.integers(-127, 128, (nb, 32), dtype=np.int8).view(np.uint8)
+    return np.concatenate([d, q], axis=1).reshape(-1)
+
+
+def weights(type_id: int, rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    gen = {Q4_K: q4_k, Q5_K: q5_k, Q6_K: q6_k, Q8_0: q8_0}[type_id]
+    return gen(rng, rows, cols)
+
+
+def activations(rng: np.random.Generator, m: int, k: int) -> np.ndarray:
+    return rng.standard_normal((m, k), dtype=np.float32)
+
+
+def row_bytes(type_id: int, cols: int) -> int:
+    per = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34)}[type_id]
+    return cols // per[0] * per[1]

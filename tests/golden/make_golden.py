@@ -1,0 +1,125 @@
+"""Write the golden vectors under tests/golden/.
+
+1. ref_kat.json -- the reference's own known-answer fixtures for the quantized path
+   (tests/test_phase2a.cpp:50-106,132-289 of the reference): block recipes and the values the
+   reference asserts for them.  They are restated here as data (bytes in hex, expected floats).
+2. ref_random.npz -- seeded random rows run through the reference's own decoder and matvec,
+   compiled from its sources into oracle/_ref/libref.so (oracle/Makefile).  Q4_K has no
+   reference decoder; its vectors are the reference's Q5_K results on the same blocks with an
+   all-zero fifth-bit plane, which GGML's Q4_K format must reproduce exactly.
+
+Run from the repository root after `make -C oracle all ref`:  python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[2]
+sys.path.insert(0, str(ROOT))
+import oracle  # noqa: E402
+from oracle_amd import synth  # noqa: E402
+
+OUT = Path(__file__).resolve().parent
+
+
+def u16le(v: int) -> list[int]:
+    return [v & 0xFF, v >> 8]
+
+
+def kat() -> dict:
+    # Q5_K: d = 0.5 (0x3800), dmin = 0.25 (0x3400), scales bytes {2,2,2,2,3,3,3,3,0x32 x4},
+    # qh = 0xFF x32, qs = 0x21 x128 -> 16.25 (low nibbles) / 17.25 (high nibbles)
+    q5 = u16le(0x3800) + u16le(0x3400) + [2, 2, 2, 2, 3, 3, 3, 3, 0x32, 0x32, 0x32, 0x32] + [0xFF] * 32 + [0x21] * 128
+    q5_second = q5[:16] + [0] * 160  # qh and qs cleared -> every element -0.75
+    # Q6_K: ql = 0x21 x128, qh = 0xFF x64, sc = 2 x16, d = 0.5 -> 17 (lower 64) / 18 (upper 64)
+    q6 = [0x21] * 128 + [0xFF] * 64 + [0x02] * 16 + u16le(0x3800)
+    q8_quants = [0, 1, -1, 127, -128, 2, -2, 3, -3, 4, -4, 5, -5, 6, -6, 7,
+                 -7, 8, -8, 9, -9, 10, -10, 11, -11, 12, -12, 13, -13, 14, -14, 15]
+    q8 = u16le(0x3C00) + [q & 0xFF for q in q8_quants]
+    q8_second = u16le(0x3800) + [10] * 32
+    q8_second_row = u16le(0x3800) + [4] * 32
+    hexs = lambda b: bytes(b).hex()  # noqa: E731
+    return {
+        "source": "reference tests/test_phase2a.cpp (known-answer fixtures of the quantized path)",
+        "f16": [[0x3C00, 1.0], [0xC000, -2.0], [0x0001, 2.0 ** -24]],
+        "f16_special": {"inf": 0x7C00, "nan": 0x7E00, "neg_zero": 0x8000},
+        "bf16": [[0x3F80, 1.0], [0xC000, -2.0]],
+        "f16_row": {"bits": [0x3C00, 0xC000, 0x4200, 0x0000], "expected": [1.0, -2.0, 3.0, 0.0]},
+        "bf16_row": {"bits": [0x3F80, 0xC000, 0x4040, 0x0000], "expected": [1.0, -2.0, 3.0, 0.0]},
+        "q5_k": {"block": hexs(q5), "low": 16.25, "high": 17.25, "dot_ones": 4288.0,
+                 "dot_ones_two_blocks": 8576.0},
+        "q5_k_matvec": {"rows": [hexs(q5), hexs(q5_second)], "expected": [4288.0, -192.0]},
+        "q6_k": {"block": hexs(q6), "lower": 17.0, "upper": 18.0, "dot_ones": 4480.0},
+        "q8_0": {"block": hexs(q8), "expected": q8_quants, "dot_ones": 14.0},
+        "q8_0_two_blocks": {"blocks": hexs(q8 + q8_second), "at3": 127.0, "at32": 5.0, "at63": 5.0},
+        "q8_0_matvec": {"rows": [hexs(q8), hexs(q8_second_row)], "expected": [14.0, 64.0]},
+    }
+
+
+def random_vectors() -> dict[str, np.ndarray]:
+    rng = np.random.default_rng(20261201)
+    out: dict[str, np.ndarray] = {}
+    rows, cols = 4, 512
+    cases = {
+        "q5_k": (13, synth.q5_k(rng, rows, cols)),
+        "q6_k": (14, synth.q6_k(rng, rows, cols)),
+        "q8_0": (8, synth.q8_0(rng, rows, cols)),
+        # raw random bytes with finite, moderate scales: every quant bit pattern is reachable
+        "q5_k_raw": (13, None),
+        "q6_k_raw": (14, None),
+        "q8_0_raw": (8, None),
+    }
+    for name, (t, data) in list(cases.items()):
+        if data is None:
+            rb = synth.row_bytes(t, cols)
+            data = np.frombuffer(rng.bytes(rows * rb), dtype=np.uint8).copy()
+            blk = {13: 176, 14: 210, 8: 34}[t]
+            view = data.reshape(-1, blk)
+            dpos = {13: [0, 2], 14: [208], 8: [0]}[t]
+            for p in dpos:  # finite f16 scales in [2^-15, 2^-1), sign random
+                e = rng.integers(0, 15, view.shape[0]).astype(np.uint16)
+                bits = (rng.integers(0, 2, view.shape[0]).astype(np.uint16) << 15) | (e << 10) | \
+                    rng.integers(0, 1024, view.shape[0]).astype(np.uint16)
+                view[:, p:p + 2] = bits.astype("<u2").view(np.uint8).reshape(-1, 2)
+        cases[name] = (t, data)
+    x = rng.standard_normal(cols, dtype=np.float32)
+    out["x"] = x
+    for name, (t, data) in cases.items():
+        dec = np.stack([oracle.ref_decode_row(t, cols, data.reshape(rows, -1)[r]) for r in range(rows)])
+        y = oracle.ref_storage_matvec(t, rows, cols, data, x)
+        out[f"{name}_type"] = np.array([t])
+        out[f"{name}_bytes"] = data
+        out[f"{name}_decoded_bits"] = dec.view(np.uint32)
+        out[f"{name}_matvec_bits"] = y.view(np.uint32)
+    # Q4_K via the Q5_K decoder with qh = 0 (the same 144-byte block without the qh plane)
+    q5 = synth.q5_k(rng, rows, cols).reshape(-1, 176)
+    q5[:, 16:48] = 0
+    q5 = q5.reshape(-1)
+    q4 = np.concatenate([q5.reshape(-1, 176)[:, :16], q5.reshape(-1, 176)[:, 48:]], axis=1).reshape(-1)
+    out["q4_k_bytes"] = q4
+    out["q4_k_decoded_bits"] = np.stack(
+        [oracle.ref_decode_row(13, cols, q5.reshape(rows, -1)[r]) for r in range(rows)]).view(np.uint32)
+    out["q4_k_matvec_bits"] = oracle.ref_storage_matvec(13, rows, cols, q5, x).view(np.uint32)
+    # F16 / BF16 / F32 rows, all bit patterns of f16 included once
+    f16_bits = np.arange(65536, dtype=np.uint16)
+    out["f16_all_bits"] = f16_bits
+    out["f16_all_decoded_bits"] = oracle.ref_decode_row(1, 65536, f16_bits.view(np.uint8)).view(np.uint32)
+    out["bf16_sample_bits"] = rng.integers(0, 65536, 4096, dtype=np.uint16)
+    out["bf16_sample_decoded_bits"] = oracle.ref_decode_row(30, 4096, out["bf16_sample_bits"].view(np.uint8)).view(np.uint32)
+    return out
+
+
+def main() -> None:
+    if not oracle.ref_available():
+        raise SystemExit("oracle/_ref/libref.so is not built: run `make -C oracle ref` first")
+    (OUT / "ref_kat.json").write_text(json.dumps(kat(), indent=1) + "\n")
+    np.savez_compressed(OUT / "ref_random.npz", **random_vectors())
+    print("wrote", OUT / "ref_kat.json", OUT / "ref_random.npz")
+
+
+if __name__ == "__main__":
+    main()

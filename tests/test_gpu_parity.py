@@ -1,0 +1,304 @@
+"""GPU parity through the C ABI against the CPU oracle on identical seeded inputs.
+
+Bars: dequantized rows and Q8_K blocks bit-exact; products within
+    |y_gpu - y_ref| <= 1e-4 * sum_k |w_k * xhat_k|   per output,
+where y_ref is the reference's sequential F32 dot (oracle) of the decoded row with xhat, the F32
+activation (q8_0 and plain rows) or the dequantized Q8_K activation (K-quant rows).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import oracle_amd
+from oracle_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+THREADS = min(16, oracle.default_threads())
+KQ = (12, 13, 14)
+
+
+def weights(t, rng, rows, cols):
+    if t in (12, 13, 14, 8):
+        return synth.weights(t, rng, rows, cols)
+    if t == 0:
+        return rng.standard_normal(rows * cols).astype(np.float32).view(np.uint8)
+    if t == 1:
+        return (rng.standard_normal(rows * cols) * 0.1).astype(np.float16).view(np.uint8)
+    bits = (rng.standard_normal(rows * cols).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    return bits.view(np.uint8)
+
+
+def reference_products(t, rows, cols, data, x):
+    """Oracle y (F32 sequential dots), normaliser sum|w xhat| per output, for x of shape [m, cols]."""
+    x = np.atleast_2d(x)
+    ys, norms = [], []
+    for xm in x:
+        xhat = oracle.dequantize_q8k(oracle.quantize_q8k(xm), cols) if t in KQ else xm
+        ys.append(oracle.storage_matvec(t, rows, cols, data, xhat, threads=THREADS))
+        norms.append(oracle.matvec_stats(t, rows, cols, data, xhat, threads=THREADS)[1])
+    return np.stack(ys), np.stack(norms)
+
+
+def check_close(y_gpu, y_ref, norm, tol=TOL):
+    err = np.abs(y_gpu.astype(np.float64) - y_ref.astype(np.float64))
+    bound = tol * np.maximum(norm, 1e-30)
+    worst = float(np.max(err / np.maximum(norm, 1e-30)))
+    assert np.all(err <= bound), f"max normalised error {worst:.3e} > {tol}"
+    return worst
+
+
+def gpu_matmul(ctx, w, x, rows):
+    x = np.atleast_2d(np.ascontiguousarray(x, np.float32))
+    xb = ctx.to_device(x)
+    yb = ctx.alloc(x.shape[0] * rows * 4)
+    if x.shape[0] == 1:
+        ctx.matvec(w, xb, yb)
+    else:
+        ctx.matmul(w, x.shape[0], xb, yb)
+    y = yb.download(np.float32, x.shape[0] * rows).reshape(x.shape[0], rows)
+    xb.free()
+    yb.free()
+    return y
+
+
+# ---------------------------------------------------------------- dequantization (bit-exact)
+
+@pytest.mark.parametrize("t,rows,cols", [
+    (12, 37, 4096), (12, 5, 256), (13, 19, 1024), (14, 23, 4096), (14, 3, 768),
+    (8, 29, 4096), (8, 4, 96), (0, 7, 33), (1, 9, 1000), (30, 6, 130)])
+def test_dequantize_bit_exact(ctx, t, rows, cols):
+    rng = np.random.default_rng(1000 + t * 7 + cols)
+    data = weights(t, rng, rows, cols)
+    w = ctx.upload(t, cols, rows, data)
+    out = ctx.alloc(rows * cols * 4)
+    ctx.dequantize_rows(w, 0, rows, out)
+    got = out.download(np.float32, rows * cols).reshape(rows, cols)
+    want = oracle.decode_matrix(t, cols, rows, data)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # a row window
+    r0, nr = rows // 3, max(1, rows // 2)
+    ctx.dequantize_rows(w, r0, nr, out)
+    part = out.download(np.float32, nr * cols).reshape(nr, cols)
+    assert np.array_equal(part.view(np.uint32), want[r0:r0 + nr].view(np.uint32))
+    out.free()
+    w.release()
+
+
+def test_dequantize_golden_vectors(ctx, golden):
+    for name in ("q5_k", "q6_k", "q8_0", "q5_k_raw", "q6_k_raw", "q8_0_raw", "q4_k"):
+        t = int(golden[f"{name}_type"][0]) if f"{name}_type" in golden else 12
+        rows, cols = golden[f"{name}_decoded_bits"].shape
+        got = oracle_amd.decode_rows(ctx, t, cols, rows, golden[f"{name}_bytes"])
+        assert np.array_equal(got.view(np.uint32), golden[f"{name}_decoded_bits"]), name
+    # every binary16 pattern, NaN payloads included
+    got = oracle_amd.decode_rows(ctx, 1, 65536, 1, golden["f16_all_bits"].view(np.uint8))
+    assert np.array_equal(got.reshape(-1).view(np.uint32), golden["f16_all_decoded_bits"])
+
+
+def test_dequantize_rejects_rows_out_of_range(ctx):
+    rng = np.random.default_rng(5)
+    w = ctx.upload(12, 256, 4, synth.q4_k(rng, 4, 256))
+    out = ctx.alloc(4 * 256 * 4)
+    with pytest.raises(oracle_amd.OutOfRange):
+        ctx.dequantize_rows(w, 3, 2, out)
+    ctx.dequantize_rows(w, 4, 0, out)  # empty window at the end is fine
+    out.free()
+    w.release()
+
+
+# ---------------------------------------------------------------- Q8_K quantization (bit-exact)
+
+def q8k_cases(rng):
+    x = rng.standard_normal((5, 1024)).astype(np.float32)
+    x[0, :256] = 0.0                                   # all-zero block
+    x[1, :256] = 0.0
+    x[1, 10], x[1, 200] = -3.0, 3.0                    # tie, first index negative
+    x[1, 300], x[1, 301] = 7.0, -7.0                   # tie, first index positive
+    x[2, :256] *= 1e-35                                # subnormal-range scale
+    x[2, 256:512] *= 1e30
+    x[3, :] = np.round(x[3, :] * 4) / 4                # many exact halves after scaling
+    x[4, 0:256] = np.linspace(-127, 127, 256, dtype=np.float32)
+    return x
+
+
+def test_quantize_q8k_bit_exact(ctx):
+    rng = np.random.default_rng(17)
+    x = q8k_cases(rng)
+    m, k = x.shape
+    xb = ctx.to_device(x)
+    qb = ctx.alloc(m * k // 256 * 292)
+    ctx.quantize_q8k(xb, m, k, qb)
+    got = qb.download(np.uint8)
+    want = np.concatenate([oracle.quantize_q8k(row) for row in x])
+    assert np.array_equal(got, want)
+    xb.free()
+    qb.free()
+
+
+def test_quantize_q8k_rejects_ragged(ctx):
+    xb = ctx.alloc(300 * 4)
+    qb = ctx.alloc(292 * 2)
+    with pytest.raises(oracle_amd.InvalidArgument):
+        ctx.quantize_q8k(xb, 1, 300, qb)
+    xb.free()
+    qb.free()
+
+
+# ---------------------------------------------------------------- products (tolerance)
+
+@pytest.mark.parametrize("t,rows,cols", [
+    (12, 301, 4096), (12, 64, 256), (12, 17, 768), (12, 40, 12288),
+    (13, 77, 4096), (14, 129, 4096), (14, 33, 512), (14, 16, 12288),
+    (8, 203, 4096), (8, 20, 96), (0, 33, 100), (1, 31, 1000), (30, 10, 512)])
+def test_matvec_tolerance(ctx, t, rows, cols):
+    rng = np.random.default_rng(2000 + t + rows)
+    data = weights(t, rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    w = ctx.upload(t, cols, rows, data)
+    y = gpu_matmul(ctx, w, x, rows)
+    y_ref, norm = reference_products(t, rows, cols, data, x)
+    check_close(y, y_ref, norm)
+    w.release()
+
+
+@pytest.mark.parametrize("t", KQ)
+def test_matvec_q8k_matches_integer_oracle(ctx, t):
+    rng = np.random.default_rng(31 + t)
+    rows, cols = 96, 2048
+    data = synth.weights(t, rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    q8 = oracle.quantize_q8k(x)
+    w = ctx.upload(t, cols, rows, data)
+    qb = ctx.to_device(q8)
+    yb = ctx.alloc(rows * 4)
+    ctx.matvec_q8k(w, qb, yb)
+    y = yb.download(np.float32, rows)
+    ints = np.array([oracle.vec_dot_q8k(t, cols, r, q8) for r in data.reshape(rows, -1)], np.float32)
+    _, norm = oracle.matvec_stats(t, rows, cols, data, oracle.dequantize_q8k(q8, cols), threads=THREADS)
+    check_close(y, ints, norm, tol=2e-6)
+    for b in (qb, yb):
+        b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("t", [12, 14, 8])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 8, 11])
+def test_matmul_small_batch(ctx, t, m):
+    rng = np.random.default_rng(400 + 10 * t + m)
+    rows, cols = 130, 2048
+    data = synth.weights(t, rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(t, cols, rows, data)
+    y = gpu_matmul(ctx, w, x, rows)
+    y_ref, norm = reference_products(t, rows, cols, data, x)
+    check_close(y, y_ref, norm)
+    w.release()
+
+
+@pytest.mark.parametrize("env", [{"OQ_GEMV_ROWS": "2"}, {"OQ_FUSED_QUANT": "0"}, {"OQ_GEMV_MAX_WG": "7"}])
+def test_launch_variants_agree(ctx, env):
+    rng = np.random.default_rng(77)
+    rows, cols = 211, 4096
+    results = {}
+    for t in KQ:
+        data = synth.weights(t, rng, rows, cols)
+        x = rng.standard_normal((3, cols)).astype(np.float32)
+        w = ctx.upload(t, cols, rows, data)
+        base = gpu_matmul(ctx, w, x, rows)
+        old = {k: os.environ.get(k) for k in env}
+        os.environ.update(env)
+        try:
+            var = gpu_matmul(ctx, w, x, rows)
+        finally:
+            for k, v in old.items():
+                if v is None:
+                    os.environ.pop(k, None)
+                else:
+                    os.environ[k] = v
+        y_ref, norm = reference_products(t, rows, cols, data, x)
+        check_close(var, y_ref, norm)
+        results[t] = np.max(np.abs(var - base))
+        w.release()
+
+
+def test_matvec_deterministic(ctx):
+    rng = np.random.default_rng(8)
+    rows, cols = 1000, 4096
+    data = synth.q4_k(rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    w = ctx.upload(12, cols, rows, data)
+    a = gpu_matmul(ctx, w, x, rows)
+    b = gpu_matmul(ctx, w, x, rows)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    w.release()
+
+
+# ---------------------------------------------------------------- argument errors through the ABI
+
+def test_abi_argument_errors(ctx):
+    rng = np.random.default_rng(9)
+    data = synth.q4_k(rng, 4, 512)
+    with pytest.raises(oracle_amd.InvalidArgument):
+        ctx.upload(12, 512, 4, data[:-1])                # byte size mismatch
+    with pytest.raises(oracle_amd.InvalidArgument):
+        ctx.upload(12, 512, 0, data)                     # zero rows
+    with pytest.raises(oracle_amd.UnsupportedType):
+        ctx.upload(12, 500, 4, data)                     # ragged row
+    with pytest.raises(oracle_amd.UnsupportedType):
+        ctx.upload(99, 512, 4, data)                     # unregistered type
+    with pytest.raises(oracle_amd.InvalidArgument):
+        ctx.upload(2, 512, 4, np.zeros(4 * 16 * 18, np.uint8))  # q4_0: registered, not decodable
+    w8 = ctx.upload(8, 512, 4, synth.q8_0(rng, 4, 512))
+    qb = ctx.alloc(2 * 292)
+    yb = ctx.alloc(16)
+    with pytest.raises(oracle_amd.InvalidArgument):
+        ctx.matvec_q8k(w8, qb, yb)                       # Q8_K activations need a K-quant weight
+    w4 = ctx.upload(12, 512, 4, data)
+    xb = ctx.alloc(512 * 4 + 16)
+
+    class Shifted:
+        ptr = xb.ptr + 4
+    with pytest.raises(oracle_amd.InvalidArgument):
+        ctx.matvec(w4, Shifted, yb)                      # misaligned activations
+    with pytest.raises(oracle_amd.InvalidArgument):
+        ctx.matmul(w4, 0, xb, yb)
+    for b in (qb, yb, xb):
+        b.free()
+    w8.release()
+    w4.release()
+
+
+# ---------------------------------------------------------------- graph replay
+
+def test_graph_replay_matches_eager(ctx):
+    rng = np.random.default_rng(21)
+    rows, cols = 512, 4096
+    ws = [ctx.upload(t, cols, rows, synth.weights(t, rng, rows, cols)) for t in (12, 14, 8)]
+    x = rng.standard_normal(cols).astype(np.float32)
+    xb = ctx.to_device(x)
+    ybs = [ctx.alloc(rows * 4) for _ in ws]
+    for w, yb in zip(ws, ybs):
+        ctx.matvec(w, xb, yb)
+    ctx.sync()
+    eager = [yb.download(np.float32, rows) for yb in ybs]
+    ctx.capture_begin()
+    for w, yb in zip(ws, ybs):
+        ctx.matvec(w, xb, yb)
+    g = ctx.capture_end()
+    for rep in range(3):
+        for yb in ybs:  # clobber outputs with eager work between replays
+            ctx.matvec(ws[0], xb, ybs[0])
+            yb.upload(np.full(rows, np.nan, np.float32))
+        g.launch()
+        ctx.sync()
+        for e, yb in zip(eager, ybs):
+            assert np.array_equal(yb.download(np.float32, rows).view(np.uint32), e.view(np.uint32)), rep
+    g.destroy()
+    for b in ybs + [xb]:
+        b.free()
+    for w in ws:
+        w.release()
