@@ -168,7 +168,7 @@ int upload_common(oq_context* ctx, uint32_t type, uint64_t ne0, uint64_t ne1, co
         (void)hipFree(dst);
         return rc;
     };
-    const bool identity = pitch == rb && type != OQ_TYPE_Q6_K && type != OQ_TYPE_Q8_0;
+    const bool identity = pitch == rb && (type == OQ_TYPE_F32 || type == OQ_TYPE_F16 || type == OQ_TYPE_BF16);
     hipError_t e = hipSuccess;
     if (identity) {
         e = hipMemcpyAsync(dst, bytes, nbytes, from_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,

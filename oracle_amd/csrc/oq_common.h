@@ -79,6 +79,42 @@ OQ_DEVICE int quad_sum_int(int v) {
     return v;
 }
 
+// DPP lane exchanges (GFX9 encodings): quad_perm [1,0,3,2] = lane^1, [2,3,0,1] = lane^2,
+// row_half_mirror = 7-i within 8 lanes, row_mirror = 15-i within 16 lanes.
+constexpr int kDppQuadXor1 = 0xB1;
+constexpr int kDppQuadXor2 = 0x4E;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL>
+OQ_DEVICE int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+OQ_DEVICE float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over each row of 16 lanes, left in every lane of the row.
+OQ_DEVICE float row16_sum(float v) {
+    v += dpp_f<kDppQuadXor1>(v);
+    v += dpp_f<kDppQuadXor2>(v);
+    v += dpp_f<kDppRowHalfMirror>(v);
+    v += dpp_f<kDppRowMirror>(v);
+    return v;
+}
+
+OQ_DEVICE float readlane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Sum over the 64 lanes of a wave; the result is wave-uniform.  Fixed association order, so
+// results are deterministic run to run.
+OQ_DEVICE float wave_sum_uniform(float v) {
+    v = row16_sum(v);
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+
 // ------------------------------------------------------------------ Q8_K
 
 // Result of quantizing one 256-value block with one wave: lane l owns values 4l..4l+3.

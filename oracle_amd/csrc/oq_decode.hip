@@ -5,6 +5,7 @@
 // F32 it writes has the bits the reference's scalar decoder produces, because the arithmetic
 // is the same sequence of correctly rounded operations with contraction off.
 #include "oq_common.h"
+#include "oq_layout.h"
 
 namespace oq {
 
@@ -24,9 +25,9 @@ uint64_t device_pitch(uint32_t type, uint64_t k) {
 
 // ------------------------------------------------------------------ relayout (upload)
 
-// GGML rows (contiguous, row_bytes each) -> device rows at `pitch`.  Plain types and q4_K/q5_K
-// keep their bytes; q6_K and q8_0 blocks are split into per-row planes so every plane starts
-// 16-byte aligned (210- and 34-byte blocks are not).
+// GGML rows (contiguous, row_bytes each) -> device rows at `pitch`.  Plain types keep their
+// bytes; quantized blocks are split into per-row planes, so that every plane starts 16-byte
+// aligned (210- and 34-byte blocks are not) and a wave streaming a row reads contiguous bytes.
 __global__ void relayout_kernel(uint32_t type, uint64_t k, uint64_t n, const uint8_t* __restrict__ src,
                                 uint8_t* __restrict__ dst, uint64_t row_bytes, uint64_t pitch) {
     const uint64_t total = n * row_bytes;
@@ -35,14 +36,25 @@ __global__ void relayout_kernel(uint32_t type, uint64_t k, uint64_t n, const uin
         const uint64_t r = t / row_bytes, off = t % row_bytes;
         uint64_t o;
         if (type == 14) {
-            const uint64_t nsb = k / kQK, sb = off / kQ6KBytes, b = off % kQ6KBytes;
-            if (b < 128) o = sb * 128 + b;
+            const uint64_t nsb = k / kQK, sb = off / kQ6KBytes;
+            const uint32_t b = (uint32_t)(off % kQ6KBytes);
+            if (b < 128) o = q6_ql_offset(nsb, sb, b);
             else if (b < 192) o = 128 * nsb + sb * 64 + (b - 128);
-            else if (b < 208) o = 192 * nsb + sb * 16 + (b - 192);
+            else if (b < 208) o = 192 * nsb + sb * 16 + q6_sc_offset(b - 192);
             else o = 208 * nsb + sb * 2 + (b - 208);
         } else if (type == 8) {
             const uint64_t nb = k / 32, blk = off / kQ80Bytes, b = off % kQ80Bytes;
             o = b < 2 ? 32 * nb + blk * 2 + b : blk * 32 + (b - 2);
+        } else if (type == 12) {
+            const uint64_t nsb = k / kQK, sb = off / kQ4KBytes;
+            const uint32_t b = (uint32_t)(off % kQ4KBytes);
+            o = b < 16 ? 128 * nsb + sb * 16 + b : q45_qs_offset(nsb, sb, b - 16);
+        } else if (type == 13) {
+            const uint64_t nsb = k / kQK, sb = off / kQ5KBytes;
+            const uint32_t b = (uint32_t)(off % kQ5KBytes);
+            if (b < 16) o = 160 * nsb + sb * 16 + b;
+            else if (b < 48) o = 128 * nsb + sb * 32 + (b - 16);
+            else o = q45_qs_offset(nsb, sb, b - 48);
         } else {
             o = off;
         }
@@ -79,18 +91,19 @@ OQ_DEVICE uint32_t ld_u32(const uint8_t* p) {
     return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
 }
 
-// one element of a q4_K / q5_K super-block (storage_decode.cpp:63-94 element map)
-OQ_DEVICE float decode_q45k_elem(const uint8_t* blk, uint32_t ii, bool q5) {
+// one element of a q4_K / q5_K super-block (storage_decode.cpp:63-94 element map), given the
+// row, the block's 16-byte header {d, dmin, scales[12]} and (q5_K) its 32 fifth-bit bytes
+OQ_DEVICE float decode_q45k_elem(const uint8_t* row, uint64_t nsb, uint64_t sb, const uint8_t* hdr,
+                                 const uint8_t* qh, uint32_t ii) {
 #pragma clang fp contract(off)
-    const float d = f16_bits_to_f32(ld_u16(blk));
-    const float dmin = f16_bits_to_f32(ld_u16(blk + 2));
+    const float d = f16_bits_to_f32(ld_u16(hdr));
+    const float dmin = f16_bits_to_f32(ld_u16(hdr + 2));
     const uint32_t g = ii / 64, hi = (ii % 64) / 32, l = ii % 32;
     uint32_t sc, mn;
-    scale_min_k4(2 * g + hi, ld_u32(blk + 4), ld_u32(blk + 8), ld_u32(blk + 12), sc, mn);
-    const uint8_t* qs = blk + (q5 ? 48 : 16);
-    const uint32_t byte = qs[g * 32 + l];
+    scale_min_k4(2 * g + hi, ld_u32(hdr + 4), ld_u32(hdr + 8), ld_u32(hdr + 12), sc, mn);
+    const uint32_t byte = row[q45_qs_offset(nsb, sb, g * 32 + l)];
     uint32_t q = hi ? (byte >> 4) : (byte & 15u);
-    if (q5 && ((blk[16 + l] >> (2 * g + hi)) & 1u)) q += 16u;
+    if (qh && ((qh[l] >> (2 * g + hi)) & 1u)) q += 16u;
     const float ds = d * (float)sc;
     const float mm = dmin * (float)mn;
     return ds * (float)q - mm;
@@ -115,22 +128,30 @@ __global__ void dequantize_kernel(DeviceMatrix w, uint64_t row0, uint64_t nrows,
                 v = d * (float)(int8_t)row[i];
                 break;
             }
-            case 12: v = decode_q45k_elem(row + (i / kQK) * kQ4KBytes, (uint32_t)(i % kQK), false); break;
-            case 13: v = decode_q45k_elem(row + (i / kQK) * kQ5KBytes, (uint32_t)(i % kQK), true); break;
+            case 12: {  // planes qs | hdr[nsb][16]
+                const uint64_t nsb = w.k / kQK, sb = i / kQK;
+                v = decode_q45k_elem(row, nsb, sb, row + 128 * nsb + sb * 16, nullptr, (uint32_t)(i % kQK));
+                break;
+            }
+            case 13: {  // planes qs | qh[nsb][32] | hdr[nsb][16]
+                const uint64_t nsb = w.k / kQK, sb = i / kQK;
+                v = decode_q45k_elem(row, nsb, sb, row + 160 * nsb + sb * 16, row + 128 * nsb + sb * 32,
+                                     (uint32_t)(i % kQK));
+                break;
+            }
             case 14: {
                 // storage_decode.cpp:96-125 element map over the plane layout
                 const uint64_t nsb = w.k / kQK, sb = i / kQK;
                 const uint32_t ii = (uint32_t)(i % kQK);
                 const uint32_t h = ii / 128, sg = (ii % 128) / 32, l = ii % 32;
-                const uint8_t* ql = row + sb * 128;
                 const uint8_t* qh = row + 128 * nsb + sb * 64;
                 const int8_t* sc = (const int8_t*)(row + 192 * nsb + sb * 16);
                 const float d = f16_bits_to_f32(ld_u16(row + 208 * nsb + sb * 2));
-                const uint32_t lb = ql[64 * h + l + 32 * (sg & 1)];
+                const uint32_t lb = row[q6_ql_offset(nsb, sb, 64 * h + l + 32 * (sg & 1))];
                 const uint32_t low = sg >= 2 ? (lb >> 4) : (lb & 15u);
                 const uint32_t high = (qh[32 * h + l] >> (2 * sg)) & 3u;
                 const int q = (int)(low | (high << 4)) - 32;
-                const int scale = sc[8 * h + l / 16 + 2 * sg];
+                const int scale = sc[q6_sc_offset(8 * h + l / 16 + 2 * sg)];
                 const float ds = d * (float)scale;
                 v = ds * (float)q;
                 break;

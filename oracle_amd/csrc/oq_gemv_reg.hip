@@ -1,0 +1,546 @@
+// Decode GEMV and small-batch products (m <= 8) for K-quant weights (q4_K, q5_K, q6_K) against
+// Q8_K activations.
+//
+// y[m][n] = sum_k W[n][k] * x[m][k]; arithmetic as GGML's vec_dot_qX_K_q8_K: int8 dot products of
+// the weight quants with the Q8_K activation quants, block scales applied in F32 (reference
+// semantics: reference_storage_matvec, src/backend/cpu/quantized_reference.cpp:128-162, applied to
+// each activation row as the reference's multi-token evaluation does).
+//
+// Weights stream from the permuted row planes of oq_layout.h: in pass P (16 super-blocks) lane
+// l = 4*s + q loads chunks 128P + l and 128P + 4m + l -- every load instruction of the wave reads
+// 1 KiB of consecutive bytes -- and gets, for q4_K/q5_K, both halves of 64-element group q of
+// super-block s (one header / scale unpack per 64 weights), for q6_K the low and high segments
+// sharing one 16-byte high-bit chunk and four scales.
+//
+// Activations: each workgroup stages the Q8_K form of its m rows once in LDS, quantizing F32 x
+// itself (one wave per 256-block, DPP reductions; bit-identical to quantize_q8k_kernel) or copying
+// Q8_K blocks.  For m = 1 every lane then keeps its 64 quants, scale and 16-element sums in
+// registers (its slot is the same in every row); for m > 1 they are read from LDS per use, so each
+// weight byte is decoded once for all m rows.  Weight loads for the first rows are issued before
+// the staging completes.  Row sums: DPP row reductions + readlane in a fixed order.
+#include "oq_common.h"
+#include "oq_layout.h"
+
+namespace oq {
+
+namespace {
+
+constexpr int kMaxIters = 4;  // passes of 16 super-blocks: K <= 16384
+constexpr uint64_t kLdsBudget = 64 * 1024;
+
+OQ_DEVICE uint4 ldg128(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+OQ_DEVICE uint32_t ldg32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+OQ_DEVICE int dot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+OQ_DEVICE float h2f(uint32_t bits16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16); }
+
+OQ_DEVICE float row16_max(float v) {
+    v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppRowMirror>(v));
+    return v;
+}
+OQ_DEVICE int row16_min(int v) {
+    v = min(v, dpp_i<kDppQuadXor1>(v));
+    v = min(v, dpp_i<kDppQuadXor2>(v));
+    v = min(v, dpp_i<kDppRowHalfMirror>(v));
+    v = min(v, dpp_i<kDppRowMirror>(v));
+    return v;
+}
+OQ_DEVICE float wave_max_uniform(float v) {
+    v = row16_max(v);
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+OQ_DEVICE int wave_min_uniform(int v) {
+    v = row16_min(v);
+    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// ---------------------------------------------------------------- LDS image of activation rows
+
+// per row: q8[K] | d[K/256] | bsum[K/16] (int32)
+struct ActLds {
+    uint8_t* base;
+    uint64_t k;
+    OQ_DEVICE uint64_t stride() const { return k + (k / kQK) * 4 + (k / 16) * 4; }
+    OQ_DEVICE int8_t* q(int mi) const { return reinterpret_cast<int8_t*>(base + mi * stride()); }
+    OQ_DEVICE float* d(int mi) const { return reinterpret_cast<float*>(base + mi * stride() + k); }
+    OQ_DEVICE int* bsum(int mi) const {
+        return reinterpret_cast<int*>(base + mi * stride() + k + (k / kQK) * 4);
+    }
+};
+uint64_t act_lds_bytes(uint64_t k, int m) { return (uint64_t)m * (k + (k / kQK) * 4 + (k / 16) * 4); }
+
+// GGML quantize_row_q8_K of one 256-block held by a wave (lane: values 4l..4l+3); returns the
+// lane's 4 quants, the 16-element sum of its quad (valid in every lane of the quad) and d.
+OQ_DEVICE void quantize_block(const float4 v, int lane, uint32_t& qword, int& bsum, float& d) {
+#pragma clang fp contract(off)
+    const float a0 = fabsf(v.x), a1 = fabsf(v.y), a2 = fabsf(v.z), a3 = fabsf(v.w);
+    const float amax = wave_max_uniform(fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
+    if (amax == 0.0f) {
+        qword = 0u;
+        bsum = 0;
+        d = 0.0f;
+        return;
+    }
+    int first = 1 << 30;  // first index reaching max |x| (the sequential scan keeps the first)
+    if (a3 == amax) first = 4 * lane + 3;
+    if (a2 == amax) first = 4 * lane + 2;
+    if (a1 == amax) first = 4 * lane + 1;
+    if (a0 == amax) first = 4 * lane + 0;
+    const int idx = wave_min_uniform(first);
+    const int sub = idx & 3;
+    const float mine = sub == 0 ? v.x : (sub == 1 ? v.y : (sub == 2 ? v.z : v.w));
+    const float maxv = readlane_f(mine, idx >> 2);
+    const float iscale = -127.0f / maxv;
+    const float vals[4] = {v.x, v.y, v.z, v.w};
+    qword = 0u;
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int q = (int)__builtin_rintf(iscale * vals[i]);
+        q = q < 127 ? q : 127;
+        sum += q;
+        qword |= ((uint32_t)q & 0xFFu) << (8 * i);
+    }
+    sum += dpp_i<kDppQuadXor1>(sum);
+    sum += dpp_i<kDppQuadXor2>(sum);
+    bsum = sum;
+    d = 1.0f / iscale;
+}
+
+OQ_DEVICE void store_block(const ActLds& s, int mi, uint64_t b, int lane, uint32_t qword, int bsum16_quad,
+                           float d) {
+    *reinterpret_cast<uint32_t*>(s.q(mi) + b * kQK + 4 * lane) = qword;
+    if ((lane & 3) == 0) s.bsum(mi)[b * 16 + (lane >> 2)] = bsum16_quad;
+    if (lane == 0) s.d(mi)[b] = d;
+}
+
+// Q8_K block copy: lane's quant dword, d, and bsums 2*(lane%8), +1 in one dword
+OQ_DEVICE void copy_block_store(const ActLds& s, int mi, uint64_t b, int lane, uint32_t qword, uint32_t bsdw,
+                                float d) {
+    *reinterpret_cast<uint32_t*>(s.q(mi) + b * kQK + 4 * lane) = qword;
+    if (lane < 8) {
+        s.bsum(mi)[b * 16 + 2 * lane] = (int)(int16_t)(bsdw & 0xFFFFu);
+        s.bsum(mi)[b * 16 + 2 * lane + 1] = (int)(int16_t)(bsdw >> 16);
+    }
+    if (lane == 0) s.d(mi)[b] = d;
+}
+
+// ---------------------------------------------------------------- per-lane activation slice
+
+struct Act {
+    uint4 x0, x1, x2, x3;  // 64 quants (4 pieces of 16; see piece offsets)
+    float d;
+    int b[4];              // 16-element sums of the 4 pieces
+};
+
+// element offset (within the 256-block) of piece i of lane slot q
+template <uint32_t TYPE>
+OQ_DEVICE int piece(int q, int i) {
+    if constexpr (TYPE == 14) return 128 * (q >> 1) + 16 * (q & 1) + 32 * i;
+    else return 64 * q + 16 * i;
+}
+
+template <uint32_t TYPE>
+OQ_DEVICE void slice_from_lds(Act& a, const ActLds& s, int mi, uint64_t sb, int q) {
+    const int8_t* qb = s.q(mi) + sb * kQK;
+    a.x0 = *reinterpret_cast<const uint4*>(qb + piece<TYPE>(q, 0));
+    a.x1 = *reinterpret_cast<const uint4*>(qb + piece<TYPE>(q, 1));
+    a.x2 = *reinterpret_cast<const uint4*>(qb + piece<TYPE>(q, 2));
+    a.x3 = *reinterpret_cast<const uint4*>(qb + piece<TYPE>(q, 3));
+    a.d = s.d(mi)[sb];
+    const int* bs = s.bsum(mi) + sb * 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a.b[i] = bs[piece<TYPE>(q, i) / 16];
+}
+
+// ---------------------------------------------------------------- weights
+
+struct W45 {
+    uint4 c0, c1, hdr;  // quant chunks e = 0, 1 of the lane's 64-element group; block header
+    uint4 h0, h1;       // q5_K: fifth-bit bytes l = 0..15, 16..31
+};
+struct W6 {
+    uint4 c0, c1, qh;  // ql chunks (segment parity 0, 1), high-bit chunk
+    uint32_t sc;       // four scales (segments 0..3)
+    uint32_t d;
+};
+template <uint32_t TYPE>
+struct WRegs {
+    using type = W45;
+};
+template <>
+struct WRegs<14> {
+    using type = W6;
+};
+
+template <uint32_t TYPE>
+OQ_DEVICE void load_w(typename WRegs<TYPE>::type& r, const uint8_t* row, uint64_t nsb, int it, int lane) {
+    const uint64_t m = nsb - 16u * it < 16 ? nsb - 16u * it : 16;
+    const uint64_t l = (uint64_t)lane < 4 * m ? (uint64_t)lane : 4 * m - 1;  // surplus lanes re-read
+    const uint64_t sb = 16u * it + (l >> 2);
+    const int q = (int)(l & 3);
+    r.c0 = ldg128(row + 16 * (128u * it + l));
+    r.c1 = ldg128(row + 16 * (128u * it + 4 * m + l));
+    if constexpr (TYPE == 14) {
+        r.qh = ldg128(row + 128 * nsb + 64 * sb + 16 * q);
+        r.sc = ldg32(row + 192 * nsb + 16 * sb + 4 * q);
+        r.d = *reinterpret_cast<const uint16_t*>(row + 208 * nsb + 2 * sb);
+    } else {
+        r.hdr = ldg128(row + (TYPE == 13 ? 160 : 128) * nsb + 16 * sb);
+        if constexpr (TYPE == 13) {
+            r.h0 = ldg128(row + 128 * nsb + 32 * sb);
+            r.h1 = ldg128(row + 128 * nsb + 32 * sb + 16);
+        }
+    }
+}
+
+// decoded, m-independent part of a lane's 64 weights
+struct Dec45 {
+    uint32_t lo[8], hi[8];  // 4-bit (5-bit) quants: lo pairs with pieces 0,1; hi with 2,3
+    float d, dmin;
+    int sc0, sc1, mn0, mn1;
+};
+struct Dec6 {
+    uint32_t s[4][4];  // 6-bit unsigned quants of segments 0..3
+    float d;
+    int sc[4];
+};
+
+template <uint32_t TYPE>
+OQ_DEVICE Dec45 decode_w(const W45& r, int q) {
+    Dec45 o;
+    o.d = h2f(r.hdr.x & 0xFFFFu);
+    o.dmin = h2f(r.hdr.x >> 16);
+    // the eight 6-bit (scale, min) pairs as four byte-vectors (GGML's K-quant packing)
+    const uint32_t p0 = r.hdr.y, p1 = r.hdr.z, p2 = r.hdr.w;
+    const bool low = q < 2;
+    const uint32_t scw = low ? (p0 & 0x3F3F3F3Fu) : ((p2 & 0x0F0F0F0Fu) | ((p0 >> 2) & 0x30303030u));
+    const uint32_t mnw = low ? (p1 & 0x3F3F3F3Fu) : (((p2 >> 4) & 0x0F0F0F0Fu) | ((p1 >> 2) & 0x30303030u));
+    const int sh = 16 * (q & 1);
+    o.sc0 = (int)((scw >> sh) & 0xFFu);
+    o.sc1 = (int)((scw >> (sh + 8)) & 0xFFu);
+    o.mn0 = (int)((mnw >> sh) & 0xFFu);
+    o.mn1 = (int)((mnw >> (sh + 8)) & 0xFFu);
+    const uint32_t w[8] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w, r.c1.x, r.c1.y, r.c1.z, r.c1.w};
+    const uint32_t hb[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        o.lo[i] = w[i] & 0x0F0F0F0Fu;
+        o.hi[i] = (w[i] >> 4) & 0x0F0F0F0Fu;
+        if constexpr (TYPE == 13) {
+            o.lo[i] |= ((hb[i] >> (2 * q)) & 0x01010101u) << 4;
+            o.hi[i] |= ((hb[i] >> (2 * q + 1)) & 0x01010101u) << 4;
+        }
+    }
+    return o;
+}
+
+template <uint32_t TYPE>
+OQ_DEVICE Dec6 decode_w(const W6& r, int) {
+    Dec6 o;
+    o.d = h2f(r.d);
+    const uint32_t c0[4] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w};
+    const uint32_t c1[4] = {r.c1.x, r.c1.y, r.c1.z, r.c1.w};
+    const uint32_t h[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        o.s[0][i] = (c0[i] & 0x0F0F0F0Fu) | ((h[i] << 4) & 0x30303030u);
+        o.s[1][i] = (c1[i] & 0x0F0F0F0Fu) | ((h[i] << 2) & 0x30303030u);
+        o.s[2][i] = ((c0[i] >> 4) & 0x0F0F0F0Fu) | (h[i] & 0x30303030u);
+        o.s[3][i] = ((c1[i] >> 4) & 0x0F0F0F0Fu) | ((h[i] >> 2) & 0x30303030u);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o.sc[i] = (int)(int8_t)(r.sc >> (8 * i));
+    return o;
+}
+
+OQ_DEVICE int dot16(const uint32_t* w, const uint4 x, int acc) {
+    acc = dot4(w[0], x.x, acc);
+    acc = dot4(w[1], x.y, acc);
+    acc = dot4(w[2], x.z, acc);
+    acc = dot4(w[3], x.w, acc);
+    return acc;
+}
+
+OQ_DEVICE float lane_dot(const Dec45& w, const Act& a) {
+    int slo = dot16(w.lo, a.x0, 0);
+    slo = dot16(w.lo + 4, a.x1, slo);
+    int shi = dot16(w.hi, a.x2, 0);
+    shi = dot16(w.hi + 4, a.x3, shi);
+    const int isum = w.sc0 * slo + w.sc1 * shi;
+    const int imin = w.mn0 * (a.b[0] + a.b[1]) + w.mn1 * (a.b[2] + a.b[3]);
+    return a.d * (w.d * (float)isum - w.dmin * (float)imin);
+}
+
+OQ_DEVICE float lane_dot(const Dec6& w, const Act& a) {
+    const int p0 = dot16(w.s[0], a.x0, 0) - 32 * a.b[0];
+    const int p1 = dot16(w.s[1], a.x1, 0) - 32 * a.b[1];
+    const int p2 = dot16(w.s[2], a.x2, 0) - 32 * a.b[2];
+    const int p3 = dot16(w.s[3], a.x3, 0) - 32 * a.b[3];
+    const int isum = w.sc[0] * p0 + w.sc[1] * p1 + w.sc[2] * p2 + w.sc[3] * p3;
+    return a.d * (w.d * (float)isum);
+}
+
+// ---------------------------------------------------------------- kernel
+
+template <uint32_t TYPE, int ITERS, int R>
+OQ_DEVICE void load_group(typename WRegs<TYPE>::type (&W)[R][ITERS], const DeviceMatrix& w, uint64_t grp,
+                          int lane) {
+    const uint64_t nsb = w.k / kQK;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        uint64_t row = grp * R + r;
+        row = row < w.n ? row : w.n - 1;
+        const uint8_t* base = w.base + row * w.pitch;
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) load_w<TYPE>(W[r][it], base, nsb, it, lane);
+    }
+}
+
+template <uint32_t TYPE, int ITERS, int R, int MT>
+OQ_DEVICE void finish_group(const typename WRegs<TYPE>::type (&W)[R][ITERS], const Act (&act)[ITERS],
+                            const ActLds& s, int m, const DeviceMatrix& w, uint64_t grp, int lane, float* y) {
+    const uint64_t nsb = w.k / kQK;
+    const int q = lane & 3;
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi) acc[r][mi] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const uint64_t sb = 16u * it + (lane >> 2);
+        if (sb >= nsb) continue;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const auto dec = decode_w<TYPE>(W[r][it], q);
+            if constexpr (MT == 1) {
+                acc[r][0] += lane_dot(dec, act[it]);
+            } else {
+#pragma unroll
+                for (int mi = 0; mi < MT; ++mi) {
+                    if (mi < m) {
+                        Act a;
+                        slice_from_lds<TYPE>(a, s, mi, sb, q);
+                        acc[r][mi] += lane_dot(dec, a);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) {
+        if (mi >= m) break;
+        float out = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = wave_sum_uniform(acc[r][mi]);
+            out = lane == r ? v : out;
+        }
+        const uint64_t row = grp * R + lane;
+        if (lane < R && row < w.n) y[(uint64_t)mi * w.n + row] = out;
+    }
+}
+
+template <uint32_t TYPE, int ITERS, int R, int MT, bool FUSED, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemv_kq_kernel(DeviceMatrix w, int m, const float* x,
+                                                             const uint8_t* q8k, float* __restrict__ y) {
+    using WR = typename WRegs<TYPE>::type;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave_in_wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
+    const uint64_t wave = (uint64_t)blockIdx.x * WAVES + wave_in_wg;
+    const uint64_t nw = (uint64_t)gridDim.x * WAVES;
+    const uint64_t nsb = w.k / kQK;
+    const uint64_t groups = (w.n + R - 1) / R;
+    const ActLds s{smem, w.k};
+    const bool active = wave < groups;
+    WR A[R][ITERS];
+
+    if constexpr (MT == 1) {
+        // Activation loads first (unconditional, clamped) so the waits before quantizing count
+        // only them; x and q8k are deliberately not __restrict__, so the fence below keeps them
+        // ahead of the weight loads, which then stay in flight through the staging.
+        constexpr int SBW = (ITERS * 16 + WAVES - 1) / WAVES;
+        float4 xv[SBW];
+        uint32_t qv[SBW], bv[SBW];
+        float dv[SBW];
+#pragma unroll
+        for (int j = 0; j < SBW; ++j) {
+            uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+            b = b < nsb ? b : nsb - 1;
+            if constexpr (FUSED) {
+                xv[j] = reinterpret_cast<const float4*>(x + b * kQK)[lane];
+            } else {
+                const uint8_t* blk = q8k + b * kQ8KBytes;
+                qv[j] = ldg32(blk + 4 + 4 * lane);
+                bv[j] = ldg32(blk + 260 + 4 * (lane & 7));
+                dv[j] = __uint_as_float(ldg32(blk));
+            }
+        }
+        asm volatile("" ::: "memory");
+        load_group<TYPE, ITERS, R>(A, w, active ? wave : groups - 1, lane);
+#pragma unroll
+        for (int j = 0; j < SBW; ++j) {
+            const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+            if (b >= nsb) break;
+            if constexpr (FUSED) {
+                uint32_t qw;
+                int bs;
+                float d;
+                quantize_block(xv[j], lane, qw, bs, d);
+                store_block(s, 0, b, lane, qw, bs, d);
+            } else {
+                copy_block_store(s, 0, b, lane, qv[j], bv[j], dv[j]);
+            }
+        }
+    } else {
+        const uint64_t nblk = (uint64_t)m * nsb;
+        for (uint64_t b = wave_in_wg; b < nblk; b += WAVES) {
+            const int mi = (int)(b / nsb);
+            const uint64_t sb = b % nsb;
+            if constexpr (FUSED) {
+                uint32_t qw;
+                int bs;
+                float d;
+                quantize_block(reinterpret_cast<const float4*>(x + (uint64_t)mi * w.k + sb * kQK)[lane], lane, qw,
+                               bs, d);
+                store_block(s, mi, sb, lane, qw, bs, d);
+            } else {
+                const uint8_t* blk = q8k + b * kQ8KBytes;
+                copy_block_store(s, mi, sb, lane, ldg32(blk + 4 + 4 * lane), ldg32(blk + 260 + 4 * (lane & 7)),
+                                 __uint_as_float(ldg32(blk)));
+            }
+        }
+        load_group<TYPE, ITERS, R>(A, w, active ? wave : groups - 1, lane);
+    }
+    __syncthreads();
+    if (!active) return;
+
+    Act act[ITERS];
+    if constexpr (MT == 1) {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const uint64_t sb = 16u * it + (lane >> 2);
+            if (sb < nsb) slice_from_lds<TYPE>(act[it], s, 0, sb, lane & 3);
+        }
+    }
+    uint64_t grp = wave;
+    while (true) {
+        finish_group<TYPE, ITERS, R, MT>(A, act, s, m, w, grp, lane, y);
+        grp += nw;
+        if (grp >= groups) break;
+        load_group<TYPE, ITERS, R>(A, w, grp, lane);
+    }
+}
+
+// ---------------------------------------------------------------- launch
+
+int g_cu_count = 0;
+
+int cu_count() {
+    if (g_cu_count == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) {
+            g_cu_count = cus;
+        } else {
+            g_cu_count = 256;
+        }
+    }
+    return g_cu_count;
+}
+
+int env_int(const char* name, int fallback) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : fallback;
+}
+
+template <uint32_t TYPE, int ITERS, int R, int MT, bool FUSED, int WAVES>
+hipError_t launch_one(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+    const uint64_t groups = (w.n + R - 1) / R;
+    const int wg_per_cu = env_int("OQ_GEMV_WG_PER_CU", 2);
+    uint64_t wgs = (uint64_t)cu_count() * (uint64_t)(wg_per_cu > 0 ? wg_per_cu : 1);
+    const uint64_t need = (groups + WAVES - 1) / WAVES;
+    if (wgs > need) wgs = need;
+    hipLaunchKernelGGL((gemv_kq_kernel<TYPE, ITERS, R, MT, FUSED, WAVES>), dim3((unsigned)wgs), dim3(64 * WAVES),
+                       act_lds_bytes(w.k, MT), s, w, m, x, q8k, y);
+    return hipGetLastError();
+}
+
+template <uint32_t TYPE, int ITERS, int MT, bool FUSED>
+hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+    const int rows = env_int("OQ_GEMV_ROWS", MT == 1 && ITERS <= 2 ? 2 : 1);
+    const int waves = env_int("OQ_GEMV_WAVES", 8);
+    if constexpr (MT == 1 && ITERS <= 3) {  // two rows per wave would spill beyond 3 passes
+        if (rows >= 2) {
+            return waves == 4 ? launch_one<TYPE, ITERS, 2, MT, FUSED, 4>(w, m, x, q8k, y, s)
+                              : launch_one<TYPE, ITERS, 2, MT, FUSED, 8>(w, m, x, q8k, y, s);
+        }
+    }
+    return waves == 4 ? launch_one<TYPE, ITERS, 1, MT, FUSED, 4>(w, m, x, q8k, y, s)
+                      : launch_one<TYPE, ITERS, 1, MT, FUSED, 8>(w, m, x, q8k, y, s);
+}
+
+template <uint32_t TYPE, int MT, bool FUSED>
+hipError_t launch_iters(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+    switch ((w.k / kQK + 15) / 16) {
+        case 1: return launch_rows<TYPE, 1, MT, FUSED>(w, m, x, q8k, y, s);
+        case 2: return launch_rows<TYPE, 2, MT, FUSED>(w, m, x, q8k, y, s);
+        case 3: return launch_rows<TYPE, 3, MT, FUSED>(w, m, x, q8k, y, s);
+        case 4: return launch_rows<TYPE, 4, MT, FUSED>(w, m, x, q8k, y, s);
+        default: return hipErrorNotSupported;
+    }
+}
+
+template <uint32_t TYPE, bool FUSED>
+hipError_t launch_m(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+    if (m <= 1) return launch_iters<TYPE, 1, FUSED>(w, m, x, q8k, y, s);
+    if (m <= 2) return launch_iters<TYPE, 2, FUSED>(w, m, x, q8k, y, s);
+    if (m <= 4) return launch_iters<TYPE, 4, FUSED>(w, m, x, q8k, y, s);
+    return launch_iters<TYPE, 8, FUSED>(w, m, x, q8k, y, s);
+}
+
+template <bool FUSED>
+hipError_t launch_type(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+    switch (w.type) {
+        case 12: return launch_m<12, FUSED>(w, m, x, q8k, y, s);
+        case 13: return launch_m<13, FUSED>(w, m, x, q8k, y, s);
+        case 14: return launch_m<14, FUSED>(w, m, x, q8k, y, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+int gemv_max_m() { return 8; }
+
+bool gemv_kquant_supported(const DeviceMatrix& w) {
+    const bool kq = w.type == 12 || w.type == 13 || w.type == 14;
+    return kq && (w.k / kQK + 15) / 16 <= kMaxIters && act_lds_bytes(w.k, 1) <= kLdsBudget;
+}
+
+hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
+                              hipStream_t s) {
+    if (!gemv_kquant_supported(w)) return hipErrorNotSupported;
+    // activation rows per launch: what fits the LDS budget, at most 8
+    int chunk = 8;
+    while (chunk > 1 && act_lds_bytes(w.k, chunk) > kLdsBudget) chunk >>= 1;
+    for (int m0 = 0; m0 < m; m0 += chunk) {
+        const int mc = m - m0 < chunk ? m - m0 : chunk;
+        hipError_t e;
+        if (x != nullptr) {
+            e = launch_type<true>(w, mc, x + (uint64_t)m0 * w.k, nullptr, y + (uint64_t)m0 * w.n, s);
+        } else {
+            e = launch_type<false>(w, mc, nullptr, q8k + (uint64_t)m0 * (w.k / kQK) * kQ8KBytes,
+                                   y + (uint64_t)m0 * w.n, s);
+        }
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace oq

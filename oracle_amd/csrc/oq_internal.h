@@ -15,7 +15,8 @@ constexpr int kQ8KBytes = 292;    // {f32 d, i8 qs[256], i16 bsums[16]}
 
 // How a weight's rows sit in HBM.  Every row starts at a multiple of `pitch` bytes from
 // `base`, and `pitch` is a multiple of 16 so rows can be streamed with 128-bit loads.
-//   q4_K, q5_K : native GGML blocks (144 / 176 B are multiples of 16)
+//   q4_K       : per-row planes  qs[nsb][128] | hdr[nsb][16]   (hdr = f16 d, f16 dmin, scales[12])
+//   q5_K       : per-row planes  qs[nsb][128] | qh[nsb][32] | hdr[nsb][16]
 //   q6_K       : per-row planes  ql[nsb][128] | qh[nsb][64] | sc[nsb][16] | d[nsb] (f16)
 //   q8_0       : per-row planes  qs[nb][32] | d[nb] (f16)
 //   f32/f16/bf16: native
@@ -37,15 +38,17 @@ hipError_t launch_dequantize(const DeviceMatrix& w, uint64_t row0, uint64_t nrow
 hipError_t launch_quantize_q8k(const float* x, uint64_t m, uint64_t k, uint8_t* q8k,
                                hipStream_t s);
 
-// ---- oq_gemv.hip  (m activation rows, small m: weights streamed once, reuse in registers)
-// K-quant weights against Q8_K activations given as blocks (q8k) or as F32 (x, quantized in
-// the prologue of every workgroup into LDS; bit-identical to launch_quantize_q8k).
+// ---- oq_gemv_reg.hip  (K-quant weights, m <= 8 activation rows per launch, weights streamed once)
+// Q8_K activations given as blocks (q8k) or as F32 (x, quantized by every workgroup into LDS;
+// bit-identical to launch_quantize_q8k).
+bool gemv_kquant_supported(const DeviceMatrix& w);
 hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k,
                               float* y, hipStream_t s);
-// q8_0 / f32 / f16 / bf16 weights against F32 activations
+int gemv_max_m();
+
+// ---- oq_gemv.hip  (q8_0 / f32 / f16 / bf16 weights against F32 activations)
 hipError_t launch_gemv_f32act(const DeviceMatrix& w, int m, const float* x, float* y,
                               hipStream_t s);
-int gemv_max_m();
 
 // ---- oq_gemm.hip  (m >= 16, q4_K on fp16 MFMA)
 hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const uint8_t* q8k, float* y,

@@ -185,6 +185,35 @@ def test_matvec_q8k_matches_integer_oracle(ctx, t):
     w.release()
 
 
+@pytest.mark.parametrize("t", KQ)
+@pytest.mark.parametrize("cols", [256, 4096, 8192, 12288, 16384])
+def test_fused_quantization_is_bit_identical(ctx, t, cols):
+    """F32 activations quantized inside the GEMV give exactly the result of the same GEMV fed with
+    the standalone quantizer's Q8_K blocks (same integer sums, same float operations)."""
+    rng = np.random.default_rng(500 + t + cols)
+    rows = 97
+    data = synth.weights(t, rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    x[:256] = np.where(np.arange(256) % 3 == 0, 0.0, x[:256])
+    x[17], x[200] = 5.5, -5.5  # |x| tie inside the first super-block
+    w = ctx.upload(t, cols, rows, data)
+    xb = ctx.to_device(x)
+    qb = ctx.alloc(cols // 256 * 292)
+    y1 = ctx.alloc(rows * 4)
+    y2 = ctx.alloc(rows * 4)
+    ctx.matvec(w, xb, y1)
+    ctx.quantize_q8k(xb, 1, cols, qb)
+    ctx.matvec_q8k(w, qb, y2)
+    a = y1.download(np.float32, rows)
+    b = y2.download(np.float32, rows)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    y_ref, norm = reference_products(t, rows, cols, data, x)
+    check_close(a, y_ref[0], norm[0])
+    for buf in (xb, qb, y1, y2):
+        buf.free()
+    w.release()
+
+
 @pytest.mark.parametrize("t", [12, 14, 8])
 @pytest.mark.parametrize("m", [2, 3, 4, 5, 8, 11])
 def test_matmul_small_batch(ctx, t, m):
