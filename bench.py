@@ -103,6 +103,22 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
     return res
 
 
+def run_copy_calibration(ctx, steps, nbytes=28311552):
+    """Device-to-device copies of a known size: the FETCH_SIZE / WRITE_SIZE counters of this
+    dispatch calibrate the same counters read on the GEMV kernels."""
+    src = ctx.alloc(nbytes)
+    dst = ctx.alloc(nbytes)
+    ctx.lib.oq_copy_device(ctx.h, dst.ptr, src.ptr, nbytes)
+    ctx.sync()
+    ctx.timer_start()
+    for _ in range(steps):
+        ctx.lib.oq_copy_device(ctx.h, dst.ptr, src.ptr, nbytes)
+    ms = ctx.timer_stop()
+    src.free()
+    dst.free()
+    return {"workload": "copy_calibration", "bytes": nbytes, "us_per_copy": ms * 1e3 / steps}
+
+
 def cpu_baseline(name, budget_s=12.0):
     """The reference's CPU algorithm (oracle restatement: decode block, sequential F32 dot) on
     the same workload, single thread, repeated until ~budget_s seconds; plus all host cores."""
@@ -148,7 +164,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="q4k_gemv", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="q4k_gemv", choices=sorted(WORKLOADS) + ["copy_calibration"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     args = ap.parse_args()
@@ -161,6 +177,10 @@ def main():
         sys.exit(2)
 
     ctx = oracle_amd.Context(0)
+    if args.workload == "copy_calibration":
+        print(json.dumps(run_copy_calibration(ctx, args.steps)), flush=True)
+        ctx.close()
+        return
     main_res = run_gpu(ctx, args.workload, args.steps, args.warmup)
     secondary = None
     if not args.no_secondary and args.workload == "q4k_gemv":

@@ -33,6 +33,7 @@ OQ_DEVICE uint32_t ldg32(const uint8_t* p) { return *reinterpret_cast<const uint
 OQ_DEVICE int dot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 OQ_DEVICE float h2f(uint32_t bits16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16); }
 
+
 OQ_DEVICE float row16_max(float v) {
     v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
     v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
@@ -176,23 +177,25 @@ struct WRegs<14> {
     using type = W6;
 };
 
+// Offsets are 32-bit (a row is far below 4 GiB) so the loads use a scalar row base plus a
+// per-lane 32-bit offset.
 template <uint32_t TYPE>
-OQ_DEVICE void load_w(typename WRegs<TYPE>::type& r, const uint8_t* row, uint64_t nsb, int it, int lane) {
-    const uint64_t m = nsb - 16u * it < 16 ? nsb - 16u * it : 16;
-    const uint64_t l = (uint64_t)lane < 4 * m ? (uint64_t)lane : 4 * m - 1;  // surplus lanes re-read
-    const uint64_t sb = 16u * it + (l >> 2);
-    const int q = (int)(l & 3);
-    r.c0 = ldg128(row + 16 * (128u * it + l));
-    r.c1 = ldg128(row + 16 * (128u * it + 4 * m + l));
+OQ_DEVICE void load_w(typename WRegs<TYPE>::type& r, const uint8_t* row, uint32_t nsb, int it, int lane) {
+    const uint32_t m = nsb - 16u * it < 16u ? nsb - 16u * it : 16u;
+    const uint32_t l = (uint32_t)lane < 4 * m ? (uint32_t)lane : 4 * m - 1;  // surplus lanes re-read
+    const uint32_t sb = 16u * it + (l >> 2);
+    const uint32_t q = l & 3;
+    r.c0 = ldg128(row + 16u * (128u * it + l));
+    r.c1 = ldg128(row + 16u * (128u * it + 4u * m + l));
     if constexpr (TYPE == 14) {
-        r.qh = ldg128(row + 128 * nsb + 64 * sb + 16 * q);
-        r.sc = ldg32(row + 192 * nsb + 16 * sb + 4 * q);
-        r.d = *reinterpret_cast<const uint16_t*>(row + 208 * nsb + 2 * sb);
+        r.qh = ldg128(row + (128u * nsb + 64u * sb + 16u * q));
+        r.sc = ldg32(row + (192u * nsb + 16u * sb + 4u * q));
+        r.d = *reinterpret_cast<const uint16_t*>(row + (208u * nsb + 2u * sb));
     } else {
-        r.hdr = ldg128(row + (TYPE == 13 ? 160 : 128) * nsb + 16 * sb);
+        r.hdr = ldg128(row + ((TYPE == 13 ? 160u : 128u) * nsb + 16u * sb));
         if constexpr (TYPE == 13) {
-            r.h0 = ldg128(row + 128 * nsb + 32 * sb);
-            r.h1 = ldg128(row + 128 * nsb + 32 * sb + 16);
+            r.h0 = ldg128(row + (128u * nsb + 32u * sb));
+            r.h1 = ldg128(row + (128u * nsb + 32u * sb + 16u));
         }
     }
 }
@@ -209,17 +212,28 @@ struct Dec6 {
     int sc[4];
 };
 
+// Lane-constant masks and shifts that pick, without branches, the (scale, min) byte-vector
+// holding the lane's sub-blocks 2q, 2q+1 out of GGML's 12-byte K-quant packing:
+//   pairs 0..3: scales = p0 & 0x3f.., mins = p1 & 0x3f..
+//   pairs 4..7: scales = (p2 & 0x0f..) | ((p0 >> 2) & 0x30..), mins = ((p2 >> 4) & 0x0f..) | ((p1 >> 2) & 0x30..)
+struct ScaleSel {
+    uint32_t mask_a, mask_b;  // applied to p0/p1 (shifted) and to p2 (shifted)
+    int sh_a, sh_b, sh_pair;  // p0/p1 shift, p2 shift for the mins, byte offset of the pair
+};
+OQ_DEVICE ScaleSel scale_sel(int q) {
+    const bool low = q < 2;
+    return {low ? 0x3F3F3F3Fu : 0x30303030u, low ? 0u : 0x0F0F0F0Fu, low ? 0 : 2, low ? 0 : 4, 16 * (q & 1)};
+}
+
 template <uint32_t TYPE>
-OQ_DEVICE Dec45 decode_w(const W45& r, int q) {
+OQ_DEVICE Dec45 decode_w(const W45& r, const ScaleSel& ss, int q) {
     Dec45 o;
     o.d = h2f(r.hdr.x & 0xFFFFu);
     o.dmin = h2f(r.hdr.x >> 16);
-    // the eight 6-bit (scale, min) pairs as four byte-vectors (GGML's K-quant packing)
     const uint32_t p0 = r.hdr.y, p1 = r.hdr.z, p2 = r.hdr.w;
-    const bool low = q < 2;
-    const uint32_t scw = low ? (p0 & 0x3F3F3F3Fu) : ((p2 & 0x0F0F0F0Fu) | ((p0 >> 2) & 0x30303030u));
-    const uint32_t mnw = low ? (p1 & 0x3F3F3F3Fu) : (((p2 >> 4) & 0x0F0F0F0Fu) | ((p1 >> 2) & 0x30303030u));
-    const int sh = 16 * (q & 1);
+    const uint32_t scw = ((p0 >> ss.sh_a) & ss.mask_a) | (p2 & ss.mask_b);
+    const uint32_t mnw = ((p1 >> ss.sh_a) & ss.mask_a) | ((p2 >> ss.sh_b) & ss.mask_b);
+    const int sh = ss.sh_pair;
     o.sc0 = (int)((scw >> sh) & 0xFFu);
     o.sc1 = (int)((scw >> (sh + 8)) & 0xFFu);
     o.mn0 = (int)((mnw >> sh) & 0xFFu);
@@ -239,7 +253,7 @@ OQ_DEVICE Dec45 decode_w(const W45& r, int q) {
 }
 
 template <uint32_t TYPE>
-OQ_DEVICE Dec6 decode_w(const W6& r, int) {
+OQ_DEVICE Dec6 decode_w(const W6& r, const ScaleSel&, int) {
     Dec6 o;
     o.d = h2f(r.d);
     const uint32_t c0[4] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w};
@@ -270,8 +284,10 @@ OQ_DEVICE float lane_dot(const Dec45& w, const Act& a) {
     slo = dot16(w.lo + 4, a.x1, slo);
     int shi = dot16(w.hi, a.x2, 0);
     shi = dot16(w.hi + 4, a.x3, shi);
-    const int isum = w.sc0 * slo + w.sc1 * shi;
-    const int imin = w.mn0 * (a.b[0] + a.b[1]) + w.mn1 * (a.b[2] + a.b[3]);
+    // all factors fit in 24 bits (|slo| <= 32*31*127, scales <= 63, |bsum| <= 16*127): full-rate
+    // 24-bit multiplies are exact here
+    const int isum = __mul24(w.sc0, slo) + __mul24(w.sc1, shi);
+    const int imin = __mul24(w.mn0, a.b[0] + a.b[1]) + __mul24(w.mn1, a.b[2] + a.b[3]);
     return a.d * (w.d * (float)isum - w.dmin * (float)imin);
 }
 
@@ -280,7 +296,8 @@ OQ_DEVICE float lane_dot(const Dec6& w, const Act& a) {
     const int p1 = dot16(w.s[1], a.x1, 0) - 32 * a.b[1];
     const int p2 = dot16(w.s[2], a.x2, 0) - 32 * a.b[2];
     const int p3 = dot16(w.s[3], a.x3, 0) - 32 * a.b[3];
-    const int isum = w.sc[0] * p0 + w.sc[1] * p1 + w.sc[2] * p2 + w.sc[3] * p3;
+    // |p_i| <= 16*63*127 + 32*16*127, |sc| <= 128: exact in 24-bit multiplies
+    const int isum = __mul24(w.sc[0], p0) + __mul24(w.sc[1], p1) + __mul24(w.sc[2], p2) + __mul24(w.sc[3], p3);
     return a.d * (w.d * (float)isum);
 }
 
@@ -289,22 +306,25 @@ OQ_DEVICE float lane_dot(const Dec6& w, const Act& a) {
 template <uint32_t TYPE, int ITERS, int R>
 OQ_DEVICE void load_group(typename WRegs<TYPE>::type (&W)[R][ITERS], const DeviceMatrix& w, uint64_t grp,
                           int lane) {
-    const uint64_t nsb = w.k / kQK;
+    const uint32_t nsb = (uint32_t)(w.k / kQK);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         uint64_t row = grp * R + r;
         row = row < w.n ? row : w.n - 1;
-        const uint8_t* base = w.base + row * w.pitch;
+        // the row index is wave-uniform: keep it (and the row address) in scalar registers
+        const uint32_t row_s = __builtin_amdgcn_readfirstlane((uint32_t)row);
+        const uint8_t* base = w.base + (uint64_t)row_s * w.pitch;
 #pragma unroll
         for (int it = 0; it < ITERS; ++it) load_w<TYPE>(W[r][it], base, nsb, it, lane);
     }
 }
 
-template <uint32_t TYPE, int ITERS, int R, int MT>
+template <uint32_t TYPE, int ITERS, int R, int MT, bool FULL>
 OQ_DEVICE void finish_group(const typename WRegs<TYPE>::type (&W)[R][ITERS], const Act (&act)[ITERS],
                             const ActLds& s, int m, const DeviceMatrix& w, uint64_t grp, int lane, float* y) {
     const uint64_t nsb = w.k / kQK;
     const int q = lane & 3;
+    const ScaleSel ss = scale_sel(q);
     float acc[R][MT];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -313,10 +333,10 @@ OQ_DEVICE void finish_group(const typename WRegs<TYPE>::type (&W)[R][ITERS], con
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
         const uint64_t sb = 16u * it + (lane >> 2);
-        if (sb >= nsb) continue;
+        if (!FULL && sb >= nsb) continue;  // FULL: K is a multiple of 4096, every lane has a slot
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const auto dec = decode_w<TYPE>(W[r][it], q);
+            const auto dec = decode_w<TYPE>(W[r][it], ss, q);
             if constexpr (MT == 1) {
                 acc[r][0] += lane_dot(dec, act[it]);
             } else {
@@ -345,7 +365,7 @@ OQ_DEVICE void finish_group(const typename WRegs<TYPE>::type (&W)[R][ITERS], con
     }
 }
 
-template <uint32_t TYPE, int ITERS, int R, int MT, bool FUSED, int WAVES>
+template <uint32_t TYPE, int ITERS, int R, int MT, bool FUSED, int WAVES, bool FULL>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kq_kernel(DeviceMatrix w, int m, const float* x,
                                                              const uint8_t* q8k, float* __restrict__ y) {
     using WR = typename WRegs<TYPE>::type;
@@ -430,7 +450,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kq_kernel(DeviceMatrix w, int
     }
     uint64_t grp = wave;
     while (true) {
-        finish_group<TYPE, ITERS, R, MT>(A, act, s, m, w, grp, lane, y);
+        finish_group<TYPE, ITERS, R, MT, FULL>(A, act, s, m, w, grp, lane, y);
         grp += nw;
         if (grp >= groups) break;
         load_group<TYPE, ITERS, R>(A, w, grp, lane);
@@ -466,8 +486,13 @@ hipError_t launch_one(const DeviceMatrix& w, int m, const float* x, const uint8_
     uint64_t wgs = (uint64_t)cu_count() * (uint64_t)(wg_per_cu > 0 ? wg_per_cu : 1);
     const uint64_t need = (groups + WAVES - 1) / WAVES;
     if (wgs > need) wgs = need;
-    hipLaunchKernelGGL((gemv_kq_kernel<TYPE, ITERS, R, MT, FUSED, WAVES>), dim3((unsigned)wgs), dim3(64 * WAVES),
-                       act_lds_bytes(w.k, MT), s, w, m, x, q8k, y);
+    if ((w.k / kQK) % 16 == 0) {
+        hipLaunchKernelGGL((gemv_kq_kernel<TYPE, ITERS, R, MT, FUSED, WAVES, true>), dim3((unsigned)wgs),
+                           dim3(64 * WAVES), act_lds_bytes(w.k, MT), s, w, m, x, q8k, y);
+    } else {
+        hipLaunchKernelGGL((gemv_kq_kernel<TYPE, ITERS, R, MT, FUSED, WAVES, false>), dim3((unsigned)wgs),
+                           dim3(64 * WAVES), act_lds_bytes(w.k, MT), s, w, m, x, q8k, y);
+    }
     return hipGetLastError();
 }
 
@@ -477,12 +502,11 @@ hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8
     const int waves = env_int("OQ_GEMV_WAVES", 8);
     if constexpr (MT == 1 && ITERS <= 3) {  // two rows per wave would spill beyond 3 passes
         if (rows >= 2) {
-            return waves == 4 ? launch_one<TYPE, ITERS, 2, MT, FUSED, 4>(w, m, x, q8k, y, s)
-                              : launch_one<TYPE, ITERS, 2, MT, FUSED, 8>(w, m, x, q8k, y, s);
+            if (waves >= 16 && ITERS == 1) return launch_one<TYPE, ITERS, 2, MT, FUSED, 16>(w, m, x, q8k, y, s);
+            return launch_one<TYPE, ITERS, 2, MT, FUSED, 8>(w, m, x, q8k, y, s);
         }
     }
-    return waves == 4 ? launch_one<TYPE, ITERS, 1, MT, FUSED, 4>(w, m, x, q8k, y, s)
-                      : launch_one<TYPE, ITERS, 1, MT, FUSED, 8>(w, m, x, q8k, y, s);
+    return launch_one<TYPE, ITERS, 1, MT, FUSED, 8>(w, m, x, q8k, y, s);
 }
 
 template <uint32_t TYPE, int MT, bool FUSED>
