@@ -380,15 +380,19 @@ int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, f
         return fail(ctx, OQ_INVALID_ARGUMENT, "activation / output buffers are misaligned");
     }
     if (is_kquant(t)) {
-        const uint64_t q8bytes = m * (w->m.k / oq::kQK) * oq::kQ8KBytes;
-        const bool mfma = m >= 16 && oq::gemm_mfma_supported(w->m, (int)m);
+        if (!oq::gemv_kquant_supported(w->m)) {
+            return fail(ctx, OQ_INVALID_ARGUMENT, "K-quant rows longer than 16384 elements are not supported yet");
+        }
+        const uint64_t q8bytes = (m * (w->m.k / oq::kQK) * oq::kQ8KBytes + 255) & ~uint64_t(255);
+        const bool mfma = oq::gemm_mfma_supported(w->m, (int)m) && env_flag("OQ_GEMM_MFMA", true);
         const bool fused = env_flag("OQ_FUSED_QUANT", true);
         if (mfma || !fused) {
-            if (int rc = ensure_scratch(ctx, q8bytes)) return rc;
+            const uint64_t need = q8bytes + (mfma ? oq::gemm_scratch_bytes(w->m, (int)m) : 0);
+            if (int rc = ensure_scratch(ctx, need)) return rc;
             uint8_t* q8 = static_cast<uint8_t*>(ctx->scratch);
             hipError_t e = oq::launch_quantize_q8k(x, m, w->m.k, q8, ctx->stream);
             if (e == hipSuccess) {
-                e = mfma ? oq::launch_gemm_q4k_mfma(w->m, (int)m, q8, y, ctx->stream)
+                e = mfma ? oq::launch_gemm_q4k_mfma(w->m, (int)m, q8, y, q8 + q8bytes, ctx->stream)
                          : oq::launch_gemv_kquant(w->m, (int)m, nullptr, q8, y, ctx->stream);
             }
             return launch_rc(ctx, e, "matmul");
@@ -412,9 +416,14 @@ int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q
     if (m > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "matmul batch too large");
     if (!q8k || !y) return fail(ctx, OQ_INVALID_ARGUMENT, "null buffer");
     if (!aligned(q8k, 4) || !aligned(y, 4)) return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer");
+    if (!oq::gemv_kquant_supported(w->m)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "K-quant rows longer than 16384 elements are not supported yet");
+    }
     const uint8_t* q8 = static_cast<const uint8_t*>(q8k);
-    if (m >= 16 && oq::gemm_mfma_supported(w->m, (int)m)) {
-        return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, q8, y, ctx->stream), "matmul_q8k");
+    if (oq::gemm_mfma_supported(w->m, (int)m) && env_flag("OQ_GEMM_MFMA", true)) {
+        if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
+        return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, q8, y, ctx->scratch, ctx->stream),
+                         "matmul_q8k");
     }
     return launch_rc(ctx, oq::launch_gemv_kquant(w->m, (int)m, nullptr, q8, y, ctx->stream), "matmul_q8k");
 }

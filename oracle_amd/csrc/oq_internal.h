@@ -50,9 +50,10 @@ int gemv_max_m();
 hipError_t launch_gemv_f32act(const DeviceMatrix& w, int m, const float* x, float* y,
                               hipStream_t s);
 
-// ---- oq_gemm.hip  (m >= 16, q4_K on fp16 MFMA)
-hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const uint8_t* q8k, float* y,
-                                hipStream_t s);
+// ---- oq_gemm.hip  (m >= 16, q4_K, K >= 4096: F16 matrix cores on F16-rounded operands)
 bool gemm_mfma_supported(const DeviceMatrix& w, int m);
+uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m);  // F16 activation image
+hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const uint8_t* q8k, float* y, void* scratch,
+                                hipStream_t s);
 
 }  // namespace oq

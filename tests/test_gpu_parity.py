@@ -228,6 +228,36 @@ def test_matmul_small_batch(ctx, t, m):
     w.release()
 
 
+@pytest.mark.parametrize("m,rows,cols", [(16, 256, 4096), (37, 300, 4096), (64, 130, 12288), (200, 128, 8192)])
+def test_matmul_matrix_cores(ctx, m, rows, cols):
+    """m >= 16 q4_K products run on the F16 MFMA path; same tolerance as every other product."""
+    rng = np.random.default_rng(900 + m + rows)
+    data = synth.q4_k(rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(12, cols, rows, data)
+    y = gpu_matmul(ctx, w, x, rows)
+    y_ref, norm = reference_products(12, rows, cols, data, x)
+    worst = check_close(y, y_ref, norm)
+    assert worst < 0.5 * TOL, f"MFMA path margin too thin: {worst:.2e}"
+    w.release()
+
+
+def test_prefill_gemm_full_size_sampled_rows(ctx):
+    """The 4096 x 12288 q4_K down projection at M = 512: every output of 24 sampled activation
+    rows against the oracle (the rows are computed inside the full 512-row product)."""
+    rng = np.random.default_rng(4242)
+    rows, cols, m = 4096, 12288, 512
+    data = synth.q4_k(rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(12, cols, rows, data)
+    y = gpu_matmul(ctx, w, x, rows)
+    pick = np.array(sorted(set([0, 1, 255, 256, 511] + list(rng.integers(0, m, 19)))))
+    y_ref, norm = reference_products(12, rows, cols, data, x[pick])
+    check_close(y[pick], y_ref, norm)
+    assert np.all(np.isfinite(y))
+    w.release()
+
+
 @pytest.mark.parametrize("env", [{"OQ_GEMV_ROWS": "2"}, {"OQ_FUSED_QUANT": "0"}, {"OQ_GEMV_MAX_WG": "7"}])
 def test_launch_variants_agree(ctx, env):
     rng = np.random.default_rng(77)
