@@ -15,13 +15,36 @@
 #include "../../include/oq.h"
 #include "oq_internal.h"
 
+namespace oq {
+
+int env_int(const char* name, int fallback) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : fallback;
+}
+
+int cu_count() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) {
+            cus = v;
+        } else {
+            cus = 256;
+        }
+    }
+    return cus;
+}
+
+}  // namespace oq
+
 struct oq_context {
     int device = 0;
     hipStream_t stream = nullptr;
     hipEvent_t t0 = nullptr, t1 = nullptr;
     std::string error;
     bool capturing = false;
-    void* scratch = nullptr;  // Q8_K staging for the un-fused and MFMA paths
+    void* scratch = nullptr;  // Q8_K staging (un-fused GEMV) or planar image + split partials (GEMM)
     uint64_t scratch_bytes = 0;
 };
 
@@ -383,18 +406,17 @@ int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, f
         if (!oq::gemv_kquant_supported(w->m)) {
             return fail(ctx, OQ_INVALID_ARGUMENT, "K-quant rows longer than 16384 elements are not supported yet");
         }
-        const uint64_t q8bytes = (m * (w->m.k / oq::kQK) * oq::kQ8KBytes + 255) & ~uint64_t(255);
-        const bool mfma = oq::gemm_mfma_supported(w->m, (int)m) && env_flag("OQ_GEMM_MFMA", true);
-        const bool fused = env_flag("OQ_FUSED_QUANT", true);
-        if (mfma || !fused) {
-            const uint64_t need = q8bytes + (mfma ? oq::gemm_scratch_bytes(w->m, (int)m) : 0);
-            if (int rc = ensure_scratch(ctx, need)) return rc;
+        if (oq::gemm_mfma_supported(w->m, (int)m) && env_flag("OQ_GEMM_MFMA", true)) {
+            if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
+            return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, x, nullptr, y, ctx->scratch, ctx->stream),
+                             "matmul");
+        }
+        if (!env_flag("OQ_FUSED_QUANT", true)) {
+            const uint64_t q8bytes = (m * (w->m.k / oq::kQK) * oq::kQ8KBytes + 255) & ~uint64_t(255);
+            if (int rc = ensure_scratch(ctx, q8bytes)) return rc;
             uint8_t* q8 = static_cast<uint8_t*>(ctx->scratch);
             hipError_t e = oq::launch_quantize_q8k(x, m, w->m.k, q8, ctx->stream);
-            if (e == hipSuccess) {
-                e = mfma ? oq::launch_gemm_q4k_mfma(w->m, (int)m, q8, y, q8 + q8bytes, ctx->stream)
-                         : oq::launch_gemv_kquant(w->m, (int)m, nullptr, q8, y, ctx->stream);
-            }
+            if (e == hipSuccess) e = oq::launch_gemv_kquant(w->m, (int)m, nullptr, q8, y, ctx->stream);
             return launch_rc(ctx, e, "matmul");
         }
         return launch_rc(ctx, oq::launch_gemv_kquant(w->m, (int)m, x, nullptr, y, ctx->stream), "matmul");
@@ -422,7 +444,7 @@ int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q
     const uint8_t* q8 = static_cast<const uint8_t*>(q8k);
     if (oq::gemm_mfma_supported(w->m, (int)m) && env_flag("OQ_GEMM_MFMA", true)) {
         if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
-        return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, q8, y, ctx->scratch, ctx->stream),
+        return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, nullptr, q8, y, ctx->scratch, ctx->stream),
                          "matmul_q8k");
     }
     return launch_rc(ctx, oq::launch_gemv_kquant(w->m, (int)m, nullptr, q8, y, ctx->stream), "matmul_q8k");

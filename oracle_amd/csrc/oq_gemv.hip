@@ -108,11 +108,6 @@ __global__ __launch_bounds__(kThreads) void gemv_plain_kernel(DeviceMatrix w, in
 
 // ---------------------------------------------------------------- launch configuration
 
-int env_int(const char* name, int fallback) {
-    const char* v = getenv(name);
-    return v ? atoi(v) : fallback;
-}
-
 unsigned grid_for(uint64_t work_items, int per_wg_items) {
     const uint64_t want = (work_items + per_wg_items - 1) / per_wg_items;
     const uint64_t cap = (uint64_t)env_int("OQ_GEMV_MAX_WG", 1 << 20);

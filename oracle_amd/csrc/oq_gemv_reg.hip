@@ -459,26 +459,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kq_kernel(DeviceMatrix w, int
 
 // ---------------------------------------------------------------- launch
 
-int g_cu_count = 0;
-
-int cu_count() {
-    if (g_cu_count == 0) {
-        int dev = 0, cus = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) {
-            g_cu_count = cus;
-        } else {
-            g_cu_count = 256;
-        }
-    }
-    return g_cu_count;
-}
-
-int env_int(const char* name, int fallback) {
-    const char* v = getenv(name);
-    return v ? atoi(v) : fallback;
-}
-
 template <uint32_t TYPE, int ITERS, int R, int MT, bool FUSED, int WAVES>
 hipError_t launch_one(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
     const uint64_t groups = (w.n + R - 1) / R;

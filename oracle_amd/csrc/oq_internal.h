@@ -30,6 +30,10 @@ struct DeviceMatrix {
 
 uint64_t device_pitch(uint32_t type, uint64_t k);
 
+// ---- oq_api.cpp
+int env_int(const char* name, int fallback);  // integer launch knob; fallback when unset
+int cu_count();                               // compute units of the current device (cached)
+
 // ---- oq_decode.hip
 hipError_t launch_relayout(uint32_t type, uint64_t k, uint64_t n, const uint8_t* src,
                            uint8_t* dst, uint64_t pitch, hipStream_t s);
@@ -51,9 +55,11 @@ hipError_t launch_gemv_f32act(const DeviceMatrix& w, int m, const float* x, floa
                               hipStream_t s);
 
 // ---- oq_gemm.hip  (m >= 16, q4_K, K >= 4096: F16 matrix cores on F16-rounded operands)
+// Activations are given either as F32 (x; quantized to Q8_K inside, bit-identical to
+// launch_quantize_q8k) or as Q8_K blocks (q8k); exactly one of the two is non-null.
 bool gemm_mfma_supported(const DeviceMatrix& w, int m);
-uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m);  // F16 activation image
-hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const uint8_t* q8k, float* y, void* scratch,
-                                hipStream_t s);
+uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m);  // planar Q8_K image + split partials
+hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
+                                void* scratch, hipStream_t s);
 
 }  // namespace oq

@@ -242,6 +242,40 @@ def test_matmul_matrix_cores(ctx, m, rows, cols):
     w.release()
 
 
+@pytest.mark.parametrize("splits", [None, "1", "3", "8"])
+def test_matrix_cores_q8k_input_and_split_counts(ctx, splits):
+    """The MFMA path from caller-supplied Q8_K blocks equals the path from F32 activations bit
+    for bit (same planar image), and every K-split count stays within the tolerance."""
+    rng = np.random.default_rng(31337)
+    m, rows, cols = 70, 520, 8192
+    data = synth.q4_k(rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(12, cols, rows, data)
+    old = os.environ.get("OQ_GEMM_SPLITS")
+    if splits is not None:
+        os.environ["OQ_GEMM_SPLITS"] = splits
+    try:
+        y = gpu_matmul(ctx, w, x, rows)
+        xb = ctx.to_device(x)
+        qb = ctx.alloc(m * (cols // 256) * 292)
+        yb = ctx.alloc(m * rows * 4)
+        ctx.quantize_q8k(xb, m, cols, qb)
+        ctx.matmul_q8k(w, m, qb, yb)
+        y_q8k = yb.download(np.float32, m * rows).reshape(m, rows)
+        for b in (xb, qb, yb):
+            b.free()
+    finally:
+        if old is None:
+            os.environ.pop("OQ_GEMM_SPLITS", None)
+        else:
+            os.environ["OQ_GEMM_SPLITS"] = old
+    assert np.array_equal(y.view(np.uint32), y_q8k.view(np.uint32))
+    y_ref, norm = reference_products(12, rows, cols, data, x)
+    worst = check_close(y, y_ref, norm)
+    assert worst < 0.5 * TOL, f"MFMA path margin too thin: {worst:.2e}"
+    w.release()
+
+
 def test_prefill_gemm_full_size_sampled_rows(ctx):
     """The 4096 x 12288 q4_K down projection at M = 512: every output of 24 sampled activation
     rows against the oracle (the rows are computed inside the full 512-row product)."""
