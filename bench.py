@@ -119,6 +119,15 @@ def run_copy_calibration(ctx, steps, nbytes=28311552):
     return {"workload": "copy_calibration", "bytes": nbytes, "us_per_copy": ms * 1e3 / steps}
 
 
+def committed_traffic(name):
+    """HBM bytes per launch of the workload's dominant kernel, from the committed rocprofv3
+    counter summary (oracle_amd/profile.sh writes it); None when there is none."""
+    p = ROOT / "profiles" / f"{name}_traffic.json"
+    if not p.exists():
+        return None
+    return json.loads(p.read_text())["traffic_bytes"]
+
+
 def cpu_baseline(name, budget_s=12.0):
     """The reference's CPU algorithm (oracle restatement: decode block, sequential F32 dot) on
     the same workload, single thread, repeated until ~budget_s seconds; plus all host cores."""
@@ -206,7 +215,7 @@ def main():
         "config": {"workload": desc, "rows": n, "cols": k, "batch": m, "weight_type": "q4_K" if t == 12 else t,
                    "weight_copies_cycled": main_res["copies"], "seed": SEED},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(args.workload)},
         "us_per_gemv": round(main_res["us_per_step"], 3),
         "hbm_frac_weight_bytes": round(gbs / HBM_PEAK_GBS, 4),
     }

@@ -1,0 +1,45 @@
+#!/bin/bash
+# Profiles one bench.py workload with rocprofv3 and writes short text summaries:
+#   OUT/<workload>_kernel_stats.txt   rocprofv3 --kernel-trace --stats of the bench command
+#   OUT/<workload>_traffic.json       HBM bytes per dispatch of KERNEL (FETCH_SIZE, WRITE_SIZE),
+#                                     each scaled against a device-to-device copy of known size
+#
+#   bash oracle_amd/profile.sh WORKLOAD KERNEL_SUBSTRING [OUT]      (OUT defaults to prof_out)
+#
+# Every rocprofv3 run has a time limit of its own; counters are collected one per run, with no
+# trace domain beside them.
+set -euo pipefail
+WL=$1
+KERN=$2
+OUT=${3:-prof_out}
+ROOT=$(cd "$(dirname "$0")/.." && pwd)
+cd /tmp && export TMPDIR=/tmp
+cd "$ROOT"
+mkdir -p "$OUT"
+RAW="$OUT/raw_$WL"
+COPY_BYTES=28311552
+SECONDARY=""
+[ "$WL" = "q4k_gemv" ] && SECONDARY="--no-secondary"
+
+TRACE_CMD="rocprofv3 --kernel-trace --stats --output-format csv -d $RAW/trace -o run -- python3 bench.py --workload $WL --steps 200 --warmup 20 --no-cpu $SECONDARY"
+echo "trace: $TRACE_CMD"
+timeout -k 10 300 $TRACE_CMD > "$RAW.trace.log" 2>&1
+for C in FETCH_SIZE WRITE_SIZE; do
+    echo "pmc $C"
+    timeout -s KILL 60 rocprofv3 --pmc $C --output-format csv -d "$RAW/$C" -o run -- \
+        python3 bench.py --workload "$WL" --steps 20 --warmup 2 --no-cpu $SECONDARY > "$RAW.$C.log" 2>&1
+    timeout -s KILL 60 rocprofv3 --pmc $C --output-format csv -d "$RAW/copy_$C" -o run -- \
+        python3 bench.py --workload copy_calibration --steps 20 > "$RAW.copy_$C.log" 2>&1
+done
+
+{
+    echo "# rocprofv3 kernel statistics, workload $WL"
+    echo "# command: (cd \$REPO && $TRACE_CMD)"
+    echo "# bench line of that run:"
+    grep '^{' "$RAW.trace.log" | tail -1 | sed 's/^/#   /'
+    python3 -m oracle_amd.profsum stats "$RAW/trace"
+} > "$OUT/${WL}_kernel_stats.txt"
+python3 -m oracle_amd.profsum traffic --kernel "$KERN" --fetch "$RAW/FETCH_SIZE" --write "$RAW/WRITE_SIZE" \
+    --copy-fetch "$RAW/copy_FETCH_SIZE" --copy-write "$RAW/copy_WRITE_SIZE" --copy-bytes $COPY_BYTES \
+    > "$OUT/${WL}_traffic.json"
+echo "wrote $OUT/${WL}_kernel_stats.txt $OUT/${WL}_traffic.json"

@@ -1,0 +1,95 @@
+"""Summaries of rocprofv3 output for the profiles/ directory (run by oracle_amd/profile.sh).
+
+    python -m oracle_amd.profsum stats DIR [--match SUBSTR ...]
+        per-kernel call count and durations from DIR/**/*kernel_stats.csv
+    python -m oracle_amd.profsum traffic --kernel SUBSTR --fetch DIR --write DIR
+                                         --copy-fetch DIR --copy-write DIR --copy-bytes N
+        HBM bytes per dispatch of the matching kernel: FETCH_SIZE and WRITE_SIZE (KiB per
+        dispatch, median over dispatches) each scaled by bytes / counter of a device-to-device
+        copy of N bytes profiled the same way.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import statistics
+import sys
+
+
+def _rows(directory: str, pattern: str) -> list[dict]:
+    rows: list[dict] = []
+    for f in sorted(glob.glob(f"{directory}/**/{pattern}", recursive=True)):
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def kernel_stats(directory: str, match: list[str] | None = None) -> list[dict]:
+    out = []
+    for r in _rows(directory, "*kernel_stats.csv"):
+        name = r["Name"]
+        if match and not any(m in name for m in match):
+            continue
+        out.append({
+            "kernel": name,
+            "calls": int(r["Calls"]),
+            "avg_us": float(r["AverageNs"]) / 1e3,
+            "min_us": float(r["MinNs"]) / 1e3,
+            "max_us": float(r["MaxNs"]) / 1e3,
+            "percent": float(r["Percentage"]),
+        })
+    return out
+
+
+def counter_median(directory: str, kernel: str, counter: str) -> tuple[float, int]:
+    vals = [float(r["Counter_Value"]) for r in _rows(directory, "*counter_collection.csv")
+            if kernel in r["Kernel_Name"] and r["Counter_Name"] == counter]
+    if not vals:
+        raise SystemExit(f"no {counter} samples for kernel matching {kernel!r} under {directory}")
+    return statistics.median(vals), len(vals)
+
+
+def traffic(kernel: str, fetch: str, write: str, copy_fetch: str, copy_write: str, copy_bytes: int,
+            copy_kernel: str = "copyBuffer") -> dict:
+    kf, nf = counter_median(fetch, kernel, "FETCH_SIZE")
+    kw, nw = counter_median(write, kernel, "WRITE_SIZE")
+    cf, _ = counter_median(copy_fetch, copy_kernel, "FETCH_SIZE")
+    cw, _ = counter_median(copy_write, copy_kernel, "WRITE_SIZE")
+    f_scale = copy_bytes / (cf * 1024.0)
+    w_scale = copy_bytes / (cw * 1024.0)
+    return {
+        "kernel": kernel,
+        "fetch_kib_per_dispatch": kf, "write_kib_per_dispatch": kw, "dispatches": [nf, nw],
+        "copy_bytes": copy_bytes, "copy_fetch_kib": cf, "copy_write_kib": cw,
+        "fetch_scale": f_scale, "write_scale": w_scale,
+        "fetch_bytes": kf * 1024.0 * f_scale, "write_bytes": kw * 1024.0 * w_scale,
+        "traffic_bytes": kf * 1024.0 * f_scale + kw * 1024.0 * w_scale,
+    }
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("dir")
+    s.add_argument("--match", nargs="*")
+    t = sub.add_parser("traffic")
+    for k in ("kernel", "fetch", "write", "copy_fetch", "copy_write"):
+        t.add_argument("--" + k.replace("_", "-"), required=True)
+    t.add_argument("--copy-bytes", type=int, required=True)
+    a = ap.parse_args(argv)
+    if a.cmd == "stats":
+        rows = kernel_stats(a.dir, a.match)
+        print(f"{'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'pct':>7}  kernel")
+        for r in rows:
+            print(f"{r['calls']:>6} {r['avg_us']:>10.3f} {r['min_us']:>10.3f} {r['max_us']:>10.3f} "
+                  f"{r['percent']:>7.2f}  {r['kernel'][:160]}")
+        return 0
+    print(json.dumps(traffic(a.kernel, a.fetch, a.write, a.copy_fetch, a.copy_write, a.copy_bytes), indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
