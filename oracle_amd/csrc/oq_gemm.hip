@@ -11,13 +11,12 @@
 //   1. activations -> F16 image Xhat[m][K] in scratch.  From F32 x the Q8_K quantization is
 //      the one of quantize_q8k (bit-identical q and d) and Xhat = f16(d*q); caller-supplied
 //      Q8_K blocks are converted the same way.
-//   2. GEMM: a 128 (m) x 256 (n) output tile per 1024-thread workgroup over one K-split of
-//      whole super-blocks, in steps of 64 k, double-buffered in LDS.  Eight waves issue the
-//      MFMAs (each a 64 x 64 sub-tile, four 32 x 32 accumulators) from one pair of F16 tiles
-//      while the other eight copy the next step's activations into the other pair and
-//      dequantize the next step's 4-bit weights into it.  Two VALU-issuing waves per SIMD keep
-//      the vector ALU at full rate (one wave alone issues at about half rate) and the matrix
-//      cores run beside them.
+//   2. GEMM: a 128 (m) x 256 (n) output tile per 256-thread workgroup (one wave per SIMD)
+//      over one K-split of whole super-blocks, in steps of 64 k, double-buffered in LDS.  Each
+//      wave issues the MFMAs of its 64 x 128 sub-tile (eight 32 x 32 accumulators) from one
+//      pair of F16 tiles and, while they run, copies its share of the next step's activations
+//      into the other pair and dequantizes its share of the next step's 4-bit weights into it.
+//      Large sub-tiles keep the LDS operand traffic near 96 KB per step.
 //   3. with more than one K-split, partial tiles go to scratch and a reduction kernel adds
 //      them in split order (deterministic).
 //
@@ -36,12 +35,11 @@ typedef float float2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int kBM = 128, kBN = 256, kBK = 64;
-constexpr int kThreads = 1024;
+constexpr int kThreads = 256;       // 4 waves, one per SIMD
 constexpr uint64_t kMinK = 4096;
 constexpr int kMaxSplits = 8;
 constexpr int kLdsA = kBM * kBK;    // f16 elements per A tile buffer
 constexpr int kLdsB = kBN * kBK;    // f16 elements per B tile buffer
-constexpr int kRawB = kBN * 128;    // q4_K quants of one super-block for the tile's 256 weight rows
 
 // F16 tiles: row r holds 64 k as eight 16-byte chunks; logical chunk c sits at physical chunk
 // c ^ ((r / 2) % 8), which keeps the MFMA operand reads and the tile writes free of LDS bank
@@ -91,84 +89,71 @@ struct Tile {
     uint32_t sb0;  // first super-block of this split
 };
 
-// Raw quant slot c (16 bytes) of a super-block holds chunk (row c/8, piece ((c/4)%2) ^ h(row),
-// group (c%4) ^ f(row)) with h(row) = (row/2)%2, f(row) = (row/4)%4.  Four consecutive slots
-// are one 64-byte line of one weight row (the chunks of one piece, see oq_layout.h), so the
-// global loads that fill the slots are fully coalesced; the swizzle makes the per-row
-// read-back free of LDS bank conflicts.
-OQ_DEVICE uint32_t raw_slot(uint32_t row, uint32_t piece, uint32_t g) {
-    return 8 * row + 4 * (piece ^ ((row >> 1) & 1)) + (g ^ ((row >> 2) & 3));
-}
-
-// ---------------------------------------------------------------- converter waves
+// ---------------------------------------------------------------- conversion share
 //
-// Waves 8..15 (thread index u = tid - 512, 0..511):
-//   activations: 16-byte chunks u and u + 512 of the step's 128 x 64 F16 tile (row c/8,
+// Thread u = tid (0..255) of the workgroup:
+//   activations: 16-byte chunks u + 256 j (j = 0..3) of the step's 128 x 64 F16 tile (row c/8,
 //                chunk c%8), copied from the F16 image;
-//   weights:     row u % 256, piece u / 256 (32 weights) of the step's 64-group, dequantized
-//                from the raw quants in LDS.
-// The raw quants of super-block i+1 are loaded while super-block i is converted: slots
-// 512 j + u (j = 0..3), in two halves of two.
+//   weights:     row u of the tile: per super-block the thread loads both 64-byte lines of the
+//                row (piece 0 and 1: four 16-byte chunks each, one per 64-group, adjacent in
+//                the row layout of oq_layout.h) and dequantizes one chunk of each (64 weights)
+//                per step.
 
-struct QuantHalf {
-    uint4 q0, q1;
+struct Lines {
+    uint4 p0[4], p1[4];  // piece 0 / piece 1 chunk of group 0..3
 };
 
-OQ_DEVICE uint4 load_quant_slot(const DeviceMatrix& w, const Tile& t, uint64_t sb, uint32_t c) {
+OQ_DEVICE Lines load_lines(const DeviceMatrix& w, const Tile& t, uint64_t sb, int u) {
     const uint64_t nsb = w.k / kQK;
-    const uint32_t row = c >> 3;
-    const uint32_t piece = ((c >> 2) & 1) ^ ((row >> 1) & 1), g = (c & 3) ^ ((row >> 2) & 3);
-    uint64_t n = t.n0 + row;
+    uint64_t n = t.n0 + u;
     n = n < w.n ? n : w.n - 1;
-    return *reinterpret_cast<const uint4*>(w.base + n * w.pitch + 16 * perm_chunk(nsb, sb, g, piece));
-}
-
-OQ_DEVICE void load_quant_half(QuantHalf& l, const DeviceMatrix& w, const Tile& t, uint64_t sb, int h, int u) {
-    l.q0 = load_quant_slot(w, t, sb, 512u * (2 * h) + u);
-    l.q1 = load_quant_slot(w, t, sb, 512u * (2 * h + 1) + u);
-}
-
-OQ_DEVICE void store_quant_half(const QuantHalf& l, uint8_t* raw, int h, int u) {
-    *reinterpret_cast<uint4*>(raw + 16 * (512 * (2 * h) + u)) = l.q0;
-    *reinterpret_cast<uint4*>(raw + 16 * (512 * (2 * h + 1) + u)) = l.q1;
+    const uint8_t* row = w.base + n * w.pitch;
+    const uint4* q0 = reinterpret_cast<const uint4*>(row + 16 * perm_chunk(nsb, sb, 0, 0));
+    const uint4* q1 = reinterpret_cast<const uint4*>(row + 16 * perm_chunk(nsb, sb, 0, 1));
+    Lines l;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        l.p0[g] = q0[g];
+        l.p1[g] = q1[g];
+    }
+    return l;
 }
 
 OQ_DEVICE uint4 load_header(const DeviceMatrix& w, const Tile& t, uint64_t sb, int u) {
-    uint64_t n = t.n0 + (u & 255);
+    uint64_t n = t.n0 + u;
     n = n < w.n ? n : w.n - 1;
     return *reinterpret_cast<const uint4*>(w.base + n * w.pitch + 128 * (w.k / kQK) + 16 * sb);
 }
 
 struct Act {
-    uint4 c0, c1;  // chunks u and u + 512 of one step's activation tile
+    uint4 c[4];  // chunks u + 256 j of one step's activation tile
 };
-
-OQ_DEVICE uint4 load_act_chunk(const _Float16* a16, const DeviceMatrix& w, int m, const Tile& t, uint32_t step,
-                               uint32_t c) {
-    uint64_t row = t.m0 + (c >> 3);
-    row = row < (uint64_t)m ? row : (uint64_t)m - 1;
-    return *reinterpret_cast<const uint4*>(a16 + row * w.k + (uint64_t)t.sb0 * kQK + (uint64_t)step * kBK +
-                                           8 * (c & 7));
-}
 
 OQ_DEVICE Act load_act(const _Float16* a16, const DeviceMatrix& w, int m, const Tile& t, uint32_t step, int u) {
     Act a;
-    a.c0 = load_act_chunk(a16, w, m, t, step, u);
-    a.c1 = load_act_chunk(a16, w, m, t, step, u + 512);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t c = u + 256 * j;
+        uint64_t row = t.m0 + (c >> 3);
+        row = row < (uint64_t)m ? row : (uint64_t)m - 1;
+        a.c[j] = *reinterpret_cast<const uint4*>(a16 + row * w.k + (uint64_t)t.sb0 * kQK + (uint64_t)step * kBK +
+                                                 8 * (c & 7));
+    }
     return a;
 }
 
 OQ_DEVICE void store_act(const Act& a, _Float16* As, int u) {
-    *reinterpret_cast<uint4*>(As + tile_off(u >> 3, u & 7)) = a.c0;
-    *reinterpret_cast<uint4*>(As + tile_off((u + 512) >> 3, u & 7)) = a.c1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int c = u + 256 * j;
+        *reinterpret_cast<uint4*>(As + tile_off(c >> 3, c & 7)) = a.c[j];
+    }
 }
 
-// Hides a value from the optimizer, so that the byte extractions below map onto
-// v_cvt_f32_ubyte<i>.
-OQ_DEVICE uint32_t opaque(uint32_t v) {
-    asm volatile("" : "+v"(v));
-    return v;
-}
+// Identity byte permutation (one v_perm_b32): keeps the optimizer from merging a byte mask into
+// the extractions below, so that they map onto v_cvt_f32_ubyte<i>, while remaining an ordinary
+// vector instruction the scheduler can move.
+OQ_DEVICE uint32_t opaque(uint32_t v) { return __builtin_amdgcn_perm(0u, v, 0x03020100u); }
 
 template <int I>
 OQ_DEVICE float ubyte(uint32_t u) {
@@ -183,11 +168,30 @@ OQ_DEVICE uint2 convert4(uint32_t u, float s, float c) {
     return r;
 }
 
-// f16((d*sc)*q - dmin*m) for the 32 weights of group G, piece P of this thread's weight row:
+// f16((d*sc)*q - dmin*m) for the 32 weights of one chunk of group G of weight row r:
 // low nibbles -> k = 16P + i (sub-block 2G), high nibbles -> k = 32 + 16P + i (sub-block 2G+1)
+OQ_DEVICE void convert_chunk(uint4 qv, float ds0, float dm0, float ds1, float dm1, _Float16* Bs, int r, int piece) {
+    const uint32_t words[4] = {qv.x, qv.y, qv.z, qv.w};
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t l4 = opaque(words[j] & 0x0F0F0F0Fu), h4 = opaque((words[j] >> 4) & 0x0F0F0F0Fu);
+        const uint2 a = convert4(l4, ds0, -dm0), b = convert4(h4, ds1, -dm1);
+        lo[2 * j] = a.x;
+        lo[2 * j + 1] = a.y;
+        hi[2 * j] = b.x;
+        hi[2 * j + 1] = b.y;
+    }
+    const int c = 2 * piece;
+    *reinterpret_cast<uint4*>(Bs + tile_off(r, c)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    *reinterpret_cast<uint4*>(Bs + tile_off(r, c + 1)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+    *reinterpret_cast<uint4*>(Bs + tile_off(r, c + 4)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    *reinterpret_cast<uint4*>(Bs + tile_off(r, c + 5)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+}
+
+// both chunks (pieces) of group G of weight row u
 template <int G>
-OQ_DEVICE void convert_weights(uint4 hdr, const uint8_t* raw, _Float16* Bs, int u) {
-    const int row = u & 255, piece = u >> 8;
+OQ_DEVICE void convert_weights(uint4 hdr, const Lines& l, _Float16* Bs, int u) {
     // hardware f16 -> f32 (exact for every finite value; NaN payloads do not matter here)
     const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu));
     const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
@@ -202,41 +206,106 @@ OQ_DEVICE void convert_weights(uint4 hdr, const uint8_t* raw, _Float16* Bs, int 
         ds1 = d * (float)sc1;
         dm1 = dmin * (float)mn1;
     }
-    const uint4 qv = *reinterpret_cast<const uint4*>(raw + 16 * raw_slot(row, piece, G));
-    const uint32_t words[4] = {qv.x, qv.y, qv.z, qv.w};
-    uint32_t lo[8], hi[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t l4 = opaque(words[j] & 0x0F0F0F0Fu), h4 = opaque((words[j] >> 4) & 0x0F0F0F0Fu);
-        const uint2 a = convert4(l4, ds0, -dm0), b = convert4(h4, ds1, -dm1);
-        lo[2 * j] = a.x;
-        lo[2 * j + 1] = a.y;
-        hi[2 * j] = b.x;
-        hi[2 * j + 1] = b.y;
-    }
-    const int c = 2 * piece;
-    *reinterpret_cast<uint4*>(Bs + tile_off(row, c)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-    *reinterpret_cast<uint4*>(Bs + tile_off(row, c + 1)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-    *reinterpret_cast<uint4*>(Bs + tile_off(row, c + 4)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-    *reinterpret_cast<uint4*>(Bs + tile_off(row, c + 5)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+    convert_chunk(l.p0[G], ds0, dm0, ds1, dm1, Bs, u, 0);
+    convert_chunk(l.p1[G], ds0, dm0, ds1, dm1, Bs, u, 1);
 }
 
 // ---------------------------------------------------------------- MFMA waves
 //
-// Waves 0..7 in a 2 (m) x 4 (n) grid, each a 64 x 64 sub-tile: 2 x 2 accumulators of 32 x 32.
-OQ_DEVICE void mma_step(const _Float16* As, const _Float16* Bs, int wm, int wn, int lane, float16v (&acc)[2][2]) {
-    const int ra = 64 * wm + (lane & 31), rb = 64 * wn + (lane & 31), h = lane >> 5;
+// Wave w in a 2 (m) x 2 (n) grid: a 64 x 128 sub-tile, 2 x 4 accumulators of 32 x 32.
+OQ_DEVICE void mma_step(const _Float16* As, const _Float16* Bs, int wm, int wn, int lane, float16v (&acc)[2][4]) {
+    const int ra = 64 * wm + (lane & 31), rb = 128 * wn + (lane & 31), h = lane >> 5;
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-        half8 a[2], b[2];
+        half8 a[2], b[4];
 #pragma unroll
         for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const half8*>(As + tile_off(ra + 32 * i, 2 * ks + h));
 #pragma unroll
-        for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const half8*>(Bs + tile_off(rb + 32 * j, 2 * ks + h));
+        for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const half8*>(Bs + tile_off(rb + 32 * j, 2 * ks + h));
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+}
+
+// One step of one wave, in an explicit instruction order: the MFMAs of this step's tiles (64 x
+// 128 sub-tile, four k-slices of 16) with, after every fourth MFMA, one unit of the conversion
+// of the next step (four weight nibble-words -> 32 f16, i.e. one 16-byte quant dword pair of
+// lanes) and the operand reads of the next k-slice issued one slice ahead.  A wave issues in
+// order, so MFMAs grouped together would hold the conversion back until the last one issued;
+// interleaved, the vector ALU works while the matrix core executes.  sched_barrier keeps the
+// compiler from regrouping them.
+template <int G>
+OQ_DEVICE void fused_step(const _Float16* Ac, const _Float16* Bc, _Float16* An, _Float16* Bn, int wm, int wn,
+                          int lane, float16v (&acc)[2][4], const Act& act, uint4 hdr, const Lines& l, int u) {
+    const int ra = 64 * wm + (lane & 31), rb = 128 * wn + (lane & 31), h = lane >> 5;
+    half8 a[2], b[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const half8*>(Ac + tile_off(ra + 32 * i, h));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const half8*>(Bc + tile_off(rb + 32 * j, h));
+    store_act(act, An, u);
+    // scales of sub-blocks 2G, 2G+1 of weight row u
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu));
+    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
+    uint32_t sc0, mn0, sc1, mn1;
+    scale_min_k4(2 * G, hdr.y, hdr.z, hdr.w, sc0, mn0);
+    scale_min_k4(2 * G + 1, hdr.y, hdr.z, hdr.w, sc1, mn1);
+    float ds0, dm0, ds1, dm1;
+    {
+#pragma clang fp contract(off)
+        ds0 = d * (float)sc0;
+        dm0 = dmin * (float)mn0;
+        ds1 = d * (float)sc1;
+        dm1 = dmin * (float)mn1;
+    }
+    const uint32_t words[8] = {l.p0[G].x, l.p0[G].y, l.p0[G].z, l.p0[G].w,
+                               l.p1[G].x, l.p1[G].y, l.p1[G].z, l.p1[G].w};
+    uint32_t lo[8], hi[8], l4 = 0, h4 = 0;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        half8 an[2], bn[4];
+        if (ks < 3) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) an[i] = *reinterpret_cast<const half8*>(Ac + tile_off(ra + 32 * i, 2 * (ks + 1) + h));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bn[j] = *reinterpret_cast<const half8*>(Bc + tile_off(rb + 32 * j, 2 * (ks + 1) + h));
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int i = q >> 2, j = q & 3;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            // weight pair p = 8 ks + q of the 32 this thread converts: quant word p/4, pair p%4
+            // (0, 1: low nibbles of bytes 0-1 / 2-3; 2, 3: high nibbles)
+            const int p = 8 * ks + q, wd = p >> 2, pp = p & 3, wi = wd & 3;
+            if (pp == 0) {
+                l4 = opaque(words[wd] & 0x0F0F0F0Fu);
+                h4 = opaque((words[wd] >> 4) & 0x0F0F0F0Fu);
+            }
+            if (pp == 0) lo[2 * wi] = pack_f16(__builtin_fmaf(ubyte<0>(l4), ds0, -dm0), __builtin_fmaf(ubyte<1>(l4), ds0, -dm0));
+            if (pp == 1) lo[2 * wi + 1] = pack_f16(__builtin_fmaf(ubyte<2>(l4), ds0, -dm0), __builtin_fmaf(ubyte<3>(l4), ds0, -dm0));
+            if (pp == 2) hi[2 * wi] = pack_f16(__builtin_fmaf(ubyte<0>(h4), ds1, -dm1), __builtin_fmaf(ubyte<1>(h4), ds1, -dm1));
+            if (pp == 3) {
+                hi[2 * wi + 1] = pack_f16(__builtin_fmaf(ubyte<2>(h4), ds1, -dm1), __builtin_fmaf(ubyte<3>(h4), ds1, -dm1));
+                if (wi == 3) {  // a whole 16-byte chunk (32 weights) of piece wd/4 is ready
+                    const int c = 2 * (wd >> 2);
+                    *reinterpret_cast<uint4*>(Bn + tile_off(u, c)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                    *reinterpret_cast<uint4*>(Bn + tile_off(u, c + 1)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+                    *reinterpret_cast<uint4*>(Bn + tile_off(u, c + 4)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                    *reinterpret_cast<uint4*>(Bn + tile_off(u, c + 5)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (ks < 3) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) a[i] = an[i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = bn[j];
+        }
     }
 }
 
@@ -244,114 +313,101 @@ OQ_DEVICE void mma_step(const _Float16* As, const _Float16* Bs, int wm, int wn, 
 // not wait for outstanding global loads (the prefetches in flight across the barrier).
 OQ_DEVICE void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// grid: x = n-tile, y = m-tile, z = K-split.  Output: y (one split) or partial[z][m][n].
+// Work units (n-tile, m-tile, K-split) are numbered so that the workgroups one XCD receives
+// (workgroup ids are dealt to the eight XCDs in turn) share a K-split and a band of n-tiles:
+// each XCD then reads its activation rows once and its weight rows once.
+struct Unit {
+    uint32_t nt, mt, z;
+};
+
+OQ_DEVICE Unit unit_of(uint32_t id, uint32_t tiles_n, uint32_t tiles_m, uint32_t splits) {
+    const uint32_t total = tiles_n * tiles_m * splits;
+    uint32_t u = id;
+    if (total % 8 == 0) u = (id % 8) * (total / 8) + id / 8;
+    Unit r;
+    r.mt = u % tiles_m;
+    r.nt = (u / tiles_m) % tiles_n;
+    r.z = u / (tiles_m * tiles_n);
+    return r;
+}
+
+// grid: tiles_n * tiles_m * splits workgroups.  Output: y (one split) or partial[z][m][n].
 //
-// Step s (64 k) is multiplied from tile buffer s%2 while buffer (s+1)%2 receives step s+1;
-// all waves meet at one barrier per step (and two in the prologue), so every wave passes the
-// same number of barriers.  Converter pipeline: activations two steps ahead; for super-block
-// i (steps 4i..4i+3) the raw quants of super-block i+1 are loaded at steps 4i-2 / 4i-1 and
-// stored to the other raw buffer at steps 4i / 4i+1 (read from step 4i+3 on), and its headers
-// are loaded at step 4i.
+// Each of the four waves (one per SIMD) multiplies its 64 x 128 sub-tile of step s from tile
+// buffer s%2 while it converts its share of step s+1 (weight row u = tid, activation chunks
+// u + 256 j) into buffer (s+1)%2: the MFMAs run asynchronously in the matrix core while the
+// same wave's conversion instructions issue on the vector ALU.  One barrier per step.
+// Activations are loaded two steps ahead, the weight lines and headers of super-block i+1 at
+// the first step of super-block i.
 __global__ __launch_bounds__(kThreads) void gemm_q4k_f16_kernel(DeviceMatrix w, int m, const _Float16* a16,
-                                                               uint32_t splits, float* __restrict__ out) {
-    __shared__ __align__(16) _Float16 tiles[2 * (kLdsA + kLdsB)];
-    __shared__ __align__(16) uint8_t raw[2][kRawB];
-    _Float16* const As[2] = {tiles, tiles + kLdsA};
-    _Float16* const Bs[2] = {tiles + 2 * kLdsA, tiles + 2 * kLdsA + kLdsB};
+                                                               uint32_t tiles_n, uint32_t tiles_m, uint32_t splits,
+                                                               float* __restrict__ out) {
+    // separate objects per buffer, so that the compiler may interleave the conversion's stores
+    // to one buffer with the operand loads from the other
+    __shared__ __align__(16) _Float16 As0[kLdsA], Bs0[kLdsB];
+    __shared__ __align__(16) _Float16 As1[kLdsA], Bs1[kLdsB];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1, u = tid;
     const uint32_t nsb = (uint32_t)(w.k / kQK);
-    const uint32_t z = blockIdx.z;
+    const Unit un = unit_of(blockIdx.x, tiles_n, tiles_m, splits);
+    const uint32_t z = un.z;
     Tile t;
-    t.n0 = (uint64_t)blockIdx.x * kBN;
-    t.m0 = (uint64_t)blockIdx.y * kBM;
+    t.n0 = (uint64_t)un.nt * kBN;
+    t.m0 = (uint64_t)un.mt * kBM;
     t.sb0 = (uint32_t)((uint64_t)z * nsb / splits);
     const uint32_t sb1 = (uint32_t)((uint64_t)(z + 1) * nsb / splits);
-    const uint32_t nsbu = sb1 - t.sb0;  // >= 1: splits <= nsb
-
-    if (wave < 8) {
-        const int wm = wave >> 2, wn = wave & 3;
-        float16v acc[2][2] = {};
-        lds_barrier();  // raw quants of super-block 0 stored
-        lds_barrier();  // step 0 converted
-        for (uint32_t i = 0; i < nsbu; ++i) {
-            mma_step(As[0], Bs[0], wm, wn, lane, acc);
-            lds_barrier();
-            mma_step(As[1], Bs[1], wm, wn, lane, acc);
-            lds_barrier();
-            mma_step(As[0], Bs[0], wm, wn, lane, acc);
-            lds_barrier();
-            mma_step(As[1], Bs[1], wm, wn, lane, acc);
-            lds_barrier();
-        }
-        // result register r of lane l: row 8*(r/4) + 4*(l/32) + r%4, column l%32
-        float* o = out + (uint64_t)z * (uint64_t)m * w.n;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint64_t col = t.n0 + 64 * wn + 32 * j + (lane & 31);
-            if (col >= w.n) continue;
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint64_t row = t.m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-                    if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][r];
-                }
-            }
-        }
-        return;
-    }
-
-    const int u = tid - 512;
+    const uint32_t nsbu = sb1 - t.sb0;   // >= 1: splits <= nsb
     const uint32_t last = 4 * nsbu - 1;  // last step
     auto step_of = [last](uint32_t s) { return s <= last ? s : last; };
     auto sb_of = [&](uint32_t i) { return (uint64_t)t.sb0 + (i < nsbu ? i : nsbu - 1); };
-    QuantHalf qa, qb;  // halves 0 and 1 of the next super-block's raw quants
-    load_quant_half(qa, w, t, sb_of(0), 0, u);
-    load_quant_half(qb, w, t, sb_of(0), 1, u);
+
+    float16v acc[2][4] = {};
+    Lines cur = load_lines(w, t, sb_of(0), u), nxt;
     uint4 hdr = load_header(w, t, sb_of(0), u), hdr_next;
     Act a0 = load_act(a16, w, m, t, 0, u);
     Act a1 = load_act(a16, w, m, t, step_of(1), u);
-    store_quant_half(qa, raw[0], 0, u);
-    store_quant_half(qb, raw[0], 1, u);
-    lds_barrier();  // raw quants of super-block 0 stored
-    store_act(a0, As[0], u);
-    convert_weights<0>(hdr, raw[0], Bs[0], u);
+    store_act(a0, As0, u);
+    convert_weights<0>(hdr, cur, Bs0, u);
     a0 = load_act(a16, w, m, t, step_of(2), u);
-    load_quant_half(qa, w, t, sb_of(1), 0, u);
-    load_quant_half(qb, w, t, sb_of(1), 1, u);
     lds_barrier();  // step 0 converted
-    // Every iteration passes four barriers, as every MFMA-wave iteration does.
     for (uint32_t i = 0; i < nsbu; ++i) {
         const uint32_t s = 4 * i;
-        const uint8_t* rc = raw[i & 1];
-        uint8_t* rn = raw[(i + 1) & 1];
-        // step s: convert s+1
-        store_quant_half(qa, rn, 0, u);
+        // step s: multiply s, convert s+1
+        nxt = load_lines(w, t, sb_of(i + 1), u);
         hdr_next = load_header(w, t, sb_of(i + 1), u);
-        store_act(a1, As[1], u);
-        convert_weights<1>(hdr, rc, Bs[1], u);
+        fused_step<1>(As0, Bs0, As1, Bs1, wm, wn, lane, acc, a1, hdr, cur, u);
         a1 = load_act(a16, w, m, t, step_of(s + 3), u);
         lds_barrier();
-        // step s+1: convert s+2
-        store_quant_half(qb, rn, 1, u);
-        store_act(a0, As[0], u);
-        convert_weights<2>(hdr, rc, Bs[0], u);
+        // step s+1
+        fused_step<2>(As1, Bs1, As0, Bs0, wm, wn, lane, acc, a0, hdr, cur, u);
         a0 = load_act(a16, w, m, t, step_of(s + 4), u);
         lds_barrier();
-        // step s+2: convert s+3
-        store_act(a1, As[1], u);
-        convert_weights<3>(hdr, rc, Bs[1], u);
+        // step s+2
+        fused_step<3>(As0, Bs0, As1, Bs1, wm, wn, lane, acc, a1, hdr, cur, u);
         a1 = load_act(a16, w, m, t, step_of(s + 5), u);
-        load_quant_half(qa, w, t, sb_of(i + 2), 0, u);
         lds_barrier();
-        // step s+3: convert s+4 (first group of super-block i+1)
+        // step s+3: convert the first group of super-block i+1
+        cur = nxt;
         hdr = hdr_next;
-        store_act(a0, As[0], u);
-        convert_weights<0>(hdr, rn, Bs[0], u);
+        fused_step<0>(As1, Bs1, As0, Bs0, wm, wn, lane, acc, a0, hdr, cur, u);
         a0 = load_act(a16, w, m, t, step_of(s + 6), u);
-        load_quant_half(qb, w, t, sb_of(i + 2), 1, u);
         lds_barrier();
+    }
+    // result register r of lane l: row 8*(r/4) + 4*(l/32) + r%4, column l%32
+    float* o = out + (uint64_t)z * (uint64_t)m * w.n;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint64_t col = t.n0 + 128 * wn + 32 * j + (lane & 31);
+        if (col >= w.n) continue;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint64_t row = t.m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][r];
+            }
+        }
     }
 }
 
@@ -433,9 +489,9 @@ hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const float* x, co
     } else {
         hipLaunchKernelGGL(q8k_to_f16_kernel, dim3(qgrid), dim3(256), 0, s, q8k, nblocks, a16);
     }
-    const dim3 grid(p.tiles_n, p.tiles_m, p.splits);
-    hipLaunchKernelGGL(gemm_q4k_f16_kernel, grid, dim3(kThreads), 0, s, w, m, a16, p.splits,
-                       p.splits > 1 ? part : y);
+    const unsigned wgs = p.tiles_n * p.tiles_m * p.splits;
+    hipLaunchKernelGGL(gemm_q4k_f16_kernel, dim3(wgs), dim3(kThreads), 0, s, w, m, a16, p.tiles_n, p.tiles_m,
+                       p.splits, p.splits > 1 ? part : y);
     if (p.splits > 1) {
         const uint64_t count = (uint64_t)m * w.n;
         if (count % 4 == 0) {
