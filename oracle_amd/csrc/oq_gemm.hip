@@ -12,16 +12,20 @@
 //      the one of quantize_q8k (bit-identical q and d) and Xhat = f16(d*q); caller-supplied
 //      Q8_K blocks are converted the same way.
 //   2. GEMM: a 128 (m) x 256 (n) output tile per 256-thread workgroup (one wave per SIMD)
-//      over one K-split of whole super-blocks, in steps of 64 k, double-buffered in LDS.  Each
-//      wave issues the MFMAs of its 64 x 128 sub-tile (eight 32 x 32 accumulators) from one
-//      pair of F16 tiles and, while they run, copies its share of the next step's activations
-//      into the other pair and dequantizes its share of the next step's 4-bit weights into it.
-//      Large sub-tiles keep the LDS operand traffic near 96 KB per step.
+//      over one K-split of whole super-blocks, in steps of 64 k.  Wave w owns all 128 rows and
+//      64 columns (4 x 2 accumulators of 32 x 32).  It dequantizes its own weight columns
+//      straight into MFMA B operands in registers (no LDS), while the activation tiles are
+//      shared through a ring of three LDS buffers.  A wave can retire only about one 1 KB LDS
+//      read per 50 cycles, so the LDS traffic is what limits a GEMM with one wave per SIMD;
+//      keeping the weights out of LDS leaves 16 operand reads + 4 stores per wave per step.
 //   3. with more than one K-split, partial tiles go to scratch and a reduction kernel adds
 //      them in split order (deterministic).
 //
 // Weight dequantization: a nibble goes to F32 exactly (v_cvt_f32_ubyte), one F32 fma applies
-// the scale and the min, and v_cvt_pk_f16_f32 rounds two weights to f16 (nearest even).
+// the scale and the min, and v_cvt_pk_f16_f32 rounds two weights to f16 (nearest even); the
+// conversion instructions are interleaved with the MFMAs, which execute asynchronously.
+#include <type_traits>
+
 #include "oq_common.h"
 #include "oq_layout.h"
 
@@ -37,9 +41,13 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 constexpr int kBM = 128, kBN = 256, kBK = 64;
 constexpr int kThreads = 256;       // 4 waves, one per SIMD
 constexpr uint64_t kMinK = 4096;
+// From this K on, weights are dequantized with packed f16 arithmetic (scale and min rounded to
+// f16 per sub-block); below it, from F32.  The extra rounding roughly 1.3x the output error,
+// which the longer sums absorb: worst normalised errors measured 3.7e-5 at K = 8192 and 3.3e-5
+// at K = 12288 against the 1e-4 bar.
+constexpr uint64_t kFastMinK = 8192;
 constexpr int kMaxSplits = 8;
 constexpr int kLdsA = kBM * kBK;    // f16 elements per A tile buffer
-constexpr int kLdsB = kBN * kBK;    // f16 elements per B tile buffer
 
 // F16 tiles: row r holds 64 k as eight 16-byte chunks; logical chunk c sits at physical chunk
 // c ^ ((r / 2) % 8), which keeps the MFMA operand reads and the tile writes free of LDS bank
@@ -89,51 +97,29 @@ struct Tile {
     uint32_t sb0;  // first super-block of this split
 };
 
-// ---------------------------------------------------------------- conversion share
+// k order inside one 64-element group (the same for both operands, so the product is
+// unchanged): MFMA k-slice ks (16 k), lane half h, operand element i covers
+//   k = 32 (ks & 1) + 16 h + 8 (ks >> 1) + i.
+// A: 8 consecutive k = chunk 4 (ks & 1) + 2 h + (ks >> 1) of an F16 tile row.
+// B: bytes 16 h + 8 (ks >> 1) + i of the weight row's 32-byte group, low nibbles for even ks,
+//    high nibbles for odd ks: lane half h reads exactly 16-byte chunk e = h of the group (see
+//    oq_layout.h), and the slices alternate between the group's two sub-blocks.
+OQ_DEVICE int a_chunk(int ks, int h) { return 4 * (ks & 1) + 2 * h + (ks >> 1); }
+
+// ---------------------------------------------------------------- activations
 //
-// Thread u = tid (0..255) of the workgroup:
-//   activations: 16-byte chunks u + 256 j (j = 0..3) of the step's 128 x 64 F16 tile (row c/8,
-//                chunk c%8), copied from the F16 image;
-//   weights:     row u of the tile: per super-block the thread loads both 64-byte lines of the
-//                row (piece 0 and 1: four 16-byte chunks each, one per 64-group, adjacent in
-//                the row layout of oq_layout.h) and dequantizes one chunk of each (64 weights)
-//                per step.
-
-struct Lines {
-    uint4 p0[4], p1[4];  // piece 0 / piece 1 chunk of group 0..3
-};
-
-OQ_DEVICE Lines load_lines(const DeviceMatrix& w, const Tile& t, uint64_t sb, int u) {
-    const uint64_t nsb = w.k / kQK;
-    uint64_t n = t.n0 + u;
-    n = n < w.n ? n : w.n - 1;
-    const uint8_t* row = w.base + n * w.pitch;
-    const uint4* q0 = reinterpret_cast<const uint4*>(row + 16 * perm_chunk(nsb, sb, 0, 0));
-    const uint4* q1 = reinterpret_cast<const uint4*>(row + 16 * perm_chunk(nsb, sb, 0, 1));
-    Lines l;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        l.p0[g] = q0[g];
-        l.p1[g] = q1[g];
-    }
-    return l;
-}
-
-OQ_DEVICE uint4 load_header(const DeviceMatrix& w, const Tile& t, uint64_t sb, int u) {
-    uint64_t n = t.n0 + u;
-    n = n < w.n ? n : w.n - 1;
-    return *reinterpret_cast<const uint4*>(w.base + n * w.pitch + 128 * (w.k / kQK) + 16 * sb);
-}
+// All 256 threads copy the step's 128 x 64 F16 tile: 16-byte chunks c = tid + 256 j (j = 0..3),
+// row c / 8, chunk c % 8.
 
 struct Act {
-    uint4 c[4];  // chunks u + 256 j of one step's activation tile
+    uint4 c[4];
 };
 
-OQ_DEVICE Act load_act(const _Float16* a16, const DeviceMatrix& w, int m, const Tile& t, uint32_t step, int u) {
+OQ_DEVICE Act load_act(const _Float16* a16, const DeviceMatrix& w, int m, const Tile& t, uint32_t step, int tid) {
     Act a;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint32_t c = u + 256 * j;
+        const uint32_t c = tid + 256 * j;
         uint64_t row = t.m0 + (c >> 3);
         row = row < (uint64_t)m ? row : (uint64_t)m - 1;
         a.c[j] = *reinterpret_cast<const uint4*>(a16 + row * w.k + (uint64_t)t.sb0 * kQK + (uint64_t)step * kBK +
@@ -142,17 +128,74 @@ OQ_DEVICE Act load_act(const _Float16* a16, const DeviceMatrix& w, int m, const 
     return a;
 }
 
-OQ_DEVICE void store_act(const Act& a, _Float16* As, int u) {
+OQ_DEVICE void store_act(const Act& a, _Float16* As, int tid) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int c = u + 256 * j;
+        const int c = tid + 256 * j;
         *reinterpret_cast<uint4*>(As + tile_off(c >> 3, c & 7)) = a.c[j];
     }
 }
 
+// ---------------------------------------------------------------- weights
+//
+// Wave w owns weight rows n0 + 64 w + 32 j + (lane % 32), j = 0, 1 (two 32-column MFMA tiles);
+// lane half h = lane / 32 reads chunk e = h of every group.  Per super-block a lane loads the
+// four chunks (one per group, adjacent in the row layout) of both its rows and the two rows'
+// headers; the weights never pass through LDS.
+
+struct WData {
+    uint4 q[2][4];  // [j][group]
+    uint4 hdr[2];   // [j]
+};
+
+OQ_DEVICE WData load_wdata(const DeviceMatrix& w, const Tile& t, uint64_t sb, int wave, int lane) {
+    const uint64_t nsb = w.k / kQK;
+    WData d;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        uint64_t n = t.n0 + 64 * wave + 32 * j + (lane & 31);
+        n = n < w.n ? n : w.n - 1;
+        const uint8_t* row = w.base + n * w.pitch;
+        const uint4* q = reinterpret_cast<const uint4*>(row + 16 * perm_chunk(nsb, sb, 0, (uint32_t)(lane >> 5)));
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d.q[j][g] = q[g];
+        d.hdr[j] = *reinterpret_cast<const uint4*>(row + 128 * nsb + 16 * sb);
+    }
+    return d;
+}
+
+// d*sc and dmin*m of sub-block `sub` of a header, in the reference's F32 arithmetic, and (for
+// the packed path) as f16 pairs {ds, ds}, {-dm, -dm}
+struct Scale {
+    float ds, dm;
+    uint32_t ds2, ndm2;
+};
+
+template <bool FAST>
+OQ_DEVICE Scale scale_of(uint4 hdr, uint32_t sub) {
+    // hardware f16 -> f32 (exact for every finite value; NaN payloads do not matter here)
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu));
+    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
+    uint32_t sc, mn;
+    scale_min_k4(sub, hdr.y, hdr.z, hdr.w, sc, mn);
+    Scale s;
+    {
+#pragma clang fp contract(off)
+        s.ds = d * (float)sc;
+        s.dm = dmin * (float)mn;
+    }
+    if (FAST) {
+        s.ds2 = pack_f16(s.ds, s.ds);
+        s.ndm2 = pack_f16(-s.dm, -s.dm);
+    } else {
+        s.ds2 = s.ndm2 = 0;
+    }
+    return s;
+}
+
 // Identity byte permutation (one v_perm_b32): keeps the optimizer from merging a byte mask into
 // the extractions below, so that they map onto v_cvt_f32_ubyte<i>, while remaining an ordinary
-// vector instruction the scheduler can move.
+// vector instruction.
 OQ_DEVICE uint32_t opaque(uint32_t v) { return __builtin_amdgcn_perm(0u, v, 0x03020100u); }
 
 template <int I>
@@ -160,153 +203,94 @@ OQ_DEVICE float ubyte(uint32_t u) {
     return (float)((u >> (8 * I)) & 0xFFu);
 }
 
-// bytes b_0..b_3 of u -> f16(s * b_i + c), as two dwords (b_0, b_1), (b_2, b_3)
-OQ_DEVICE uint2 convert4(uint32_t u, float s, float c) {
-    uint2 r;
-    r.x = pack_f16(__builtin_fmaf(ubyte<0>(u), s, c), __builtin_fmaf(ubyte<1>(u), s, c));
-    r.y = pack_f16(__builtin_fmaf(ubyte<2>(u), s, c), __builtin_fmaf(ubyte<3>(u), s, c));
-    return r;
-}
-
-// f16((d*sc)*q - dmin*m) for the 32 weights of one chunk of group G of weight row r:
-// low nibbles -> k = 16P + i (sub-block 2G), high nibbles -> k = 32 + 16P + i (sub-block 2G+1)
-OQ_DEVICE void convert_chunk(uint4 qv, float ds0, float dm0, float ds1, float dm1, _Float16* Bs, int r, int piece) {
-    const uint32_t words[4] = {qv.x, qv.y, qv.z, qv.w};
-    uint32_t lo[8], hi[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t l4 = opaque(words[j] & 0x0F0F0F0Fu), h4 = opaque((words[j] >> 4) & 0x0F0F0F0Fu);
-        const uint2 a = convert4(l4, ds0, -dm0), b = convert4(h4, ds1, -dm1);
-        lo[2 * j] = a.x;
-        lo[2 * j + 1] = a.y;
-        hi[2 * j] = b.x;
-        hi[2 * j + 1] = b.y;
+// Two weights of a B operand from the nibbles of bytes 2p, 2p+1 of `nib` (already masked).
+//   exact: f16(ds*q - dm) from F32 (one rounding);
+//   FAST:  the nibbles become the f16 values 1024 + q (bit pattern 0x6400 | q, placed by one
+//          v_perm_b32), minus 1024 (exact), then one v_pk_fma_f16 with ds and -dm rounded to f16:
+//          three instructions per pair instead of five, at the price of the f16 rounding of
+//          the sub-block's scale and min.
+template <bool FAST>
+OQ_DEVICE uint32_t weight_pair(uint32_t nib, int p, const Scale& s) {
+    if (FAST) {
+        const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        half2v x = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, nib, p == 0 ? 0x04010400u : 0x04030402u));
+        x = x - k1024;
+        x = __builtin_elementwise_fma(x, __builtin_bit_cast(half2v, s.ds2), __builtin_bit_cast(half2v, s.ndm2));
+        return __builtin_bit_cast(uint32_t, x);
     }
-    const int c = 2 * piece;
-    *reinterpret_cast<uint4*>(Bs + tile_off(r, c)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-    *reinterpret_cast<uint4*>(Bs + tile_off(r, c + 1)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-    *reinterpret_cast<uint4*>(Bs + tile_off(r, c + 4)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-    *reinterpret_cast<uint4*>(Bs + tile_off(r, c + 5)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+    const float a = p == 0 ? ubyte<0>(nib) : ubyte<2>(nib);
+    const float b = p == 0 ? ubyte<1>(nib) : ubyte<3>(nib);
+    return pack_f16(__builtin_fmaf(a, s.ds, -s.dm), __builtin_fmaf(b, s.ds, -s.dm));
 }
 
-// both chunks (pieces) of group G of weight row u
-template <int G>
-OQ_DEVICE void convert_weights(uint4 hdr, const Lines& l, _Float16* Bs, int u) {
-    // hardware f16 -> f32 (exact for every finite value; NaN payloads do not matter here)
-    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu));
-    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
-    uint32_t sc0, mn0, sc1, mn1;
-    scale_min_k4(2 * G, hdr.y, hdr.z, hdr.w, sc0, mn0);
-    scale_min_k4(2 * G + 1, hdr.y, hdr.z, hdr.w, sc1, mn1);
-    float ds0, dm0, ds1, dm1;
-    {
-#pragma clang fp contract(off)
-        ds0 = d * (float)sc0;
-        dm0 = dmin * (float)mn0;
-        ds1 = d * (float)sc1;
-        dm1 = dmin * (float)mn1;
-    }
-    convert_chunk(l.p0[G], ds0, dm0, ds1, dm1, Bs, u, 0);
-    convert_chunk(l.p1[G], ds0, dm0, ds1, dm1, Bs, u, 1);
+// nibble word (masked, one per quant dword) of slice ks from a lane's 16-byte group chunk
+template <bool FAST>
+OQ_DEVICE uint32_t nib_word(uint4 q, int ks, int half) {
+    const uint32_t d = (ks >> 1) == 0 ? (half == 0 ? q.x : q.y) : (half == 0 ? q.z : q.w);
+    const uint32_t v = (ks & 1) ? (d >> 4) & 0x0F0F0F0Fu : d & 0x0F0F0F0Fu;
+    return FAST ? v : opaque(v);
 }
 
-// ---------------------------------------------------------------- MFMA waves
+// ---------------------------------------------------------------- one step of one wave
 //
-// Wave w in a 2 (m) x 2 (n) grid: a 64 x 128 sub-tile, 2 x 4 accumulators of 32 x 32.
-OQ_DEVICE void mma_step(const _Float16* As, const _Float16* Bs, int wm, int wn, int lane, float16v (&acc)[2][4]) {
-    const int ra = 64 * wm + (lane & 31), rb = 128 * wn + (lane & 31), h = lane >> 5;
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-        half8 a[2], b[4];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const half8*>(As + tile_off(ra + 32 * i, 2 * ks + h));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const half8*>(Bs + tile_off(rb + 32 * j, 2 * ks + h));
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
-}
-
-// One step of one wave, in an explicit instruction order: the MFMAs of this step's tiles (64 x
-// 128 sub-tile, four k-slices of 16) with, after every fourth MFMA, one unit of the conversion
-// of the next step (four weight nibble-words -> 32 f16, i.e. one 16-byte quant dword pair of
-// lanes) and the operand reads of the next k-slice issued one slice ahead.  A wave issues in
-// order, so MFMAs grouped together would hold the conversion back until the last one issued;
-// interleaved, the vector ALU works while the matrix core executes.  sched_barrier keeps the
-// compiler from regrouping them.
-template <int G>
-OQ_DEVICE void fused_step(const _Float16* Ac, const _Float16* Bc, _Float16* An, _Float16* Bn, int wm, int wn,
-                          int lane, float16v (&acc)[2][4], const Act& act, uint4 hdr, const Lines& l, int u) {
-    const int ra = 64 * wm + (lane & 31), rb = 128 * wn + (lane & 31), h = lane >> 5;
-    half8 a[2], b[4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const half8*>(Ac + tile_off(ra + 32 * i, h));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const half8*>(Bc + tile_off(rb + 32 * j, h));
-    store_act(act, An, u);
-    // scales of sub-blocks 2G, 2G+1 of weight row u
-    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu));
-    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
-    uint32_t sc0, mn0, sc1, mn1;
-    scale_min_k4(2 * G, hdr.y, hdr.z, hdr.w, sc0, mn0);
-    scale_min_k4(2 * G + 1, hdr.y, hdr.z, hdr.w, sc1, mn1);
-    float ds0, dm0, ds1, dm1;
-    {
-#pragma clang fp contract(off)
-        ds0 = d * (float)sc0;
-        dm0 = dmin * (float)mn0;
-        ds1 = d * (float)sc1;
-        dm1 = dmin * (float)mn1;
-    }
-    const uint32_t words[8] = {l.p0[G].x, l.p0[G].y, l.p0[G].z, l.p0[G].w,
-                               l.p1[G].x, l.p1[G].y, l.p1[G].z, l.p1[G].w};
-    uint32_t lo[8], hi[8], l4 = 0, h4 = 0;
+// Multiplies step s (group G) from A buffer Ac, with B operands converted in registers, and
+// meanwhile: reads the A operands of its next k-slice; converts the B operands of its next
+// k-slice; during the last slice, reads the first A operands of step s+1 (buffer An1, filled at
+// step s-1) and converts the first B operands of step s+1 (group G1 of `wn`, scales sn0 of
+// sub-block 2 G1); at the end stores the activation tile of step s+2 (loaded two steps
+// earlier) into buffer An2.
+//
+// The MFMAs alternate with small pieces of the conversion (a wave issues in order; MFMAs
+// grouped together would hold the conversion back), fixed by sched_barrier.
+template <bool FAST, int G, int G1>
+OQ_DEVICE void wave_step(const _Float16* Ac, const _Float16* An1, _Float16* An2, float16v (&acc)[4][2],
+                         half8 (&a)[4], uint32_t (&b)[2][4], const WData& wc, const WData& wn, Scale sn0_0,
+                         Scale sn0_1, const Act& act2, int lane, int tid) {
+    const int h = lane >> 5, r0 = lane & 31;
+    const Scale s0[2] = {scale_of<FAST>(wc.hdr[0], 2 * G), scale_of<FAST>(wc.hdr[1], 2 * G)};
+    const Scale s1[2] = {scale_of<FAST>(wc.hdr[0], 2 * G + 1), scale_of<FAST>(wc.hdr[1], 2 * G + 1)};
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-        half8 an[2], bn[4];
-        if (ks < 3) {
+        // operands of the next slice (of this step, or slice 0 of step s+1)
+        const _Float16* As = ks < 3 ? Ac : An1;
+        const int nks = (ks + 1) & 3;
+        half8 an[4];
+        uint32_t bn[2][4];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) an[i] = *reinterpret_cast<const half8*>(Ac + tile_off(ra + 32 * i, 2 * (ks + 1) + h));
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bn[j] = *reinterpret_cast<const half8*>(Bc + tile_off(rb + 32 * j, 2 * (ks + 1) + h));
-        }
+        for (int i = 0; i < 4; ++i) an[i] = *reinterpret_cast<const half8*>(As + tile_off(32 * i + r0, a_chunk(nks, h)));
+        uint32_t nw[2][2];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const int i = q >> 2, j = q & 3;
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+            const int i = q >> 1, j = q & 1;
+            half8 bj;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t v = b[j][e];
+                bj[2 * e] = __builtin_bit_cast(half2v, v)[0];
+                bj[2 * e + 1] = __builtin_bit_cast(half2v, v)[1];
+            }
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bj, acc[i][j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            // weight pair p = 8 ks + q of the 32 this thread converts: quant word p/4, pair p%4
-            // (0, 1: low nibbles of bytes 0-1 / 2-3; 2, 3: high nibbles)
-            const int p = 8 * ks + q, wd = p >> 2, pp = p & 3, wi = wd & 3;
+            // B operand of the next slice: MFMA q converts pair q % 4 of n-tile q / 4
+            const int jj = q >> 2, pp = q & 3;
+            const uint4 src = ks < 3 ? wc.q[jj][G] : wn.q[jj][G1];
+            const Scale sc = ks < 3 ? ((nks & 1) ? s1[jj] : s0[jj]) : (jj == 0 ? sn0_0 : sn0_1);
             if (pp == 0) {
-                l4 = opaque(words[wd] & 0x0F0F0F0Fu);
-                h4 = opaque((words[wd] >> 4) & 0x0F0F0F0Fu);
+                nw[jj][0] = nib_word<FAST>(src, nks, 0);
+                nw[jj][1] = nib_word<FAST>(src, nks, 1);
             }
-            if (pp == 0) lo[2 * wi] = pack_f16(__builtin_fmaf(ubyte<0>(l4), ds0, -dm0), __builtin_fmaf(ubyte<1>(l4), ds0, -dm0));
-            if (pp == 1) lo[2 * wi + 1] = pack_f16(__builtin_fmaf(ubyte<2>(l4), ds0, -dm0), __builtin_fmaf(ubyte<3>(l4), ds0, -dm0));
-            if (pp == 2) hi[2 * wi] = pack_f16(__builtin_fmaf(ubyte<0>(h4), ds1, -dm1), __builtin_fmaf(ubyte<1>(h4), ds1, -dm1));
-            if (pp == 3) {
-                hi[2 * wi + 1] = pack_f16(__builtin_fmaf(ubyte<2>(h4), ds1, -dm1), __builtin_fmaf(ubyte<3>(h4), ds1, -dm1));
-                if (wi == 3) {  // a whole 16-byte chunk (32 weights) of piece wd/4 is ready
-                    const int c = 2 * (wd >> 2);
-                    *reinterpret_cast<uint4*>(Bn + tile_off(u, c)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-                    *reinterpret_cast<uint4*>(Bn + tile_off(u, c + 1)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-                    *reinterpret_cast<uint4*>(Bn + tile_off(u, c + 4)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-                    *reinterpret_cast<uint4*>(Bn + tile_off(u, c + 5)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-                }
-            }
+            bn[jj][pp] = weight_pair<FAST>(nw[jj][pp >> 1], pp & 1, sc);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (ks < 3) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) a[i] = an[i];
+        for (int i = 0; i < 4; ++i) a[i] = an[i];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = bn[j];
-        }
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) b[j][e] = bn[j][e];
     }
+    store_act(act2, An2, tid);
 }
 
 // Workgroup barrier after this wave's LDS writes have completed.  Unlike __syncthreads() it does
@@ -331,24 +315,20 @@ OQ_DEVICE Unit unit_of(uint32_t id, uint32_t tiles_n, uint32_t tiles_m, uint32_t
     return r;
 }
 
-// grid: tiles_n * tiles_m * splits workgroups.  Output: y (one split) or partial[z][m][n].
-//
-// Each of the four waves (one per SIMD) multiplies its 64 x 128 sub-tile of step s from tile
-// buffer s%2 while it converts its share of step s+1 (weight row u = tid, activation chunks
-// u + 256 j) into buffer (s+1)%2: the MFMAs run asynchronously in the matrix core while the
-// same wave's conversion instructions issue on the vector ALU.  One barrier per step.
-// Activations are loaded two steps ahead, the weight lines and headers of super-block i+1 at
-// the first step of super-block i.
+// grid: tiles_n * tiles_m * splits workgroups of 4 waves.  Output: y (one split) or
+// partial[z][m][n].  Wave w computes rows m0..m0+127 x columns n0+64w..n0+64w+63 (4 x 2
+// accumulators of 32 x 32).  Activation tiles go through a ring of three LDS buffers: step s
+// reads buffer s%3, stores step s+2 into buffer (s+2)%3 (last read at step s-1), and reads the
+// first operands of step s+1 from buffer (s+1)%3 (stored at step s-1); one barrier per step.
+template <bool FAST>
 __global__ __launch_bounds__(kThreads) void gemm_q4k_f16_kernel(DeviceMatrix w, int m, const _Float16* a16,
                                                                uint32_t tiles_n, uint32_t tiles_m, uint32_t splits,
                                                                float* __restrict__ out) {
-    // separate objects per buffer, so that the compiler may interleave the conversion's stores
-    // to one buffer with the operand loads from the other
-    __shared__ __align__(16) _Float16 As0[kLdsA], Bs0[kLdsB];
-    __shared__ __align__(16) _Float16 As1[kLdsA], Bs1[kLdsB];
+    __shared__ __align__(16) _Float16 ring[3 * kLdsA];
+    _Float16* const A0 = ring;
+    _Float16* const A1 = ring + kLdsA;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1, u = tid;
     const uint32_t nsb = (uint32_t)(w.k / kQK);
     const Unit un = unit_of(blockIdx.x, tiles_n, tiles_m, splits);
     const uint32_t z = un.z;
@@ -361,51 +341,67 @@ __global__ __launch_bounds__(kThreads) void gemm_q4k_f16_kernel(DeviceMatrix w, 
     const uint32_t last = 4 * nsbu - 1;  // last step
     auto step_of = [last](uint32_t s) { return s <= last ? s : last; };
     auto sb_of = [&](uint32_t i) { return (uint64_t)t.sb0 + (i < nsbu ? i : nsbu - 1); };
+    const int h = lane >> 5, r0 = lane & 31;
 
-    float16v acc[2][4] = {};
-    Lines cur = load_lines(w, t, sb_of(0), u), nxt;
-    uint4 hdr = load_header(w, t, sb_of(0), u), hdr_next;
-    Act a0 = load_act(a16, w, m, t, 0, u);
-    Act a1 = load_act(a16, w, m, t, step_of(1), u);
-    store_act(a0, As0, u);
-    convert_weights<0>(hdr, cur, Bs0, u);
-    a0 = load_act(a16, w, m, t, step_of(2), u);
-    lds_barrier();  // step 0 converted
+    float16v acc[4][2] = {};
+    // prologue: activation tiles of steps 0 and 1, the operands of step 0's first slice
+    Act act = load_act(a16, w, m, t, 0, tid);
+    store_act(act, A0, tid);
+    act = load_act(a16, w, m, t, step_of(1), tid);
+    store_act(act, A1, tid);
+    // activation tiles in flight: actA for steps 2, 4, ..., actB for steps 3, 5, ...
+    Act actA = load_act(a16, w, m, t, step_of(2), tid);
+    Act actB = load_act(a16, w, m, t, step_of(3), tid);
+    WData cur = load_wdata(w, t, sb_of(0), wave, lane), nxt = cur;
+    lds_barrier();
+    half8 a[4];
+    uint32_t b[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const half8*>(A0 + tile_off(32 * i + r0, a_chunk(0, h)));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const Scale sc = scale_of<FAST>(cur.hdr[j], 0);
+        const uint32_t n0w = nib_word<FAST>(cur.q[j][0], 0, 0), n1w = nib_word<FAST>(cur.q[j][0], 0, 1);
+        b[j][0] = weight_pair<FAST>(n0w, 0, sc);
+        b[j][1] = weight_pair<FAST>(n0w, 1, sc);
+        b[j][2] = weight_pair<FAST>(n1w, 0, sc);
+        b[j][3] = weight_pair<FAST>(n1w, 1, sc);
+    }
+    // Each step: wave_step, then the activation load of step s+4, then the barrier.
+    auto step = [&](auto G_, auto G1_, const _Float16* Ac, const _Float16* An1, _Float16* An2, uint32_t s,
+                    const WData& wc, const WData& wn, Act& act2) {
+        constexpr int G = decltype(G_)::value, G1 = decltype(G1_)::value;
+        const Scale sn0_0 = scale_of<FAST>(wn.hdr[0], 2 * G1), sn0_1 = scale_of<FAST>(wn.hdr[1], 2 * G1);
+        wave_step<FAST, G, G1>(Ac, An1, An2, acc, a, b, wc, wn, sn0_0, sn0_1, act2, lane, tid);
+        act2 = load_act(a16, w, m, t, step_of(s + 4), tid);
+        lds_barrier();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    auto buf = [&](uint32_t k) { return ring + kLdsA * (k % 3); };  // tile buffer of step k
     for (uint32_t i = 0; i < nsbu; ++i) {
         const uint32_t s = 4 * i;
-        // step s: multiply s, convert s+1
-        nxt = load_lines(w, t, sb_of(i + 1), u);
-        hdr_next = load_header(w, t, sb_of(i + 1), u);
-        fused_step<1>(As0, Bs0, As1, Bs1, wm, wn, lane, acc, a1, hdr, cur, u);
-        a1 = load_act(a16, w, m, t, step_of(s + 3), u);
-        lds_barrier();
-        // step s+1
-        fused_step<2>(As1, Bs1, As0, Bs0, wm, wn, lane, acc, a0, hdr, cur, u);
-        a0 = load_act(a16, w, m, t, step_of(s + 4), u);
-        lds_barrier();
-        // step s+2
-        fused_step<3>(As0, Bs0, As1, Bs1, wm, wn, lane, acc, a1, hdr, cur, u);
-        a1 = load_act(a16, w, m, t, step_of(s + 5), u);
-        lds_barrier();
-        // step s+3: convert the first group of super-block i+1
+        nxt = load_wdata(w, t, sb_of(i + 1), wave, lane);
+        step(I0{}, I1{}, buf(s), buf(s + 1), buf(s + 2), s, cur, cur, actA);
+        step(I1{}, I2{}, buf(s + 1), buf(s + 2), buf(s + 3), s + 1, cur, cur, actB);
+        step(I2{}, I3{}, buf(s + 2), buf(s + 3), buf(s + 4), s + 2, cur, cur, actA);
+        step(I3{}, I0{}, buf(s + 3), buf(s + 4), buf(s + 5), s + 3, cur, nxt, actB);
         cur = nxt;
-        hdr = hdr_next;
-        fused_step<0>(As1, Bs1, As0, Bs0, wm, wn, lane, acc, a0, hdr, cur, u);
-        a0 = load_act(a16, w, m, t, step_of(s + 6), u);
-        lds_barrier();
     }
     // result register r of lane l: row 8*(r/4) + 4*(l/32) + r%4, column l%32
     float* o = out + (uint64_t)z * (uint64_t)m * w.n;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint64_t col = t.n0 + 128 * wn + 32 * j + (lane & 31);
+    for (int j = 0; j < 2; ++j) {
+        const uint64_t col = t.n0 + 64 * wave + 32 * j + (lane & 31);
         if (col >= w.n) continue;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 4; ++i) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint64_t row = t.m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-                if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][r];
+            for (int rr = 0; rr < 16; ++rr) {
+                const uint64_t row = t.m0 + 32 * i + 8 * (rr / 4) + 4 * (lane >> 5) + (rr % 4);
+                if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][rr];
             }
         }
     }
@@ -490,8 +486,13 @@ hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const float* x, co
         hipLaunchKernelGGL(q8k_to_f16_kernel, dim3(qgrid), dim3(256), 0, s, q8k, nblocks, a16);
     }
     const unsigned wgs = p.tiles_n * p.tiles_m * p.splits;
-    hipLaunchKernelGGL(gemm_q4k_f16_kernel, dim3(wgs), dim3(kThreads), 0, s, w, m, a16, p.tiles_n, p.tiles_m,
-                       p.splits, p.splits > 1 ? part : y);
+    if (w.k >= kFastMinK && env_int("OQ_GEMM_EXACT_DEQUANT", 0) == 0) {
+        hipLaunchKernelGGL(gemm_q4k_f16_kernel<true>, dim3(wgs), dim3(kThreads), 0, s, w, m, a16, p.tiles_n,
+                           p.tiles_m, p.splits, p.splits > 1 ? part : y);
+    } else {
+        hipLaunchKernelGGL(gemm_q4k_f16_kernel<false>, dim3(wgs), dim3(kThreads), 0, s, w, m, a16, p.tiles_n,
+                           p.tiles_m, p.splits, p.splits > 1 ? part : y);
+    }
     if (p.splits > 1) {
         const uint64_t count = (uint64_t)m * w.n;
         if (count % 4 == 0) {
