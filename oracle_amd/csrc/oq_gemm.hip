@@ -47,12 +47,6 @@ constexpr uint64_t kMinK = 4096;
 // at K = 12288 against the 1e-4 bar.
 constexpr uint64_t kFastMinK = 8192;
 constexpr int kMaxSplits = 8;
-constexpr int kLdsA = kBM * kBK;    // f16 elements per A tile buffer
-
-// F16 tiles: row r holds 64 k as eight 16-byte chunks; logical chunk c sits at physical chunk
-// c ^ ((r / 2) % 8), which keeps the MFMA operand reads and the tile writes free of LDS bank
-// conflicts without padding.
-OQ_DEVICE int tile_off(int r, int c) { return r * kBK + 8 * (c ^ ((r >> 1) & 7)); }
 
 // ---------------------------------------------------------------- activation image
 
@@ -90,211 +84,147 @@ __global__ __launch_bounds__(256) void q8k_to_f16_kernel(const uint8_t* __restri
     *reinterpret_cast<uint2*>(out + blk * kQK + 4 * lane) = make_uint2(pack_f16(f[0], f[1]), pack_f16(f[2], f[3]));
 }
 
-// ---------------------------------------------------------------- tiles
-
-struct Tile {
-    uint64_t m0, n0;
-    uint32_t sb0;  // first super-block of this split
-};
-
-// k order inside one 64-element group (the same for both operands, so the product is
-// unchanged): MFMA k-slice ks (16 k), lane half h, operand element i covers
-//   k = 32 (ks & 1) + 16 h + 8 (ks >> 1) + i.
-// A: 8 consecutive k = chunk 4 (ks & 1) + 2 h + (ks >> 1) of an F16 tile row.
-// B: bytes 16 h + 8 (ks >> 1) + i of the weight row's 32-byte group, low nibbles for even ks,
-//    high nibbles for odd ks: lane half h reads exactly 16-byte chunk e = h of the group (see
-//    oq_layout.h), and the slices alternate between the group's two sub-blocks.
+// ---------------------------------------------------------------- tiles and addressing
+//
+// One workgroup: a 128 (m) x 256 (n) output tile over one K-split, in steps of 64 k (a quarter
+// super-block, "group" G = 0..3: sub-blocks 2G and 2G+1).  Wave w owns all 128 rows and columns
+// n0 + 64 w .. n0 + 64 w + 63 (4 x 2 accumulators of 32 x 32).
+//
+// Activation tiles (F16, 128 rows x 64 k = 16 KB) pass through a ring of four LDS buffers; the
+// tile of step s sits in buffer s % 4, so inside the four-step loop body every LDS address is a
+// per-lane constant plus an immediate.  Row r holds eight 16-byte chunks; logical chunk c sits at
+// physical chunk c ^ ((r / 2) % 8), which keeps the operand reads and the tile writes free of
+// bank conflicts without padding.
+//
+// k order inside one group (the same for both operands, so the product is unchanged): MFMA
+// k-slice ks (16 k), lane half h, operand element i covers k = 32 (ks & 1) + 16 h + 8 (ks >> 1) + i.
+//   A: 8 consecutive k = logical chunk 4 (ks & 1) + 2 h + (ks >> 1) of a tile row;
+//   B: bytes 16 h + 8 (ks >> 1) + i of the weight row's 32-byte group chunk pair, low nibbles for
+//      even ks, high nibbles for odd ks: lane half h reads only chunk e = h of the group (see
+//      oq_layout.h), and slice ks lies inside sub-block 2G + (ks & 1).
 OQ_DEVICE int a_chunk(int ks, int h) { return 4 * (ks & 1) + 2 * h + (ks >> 1); }
 
-// ---------------------------------------------------------------- activations
+constexpr uint32_t kTileBytes = kBM * kBK * 2;  // 16 KB
+
+// ---------------------------------------------------------------- per-sub-block scales
 //
-// All 256 threads copy the step's 128 x 64 F16 tile: 16-byte chunks c = tid + 256 j (j = 0..3),
-// row c / 8, chunk c % 8.
-
-struct Act {
-    uint4 c[4];
-};
-
-OQ_DEVICE Act load_act(const _Float16* a16, const DeviceMatrix& w, int m, const Tile& t, uint32_t step, int tid) {
-    Act a;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t c = tid + 256 * j;
-        uint64_t row = t.m0 + (c >> 3);
-        row = row < (uint64_t)m ? row : (uint64_t)m - 1;
-        a.c[j] = *reinterpret_cast<const uint4*>(a16 + row * w.k + (uint64_t)t.sb0 * kQK + (uint64_t)step * kBK +
-                                                 8 * (c & 7));
-    }
-    return a;
-}
-
-OQ_DEVICE void store_act(const Act& a, _Float16* As, int tid) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int c = tid + 256 * j;
-        *reinterpret_cast<uint4*>(As + tile_off(c >> 3, c & 7)) = a.c[j];
-    }
-}
-
-// ---------------------------------------------------------------- weights
-//
-// Wave w owns weight rows n0 + 64 w + 32 j + (lane % 32), j = 0, 1 (two 32-column MFMA tiles);
-// lane half h = lane / 32 reads chunk e = h of every group.  Per super-block a lane loads the
-// four chunks (one per group, adjacent in the row layout) of both its rows and the two rows'
-// headers; the weights never pass through LDS.
-
-struct WData {
-    uint4 q[2][4];  // [j][group]
-    uint4 hdr[2];   // [j]
-};
-
-OQ_DEVICE WData load_wdata(const DeviceMatrix& w, const Tile& t, uint64_t sb, int wave, int lane) {
-    const uint64_t nsb = w.k / kQK;
-    WData d;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        uint64_t n = t.n0 + 64 * wave + 32 * j + (lane & 31);
-        n = n < w.n ? n : w.n - 1;
-        const uint8_t* row = w.base + n * w.pitch;
-        const uint4* q = reinterpret_cast<const uint4*>(row + 16 * perm_chunk(nsb, sb, 0, (uint32_t)(lane >> 5)));
-#pragma unroll
-        for (int g = 0; g < 4; ++g) d.q[j][g] = q[g];
-        d.hdr[j] = *reinterpret_cast<const uint4*>(row + 128 * nsb + 16 * sb);
-    }
-    return d;
-}
-
-// d*sc and dmin*m of sub-block `sub` of a header, in the reference's F32 arithmetic, and (for
-// the packed path) as f16 pairs {ds, ds}, {-dm, -dm}
-struct Scale {
-    float ds, dm;
-    uint32_t ds2, ndm2;
-};
-
-template <bool FAST>
-OQ_DEVICE Scale scale_of(uint4 hdr, uint32_t sub) {
-    // hardware f16 -> f32 (exact for every finite value; NaN payloads do not matter here)
-    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu));
-    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
-    uint32_t sc, mn;
-    scale_min_k4(sub, hdr.y, hdr.z, hdr.w, sc, mn);
-    Scale s;
-    {
-#pragma clang fp contract(off)
-        s.ds = d * (float)sc;
-        s.dm = dmin * (float)mn;
-    }
-    if (FAST) {
-        s.ds2 = pack_f16(s.ds, s.ds);
-        s.ndm2 = pack_f16(-s.dm, -s.dm);
+// Scale state of one (weight row, sub-block):
+//   FAST : one dword = f16 pair {d*sc, -(dmin*m)}, each the exact product rounded once to f16;
+//   exact: F32 {d*sc, dmin*m} as the reference computes them (two F32 products, no contraction).
+// Pairs for sub-blocks 2G, 2G+1 of a header (f16 d, f16 dmin, 12 packed 6-bit scale/min bytes):
+// the four 6-bit values of a half super-block are unpacked bytewise in one go, the same unpack
+// as scale_min_k4 (src/model/storage_decode.cpp:44-61).
+template <int G>
+OQ_DEVICE void unpack_scale_bytes(uint4 hdr, uint32_t& scb, uint32_t& mnb) {
+    if (G < 2) {
+        scb = hdr.y & 0x3F3F3F3Fu;
+        mnb = hdr.z & 0x3F3F3F3Fu;
     } else {
-        s.ds2 = s.ndm2 = 0;
+        scb = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+        mnb = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
     }
-    return s;
 }
 
-// Identity byte permutation (one v_perm_b32): keeps the optimizer from merging a byte mask into
-// the extractions below, so that they map onto v_cvt_f32_ubyte<i>, while remaining an ordinary
-// vector instruction.
-OQ_DEVICE uint32_t opaque(uint32_t v) { return __builtin_amdgcn_perm(0u, v, 0x03020100u); }
-
-template <int I>
-OQ_DEVICE float ubyte(uint32_t u) {
-    return (float)((u >> (8 * I)) & 0xFFu);
-}
-
-// Two weights of a B operand from the nibbles of bytes 2p, 2p+1 of `nib` (already masked).
-//   exact: f16(ds*q - dm) from F32 (one rounding);
-//   FAST:  the nibbles become the f16 values 1024 + q (bit pattern 0x6400 | q, placed by one
-//          v_perm_b32), minus 1024 (exact), then one v_pk_fma_f16 with ds and -dm rounded to f16:
-//          three instructions per pair instead of five, at the price of the f16 rounding of
-//          the sub-block's scale and min.
 template <bool FAST>
-OQ_DEVICE uint32_t weight_pair(uint32_t nib, int p, const Scale& s) {
-    if (FAST) {
-        const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-        half2v x = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, nib, p == 0 ? 0x04010400u : 0x04030402u));
-        x = x - k1024;
-        x = __builtin_elementwise_fma(x, __builtin_bit_cast(half2v, s.ds2), __builtin_bit_cast(half2v, s.ndm2));
-        return __builtin_bit_cast(uint32_t, x);
-    }
-    const float a = p == 0 ? ubyte<0>(nib) : ubyte<2>(nib);
-    const float b = p == 0 ? ubyte<1>(nib) : ubyte<3>(nib);
-    return pack_f16(__builtin_fmaf(a, s.ds, -s.dm), __builtin_fmaf(b, s.ds, -s.dm));
-}
+struct ScaleT;
+template <>
+struct ScaleT<true> {
+    uint32_t v;
+};
+template <>
+struct ScaleT<false> {
+    float ds, dm;
+};
 
-// nibble word (masked, one per quant dword) of slice ks from a lane's 16-byte group chunk
-template <bool FAST>
-OQ_DEVICE uint32_t nib_word(uint4 q, int ks, int half) {
-    const uint32_t d = (ks >> 1) == 0 ? (half == 0 ? q.x : q.y) : (half == 0 ? q.z : q.w);
-    const uint32_t v = (ks & 1) ? (d >> 4) & 0x0F0F0F0Fu : d & 0x0F0F0F0Fu;
-    return FAST ? v : opaque(v);
-}
-
-// ---------------------------------------------------------------- one step of one wave
-//
-// Multiplies step s (group G) from A buffer Ac, with B operands converted in registers, and
-// meanwhile: reads the A operands of its next k-slice; converts the B operands of its next
-// k-slice; during the last slice, reads the first A operands of step s+1 (buffer An1, filled at
-// step s-1) and converts the first B operands of step s+1 (group G1 of `wn`, scales sn0 of
-// sub-block 2 G1); at the end stores the activation tile of step s+2 (loaded two steps
-// earlier) into buffer An2.
-//
-// The MFMAs alternate with small pieces of the conversion (a wave issues in order; MFMAs
-// grouped together would hold the conversion back), fixed by sched_barrier.
-template <bool FAST, int G, int G1>
-OQ_DEVICE void wave_step(const _Float16* Ac, const _Float16* An1, _Float16* An2, float16v (&acc)[4][2],
-                         half8 (&a)[4], uint32_t (&b)[2][4], const WData& wc, const WData& wn, Scale sn0_0,
-                         Scale sn0_1, const Act& act2, int lane, int tid) {
-    const int h = lane >> 5, r0 = lane & 31;
-    const Scale s0[2] = {scale_of<FAST>(wc.hdr[0], 2 * G), scale_of<FAST>(wc.hdr[1], 2 * G)};
-    const Scale s1[2] = {scale_of<FAST>(wc.hdr[0], 2 * G + 1), scale_of<FAST>(wc.hdr[1], 2 * G + 1)};
-    __builtin_amdgcn_sched_barrier(0);
+template <bool FAST, int G>
+OQ_DEVICE void scale_pairs(uint4 hdr, ScaleT<FAST> (&out)[2]) {
+    uint32_t scb, mnb;
+    unpack_scale_bytes<G>(hdr, scb, mnb);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        // operands of the next slice (of this step, or slice 0 of step s+1)
-        const _Float16* As = ks < 3 ? Ac : An1;
-        const int nks = (ks + 1) & 3;
-        half8 an[4];
-        uint32_t bn[2][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) an[i] = *reinterpret_cast<const half8*>(As + tile_off(32 * i + r0, a_chunk(nks, h)));
-        uint32_t nw[2][2];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int i = q >> 1, j = q & 1;
-            half8 bj;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t v = b[j][e];
-                bj[2 * e] = __builtin_bit_cast(half2v, v)[0];
-                bj[2 * e + 1] = __builtin_bit_cast(half2v, v)[1];
+    for (int par = 0; par < 2; ++par) {
+        const uint32_t b = (2 * G + par) & 3;
+        if constexpr (FAST) {
+            // {sc, mn} as the f16 values 1024 + sc, 1024 + mn (exact), minus 1024, times {d, -dmin}
+            const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+            const uint32_t sel = b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24);
+            const uint32_t v = __builtin_amdgcn_perm(mnb, scb, sel) | 0x64006400u;
+            const half2v dd = __builtin_bit_cast(half2v, hdr.x ^ 0x80000000u);
+            half2v x = __builtin_bit_cast(half2v, v) - k1024;
+            out[par].v = __builtin_bit_cast(uint32_t, x * dd);
+        } else {
+            // hardware f16 -> f32 (exact for every finite value; NaN payloads do not matter here)
+            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu));
+            const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
+            const float sc = (float)((scb >> (8 * b)) & 0xFFu);
+            const float mn = (float)((mnb >> (8 * b)) & 0xFFu);
+            {
+#pragma clang fp contract(off)
+                out[par].ds = d * sc;
+                out[par].dm = dmin * mn;
             }
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bj, acc[i][j], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            // B operand of the next slice: MFMA q converts pair q % 4 of n-tile q / 4
-            const int jj = q >> 2, pp = q & 3;
-            const uint4 src = ks < 3 ? wc.q[jj][G] : wn.q[jj][G1];
-            const Scale sc = ks < 3 ? ((nks & 1) ? s1[jj] : s0[jj]) : (jj == 0 ? sn0_0 : sn0_1);
-            if (pp == 0) {
-                nw[jj][0] = nib_word<FAST>(src, nks, 0);
-                nw[jj][1] = nib_word<FAST>(src, nks, 1);
-            }
-            bn[jj][pp] = weight_pair<FAST>(nw[jj][pp >> 1], pp & 1, sc);
-            __builtin_amdgcn_sched_barrier(0);
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = an[i];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) b[j][e] = bn[j][e];
     }
-    store_act(act2, An2, tid);
 }
 
-// Workgroup barrier after this wave's LDS writes have completed.  Unlike __syncthreads() it does
-// not wait for outstanding global loads (the prefetches in flight across the barrier).
+// ---------------------------------------------------------------- weight conversion
+//
+// Nibble word of slice ks (4 weights, one per byte, values 0..15) from a lane's 16-byte group
+// chunk: dwords x, y for ks < 2, z, w for ks >= 2; low nibbles for even ks, high for odd.
+template <int KS>
+OQ_DEVICE uint32_t nib_word(uint4 q, int half) {
+    const uint32_t d = (KS >> 1) == 0 ? (half == 0 ? q.x : q.y) : (half == 0 ? q.z : q.w);
+    return (KS & 1) ? (d >> 4) & 0x0F0F0F0Fu : d & 0x0F0F0F0Fu;
+}
+
+// Two weights of a B operand from bytes 2p, 2p+1 of a nibble word.  A byte q in 0..15 read as
+// an fp8 e4m3 pattern is q * 2^-9 (subnormal or the first binade), so the scaled fp8 conversion
+// with scale 2^9 yields q exactly, two per instruction.
+//   FAST : one v_pk_fma_f16 with {d*sc, -(dmin*m)}: f16(d*sc*q - dmin*m) from the f16-rounded
+//          scale and min, one rounding;
+//   exact: F32 fma with the reference's F32 scale and min, then one rounding to f16.
+template <bool FAST, int P>
+OQ_DEVICE uint32_t weight_pair(uint32_t nib, const ScaleT<FAST>& s) {
+    if constexpr (FAST) {
+        const half2v x = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(nib, 512.0f, P != 0);
+        const half2v sv = __builtin_bit_cast(half2v, s.v);
+        const half2v r = __builtin_elementwise_fma(x, __builtin_shufflevector(sv, sv, 0, 0),
+                                                   __builtin_shufflevector(sv, sv, 1, 1));
+        return __builtin_bit_cast(uint32_t, r);
+    } else {
+        const float2v f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(nib, 512.0f, P != 0);
+        return pack_f16(__builtin_fmaf(f.x, s.ds, -s.dm), __builtin_fmaf(f.y, s.ds, -s.dm));
+    }
+}
+
+// ---------------------------------------------------------------- wave state
+//
+// Per lane, fixed for the whole workgroup:
+//   act_off[j]  byte offset of activation chunk c = tid + 256 j (row c / 8 of the m-tile, chunk
+//               c % 8) within a 64-k column block of the F16 image (rows clamped to m - 1);
+//   st_off      LDS byte offset of the tile stores (buffer 0, j = 0; +4096 per j);
+//   rd_off[ks]  LDS byte offset of the A operand read of slice ks (buffer 0, m-subtile 0);
+//   row_off[j]  byte offset of weight row n0 + 64 w + 32 j + lane % 32 (clamped to n - 1).
+// Global addresses are a uniform (scalar) base plus these 32-bit lane offsets.
+struct WaveState {
+    uint32_t act_off[4];
+    uint32_t st_off;
+    uint32_t rd_off[4];
+    uint32_t row_off[2];
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+OQ_DEVICE half8 lds_read(const uint8_t* lds, uint32_t off) {
+    return *reinterpret_cast<const half8*>(lds + off);
+}
+
+OQ_DEVICE half8 as_b_operand(const uint32_t (&b)[4]) {
+    const u32x4 v = {b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(half8, v);
+}
+
+// Workgroup barrier after this wave's LDS operations have completed.  Unlike __syncthreads() it
+// does not wait for outstanding global loads (the prefetches in flight across the barrier).
 OQ_DEVICE void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Work units (n-tile, m-tile, K-split) are numbered so that the workgroups one XCD receives
@@ -315,92 +245,239 @@ OQ_DEVICE Unit unit_of(uint32_t id, uint32_t tiles_n, uint32_t tiles_m, uint32_t
     return r;
 }
 
+// Uniform addressing of one K-split: super-block i (0-based within the split, clamped to the
+// last one) and activation step s (clamped to the last step).
+struct Split {
+    const uint8_t* wbase;   // weight matrix base
+    const uint8_t* a16;     // F16 image, column of the split's first super-block
+    uint32_t sb0, nsbu, nsb, last_step, hdr_base;
+};
+
+OQ_DEVICE uint32_t split_sb(const Split& sp, uint32_t i) { return sp.sb0 + (i < sp.nsbu ? i : sp.nsbu - 1); }
+
+// quant chunk (group g, lane half h) of super-block sb: uniform part, and the lane part that
+// depends on the pass length of that super-block
+OQ_DEVICE const uint8_t* quant_base(const Split& sp, uint32_t sb, int g) {
+    return sp.wbase + 16u * (128u * (sb / 16u) + 4u * (sb % 16u) + (uint32_t)g);
+}
+
+OQ_DEVICE uint32_t quant_lane(const Split& sp, uint32_t sb, uint32_t hmask) {
+    const uint32_t pass = sb / 16u;
+    const uint32_t mp = sp.nsb - 16u * pass < 16u ? sp.nsb - 16u * pass : 16u;
+    return hmask & (64u * mp);
+}
+
+OQ_DEVICE uint4 load_u4(const uint8_t* base, uint32_t off) {
+    return *reinterpret_cast<const uint4*>(base + off);
+}
+
+// ---------------------------------------------------------------- one step of one wave
+//
+// Multiplies group G of the current super-block (activation tile in buffer G) and meanwhile:
+//   - reads the A operands of the next k-slice (the last slice reads slice 0 of the next step
+//     from buffer (G + 1) % 4) and converts the B operands of the next k-slice (the last slice
+//     converts slice 0 of the next step from wq[(G + 1) % 4], holding the next super-block's
+//     group 0 when G = 3);
+//   - stores the activation tile of step s + 3 (loaded two steps earlier, register set
+//     (G + 1) % 2) into buffer (G + 3) % 4, whose last reader was step s - 1, and loads the
+//     tile of step s + 5 into the same register set;
+//   - computes the scale state of the next step (from hdr, or from hdrn when G = 3);
+//   - when G = 0 loads the next super-block's headers; after its last use of wq[G] loads the
+//     next super-block's group G into it.
+// MFMAs execute asynchronously; every MFMA is followed by a small piece of the conversion and
+// pinned there with sched_barrier, since a wave issues in order and MFMAs grouped together
+// would hold the conversion back.
+template <bool FAST, int G>
+OQ_DEVICE void wave_step(const uint8_t* lds, uint8_t* lds_w, const WaveState& ws, const Split& sp,
+                         uint32_t i_sb, uint32_t s, uint32_t hmask, float16v (&acc)[4][2], half8 (&a)[4],
+                         uint32_t (&b)[2][4], uint4 (&wq)[4][2], uint4 (&hdr)[2], uint4 (&hdrn)[2],
+                         ScaleT<FAST> (&sc)[2][2][2], uint4 (&act)[2][4]) {
+    constexpr int G1 = (G + 1) & 3;
+    constexpr int P = G & 1;       // scale set of this step
+    constexpr int AS = (G + 1) & 1;  // activation register set stored and reloaded by this step
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const int nks = (ks + 1) & 3;
+        const uint32_t nbuf = ks < 3 ? (uint32_t)G : (uint32_t)G1;
+        half8 an[4];
+        uint32_t bn[2][4];
+        uint32_t nw[2][2];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int i = q >> 1, j = q & 1;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], as_b_operand(b[j]), acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (q == 0) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) an[ii] = lds_read(lds, nbuf * kTileBytes + 4096u * ii + ws.rd_off[nks]);
+            }
+            // B operand of the next slice: MFMA q converts pair q % 4 of n-tile q / 4
+            const int jj = q >> 2, pp = q & 3;
+            const uint4 src = ks < 3 ? wq[G][jj] : wq[G1][jj];
+            const ScaleT<FAST>& scl = ks < 3 ? sc[P][jj][nks & 1] : sc[P ^ 1][jj][0];
+            if (pp == 0) {
+                if (nks == 0) {
+                    nw[jj][0] = nib_word<0>(src, 0);
+                    nw[jj][1] = nib_word<0>(src, 1);
+                } else if (nks == 1) {
+                    nw[jj][0] = nib_word<1>(src, 0);
+                    nw[jj][1] = nib_word<1>(src, 1);
+                } else if (nks == 2) {
+                    nw[jj][0] = nib_word<2>(src, 0);
+                    nw[jj][1] = nib_word<2>(src, 1);
+                } else {
+                    nw[jj][0] = nib_word<3>(src, 0);
+                    nw[jj][1] = nib_word<3>(src, 1);
+                }
+            }
+            bn[jj][pp] = (pp & 1) ? weight_pair<FAST, 1>(nw[jj][pp >> 1], scl) : weight_pair<FAST, 0>(nw[jj][pp >> 1], scl);
+            // side work
+            if (ks == 0 && q >= 1 && q <= 4) {
+                const int jt = q - 1;
+                *reinterpret_cast<uint4*>(lds_w + ((G + 3) & 3) * kTileBytes + 4096u * jt + ws.st_off) = act[AS][jt];
+            }
+            if (ks == 1 && q < 4) {
+                const uint32_t st = s + 5 < sp.last_step ? s + 5 : sp.last_step;
+                act[AS][q] = load_u4(sp.a16 + 128u * st, ws.act_off[q]);
+            }
+            if (ks == 1 && q == 4) {
+                if (G < 3) scale_pairs<FAST, G1>(hdr[0], sc[P ^ 1][0]);
+                else scale_pairs<FAST, 0>(hdrn[0], sc[P ^ 1][0]);
+            }
+            if (ks == 1 && q == 6) {
+                if (G < 3) scale_pairs<FAST, G1>(hdr[1], sc[P ^ 1][1]);
+                else scale_pairs<FAST, 0>(hdrn[1], sc[P ^ 1][1]);
+            }
+            if (G == 0 && ks == 2 && q < 2) {
+                const uint32_t sbn = split_sb(sp, i_sb + 1);
+                hdrn[q] = load_u4(sp.wbase + sp.hdr_base + 16u * sbn, ws.row_off[q]);
+            }
+            if (ks == 3 && q < 2) {
+                const uint32_t sbn = split_sb(sp, i_sb + 1);
+                wq[G][q] = load_u4(quant_base(sp, sbn, G), ws.row_off[q] + quant_lane(sp, sbn, hmask));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) a[ii] = an[ii];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) b[j][e] = bn[j][e];
+    }
+}
+
 // grid: tiles_n * tiles_m * splits workgroups of 4 waves.  Output: y (one split) or
-// partial[z][m][n].  Wave w computes rows m0..m0+127 x columns n0+64w..n0+64w+63 (4 x 2
-// accumulators of 32 x 32).  Activation tiles go through a ring of three LDS buffers: step s
-// reads buffer s%3, stores step s+2 into buffer (s+2)%3 (last read at step s-1), and reads the
-// first operands of step s+1 from buffer (s+1)%3 (stored at step s-1); one barrier per step.
+// partial[z][m][n].
 template <bool FAST>
 __global__ __launch_bounds__(kThreads) void gemm_q4k_f16_kernel(DeviceMatrix w, int m, const _Float16* a16,
                                                                uint32_t tiles_n, uint32_t tiles_m, uint32_t splits,
                                                                float* __restrict__ out) {
-    __shared__ __align__(16) _Float16 ring[3 * kLdsA];
-    _Float16* const A0 = ring;
-    _Float16* const A1 = ring + kLdsA;
+    __shared__ __align__(16) uint8_t lds[4 * kTileBytes];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, r0 = lane & 31;
+    const uint32_t hmask = h ? 0xFFFFFFFFu : 0u;
     const uint32_t nsb = (uint32_t)(w.k / kQK);
     const Unit un = unit_of(blockIdx.x, tiles_n, tiles_m, splits);
     const uint32_t z = un.z;
-    Tile t;
-    t.n0 = (uint64_t)un.nt * kBN;
-    t.m0 = (uint64_t)un.mt * kBM;
-    t.sb0 = (uint32_t)((uint64_t)z * nsb / splits);
+    const uint64_t n0 = (uint64_t)un.nt * kBN, m0 = (uint64_t)un.mt * kBM;
+    Split sp;
+    sp.sb0 = (uint32_t)((uint64_t)z * nsb / splits);
     const uint32_t sb1 = (uint32_t)((uint64_t)(z + 1) * nsb / splits);
-    const uint32_t nsbu = sb1 - t.sb0;   // >= 1: splits <= nsb
-    const uint32_t last = 4 * nsbu - 1;  // last step
-    auto step_of = [last](uint32_t s) { return s <= last ? s : last; };
-    auto sb_of = [&](uint32_t i) { return (uint64_t)t.sb0 + (i < nsbu ? i : nsbu - 1); };
-    const int h = lane >> 5, r0 = lane & 31;
+    sp.nsbu = sb1 - sp.sb0;  // >= 1: splits <= nsb
+    sp.nsb = nsb;
+    sp.last_step = 4 * sp.nsbu - 1;
+    sp.hdr_base = 128u * nsb;
+    sp.wbase = w.base;
+    sp.a16 = reinterpret_cast<const uint8_t*>(a16) + 2ull * kQK * sp.sb0;
+
+    WaveState ws;
+    const uint32_t krow = (uint32_t)(w.k * 2);  // bytes per F16 image row
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint64_t row = m0 + (uint32_t)(tid >> 3) + 32u * j;
+        row = row < (uint64_t)m ? row : (uint64_t)m - 1;
+        ws.act_off[j] = (uint32_t)row * krow + 16u * (uint32_t)(tid & 7);
+    }
+    ws.st_off = 128u * (uint32_t)(tid >> 3) + 16u * (uint32_t)((tid & 7) ^ ((tid >> 4) & 7));
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) ws.rd_off[ks] = 128u * (uint32_t)r0 + 16u * (uint32_t)(a_chunk(ks, h) ^ ((r0 >> 1) & 7));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        uint64_t n = n0 + 64 * wave + 32 * j + r0;
+        n = n < w.n ? n : w.n - 1;
+        ws.row_off[j] = (uint32_t)(n * w.pitch);
+    }
 
     float16v acc[4][2] = {};
-    // prologue: activation tiles of steps 0 and 1, the operands of step 0's first slice
-    Act act = load_act(a16, w, m, t, 0, tid);
-    store_act(act, A0, tid);
-    act = load_act(a16, w, m, t, step_of(1), tid);
-    store_act(act, A1, tid);
-    // activation tiles in flight: actA for steps 2, 4, ..., actB for steps 3, 5, ...
-    Act actA = load_act(a16, w, m, t, step_of(2), tid);
-    Act actB = load_act(a16, w, m, t, step_of(3), tid);
-    WData cur = load_wdata(w, t, sb_of(0), wave, lane), nxt = cur;
+    // prologue: activation tiles 0..2 into buffers 0..2, tiles 3 and 4 in flight (sets 1, 0)
+    uint4 act[2][4];
+    for (uint32_t t = 0; t < 3; ++t) {
+        const uint32_t st = t < sp.last_step ? t : sp.last_step;
+        uint4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = load_u4(sp.a16 + 128u * st, ws.act_off[j]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(lds + t * kTileBytes + 4096u * j + ws.st_off) = v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        act[1][j] = load_u4(sp.a16 + 128u * (3 < sp.last_step ? 3 : sp.last_step), ws.act_off[j]);
+        act[0][j] = load_u4(sp.a16 + 128u * (4 < sp.last_step ? 4 : sp.last_step), ws.act_off[j]);
+    }
+    // weights of the first super-block: headers and the four groups
+    uint4 hdr[2], hdrn[2], wq[4][2];
+    {
+        const uint32_t sb = sp.sb0;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            hdr[j] = load_u4(sp.wbase + sp.hdr_base + 16u * sb, ws.row_off[j]);
+            hdrn[j] = hdr[j];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) wq[g][j] = load_u4(quant_base(sp, sb, g), ws.row_off[j] + quant_lane(sp, sb, hmask));
+        }
+    }
+    ScaleT<FAST> sc[2][2][2];
+    scale_pairs<FAST, 0>(hdr[0], sc[0][0]);
+    scale_pairs<FAST, 0>(hdr[1], sc[0][1]);
     lds_barrier();
     half8 a[4];
     uint32_t b[2][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const half8*>(A0 + tile_off(32 * i + r0, a_chunk(0, h)));
+    for (int i = 0; i < 4; ++i) a[i] = lds_read(lds, 4096u * i + ws.rd_off[0]);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const Scale sc = scale_of<FAST>(cur.hdr[j], 0);
-        const uint32_t n0w = nib_word<FAST>(cur.q[j][0], 0, 0), n1w = nib_word<FAST>(cur.q[j][0], 0, 1);
-        b[j][0] = weight_pair<FAST>(n0w, 0, sc);
-        b[j][1] = weight_pair<FAST>(n0w, 1, sc);
-        b[j][2] = weight_pair<FAST>(n1w, 0, sc);
-        b[j][3] = weight_pair<FAST>(n1w, 1, sc);
+        const uint32_t w0 = nib_word<0>(wq[0][j], 0), w1 = nib_word<0>(wq[0][j], 1);
+        b[j][0] = weight_pair<FAST, 0>(w0, sc[0][j][0]);
+        b[j][1] = weight_pair<FAST, 1>(w0, sc[0][j][0]);
+        b[j][2] = weight_pair<FAST, 0>(w1, sc[0][j][0]);
+        b[j][3] = weight_pair<FAST, 1>(w1, sc[0][j][0]);
     }
-    // Each step: wave_step, then the activation load of step s+4, then the barrier.
-    auto step = [&](auto G_, auto G1_, const _Float16* Ac, const _Float16* An1, _Float16* An2, uint32_t s,
-                    const WData& wc, const WData& wn, Act& act2) {
-        constexpr int G = decltype(G_)::value, G1 = decltype(G1_)::value;
-        const Scale sn0_0 = scale_of<FAST>(wn.hdr[0], 2 * G1), sn0_1 = scale_of<FAST>(wn.hdr[1], 2 * G1);
-        wave_step<FAST, G, G1>(Ac, An1, An2, acc, a, b, wc, wn, sn0_0, sn0_1, act2, lane, tid);
-        act2 = load_act(a16, w, m, t, step_of(s + 4), tid);
-        lds_barrier();
-    };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    using I3 = std::integral_constant<int, 3>;
-    auto buf = [&](uint32_t k) { return ring + kLdsA * (k % 3); };  // tile buffer of step k
-    for (uint32_t i = 0; i < nsbu; ++i) {
+    for (uint32_t i = 0; i < sp.nsbu; ++i) {
         const uint32_t s = 4 * i;
-        nxt = load_wdata(w, t, sb_of(i + 1), wave, lane);
-        step(I0{}, I1{}, buf(s), buf(s + 1), buf(s + 2), s, cur, cur, actA);
-        step(I1{}, I2{}, buf(s + 1), buf(s + 2), buf(s + 3), s + 1, cur, cur, actB);
-        step(I2{}, I3{}, buf(s + 2), buf(s + 3), buf(s + 4), s + 2, cur, cur, actA);
-        step(I3{}, I0{}, buf(s + 3), buf(s + 4), buf(s + 5), s + 3, cur, nxt, actB);
-        cur = nxt;
+        wave_step<FAST, 0>(lds, lds, ws, sp, i, s, hmask, acc, a, b, wq, hdr, hdrn, sc, act);
+        lds_barrier();
+        wave_step<FAST, 1>(lds, lds, ws, sp, i, s + 1, hmask, acc, a, b, wq, hdr, hdrn, sc, act);
+        lds_barrier();
+        wave_step<FAST, 2>(lds, lds, ws, sp, i, s + 2, hmask, acc, a, b, wq, hdr, hdrn, sc, act);
+        lds_barrier();
+        wave_step<FAST, 3>(lds, lds, ws, sp, i, s + 3, hmask, acc, a, b, wq, hdr, hdrn, sc, act);
+        lds_barrier();
+        hdr[0] = hdrn[0];
+        hdr[1] = hdrn[1];
     }
     // result register r of lane l: row 8*(r/4) + 4*(l/32) + r%4, column l%32
     float* o = out + (uint64_t)z * (uint64_t)m * w.n;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const uint64_t col = t.n0 + 64 * wave + 32 * j + (lane & 31);
+        const uint64_t col = n0 + 64 * wave + 32 * j + r0;
         if (col >= w.n) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
 #pragma unroll
             for (int rr = 0; rr < 16; ++rr) {
-                const uint64_t row = t.m0 + 32 * i + 8 * (rr / 4) + 4 * (lane >> 5) + (rr % 4);
+                const uint64_t row = m0 + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
                 if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][rr];
             }
         }
