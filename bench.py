@@ -103,6 +103,49 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
     return res
 
 
+def run_deltanet(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
+    """One Gated DeltaNet decode block (hidden 4096, 32 heads of dk = dv = 128, FFN 12288) per
+    step, chained on the device (oq_deltanet_step); steps cycle over block copies whose weights
+    total >= 512 MiB, so every step streams its projections from HBM."""
+    rng = np.random.default_rng(SEED + 100)
+    d, w, vec, hist, st, x = synth.deltanet_block(rng)
+    first = oracle_amd.DeltaNetBlockWeights(ctx, d, w, vec)
+    wb = first.weight_bytes()
+    ncopies = max(1, math.ceil(copies_min_bytes / wb))
+    blocks = [first] + [oracle_amd.DeltaNetBlockWeights(ctx, d, w, vec) for _ in range(ncopies - 1)]
+    hb, sb, xb = ctx.to_device(hist), ctx.to_device(st), ctx.to_device(x)
+    yb = ctx.alloc(d["embedding"] * 4)
+
+    def step(i):
+        ctx.deltanet_step(blocks[i % ncopies], hb, sb, xb, yb)
+
+    step(0)  # sizes the block workspace before capture
+    ctx.sync()
+    ctx.capture_begin()
+    for i in range(warmup):
+        step(i)
+    g_warm = ctx.capture_end()
+    ctx.capture_begin()
+    for i in range(steps):
+        step(i)
+    g = ctx.capture_end()
+    g_warm.launch()
+    ctx.sync()
+    ctx.timer_start()
+    g.launch()
+    ms = ctx.timer_stop()
+    g.destroy()
+    g_warm.destroy()
+    for b in blocks:
+        b.release()
+    for buf in (hb, sb, xb, yb):
+        buf.free()
+    ms_step = ms / steps
+    return {"workload": "deltanet_block", "weight_bytes": wb, "copies": ncopies, "ms_per_step": ms_step,
+            "us_per_block": ms_step * 1e3, "weight_gbs": wb / (ms_step * 1e-3) / 1e9,
+            "state_bytes": 2 * st.nbytes, "dims": d}
+
+
 def run_copy_calibration(ctx, steps, nbytes=28311552):
     """Device-to-device copies of a known size: the FETCH_SIZE / WRITE_SIZE counters of this
     dispatch calibrate the same counters read on the GEMV kernels."""
@@ -173,7 +216,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="q4k_gemv", choices=sorted(WORKLOADS) + ["copy_calibration"])
+    ap.add_argument("--workload", default="q4k_gemv",
+                    choices=sorted(WORKLOADS) + ["copy_calibration", "deltanet_block"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     args = ap.parse_args()
@@ -190,10 +234,24 @@ def main():
         print(json.dumps(run_copy_calibration(ctx, args.steps)), flush=True)
         ctx.close()
         return
+    if args.workload == "deltanet_block":
+        r = run_deltanet(ctx, args.steps, args.warmup)
+        ctx.close()
+        print(json.dumps({
+            "metric": "DeltaNet decode block weight GB/s", "value": round(r["weight_gbs"], 2), "unit": "GB/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8xu4 dot (i32) + f32",
+            "data": "synthetic (seeded block weights, state ~ N(0, 0.01), x ~ N(0,1))",
+            "config": {"workload": "Gated DeltaNet decode block, batch 1", **r["dims"],
+                       "weight_bytes": r["weight_bytes"], "block_copies_cycled": r["copies"]},
+            "us_per_block": round(r["us_per_block"], 2),
+            "hbm_frac_weight_bytes": round(r["weight_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
+        return
     main_res = run_gpu(ctx, args.workload, args.steps, args.warmup)
-    secondary = None
+    secondary = block = None
     if not args.no_secondary and args.workload == "q4k_gemv":
         secondary = run_gpu(ctx, "q4k_down_m512", max(5, args.steps // 20), max(2, args.warmup // 5))
+        block = run_deltanet(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
     ctx.close()
 
     t, n, k, m, desc = WORKLOADS[args.workload]
@@ -223,6 +281,10 @@ def main():
         out["gemm_m512"] = {"tops": round(secondary["tops"], 2), "us": round(secondary["us_per_step"], 2),
                             "frac_fp16_mfma_peak": round(secondary["tops"] / MFMA_PEAK_TFLOPS["fp16"], 4),
                             "frac_int8_mfma_peak": round(secondary["tops"] / MFMA_PEAK_TFLOPS["int8"], 4)}
+    if block is not None:
+        out["deltanet_block"] = {"us": round(block["us_per_block"], 2), "weight_gbs": round(block["weight_gbs"], 1),
+                                 "hbm_frac": round(block["weight_gbs"] / HBM_PEAK_GBS, 4),
+                                 "weight_bytes": block["weight_bytes"]}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.workload)
     print(json.dumps(out), flush=True)

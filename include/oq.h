@@ -146,6 +146,44 @@ int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x_de
 int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q8k_dev,
                   float* y_dev);
 
+/* ------------------------------------------------------------------ Gated DeltaNet block */
+/* One Qwen3.5 recurrent (Gated DeltaNet) decoder block at batch 1, chained on the device.
+   Replaces oracle::runtime::execute_qwen35_recurrent_block_reference
+   (src/runtime/qwen35_block.cpp:406-605, with finish_block :326-352 and execute_mlp :296-324):
+     normed = RMSNorm(x) * input_norm
+     qkv, z, beta, alpha = projections of normed          (qkv: [2*Hk*dk + Hv*dv] rows)
+     conv = SiLU(causal depthwise conv step of qkv)       (reference_kernels.cpp:197-225)
+     out  = gated delta rule step over Hv heads            (reference_kernels.cpp:227-335)
+            with q, k of key head h % Hk, beta = sigmoid(beta),
+            log_decay = softplus(alpha + dt_bias) * decay
+     gated = RMSNorm_head(out) * out_norm * SiLU(z);  branch = out_proj(gated)
+     resid = x + branch;  post = RMSNorm(resid) * post_norm
+     y = resid + down(SiLU(gate(post)) * up(post))
+   The projections run on the library's matvec path (K-quant weights: activations quantized to
+   Q8_K, as oq_matvec).  conv_history_dev [C][conv_kernel] and state_dev [Hv][dk][dv] (the
+   reference's SsmState buffers, hybrid_cache.hpp:76-120) are updated in place.  trace_dev, if
+   not NULL, receives the intermediates in this order (F32, packed):
+     qkv[C] z[Hv*dv] beta[Hv] alpha[Hv] conv[C] out[Hv*dv] gated[Hv*dv] branch[E] resid[E]
+     post[E] gate[F] up[F] act[F] ffn[E]       with C = 2*Hk*dk + Hv*dv.
+   Device path limits: dk <= 128, dv in {64, 128, 192, 256}, conv_kernel <= 16, K-quant rows
+   <= 16384; otherwise OQ_INVALID_ARGUMENT.  Weight shape mismatches -> OQ_INVALID_ARGUMENT. */
+typedef struct oq_deltanet_block {
+    uint64_t embedding;   /* E */
+    uint64_t key_heads;   /* Hk */
+    uint64_t value_heads; /* Hv, a multiple of Hk */
+    uint64_t key_dim;     /* dk */
+    uint64_t value_dim;   /* dv */
+    uint64_t conv_kernel; /* taps of the causal convolution */
+    uint64_t ffn;         /* F */
+    float eps;            /* RMSNorm / L2-norm epsilon (manifest attention_rms_epsilon) */
+    const oq_weight *qkv, *z, *beta, *alpha, *out, *gate, *up, *down;
+    /* F32 device vectors: input_norm[E], conv_weight[C][conv_kernel], dt_bias[Hv], decay[Hv],
+       out_norm[dv], post_norm[E] */
+    const float *input_norm, *conv_weight, *dt_bias, *decay, *out_norm, *post_norm;
+} oq_deltanet_block;
+int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* block, float* conv_history_dev,
+                     float* state_dev, const float* x_dev, float* y_dev, float* trace_dev);
+
 /* ------------------------------------------------------------------ timing / graphs */
 
 /* HIP events on the context's stream, for timing the kernels launched there. */

@@ -42,6 +42,14 @@ _ORC_SIGS = [
     ("orc_dequantize_row_q8_k", C.c_int, [_P, _U64, _P]),
     ("orc_vec_dot_q8_k", C.c_int, [_U32, _U64, _P, _P, _F]),
     ("orc_fnv1a64", _U64, [_P, _U64]),
+    ("orc_sigmoid", C.c_float, [C.c_float]),
+    ("orc_softplus", C.c_float, [C.c_float]),
+    ("orc_silu", C.c_float, [C.c_float]),
+    ("orc_rms_norm_rows", C.c_int, [_P, _P, _U64, _U64, C.c_float, _P]),
+    ("orc_conv_step", C.c_int, [_P, _P, _U64, _U64, _P, _P, C.c_int]),
+    ("orc_gated_delta_step", C.c_int, [_P, _P, _P, _P, _P, _U64, _U64, _U64, C.c_float, _P, _P]),
+    ("orc_deltanet_trace_size", _U64, [_P]),
+    ("orc_deltanet_step", C.c_int, [_P, _P, _P, _P, _P, _P, C.c_int]),
 ]
 
 _REF_SIGS = [
@@ -55,6 +63,8 @@ _REF_SIGS = [
     ("ref_storage_matvec", C.c_int, [_U32, _U64, _U64, _P, _U64, _P, _U64, _P, _U64]),
     ("ref_mapped_tensor_matvec", C.c_int, [_U32, _U64, _U64, _P, _U64, _P, _U64, _P, _U64]),
     ("ref_storage_matvec_rows", C.c_int, [_U32, _U64, _P, _U64, _U64, _U64, _P, _P]),
+    ("ref_conv_step", C.c_int, [_U64, _U64, _P, _P, _P, _P, C.c_int]),
+    ("ref_gated_delta_step", C.c_int, [_U64, _U64, _U64, _P, _P, _P, _P, _P, C.c_float, _P, _P]),
 ]
 
 
@@ -241,6 +251,27 @@ def ref_storage_matvec(type_id: int, rows: int, cols: int, data: np.ndarray, x: 
     return y
 
 
+def ref_conv_step(history: np.ndarray, weights: np.ndarray, x: np.ndarray, apply_silu: bool = False) -> np.ndarray:
+    """One step of the reference's causal depthwise convolution; updates `history` in place."""
+    ch, kern = history.shape
+    w = np.ascontiguousarray(weights, dtype=np.float32)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(ch, dtype=np.float32)
+    _chk(ref().ref_conv_step(ch, kern, _ptr(history), _ptr(w), _ptr(xv), _ptr(out), int(apply_silu)), ref(),
+         "ref_last_error")
+    return out
+
+
+def ref_gated_delta_step(q, k, v, beta, log_decay, state: np.ndarray, eps: float) -> np.ndarray:
+    """One step of the reference's gated delta rule; updates `state` [H][dk][dv] in place."""
+    heads, dk, dv = state.shape
+    arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v, beta, log_decay)]
+    out = np.empty((heads, dv), dtype=np.float32)
+    _chk(ref().ref_gated_delta_step(heads, dk, dv, *[_ptr(a) for a in arrs], eps, _ptr(state), _ptr(out)), ref(),
+         "ref_last_error")
+    return out
+
+
 def ref_status(fn: str, *args) -> int:
     return getattr(ref(), fn)(*args)
 
@@ -250,3 +281,99 @@ def default_threads() -> int:
         return max(1, len(os.sched_getaffinity(0)))
     except AttributeError:
         return os.cpu_count() or 1
+
+
+# ---------------------------------------------------------------- Gated DeltaNet block
+
+def sigmoid(v: float) -> float:
+    return lib().orc_sigmoid(v)
+
+
+def softplus(v: float) -> float:
+    return lib().orc_softplus(v)
+
+
+def silu(v: float) -> float:
+    return lib().orc_silu(v)
+
+
+def rms_norm_rows(x: np.ndarray, weight: np.ndarray, width: int, eps: float) -> np.ndarray:
+    xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    out = np.empty_like(xv)
+    _chk(lib().orc_rms_norm_rows(_ptr(xv), _ptr(w), xv.size, width, eps, _ptr(out)), lib(), "orc_last_error")
+    return out
+
+
+def conv_step(history: np.ndarray, weights: np.ndarray, x: np.ndarray, apply_silu: bool = False) -> np.ndarray:
+    """Restated causal depthwise convolution step; updates `history` [channels][kernel] in place."""
+    ch, kern = history.shape
+    w = np.ascontiguousarray(weights, dtype=np.float32)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(ch, dtype=np.float32)
+    _chk(lib().orc_conv_step(_ptr(xv), _ptr(w), ch, kern, _ptr(history), _ptr(out), int(apply_silu)), lib(),
+         "orc_last_error")
+    return out
+
+
+def gated_delta_step(q, k, v, beta, log_decay, state: np.ndarray, eps: float) -> np.ndarray:
+    """Restated gated delta rule step; updates `state` [H][dk][dv] in place."""
+    heads, dk, dv = state.shape
+    arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v, beta, log_decay)]
+    out = np.empty((heads, dv), dtype=np.float32)
+    _chk(lib().orc_gated_delta_step(*[_ptr(a) for a in arrs], heads, dk, dv, eps, _ptr(state), _ptr(out)), lib(),
+         "orc_last_error")
+    return out
+
+
+class _DNBlock(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("embedding", "key_heads", "value_heads", "key_dim", "value_dim",
+                                          "conv_kernel", "ffn")] + [("eps", C.c_float)] + \
+               [(n + "_type", C.c_uint32) for n in ("qkv", "z", "beta", "alpha", "out", "gate", "up", "down")] + \
+               [(n, C.c_void_p) for n in ("qkv", "z", "beta", "alpha", "out", "gate", "up", "down")] + \
+               [(n, C.c_void_p) for n in ("input_norm", "conv_weight", "dt_bias", "decay", "out_norm", "post_norm")]
+
+
+DN_WEIGHTS = ("qkv", "z", "beta", "alpha", "out", "gate", "up", "down")
+DN_VECTORS = ("input_norm", "conv_weight", "dt_bias", "decay", "out_norm", "post_norm")
+DN_TRACE = ("qkv", "z", "beta", "alpha", "conv", "rec", "gated", "branch", "resid", "post", "gate", "up", "act", "ffn")
+
+
+def deltanet_trace_sizes(dims: dict) -> dict:
+    C_ = 2 * dims["key_heads"] * dims["key_dim"] + dims["value_heads"] * dims["value_dim"]
+    V = dims["value_heads"] * dims["value_dim"]
+    E, F, Hv = dims["embedding"], dims["ffn"], dims["value_heads"]
+    return dict(zip(DN_TRACE, (C_, V, Hv, Hv, C_, V, V, E, E, E, F, F, F, E)))
+
+
+def deltanet_step(dims: dict, weights: dict, vectors: dict, conv_history: np.ndarray, state: np.ndarray,
+                  x: np.ndarray, threads: int | None = None, trace: bool = False):
+    """Restated recurrent block step.  weights[name] = (ggml type, uint8 bytes); vectors[name] = F32;
+    conv_history and state are updated in place.  Returns y (and the intermediates when trace)."""
+    b = _DNBlock()
+    for k_ in ("embedding", "key_heads", "value_heads", "key_dim", "value_dim", "conv_kernel", "ffn"):
+        setattr(b, k_, int(dims[k_]))
+    b.eps = float(dims["eps"])
+    keep = []
+    for n in DN_WEIGHTS:
+        t, data = weights[n]
+        a = np.ascontiguousarray(data, dtype=np.uint8)
+        keep.append(a)
+        setattr(b, n + "_type", int(t))
+        setattr(b, n, a.ctypes.data)
+    for n in DN_VECTORS:
+        a = np.ascontiguousarray(vectors[n], dtype=np.float32)
+        keep.append(a)
+        setattr(b, n, a.ctypes.data)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(int(dims["embedding"]), dtype=np.float32)
+    tr = np.empty(int(lib().orc_deltanet_trace_size(C.byref(b))), dtype=np.float32) if trace else None
+    _chk(lib().orc_deltanet_step(C.byref(b), _ptr(conv_history), _ptr(state), _ptr(xv), _ptr(y),
+                                 _ptr(tr) if trace else None, threads or default_threads()), lib(), "orc_last_error")
+    if not trace:
+        return y
+    out, off = {}, 0
+    for n, sz in deltanet_trace_sizes(dims).items():
+        out[n] = tr[off:off + sz]
+        off += sz
+    return y, out

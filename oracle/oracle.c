@@ -607,3 +607,213 @@ uint64_t orc_fnv1a64(const void* data, uint64_t n) {
     }
     return h;
 }
+
+/* ---------------------------------------------------------------- Gated DeltaNet decode block */
+
+/* qwen35_block.cpp:138-145: branch on the sign so exp never overflows */
+float orc_sigmoid(float v) {
+    if (v >= 0.0f) {
+        const float e = expf(-v);
+        return 1.0f / (1.0f + e);
+    }
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+
+/* qwen35_block.cpp:147-155 */
+float orc_softplus(float v) {
+    if (v > 20.0f) return v;
+    if (v < -20.0f) return expf(v);
+    return log1pf(expf(v));
+}
+
+/* qwen35_block.cpp:157-159 */
+float orc_silu(float v) { return v * orc_sigmoid(v); }
+
+/* qwen35_block.cpp:161-186: sum of squares in double, inverse_rms rounded to F32, then
+   (x * inverse_rms) * weight in F32 */
+int orc_rms_norm_rows(const float* in, const float* weight, uint64_t n, uint64_t width, float eps,
+                      float* out) {
+    if (width == 0 || n % width != 0) return fail(ORC_INVALID_ARGUMENT, "Qwen3.5 RMSNorm dimensions are incompatible");
+    if (!(eps > 0.0f) || !isfinite(eps)) return fail(ORC_INVALID_ARGUMENT, "Qwen3.5 RMSNorm epsilon must be positive and finite");
+    for (uint64_t r = 0; r < n / width; ++r) {
+        const float* x = in + r * width;
+        double ss = 0.0;
+        for (uint64_t c = 0; c < width; ++c) ss += (double)x[c] * (double)x[c];
+        const double mean = ss / (double)width;
+        const float inv = (float)(1.0 / sqrt(mean + (double)eps));
+        for (uint64_t c = 0; c < width; ++c) out[r * width + c] = x[c] * inv * weight[c];
+    }
+    return ORC_OK;
+}
+
+/* reference_kernels.cpp:197-225: shift the channel's history left, append the input, dot in
+   double with the channel's kernel taps */
+int orc_conv_step(const float* input, const float* weights, uint64_t channels, uint64_t kernel,
+                  float* history, float* out, int apply_silu) {
+    if (channels == 0 || kernel == 0) return fail(ORC_INVALID_ARGUMENT, "depthwise convolution dimensions do not match SSM state");
+    for (uint64_t c = 0; c < channels; ++c) {
+        float* h = history + c * kernel;
+        for (uint64_t i = 1; i < kernel; ++i) h[i - 1] = h[i];
+        h[kernel - 1] = input[c];
+        double sum = 0.0;
+        for (uint64_t i = 0; i < kernel; ++i) sum += (double)h[i] * (double)weights[c * kernel + i];
+        const float v = (float)sum;
+        out[c] = apply_silu ? v * orc_sigmoid(v) : v;
+    }
+    return ORC_OK;
+}
+
+/* reference_kernels.cpp:227-335, per head: L2-normalise q and k (norms in double,
+   1 / max(norm, eps) rounded to F32, q also scaled by 1/sqrt(dk)); decay the state by
+   exp(log_decay); memory = state^T k (F32, key order); delta = (v - memory) * beta;
+   state += k outer delta; out = state^T q (double accumulation, key order) */
+int orc_gated_delta_step(const float* q, const float* k, const float* v, const float* beta,
+                         const float* log_decay, uint64_t heads, uint64_t dk, uint64_t dv,
+                         float eps, float* state, float* out) {
+    if (!(eps > 0.0f)) return fail(ORC_INVALID_ARGUMENT, "gated delta normalization epsilon must be positive");
+    if (heads == 0 || dk == 0 || dv == 0) return fail(ORC_INVALID_ARGUMENT, "gated_delta_step dimensions do not match SSM state");
+    float* nq = (float*)malloc(dk * sizeof(float));
+    float* nk = (float*)malloc(dk * sizeof(float));
+    float* mem = (float*)malloc(dv * sizeof(float));
+    float* delta = (float*)malloc(dv * sizeof(float));
+    if (!nq || !nk || !mem || !delta) {
+        free(nq); free(nk); free(mem); free(delta);
+        return fail(ORC_RUNTIME_ERROR, "out of memory");
+    }
+    const float query_scale = 1.0f / sqrtf((float)dk);
+    int rc = ORC_OK;
+    for (uint64_t h = 0; h < heads; ++h) {
+        if (!(beta[h] >= 0.0f && beta[h] <= 1.0f) || !isfinite(beta[h]) || !isfinite(log_decay[h])) {
+            rc = fail(ORC_INVALID_ARGUMENT, "gated delta beta/decay values are invalid");
+            break;
+        }
+        const float* qh = q + h * dk;
+        const float* kh = k + h * dk;
+        double qn = 0.0, kn = 0.0;
+        for (uint64_t d = 0; d < dk; ++d) {
+            qn += (double)qh[d] * (double)qh[d];
+            kn += (double)kh[d] * (double)kh[d];
+        }
+        const double ql = sqrt(qn), kl = sqrt(kn);
+        const float iq = (float)(1.0 / (ql > (double)eps ? ql : (double)eps));
+        const float ik = (float)(1.0 / (kl > (double)eps ? kl : (double)eps));
+        for (uint64_t d = 0; d < dk; ++d) {
+            nq[d] = qh[d] * iq * query_scale;
+            nk[d] = kh[d] * ik;
+        }
+        const float decay = expf(log_decay[h]);
+        float* s = state + h * dk * dv;
+        for (uint64_t i = 0; i < dk * dv; ++i) s[i] *= decay;
+        for (uint64_t j = 0; j < dv; ++j) mem[j] = 0.0f;
+        for (uint64_t d = 0; d < dk; ++d)
+            for (uint64_t j = 0; j < dv; ++j) mem[j] += s[d * dv + j] * nk[d];
+        for (uint64_t j = 0; j < dv; ++j) delta[j] = (v[h * dv + j] - mem[j]) * beta[h];
+        for (uint64_t d = 0; d < dk; ++d)
+            for (uint64_t j = 0; j < dv; ++j) s[d * dv + j] += nk[d] * delta[j];
+        for (uint64_t j = 0; j < dv; ++j) {
+            double sum = 0.0;
+            for (uint64_t d = 0; d < dk; ++d) sum += (double)s[d * dv + j] * (double)nq[d];
+            out[h * dv + j] = (float)sum;
+        }
+    }
+    free(nq); free(nk); free(mem); free(delta);
+    return rc;
+}
+
+static int is_kquant(uint32_t type) {
+    return type == ORC_TYPE_Q4_K || type == ORC_TYPE_Q5_K || type == ORC_TYPE_Q6_K;
+}
+
+/* one projection of the block: rows x cols weight against x (see oracle.h for the semantics) */
+static int block_matvec(uint32_t type, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
+                        float* y, int threads) {
+    uint64_t rb = 0;
+    int rc = orc_row_byte_size(cols, type, &rb);
+    if (rc != ORC_OK) return rc;
+    const float* xin = x;
+    float* xhat = NULL;
+    if (is_kquant(type)) {
+        uint8_t* blocks = (uint8_t*)malloc(cols / ORC_QK_K * ORC_Q8_K_BYTES);
+        xhat = (float*)malloc(cols * sizeof(float));
+        if (!blocks || !xhat) {
+            free(blocks); free(xhat);
+            return fail(ORC_RUNTIME_ERROR, "out of memory");
+        }
+        rc = orc_quantize_row_q8_k(x, cols, blocks);
+        if (rc == ORC_OK) rc = orc_dequantize_row_q8_k(blocks, cols, xhat);
+        free(blocks);
+        if (rc != ORC_OK) {
+            free(xhat);
+            return rc;
+        }
+        xin = xhat;
+    }
+    rc = orc_storage_matvec_mt(type, rows, cols, w, rows * rb, xin, y, threads);
+    free(xhat);
+    return rc;
+}
+
+uint64_t orc_deltanet_trace_size(const orc_deltanet_block* b) {
+    const uint64_t C = 2 * b->key_heads * b->key_dim + b->value_heads * b->value_dim;
+    const uint64_t V = b->value_heads * b->value_dim;
+    return 2 * C + 3 * V + 2 * b->value_heads + 4 * b->embedding + 3 * b->ffn;
+}
+
+/* qwen35_block.cpp:406-605 (recurrent block), :326-352 (finish_block), :296-324 (MLP) */
+int orc_deltanet_step(const orc_deltanet_block* b, float* conv_history, float* state,
+                      const float* x, float* y, float* trace, int threads) {
+    const uint64_t E = b->embedding, Hk = b->key_heads, Hv = b->value_heads, dk = b->key_dim,
+                   dv = b->value_dim, F = b->ffn;
+    if (E == 0 || Hk == 0 || Hv == 0 || dk == 0 || dv == 0 || F == 0 || b->conv_kernel == 0 || Hv % Hk != 0)
+        return fail(ORC_INVALID_ARGUMENT, "Qwen3.5 recurrent block dimensions are incompatible");
+    const uint64_t KW = Hk * dk, V = Hv * dv, C = 2 * KW + V;
+    float* buf = (float*)calloc(orc_deltanet_trace_size(b) + 2 * Hv + E + 2 * Hv * dk, sizeof(float));
+    if (!buf) return fail(ORC_RUNTIME_ERROR, "out of memory");
+    float *qkv = buf, *z = qkv + C, *beta = z + V, *alpha = beta + Hv, *conv = alpha + Hv, *rec = conv + C,
+          *gated = rec + V, *branch = gated + V, *resid = branch + E, *post = resid + E, *gate = post + E,
+          *up = gate + F, *act = up + F, *ffn = act + F, *beta_s = ffn + E, *log_decay = beta_s + Hv,
+          *normed = log_decay + Hv, *query = normed + E, *key = query + Hv * dk;
+    int rc = orc_rms_norm_rows(x, b->input_norm, E, E, b->eps, normed);
+    if (rc == ORC_OK) rc = block_matvec(b->qkv_type, b->qkv, C, E, normed, qkv, threads);
+    if (rc == ORC_OK) rc = block_matvec(b->z_type, b->z, V, E, normed, z, threads);
+    if (rc == ORC_OK) rc = block_matvec(b->beta_type, b->beta, Hv, E, normed, beta, threads);
+    if (rc == ORC_OK) rc = block_matvec(b->alpha_type, b->alpha, Hv, E, normed, alpha, threads);
+    if (rc == ORC_OK) {
+        for (uint64_t h = 0; h < Hv; ++h) {
+            beta_s[h] = orc_sigmoid(beta[h]);
+            log_decay[h] = orc_softplus(alpha[h] + b->dt_bias[h]) * b->decay[h];
+        }
+        rc = orc_conv_step(qkv, b->conv_weight, C, b->conv_kernel, conv_history, conv, 0);
+    }
+    if (rc == ORC_OK) {
+        for (uint64_t c = 0; c < C; ++c) conv[c] = orc_silu(conv[c]);
+        /* repeat_heads_tiled (qwen35_block.cpp:233-251): value head t takes key head t % Hk */
+        for (uint64_t t = 0; t < Hv; ++t) {
+            memcpy(query + t * dk, conv + (t % Hk) * dk, dk * sizeof(float));
+            memcpy(key + t * dk, conv + KW + (t % Hk) * dk, dk * sizeof(float));
+        }
+        rc = orc_gated_delta_step(query, key, conv + 2 * KW, beta_s, log_decay, Hv, dk, dv, b->eps, state, rec);
+    }
+    if (rc == ORC_OK) rc = orc_rms_norm_rows(rec, b->out_norm, V, dv, b->eps, gated);
+    if (rc == ORC_OK) {
+        for (uint64_t i = 0; i < V; ++i) gated[i] *= orc_silu(z[i]);
+        rc = block_matvec(b->out_type, b->out, E, V, gated, branch, threads);
+    }
+    if (rc == ORC_OK) {
+        for (uint64_t i = 0; i < E; ++i) resid[i] = x[i] + branch[i];
+        rc = orc_rms_norm_rows(resid, b->post_norm, E, E, b->eps, post);
+    }
+    if (rc == ORC_OK) rc = block_matvec(b->gate_type, b->gate, F, E, post, gate, threads);
+    if (rc == ORC_OK) rc = block_matvec(b->up_type, b->up, F, E, post, up, threads);
+    if (rc == ORC_OK) {
+        for (uint64_t i = 0; i < F; ++i) act[i] = orc_silu(gate[i]) * up[i];
+        rc = block_matvec(b->down_type, b->down, E, F, act, ffn, threads);
+    }
+    if (rc == ORC_OK) {
+        for (uint64_t i = 0; i < E; ++i) y[i] = resid[i] + ffn[i];
+        if (trace) memcpy(trace, buf, orc_deltanet_trace_size(b) * sizeof(float));
+    }
+    free(buf);
+    return rc;
+}

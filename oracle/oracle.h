@@ -105,6 +105,52 @@ int orc_dequantize_row_q8_k(const uint8_t* blocks, uint64_t k, float* out);
 /* GGML integer dots of a weight row against a Q8_K row */
 int orc_vec_dot_q8_k(uint32_t type, uint64_t k, const uint8_t* wrow, const uint8_t* q8k, float* out);
 
+/* ---------------------------------------------------------------- Gated DeltaNet decode block
+ * Restatement of the reference's recurrent (linear-attention) block at batch 1:
+ *   orc_sigmoid / orc_softplus / orc_silu    qwen35_block.cpp:138-159
+ *   orc_rms_norm_rows                        qwen35_block.cpp:161-186 (double sum of squares)
+ *   orc_l2_inverse (inside the delta step)   reference_kernels.cpp:283-292
+ *   orc_conv_step                            reference_kernels.cpp:197-225
+ *   orc_gated_delta_step                     reference_kernels.cpp:227-335 (state [head][key][value])
+ *   orc_deltanet_step                        qwen35_block.cpp:406-605 + finish_block :326-352 +
+ *                                            execute_mlp :296-324
+ * The block's projections use the device path's product semantics: a K-quant weight row is
+ * dotted (quantized_reference.cpp:24-82 arithmetic) with the activation after Q8_K
+ * quantization and dequantization; other types with the F32 activation.
+ */
+float orc_sigmoid(float v);
+float orc_softplus(float v);
+float orc_silu(float v);
+/* out[r][c] = in[r][c] * inverse_rms(r) * weight[c]; rows = n / width */
+int orc_rms_norm_rows(const float* in, const float* weight, uint64_t n, uint64_t width, float eps,
+                      float* out);
+/* history [channels][kernel] is shifted and receives input; out = sum(history * weights) */
+int orc_conv_step(const float* input, const float* weights, uint64_t channels, uint64_t kernel,
+                  float* history, float* out, int apply_silu);
+/* q, k [heads][dk]; v, out [heads][dv]; beta, log_decay [heads]; state [heads][dk][dv] */
+int orc_gated_delta_step(const float* q, const float* k, const float* v, const float* beta,
+                         const float* log_decay, uint64_t heads, uint64_t dk, uint64_t dv,
+                         float eps, float* state, float* out);
+
+typedef struct orc_deltanet_block {
+    uint64_t embedding, key_heads, value_heads, key_dim, value_dim, conv_kernel, ffn;
+    float eps;
+    /* GGML weights, rows x cols row-major GGML rows (dimensions[1] x dimensions[0]) */
+    uint32_t qkv_type, z_type, beta_type, alpha_type, out_type, gate_type, up_type, down_type;
+    const uint8_t *qkv, *z, *beta, *alpha, *out, *gate, *up, *down;
+    /* F32 vectors: input_norm[E], conv_weight[C][kernel], dt_bias[Hv], decay[Hv],
+       out_norm[dv], post_norm[E] */
+    const float *input_norm, *conv_weight, *dt_bias, *decay, *out_norm, *post_norm;
+} orc_deltanet_block;
+
+/* intermediates, in order (NULL to skip); sizes: C = 2*Hk*dk + Hv*dv, V = Hv*dv, F = ffn */
+enum { ORC_DN_TRACE_FIELDS = 14 };
+/* trace layout: qkv[C] z[V] beta[Hv] alpha[Hv] conv[C] rec[V] gated[V] branch[E] resid[E]
+   post[E] gate[F] up[F] act[F] ffn[E] */
+uint64_t orc_deltanet_trace_size(const orc_deltanet_block* b);
+int orc_deltanet_step(const orc_deltanet_block* b, float* conv_history, float* state,
+                      const float* x, float* y, float* trace, int threads);
+
 /* FNV-1a 64 over raw bytes (the reference fingerprints F32 bit patterns the same way,
    qwen35_block.cpp:354-364) */
 uint64_t orc_fnv1a64(const void* data, uint64_t nbytes);

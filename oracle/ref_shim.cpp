@@ -11,6 +11,9 @@
 #include "oracle/model/gguf.hpp"
 #include "oracle/model/mapped_gguf.hpp"
 #include "oracle/model/storage_decode.hpp"
+#include "oracle/core/tensor.hpp"
+#include "oracle/runtime/hybrid_cache.hpp"
+#include "oracle/runtime/reference_kernels.hpp"
 
 #include <cstdio>
 #include <cstring>
@@ -148,4 +151,42 @@ int ref_storage_matvec_rows(std::uint32_t type, std::uint64_t cols, const void* 
     });
 }
 
+
+// The reference's causal depthwise convolution step (src/runtime/reference_kernels.cpp:197-225)
+// on an SsmState whose history is loaded from and stored back to `history` [channels][kernel].
+int ref_conv_step(std::uint64_t channels, std::uint64_t kernel, float* history, const float* weights,
+                  const float* input, float* out, int apply_silu) {
+    return guarded([&] {
+        oracle::runtime::SsmState st(static_cast<std::size_t>(channels), static_cast<std::size_t>(kernel), 1, 1, 1);
+        auto h = st.convolution_history();
+        std::copy(history, history + channels * kernel, h.begin());
+        oracle::runtime::causal_depthwise_convolution_step(
+            std::span<const float>(input, static_cast<std::size_t>(channels)),
+            std::span<const float>(weights, static_cast<std::size_t>(channels * kernel)), st,
+            std::span<float>(out, static_cast<std::size_t>(channels)), apply_silu != 0);
+        std::copy(h.begin(), h.end(), history);
+    });
+}
+
+// The reference's gated delta rule step (src/runtime/reference_kernels.cpp:227-335) with the
+// recurrent state [heads][dk][dv] loaded from and stored back to `state`.
+int ref_gated_delta_step(std::uint64_t heads, std::uint64_t dk, std::uint64_t dv, const float* q,
+                         const float* k, const float* v, const float* beta, const float* log_decay,
+                         float eps, float* state, float* out) {
+    return guarded([&] {
+        const auto H = static_cast<std::size_t>(heads), K = static_cast<std::size_t>(dk),
+                   D = static_cast<std::size_t>(dv);
+        oracle::runtime::SsmState st(1, 1, H, K, D);
+        auto r = st.recurrent();
+        std::copy(state, state + H * K * D, r.begin());
+        oracle::core::Tensor tq({H, K}), tk({H, K}), tv({H, D}), to({H, D});
+        std::copy(q, q + H * K, tq.data().begin());
+        std::copy(k, k + H * K, tk.data().begin());
+        std::copy(v, v + H * D, tv.data().begin());
+        oracle::runtime::gated_delta_step(tq, tk, tv, std::span<const float>(beta, H),
+                                          std::span<const float>(log_decay, H), st, to, eps);
+        std::copy(r.begin(), r.end(), state);
+        std::copy(to.data().begin(), to.data().end(), out);
+    });
+}
 }  // extern "C"

@@ -241,6 +241,12 @@ class Context:
     def matmul_q8k(self, w: Weight, m: int, q8k: DeviceBuffer, y: DeviceBuffer) -> None:
         self._call(self.lib.oq_matmul_q8k, self.h, w.h, m, q8k.ptr, y.ptr)
 
+    def deltanet_step(self, block: "DeltaNetBlockWeights", conv_history: DeviceBuffer, state: DeviceBuffer,
+                      x: DeviceBuffer, y: DeviceBuffer, trace: DeviceBuffer | None = None) -> None:
+        """One Gated DeltaNet decode block step (oq_deltanet_step); updates conv_history and state."""
+        self._call(self.lib.oq_deltanet_step, self.h, C.byref(block.desc), conv_history.ptr, state.ptr, x.ptr, y.ptr,
+                   trace.ptr if trace is not None else None)
+
     # timing / graphs
     def timer_start(self) -> None:
         self._call(self.lib.oq_timer_start, self.h)
@@ -294,3 +300,44 @@ def decode_rows(ctx: Context, type_id: int, cols: int, rows: int, data: np.ndarr
         return r.reshape(rows, cols)
     finally:
         w.release()
+
+
+DELTANET_WEIGHTS = ("qkv", "z", "beta", "alpha", "out", "gate", "up", "down")
+DELTANET_VECTORS = ("input_norm", "conv_weight", "dt_bias", "decay", "out_norm", "post_norm")
+
+
+class DeltaNetBlockWeights:
+    """Device-resident weights of one Gated DeltaNet block: the eight projections uploaded once
+    (weights[name] = (ggml type, host bytes)) and the F32 vectors copied to HBM."""
+
+    def __init__(self, ctx: Context, dims: dict, weights: dict, vectors: dict):
+        from ._lib import DeltaNetBlock
+        E, F = int(dims["embedding"]), int(dims["ffn"])
+        Hk, Hv, dk, dv = (int(dims[k]) for k in ("key_heads", "value_heads", "key_dim", "value_dim"))
+        C_, V = 2 * Hk * dk + Hv * dv, Hv * dv
+        shapes = {"qkv": (E, C_), "z": (E, V), "beta": (E, Hv), "alpha": (E, Hv), "out": (V, E),
+                  "gate": (E, F), "up": (E, F), "down": (F, E)}
+        self.weights = {n: ctx.upload(weights[n][0], shapes[n][0], shapes[n][1], weights[n][1])
+                        for n in DELTANET_WEIGHTS}
+        self.vectors = {n: ctx.to_device(np.ascontiguousarray(vectors[n], dtype=np.float32))
+                        for n in DELTANET_VECTORS}
+        d = DeltaNetBlock()
+        for k in ("embedding", "key_heads", "value_heads", "key_dim", "value_dim", "conv_kernel", "ffn"):
+            setattr(d, k, int(dims[k]))
+        d.eps = float(dims["eps"])
+        for n in DELTANET_WEIGHTS:
+            setattr(d, n, self.weights[n].h)
+        for n in DELTANET_VECTORS:
+            setattr(d, n, self.vectors[n].ptr)
+        self.desc = d
+        self.dims = dict(dims)
+
+    def weight_bytes(self) -> int:
+        """GGML bytes of the eight projections (what one block step streams)."""
+        return sum(ggml_row_byte_size(w.ne0, w.type) * w.ne1 for w in self.weights.values())
+
+    def release(self) -> None:
+        for w in self.weights.values():
+            w.release()
+        for v in self.vectors.values():
+            v.free()

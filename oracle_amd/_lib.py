@@ -47,6 +47,7 @@ SIGNATURES = [
     ("oq_matvec_q8k", C.c_int, [_P, _P, _P, _P]),
     ("oq_matmul", C.c_int, [_P, _P, _U64, _P, _P]),
     ("oq_matmul_q8k", C.c_int, [_P, _P, _U64, _P, _P]),
+    ("oq_deltanet_step", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     ("oq_timer_start", C.c_int, [_P]),
     ("oq_timer_stop", C.c_int, [_P, C.POINTER(C.c_float)]),
     ("oq_capture_begin", C.c_int, [_P]),
@@ -54,6 +55,16 @@ SIGNATURES = [
     ("oq_graph_launch", C.c_int, [_P, _P]),
     ("oq_graph_destroy", None, [_P]),
 ]
+
+
+
+class DeltaNetBlock(C.Structure):
+    """oq_deltanet_block (include/oq.h)."""
+    _fields_ = [(n, C.c_uint64) for n in ("embedding", "key_heads", "value_heads", "key_dim", "value_dim",
+                                          "conv_kernel", "ffn")] + [("eps", C.c_float)] + \
+               [(n, C.c_void_p) for n in ("qkv", "z", "beta", "alpha", "out", "gate", "up", "down")] + \
+               [(n, C.c_void_p) for n in ("input_norm", "conv_weight", "dt_bias", "decay", "out_norm", "post_norm")]
+
 
 _lib: C.CDLL | None = None
 

@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <cmath>
 #include <string>
 
 #include "../../include/oq.h"
@@ -46,6 +47,8 @@ struct oq_context {
     bool capturing = false;
     void* scratch = nullptr;  // Q8_K staging (un-fused GEMV) or planar image + split partials (GEMM)
     uint64_t scratch_bytes = 0;
+    void* work = nullptr;  // intermediates of the DeltaNet block step
+    uint64_t work_bytes = 0;
 };
 
 struct oq_weight {
@@ -160,6 +163,23 @@ int ensure_scratch(oq_context* ctx, uint64_t bytes) {
     return OQ_OK;
 }
 
+int ensure_work(oq_context* ctx, uint64_t bytes) {
+    if (ctx->work_bytes >= bytes) return OQ_OK;
+    if (ctx->capturing) {
+        return fail(ctx, OQ_INVALID_ARGUMENT,
+                    "block workspace must be sized before graph capture (run the call once first)");
+    }
+    if (ctx->work) {
+        OQ_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        OQ_HIP(ctx, hipFree(ctx->work), "hipFree");
+        ctx->work = nullptr;
+        ctx->work_bytes = 0;
+    }
+    OQ_HIP(ctx, hipMalloc(&ctx->work, bytes), "hipMalloc(block workspace)");
+    ctx->work_bytes = bytes;
+    return OQ_OK;
+}
+
 bool env_flag(const char* name, bool fallback) {
     const char* v = getenv(name);
     return v ? atoi(v) != 0 : fallback;
@@ -230,6 +250,108 @@ int launch_rc(oq_context* ctx, hipError_t e, const char* what) {
     return e == hipSuccess ? OQ_OK : hip_fail(ctx, e, what);
 }
 
+// One projection of the DeltaNet block (batch 1): the matvec path of oq_matvec with the F32
+// activation quantized inside the K-quant GEMV.
+hipError_t block_project(const oq_weight* w, const float* x, float* y, hipStream_t s) {
+    if (is_kquant(w->m.type)) return oq::launch_gemv_kquant(w->m, 1, x, nullptr, y, s);
+    return oq::launch_gemv_f32act(w->m, 1, x, y, s);
+}
+
+int check_block_weight(oq_context* ctx, const oq_weight* w, uint64_t ne0, uint64_t ne1, const char* name) {
+    if (int rc = check_weight(ctx, w)) return fail(ctx, rc, std::string("DeltaNet block weight ") + name + ": " + ctx->error);
+    if (w->m.k != ne0 || w->m.n != ne1) {
+        return fail(ctx, OQ_INVALID_ARGUMENT,
+                    std::string("DeltaNet block weight ") + name + " has shape [" + std::to_string(w->m.k) + ", " +
+                        std::to_string(w->m.n) + "], expected [" + std::to_string(ne0) + ", " + std::to_string(ne1) + "]");
+    }
+    if (is_kquant(w->m.type) && !oq::gemv_kquant_supported(w->m)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, std::string("DeltaNet block weight ") + name + ": K-quant rows longer than 16384 elements are not supported yet");
+    }
+    return OQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, float* state, const float* x,
+                     float* y, float* trace) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (!b || !hist || !state || !x || !y) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    const uint64_t E = b->embedding, Hk = b->key_heads, Hv = b->value_heads, dk = b->key_dim, dv = b->value_dim,
+                   K = b->conv_kernel, F = b->ffn;
+    if (E == 0 || Hk == 0 || Hv == 0 || dk == 0 || dv == 0 || K == 0 || F == 0 || Hv % Hk != 0) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 recurrent block dimensions are incompatible");
+    }
+    if (!(b->eps > 0.0f) || !std::isfinite(b->eps)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 RMSNorm epsilon must be positive and finite");
+    }
+    if (!oq::deltanet_dims_supported(dk, dv, K)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT,
+                    "DeltaNet block device path needs key_dim <= 128, value_dim in {64,128,192,256}, conv_kernel <= 16");
+    }
+    if (E > 0x7FFFFFFF || F > 0x7FFFFFFF || Hv * dv > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "block too large");
+    const uint64_t V = Hv * dv, C = 2 * Hk * dk + V;
+    if (int rc = check_block_weight(ctx, b->qkv, E, C, "qkv")) return rc;
+    if (int rc = check_block_weight(ctx, b->z, E, V, "z")) return rc;
+    if (int rc = check_block_weight(ctx, b->beta, E, Hv, "beta")) return rc;
+    if (int rc = check_block_weight(ctx, b->alpha, E, Hv, "alpha")) return rc;
+    if (int rc = check_block_weight(ctx, b->out, V, E, "out")) return rc;
+    if (int rc = check_block_weight(ctx, b->gate, E, F, "gate")) return rc;
+    if (int rc = check_block_weight(ctx, b->up, E, F, "up")) return rc;
+    if (int rc = check_block_weight(ctx, b->down, F, E, "down")) return rc;
+    if (!b->input_norm || !b->conv_weight || !b->dt_bias || !b->decay || !b->out_norm || !b->post_norm) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "null block vector");
+    }
+    if (!aligned(x, 4) || !aligned(y, 4) || !aligned(hist, 4) || !aligned(state, 4)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer");
+    }
+    // workspace: the trace fields, then beta_s, log_decay and the normalised input, each padded
+    // to 64 floats so every projection input is 256-byte aligned
+    const uint64_t sizes[17] = {C, V, Hv, Hv, C, V, V, E, E, E, F, F, F, E, Hv, Hv, E};
+    uint64_t off[17], total = 0;
+    for (int i = 0; i < 17; ++i) {
+        off[i] = total;
+        total += (sizes[i] + 63) & ~uint64_t(63);
+    }
+    if (int rc = ensure_work(ctx, total * sizeof(float))) return rc;
+    float* ws = static_cast<float*>(ctx->work);
+    float *qkv = ws + off[0], *z = ws + off[1], *beta = ws + off[2], *alpha = ws + off[3], *conv = ws + off[4],
+          *rec = ws + off[5], *gated = ws + off[6], *branch = ws + off[7], *resid = ws + off[8], *post = ws + off[9],
+          *gate = ws + off[10], *up = ws + off[11], *act = ws + off[12], *ffn = ws + off[13], *beta_s = ws + off[14],
+          *log_decay = ws + off[15], *normed = ws + off[16];
+    hipStream_t s = ctx->stream;
+    hipError_t e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s);
+    if (e == hipSuccess) e = block_project(b->qkv, normed, qkv, s);
+    if (e == hipSuccess) e = block_project(b->z, normed, z, s);
+    if (e == hipSuccess) e = block_project(b->beta, normed, beta, s);
+    if (e == hipSuccess) e = block_project(b->alpha, normed, alpha, s);
+    if (e == hipSuccess)
+        e = oq::launch_conv_gates(qkv, b->conv_weight, hist, C, K, beta, alpha, b->dt_bias, b->decay, Hv, conv, beta_s,
+                                  log_decay, s);
+    if (e == hipSuccess)
+        e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, z, b->out_norm, rec, gated, s);
+    if (e == hipSuccess) e = block_project(b->out, gated, branch, s);
+    if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s);
+    if (e == hipSuccess) e = block_project(b->gate, post, gate, s);
+    if (e == hipSuccess) e = block_project(b->up, post, up, s);
+    if (e == hipSuccess) e = oq::launch_swiglu(gate, up, F, act, s);
+    if (e == hipSuccess) e = block_project(b->down, act, ffn, s);
+    if (e == hipSuccess) e = oq::launch_add(resid, ffn, E, y, s);
+    if (e == hipSuccess && trace) {
+        uint64_t t = 0;
+        for (int i = 0; i < 14 && e == hipSuccess; ++i) {
+            e = hipMemcpyAsync(trace + t, ws + off[i], sizes[i] * sizeof(float), hipMemcpyDeviceToDevice, s);
+            t += sizes[i];
+        }
+    }
+    return launch_rc(ctx, e, "deltanet_step");
+}
+
+}  // extern "C"
+
+namespace {
+
 }  // namespace
 
 extern "C" {
@@ -285,6 +407,7 @@ void oq_context_destroy(oq_context* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->work) (void)hipFree(ctx->work);
     if (ctx->t0) (void)hipEventDestroy(ctx->t0);
     if (ctx->t1) (void)hipEventDestroy(ctx->t1);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

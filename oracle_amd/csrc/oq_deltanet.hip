@@ -1,0 +1,241 @@
+// Gated DeltaNet (linear-attention) decode block at batch 1 on gfx950: the elementwise and
+// per-head kernels between the block's quantized projections.
+//
+// The block order is the reference's execute_qwen35_recurrent_block_reference
+// (src/runtime/qwen35_block.cpp:406-605) followed by finish_block (:326-352) and execute_mlp
+// (:296-324); the projections are launched by the C ABI (oq_api.cpp) on the GEMV kernels.
+// Arithmetic follows the reference's: F32 values, double sums of squares, the gated delta
+// rule's memory in F32 key order and its output in double (reference_kernels.cpp:227-335), and
+// no fused multiply-add where the reference multiplies and adds separately.
+#include "oq_common.h"
+
+// The reference multiplies and adds separately (no contraction) everywhere on this path.
+#pragma clang fp contract(off)
+
+namespace oq {
+
+namespace {
+
+constexpr int kNormThreads = 1024;
+constexpr int kMaxKeyDim = 128;    // state column held in registers by one thread
+constexpr int kMaxConvKernel = 16;
+
+// qwen35_block.cpp:138-145
+OQ_DEVICE float sigmoid_ref(float v) {
+    if (v >= 0.0f) {
+        const float e = expf(-v);
+        return 1.0f / (1.0f + e);
+    }
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+
+// qwen35_block.cpp:147-155
+OQ_DEVICE float softplus_ref(float v) {
+    if (v > 20.0f) return v;
+    if (v < -20.0f) return expf(v);
+    return log1pf(expf(v));
+}
+
+OQ_DEVICE float silu_ref(float v) { return v * sigmoid_ref(v); }
+
+OQ_DEVICE double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// sum over the workgroup (blockDim.x a multiple of 64, at most 1024); every thread gets it
+OQ_DEVICE double block_sum_f64(double v, double* lds) {
+    v = wave_sum_f64(v);
+    const int wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds[wave] = v;
+    __syncthreads();
+    double s = 0.0;
+    for (int i = 0; i < waves; ++i) s += lds[i];
+    return s;
+}
+
+// out = rms_norm(a [+ b]) * w over one row of n values (qwen35_block.cpp:161-186); with b the
+// sum a + b is also stored to sum_out (the block's residual, qwen35_block.cpp:334).
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                               const float* __restrict__ w, uint32_t n, float eps,
+                                                               float* __restrict__ sum_out, float* __restrict__ out) {
+    __shared__ double red[16];
+    double ss = 0.0;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = a[i];
+        if (b) {
+            v = v + b[i];
+            sum_out[i] = v;
+        }
+        ss += (double)v * (double)v;
+    }
+    ss = block_sum_f64(ss, red);
+    const float inv = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = b ? sum_out[i] : a[i];
+        out[i] = v * inv * w[i];
+    }
+}
+
+// Causal depthwise convolution step with SiLU (reference_kernels.cpp:197-225 with
+// qwen35_block.cpp:500-503) over `channels` channels of `kernel` taps; the first workgroup
+// also forms the per-head gates: beta_s = sigmoid(beta), log_decay = softplus(alpha + dt_bias)
+// * decay (qwen35_block.cpp:464-494).
+__global__ __launch_bounds__(256) void conv_gates_kernel(const float* __restrict__ qkv, const float* __restrict__ conv_w,
+                                                         float* __restrict__ history, uint32_t channels, uint32_t kernel,
+                                                         const float* __restrict__ beta, const float* __restrict__ alpha,
+                                                         const float* __restrict__ dt_bias,
+                                                         const float* __restrict__ decay, uint32_t heads,
+                                                         float* __restrict__ conv_out, float* __restrict__ beta_s,
+                                                         float* __restrict__ log_decay) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+    if (blockIdx.x == 0) {
+        for (uint32_t h = threadIdx.x; h < heads; h += 256) {
+            beta_s[h] = sigmoid_ref(beta[h]);
+            log_decay[h] = softplus_ref(alpha[h] + dt_bias[h]) * decay[h];
+        }
+    }
+    if (c >= channels) return;
+    float* hst = history + (uint64_t)c * kernel;
+    const float* wc = conv_w + (uint64_t)c * kernel;
+    double sum = 0.0;
+    for (uint32_t i = 0; i < kernel; ++i) {
+        // shift left in place (tap i + 1 is read before it is overwritten), append the input
+        const float t = i + 1 < kernel ? hst[i + 1] : qkv[c];
+        hst[i] = t;
+        sum += (double)t * (double)wc[i];
+    }
+    conv_out[c] = silu_ref((float)sum);
+}
+
+// One value head per workgroup, one value column per thread (blockDim.x = dv): the gated delta
+// rule step (reference_kernels.cpp:227-335) on the state [head][key][value] with the head's
+// query/key taken from key head h % Hk (repeat_heads_tiled, qwen35_block.cpp:233-251), then the
+// head's RMSNorm with weight out_norm gated by SiLU(z) (qwen35_block.cpp:579-588).
+// Thread v keeps state column v (dk <= 128 values) in registers: one read and one write of the
+// state; dv is 64, 128, 192 or 256.
+__global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ conv, uint32_t key_heads, uint32_t dk,
+                                                     uint32_t dv, const float* __restrict__ beta_s,
+                                                     const float* __restrict__ log_decay, float eps,
+                                                     float* __restrict__ state, const float* __restrict__ z,
+                                                     const float* __restrict__ out_norm, float* __restrict__ rec_out,
+                                                     float* __restrict__ gated) {
+    __shared__ float nq[kMaxKeyDim], nk[kMaxKeyDim];
+    __shared__ double red[16];
+    const uint32_t h = blockIdx.x, v = threadIdx.x;
+    const uint32_t kw = key_heads * dk;
+    const float* q = conv + (uint64_t)(h % key_heads) * dk;
+    const float* k = conv + kw + (uint64_t)(h % key_heads) * dk;
+    double qs = 0.0, ks = 0.0;
+    for (uint32_t d = v; d < dk; d += blockDim.x) {
+        qs += (double)q[d] * (double)q[d];
+        ks += (double)k[d] * (double)k[d];
+    }
+    qs = block_sum_f64(qs, red);
+    ks = block_sum_f64(ks, red);
+    const double ql = sqrt(qs), kl = sqrt(ks);
+    const float iq = (float)(1.0 / (ql > (double)eps ? ql : (double)eps));
+    const float ik = (float)(1.0 / (kl > (double)eps ? kl : (double)eps));
+    const float query_scale = 1.0f / sqrtf((float)dk);
+    for (uint32_t d = v; d < dk; d += blockDim.x) {
+        nq[d] = q[d] * iq * query_scale;
+        nk[d] = k[d] * ik;
+    }
+    __syncthreads();
+
+    const float decay = expf(log_decay[h]);
+    const float beta = beta_s[h];
+    float* col = state + (uint64_t)h * dk * dv + v;
+    float s[kMaxKeyDim];
+#pragma unroll
+    for (int d = 0; d < kMaxKeyDim; ++d)
+        if ((uint32_t)d < dk) s[d] = col[(uint64_t)d * dv];
+    float mem = 0.0f;
+#pragma unroll
+    for (int d = 0; d < kMaxKeyDim; ++d) {
+        if ((uint32_t)d < dk) {
+            s[d] = s[d] * decay;
+            mem = mem + s[d] * nk[d];
+        }
+    }
+    const float vv = conv[2u * kw + (uint64_t)h * dv + v];
+    double o = 0.0;
+    const float delta = (vv - mem) * beta;
+#pragma unroll
+    for (int d = 0; d < kMaxKeyDim; ++d) {
+        if ((uint32_t)d < dk) {
+            s[d] = s[d] + nk[d] * delta;
+            col[(uint64_t)d * dv] = s[d];
+            o = o + (double)s[d] * (double)nq[d];
+        }
+    }
+    const float of = (float)o;
+    rec_out[(uint64_t)h * dv + v] = of;
+    const double ss = block_sum_f64((double)of * (double)of, red);
+    const float inv = (float)(1.0 / sqrt(ss / (double)dv + (double)eps));
+    const float g = silu_ref(z[(uint64_t)h * dv + v]);
+    gated[(uint64_t)h * dv + v] = of * inv * out_norm[v] * g;
+}
+
+// act = silu(gate) * up (qwen35_block.cpp:313-316)
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                                     uint32_t n, float* __restrict__ act) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    act[i] = silu_ref(gate[i]) * up[i];
+}
+
+// out = a + b (qwen35_block.cpp:188-198)
+__global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ a, const float* __restrict__ b, uint32_t n,
+                                                  float* __restrict__ out) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+unsigned blocks_of(uint64_t n, unsigned t) { return (unsigned)((n + t - 1) / t); }
+
+}  // namespace
+
+bool deltanet_dims_supported(uint64_t key_dim, uint64_t value_dim, uint64_t conv_kernel) {
+    return key_dim >= 1 && key_dim <= kMaxKeyDim && value_dim >= 64 && value_dim <= 256 && value_dim % 64 == 0 &&
+           conv_kernel >= 1 && conv_kernel <= kMaxConvKernel;
+}
+
+hipError_t launch_rmsnorm(const float* a, const float* b, const float* w, uint64_t n, float eps, float* sum_out,
+                          float* out, hipStream_t s) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, s, a, b, w, (uint32_t)n, eps, sum_out, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv_gates(const float* qkv, const float* conv_w, float* history, uint64_t channels,
+                             uint64_t kernel, const float* beta, const float* alpha, const float* dt_bias,
+                             const float* decay, uint64_t heads, float* conv_out, float* beta_s, float* log_decay,
+                             hipStream_t s) {
+    hipLaunchKernelGGL(conv_gates_kernel, dim3(blocks_of(channels, 256)), dim3(256), 0, s, qkv, conv_w, history,
+                       (uint32_t)channels, (uint32_t)kernel, beta, alpha, dt_bias, decay, (uint32_t)heads, conv_out,
+                       beta_s, log_decay);
+    return hipGetLastError();
+}
+
+hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_heads, uint64_t dk, uint64_t dv,
+                        const float* beta_s, const float* log_decay, float eps, float* state, const float* z,
+                        const float* out_norm, float* rec_out, float* gated, hipStream_t s) {
+    hipLaunchKernelGGL(delta_kernel, dim3((unsigned)value_heads), dim3((unsigned)dv), 0, s, conv, (uint32_t)key_heads,
+                       (uint32_t)dk, (uint32_t)dv, beta_s, log_decay, eps, state, z, out_norm, rec_out, gated);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s) {
+    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_of(n, 256)), dim3(256), 0, s, gate, up, (uint32_t)n, act);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(const float* a, const float* b, uint64_t n, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(add_kernel, dim3(blocks_of(n, 256)), dim3(256), 0, s, a, b, (uint32_t)n, out);
+    return hipGetLastError();
+}
+
+}  // namespace oq

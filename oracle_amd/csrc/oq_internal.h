@@ -62,4 +62,18 @@ uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m);  // planar Q8_K image
 hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
                                 void* scratch, hipStream_t s);
 
+// ---- oq_deltanet.hip  (Gated DeltaNet decode block: kernels between the projections)
+bool deltanet_dims_supported(uint64_t key_dim, uint64_t value_dim, uint64_t conv_kernel);
+hipError_t launch_rmsnorm(const float* a, const float* b, const float* w, uint64_t n, float eps, float* sum_out,
+                          float* out, hipStream_t s);
+hipError_t launch_conv_gates(const float* qkv, const float* conv_w, float* history, uint64_t channels,
+                             uint64_t kernel, const float* beta, const float* alpha, const float* dt_bias,
+                             const float* decay, uint64_t heads, float* conv_out, float* beta_s, float* log_decay,
+                             hipStream_t s);
+hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_heads, uint64_t dk, uint64_t dv,
+                        const float* beta_s, const float* log_decay, float eps, float* state, const float* z,
+                        const float* out_norm, float* rec_out, float* gated, hipStream_t s);
+hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s);
+hipError_t launch_add(const float* a, const float* b, uint64_t n, float* out, hipStream_t s);
+
 }  // namespace oq

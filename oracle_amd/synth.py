@@ -95,3 +95,35 @@ def activations(rng: np.random.Generator, m: int, k: int) -> np.ndarray:
 def row_bytes(type_id: int, cols: int) -> int:
     per = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34)}[type_id]
     return cols // per[0] * per[1]
+
+
+# Gated DeltaNet decode block (Qwen3.5-style recurrent layer, batch 1).  Projections use the
+# distributions above (q/k/v/z/beta/alpha and the FFN in q4_K, the output projection in q6_K);
+# the recurrent state is F32 ~ N(0, 0.01) (standard deviation), the convolution history and
+# input x ~ N(0, 1); norm weights 1 + N(0, 0.1); conv taps N(0, 0.5); dt_bias ~ N(0, 1);
+# decay = -exp(N(0, 0.5)) < 0, so every head's state decay exp(softplus(.) * decay) is in (0, 1).
+DELTANET_DIMS = {"embedding": 4096, "key_heads": 32, "value_heads": 32, "key_dim": 128, "value_dim": 128,
+                 "conv_kernel": 4, "ffn": 12288, "eps": 1e-6}
+
+
+def deltanet_block(rng: np.random.Generator, dims: dict | None = None):
+    """(dims, weights {name: (type, bytes)}, vectors {name: F32}, conv_history, state, x)."""
+    d = dict(DELTANET_DIMS if dims is None else dims)
+    E, F = d["embedding"], d["ffn"]
+    Hk, Hv, dk, dv, K = d["key_heads"], d["value_heads"], d["key_dim"], d["value_dim"], d["conv_kernel"]
+    C, V = 2 * Hk * dk + Hv * dv, Hv * dv
+    shapes = {"qkv": (Q4_K, C, E), "z": (Q4_K, V, E), "beta": (Q4_K, Hv, E), "alpha": (Q4_K, Hv, E),
+              "out": (Q6_K, E, V), "gate": (Q4_K, F, E), "up": (Q4_K, F, E), "down": (Q4_K, E, F)}
+    w = {n: (t, weights(t, rng, rows, cols)) for n, (t, rows, cols) in shapes.items()}
+    vec = {
+        "input_norm": (1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32),
+        "conv_weight": (0.5 * rng.standard_normal(C * K)).astype(np.float32),
+        "dt_bias": rng.standard_normal(Hv).astype(np.float32),
+        "decay": (-np.exp(0.5 * rng.standard_normal(Hv))).astype(np.float32),
+        "out_norm": (1.0 + 0.1 * rng.standard_normal(dv)).astype(np.float32),
+        "post_norm": (1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32),
+    }
+    conv_history = rng.standard_normal((C, K)).astype(np.float32)
+    state = (0.01 * rng.standard_normal((Hv, dk, dv))).astype(np.float32)
+    x = rng.standard_normal(E).astype(np.float32)
+    return d, w, vec, conv_history, state, x

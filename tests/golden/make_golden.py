@@ -8,6 +8,10 @@
    reference decoder; its vectors are the reference's Q5_K results on the same blocks with an
    all-zero fifth-bit plane, which GGML's Q4_K format must reproduce exactly.
 
+3. ref_deltanet.npz -- seeded random inputs run through the reference's own causal depthwise
+   convolution step and gated delta rule step (src/runtime/reference_kernels.cpp:197-335,
+   compiled into the same library), several steps in a row with the state carried.
+
 Run from the repository root after `make -C oracle all ref`:  python tests/golden/make_golden.py
 """
 from __future__ import annotations
@@ -57,6 +61,14 @@ def kat() -> dict:
         "q8_0": {"block": hexs(q8), "expected": q8_quants, "dot_ones": 14.0},
         "q8_0_two_blocks": {"blocks": hexs(q8 + q8_second), "at3": 127.0, "at32": 5.0, "at63": 5.0},
         "q8_0_matvec": {"rows": [hexs(q8), hexs(q8_second_row)], "expected": [14.0, 64.0]},
+        # reference tests/test_phase1e.cpp:188-245 and tests/test_phase2c.cpp:265-285
+        "ssm": {"conv": {"taps": [1.0, 2.0, 3.0], "inputs": [1.0, 2.0], "expected": [3.0, 8.0]},
+                "delta": {"q": [1.0, 0.0], "k": [1.0, 0.0], "v": [2.0],
+                          "steps": [{"beta": 0.5, "log_decay": 0.0, "expected": 0.7071067811865476, "tol": 2e-6},
+                                    {"beta": 1.0, "log_decay_of": 0.5, "expected": 1.4142135623730951, "tol": 3e-6}],
+                          "eps": 1e-12},
+                "delta_eps": {"q": [1e-4, 0.0], "k": [1e-4, 0.0], "v": [2.0], "beta": 1.0, "log_decay": 0.0,
+                              "eps": 1e-6, "expected": 1.4142135623730951, "tol": 2e-6}},
     }
 
 
@@ -113,12 +125,42 @@ def random_vectors() -> dict[str, np.ndarray]:
     return out
 
 
+def deltanet_vectors() -> dict[str, np.ndarray]:
+    rng = np.random.default_rng(20261202)
+    out: dict[str, np.ndarray] = {}
+    channels, kernel, steps = 24, 4, 3
+    hist = rng.standard_normal((channels, kernel)).astype(np.float32)
+    taps = rng.standard_normal(channels * kernel).astype(np.float32)
+    out["conv_taps"] = taps
+    out["conv_history0"] = hist.copy()
+    xs = rng.standard_normal((steps, channels)).astype(np.float32)
+    out["conv_inputs"] = xs
+    outs = [oracle.ref_conv_step(hist, taps, xs[i]) for i in range(steps)]
+    out["conv_outputs_bits"] = np.stack(outs).view(np.uint32)
+    out["conv_history_bits"] = hist.view(np.uint32)
+    heads, dk, dv = 3, 16, 8
+    state = (0.1 * rng.standard_normal((heads, dk, dv))).astype(np.float32)
+    out["delta_state0"] = state.copy()
+    q = rng.standard_normal((steps, heads, dk)).astype(np.float32)
+    k = rng.standard_normal((steps, heads, dk)).astype(np.float32)
+    v = rng.standard_normal((steps, heads, dv)).astype(np.float32)
+    beta = rng.uniform(0.0, 1.0, (steps, heads)).astype(np.float32)
+    log_decay = (-rng.uniform(0.0, 2.0, (steps, heads))).astype(np.float32)
+    for n, a in (("q", q), ("k", k), ("v", v), ("beta", beta), ("log_decay", log_decay)):
+        out[f"delta_{n}"] = a
+    outs = [oracle.ref_gated_delta_step(q[i], k[i], v[i], beta[i], log_decay[i], state, 1e-6) for i in range(steps)]
+    out["delta_outputs_bits"] = np.stack(outs).view(np.uint32)
+    out["delta_state_bits"] = state.view(np.uint32)
+    return out
+
+
 def main() -> None:
     if not oracle.ref_available():
         raise SystemExit("oracle/_ref/libref.so is not built: run `make -C oracle ref` first")
     (OUT / "ref_kat.json").write_text(json.dumps(kat(), indent=1) + "\n")
     np.savez_compressed(OUT / "ref_random.npz", **random_vectors())
-    print("wrote", OUT / "ref_kat.json", OUT / "ref_random.npz")
+    np.savez_compressed(OUT / "ref_deltanet.npz", **deltanet_vectors())
+    print("wrote", OUT / "ref_kat.json", OUT / "ref_random.npz", OUT / "ref_deltanet.npz")
 
 
 if __name__ == "__main__":

@@ -1,0 +1,193 @@
+"""Pins of the oracle's Gated DeltaNet block restatement (oracle/oracle.c), CPU only.
+
+- the reference's own known answers for the convolution and the delta rule
+  (reference tests/test_phase1e.cpp:188-245, tests/test_phase2c.cpp:265-285);
+- bit-for-bit equality with the reference's compiled kernels (reference_kernels.cpp:197-335)
+  on seeded random multi-step inputs, through the committed fixtures (tests/golden/
+  ref_deltanet.npz) and, where oracle/_ref is built, live;
+- closed forms of sigmoid / softplus / SiLU / RMSNorm and the delta rule;
+- block-level invariants of the restated block order (qwen35_block.cpp:406-605).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle_amd import synth
+
+GOLDEN_DN = "ref_deltanet.npz"
+
+
+@pytest.fixture(scope="module")
+def dn_golden():
+    from conftest import GOLDEN
+    with np.load(GOLDEN / GOLDEN_DN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def test_conv_known_answers(kat):
+    c = kat["ssm"]["conv"]
+    hist = np.zeros((1, len(c["taps"])), np.float32)
+    outs = [float(oracle.conv_step(hist, np.array(c["taps"], np.float32), np.array([x], np.float32))[0])
+            for x in c["inputs"]]
+    assert outs == c["expected"]
+
+
+def test_delta_known_answers(kat):
+    d = kat["ssm"]["delta"]
+    state = np.zeros((1, 2, 1), np.float32)
+    q, k, v = (np.array([d[n]], np.float32) for n in ("q", "k", "v"))
+    for st in d["steps"]:
+        ld = st["log_decay"] if "log_decay" in st else math.log(st["log_decay_of"])
+        out = oracle.gated_delta_step(q, k, v, [st["beta"]], [np.float32(ld)], state, d["eps"])
+        assert abs(float(out[0, 0]) - st["expected"]) <= st["tol"]
+    e = kat["ssm"]["delta_eps"]
+    state = np.zeros((1, 2, 1), np.float32)
+    out = oracle.gated_delta_step(np.array([e["q"]], np.float32), np.array([e["k"]], np.float32),
+                                  np.array([e["v"]], np.float32), [e["beta"]], [e["log_decay"]], state, e["eps"])
+    assert abs(float(out[0, 0]) - e["expected"]) <= e["tol"]
+
+
+def test_conv_matches_reference_fixtures(dn_golden):
+    g = dn_golden
+    hist = g["conv_history0"].copy()
+    outs = np.stack([oracle.conv_step(hist, g["conv_taps"], x) for x in g["conv_inputs"]])
+    assert np.array_equal(outs.view(np.uint32), g["conv_outputs_bits"])
+    assert np.array_equal(hist.view(np.uint32), g["conv_history_bits"])
+
+
+def test_delta_matches_reference_fixtures(dn_golden):
+    g = dn_golden
+    state = g["delta_state0"].copy()
+    outs = np.stack([oracle.gated_delta_step(g["delta_q"][i], g["delta_k"][i], g["delta_v"][i], g["delta_beta"][i],
+                                             g["delta_log_decay"][i], state, 1e-6)
+                     for i in range(g["delta_q"].shape[0])])
+    assert np.array_equal(outs.view(np.uint32), g["delta_outputs_bits"])
+    assert np.array_equal(state.view(np.uint32), g["delta_state_bits"])
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="compiled reference (oracle/_ref) not built here")
+def test_delta_and_conv_match_live_reference():
+    rng = np.random.default_rng(7)
+    heads, dk, dv = 4, 128, 128
+    s1 = (0.01 * rng.standard_normal((heads, dk, dv))).astype(np.float32)
+    s2 = s1.copy()
+    for _ in range(2):
+        q, k = rng.standard_normal((2, heads, dk)).astype(np.float32)
+        v = rng.standard_normal((heads, dv)).astype(np.float32)
+        beta = rng.uniform(0, 1, heads).astype(np.float32)
+        ld = (-rng.uniform(0, 3, heads)).astype(np.float32)
+        a = oracle.gated_delta_step(q, k, v, beta, ld, s1, 1e-6)
+        b = oracle.ref_gated_delta_step(q, k, v, beta, ld, s2, 1e-6)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+    h1 = rng.standard_normal((64, 4)).astype(np.float32)
+    h2 = h1.copy()
+    taps = rng.standard_normal(256).astype(np.float32)
+    x = rng.standard_normal(64).astype(np.float32)
+    for silu in (False, True):
+        assert np.array_equal(oracle.conv_step(h1, taps, x, silu), oracle.ref_conv_step(h2, taps, x, silu))
+    assert np.array_equal(h1, h2)
+
+
+def test_activation_closed_forms():
+    assert oracle.sigmoid(0.0) == 0.5
+    assert oracle.silu(0.0) == 0.0
+    assert abs(oracle.softplus(0.0) - math.log(2.0)) < 1e-7
+    assert oracle.softplus(25.0) == 25.0          # identity above 20
+    assert oracle.softplus(-25.0) == np.float32(math.exp(-25.0))  # exp below -20
+    for v in (-30.0, -3.0, -0.5, 0.5, 3.0, 30.0):
+        assert abs(oracle.sigmoid(v) - 1.0 / (1.0 + math.exp(-v))) < 1e-7
+        assert abs(oracle.sigmoid(v) + oracle.sigmoid(-v) - 1.0) < 1e-7
+        assert abs(oracle.silu(v) - v / (1.0 + math.exp(-v))) < 1e-6 * max(1.0, abs(v))
+
+
+def test_rms_norm_closed_form():
+    # a constant row c: inverse_rms = 1 / sqrt(c^2 + eps); rows are normalised independently
+    x = np.array([3.0] * 8 + [-2.0] * 8, np.float32)
+    w = np.linspace(0.5, 2.0, 8).astype(np.float32)
+    out = oracle.rms_norm_rows(x, w, 8, 1e-6).reshape(2, 8)
+    for r, c in enumerate((3.0, -2.0)):
+        inv = np.float32(1.0 / math.sqrt(c * c + 1e-6))
+        assert np.array_equal(out[r], (np.float32(c) * inv) * w)
+
+
+def test_delta_rule_closed_forms():
+    rng = np.random.default_rng(3)
+    heads, dk, dv = 2, 8, 4
+    # beta = 0: the state only decays, out = (decay * S)^T q_hat
+    s = rng.standard_normal((heads, dk, dv)).astype(np.float32)
+    s0 = s.copy()
+    q, k = rng.standard_normal((2, heads, dk)).astype(np.float32)
+    v = rng.standard_normal((heads, dv)).astype(np.float32)
+    ld = np.array([-0.5, -1.5], np.float32)
+    out = oracle.gated_delta_step(q, k, v, [0.0, 0.0], ld, s, 1e-6)
+    dec = np.exp(ld.astype(np.float64))[:, None, None]
+    assert np.allclose(s, s0 * dec, rtol=1e-6, atol=0)
+    qh = q / np.linalg.norm(q, axis=1, keepdims=True) / math.sqrt(dk)
+    assert np.allclose(out, np.einsum("hkv,hk->hv", s.astype(np.float64), qh), rtol=1e-5, atol=1e-6)
+    # zero state, no decay, beta = 1: S = k_hat (x) v, out = (k_hat . q_hat) v
+    s = np.zeros((heads, dk, dv), np.float32)
+    out = oracle.gated_delta_step(q, k, v, [1.0, 1.0], [0.0, 0.0], s, 1e-6)
+    kh = k / np.linalg.norm(k, axis=1, keepdims=True)
+    assert np.allclose(s, np.einsum("hk,hv->hkv", kh, v), rtol=1e-5, atol=1e-6)
+    assert np.allclose(out, np.sum(kh * qh, axis=1)[:, None] * v, rtol=1e-5, atol=1e-6)
+    # invalid beta / decay are rejected as the reference does
+    with pytest.raises(oracle.OracleError):
+        oracle.gated_delta_step(q, k, v, [1.5, 0.0], [0.0, 0.0], s, 1e-6)
+    with pytest.raises(oracle.OracleError):
+        oracle.gated_delta_step(q, k, v, [0.5, 0.5], [float("inf"), 0.0], s, 1e-6)
+
+
+SMALL = dict(synth.DELTANET_DIMS, embedding=512, key_heads=2, value_heads=4, ffn=512)
+
+
+def test_block_residual_wiring():
+    # with zero output and down projections the block is the identity on x (both residual adds),
+    # while the state and the convolution history still advance
+    d, w, vec, hist, st, x = synth.deltanet_block(np.random.default_rng(11), SMALL)
+    for n in ("out", "down"):
+        w[n] = (w[n][0], np.zeros_like(w[n][1]))
+    st0, h0 = st.copy(), hist.copy()
+    y, tr = oracle.deltanet_step(d, w, vec, hist, st, x, threads=2, trace=True)
+    assert np.array_equal(y, x)
+    assert np.array_equal(tr["branch"], np.zeros(d["embedding"], np.float32))
+    assert not np.array_equal(st, st0) and np.array_equal(hist[:, :-1], h0[:, 1:])
+    assert np.array_equal(hist[:, -1], tr["qkv"])
+
+
+def test_block_stages_follow_reference_order():
+    # every stage of the restated block, recomputed from the previous stage's traced values with
+    # the separately pinned pieces (projection semantics, conv, delta rule, norms)
+    d, w, vec, hist, st, x = synth.deltanet_block(np.random.default_rng(12), SMALL)
+    h0, s0 = hist.copy(), st.copy()
+    y, tr = oracle.deltanet_step(d, w, vec, hist, st, x, threads=2, trace=True)
+    E, Hk, Hv, dk, dv = (d[k] for k in ("embedding", "key_heads", "value_heads", "key_dim", "value_dim"))
+    eps = d["eps"]
+
+    def proj(name, inp, rows, cols):
+        t, data = w[name]
+        xhat = oracle.dequantize_q8k(oracle.quantize_q8k(inp), cols)
+        return oracle.storage_matvec(t, rows, cols, data, xhat, threads=2)
+
+    normed = oracle.rms_norm_rows(x, vec["input_norm"], E, eps)
+    C_, V = 2 * Hk * dk + Hv * dv, Hv * dv
+    assert np.array_equal(tr["qkv"], proj("qkv", normed, C_, E))
+    assert np.array_equal(tr["z"], proj("z", normed, V, E))
+    conv = oracle.conv_step(h0, vec["conv_weight"], tr["qkv"], apply_silu=True)
+    assert np.array_equal(tr["conv"], conv)
+    q = np.stack([conv[(t % Hk) * dk:(t % Hk + 1) * dk] for t in range(Hv)])
+    k = np.stack([conv[Hk * dk + (t % Hk) * dk:Hk * dk + (t % Hk + 1) * dk] for t in range(Hv)])
+    beta = np.array([oracle.sigmoid(b) for b in tr["beta"]], np.float32)
+    ld = np.array([np.float32(oracle.softplus(float(np.float32(a + b)))) * c
+                   for a, b, c in zip(tr["alpha"], vec["dt_bias"], vec["decay"])], np.float32)
+    rec = oracle.gated_delta_step(q, k, conv[2 * Hk * dk:].reshape(Hv, dv), beta, ld, s0, eps).reshape(-1)
+    assert np.array_equal(tr["rec"], rec) and np.array_equal(st, s0)
+    g = oracle.rms_norm_rows(rec, vec["out_norm"], dv, eps) * np.array([oracle.silu(v) for v in tr["z"]], np.float32)
+    assert np.array_equal(tr["gated"], g)
+    assert np.array_equal(tr["resid"], x + tr["branch"])
+    assert np.array_equal(tr["post"], oracle.rms_norm_rows(tr["resid"], vec["post_norm"], E, eps))
+    act = np.array([oracle.silu(a) for a in tr["gate"]], np.float32) * tr["up"]
+    assert np.array_equal(tr["act"], act)
+    assert np.array_equal(y, tr["resid"] + tr["ffn"])
