@@ -39,6 +39,7 @@ WORKLOADS = {
     "q4k_gemv": (12, 12288, 4096, 1, "Q4_K FFN gate/up decode GEMV 12288x4096, batch 1, Q8_K activations"),
     "q8_0_gemv": (8, 4096, 4096, 1, "Q8_0 GEMV 4096x4096, batch 1, F32 activations"),
     "q6k_head": (14, 151936, 4096, 1, "Q6_K output-head GEMV 151936x4096, batch 1, Q8_K activations"),
+    "q4k_down_m1": (12, 4096, 12288, 1, "Q4_K down-projection GEMV 4096x12288, batch 1, Q8_K activations"),
     "q4k_down_m4": (12, 4096, 12288, 4, "Q4_K down-projection GEMM 4096x12288, M=4, Q8_K activations"),
     "q4k_down_m512": (12, 4096, 12288, 512, "Q4_K down-projection GEMM 4096x12288, M=512, Q8_K activations"),
 }

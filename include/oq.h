@@ -165,7 +165,7 @@ int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q
    not NULL, receives the intermediates in this order (F32, packed):
      qkv[C] z[Hv*dv] beta[Hv] alpha[Hv] conv[C] out[Hv*dv] gated[Hv*dv] branch[E] resid[E]
      post[E] gate[F] up[F] act[F] ffn[E]       with C = 2*Hk*dk + Hv*dv.
-   Device path limits: dk <= 128, dv in {64, 128, 192, 256}, conv_kernel <= 16, K-quant rows
+   Device path limits: dk in {32, 64, 128}, dv in {64, 128, 192, 256}, conv_kernel <= 16, K-quant rows
    <= 16384; otherwise OQ_INVALID_ARGUMENT.  Weight shape mismatches -> OQ_INVALID_ARGUMENT. */
 typedef struct oq_deltanet_block {
     uint64_t embedding;   /* E */

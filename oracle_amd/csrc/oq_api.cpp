@@ -288,7 +288,7 @@ int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, f
     }
     if (!oq::deltanet_dims_supported(dk, dv, K)) {
         return fail(ctx, OQ_INVALID_ARGUMENT,
-                    "DeltaNet block device path needs key_dim <= 128, value_dim in {64,128,192,256}, conv_kernel <= 16");
+                    "DeltaNet block device path needs key_dim in {32,64,128}, value_dim in {64,128,192,256}, conv_kernel <= 16");
     }
     if (E > 0x7FFFFFFF || F > 0x7FFFFFFF || Hv * dv > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "block too large");
     const uint64_t V = Hv * dv, C = 2 * Hk * dk + V;

@@ -17,7 +17,6 @@ namespace oq {
 namespace {
 
 constexpr int kNormThreads = 1024;
-constexpr int kMaxKeyDim = 128;    // state column held in registers by one thread
 constexpr int kMaxConvKernel = 16;
 
 // qwen35_block.cpp:138-145
@@ -115,22 +114,29 @@ __global__ __launch_bounds__(256) void conv_gates_kernel(const float* __restrict
 // rule step (reference_kernels.cpp:227-335) on the state [head][key][value] with the head's
 // query/key taken from key head h % Hk (repeat_heads_tiled, qwen35_block.cpp:233-251), then the
 // head's RMSNorm with weight out_norm gated by SiLU(z) (qwen35_block.cpp:579-588).
-// Thread v keeps state column v (dk <= 128 values) in registers: one read and one write of the
-// state; dv is 64, 128, 192 or 256.
-__global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ conv, uint32_t key_heads, uint32_t dk,
-                                                     uint32_t dv, const float* __restrict__ beta_s,
-                                                     const float* __restrict__ log_decay, float eps,
-                                                     float* __restrict__ state, const float* __restrict__ z,
-                                                     const float* __restrict__ out_norm, float* __restrict__ rec_out,
-                                                     float* __restrict__ gated) {
-    __shared__ float nq[kMaxKeyDim], nk[kMaxKeyDim];
+// Thread v keeps state column v (DK values) in registers: the DK loads are issued together, then
+// the column is decayed and reduced in key order, updated, stored and reduced again: one read
+// and one write of the state.  dv is 64, 128, 192 or 256.
+template <int DK>
+__global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ conv, uint32_t key_heads, uint32_t dv,
+                                                    const float* __restrict__ beta_s, const float* __restrict__ log_decay,
+                                                    float eps, float* __restrict__ state, const float* __restrict__ z,
+                                                    const float* __restrict__ out_norm, float* __restrict__ rec_out,
+                                                    float* __restrict__ gated) {
+    __shared__ __align__(16) float nq[DK];
+    __shared__ __align__(16) float nk[DK];
     __shared__ double red[16];
     const uint32_t h = blockIdx.x, v = threadIdx.x;
-    const uint32_t kw = key_heads * dk;
-    const float* q = conv + (uint64_t)(h % key_heads) * dk;
-    const float* k = conv + kw + (uint64_t)(h % key_heads) * dk;
+    float* col = state + (uint64_t)h * DK * dv + v;
+    float s[DK];
+#pragma unroll
+    for (int d = 0; d < DK; ++d) s[d] = col[(uint64_t)d * dv];
+
+    const uint32_t kw = key_heads * DK;
+    const float* q = conv + (uint64_t)(h % key_heads) * DK;
+    const float* k = conv + kw + (uint64_t)(h % key_heads) * DK;
     double qs = 0.0, ks = 0.0;
-    for (uint32_t d = v; d < dk; d += blockDim.x) {
+    for (uint32_t d = v; d < DK; d += blockDim.x) {
         qs += (double)q[d] * (double)q[d];
         ks += (double)k[d] * (double)k[d];
     }
@@ -139,8 +145,8 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
     const double ql = sqrt(qs), kl = sqrt(ks);
     const float iq = (float)(1.0 / (ql > (double)eps ? ql : (double)eps));
     const float ik = (float)(1.0 / (kl > (double)eps ? kl : (double)eps));
-    const float query_scale = 1.0f / sqrtf((float)dk);
-    for (uint32_t d = v; d < dk; d += blockDim.x) {
+    const float query_scale = 1.0f / sqrtf((float)DK);
+    for (uint32_t d = v; d < DK; d += blockDim.x) {
         nq[d] = q[d] * iq * query_scale;
         nk[d] = k[d] * ik;
     }
@@ -148,28 +154,35 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
 
     const float decay = expf(log_decay[h]);
     const float beta = beta_s[h];
-    float* col = state + (uint64_t)h * dk * dv + v;
-    float s[kMaxKeyDim];
-#pragma unroll
-    for (int d = 0; d < kMaxKeyDim; ++d)
-        if ((uint32_t)d < dk) s[d] = col[(uint64_t)d * dv];
+    const float4* nk4 = reinterpret_cast<const float4*>(nk);
+    const float4* nq4 = reinterpret_cast<const float4*>(nq);
+    // the empty asm statements keep each chunk's LDS reads next to their use, so the unrolled
+    // loops hold the state column and only four keys in registers
     float mem = 0.0f;
 #pragma unroll
-    for (int d = 0; d < kMaxKeyDim; ++d) {
-        if ((uint32_t)d < dk) {
-            s[d] = s[d] * decay;
-            mem = mem + s[d] * nk[d];
+    for (int d = 0; d < DK; d += 4) {
+        asm volatile("" ::: "memory");
+        const float4 kk = nk4[d / 4];
+        const float kv[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s[d + i] = s[d + i] * decay;
+            mem = mem + s[d + i] * kv[i];
         }
     }
     const float vv = conv[2u * kw + (uint64_t)h * dv + v];
-    double o = 0.0;
     const float delta = (vv - mem) * beta;
+    double o = 0.0;
 #pragma unroll
-    for (int d = 0; d < kMaxKeyDim; ++d) {
-        if ((uint32_t)d < dk) {
-            s[d] = s[d] + nk[d] * delta;
-            col[(uint64_t)d * dv] = s[d];
-            o = o + (double)s[d] * (double)nq[d];
+    for (int d = 0; d < DK; d += 4) {
+        asm volatile("" ::: "memory");
+        const float4 kk = nk4[d / 4], qq = nq4[d / 4];
+        const float kv[4] = {kk.x, kk.y, kk.z, kk.w}, qv[4] = {qq.x, qq.y, qq.z, qq.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s[d + i] = s[d + i] + kv[i] * delta;
+            col[(uint64_t)(d + i) * dv] = s[d + i];
+            o = o + (double)s[d + i] * (double)qv[i];
         }
     }
     const float of = (float)o;
@@ -200,7 +213,8 @@ unsigned blocks_of(uint64_t n, unsigned t) { return (unsigned)((n + t - 1) / t);
 }  // namespace
 
 bool deltanet_dims_supported(uint64_t key_dim, uint64_t value_dim, uint64_t conv_kernel) {
-    return key_dim >= 1 && key_dim <= kMaxKeyDim && value_dim >= 64 && value_dim <= 256 && value_dim % 64 == 0 &&
+    return (key_dim == 32 || key_dim == 64 || key_dim == 128) && value_dim >= 64 && value_dim <= 256 &&
+           value_dim % 64 == 0 &&
            conv_kernel >= 1 && conv_kernel <= kMaxConvKernel;
 }
 
@@ -223,8 +237,23 @@ hipError_t launch_conv_gates(const float* qkv, const float* conv_w, float* histo
 hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_heads, uint64_t dk, uint64_t dv,
                         const float* beta_s, const float* log_decay, float eps, float* state, const float* z,
                         const float* out_norm, float* rec_out, float* gated, hipStream_t s) {
-    hipLaunchKernelGGL(delta_kernel, dim3((unsigned)value_heads), dim3((unsigned)dv), 0, s, conv, (uint32_t)key_heads,
-                       (uint32_t)dk, (uint32_t)dv, beta_s, log_decay, eps, state, z, out_norm, rec_out, gated);
+    const dim3 grid((unsigned)value_heads), block((unsigned)dv);
+    switch (dk) {
+        case 32:
+            hipLaunchKernelGGL(delta_kernel<32>, grid, block, 0, s, conv, (uint32_t)key_heads, (uint32_t)dv, beta_s,
+                               log_decay, eps, state, z, out_norm, rec_out, gated);
+            break;
+        case 64:
+            hipLaunchKernelGGL(delta_kernel<64>, grid, block, 0, s, conv, (uint32_t)key_heads, (uint32_t)dv, beta_s,
+                               log_decay, eps, state, z, out_norm, rec_out, gated);
+            break;
+        case 128:
+            hipLaunchKernelGGL(delta_kernel<128>, grid, block, 0, s, conv, (uint32_t)key_heads, (uint32_t)dv, beta_s,
+                               log_decay, eps, state, z, out_norm, rec_out, gated);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -459,21 +459,42 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kq_kernel(DeviceMatrix w, int
 
 // ---------------------------------------------------------------- launch
 
-template <uint32_t TYPE, int ITERS, int R, int MT, bool FUSED, int WAVES>
-hipError_t launch_one(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+// Workgroups resident per CU for this instantiation (register and LDS limits), cached.
+template <uint32_t TYPE, int ITERS, int R, int MT, bool FUSED, int WAVES, bool FULL>
+int resident_per_cu(uint64_t lds_bytes) {
+    static int cached = 0;
+    if (cached == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_kq_kernel<TYPE, ITERS, R, MT, FUSED, WAVES, FULL>,
+                                                         64 * WAVES, lds_bytes) != hipSuccess || n < 1) {
+            n = 1;
+        }
+        cached = n;
+    }
+    return cached;
+}
+
+template <uint32_t TYPE, int ITERS, int R, int MT, bool FUSED, int WAVES, bool FULL>
+hipError_t launch_full(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
     const uint64_t groups = (w.n + R - 1) / R;
-    const int wg_per_cu = env_int("OQ_GEMV_WG_PER_CU", 2);
-    uint64_t wgs = (uint64_t)cu_count() * (uint64_t)(wg_per_cu > 0 ? wg_per_cu : 1);
+    const uint64_t lds = act_lds_bytes(w.k, MT);
+    // two workgroups per CU where both fit (more would only repeat the activation staging)
+    int wg_per_cu = env_int("OQ_GEMV_WG_PER_CU", 2);
+    if (wg_per_cu < 1) wg_per_cu = 1;
+    const int resident = resident_per_cu<TYPE, ITERS, R, MT, FUSED, WAVES, FULL>(lds);
+    if (wg_per_cu > resident) wg_per_cu = resident;
+    uint64_t wgs = (uint64_t)cu_count() * (uint64_t)wg_per_cu;
     const uint64_t need = (groups + WAVES - 1) / WAVES;
     if (wgs > need) wgs = need;
-    if ((w.k / kQK) % 16 == 0) {
-        hipLaunchKernelGGL((gemv_kq_kernel<TYPE, ITERS, R, MT, FUSED, WAVES, true>), dim3((unsigned)wgs),
-                           dim3(64 * WAVES), act_lds_bytes(w.k, MT), s, w, m, x, q8k, y);
-    } else {
-        hipLaunchKernelGGL((gemv_kq_kernel<TYPE, ITERS, R, MT, FUSED, WAVES, false>), dim3((unsigned)wgs),
-                           dim3(64 * WAVES), act_lds_bytes(w.k, MT), s, w, m, x, q8k, y);
-    }
+    hipLaunchKernelGGL((gemv_kq_kernel<TYPE, ITERS, R, MT, FUSED, WAVES, FULL>), dim3((unsigned)wgs), dim3(64 * WAVES),
+                       lds, s, w, m, x, q8k, y);
     return hipGetLastError();
+}
+
+template <uint32_t TYPE, int ITERS, int R, int MT, bool FUSED, int WAVES>
+hipError_t launch_one(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+    if ((w.k / kQK) % 16 == 0) return launch_full<TYPE, ITERS, R, MT, FUSED, WAVES, true>(w, m, x, q8k, y, s);
+    return launch_full<TYPE, ITERS, R, MT, FUSED, WAVES, false>(w, m, x, q8k, y, s);
 }
 
 template <uint32_t TYPE, int ITERS, int MT, bool FUSED>
@@ -482,7 +503,9 @@ hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8
     const int waves = env_int("OQ_GEMV_WAVES", 8);
     if constexpr (MT == 1 && ITERS <= 3) {  // two rows per wave would spill beyond 3 passes
         if (rows >= 2) {
-            if (waves >= 16 && ITERS == 1) return launch_one<TYPE, ITERS, 2, MT, FUSED, 16>(w, m, x, q8k, y, s);
+            if constexpr (ITERS == 1) {
+                if (waves >= 16) return launch_one<TYPE, ITERS, 2, MT, FUSED, 16>(w, m, x, q8k, y, s);
+            }
             return launch_one<TYPE, ITERS, 2, MT, FUSED, 8>(w, m, x, q8k, y, s);
         }
     }
