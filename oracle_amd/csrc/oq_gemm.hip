@@ -484,6 +484,298 @@ __global__ __launch_bounds__(kThreads) void gemm_q4k_f16_kernel(DeviceMatrix w, 
     }
 }
 
+// ---------------------------------------------------------------- producer / consumer variant
+//
+// 8 waves per workgroup, two per SIMD: consumer waves 0..3 (the MFMA waves above: all 128 rows,
+// columns 64 c .. 64 c + 63, B converted in registers) and producer waves 4..7, which do every
+// global load of the workgroup and stage it in LDS.  An MFMA on one wave and vector work on the
+// other wave of its SIMD run side by side, and the consumers' own instruction stream holds only
+// LDS reads, conversions and MFMAs: no global load latency reaches them through the in-order
+// load counter.
+//
+// LDS (dynamic, 136 KB):
+//   A ring   4 x 16 KB  activation tile of step s in buffer s % 4 (layout as above)
+//   W ring   2 x 32 KB  the quant chunks of super-block i in slot i % 2: group g, row n, half e
+//                       at g * 8 KB + ((32 n + 16 e) ^ (64 g))
+//   H ring   2 x  4 KB  the headers of super-block i in slot i % 2: row n at 16 n
+// Producer p: activation rows 32 p .. 32 p + 31 of each tile (four 16-byte chunks per lane, eight
+// rows of 128 bytes per load instruction) and weight rows 64 p .. 64 p + 63: per super-block 8 KB
+// of quants, loaded as 16 row pieces of 64 contiguous bytes per instruction (four lanes per
+// piece), and one 16-byte header per lane.
+// Timing, step s = 4 i + g of the split:
+//   producer: stores tile s + 3 (loaded at step s - 2) into buffer (s + 3) % 4 and loads tile
+//             s + 5; at g = 0 stores super-block i + 1 (loaded during super-block i - 1) into W/H
+//             slot (i + 1) % 2, whose last reader was super-block i - 1, and loads super-block i + 2;
+//   consumer: multiplies step s; during it reads the next step's quant chunks (and at g = 3 the
+//             next super-block's headers) from LDS;
+//   all 8 waves: one barrier per step.
+constexpr uint32_t kWsThreads = 512;
+constexpr uint32_t kWsA = 4 * kTileBytes;   // 64 KB
+constexpr uint32_t kWsWSlot = 32768;
+constexpr uint32_t kWsHSlot = 4096;
+constexpr uint32_t kWsLds = kWsA + 2 * kWsWSlot + 2 * kWsHSlot;
+
+OQ_DEVICE uint32_t ws_w_off(uint32_t slot, uint32_t g, uint32_t n, uint32_t e) {
+    return kWsA + slot * kWsWSlot + g * 8192u + ((32u * n + 16u * e) ^ (64u * g));
+}
+OQ_DEVICE uint32_t ws_h_off(uint32_t slot, uint32_t n) { return kWsA + 2 * kWsWSlot + slot * kWsHSlot + 16u * n; }
+
+// consumer: one step (see wave_step); W chunks of this step in wc[j], of the next step in wn[j]
+// (read here from LDS at slice 1), scale state as there; headers of this super-block in hdr,
+// of the next one in hdrn (read at g = 3).
+template <bool FAST, int G>
+OQ_DEVICE void ws_consumer_step(const uint8_t* lds, const uint32_t (&rd_off)[4], uint32_t wslot, uint32_t wslot_next,
+                                uint32_t hslot_next, uint32_t n_lane0, uint32_t h, float16v (&acc)[4][2],
+                                half8 (&a)[4], uint32_t (&b)[2][4], const uint4 (&wc)[2], uint4 (&wn)[2],
+                                const uint4 (&hdr)[2], uint4 (&hdrn)[2], ScaleT<FAST> (&sc)[2][2][2]) {
+    constexpr int G1 = (G + 1) & 3;
+    constexpr int P = G & 1;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const int nks = (ks + 1) & 3;
+        const uint32_t nbuf = ks < 3 ? (uint32_t)G : (uint32_t)G1;
+        half8 an[4];
+        uint32_t bn[2][4];
+        uint32_t nw[2][2];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int i = q >> 1, j = q & 1;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], as_b_operand(b[j]), acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (q == 0) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) an[ii] = lds_read(lds, nbuf * kTileBytes + 4096u * ii + rd_off[nks]);
+            }
+            const int jj = q >> 2, pp = q & 3;
+            const uint4 src = ks < 3 ? wc[jj] : wn[jj];
+            const ScaleT<FAST>& scl = ks < 3 ? sc[P][jj][nks & 1] : sc[P ^ 1][jj][0];
+            if (pp == 0) {
+                if (nks == 0) {
+                    nw[jj][0] = nib_word<0>(src, 0);
+                    nw[jj][1] = nib_word<0>(src, 1);
+                } else if (nks == 1) {
+                    nw[jj][0] = nib_word<1>(src, 0);
+                    nw[jj][1] = nib_word<1>(src, 1);
+                } else if (nks == 2) {
+                    nw[jj][0] = nib_word<2>(src, 0);
+                    nw[jj][1] = nib_word<2>(src, 1);
+                } else {
+                    nw[jj][0] = nib_word<3>(src, 0);
+                    nw[jj][1] = nib_word<3>(src, 1);
+                }
+            }
+            bn[jj][pp] = (pp & 1) ? weight_pair<FAST, 1>(nw[jj][pp >> 1], scl) : weight_pair<FAST, 0>(nw[jj][pp >> 1], scl);
+            if (ks == 0 && q < 2) {
+                // quant chunks of the next step: group G + 1 of this super-block, or group 0 of the next
+                const uint32_t slot = G < 3 ? wslot : wslot_next;
+                wn[q] = *reinterpret_cast<const uint4*>(lds + ws_w_off(slot, (uint32_t)G1, n_lane0 + 32u * q, h));
+            }
+            if (G == 3 && ks == 0 && (q == 2 || q == 3)) {
+                hdrn[q - 2] = *reinterpret_cast<const uint4*>(lds + ws_h_off(hslot_next, n_lane0 + 32u * (q - 2)));
+            }
+            if (ks == 1 && q == 4) {
+                if (G < 3) scale_pairs<FAST, G1>(hdr[0], sc[P ^ 1][0]);
+                else scale_pairs<FAST, 0>(hdrn[0], sc[P ^ 1][0]);
+            }
+            if (ks == 1 && q == 6) {
+                if (G < 3) scale_pairs<FAST, G1>(hdr[1], sc[P ^ 1][1]);
+                else scale_pairs<FAST, 0>(hdrn[1], sc[P ^ 1][1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) a[ii] = an[ii];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) b[j][e] = bn[j][e];
+    }
+}
+
+// producer state: activation chunk offsets (4 per lane) and LDS store offset; weight piece
+// offsets (8 per lane, one per load instruction) and LDS store offsets; header row offset
+struct Producer {
+    uint32_t act_off[4];
+    uint32_t act_st;
+    uint32_t wrow_off[8];  // row * pitch of the piece's row
+    uint32_t w_e[8];       // half e of the piece
+    uint32_t w_st[8];      // LDS offset of the chunk within a slot
+    uint32_t hrow_off;     // row * pitch of the lane's header row
+};
+
+OQ_DEVICE void ws_load_sb(const Split& sp, const Producer& pr, uint32_t sb, int lane, uint4 (&wq)[8], uint4& hq) {
+    const uint32_t pass = sb / 16u, s16 = sb % 16u;
+    const uint32_t mp = sp.nsb - 16u * pass < 16u ? sp.nsb - 16u * pass : 16u;
+    const uint8_t* qbase = sp.wbase + 16u * (128u * pass + 4u * s16 + (uint32_t)(lane & 3));
+#pragma unroll
+    for (int t = 0; t < 8; ++t) wq[t] = load_u4(qbase, pr.wrow_off[t] + pr.w_e[t] * 64u * mp);
+    hq = load_u4(sp.wbase + sp.hdr_base + 16u * sb, pr.hrow_off);
+}
+
+OQ_DEVICE void ws_store_sb(uint8_t* lds, const Producer& pr, uint32_t slot, const uint4 (&wq)[8], uint4 hq, int pw,
+                           int lane) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) *reinterpret_cast<uint4*>(lds + kWsA + slot * kWsWSlot + pr.w_st[t]) = wq[t];
+    *reinterpret_cast<uint4*>(lds + ws_h_off(slot, 64u * (uint32_t)pw + (uint32_t)lane)) = hq;
+}
+
+template <bool FAST>
+__global__ __launch_bounds__(kWsThreads) void gemm_q4k_ws_kernel(DeviceMatrix w, int m, const _Float16* a16,
+                                                                 uint32_t tiles_n, uint32_t tiles_m, uint32_t splits,
+                                                                 float* __restrict__ out) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nsb = (uint32_t)(w.k / kQK);
+    const Unit un = unit_of(blockIdx.x, tiles_n, tiles_m, splits);
+    const uint32_t z = un.z;
+    const uint64_t n0 = (uint64_t)un.nt * kBN, m0 = (uint64_t)un.mt * kBM;
+    Split sp;
+    sp.sb0 = (uint32_t)((uint64_t)z * nsb / splits);
+    const uint32_t sb1 = (uint32_t)((uint64_t)(z + 1) * nsb / splits);
+    sp.nsbu = sb1 - sp.sb0;  // >= 1: splits <= nsb
+    sp.nsb = nsb;
+    sp.last_step = 4 * sp.nsbu - 1;
+    sp.hdr_base = 128u * nsb;
+    sp.wbase = w.base;
+    sp.a16 = reinterpret_cast<const uint8_t*>(a16) + 2ull * kQK * sp.sb0;
+    const uint32_t nsteps = 4 * sp.nsbu;
+
+    if (wave >= 4) {
+        // ------------------------------------------------------------ producer
+        const int pw = wave - 4;
+        Producer pr;
+        const uint32_t krow = (uint32_t)(w.k * 2);
+        // lane: chunk lane % 8 of rows rb + {0, 1, 16, 17} (rb even), so the four rows share the
+        // tile swizzle and the four stores differ by immediates
+        const uint32_t rb = 32u * pw + 2u * ((uint32_t)lane >> 3), c8 = (uint32_t)lane & 7;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint64_t row = m0 + rb + (uint32_t)(j & 1) + 16u * (uint32_t)(j >> 1);
+            row = row < (uint64_t)m ? row : (uint64_t)m - 1;
+            pr.act_off[j] = (uint32_t)row * krow + 16u * c8;
+        }
+        pr.act_st = 128u * rb + 16u * (c8 ^ ((rb >> 1) & 7));
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t piece = 16u * t + ((uint32_t)lane >> 2);  // 0..127: (row n', half e)
+            const uint32_t nl = 64u * pw + (piece >> 1), e = piece & 1, g = (uint32_t)lane & 3;
+            uint64_t n = n0 + nl;
+            n = n < w.n ? n : w.n - 1;
+            pr.wrow_off[t] = (uint32_t)(n * w.pitch);
+            pr.w_e[t] = e;
+            pr.w_st[t] = g * 8192u + ((32u * nl + 16u * e) ^ (64u * g));
+        }
+        {
+            uint64_t n = n0 + 64u * pw + lane;
+            n = n < w.n ? n : w.n - 1;
+            pr.hrow_off = (uint32_t)(n * w.pitch);
+        }
+        auto act_load = [&](uint32_t t, uint4 (&v)[4]) {
+            const uint32_t st = t < sp.last_step ? t : sp.last_step;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = load_u4(sp.a16 + 128u * st, pr.act_off[j]);
+        };
+        auto act_store = [&](uint32_t buf, const uint4 (&v)[4]) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<uint4*>(lds + buf * kTileBytes + pr.act_st + 128u * (j & 1) + 2048u * (j >> 1)) = v[j];
+        };
+        uint4 av[2][4], wq[8], hq;
+        // prologue: tiles 0..2, super-block 0 into slot 0; tiles 3, 4 and super-block 1 in flight
+        {
+            uint4 t0[4], t1[4], t2[4];
+            act_load(0, t0);
+            act_load(1, t1);
+            act_load(2, t2);
+            ws_load_sb(sp, pr, split_sb(sp, 0), lane, wq, hq);
+            act_store(0, t0);
+            act_store(1, t1);
+            act_store(2, t2);
+            ws_store_sb(lds, pr, 0, wq, hq, pw, lane);
+        }
+        act_load(3, av[1]);
+        act_load(4, av[0]);
+        ws_load_sb(sp, pr, split_sb(sp, 1), lane, wq, hq);
+        lds_barrier();
+        for (uint32_t s = 0; s < nsteps; s += 4) {
+            const uint32_t i = s / 4;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int as = (g + 1) & 1;  // register set of tiles s + 3 (stored) and s + 5 (loaded)
+                act_store((uint32_t)((g + 3) & 3), av[as]);
+                act_load(s + g + 5, av[as]);
+                if (g == 0) {
+                    ws_store_sb(lds, pr, (i + 1) & 1, wq, hq, pw, lane);
+                    ws_load_sb(sp, pr, split_sb(sp, i + 2), lane, wq, hq);
+                }
+                lds_barrier();
+            }
+        }
+        return;
+    }
+
+    // ---------------------------------------------------------------- consumer
+    const int h = lane >> 5, r0 = lane & 31;
+    uint32_t rd_off[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) rd_off[ks] = 128u * (uint32_t)r0 + 16u * (uint32_t)(a_chunk(ks, h) ^ ((r0 >> 1) & 7));
+    const uint32_t n_lane0 = 64u * (uint32_t)wave + (uint32_t)r0;  // row of n-subtile j: + 32 j
+
+    float16v acc[4][2] = {};
+    lds_barrier();  // the producers' prologue
+    uint4 wcur[2], wnext[2], hdr[2], hdrn[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        wcur[j] = *reinterpret_cast<const uint4*>(lds + ws_w_off(0, 0, n_lane0 + 32u * j, h));
+        hdr[j] = *reinterpret_cast<const uint4*>(lds + ws_h_off(0, n_lane0 + 32u * j));
+        hdrn[j] = hdr[j];
+        wnext[j] = wcur[j];
+    }
+    ScaleT<FAST> sc[2][2][2];
+    scale_pairs<FAST, 0>(hdr[0], sc[0][0]);
+    scale_pairs<FAST, 0>(hdr[1], sc[0][1]);
+    half8 a[4];
+    uint32_t b[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = lds_read(lds, 4096u * i + rd_off[0]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t w0 = nib_word<0>(wcur[j], 0), w1 = nib_word<0>(wcur[j], 1);
+        b[j][0] = weight_pair<FAST, 0>(w0, sc[0][j][0]);
+        b[j][1] = weight_pair<FAST, 1>(w0, sc[0][j][0]);
+        b[j][2] = weight_pair<FAST, 0>(w1, sc[0][j][0]);
+        b[j][3] = weight_pair<FAST, 1>(w1, sc[0][j][0]);
+    }
+    for (uint32_t s = 0; s < nsteps; s += 4) {
+        const uint32_t i = s / 4, slot = i & 1, slot1 = (i + 1) & 1;
+        ws_consumer_step<FAST, 0>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wcur, wnext, hdr, hdrn, sc);
+        lds_barrier();
+        ws_consumer_step<FAST, 1>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wnext, wcur, hdr, hdrn, sc);
+        lds_barrier();
+        ws_consumer_step<FAST, 2>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wcur, wnext, hdr, hdrn, sc);
+        lds_barrier();
+        ws_consumer_step<FAST, 3>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wnext, wcur, hdr, hdrn, sc);
+        lds_barrier();
+        hdr[0] = hdrn[0];
+        hdr[1] = hdrn[1];
+    }
+    float* o = out + (uint64_t)z * (uint64_t)m * w.n;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint64_t col = n0 + 64 * wave + 32 * j + r0;
+        if (col >= w.n) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int rr = 0; rr < 16; ++rr) {
+                const uint64_t row = m0 + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
+                if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][rr];
+            }
+        }
+    }
+}
+
 // y[i] = sum over splits s (in order) of partial[s][i]; count4 = outputs / 4
 __global__ __launch_bounds__(256) void reduce_splits_kernel(const float4* __restrict__ part, uint64_t count4,
                                                             uint32_t splits, float4* __restrict__ y) {
@@ -563,7 +855,29 @@ hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const float* x, co
         hipLaunchKernelGGL(q8k_to_f16_kernel, dim3(qgrid), dim3(256), 0, s, q8k, nblocks, a16);
     }
     const unsigned wgs = p.tiles_n * p.tiles_m * p.splits;
-    if (w.k >= kFastMinK && env_int("OQ_GEMM_EXACT_DEQUANT", 0) == 0) {
+    const bool fast = w.k >= kFastMinK && env_int("OQ_GEMM_EXACT_DEQUANT", 0) == 0;
+    if (env_int("OQ_GEMM_WS", 1) != 0) {
+        float* dst = p.splits > 1 ? part : y;
+        if (fast) {
+            static bool attr = false;
+            if (!attr) {
+                (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_q4k_ws_kernel<true>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWsLds);
+                attr = true;
+            }
+            hipLaunchKernelGGL(gemm_q4k_ws_kernel<true>, dim3(wgs), dim3(kWsThreads), kWsLds, s, w, m, a16, p.tiles_n,
+                               p.tiles_m, p.splits, dst);
+        } else {
+            static bool attr = false;
+            if (!attr) {
+                (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_q4k_ws_kernel<false>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWsLds);
+                attr = true;
+            }
+            hipLaunchKernelGGL(gemm_q4k_ws_kernel<false>, dim3(wgs), dim3(kWsThreads), kWsLds, s, w, m, a16, p.tiles_n,
+                               p.tiles_m, p.splits, dst);
+        }
+    } else if (fast) {
         hipLaunchKernelGGL(gemm_q4k_f16_kernel<true>, dim3(wgs), dim3(kThreads), 0, s, w, m, a16, p.tiles_n,
                            p.tiles_m, p.splits, p.splits > 1 ? part : y);
     } else {

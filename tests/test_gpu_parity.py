@@ -276,6 +276,32 @@ def test_matrix_cores_q8k_input_and_split_counts(ctx, splits):
     w.release()
 
 
+@pytest.mark.parametrize("cols", [4096, 8192])
+def test_matrix_core_kernels_agree(ctx, cols):
+    """The producer/consumer GEMM kernel (default) and the four-wave kernel (OQ_GEMM_WS=0)
+    accumulate the same f16 operands in the same order: identical outputs, bit for bit."""
+    rng = np.random.default_rng(2718 + cols)
+    m, rows = 70, 520
+    data = synth.q4_k(rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(12, cols, rows, data)
+    ys = {}
+    old = os.environ.get("OQ_GEMM_WS")
+    try:
+        for v in ("1", "0"):
+            os.environ["OQ_GEMM_WS"] = v
+            ys[v] = gpu_matmul(ctx, w, x, rows)
+    finally:
+        if old is None:
+            os.environ.pop("OQ_GEMM_WS", None)
+        else:
+            os.environ["OQ_GEMM_WS"] = old
+    assert np.array_equal(ys["1"].view(np.uint32), ys["0"].view(np.uint32))
+    y_ref, norm = reference_products(12, rows, cols, data, x)
+    check_close(ys["1"], y_ref, norm)
+    w.release()
+
+
 def test_prefill_gemm_full_size_sampled_rows(ctx):
     """The 4096 x 12288 q4_K down projection at M = 512: every output of 24 sampled activation
     rows against the oracle (the rows are computed inside the full 512-row product)."""
