@@ -321,23 +321,91 @@ int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, f
           *gate = ws + off[10], *up = ws + off[11], *act = ws + off[12], *ffn = ws + off[13], *beta_s = ws + off[14],
           *log_decay = ws + off[15], *normed = ws + off[16];
     hipStream_t s = ctx->stream;
-    hipError_t e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s);
-    if (e == hipSuccess) e = block_project(b->qkv, normed, qkv, s);
-    if (e == hipSuccess) e = block_project(b->z, normed, z, s);
-    if (e == hipSuccess) e = block_project(b->beta, normed, beta, s);
-    if (e == hipSuccess) e = block_project(b->alpha, normed, alpha, s);
-    if (e == hipSuccess)
-        e = oq::launch_conv_gates(qkv, b->conv_weight, hist, C, K, beta, alpha, b->dt_bias, b->decay, Hv, conv, beta_s,
-                                  log_decay, s);
-    if (e == hipSuccess)
-        e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, z, b->out_norm, rec, gated, s);
-    if (e == hipSuccess) e = block_project(b->out, gated, branch, s);
-    if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s);
-    if (e == hipSuccess) e = block_project(b->gate, post, gate, s);
-    if (e == hipSuccess) e = block_project(b->up, post, up, s);
-    if (e == hipSuccess) e = oq::launch_swiglu(gate, up, F, act, s);
-    if (e == hipSuccess) e = block_project(b->down, act, ffn, s);
-    if (e == hipSuccess) e = oq::launch_add(resid, ffn, E, y, s);
+    hipError_t e = hipSuccess;
+    // Fused path: five launches (normed in-projections with the convolution and gates, the delta
+    // rule, the out projection with the residual, normed gate/up with SwiGLU, down with the
+    // residual) when every projection is a K-quant GEMV of the supported shapes.
+    oq::BlockGemv in{}, outp{}, ffn_in{}, down{};
+    in.nmat = 4;
+    in.mat[0] = b->qkv->m;
+    in.mat[1] = b->z->m;
+    in.mat[2] = b->beta->m;
+    in.mat[3] = b->alpha->m;
+    in.row_end[0] = (uint32_t)C;
+    in.row_end[1] = (uint32_t)(C + V);
+    in.row_end[2] = (uint32_t)(C + V + Hv);
+    in.row_end[3] = (uint32_t)(C + V + 2 * Hv);
+    in.x = x;
+    in.norm_w = b->input_norm;
+    in.eps = b->eps;
+    in.raw[0] = qkv;
+    in.raw[1] = z;
+    in.raw[2] = beta;
+    in.raw[3] = alpha;
+    in.conv_w = b->conv_weight;
+    in.history = hist;
+    in.conv_kernel = (uint32_t)K;
+    in.conv_out = conv;
+    in.dt_bias = b->dt_bias;
+    in.decay = b->decay;
+    in.beta_s = beta_s;
+    in.log_decay = log_decay;
+    outp.nmat = 1;
+    outp.mat[0] = b->out->m;
+    outp.row_end[0] = (uint32_t)E;
+    outp.x = gated;
+    outp.raw[0] = branch;
+    outp.add = x;
+    outp.sum_out = resid;
+    ffn_in.nmat = 2;
+    ffn_in.mat[0] = b->gate->m;
+    ffn_in.mat[1] = b->up->m;
+    ffn_in.row_end[0] = (uint32_t)F;
+    ffn_in.row_end[1] = (uint32_t)(2 * F);
+    ffn_in.x = resid;
+    ffn_in.norm_w = b->post_norm;
+    ffn_in.eps = b->eps;
+    ffn_in.norm_out = post;
+    ffn_in.raw[0] = gate;
+    ffn_in.raw[1] = up;
+    ffn_in.act = act;
+    down.nmat = 1;
+    down.mat[0] = b->down->m;
+    down.row_end[0] = (uint32_t)E;
+    down.x = act;
+    down.raw[0] = ffn;
+    down.add = resid;
+    down.sum_out = y;
+    const bool even = C % 2 == 0 && V % 2 == 0 && Hv % 2 == 0 && E % 2 == 0;
+    const bool fused = env_flag("OQ_BLOCK_FUSED", true) && even && aligned(x, 16) && oq::gemv_block_supported(in) &&
+                       oq::gemv_block_supported(outp) && oq::gemv_block_supported(ffn_in) &&
+                       oq::gemv_block_supported(down);
+    if (fused) {
+        e = oq::launch_gemv_block(oq::kBlockIn, in, s);
+        if (e == hipSuccess)
+            e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, z, b->out_norm, rec, gated, s);
+        if (e == hipSuccess) e = oq::launch_gemv_block(oq::kBlockAdd, outp, s);
+        if (e == hipSuccess) e = oq::launch_gemv_block(oq::kBlockFfn, ffn_in, s);
+        if (e == hipSuccess) e = oq::launch_gemv_block(oq::kBlockAdd, down, s);
+    } else {
+        e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s);
+        if (e == hipSuccess) e = block_project(b->qkv, normed, qkv, s);
+        if (e == hipSuccess) e = block_project(b->z, normed, z, s);
+        if (e == hipSuccess) e = block_project(b->beta, normed, beta, s);
+        if (e == hipSuccess) e = block_project(b->alpha, normed, alpha, s);
+        if (e == hipSuccess)
+            e = oq::launch_conv_gates(qkv, b->conv_weight, hist, C, K, beta, alpha, b->dt_bias, b->decay, Hv, conv, beta_s,
+                                      log_decay, s);
+        if (e == hipSuccess)
+            e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, z, b->out_norm, rec, gated, s);
+        if (e == hipSuccess) e = block_project(b->out, gated, branch, s);
+        if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s);
+        if (e == hipSuccess) e = block_project(b->gate, post, gate, s);
+        if (e == hipSuccess) e = block_project(b->up, post, up, s);
+        if (e == hipSuccess) e = oq::launch_swiglu(gate, up, F, act, s);
+        if (e == hipSuccess) e = block_project(b->down, act, ffn, s);
+        if (e == hipSuccess) e = oq::launch_add(resid, ffn, E, y, s);
+    }
     if (e == hipSuccess && trace) {
         uint64_t t = 0;
         for (int i = 0; i < 14 && e == hipSuccess; ++i) {

@@ -76,4 +76,30 @@ hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_he
 hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s);
 hipError_t launch_add(const float* a, const float* b, uint64_t n, float* out, hipStream_t s);
 
+// ---- oq_gemv_reg.hip  (fused m = 1 GEMV of the DeltaNet decode block; see the kernel comment)
+enum : int { kBlockIn = 0, kBlockAdd = 1, kBlockFfn = 2 };
+struct BlockGemv {
+    DeviceMatrix mat[4];   // same type, K and pitch
+    uint32_t row_end[4];   // IN / ADD: cumulative row counts of mat[0..nmat)
+    uint32_t nmat;
+    const float* x;        // F32 activation, K values
+    const float* norm_w;   // RMSNorm weight (K values) or null
+    float eps;
+    float* norm_out;       // the normalised activation (written by workgroup 0) or null
+    float* raw[4];         // per-matrix outputs
+    const float* conv_w;   // IN: convolution taps [rows of mat[0]][conv_kernel]
+    float* history;        // IN: convolution history, same shape, updated in place
+    uint32_t conv_kernel;
+    float* conv_out;       // IN: SiLU(conv) per channel of mat[0]
+    const float* dt_bias;  // IN: per row of mat[3]
+    const float* decay;
+    float* beta_s;         // IN: sigmoid of mat[2]'s outputs
+    float* log_decay;      // IN: softplus(mat[3] + dt_bias) * decay
+    const float* add;      // ADD: sum_out = add + y
+    float* sum_out;
+    float* act;            // FFN: SiLU(gate) * up
+};
+bool gemv_block_supported(const BlockGemv& a);
+hipError_t launch_gemv_block(int mode, const BlockGemv& a, hipStream_t s);
+
 }  // namespace oq
