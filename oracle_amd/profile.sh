@@ -34,7 +34,8 @@ done
 
 {
     echo "# rocprofv3 kernel statistics, workload $WL"
-    echo "# command: (cd \$REPO && $TRACE_CMD)"
+    echo "# recipe: bash oracle_amd/profile.sh $WL '$KERN' <out>"
+    echo "# command: (cd \$REPO && ${TRACE_CMD//$OUT/<out>})   (<out>: the OUT argument)"
     echo "# bench line of that run:"
     grep '^{' "$RAW.trace.log" | tail -1 | sed 's/^/#   /'
     python3 -m oracle_amd.profsum stats "$RAW/trace"
