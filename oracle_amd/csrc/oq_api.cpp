@@ -602,7 +602,9 @@ int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, f
             return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, x, nullptr, y, ctx->scratch, ctx->stream),
                              "matmul");
         }
-        if (!env_flag("OQ_FUSED_QUANT", true)) {
+        // one row: every workgroup quantizes x itself (saves a launch); several rows: quantize
+        // once and let the workgroups copy the Q8_K blocks
+        if (!env_flag("OQ_FUSED_QUANT", m == 1)) {
             const uint64_t q8bytes = (m * (w->m.k / oq::kQK) * oq::kQ8KBytes + 255) & ~uint64_t(255);
             if (int rc = ensure_scratch(ctx, q8bytes)) return rc;
             uint8_t* q8 = static_cast<uint8_t*>(ctx->scratch);

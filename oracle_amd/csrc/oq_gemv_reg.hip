@@ -111,17 +111,34 @@ OQ_DEVICE void quantize_block(const float4 v, int lane, uint32_t& qword, int& bs
     d = 1.0f / iscale;
 }
 
+// The 16 sixteen-byte chunks of a staged 256-block are stored in permuted order: chunk c of
+// block b sits at c ^ swz(b).  The lanes that read one piece each (4 per block, 16 blocks per
+// wave) then hit 16 different chunk positions in every group of 16 lanes instead of 4 (the
+// pieces of one lane slot are 64 bytes apart for q4_K/q5_K, 128 + 16 for q6_K): no bank
+// conflicts when the small-batch kernels re-read the slices for every activation row.
+template <uint32_t TYPE>
+OQ_DEVICE uint32_t swz(uint64_t b) {
+    return TYPE == 14 ? ((uint32_t)b & 3u) << 1 : ((uint32_t)b & 3u);
+}
+
+template <uint32_t TYPE>
+OQ_DEVICE uint32_t stage_off(uint64_t b, int lane) {
+    return 16u * (((uint32_t)lane >> 2) ^ swz<TYPE>(b)) + 4u * ((uint32_t)lane & 3u);
+}
+
+template <uint32_t TYPE>
 OQ_DEVICE void store_block(const ActLds& s, int mi, uint64_t b, int lane, uint32_t qword, int bsum16_quad,
                            float d) {
-    *reinterpret_cast<uint32_t*>(s.q(mi) + b * kQK + 4 * lane) = qword;
+    *reinterpret_cast<uint32_t*>(s.q(mi) + b * kQK + stage_off<TYPE>(b, lane)) = qword;
     if ((lane & 3) == 0) s.bsum(mi)[b * 16 + (lane >> 2)] = bsum16_quad;
     if (lane == 0) s.d(mi)[b] = d;
 }
 
 // Q8_K block copy: lane's quant dword, d, and bsums 2*(lane%8), +1 in one dword
+template <uint32_t TYPE>
 OQ_DEVICE void copy_block_store(const ActLds& s, int mi, uint64_t b, int lane, uint32_t qword, uint32_t bsdw,
                                 float d) {
-    *reinterpret_cast<uint32_t*>(s.q(mi) + b * kQK + 4 * lane) = qword;
+    *reinterpret_cast<uint32_t*>(s.q(mi) + b * kQK + stage_off<TYPE>(b, lane)) = qword;
     if (lane < 8) {
         s.bsum(mi)[b * 16 + 2 * lane] = (int)(int16_t)(bsdw & 0xFFFFu);
         s.bsum(mi)[b * 16 + 2 * lane + 1] = (int)(int16_t)(bsdw >> 16);
@@ -147,10 +164,11 @@ OQ_DEVICE int piece(int q, int i) {
 template <uint32_t TYPE>
 OQ_DEVICE void slice_from_lds(Act& a, const ActLds& s, int mi, uint64_t sb, int q) {
     const int8_t* qb = s.q(mi) + sb * kQK;
-    a.x0 = *reinterpret_cast<const uint4*>(qb + piece<TYPE>(q, 0));
-    a.x1 = *reinterpret_cast<const uint4*>(qb + piece<TYPE>(q, 1));
-    a.x2 = *reinterpret_cast<const uint4*>(qb + piece<TYPE>(q, 2));
-    a.x3 = *reinterpret_cast<const uint4*>(qb + piece<TYPE>(q, 3));
+    const uint32_t z = swz<TYPE>(sb);
+    a.x0 = *reinterpret_cast<const uint4*>(qb + 16 * ((piece<TYPE>(q, 0) / 16) ^ z));
+    a.x1 = *reinterpret_cast<const uint4*>(qb + 16 * ((piece<TYPE>(q, 1) / 16) ^ z));
+    a.x2 = *reinterpret_cast<const uint4*>(qb + 16 * ((piece<TYPE>(q, 2) / 16) ^ z));
+    a.x3 = *reinterpret_cast<const uint4*>(qb + 16 * ((piece<TYPE>(q, 3) / 16) ^ z));
     a.d = s.d(mi)[sb];
     const int* bs = s.bsum(mi) + sb * 16;
 #pragma unroll
@@ -334,19 +352,21 @@ OQ_DEVICE void finish_group(const typename WRegs<TYPE>::type (&W)[R][ITERS], con
     for (int it = 0; it < ITERS; ++it) {
         const uint64_t sb = 16u * it + (lane >> 2);
         if (!FULL && sb >= nsb) continue;  // FULL: K is a multiple of 4096, every lane has a slot
+        if constexpr (MT == 1) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const auto dec = decode_w<TYPE>(W[r][it], ss, q);
-            if constexpr (MT == 1) {
-                acc[r][0] += lane_dot(dec, act[it]);
-            } else {
+            for (int r = 0; r < R; ++r) acc[r][0] += lane_dot(decode_w<TYPE>(W[r][it], ss, q), act[it]);
+        } else {
+            // each activation slice is read from LDS once for the R rows
+            decltype(decode_w<TYPE>(W[0][it], ss, q)) dec[R];
 #pragma unroll
-                for (int mi = 0; mi < MT; ++mi) {
-                    if (mi < m) {
-                        Act a;
-                        slice_from_lds<TYPE>(a, s, mi, sb, q);
-                        acc[r][mi] += lane_dot(dec, a);
-                    }
+            for (int r = 0; r < R; ++r) dec[r] = decode_w<TYPE>(W[r][it], ss, q);
+#pragma unroll
+            for (int mi = 0; mi < MT; ++mi) {
+                if (mi < m) {
+                    Act a;
+                    slice_from_lds<TYPE>(a, s, mi, sb, q);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[r][mi] += lane_dot(dec[r], a);
                 }
             }
         }
@@ -412,30 +432,63 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kq_kernel(DeviceMatrix w, int
                 int bs;
                 float d;
                 quantize_block(xv[j], lane, qw, bs, d);
-                store_block(s, 0, b, lane, qw, bs, d);
+                store_block<TYPE>(s, 0, b, lane, qw, bs, d);
             } else {
-                copy_block_store(s, 0, b, lane, qv[j], bv[j], dv[j]);
+                copy_block_store<TYPE>(s, 0, b, lane, qv[j], bv[j], dv[j]);
             }
         }
     } else {
+        // m rows: the wave's blocks are staged U at a time (their loads issued together); the
+        // first batch goes out before the weight loads so that its wait does not include them
+        constexpr int U = 4;
         const uint64_t nblk = (uint64_t)m * nsb;
-        for (uint64_t b = wave_in_wg; b < nblk; b += WAVES) {
-            const int mi = (int)(b / nsb);
-            const uint64_t sb = b % nsb;
-            if constexpr (FUSED) {
-                uint32_t qw;
-                int bs;
-                float d;
-                quantize_block(reinterpret_cast<const float4*>(x + (uint64_t)mi * w.k + sb * kQK)[lane], lane, qw,
-                               bs, d);
-                store_block(s, mi, sb, lane, qw, bs, d);
-            } else {
-                const uint8_t* blk = q8k + b * kQ8KBytes;
-                copy_block_store(s, mi, sb, lane, ldg32(blk + 4 + 4 * lane), ldg32(blk + 260 + 4 * (lane & 7)),
-                                 __uint_as_float(ldg32(blk)));
+        float4 xv[U];
+        uint32_t qv[U], bv[U];
+        float dv[U];
+        auto load_batch = [&](uint64_t b0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                uint64_t b = b0 + (uint64_t)WAVES * u;
+                b = b < nblk ? b : nblk - 1;
+                if constexpr (FUSED) {
+                    const uint64_t mi = b / nsb, sb = b % nsb;
+                    xv[u] = reinterpret_cast<const float4*>(x + mi * w.k + sb * kQK)[lane];
+                } else {
+                    const uint8_t* blk = q8k + b * kQ8KBytes;
+                    qv[u] = ldg32(blk + 4 + 4 * lane);
+                    bv[u] = ldg32(blk + 260 + 4 * (lane & 7));
+                    dv[u] = __uint_as_float(ldg32(blk));
+                }
             }
-        }
+        };
+        auto store_batch = [&](uint64_t b0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint64_t b = b0 + (uint64_t)WAVES * u;
+                if (b >= nblk) break;
+                const int mi = (int)(b / nsb);
+                const uint64_t sb = b % nsb;
+                if constexpr (FUSED) {
+                    uint32_t qw;
+                    int bs;
+                    float d;
+                    quantize_block(xv[u], lane, qw, bs, d);
+                    store_block<TYPE>(s, mi, sb, lane, qw, bs, d);
+                } else {
+                    copy_block_store<TYPE>(s, mi, sb, lane, qv[u], bv[u], dv[u]);
+                }
+            }
+        };
+        uint64_t b0 = (uint64_t)wave_in_wg;
+        load_batch(b0);
+        asm volatile("" ::: "memory");
         load_group<TYPE, ITERS, R>(A, w, active ? wave : groups - 1, lane);
+        while (true) {
+            store_batch(b0);
+            b0 += (uint64_t)WAVES * U;
+            if (b0 >= nblk) break;
+            load_batch(b0);
+        }
     }
     __syncthreads();
     if (!active) return;
@@ -508,6 +561,11 @@ hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8
             }
             return launch_one<TYPE, ITERS, 2, MT, FUSED, 8>(w, m, x, q8k, y, s);
         }
+    }
+    // small batches: two rows per wave use every activation slice read from LDS twice (Q5_K's
+    // extra high-bit words do not fit two rows of three slots for eight columns without spilling)
+    if constexpr (MT > 1 && ITERS <= 3 && !(TYPE == 13 && ITERS * MT > 16)) {
+        if (env_int("OQ_GEMV_ROWS_MT", 2) >= 2) return launch_one<TYPE, ITERS, 2, MT, FUSED, 8>(w, m, x, q8k, y, s);
     }
     return launch_one<TYPE, ITERS, 1, MT, FUSED, 8>(w, m, x, q8k, y, s);
 }
@@ -727,7 +785,7 @@ __global__ __launch_bounds__(512) void gemv_block_kernel(BlockGemv a) {
         int bs;
         float d;
         quantize_block(xv[j], lane, qw, bs, d);
-        store_block(s, 0, b, lane, qw, bs, d);
+        store_block<TYPE>(s, 0, b, lane, qw, bs, d);
     }
     __syncthreads();
     if (!active) return;
