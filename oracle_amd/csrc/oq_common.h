@@ -124,45 +124,59 @@ struct Q8KLane {
     float d;         // block scale (wave-uniform)
 };
 
+// Wave-uniform maximum of a 32-bit unsigned key: DPP maxima within rows of 16 lanes, then the
+// four row results through scalar registers.
+OQ_DEVICE uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<kDppQuadXor1>((int)v));
+    v = max(v, (uint32_t)dpp_i<kDppQuadXor2>((int)v));
+    v = max(v, (uint32_t)dpp_i<kDppRowHalfMirror>((int)v));
+    v = max(v, (uint32_t)dpp_i<kDppRowMirror>((int)v));
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
 // GGML quantize_row_q8_K on one block, wave-parallel.  amax = max |x|; `max` is x at the
 // FIRST index reaching amax (a strict > scan keeps the first); amax == 0 gives d = 0, q = 0.
 // iscale = -127/max (correctly rounded division), q = min(127, rne(iscale*x)), d = 1/iscale.
-// Identical bits to the sequential algorithm for finite x.
+// Identical bits to the sequential algorithm for finite x:
+//  - |x| is compared through its bit pattern (non-negative floats order like unsigned ints);
+//  - the first index: the lowest lane holding a value of magnitude amax (ballot + find-first),
+//    and within that lane its lowest element;
+//  - rne(t) for |t| < 2^22 is read from the bits of t + 1.5*2^23 (the product rounded first,
+//    as GGML's nearest_int does): the low byte is q's two's-complement byte and bits - 0x4B400000
+//    is q.  |iscale*x| <= 127*(1+2^-24)^2 < 127.5, so the min(127, .) clamp never binds.
 OQ_DEVICE Q8KLane quantize_q8k_block_wave(float4 v, int lane) {
 #pragma clang fp contract(off)
-    const float a0 = fabsf(v.x), a1 = fabsf(v.y), a2 = fabsf(v.z), a3 = fabsf(v.w);
-    const float lane_max = fmaxf(fmaxf(a0, a1), fmaxf(a2, a3));
-    const float amax = wave_max(lane_max);
+    (void)lane;
+    const uint32_t b0 = __float_as_uint(v.x) & 0x7FFFFFFFu, b1 = __float_as_uint(v.y) & 0x7FFFFFFFu;
+    const uint32_t b2 = __float_as_uint(v.z) & 0x7FFFFFFFu, b3 = __float_as_uint(v.w) & 0x7FFFFFFFu;
+    const uint32_t amax = wave_max_u32(max(max(b0, b1), max(b2, b3)));
     Q8KLane r;
-    if (amax == 0.0f) {
+    if (amax == 0u) {
         r.qword = 0u;
         r.quad_bsum = 0;
         r.d = 0.0f;
         return r;
     }
-    int first = 1 << 30;
-    if (a3 == amax) first = 4 * lane + 3;
-    if (a2 == amax) first = 4 * lane + 2;
-    if (a1 == amax) first = 4 * lane + 1;
-    if (a0 == amax) first = 4 * lane + 0;
-    const int idx = wave_min_int(first);
-    const int owner = idx >> 2, sub = idx & 3;
-    float mine = sub == 0 ? v.x : (sub == 1 ? v.y : (sub == 2 ? v.z : v.w));
-    const float maxv = __shfl(mine, owner, 64);
+    const bool h0 = b0 == amax, h1 = b1 == amax, h2 = b2 == amax, h3 = b3 == amax;
+    // one compare mask per element, combined in scalar registers
+    const uint64_t owners = __builtin_amdgcn_ballot_w64(h0) | __builtin_amdgcn_ballot_w64(h1) |
+                            __builtin_amdgcn_ballot_w64(h2) | __builtin_amdgcn_ballot_w64(h3);
+    const float mine = h0 ? v.x : (h1 ? v.y : (h2 ? v.z : v.w));
+    const float maxv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), (int)__builtin_ctzll(owners)));
     const float iscale = -127.0f / maxv;
-    const float vals[4] = {v.x, v.y, v.z, v.w};
-    uint32_t word = 0;
-    int s = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float t = iscale * vals[i];
-        int q = (int)__builtin_rintf(t);
-        q = q < 127 ? q : 127;
-        s += q;
-        word |= ((uint32_t)q & 0xFFu) << (8 * i);
-    }
-    r.qword = word;
-    r.quad_bsum = quad_sum_int(s);
+    constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+    const uint32_t t0 = __float_as_uint(iscale * v.x + kMagic), t1 = __float_as_uint(iscale * v.y + kMagic);
+    const uint32_t t2 = __float_as_uint(iscale * v.z + kMagic), t3 = __float_as_uint(iscale * v.w + kMagic);
+    // bytes 0 of t0..t3, little-endian
+    r.qword = __builtin_amdgcn_perm(__builtin_amdgcn_perm(t3, t2, 0x0C0C0400u), __builtin_amdgcn_perm(t1, t0, 0x0C0C0400u),
+                                    0x05040100u);
+    const int s = (int)(t0 + t1 + t2 + t3 - 4u * 0x4B400000u);
+    r.quad_bsum = s + dpp_i<kDppQuadXor1>(s);
+    r.quad_bsum += dpp_i<kDppQuadXor2>(r.quad_bsum);
     r.d = 1.0f / iscale;
     return r;
 }

@@ -34,30 +34,6 @@ OQ_DEVICE int dot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot
 OQ_DEVICE float h2f(uint32_t bits16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16); }
 
 
-OQ_DEVICE float row16_max(float v) {
-    v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
-    v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
-    v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
-    v = fmaxf(v, dpp_f<kDppRowMirror>(v));
-    return v;
-}
-OQ_DEVICE int row16_min(int v) {
-    v = min(v, dpp_i<kDppQuadXor1>(v));
-    v = min(v, dpp_i<kDppQuadXor2>(v));
-    v = min(v, dpp_i<kDppRowHalfMirror>(v));
-    v = min(v, dpp_i<kDppRowMirror>(v));
-    return v;
-}
-OQ_DEVICE float wave_max_uniform(float v) {
-    v = row16_max(v);
-    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
-}
-OQ_DEVICE int wave_min_uniform(int v) {
-    v = row16_min(v);
-    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
-}
-
 // ---------------------------------------------------------------- LDS image of activation rows
 
 // per row: q8[K] | d[K/256] | bsum[K/16] (int32)
@@ -73,42 +49,13 @@ struct ActLds {
 };
 uint64_t act_lds_bytes(uint64_t k, int m) { return (uint64_t)m * (k + (k / kQK) * 4 + (k / 16) * 4); }
 
-// GGML quantize_row_q8_K of one 256-block held by a wave (lane: values 4l..4l+3); returns the
-// lane's 4 quants, the 16-element sum of its quad (valid in every lane of the quad) and d.
+// GGML quantize_row_q8_K of one 256-block held by a wave (lane: values 4l..4l+3): the lane's 4
+// quants, the 16-element sum of its quad (valid in every lane of the quad) and d.
 OQ_DEVICE void quantize_block(const float4 v, int lane, uint32_t& qword, int& bsum, float& d) {
-#pragma clang fp contract(off)
-    const float a0 = fabsf(v.x), a1 = fabsf(v.y), a2 = fabsf(v.z), a3 = fabsf(v.w);
-    const float amax = wave_max_uniform(fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
-    if (amax == 0.0f) {
-        qword = 0u;
-        bsum = 0;
-        d = 0.0f;
-        return;
-    }
-    int first = 1 << 30;  // first index reaching max |x| (the sequential scan keeps the first)
-    if (a3 == amax) first = 4 * lane + 3;
-    if (a2 == amax) first = 4 * lane + 2;
-    if (a1 == amax) first = 4 * lane + 1;
-    if (a0 == amax) first = 4 * lane + 0;
-    const int idx = wave_min_uniform(first);
-    const int sub = idx & 3;
-    const float mine = sub == 0 ? v.x : (sub == 1 ? v.y : (sub == 2 ? v.z : v.w));
-    const float maxv = readlane_f(mine, idx >> 2);
-    const float iscale = -127.0f / maxv;
-    const float vals[4] = {v.x, v.y, v.z, v.w};
-    qword = 0u;
-    int sum = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int q = (int)__builtin_rintf(iscale * vals[i]);
-        q = q < 127 ? q : 127;
-        sum += q;
-        qword |= ((uint32_t)q & 0xFFu) << (8 * i);
-    }
-    sum += dpp_i<kDppQuadXor1>(sum);
-    sum += dpp_i<kDppQuadXor2>(sum);
-    bsum = sum;
-    d = 1.0f / iscale;
+    const Q8KLane r = quantize_q8k_block_wave(v, lane);
+    qword = r.qword;
+    bsum = r.quad_bsum;
+    d = r.d;
 }
 
 // The 16 sixteen-byte chunks of a staged 256-block are stored in permuted order: chunk c of
@@ -385,6 +332,49 @@ OQ_DEVICE void finish_group(const typename WRegs<TYPE>::type (&W)[R][ITERS], con
     }
 }
 
+// Stages the Q8_K form of one activation row in LDS (quantizing F32 x, or copying Q8_K blocks),
+// wave w taking blocks w, w + WAVES, ...  The activation loads go out first (unconditional,
+// clamped) so that the waits before quantizing count only them; x and q8k are deliberately not
+// __restrict__, so the fence keeps them ahead of the weight loads that issue() starts, which then
+// stay in flight through the staging.
+template <uint32_t TYPE, int ITERS, bool FUSED, int WAVES, typename Issue>
+OQ_DEVICE void stage_one_row(const ActLds& s, const float* x, const uint8_t* q8k, uint64_t nsb, int wave_in_wg,
+                             int lane, Issue&& issue) {
+    constexpr int SBW = (ITERS * 16 + WAVES - 1) / WAVES;
+    float4 xv[SBW];
+    uint32_t qv[SBW], bv[SBW];
+    float dv[SBW];
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        b = b < nsb ? b : nsb - 1;
+        if constexpr (FUSED) {
+            xv[j] = reinterpret_cast<const float4*>(x + b * kQK)[lane];
+        } else {
+            const uint8_t* blk = q8k + b * kQ8KBytes;
+            qv[j] = ldg32(blk + 4 + 4 * lane);
+            bv[j] = ldg32(blk + 260 + 4 * (lane & 7));
+            dv[j] = __uint_as_float(ldg32(blk));
+        }
+    }
+    asm volatile("" ::: "memory");
+    issue();
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        if (b >= nsb) break;
+        if constexpr (FUSED) {
+            uint32_t qw;
+            int bs;
+            float d;
+            quantize_block(xv[j], lane, qw, bs, d);
+            store_block<TYPE>(s, 0, b, lane, qw, bs, d);
+        } else {
+            copy_block_store<TYPE>(s, 0, b, lane, qv[j], bv[j], dv[j]);
+        }
+    }
+}
+
 template <uint32_t TYPE, int ITERS, int R, int MT, bool FUSED, int WAVES, bool FULL>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kq_kernel(DeviceMatrix w, int m, const float* x,
                                                              const uint8_t* q8k, float* __restrict__ y) {
@@ -401,42 +391,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kq_kernel(DeviceMatrix w, int
     WR A[R][ITERS];
 
     if constexpr (MT == 1) {
-        // Activation loads first (unconditional, clamped) so the waits before quantizing count
-        // only them; x and q8k are deliberately not __restrict__, so the fence below keeps them
-        // ahead of the weight loads, which then stay in flight through the staging.
-        constexpr int SBW = (ITERS * 16 + WAVES - 1) / WAVES;
-        float4 xv[SBW];
-        uint32_t qv[SBW], bv[SBW];
-        float dv[SBW];
-#pragma unroll
-        for (int j = 0; j < SBW; ++j) {
-            uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
-            b = b < nsb ? b : nsb - 1;
-            if constexpr (FUSED) {
-                xv[j] = reinterpret_cast<const float4*>(x + b * kQK)[lane];
-            } else {
-                const uint8_t* blk = q8k + b * kQ8KBytes;
-                qv[j] = ldg32(blk + 4 + 4 * lane);
-                bv[j] = ldg32(blk + 260 + 4 * (lane & 7));
-                dv[j] = __uint_as_float(ldg32(blk));
-            }
-        }
-        asm volatile("" ::: "memory");
-        load_group<TYPE, ITERS, R>(A, w, active ? wave : groups - 1, lane);
-#pragma unroll
-        for (int j = 0; j < SBW; ++j) {
-            const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
-            if (b >= nsb) break;
-            if constexpr (FUSED) {
-                uint32_t qw;
-                int bs;
-                float d;
-                quantize_block(xv[j], lane, qw, bs, d);
-                store_block<TYPE>(s, 0, b, lane, qw, bs, d);
-            } else {
-                copy_block_store<TYPE>(s, 0, b, lane, qv[j], bv[j], dv[j]);
-            }
-        }
+        stage_one_row<TYPE, ITERS, FUSED, WAVES>(s, x, q8k, nsb, wave_in_wg, lane,
+                                                 [&] { load_group<TYPE, ITERS, R>(A, w, active ? wave : groups - 1, lane); });
     } else {
         // m rows: the wave's blocks are staged U at a time (their loads issued together); the
         // first batch goes out before the weight loads so that its wait does not include them
@@ -510,6 +466,126 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kq_kernel(DeviceMatrix w, int
     }
 }
 
+// Marks the registers of a loaded pass as redefined here, after every memory operation above
+// (memory clobber): their decode cannot be scheduled earlier.
+OQ_DEVICE void hold4(uint4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)::"memory"); }
+template <uint32_t TYPE>
+OQ_DEVICE void hold(W45& r) {
+    hold4(r.c0);
+    hold4(r.c1);
+    hold4(r.hdr);
+    if constexpr (TYPE == 13) {
+        hold4(r.h0);
+        hold4(r.h1);
+    }
+}
+template <uint32_t TYPE>
+OQ_DEVICE void hold(W6& r) {
+    hold4(r.c0);
+    hold4(r.c1);
+    hold4(r.qh);
+    asm volatile("" : "+v"(r.sc), "+v"(r.d)::"memory");
+}
+
+// Decode GEMV (one activation row), streamed.  Wave i of workgroup b owns the rows
+// b*WAVES + i + k*nw (k >= 0, nw = waves in the grid) and walks their passes (16 super-blocks:
+// 2 KiB of quants plus headers per wave) in order, holding exactly one pass in flight while it
+// computes the previous one: the loads of pass u + 1 are issued once pass u has arrived.  The
+// chip then keeps about one pass per resident wave in flight, enough to keep HBM streaming, while
+// the memory queues stay short.  Per-lane partial sums and the row reduction are those of
+// gemv_kq_kernel, so both kernels give the same bits.
+template <uint32_t TYPE, int ITERS, bool FUSED, int WAVES, bool FULL>
+__global__ __launch_bounds__(64 * WAVES) void gemv_stream_kernel(DeviceMatrix w, const float* x, const uint8_t* q8k,
+                                                                 float* __restrict__ y) {
+    using WR = typename WRegs<TYPE>::type;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave_in_wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = gridDim.x * WAVES;
+    const uint32_t n = (uint32_t)w.n;
+    const uint32_t nsb = (uint32_t)(w.k / kQK);
+    const ActLds s{smem, w.k};
+    const uint32_t first = blockIdx.x * WAVES + (uint32_t)wave_in_wg;
+    auto row_base = [&](uint32_t row) {
+        row = row < n ? row : n - 1;  // a wave without rows reads row n-1 once
+        return w.base + (uint64_t)__builtin_amdgcn_readfirstlane(row) * w.pitch;
+    };
+
+    // The first pass is requested once the activation row is staged: weight requests in flight
+    // delay the activation loads of the workgroups that start later, which all wait on them.
+    WR buf[2];
+    stage_one_row<TYPE, ITERS, FUSED, WAVES>(s, x, q8k, nsb, wave_in_wg, lane, [] {});
+    load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane);
+    __syncthreads();
+    if (first >= n) return;
+
+    const int q = lane & 3;
+    const ScaleSel ss = scale_sel(q);
+    // up to two passes the lane's activation slices stay in registers; longer rows read the
+    // slice of each pass from LDS when it is used
+    constexpr bool kActRegs = ITERS <= 2;
+    Act act[kActRegs ? ITERS : 1];
+    if constexpr (kActRegs) {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const uint32_t sb = 16u * it + (lane >> 2);
+            if (sb < nsb) slice_from_lds<TYPE>(act[it], s, 0, sb, q);
+        }
+    }
+
+    // Finished rows: lane (done % 64) keeps the sum and the row index of the done-th row; 64 at
+    // a time are stored together.
+    float acc = 0.0f, out = 0.0f;
+    uint32_t out_row = 0, done = 0;
+    uint32_t row = first, it = 0;  // the unit whose loads are in flight
+    bool more = true;
+    while (more) {
+        // two units per trip, so that the buffer of every unit is a compile-time index (rows have
+        // ITERS units: for ITERS <= 2 the pass of unit j is a compile-time index too)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int its = ITERS == 1 ? 0 : (ITERS == 2 ? j : (int)it);
+            // Wait for unit (row, it), the only memory operation outstanding.  acc ties the wait
+            // to the previous unit's arithmetic, which therefore stays ahead of it instead of
+            // being deferred while the loads of further units are issued.
+            asm volatile("s_waitcnt vmcnt(0)" : "+v"(acc), "+v"(out) :: "memory");
+            uint32_t nrow = row, nit = it + 1;
+            if (nit == ITERS) {
+                nrow = row + nw < row ? n : row + nw;  // (no wrap-around)
+                nit = 0;
+            }
+            more = nrow < n;
+            // past the wave's last row the load re-reads the current pass (a cache hit), which
+            // keeps the loads unconditional and the compiler's wait counts exact
+            load_w<TYPE>(buf[(j + 1) & 1], row_base(more ? nrow : row), nsb, (int)(more ? nit : it), lane);
+            hold<TYPE>(buf[j & 1]);  // the arithmetic below follows those loads
+            const uint32_t sb = 16u * (uint32_t)its + (lane >> 2);
+            if (FULL || sb < nsb) {
+                if constexpr (kActRegs) {
+                    acc += lane_dot(decode_w<TYPE>(buf[j & 1], ss, q), act[its]);
+                } else {
+                    Act a;
+                    slice_from_lds<TYPE>(a, s, 0, sb, q);
+                    acc += lane_dot(decode_w<TYPE>(buf[j & 1], ss, q), a);
+                }
+            }
+            if (it == ITERS - 1) {
+                const float v = wave_sum_uniform(acc);
+                const bool mine = lane == (int)(done & 63u);
+                out = mine ? v : out;
+                out_row = mine ? row : out_row;
+                acc = 0.0f;
+                ++done;
+                if ((done & 63u) == 0u) y[out_row] = out;
+            }
+            row = nrow;
+            it = nit;
+            if (!more) break;
+        }
+    }
+    if ((uint32_t)lane < (done & 63u)) y[out_row] = out;
+}
+
 // ---------------------------------------------------------------- launch
 
 // Workgroups resident per CU for this instantiation (register and LDS limits), cached.
@@ -550,8 +626,46 @@ hipError_t launch_one(const DeviceMatrix& w, int m, const float* x, const uint8_
     return launch_full<TYPE, ITERS, R, MT, FUSED, WAVES, false>(w, m, x, q8k, y, s);
 }
 
+template <uint32_t TYPE, int ITERS, bool FUSED, int WAVES, bool FULL>
+hipError_t launch_stream(const DeviceMatrix& w, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+    const uint64_t lds = act_lds_bytes(w.k, 1);
+    static int resident = 0;
+    if (resident == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_stream_kernel<TYPE, ITERS, FUSED, WAVES, FULL>,
+                                                         64 * WAVES, lds) != hipSuccess || n < 1) {
+            n = 1;
+        }
+        resident = n;
+    }
+    // sixteen waves per CU: ~37 KiB of weights in flight per CU, and each CU stages the
+    // activation row once per sixteen waves
+    int wg_per_cu = env_int("OQ_STREAM_WG_PER_CU", 16 / WAVES);
+    wg_per_cu = wg_per_cu < 1 ? 1 : (wg_per_cu > resident ? resident : wg_per_cu);
+    uint64_t wgs = (uint64_t)cu_count() * (uint64_t)wg_per_cu;
+    const uint64_t need = (w.n + WAVES - 1) / WAVES;
+    if (wgs > need) wgs = need;
+    hipLaunchKernelGGL((gemv_stream_kernel<TYPE, ITERS, FUSED, WAVES, FULL>), dim3((unsigned)wgs), dim3(64 * WAVES), lds,
+                       s, w, x, q8k, y);
+    return hipGetLastError();
+}
+
 template <uint32_t TYPE, int ITERS, int MT, bool FUSED>
 hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+    if constexpr (MT == 1) {
+        // Streamed kernel for rows of two or more passes and for matrices of four or more rows
+        // per resident wave; otherwise every wave's rows fit in flight at once (below).
+        const bool stream = ITERS >= 2 || w.n >= (uint64_t)cu_count() * 16u * 4u;
+        if (env_int("OQ_GEMV_STREAM", stream ? 1 : 0) != 0) {
+            const bool full = (w.k / kQK) % 16 == 0;
+            if (env_int("OQ_STREAM_WAVES", 16) >= 16) {
+                return full ? launch_stream<TYPE, ITERS, FUSED, 16, true>(w, x, q8k, y, s)
+                            : launch_stream<TYPE, ITERS, FUSED, 16, false>(w, x, q8k, y, s);
+            }
+            return full ? launch_stream<TYPE, ITERS, FUSED, 8, true>(w, x, q8k, y, s)
+                        : launch_stream<TYPE, ITERS, FUSED, 8, false>(w, x, q8k, y, s);
+        }
+    }
     const int rows = env_int("OQ_GEMV_ROWS", MT == 1 && ITERS <= 2 ? 2 : 1);
     const int waves = env_int("OQ_GEMV_WAVES", 8);
     if constexpr (MT == 1 && ITERS <= 3) {  // two rows per wave would spill beyond 3 passes

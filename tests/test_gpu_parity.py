@@ -318,7 +318,9 @@ def test_prefill_gemm_full_size_sampled_rows(ctx):
     w.release()
 
 
-@pytest.mark.parametrize("env", [{"OQ_GEMV_ROWS": "2"}, {"OQ_FUSED_QUANT": "0"}, {"OQ_GEMV_MAX_WG": "7"}])
+@pytest.mark.parametrize("env", [{"OQ_GEMV_ROWS": "2"}, {"OQ_FUSED_QUANT": "0"}, {"OQ_GEMV_MAX_WG": "7"},
+                                 {"OQ_GEMV_STREAM": "1"}, {"OQ_GEMV_STREAM": "1", "OQ_STREAM_WAVES": "8"},
+                                 {"OQ_GEMV_STREAM": "0"}])
 def test_launch_variants_agree(ctx, env):
     rng = np.random.default_rng(77)
     rows, cols = 211, 4096
@@ -354,6 +356,71 @@ def test_matvec_deterministic(ctx):
     b = gpu_matmul(ctx, w, x, rows)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     w.release()
+
+
+@pytest.mark.parametrize("t,rows,cols", [(12, 8269, 512), (12, 8269, 4096), (12, 12293, 4096), (13, 8269, 512),
+                                         (14, 12293, 512), (12, 8269, 12288)])
+def test_decode_gemv_many_rows_per_wave(ctx, t, rows, cols):
+    # Several rows per wave (and a ragged last round), through the streamed and the batched
+    # decode kernels: each row is computed on every launch (outputs are poisoned with NaN before
+    # each), with the same bits.
+    rng = np.random.default_rng(4242 + t + rows + cols)
+    data = synth.weights(t, rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    w = ctx.upload(t, cols, rows, data)
+    xb = ctx.to_device(x)
+    yb = ctx.alloc(rows * 4)
+    runs = []
+    for env in ({}, {"OQ_GEMV_STREAM": "1"}, {"OQ_GEMV_STREAM": "0"}, {"OQ_GEMV_STREAM": "1"}):
+        old = {k: os.environ.get(k) for k in env}
+        os.environ.update(env)
+        try:
+            yb.upload(np.full(rows, np.nan, np.float32))
+            ctx.matvec(w, xb, yb)
+            ctx.sync()
+        finally:
+            for k, v in old.items():
+                if v is None:
+                    os.environ.pop(k, None)
+                else:
+                    os.environ[k] = v
+        runs.append(yb.download(np.float32, rows))
+    for r in runs[1:]:
+        assert np.array_equal(r.view(np.uint32), runs[0].view(np.uint32))
+    y_ref, norm = reference_products(t, rows, cols, data, x)
+    check_close(runs[0], y_ref, norm)
+    xb.free()
+    yb.free()
+    w.release()
+
+
+def test_decode_gemv_many_rows_in_graph(ctx):
+    rng = np.random.default_rng(4343)
+    rows, cols = 12293, 512
+    ws = [ctx.upload(t, cols, rows, synth.weights(t, rng, rows, cols)) for t in KQ]
+    xb = ctx.to_device(rng.standard_normal(cols).astype(np.float32))
+    ybs = [ctx.alloc(rows * 4) for _ in ws]
+    for w, yb in zip(ws, ybs):
+        ctx.matvec(w, xb, yb)
+    ctx.sync()
+    eager = [yb.download(np.float32, rows) for yb in ybs]
+    ctx.capture_begin()
+    for w, yb in zip(ws, ybs):
+        ctx.matvec(w, xb, yb)
+    g = ctx.capture_end()
+    for rep in range(3):
+        for yb in ybs:
+            ctx.matvec(ws[1], xb, ybs[1])
+            yb.upload(np.full(rows, np.nan, np.float32))
+        g.launch()
+        ctx.sync()
+        for e, yb in zip(eager, ybs):
+            assert np.array_equal(yb.download(np.float32, rows).view(np.uint32), e.view(np.uint32)), rep
+    g.destroy()
+    for b in ybs + [xb]:
+        b.free()
+    for w in ws:
+        w.release()
 
 
 # ---------------------------------------------------------------- argument errors through the ABI
