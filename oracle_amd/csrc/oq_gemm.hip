@@ -55,18 +55,33 @@ OQ_DEVICE uint32_t pack_f16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2v));
 }
 
-// F32 x [m][K] -> f16(d * q) with the Q8_K quantization of quantize_q8k (one wave per block)
+// F32 x [m][K] -> f16(d * q) with the Q8_K quantization of quantize_q8k.  A wave quantizes
+// kQuantBlocksPerWave blocks (one at a time, their loads issued together); a workgroup's four waves
+// take consecutive blocks, so each load instruction of the workgroup reads 4 KiB of consecutive x.
+constexpr int kQuantBlocksPerWave = 4;
+
 __global__ __launch_bounds__(256) void quantize_f16_kernel(const float* __restrict__ x, uint64_t nblocks,
                                                            _Float16* __restrict__ out) {
     const int lane = threadIdx.x & 63;
-    const uint64_t blk = blockIdx.x * 4ull + (threadIdx.x >> 6);
-    if (blk >= nblocks) return;
-    const float4 v = reinterpret_cast<const float4*>(x + blk * kQK)[lane];
-    const Q8KLane r = quantize_q8k_block_wave(v, lane);
-    float f[4];
+    const uint64_t first = blockIdx.x * (4ull * kQuantBlocksPerWave) + (threadIdx.x >> 6);
+    float4 v[kQuantBlocksPerWave];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = r.d * (float)(int8_t)(r.qword >> (8 * i));
-    *reinterpret_cast<uint2*>(out + blk * kQK + 4 * lane) = make_uint2(pack_f16(f[0], f[1]), pack_f16(f[2], f[3]));
+    for (int u = 0; u < kQuantBlocksPerWave; ++u) {
+        uint64_t blk = first + 4ull * u;
+        blk = blk < nblocks ? blk : nblocks - 1;
+        v[u] = reinterpret_cast<const float4*>(x + blk * kQK)[lane];
+    }
+#pragma unroll
+    for (int u = 0; u < kQuantBlocksPerWave; ++u) {
+        const uint64_t blk = first + 4ull * u;
+        if (blk >= nblocks) break;
+        const Q8KLane r = quantize_q8k_block_wave(v[u], lane);
+        float f[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f[i] = r.d * (float)(int8_t)(r.qword >> (8 * i));
+        *reinterpret_cast<uint2*>(out + blk * kQK + 4 * lane) =
+            make_uint2(pack_f16(f[0], f[1]), pack_f16(f[2], f[3]));
+    }
 }
 
 // Q8_K blocks -> f16(d * q)
@@ -694,9 +709,15 @@ __global__ __launch_bounds__(kWsThreads) void gemm_q4k_ws_kernel(DeviceMatrix w,
             act_store(2, t2);
             ws_store_sb(lds, pr, 0, wq, hq, pw, lane);
         }
-        act_load(3, av[1]);
-        act_load(4, av[0]);
+        // Issued in the order of a loop trip (tile of set 1, then of set 0), each group whole: the
+        // compiler's wait counts at the loop head merge this path with the loop's back edge, and
+        // interleaved prologue loads would leave a tile with fewer younger loads here than in the
+        // loop, so that every trip would wait for the loads of the step before.
         ws_load_sb(sp, pr, split_sb(sp, 1), lane, wq, hq);
+        asm volatile("" ::: "memory");
+        act_load(3, av[1]);
+        asm volatile("" ::: "memory");
+        act_load(4, av[0]);
         lds_barrier();
         for (uint32_t s = 0; s < nsteps; s += 4) {
             const uint32_t i = s / 4;
@@ -850,7 +871,8 @@ hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const float* x, co
     const uint64_t nblocks = (uint64_t)m * (w.k / kQK);
     const unsigned qgrid = (unsigned)((nblocks + 3) / 4);
     if (x) {
-        hipLaunchKernelGGL(quantize_f16_kernel, dim3(qgrid), dim3(256), 0, s, x, nblocks, a16);
+        const unsigned xgrid = (unsigned)((nblocks + 4 * kQuantBlocksPerWave - 1) / (4 * kQuantBlocksPerWave));
+        hipLaunchKernelGGL(quantize_f16_kernel, dim3(xgrid), dim3(256), 0, s, x, nblocks, a16);
     } else {
         hipLaunchKernelGGL(q8k_to_f16_kernel, dim3(qgrid), dim3(256), 0, s, q8k, nblocks, a16);
     }

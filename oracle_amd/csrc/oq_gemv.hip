@@ -74,6 +74,84 @@ __global__ __launch_bounds__(kThreads) void gemv_q8_0_kernel(DeviceMatrix w, int
     }
 }
 
+// Decode GEMV for q8_0 (one activation row; K = 1024, 2048 or 4096, ITERS = K / 1024).
+// Wave i of workgroup b owns rows b * kRowWaves + i + j * (waves in the grid).  A lane takes the
+// 16-byte quant chunks lane + 64 j (every load instruction of the wave reads 1 KiB of consecutive
+// bytes) and their f16 scales.  Each workgroup copies x into LDS once: the x loads are issued
+// first, then the first row's weight loads, so the copy waits only for x while the weights stream.
+// In LDS the four 16-byte pieces of each 64-byte x chunk are rotated by the chunk index, so the
+// lanes of one ds_read_b128 read distinct banks.  Arithmetic per chunk as gemv_q8_0_kernel.
+constexpr int kRowWaves = 16;
+
+template <int ITERS>
+OQ_DEVICE void load_q8_0_row(uint4 (&q)[ITERS], uint32_t (&d)[ITERS], const DeviceMatrix& w, uint32_t row, int lane) {
+    const uint32_t n = (uint32_t)w.n;
+    row = row < n ? row : n - 1;
+    const uint8_t* base = w.base + (uint64_t)__builtin_amdgcn_readfirstlane(row) * w.pitch;
+#pragma unroll
+    for (int j = 0; j < ITERS; ++j) {
+        const uint32_t c = (uint32_t)lane + 64u * j;
+        q[j] = ldg128(base + 16u * c);
+        d[j] = *reinterpret_cast<const uint16_t*>(base + (uint32_t)w.k + 2u * (c >> 1));
+    }
+}
+
+template <int ITERS>
+__global__ __launch_bounds__(64 * kRowWaves) void gemv_q8_0_rows_kernel(DeviceMatrix w, const float* x,
+                                                                        float* __restrict__ y) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float4* xs = reinterpret_cast<float4*>(smem);
+    constexpr int XPT = (ITERS + 3) / 4;  // float4 of x per thread
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n = (uint32_t)w.n, k4 = (uint32_t)(w.k / 4);
+    const uint32_t nw = gridDim.x * kRowWaves;
+    uint32_t row = blockIdx.x * kRowWaves + wave;
+
+    float4 xv[XPT];
+#pragma unroll
+    for (int t = 0; t < XPT; ++t) {
+        uint32_t f = threadIdx.x + 64u * kRowWaves * t;
+        f = f < k4 ? f : k4 - 1;
+        xv[t] = reinterpret_cast<const float4*>(x)[f];
+    }
+    asm volatile("" ::: "memory");  // x is not __restrict__: its loads stay ahead of the weights'
+    uint4 q[ITERS];
+    uint32_t d[ITERS];
+    load_q8_0_row<ITERS>(q, d, w, row, lane);
+#pragma unroll
+    for (int t = 0; t < XPT; ++t) {
+        const uint32_t f = threadIdx.x + 64u * kRowWaves * t;
+        const uint32_t c = f >> 2, i = f & 3;
+        if (f < k4) xs[4u * c + ((i + c) & 3u)] = xv[t];
+    }
+    __syncthreads();
+    while (row < n) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < ITERS; ++j) {
+            const uint32_t c = (uint32_t)lane + 64u * j;
+            const float scale = f16_bits_to_f32((uint16_t)d[j]);
+            const uint32_t words[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+            float part = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 xp = xs[4u * c + ((i + c) & 3u)];
+                const uint32_t wd = words[i];
+                part += (float)(int8_t)(wd) * xp.x;
+                part += (float)(int8_t)(wd >> 8) * xp.y;
+                part += (float)(int8_t)(wd >> 16) * xp.z;
+                part += (float)(int8_t)(wd >> 24) * xp.w;
+            }
+            acc += scale * part;
+        }
+        const float v = wave_sum_uniform(acc);
+        if (lane == 0) y[row] = v;
+        row += nw;
+        if (row < n) load_q8_0_row<ITERS>(q, d, w, row, lane);
+    }
+}
+
 // f32 / f16 / bf16 rows of any length: one wave per row, lanes stride over elements.  These
 // types carry norm and gate vectors in the reference (src/model/qwen35_weights.cpp:49-59), not
 // the bandwidth-heavy projections.
@@ -114,8 +192,25 @@ unsigned grid_for(uint64_t work_items, int per_wg_items) {
     return (unsigned)(want < cap ? (want ? want : 1) : cap);
 }
 
+template <int ITERS>
+hipError_t launch_q8_0_rows(const DeviceMatrix& w, const float* x, float* y, hipStream_t s) {
+    uint64_t wgs = (w.n + kRowWaves - 1) / kRowWaves;
+    const uint64_t cap = (uint64_t)cu_count() * (ITERS <= 2 ? 2u : 1u);  // workgroups resident per CU
+    if (wgs > cap) wgs = cap;
+    hipLaunchKernelGGL((gemv_q8_0_rows_kernel<ITERS>), dim3((unsigned)wgs), dim3(64 * kRowWaves), w.k * 4, s, w, x, y);
+    return hipGetLastError();
+}
+
 template <int MT>
 hipError_t launch_q8_0_mt(const DeviceMatrix& w, int m, const float* x, float* y, hipStream_t s) {
+    if (MT == 1 && w.k % 1024 == 0 && env_int("OQ_Q8_0_ROWS", 1) != 0) {
+        switch (w.k / 1024) {
+            case 1: return launch_q8_0_rows<1>(w, x, y, s);
+            case 2: return launch_q8_0_rows<2>(w, x, y, s);
+            case 4: return launch_q8_0_rows<4>(w, x, y, s);
+            default: break;  // longer rows would not fit the registers of 16-wave workgroups
+        }
+    }
     const uint64_t lds = (uint64_t)MT * w.k * 4;
     const unsigned grid = grid_for(w.n, kWaves);
     if (lds <= kLdsBudget) {

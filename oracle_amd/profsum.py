@@ -7,6 +7,11 @@
         HBM bytes per dispatch of the matching kernel: FETCH_SIZE and WRITE_SIZE (KiB per
         dispatch, median over dispatches) each scaled by bytes / counter of a device-to-device
         copy of N bytes profiled the same way.
+    python -m oracle_amd.profsum counters --kernel SUBSTR --cus N --simds-per-cu 4 DIR [DIR ...]
+        median per dispatch of every counter collected under the DIRs for the matching kernel,
+        plus derived figures: MFMA-busy fraction of each SIMD's active cycles
+        (SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x GRBM_GUI_ACTIVE / XCDs)), MFMA rate of the dispatch
+        (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 flop / GRBM_GUI_ACTIVE cycles).
 """
 from __future__ import annotations
 
@@ -69,6 +74,26 @@ def traffic(kernel: str, fetch: str, write: str, copy_fetch: str, copy_write: st
     }
 
 
+def counters(kernel: str, dirs: list[str], cus: int, simds_per_cu: int, xcds: int) -> dict:
+    vals: dict[str, list[float]] = {}
+    for d in dirs:
+        for r in _rows(d, "*counter_collection.csv"):
+            if kernel in r["Kernel_Name"]:
+                vals.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    med = {k: statistics.median(v) for k, v in sorted(vals.items())}
+    out: dict = {"kernel": kernel, "dispatches": {k: len(v) for k, v in sorted(vals.items())}, "median": med}
+    gui = med.get("GRBM_GUI_ACTIVE")
+    if gui:
+        cycles = gui / xcds  # GRBM_GUI_ACTIVE is summed over the XCDs
+        out["active_cycles_per_xcd"] = cycles
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in med:
+            out["mfma_busy_frac"] = med["SQ_VALU_MFMA_BUSY_CYCLES"] / (cus * simds_per_cu * cycles)
+        if "SQ_INSTS_VALU_MFMA_MOPS_F16" in med:
+            # one MOPS unit = 512 flop; rate at the cycles of the dispatch (clock not assumed)
+            out["mfma_f16_flop_per_cycle_per_cu"] = med["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512.0 / (cycles * cus)
+    return out
+
+
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -79,7 +104,16 @@ def main(argv: list[str] | None = None) -> int:
     for k in ("kernel", "fetch", "write", "copy_fetch", "copy_write"):
         t.add_argument("--" + k.replace("_", "-"), required=True)
     t.add_argument("--copy-bytes", type=int, required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("--kernel", required=True)
+    c.add_argument("--cus", type=int, default=256)
+    c.add_argument("--simds-per-cu", type=int, default=4)
+    c.add_argument("--xcds", type=int, default=8)
+    c.add_argument("dirs", nargs="+")
     a = ap.parse_args(argv)
+    if a.cmd == "counters":
+        print(json.dumps(counters(a.kernel, a.dirs, a.cus, a.simds_per_cu, a.xcds), indent=1))
+        return 0
     if a.cmd == "stats":
         rows = kernel_stats(a.dir, a.match)
         print(f"{'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'pct':>7}  kernel")

@@ -346,6 +346,39 @@ def test_launch_variants_agree(ctx, env):
         w.release()
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (17, 4096), (5000, 1024), (9000, 2048), (8300, 4096)])
+def test_q8_0_decode_gemv(ctx, rows, cols):
+    """The q8_0 decode kernel (16-wave workgroups, x staged once per workgroup, several rows per
+    wave when the rows outnumber the waves) against the oracle and against the general q8_0
+    kernel (OQ_Q8_0_ROWS=0); outputs are poisoned with NaN before each launch."""
+    rng = np.random.default_rng(880 + rows + cols)
+    data = synth.q8_0(rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    w = ctx.upload(8, cols, rows, data)
+    xb = ctx.to_device(x)
+    yb = ctx.alloc(rows * 4)
+    runs = []
+    for flag in ("1", "0"):
+        old = os.environ.get("OQ_Q8_0_ROWS")
+        os.environ["OQ_Q8_0_ROWS"] = flag
+        try:
+            yb.upload(np.full(rows, np.nan, np.float32))
+            ctx.matvec(w, xb, yb)
+            ctx.sync()
+        finally:
+            if old is None:
+                os.environ.pop("OQ_Q8_0_ROWS", None)
+            else:
+                os.environ["OQ_Q8_0_ROWS"] = old
+        runs.append(yb.download(np.float32, rows))
+    y_ref, norm = reference_products(8, rows, cols, data, x)
+    for r in runs:
+        check_close(r, y_ref[0], norm[0])
+    xb.free()
+    yb.free()
+    w.release()
+
+
 def test_matvec_deterministic(ctx):
     rng = np.random.default_rng(8)
     rows, cols = 1000, 4096
@@ -371,7 +404,8 @@ def test_decode_gemv_many_rows_per_wave(ctx, t, rows, cols):
     xb = ctx.to_device(x)
     yb = ctx.alloc(rows * 4)
     runs = []
-    for env in ({}, {"OQ_GEMV_STREAM": "1"}, {"OQ_GEMV_STREAM": "0"}, {"OQ_GEMV_STREAM": "1"}):
+    for env in ({}, {"OQ_GEMV_STREAM": "1"}, {"OQ_GEMV_STREAM": "0"}, {"OQ_GEMV_STREAM": "1"},
+                {"OQ_GEMV_STREAM": "0", "OQ_GEMV_ROWS": "1"}):
         old = {k: os.environ.get(k) for k in env}
         os.environ.update(env)
         try:
