@@ -586,6 +586,139 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_stream_kernel(DeviceMatrix w,
     if ((uint32_t)lane < (done & 63u)) y[out_row] = out;
 }
 
+// Stages the Q8_K form of m activation rows in LDS (row mi at s.q(mi)...), wave w taking the
+// blocks w, w + WAVES, ... of the m * nsb blocks, four at a time with their loads issued together.
+template <uint32_t TYPE, bool FUSED, int WAVES>
+OQ_DEVICE void stage_rows(const ActLds& s, int m, const float* x, const uint8_t* q8k, uint64_t nsb, uint64_t k,
+                          int wave_in_wg, int lane) {
+    constexpr int U = 4;
+    const uint64_t nblk = (uint64_t)m * nsb;
+    for (uint64_t b0 = (uint64_t)wave_in_wg; b0 < nblk; b0 += (uint64_t)WAVES * U) {
+        float4 xv[U];
+        uint32_t qv[U], bv[U];
+        float dv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            uint64_t b = b0 + (uint64_t)WAVES * u;
+            b = b < nblk ? b : nblk - 1;
+            if constexpr (FUSED) {
+                const uint64_t mi = b / nsb, sb = b % nsb;
+                xv[u] = reinterpret_cast<const float4*>(x + mi * k + sb * kQK)[lane];
+            } else {
+                const uint8_t* blk = q8k + b * kQ8KBytes;
+                qv[u] = ldg32(blk + 4 + 4 * lane);
+                bv[u] = ldg32(blk + 260 + 4 * (lane & 7));
+                dv[u] = __uint_as_float(ldg32(blk));
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t b = b0 + (uint64_t)WAVES * u;
+            if (b >= nblk) break;
+            const int mi = (int)(b / nsb);
+            const uint64_t sb = b % nsb;
+            if constexpr (FUSED) {
+                uint32_t qw;
+                int bs;
+                float d;
+                quantize_block(xv[u], lane, qw, bs, d);
+                store_block<TYPE>(s, mi, sb, lane, qw, bs, d);
+            } else {
+                copy_block_store<TYPE>(s, mi, sb, lane, qv[u], bv[u], dv[u]);
+            }
+        }
+    }
+}
+
+// Small-batch product (2 <= m <= MT activation rows), streamed like gemv_stream_kernel: 16-wave
+// workgroups stage the m rows' Q8_K blocks in LDS once, a wave walks its weight rows one pass at
+// a time with one pass in flight, decodes each pass once and multiplies it with the m activation
+// slices read from LDS.  Per-lane sums in the order of gemv_kq_kernel (pass, then row mi) and the
+// same row reductions: the same bits.
+template <uint32_t TYPE, int ITERS, int MT, bool FUSED, bool FULL>
+__global__ __launch_bounds__(1024) void gemv_stream_mt_kernel(DeviceMatrix w, int m, const float* x, const uint8_t* q8k,
+                                                              float* __restrict__ y) {
+    constexpr int WAVES = 16;
+    using WR = typename WRegs<TYPE>::type;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave_in_wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = gridDim.x * WAVES;
+    const uint32_t n = (uint32_t)w.n;
+    const uint32_t nsb = (uint32_t)(w.k / kQK);
+    const ActLds s{smem, w.k};
+    const uint32_t first = blockIdx.x * WAVES + (uint32_t)wave_in_wg;
+    auto row_base = [&](uint32_t row) {
+        row = row < n ? row : n - 1;
+        return w.base + (uint64_t)__builtin_amdgcn_readfirstlane(row) * w.pitch;
+    };
+
+    WR buf[2];
+    stage_rows<TYPE, FUSED, WAVES>(s, m, x, q8k, nsb, w.k, wave_in_wg, lane);
+    load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane);
+    __syncthreads();
+    if (first >= n) return;
+
+    const int q = lane & 3;
+    const ScaleSel ss = scale_sel(q);
+    float acc[MT], out[MT];
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) acc[mi] = out[mi] = 0.0f;
+    uint32_t out_row = 0, done = 0;
+    uint32_t row = first, it = 0;  // the unit whose loads are in flight
+    bool more = true;
+    while (more) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            uint32_t nrow = row, nit = it + 1;
+            if (nit == ITERS) {
+                nrow = row + nw < row ? n : row + nw;
+                nit = 0;
+            }
+            more = nrow < n;
+            load_w<TYPE>(buf[(j + 1) & 1], row_base(more ? nrow : row), nsb, (int)(more ? nit : it), lane);
+            hold<TYPE>(buf[j & 1]);
+            const uint32_t sb = 16u * it + (lane >> 2);
+            if (FULL || sb < nsb) {
+                const auto dec = decode_w<TYPE>(buf[j & 1], ss, q);
+#pragma unroll
+                for (int mi = 0; mi < MT; ++mi) {
+                    if (mi < m) {
+                        Act a;
+                        slice_from_lds<TYPE>(a, s, mi, sb, q);
+                        acc[mi] += lane_dot(dec, a);
+                    }
+                }
+            }
+            if (it == ITERS - 1) {
+                const bool mine = lane == (int)(done & 63u);
+#pragma unroll
+                for (int mi = 0; mi < MT; ++mi) {
+                    const float v = wave_sum_uniform(acc[mi]);
+                    out[mi] = mine ? v : out[mi];
+                    acc[mi] = 0.0f;
+                }
+                out_row = mine ? row : out_row;
+                ++done;
+                if ((done & 63u) == 0u) {
+#pragma unroll
+                    for (int mi = 0; mi < MT; ++mi)
+                        if (mi < m) y[(uint64_t)mi * n + out_row] = out[mi];
+                }
+            }
+            row = nrow;
+            it = nit;
+            if (!more) break;
+        }
+    }
+    if ((uint32_t)lane < (done & 63u)) {
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi)
+            if (mi < m) y[(uint64_t)mi * n + out_row] = out[mi];
+    }
+}
+
 // ---------------------------------------------------------------- launch
 
 // Workgroups resident per CU for this instantiation (register and LDS limits), cached.
@@ -650,6 +783,17 @@ hipError_t launch_stream(const DeviceMatrix& w, const float* x, const uint8_t* q
     return hipGetLastError();
 }
 
+template <uint32_t TYPE, int ITERS, int MT, bool FUSED, bool FULL>
+hipError_t launch_stream_mt(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+    const uint64_t lds = act_lds_bytes(w.k, MT);
+    uint64_t wgs = (uint64_t)cu_count();
+    const uint64_t need = (w.n + 15) / 16;
+    if (wgs > need) wgs = need;
+    hipLaunchKernelGGL((gemv_stream_mt_kernel<TYPE, ITERS, MT, FUSED, FULL>), dim3((unsigned)wgs), dim3(1024), lds, s,
+                       w, m, x, q8k, y);
+    return hipGetLastError();
+}
+
 template <uint32_t TYPE, int ITERS, int MT, bool FUSED>
 hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
     if constexpr (MT == 1) {
@@ -664,6 +808,14 @@ hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8
             }
             return full ? launch_stream<TYPE, ITERS, FUSED, 8, true>(w, x, q8k, y, s)
                         : launch_stream<TYPE, ITERS, FUSED, 8, false>(w, x, q8k, y, s);
+        }
+    }
+    if constexpr (MT > 1 && !FUSED && !(TYPE == 13 && MT == 8)) {
+        // small batches from Q8_K blocks (the default for m > 1): streamed, one pass in flight
+        // (q5_K with eight rows would spill within the 128 registers of a 16-wave workgroup)
+        if (act_lds_bytes(w.k, MT) <= kLdsBudget && env_int("OQ_GEMV_STREAM_MT", 1) != 0) {
+            return (w.k / kQK) % 16 == 0 ? launch_stream_mt<TYPE, ITERS, MT, FUSED, true>(w, m, x, q8k, y, s)
+                                         : launch_stream_mt<TYPE, ITERS, MT, FUSED, false>(w, m, x, q8k, y, s);
         }
     }
     const int rows = env_int("OQ_GEMV_ROWS", MT == 1 && ITERS <= 2 ? 2 : 1);
