@@ -1001,12 +1001,18 @@ __global__ __launch_bounds__(512) void gemv_block_kernel(BlockGemv a) {
     WR A[R][ITERS];
 
     constexpr int SBW = (ITERS * 16 + WAVES - 1) / WAVES;
-    float4 xv[SBW];
+    // the norm weights are requested with x (up to two blocks per wave): otherwise their load is
+    // one more round trip after the sum-of-squares barrier
+    constexpr bool kNormEarly = SBW <= 2;
+    float4 xv[SBW], nv[kNormEarly ? SBW : 1];
 #pragma unroll
     for (int j = 0; j < SBW; ++j) {
         uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
         b = b < nsb ? b : nsb - 1;
         xv[j] = reinterpret_cast<const float4*>(a.x + b * kQK)[lane];
+        if constexpr (kNormEarly) {
+            if (a.norm_w) nv[j] = reinterpret_cast<const float4*>(a.norm_w + b * kQK)[lane];
+        }
     }
     asm volatile("" ::: "memory");
     blk_load_group<TYPE, ITERS, MODE, FULL>(A, a, active ? wave : groups - 1, lane);
@@ -1032,7 +1038,9 @@ __global__ __launch_bounds__(512) void gemv_block_kernel(BlockGemv a) {
         for (int j = 0; j < SBW; ++j) {
             const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
             if (b >= nsb) break;
-            const float4 w4 = reinterpret_cast<const float4*>(a.norm_w + b * kQK)[lane];
+            float4 w4;
+            if constexpr (kNormEarly) w4 = nv[j];
+            else w4 = reinterpret_cast<const float4*>(a.norm_w + b * kQK)[lane];
             {
 #pragma clang fp contract(off)
                 xv[j].x = xv[j].x * inv * w4.x;
@@ -1091,8 +1099,115 @@ __global__ __launch_bounds__(512) void gemv_block_kernel(BlockGemv a) {
     }
 }
 
+// The residual (ADD) projections of the block -- out projection and FFN down, one matrix each --
+// streamed: x staged as Q8_K in LDS by 16-wave workgroups, then the rows walked as in
+// gemv_stream_kernel (wave i of workgroup b owns rows b * 16 + i + j * (waves in the grid), one
+// pass of one row in flight).  Lane (done % 64) keeps the done-th finished row; every 64 rows, and
+// at the end, each lane writes its row's raw output and residual sum.  Per-lane sums and row
+// reductions as gemv_block_kernel: the same bits.
+template <uint32_t TYPE, int ITERS, bool FULL>
+__global__ __launch_bounds__(1024) void gemv_block_add_stream_kernel(BlockGemv a) {
+    constexpr int WAVES = 16;
+    using WR = typename WRegs<TYPE>::type;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave_in_wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = gridDim.x * WAVES;
+    const DeviceMatrix& w = a.mat[0];
+    const uint32_t nsb = (uint32_t)(w.k / kQK);
+    const uint32_t n = (uint32_t)w.n;
+    const ActLds s{smem, w.k};
+    const uint32_t first = blockIdx.x * WAVES + (uint32_t)wave_in_wg;
+    auto row_base = [&](uint32_t row) {
+        row = row < n ? row : n - 1;  // a wave without rows reads row n-1
+        return w.base + (uint64_t)__builtin_amdgcn_readfirstlane(row) * w.pitch;
+    };
+
+    WR buf[2];
+    stage_one_row<TYPE, ITERS, true, WAVES>(s, a.x, nullptr, nsb, wave_in_wg, lane, [] {});
+    load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane);
+    __syncthreads();
+    if (first >= n) return;
+
+    const int q = lane & 3;
+    const ScaleSel ss = scale_sel(q);
+    constexpr bool kActRegs = ITERS <= 2;
+    Act act[kActRegs ? ITERS : 1];
+    if constexpr (kActRegs) {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const uint32_t sb = 16u * it + (lane >> 2);
+            if (sb < nsb) slice_from_lds<TYPE>(act[it], s, 0, sb, q);
+        }
+    }
+    float acc = 0.0f, out = 0.0f;
+    uint32_t out_row = 0, done = 0;
+    uint32_t row = first, it = 0;  // the unit whose loads are in flight
+    bool more = true;
+    while (more) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int its = ITERS == 1 ? 0 : (ITERS == 2 ? j : (int)it);
+            asm volatile("s_waitcnt vmcnt(0)" : "+v"(acc), "+v"(out)::"memory");
+            uint32_t nrow = row, nit = it + 1;
+            if (nit == ITERS) {
+                nrow = row + nw < row ? n : row + nw;
+                nit = 0;
+            }
+            more = nrow < n;
+            load_w<TYPE>(buf[(j + 1) & 1], row_base(more ? nrow : row), nsb, (int)(more ? nit : it), lane);
+            hold<TYPE>(buf[j & 1]);
+            const uint32_t sb = 16u * (uint32_t)its + (lane >> 2);
+            if (FULL || sb < nsb) {
+                if constexpr (kActRegs) {
+                    acc += lane_dot(decode_w<TYPE>(buf[j & 1], ss, q), act[its]);
+                } else {
+                    Act av;
+                    slice_from_lds<TYPE>(av, s, 0, sb, q);
+                    acc += lane_dot(decode_w<TYPE>(buf[j & 1], ss, q), av);
+                }
+            }
+            if (it == ITERS - 1) {
+                const float v = wave_sum_uniform(acc);
+                const bool mine = lane == (int)(done & 63u);
+                out = mine ? v : out;
+                out_row = mine ? row : out_row;
+                acc = 0.0f;
+                ++done;
+                if ((done & 63u) == 0u) {
+                    a.raw[0][out_row] = out;
+                    a.sum_out[out_row] = a.add[out_row] + out;
+                }
+            }
+            row = nrow;
+            it = nit;
+            if (!more) break;
+        }
+    }
+    if ((uint32_t)lane < (done & 63u)) {
+        a.raw[0][out_row] = out;
+        a.sum_out[out_row] = a.add[out_row] + out;
+    }
+}
+
+template <uint32_t TYPE, int ITERS, bool FULL>
+hipError_t launch_block_add_stream(const BlockGemv& a, hipStream_t s) {
+    const uint64_t lds = act_lds_bytes(a.mat[0].k, 1);
+    uint64_t wgs = (uint64_t)cu_count();
+    const uint64_t need = (a.mat[0].n + 15) / 16;
+    if (wgs > need) wgs = need;
+    hipLaunchKernelGGL((gemv_block_add_stream_kernel<TYPE, ITERS, FULL>), dim3((unsigned)wgs), dim3(1024), lds, s, a);
+    return hipGetLastError();
+}
+
 template <uint32_t TYPE, int ITERS, int MODE, bool FULL>
 hipError_t launch_block_full(const BlockGemv& a, hipStream_t s) {
+    if constexpr (MODE == kBlockAdd) {
+        // the residual projections without a normalising prologue stream like the plain decode
+        // GEMV (FFN down 4096 x 12288: 9.3 us against 11.1 us in the structure below)
+        if (a.norm_w == nullptr && env_int("OQ_BLOCK_STREAM", 1) != 0)
+            return launch_block_add_stream<TYPE, ITERS, FULL>(a, s);
+    }
     const uint64_t groups = MODE == kBlockFfn ? a.mat[0].n : ((uint64_t)a.row_end[a.nmat - 1] + 1) / 2;
     const uint64_t lds = act_lds_bytes(a.mat[0].k, 1);
     static int resident = 0;

@@ -128,23 +128,26 @@ SMALL = dict(synth.DELTANET_DIMS, embedding=1024, key_heads=2, value_heads=4, ff
     dict(SMALL, key_heads=4, key_dim=64, value_dim=64, value_heads=8, conv_kernel=3),
     dict(SMALL, value_dim=256, value_heads=2, key_heads=1),
 ], ids=["hk2_hv4", "dk64_dv64_k3", "dv256"])
-@pytest.mark.parametrize("fused", ["1", "0"], ids=["fused", "separate"])
-def test_deltanet_steps_match_oracle(ctx, dims, fused):
-    """Both device schedules: the fused one (five launches: normalised in-projections with the
+@pytest.mark.parametrize("env", [{"OQ_BLOCK_FUSED": "1"}, {"OQ_BLOCK_FUSED": "1", "OQ_BLOCK_STREAM": "0"},
+                                 {"OQ_BLOCK_FUSED": "0"}], ids=["fused", "fused_batched", "separate"])
+def test_deltanet_steps_match_oracle(ctx, dims, env):
+    """Every device schedule: the fused one (five launches: normalised in-projections with the
     convolution and gates, delta rule, out projection + residual, normalised gate/up + SwiGLU,
-    down + residual) and the one launch per stage (OQ_BLOCK_FUSED=0)."""
+    down + residual; the in- and residual projections streamed, or with OQ_BLOCK_STREAM=0 in the
+    batched structure) and the one launch per stage (OQ_BLOCK_FUSED=0)."""
     d, w, vec, hist, st, _ = synth.deltanet_block(np.random.default_rng(21), dims)
     rng = np.random.default_rng(22)
     xs = [rng.standard_normal(d["embedding"]).astype(np.float32) for _ in range(3)]
-    old = os.environ.get("OQ_BLOCK_FUSED")
-    os.environ["OQ_BLOCK_FUSED"] = fused
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
     try:
         steps, hist_g, st_g = run_gpu(ctx, d, w, vec, hist, st, xs)
     finally:
-        if old is None:
-            os.environ.pop("OQ_BLOCK_FUSED", None)
-        else:
-            os.environ["OQ_BLOCK_FUSED"] = old
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
     h_o, s_o = hist.copy(), st.copy()
     for i, stp in enumerate(steps):
         after = steps[i + 1]["state0"] if i + 1 < len(steps) else st_g
