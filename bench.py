@@ -97,6 +97,23 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
         "algorithmic_bytes": wb + xbytes + ybytes,
         "tops": 2.0 * m * n * k / (ms_step * 1e-3) / 1e12,
     }
+    if name == "q6k_head":
+        # greedy token over the head's logits, on the device (oq_argmax), timed on its own
+        tb, vb = ctx.alloc(4), ctx.alloc(4)
+        ctx.argmax(yb, n, tb, vb)
+        ctx.sync()
+        ctx.capture_begin()
+        for _ in range(steps):
+            ctx.argmax(yb, n, tb, vb)
+        ga = ctx.capture_end()
+        ga.launch()
+        ctx.sync()
+        ctx.timer_start()
+        ga.launch()
+        res["greedy_token_us"] = ctx.timer_stop() * 1e3 / steps
+        ga.destroy()
+        tb.free()
+        vb.free()
     for w in ws:
         w.release()
     xb.free()
@@ -276,6 +293,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(args.workload)},
         "us_per_gemv": round(main_res["us_per_step"], 3),
+        **({"greedy_token_us": round(main_res["greedy_token_us"], 3)} if "greedy_token_us" in main_res else {}),
         "hbm_frac_weight_bytes": round(gbs / HBM_PEAK_GBS, 4),
     }
     if secondary is not None:

@@ -126,6 +126,16 @@ int oq_dequantize_rows(oq_context* ctx, const oq_weight* w, uint64_t row0, uint6
    OQ_INVALID_ARGUMENT. */
 int oq_quantize_q8k(oq_context* ctx, const float* x_dev, uint64_t m, uint64_t k, void* q8k_dev);
 
+/* Replaces the greedy choice over a logits vector, Sampler::sample at temperature 0
+   (src/runtime/sampler.cpp:22-41) and the MTP argmax (src/runtime/qwen35_mtp.cpp:300-308), on
+   logits left in device memory by the head's oq_matvec: *token_dev = the first index of the
+   maximum of logits_dev[0..n), *value_dev = that maximum.  A NaN anywhere gives *token_dev =
+   0xFFFFFFFF (the reference rejects NaN logits); all -inf gives token 0 with value -inf (the
+   sampler rejects that, the MTP argmax returns 0).  Asynchronous on the context's stream,
+   graph-capturable.  Errors: OQ_INVALID_ARGUMENT for n == 0, n > 2^32 - 1, null or misaligned
+   buffers. */
+int oq_argmax(oq_context* ctx, const float* logits_dev, uint64_t n, uint32_t* token_dev, float* value_dev);
+
 /* ------------------------------------------------------------------ products */
 
 /* Replaces oracle::backend::cpu::reference_mapped_tensor_matvec / reference_storage_matvec

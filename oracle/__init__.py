@@ -283,6 +283,25 @@ def default_threads() -> int:
         return os.cpu_count() or 1
 
 
+# ---------------------------------------------------------------- greedy token
+
+def greedy_token(logits: np.ndarray) -> tuple[int, float]:
+    """Greedy sampling at temperature 0 (src/runtime/sampler.cpp:22-44): ValueError for an
+    empty vector, a NaN, or a maximum that is not finite; otherwise the first index holding the
+    maximum (strict '>' in index order, as also src/runtime/qwen35_mtp.cpp:300-308) and its value.
+    numpy's argmax returns the first occurrence of the maximum."""
+    logits = np.asarray(logits, np.float32)
+    if logits.size == 0:
+        raise ValueError("cannot sample an empty logits vector")
+    if np.isnan(logits).any():
+        raise ValueError("logits contain NaN")
+    i = int(np.argmax(logits))
+    if not np.isfinite(logits[i]):
+        raise ValueError("logits contain no finite candidates")
+    return i, float(logits[i])
+
+
+
 # ---------------------------------------------------------------- Gated DeltaNet block
 
 def sigmoid(v: float) -> float:

@@ -229,6 +229,9 @@ class Context:
     def quantize_q8k(self, x: DeviceBuffer, m: int, k: int, out: DeviceBuffer) -> None:
         self._call(self.lib.oq_quantize_q8k, self.h, x.ptr, m, k, out.ptr)
 
+    def argmax(self, logits: DeviceBuffer, n: int, token: DeviceBuffer, value: DeviceBuffer) -> None:
+        self._call(self.lib.oq_argmax, self.h, logits.ptr, n, token.ptr, value.ptr)
+
     def matvec(self, w: Weight, x: DeviceBuffer, y: DeviceBuffer) -> None:
         self._call(self.lib.oq_matvec, self.h, w.h, x.ptr, y.ptr)
 
@@ -266,6 +269,25 @@ class Context:
 
 
 # ---------------------------------------------------------------- reference-shaped helpers
+
+def greedy_token(ctx: Context, logits: DeviceBuffer, n: int) -> tuple[int, float]:
+    """Greedy token over n logits in device memory, with the reference sampler's errors
+    (src/runtime/sampler.cpp:22-44): InvalidArgument for NaN logits and for no finite candidate."""
+    tok = ctx.alloc(4)
+    val = ctx.alloc(4)
+    try:
+        ctx.argmax(logits, n, tok, val)
+        t = int(tok.download(np.uint32, 1)[0])
+        v = float(val.download(np.float32, 1)[0])
+    finally:
+        tok.free()
+        val.free()
+    if t == 0xFFFFFFFF:
+        raise InvalidArgument("logits contain NaN")
+    if not np.isfinite(v):
+        raise InvalidArgument("logits contain no finite candidates")
+    return t, v
+
 
 def storage_matvec(ctx: Context, type_id: int, rows: int, cols: int, matrix: np.ndarray,
                    vector: np.ndarray) -> np.ndarray:

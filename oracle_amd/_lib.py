@@ -43,6 +43,7 @@ SIGNATURES = [
     ("oq_weight_info", C.c_int, [_P, C.POINTER(_U32), C.POINTER(_U64), C.POINTER(_U64), C.POINTER(_U64)]),
     ("oq_dequantize_rows", C.c_int, [_P, _P, _U64, _U64, _P]),
     ("oq_quantize_q8k", C.c_int, [_P, _P, _U64, _U64, _P]),
+    ("oq_argmax", C.c_int, [_P, _P, _U64, _P, _P]),
     ("oq_matvec", C.c_int, [_P, _P, _P, _P]),
     ("oq_matvec_q8k", C.c_int, [_P, _P, _P, _P]),
     ("oq_matmul", C.c_int, [_P, _P, _U64, _P, _P]),

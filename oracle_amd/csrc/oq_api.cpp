@@ -49,6 +49,7 @@ struct oq_context {
     uint64_t scratch_bytes = 0;
     void* work = nullptr;  // intermediates of the DeltaNet block step
     uint64_t work_bytes = 0;
+    void* argmax_parts = nullptr;  // per-slice results of oq_argmax (kArgmaxParts * 12 bytes)
 };
 
 struct oq_weight {
@@ -461,6 +462,7 @@ int oq_context_create(int device, oq_context** out) {
     e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&ctx->t0);
     if (e == hipSuccess) e = hipEventCreate(&ctx->t1);
+    if (e == hipSuccess) e = hipMalloc(&ctx->argmax_parts, oq::kArgmaxParts * 12u);
     if (e != hipSuccess) {
         const int rc = hip_fail(nullptr, e, "context creation");
         oq_context_destroy(ctx);
@@ -476,6 +478,7 @@ void oq_context_destroy(oq_context* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->work) (void)hipFree(ctx->work);
+    if (ctx->argmax_parts) (void)hipFree(ctx->argmax_parts);
     if (ctx->t0) (void)hipEventDestroy(ctx->t0);
     if (ctx->t1) (void)hipEventDestroy(ctx->t1);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -580,6 +583,18 @@ int oq_quantize_q8k(oq_context* ctx, const float* x, uint64_t m, uint64_t k, voi
     }
     return launch_rc(ctx, oq::launch_quantize_q8k(x, m, k, static_cast<uint8_t*>(q8k), ctx->stream),
                      "quantize_q8k");
+}
+
+int oq_argmax(oq_context* ctx, const float* logits, uint64_t n, uint32_t* token, float* value) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    // checks in the order of Sampler::sample (src/runtime/sampler.cpp:22-28)
+    if (n == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "cannot sample an empty logits vector");
+    if (n > 0xFFFFFFFFull) return fail(ctx, OQ_INVALID_ARGUMENT, "logits vector exceeds token-id range");
+    if (!logits || !token || !value) return fail(ctx, OQ_INVALID_ARGUMENT, "null buffer");
+    if (!aligned(logits, 4) || !aligned(token, 4) || !aligned(value, 4)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "argmax buffers must be 4-byte aligned");
+    }
+    return launch_rc(ctx, oq::launch_argmax(logits, n, token, value, ctx->argmax_parts, ctx->stream), "argmax");
 }
 
 int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, float* y) {

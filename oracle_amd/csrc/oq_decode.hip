@@ -199,4 +199,107 @@ hipError_t launch_quantize_q8k(const float* x, uint64_t m, uint64_t k, uint8_t* 
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- greedy token (argmax)
+//
+// The reference's greedy choice over a logits vector (src/runtime/sampler.cpp:30-41,
+// src/runtime/qwen35_mtp.cpp:300-308): the first index holding the maximum (strict '>' in index
+// order).  Two launches: workgroup g scans its contiguous slice (thread t visits t, t + 256, ...
+// in increasing order and keeps its first maximum) and writes (value, index, NaN seen) to
+// part[g]; one workgroup then combines the slices.  Every combination keeps the larger value and,
+// on equal values, the smaller index, so the result is the first index of the maximum whatever
+// the order of combination.  A NaN anywhere (the sampler rejects it) makes the token 0xFFFFFFFF.
+namespace {
+
+constexpr int kArgmaxThreads = 256;
+
+struct ArgmaxPart {
+    float value;
+    uint32_t index;  // 0xFFFFFFFF: no element
+    uint32_t nan;
+};
+
+OQ_DEVICE void argmax_take(float& best, uint32_t& bi, float ov, uint32_t oi) {
+    const bool take = oi != 0xFFFFFFFFu && (bi == 0xFFFFFFFFu || ov > best || (ov == best && oi < bi));
+    best = take ? ov : best;
+    bi = take ? oi : bi;
+}
+
+// workgroup reduction of (best, bi, nan); the result is valid in thread 0
+OQ_DEVICE void argmax_block(float& best, uint32_t& bi, uint32_t& nan) {
+    __shared__ float sv[kArgmaxThreads / 64];
+    __shared__ uint32_t si[kArgmaxThreads / 64];
+    __shared__ uint32_t sn[kArgmaxThreads / 64];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const uint32_t oi = __shfl_xor(bi, off, 64);
+        nan |= __shfl_xor(nan, off, 64);
+        argmax_take(best, bi, ov, oi);
+    }
+    const uint32_t t = threadIdx.x;
+    if ((t & 63) == 0) {
+        sv[t >> 6] = best;
+        si[t >> 6] = bi;
+        sn[t >> 6] = nan;
+    }
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < kArgmaxThreads / 64; ++w) {
+            nan |= sn[w];
+            argmax_take(best, bi, sv[w], si[w]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_slice_kernel(const float* __restrict__ logits, uint32_t n,
+                                                                      uint32_t slice, ArgmaxPart* __restrict__ part) {
+    const uint64_t lo = (uint64_t)blockIdx.x * slice;
+    const uint64_t hi = lo + slice < n ? lo + slice : n;
+    float best = -__builtin_inff();
+    uint32_t bi = 0xFFFFFFFFu, nan = 0;
+    for (uint64_t i = lo + threadIdx.x; i < hi; i += kArgmaxThreads) {
+        const float v = logits[i];
+        nan |= v != v ? 1u : 0u;
+        // the first visited element is taken as is (the reference starts from logits[0]), later
+        // ones only when strictly larger
+        if (bi == 0xFFFFFFFFu || v > best) {
+            best = v;
+            bi = (uint32_t)i;
+        }
+    }
+    argmax_block(best, bi, nan);
+    if (threadIdx.x == 0) part[blockIdx.x] = ArgmaxPart{best, bi, nan};
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(const ArgmaxPart* __restrict__ part, uint32_t parts,
+                                                                      uint32_t* __restrict__ token, float* __restrict__ value) {
+    float best = -__builtin_inff();
+    uint32_t bi = 0xFFFFFFFFu, nan = 0;
+    for (uint32_t g = threadIdx.x; g < parts; g += kArgmaxThreads) {
+        const ArgmaxPart p = part[g];
+        nan |= p.nan;
+        argmax_take(best, bi, p.value, p.index);
+    }
+    argmax_block(best, bi, nan);
+    if (threadIdx.x == 0) {
+        *token = nan ? 0xFFFFFFFFu : bi;
+        *value = best;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_argmax(const float* logits, uint64_t n, uint32_t* token, float* value, void* partials,
+                         hipStream_t s) {
+    // slices of at least 1024 elements, at most kArgmaxParts of them
+    uint64_t parts = (n + 1023) / 1024;
+    if (parts > kArgmaxParts) parts = kArgmaxParts;
+    const uint64_t slice = (n + parts - 1) / parts;
+    auto* part = static_cast<ArgmaxPart*>(partials);
+    hipLaunchKernelGGL(argmax_slice_kernel, dim3((unsigned)parts), dim3(kArgmaxThreads), 0, s, logits, (uint32_t)n,
+                       (uint32_t)slice, part);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, part, (uint32_t)parts, token, value);
+    return hipGetLastError();
+}
+
 }  // namespace oq

@@ -54,6 +54,12 @@ int gemv_max_m();
 hipError_t launch_gemv_f32act(const DeviceMatrix& w, int m, const float* x, float* y,
                               hipStream_t s);
 
+// greedy token: first index of the maximum of logits[0..n) (n >= 1), its value; 0xFFFFFFFF on NaN.
+// partials: kArgmaxParts * 12 bytes of device memory (per-slice results; no initial contents)
+constexpr uint32_t kArgmaxParts = 256;
+hipError_t launch_argmax(const float* logits, uint64_t n, uint32_t* token, float* value, void* partials,
+                         hipStream_t s);
+
 // ---- oq_gemm.hip  (m >= 16, q4_K, K >= 4096: F16 matrix cores on F16-rounded operands)
 // Activations are given either as F32 (x; quantized to Q8_K inside, bit-identical to
 // launch_quantize_q8k) or as Q8_K blocks (q8k); exactly one of the two is non-null.
