@@ -810,8 +810,9 @@ hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8
                         : launch_stream<TYPE, ITERS, FUSED, 8, false>(w, x, q8k, y, s);
         }
     }
-    if constexpr (MT > 1 && !FUSED && !(TYPE == 13 && MT == 8)) {
-        // small batches from Q8_K blocks (the default for m > 1): streamed, one pass in flight
+    if constexpr (MT > 1 && !(TYPE == 13 && MT == 8)) {
+        // small batches (from Q8_K blocks, or F32 rows quantized in the staging): streamed, one
+        // pass in flight
         // (q5_K with eight rows would spill within the 128 registers of a 16-wave workgroup)
         if (act_lds_bytes(w.k, MT) <= kLdsBudget && env_int("OQ_GEMV_STREAM_MT", 1) != 0) {
             return (w.k / kQK) % 16 == 0 ? launch_stream_mt<TYPE, ITERS, MT, FUSED, true>(w, m, x, q8k, y, s)

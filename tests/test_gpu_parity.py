@@ -382,9 +382,10 @@ def test_q8_0_decode_gemv(ctx, rows, cols):
 @pytest.mark.parametrize("t,rows,cols,m", [(12, 4096, 12288, 4), (12, 5000, 1280, 3), (13, 700, 4096, 2),
                                            (14, 8269, 512, 8), (14, 300, 8192, 5), (12, 9000, 4096, 7)])
 def test_small_batch_streamed_kernel(ctx, t, rows, cols, m):
-    """Small batches from Q8_K blocks run the streamed kernel (one weight pass in flight per
-    wave, m activation rows in LDS); it gives the batched kernel's bits (OQ_GEMV_STREAM_MT=0),
-    including several rows per wave, K not a multiple of 4096 and m below the tier size."""
+    """Small batches run the streamed kernel (one weight pass in flight per wave, m activation
+    rows in LDS); it gives the batched kernel's bits (OQ_GEMV_STREAM_MT=0), also when it
+    quantizes the F32 rows itself (OQ_FUSED_QUANT=1), including several rows per wave, K not a
+    multiple of 4096 and m below the tier size."""
     rng = np.random.default_rng(6060 + t + rows + m)
     data = synth.weights(t, rng, rows, cols)
     x = rng.standard_normal((m, cols)).astype(np.float32)
@@ -392,20 +393,24 @@ def test_small_batch_streamed_kernel(ctx, t, rows, cols, m):
     xb = ctx.to_device(x)
     yb = ctx.alloc(m * rows * 4)
     runs = []
-    for flag in ("1", "0"):
-        old = os.environ.get("OQ_GEMV_STREAM_MT")
-        os.environ["OQ_GEMV_STREAM_MT"] = flag
+    # streamed, batched, and streamed with the quantization inside the kernel's staging
+    for env in ({"OQ_GEMV_STREAM_MT": "1"}, {"OQ_GEMV_STREAM_MT": "0"},
+                {"OQ_GEMV_STREAM_MT": "1", "OQ_FUSED_QUANT": "1"}):
+        old = {k: os.environ.get(k) for k in env}
+        os.environ.update(env)
         try:
             yb.upload(np.full(m * rows, np.nan, np.float32))
             ctx.matmul(w, m, xb, yb)
             ctx.sync()
         finally:
-            if old is None:
-                os.environ.pop("OQ_GEMV_STREAM_MT", None)
-            else:
-                os.environ["OQ_GEMV_STREAM_MT"] = old
+            for k, v in old.items():
+                if v is None:
+                    os.environ.pop(k, None)
+                else:
+                    os.environ[k] = v
         runs.append(yb.download(np.float32, m * rows).reshape(m, rows))
-    assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
+    for r in runs[1:]:
+        assert np.array_equal(runs[0].view(np.uint32), r.view(np.uint32))
     pick = np.array(sorted(set([0, m - 1])))
     y_ref, norm = reference_products(t, rows, cols, data, x[pick])
     check_close(runs[0][pick], y_ref, norm)
