@@ -227,6 +227,31 @@ void test_against_oracle(QuantizedDevice& dev, std::uint32_t type, std::size_t r
         }
 }
 
+// greedy token against the reference's loop (first index of the strict maximum) and the
+// sampler's errors
+void test_greedy_token(QuantizedDevice& dev) {
+    require(dev.greedy_token(std::vector<float>{1.0F, 5.0F, 5.0F, 2.0F}) == 1, "ties: the first index");
+    require(dev.greedy_token(std::vector<float>{-3.0F}) == 0, "one logit");
+    const float inf = std::numeric_limits<float>::infinity();
+    require_throws<std::invalid_argument>([&] { (void)dev.greedy_token(std::vector<float>{}); }, "empty logits");
+    require_throws<std::invalid_argument>(
+        [&] { (void)dev.greedy_token(std::vector<float>{1.0F, std::nanf("")}); }, "NaN logits");
+    require_throws<std::invalid_argument>([&] { (void)dev.greedy_token(std::vector<float>{-inf, -inf}); },
+                                          "no finite candidate");
+    std::vector<float> v(151936);
+    std::uint64_t s = 0x9E3779B97F4A7C15ull;
+    for (float& e : v) {
+        s ^= s << 13;
+        s ^= s >> 7;
+        s ^= s << 17;
+        e = static_cast<float>(static_cast<int>(s % 2001) - 1000);  // many ties
+    }
+    std::size_t best = 0;
+    for (std::size_t i = 1; i < v.size(); ++i)
+        if (v[i] > v[best]) best = i;
+    require(dev.greedy_token(v) == best, "greedy token matches the reference loop");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -239,6 +264,7 @@ int main(int argc, char** argv) {
             test_against_oracle(dev, 12, 300, 4096);
             test_against_oracle(dev, 14, 130, 2048);
             test_against_oracle(dev, 8, 200, 4096);
+            test_greedy_token(dev);
             require(dev.resident_count() == 3 + 4, "one resident copy per distinct tensor");
         }
         std::cout << "host adapter tests passed (" << (gpu ? "gpu" : "cpu") << ")\n";

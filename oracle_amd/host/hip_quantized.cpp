@@ -1,6 +1,7 @@
 // Implementation of the C++20 host adapter over liboq.so (see hip_quantized.hpp).
 #include "hip_quantized.hpp"
 
+#include <cmath>
 #include <cstring>
 #include <string>
 
@@ -133,6 +134,25 @@ float QuantizedDevice::storage_dot(StorageRowView row, std::span<const float> ve
     float out = 0.0F;
     storage_matvec(row.type, 1, row.element_count, row.bytes, vector, std::span<float>(&out, 1));
     return out;
+}
+
+std::uint32_t QuantizedDevice::greedy_token(std::span<const float> logits) {
+    // the sampler's argument checks, in its order (src/runtime/sampler.cpp:23-28)
+    if (logits.empty()) throw std::invalid_argument("cannot sample an empty logits vector");
+    if (logits.size() > std::numeric_limits<std::uint32_t>::max()) {
+        throw std::invalid_argument("logits vector exceeds token-id range");
+    }
+    float* x = device_floats(x_dev_, x_cap_, logits.size());
+    float* t = device_floats(t_dev_, t_cap_, 2);  // [0]: token bits, [1]: value
+    check(oq_copy_to_device(ctx_, x, logits.data(), logits.size_bytes()), ctx_);
+    check(oq_argmax(ctx_, x, logits.size(), reinterpret_cast<std::uint32_t*>(t), t + 1), ctx_);
+    std::uint32_t token = 0;
+    float value = 0.0F;
+    check(oq_copy_to_host(ctx_, &token, t, sizeof(token)), ctx_);
+    check(oq_copy_to_host(ctx_, &value, t + 1, sizeof(value)), ctx_);
+    if (token == 0xFFFFFFFFu) throw std::invalid_argument("logits contain NaN");
+    if (!std::isfinite(value)) throw std::invalid_argument("logits contain no finite candidates");
+    return token;
 }
 
 void QuantizedDevice::decode_rows(std::uint32_t type, std::size_t rows, std::size_t cols,

@@ -102,6 +102,12 @@ public:
     void decode_rows(std::uint32_t type, std::size_t row_count, std::size_t column_count,
                      std::span<const std::byte> matrix_bytes, std::span<float> output);
 
+    // Greedy token of Sampler::sample at temperature 0 (src/runtime/sampler.cpp:22-44): the
+    // first index of the maximum, std::invalid_argument for an empty vector, a NaN or no finite
+    // candidate.  Computed on the device by oq_argmax (on a model path the logits stay in HBM and
+    // oq_argmax is called on them directly).
+    [[nodiscard]] std::uint32_t greedy_token(std::span<const float> logits);
+
     // Device-resident access for callers that keep activations in HBM (chained layers).
     const oq_weight* resident(std::uint32_t type, std::size_t row_count, std::size_t column_count,
                               std::span<const std::byte> matrix_bytes);
@@ -135,6 +141,8 @@ private:
     std::size_t x_cap_ = 0;
     void* y_dev_ = nullptr;
     std::size_t y_cap_ = 0;
+    void* t_dev_ = nullptr;  // greedy token and its value
+    std::size_t t_cap_ = 0;
 };
 
 }  // namespace oracle::backend::hip
