@@ -34,6 +34,7 @@ QuantizedDevice::~QuantizedDevice() {
     if (ctx_) {
         if (x_dev_) (void)oq_device_free(ctx_, x_dev_);
         if (y_dev_) (void)oq_device_free(ctx_, y_dev_);
+        if (t_dev_) (void)oq_device_free(ctx_, t_dev_);
         oq_context_destroy(ctx_);
     }
 }
