@@ -128,11 +128,18 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
     __shared__ double red[16];
     const uint32_t h = blockIdx.x, v = threadIdx.x;
     float* col = state + (uint64_t)h * DK * dv + v;
+    const uint32_t kw = key_heads * DK;
+    // every input is requested here, before the first barrier: a load issued after a barrier
+    // would add one more memory round trip to the kernel's chain
+    const float vv = conv[2u * kw + (uint64_t)h * dv + v];
+    const float zv = z[(uint64_t)h * dv + v];
+    const float onw = out_norm[v];
+    const float ldh = log_decay[h];
+    const float beta = beta_s[h];
     float s[DK];
 #pragma unroll
     for (int d = 0; d < DK; ++d) s[d] = col[(uint64_t)d * dv];
 
-    const uint32_t kw = key_heads * DK;
     const float* q = conv + (uint64_t)(h % key_heads) * DK;
     const float* k = conv + kw + (uint64_t)(h % key_heads) * DK;
     double qs = 0.0, ks = 0.0;
@@ -152,8 +159,7 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
     }
     __syncthreads();
 
-    const float decay = expf(log_decay[h]);
-    const float beta = beta_s[h];
+    const float decay = expf(ldh);
     const float4* nk4 = reinterpret_cast<const float4*>(nk);
     const float4* nq4 = reinterpret_cast<const float4*>(nq);
     // the empty asm statements keep each chunk's LDS reads next to their use, so the unrolled
@@ -170,7 +176,6 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
             mem = mem + s[d + i] * kv[i];
         }
     }
-    const float vv = conv[2u * kw + (uint64_t)h * dv + v];
     const float delta = (vv - mem) * beta;
     double o = 0.0;
 #pragma unroll
@@ -189,8 +194,8 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
     rec_out[(uint64_t)h * dv + v] = of;
     const double ss = block_sum_f64((double)of * (double)of, red);
     const float inv = (float)(1.0 / sqrt(ss / (double)dv + (double)eps));
-    const float g = silu_ref(z[(uint64_t)h * dv + v]);
-    gated[(uint64_t)h * dv + v] = of * inv * out_norm[v] * g;
+    const float g = silu_ref(zv);
+    gated[(uint64_t)h * dv + v] = of * inv * onw * g;
 }
 
 // act = silu(gate) * up (qwen35_block.cpp:313-316)
