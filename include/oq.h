@@ -81,6 +81,10 @@ const char* oq_last_error(const oq_context* ctx);
 int oq_synchronize(oq_context* ctx);
 /* The context's hipStream_t, for callers that interleave their own work. */
 void* oq_context_stream(oq_context* ctx);
+/* Launch-shape options (environment variables OQ_GEMV_*, OQ_GEMM_*, OQ_BLOCK_*, ... selecting
+   alternative kernel schedules for measurement) are read once, when the first context is
+   created; this re-reads them.  No reference counterpart.  Not thread-safe with launches. */
+void oq_reload_options(void);
 
 /* Device memory helpers (so callers need no other GPU runtime). */
 int oq_device_alloc(oq_context* ctx, uint64_t bytes, void** out_dev);
@@ -174,7 +178,8 @@ int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q
    reference's SsmState buffers, hybrid_cache.hpp:76-120) are updated in place.  trace_dev, if
    not NULL, receives the intermediates in this order (F32, packed):
      qkv[C] z[Hv*dv] beta[Hv] alpha[Hv] conv[C] out[Hv*dv] gated[Hv*dv] branch[E] resid[E]
-     post[E] gate[F] up[F] act[F] ffn[E]       with C = 2*Hk*dk + Hv*dv.
+     post[E] gate[F] up[F] act[F] ffn[E] beta_s[Hv] log_decay[Hv]      with C = 2*Hk*dk + Hv*dv,
+     beta_s = sigmoid(beta), log_decay = softplus(alpha + dt_bias) * decay.
    Device path limits: dk in {32, 64, 128}, dv in {64, 128, 192, 256}, conv_kernel <= 16, K-quant rows
    <= 16384; otherwise OQ_INVALID_ARGUMENT.  Weight shape mismatches -> OQ_INVALID_ARGUMENT. */
 typedef struct oq_deltanet_block {
@@ -200,7 +205,11 @@ int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* block, float* con
 int oq_timer_start(oq_context* ctx);
 int oq_timer_stop(oq_context* ctx, float* elapsed_ms); /* waits for the stop event */
 
-/* Capture every oq_* launch on ctx between begin and end into a replayable HIP graph. */
+/* Capture every oq_* launch on ctx between begin and end into a replayable HIP graph.  Run each
+   captured call once eagerly first: a call that would have to grow the context's workspace
+   during capture fails with OQ_INVALID_ARGUMENT.  A graph keeps the workspace it captured: when
+   a later eager call grows it, the old allocation is kept until the context's last graph is
+   destroyed.  Destroy a context's graphs before the context. */
 int oq_capture_begin(oq_context* ctx);
 int oq_capture_end(oq_context* ctx, oq_graph** out);
 int oq_graph_launch(oq_context* ctx, oq_graph* g);

@@ -65,6 +65,8 @@ _REF_SIGS = [
     ("ref_storage_matvec_rows", C.c_int, [_U32, _U64, _P, _U64, _U64, _U64, _P, _P]),
     ("ref_conv_step", C.c_int, [_U64, _U64, _P, _P, _P, _P, C.c_int]),
     ("ref_gated_delta_step", C.c_int, [_U64, _U64, _U64, _P, _P, _P, _P, _P, C.c_float, _P, _P]),
+    ("ref_recurrent_block", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
+    ("ref_block_trace_value", C.c_int64, [C.c_char_p, _P, _U64]),
 ]
 
 
@@ -355,14 +357,15 @@ class _DNBlock(C.Structure):
 
 DN_WEIGHTS = ("qkv", "z", "beta", "alpha", "out", "gate", "up", "down")
 DN_VECTORS = ("input_norm", "conv_weight", "dt_bias", "decay", "out_norm", "post_norm")
-DN_TRACE = ("qkv", "z", "beta", "alpha", "conv", "rec", "gated", "branch", "resid", "post", "gate", "up", "act", "ffn")
+DN_TRACE = ("qkv", "z", "beta", "alpha", "conv", "rec", "gated", "branch", "resid", "post", "gate", "up", "act", "ffn",
+            "beta_s", "log_decay")
 
 
 def deltanet_trace_sizes(dims: dict) -> dict:
     C_ = 2 * dims["key_heads"] * dims["key_dim"] + dims["value_heads"] * dims["value_dim"]
     V = dims["value_heads"] * dims["value_dim"]
     E, F, Hv = dims["embedding"], dims["ffn"], dims["value_heads"]
-    return dict(zip(DN_TRACE, (C_, V, Hv, Hv, C_, V, V, E, E, E, F, F, F, E)))
+    return dict(zip(DN_TRACE, (C_, V, Hv, Hv, C_, V, V, E, E, E, F, F, F, E, Hv, Hv)))
 
 
 def deltanet_step(dims: dict, weights: dict, vectors: dict, conv_history: np.ndarray, state: np.ndarray,
@@ -396,3 +399,62 @@ def deltanet_step(dims: dict, weights: dict, vectors: dict, conv_history: np.nda
         out[n] = tr[off:off + sz]
         off += sz
     return y, out
+
+
+class _RefDNBlock(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("embedding", "key_heads", "value_heads", "key_dim", "value_dim",
+                                          "conv_kernel", "ffn")] + [("eps", C.c_float)] + \
+               [("types", C.c_uint32 * 8), ("weights", C.c_void_p * 8)] + \
+               [(n, C.c_void_p) for n in DN_VECTORS]
+
+
+def ref_recurrent_block(dims: dict, weights: dict, vectors: dict, conv_history: np.ndarray, state: np.ndarray,
+                        x: np.ndarray, overrides: dict | None = None):
+    """The reference's own recurrent block (execute_qwen35_recurrent_block_reference) on in-memory
+    views.  Same arguments as deltanet_step; overrides maps projection names (DN_WEIGHTS) to F32
+    outputs that replace the reference's matvec for that projection.  conv_history and state are
+    updated in place.  Returns (y, trace dict with the fields of deltanet_step)."""
+    b = _RefDNBlock()
+    for k_ in ("embedding", "key_heads", "value_heads", "key_dim", "value_dim", "conv_kernel", "ffn"):
+        setattr(b, k_, int(dims[k_]))
+    b.eps = float(dims["eps"])
+    keep = []
+    for i, n in enumerate(DN_WEIGHTS):
+        t, data = weights[n]
+        a = np.ascontiguousarray(data, dtype=np.uint8)
+        keep.append(a)
+        b.types[i] = int(t)
+        b.weights[i] = a.ctypes.data
+    for n in DN_VECTORS:
+        a = np.ascontiguousarray(vectors[n], dtype=np.float32)
+        keep.append(a)
+        setattr(b, n, a.ctypes.data)
+    ov = None
+    if overrides:
+        ov = (C.c_void_p * 8)()
+        for i, n in enumerate(DN_WEIGHTS):
+            if n in overrides:
+                a = np.ascontiguousarray(overrides[n], dtype=np.float32)
+                keep.append(a)
+                ov[i] = a.ctypes.data
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(int(dims["embedding"]), dtype=np.float32)
+    sizes = deltanet_trace_sizes(dims)
+    tr = np.empty(sum(sizes.values()), dtype=np.float32)
+    _chk(ref().ref_recurrent_block(C.byref(b), _ptr(conv_history), _ptr(state), _ptr(xv), _ptr(y), _ptr(tr),
+                                   ov), ref(), "ref_last_error")
+    out, off = {}, 0
+    for n, sz in sizes.items():
+        out[n] = tr[off:off + sz]
+        off += sz
+    return y, out
+
+
+def ref_block_trace_value(name: str) -> np.ndarray:
+    """A named trace tensor of the last ref_recurrent_block call (the reference's own names)."""
+    n = int(ref().ref_block_trace_value(name.encode(), None, 0))
+    if n < 0:
+        raise KeyError(name)
+    out = np.empty(n, dtype=np.float32)
+    ref().ref_block_trace_value(name.encode(), _ptr(out), n)
+    return out

@@ -757,7 +757,7 @@ static int block_matvec(uint32_t type, const uint8_t* w, uint64_t rows, uint64_t
 uint64_t orc_deltanet_trace_size(const orc_deltanet_block* b) {
     const uint64_t C = 2 * b->key_heads * b->key_dim + b->value_heads * b->value_dim;
     const uint64_t V = b->value_heads * b->value_dim;
-    return 2 * C + 3 * V + 2 * b->value_heads + 4 * b->embedding + 3 * b->ffn;
+    return 2 * C + 3 * V + 4 * b->value_heads + 4 * b->embedding + 3 * b->ffn;
 }
 
 /* qwen35_block.cpp:406-605 (recurrent block), :326-352 (finish_block), :296-324 (MLP) */
@@ -768,7 +768,7 @@ int orc_deltanet_step(const orc_deltanet_block* b, float* conv_history, float* s
     if (E == 0 || Hk == 0 || Hv == 0 || dk == 0 || dv == 0 || F == 0 || b->conv_kernel == 0 || Hv % Hk != 0)
         return fail(ORC_INVALID_ARGUMENT, "Qwen3.5 recurrent block dimensions are incompatible");
     const uint64_t KW = Hk * dk, V = Hv * dv, C = 2 * KW + V;
-    float* buf = (float*)calloc(orc_deltanet_trace_size(b) + 2 * Hv + E + 2 * Hv * dk, sizeof(float));
+    float* buf = (float*)calloc(orc_deltanet_trace_size(b) + E + 2 * Hv * dk, sizeof(float));
     if (!buf) return fail(ORC_RUNTIME_ERROR, "out of memory");
     float *qkv = buf, *z = qkv + C, *beta = z + V, *alpha = beta + Hv, *conv = alpha + Hv, *rec = conv + C,
           *gated = rec + V, *branch = gated + V, *resid = branch + E, *post = resid + E, *gate = post + E,

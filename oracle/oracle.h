@@ -144,9 +144,10 @@ typedef struct orc_deltanet_block {
 } orc_deltanet_block;
 
 /* intermediates, in order (NULL to skip); sizes: C = 2*Hk*dk + Hv*dv, V = Hv*dv, F = ffn */
-enum { ORC_DN_TRACE_FIELDS = 14 };
+enum { ORC_DN_TRACE_FIELDS = 16 };
 /* trace layout: qkv[C] z[V] beta[Hv] alpha[Hv] conv[C] rec[V] gated[V] branch[E] resid[E]
-   post[E] gate[F] up[F] act[F] ffn[E] */
+   post[E] gate[F] up[F] act[F] ffn[E] beta_s[Hv] log_decay[Hv]  (beta_s = sigmoid(beta),
+   log_decay = softplus(alpha + dt_bias) * decay: the reference's "beta_sigmoid" and "gate") */
 uint64_t orc_deltanet_trace_size(const orc_deltanet_block* b);
 int orc_deltanet_step(const orc_deltanet_block* b, float* conv_history, float* state,
                       const float* x, float* y, float* trace, int threads);

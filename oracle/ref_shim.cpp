@@ -1,8 +1,9 @@
 // ORACLE -- test infrastructure, not product code.
 //
-// A C-callable shim over the reference engine's own quantized path, compiled together with
-// the reference's sources (ggml_type.cpp, storage_decode.cpp, quantized_reference.cpp and the
-// GgufTensorView they take) into oracle/_ref/libref.so by oracle/Makefile.  It lets the tests
+// A C-callable shim over the reference engine's own quantized path and Qwen3.5 block kernels,
+// compiled together with the reference's sources (ggml_type.cpp, storage_decode.cpp,
+// quantized_reference.cpp, the GgufTensorView they take, reference_kernels.cpp, qwen35_block.cpp
+// and what they link) into oracle/_ref/libref.so by oracle/Makefile.  It lets the tests
 // compare the C restatement (oracle.c) with the reference itself, bit for bit, and lets the
 // benchmark time the reference's CPU path.  Exceptions are caught and returned as the same
 // status codes the restatement uses.
@@ -14,6 +15,8 @@
 #include "oracle/core/tensor.hpp"
 #include "oracle/runtime/hybrid_cache.hpp"
 #include "oracle/runtime/reference_kernels.hpp"
+#include "oracle/runtime/qwen35_block.hpp"
+#include "oracle/model/qwen35_weights.hpp"
 
 #include <cstdio>
 #include <cstring>
@@ -188,5 +191,152 @@ int ref_gated_delta_step(std::uint64_t heads, std::uint64_t dk, std::uint64_t dv
         std::copy(r.begin(), r.end(), state);
         std::copy(to.data().begin(), to.data().end(), out);
     });
+}
+}  // extern "C"
+
+// ---------------------------------------------------------------- the reference's recurrent block
+//
+// execute_qwen35_recurrent_block_reference (src/runtime/qwen35_block.cpp:406-605) driven on
+// in-memory GgufTensorViews, as the reference's own block test builds them
+// (tests/test_phase2c.cpp:72-213).  The block description has the layout of the oracle's
+// orc_deltanet_block; projection weights may be any type the reference decodes (or q4_K when
+// that projection is overridden).  `overrides`, if not NULL, holds 8 pointers in the order
+// qkv, z, beta, alpha, out, gate, up, down; a non-NULL entry replaces that projection's output
+// through the reference's Qwen35MatvecOverrides.  `trace`, if not NULL, receives the oracle's 16
+// trace fields (qkv z beta alpha conv rec gated branch resid post gate up act ffn beta_s
+// log_decay) taken from the
+// reference's named trace; every named trace tensor of the last call stays readable through
+// ref_block_trace_value.
+struct RefDeltaNetBlock {
+    std::uint64_t embedding, key_heads, value_heads, key_dim, value_dim, conv_kernel, ffn;
+    float eps;
+    std::uint32_t types[8];
+    const std::uint8_t* weights[8];
+    const float *input_norm, *conv_weight, *dt_bias, *decay, *out_norm, *post_norm;
+};
+
+namespace {
+
+std::vector<oracle::runtime::Qwen35TraceTensor> g_trace;
+
+struct ViewStore {
+    std::vector<oracle::model::GgufTensorInfo> infos;
+    std::vector<oracle::model::GgufTensorView> views;
+    ViewStore() {
+        infos.reserve(32);
+        views.reserve(32);
+    }
+    const oracle::model::GgufTensorView* add(std::string name, std::vector<std::uint64_t> dims, std::uint32_t type,
+                                             const void* data) {
+        const auto* layout = oracle::model::ggml_type_layout(type);
+        if (layout == nullptr) throw std::runtime_error("unregistered type");
+        std::uint64_t elements = 1;
+        for (auto d : dims) elements *= d;
+        const std::uint64_t bytes = elements / layout->block_elements * layout->bytes_per_block;
+        infos.push_back({std::move(name), std::move(dims), type, 0});
+        views.emplace_back(&infos.back(), layout, static_cast<const std::byte*>(data),
+                           static_cast<std::size_t>(bytes), 0);
+        return &views.back();
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int ref_recurrent_block(const RefDeltaNetBlock* b, float* conv_history, float* state, const float* x, float* y,
+                        float* trace, const float* const* overrides) {
+    return guarded([&] {
+        const std::uint64_t E = b->embedding, Hk = b->key_heads, Hv = b->value_heads, dk = b->key_dim,
+                            dv = b->value_dim, K = b->conv_kernel, F = b->ffn;
+        const std::uint64_t V = Hv * dv, C = 2 * Hk * dk + V;
+        oracle::model::Qwen35Manifest m;
+        m.architecture = "qwen35";
+        m.embedding_length = static_cast<std::uint32_t>(E);
+        m.feed_forward_length = static_cast<std::uint32_t>(F);
+        m.attention_rms_epsilon = b->eps;
+        m.ssm_convolution_kernel = static_cast<std::uint32_t>(K);
+        m.ssm_state_size = static_cast<std::uint32_t>(dk);
+        m.ssm_group_count = static_cast<std::uint32_t>(Hk);
+        m.ssm_time_step_rank = static_cast<std::uint32_t>(Hv);
+        m.ssm_inner_size = static_cast<std::uint32_t>(V);
+        ViewStore vs;
+        // {dimensions[0] = columns, dimensions[1] = rows}, as GGUF stores a matrix
+        const std::uint64_t cols[8] = {E, E, E, E, V, E, E, F};
+        const std::uint64_t rows[8] = {C, V, Hv, Hv, E, F, F, E};
+        const char* names[8] = {"qkv", "z", "beta", "alpha", "out", "gate", "up", "down"};
+        const oracle::model::GgufTensorView* w[8];
+        for (int i = 0; i < 8; ++i) w[i] = vs.add(names[i], {cols[i], rows[i]}, b->types[i], b->weights[i]);
+        oracle::model::Qwen35BackboneBlockWeights blk;
+        blk.index = 0;
+        blk.kind = oracle::model::Qwen35BlockKind::recurrent;
+        blk.input_norm = vs.add("input_norm", {E}, 0, b->input_norm);
+        blk.post_attention_norm = vs.add("post_norm", {E}, 0, b->post_norm);
+        blk.mlp.gate = w[5];
+        blk.mlp.up = w[6];
+        blk.mlp.down = w[7];
+        oracle::model::Qwen35RecurrentWeights rw;
+        rw.qkv = w[0];
+        rw.gate = w[1];
+        rw.beta = w[2];
+        rw.alpha = w[3];
+        rw.output = w[4];
+        rw.convolution = vs.add("conv", {K, C}, 0, b->conv_weight);
+        rw.time_step_bias = vs.add("dt_bias", {Hv}, 0, b->dt_bias);
+        rw.decay = vs.add("decay", {Hv}, 0, b->decay);
+        rw.norm = vs.add("norm", {dv}, 0, b->out_norm);
+        blk.recurrent = rw;
+
+        oracle::runtime::SsmState st(static_cast<std::size_t>(C), static_cast<std::size_t>(K),
+                                     static_cast<std::size_t>(Hv), static_cast<std::size_t>(dk),
+                                     static_cast<std::size_t>(dv));
+        auto h = st.convolution_history();
+        std::copy(conv_history, conv_history + C * K, h.begin());
+        auto r = st.recurrent();
+        std::copy(state, state + Hv * dk * dv, r.begin());
+
+        oracle::runtime::Qwen35MatvecOverrides ov;
+        if (overrides != nullptr) {
+            const char* trace_names[8] = {"linear_attn_qkv_mixed", "z", "beta", "alpha",
+                                          "linear_attn_out", "ffn_gate", "ffn_up", "ffn_out"};
+            for (int i = 0; i < 8; ++i) {
+                if (overrides[i] == nullptr) continue;
+                ov.tensors.push_back({trace_names[i], std::vector<float>(overrides[i], overrides[i] + rows[i])});
+            }
+        }
+        auto res = oracle::runtime::execute_qwen35_recurrent_block_reference(
+            m, blk, std::span<const float>(x, static_cast<std::size_t>(E)), st, true,
+            overrides != nullptr ? &ov : nullptr);
+        std::copy(res.output.begin(), res.output.end(), y);
+        std::copy(h.begin(), h.end(), conv_history);
+        std::copy(r.begin(), r.end(), state);
+        g_trace = res.trace.tensors;
+        if (trace != nullptr) {
+            const char* fields[16] = {"linear_attn_qkv_mixed", "z", "beta", "alpha", "conv_output_silu",
+                                      "recurrent_output", "attn_out_norm", "linear_attn_out", "attn_residual",
+                                      "attn_post_norm", "ffn_gate", "ffn_up", "ffn_swiglu", "ffn_out",
+                                      "beta_sigmoid", "gate"};
+            std::uint64_t off = 0;
+            for (const char* f : fields) {
+                const auto* t = res.trace.find(f);
+                if (t == nullptr) throw std::runtime_error(std::string("reference trace lacks ") + f);
+                std::copy(t->values.begin(), t->values.end(), trace + off);
+                off += t->values.size();
+            }
+        }
+    });
+}
+
+// Named trace tensor of the last ref_recurrent_block call: copies up to cap values, returns the
+// tensor's length (or -1 when the name is absent).
+std::int64_t ref_block_trace_value(const char* name, float* out, std::uint64_t cap) {
+    for (const auto& t : g_trace) {
+        if (t.name == name) {
+            const std::uint64_t n = t.values.size() < cap ? t.values.size() : cap;
+            std::copy(t.values.begin(), t.values.begin() + static_cast<std::ptrdiff_t>(n), out);
+            return static_cast<std::int64_t>(t.values.size());
+        }
+    }
+    return -1;
 }
 }  // extern "C"

@@ -13,7 +13,9 @@ oracle::backend::cpu quantized functions.  Errors surface as the reference's exc
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
+import os
 from dataclasses import dataclass
 
 import numpy as np
@@ -74,6 +76,25 @@ def _check(rc: int, ctx_handle=None) -> None:
     lib = _lib.load()
     msg = lib.oq_last_error(ctx_handle).decode(errors="replace")
     raise _BY_CODE.get(rc, OqError)(msg)
+
+
+@contextlib.contextmanager
+def launch_options(env: dict):
+    """Run a block with the given OQ_* launch options set (they select alternative kernel
+    schedules; the library reads them once per oq_reload_options), restoring them afterwards."""
+    lib = _lib.load()
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
+    lib.oq_reload_options()
+    try:
+        yield
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        lib.oq_reload_options()
 
 
 # ---------------------------------------------------------------- registry

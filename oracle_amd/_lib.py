@@ -32,6 +32,7 @@ SIGNATURES = [
     ("oq_last_error", C.c_char_p, [_P]),
     ("oq_synchronize", C.c_int, [_P]),
     ("oq_context_stream", _P, [_P]),
+    ("oq_reload_options", None, []),
     ("oq_device_alloc", C.c_int, [_P, _U64, C.POINTER(_P)]),
     ("oq_device_free", C.c_int, [_P, _P]),
     ("oq_copy_to_device", C.c_int, [_P, _P, _P, _U64]),

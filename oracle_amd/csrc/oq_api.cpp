@@ -11,17 +11,46 @@
 #include <cstdlib>
 #include <cstring>
 #include <cmath>
+#include <algorithm>
 #include <string>
+#include <vector>
 
 #include "../../include/oq.h"
 #include "oq_internal.h"
+#include "oq_workspace.h"
 
 namespace oq {
 
-int env_int(const char* name, int fallback) {
-    const char* v = getenv(name);
-    return v ? atoi(v) : fallback;
+namespace {
+
+constexpr const char* kKnobNames[kKnobCount] = {
+    "OQ_GEMM_SPLITS",   "OQ_GEMM_EXACT_DEQUANT", "OQ_GEMM_WS",     "OQ_GEMV_MAX_WG",   "OQ_Q8_0_ROWS",
+    "OQ_GEMV_WG_PER_CU", "OQ_STREAM_WG_PER_CU",  "OQ_GEMV_STREAM", "OQ_STREAM_WAVES",  "OQ_GEMV_STREAM_MT",
+    "OQ_GEMV_ROWS",     "OQ_GEMV_WAVES",         "OQ_GEMV_ROWS_MT", "OQ_BLOCK_STREAM", "OQ_BLOCK_FUSED",
+    "OQ_GEMM_MFMA",     "OQ_FUSED_QUANT",
+};
+
+struct KnobTable {
+    int value[kKnobCount] = {};
+    bool set[kKnobCount] = {};
+};
+KnobTable g_knobs;
+bool g_knobs_loaded = false;
+
+}  // namespace
+
+void load_knobs() {
+    KnobTable t;
+    for (int i = 0; i < kKnobCount; ++i) {
+        const char* v = getenv(kKnobNames[i]);
+        t.set[i] = v != nullptr;
+        t.value[i] = v ? atoi(v) : 0;
+    }
+    g_knobs = t;
+    g_knobs_loaded = true;
 }
+
+int knob(Knob k, int fallback) { return g_knobs.set[k] ? g_knobs.value[k] : fallback; }
 
 int cu_count() {
     static int cus = 0;
@@ -45,11 +74,10 @@ struct oq_context {
     hipEvent_t t0 = nullptr, t1 = nullptr;
     std::string error;
     bool capturing = false;
-    void* scratch = nullptr;  // Q8_K staging (un-fused GEMV) or planar image + split partials (GEMM)
-    uint64_t scratch_bytes = 0;
-    void* work = nullptr;  // intermediates of the DeltaNet block step
-    uint64_t work_bytes = 0;
+    oq::Workspace scratch;  // Q8_K staging (small batches) or the GEMM's activation image + split partials
+    oq::Workspace work;     // intermediates of the DeltaNet block step
     void* argmax_parts = nullptr;  // per-slice results of oq_argmax (kArgmaxParts * 12 bytes)
+    std::vector<oq_graph*> graphs;  // live graphs captured on this context
 };
 
 struct oq_weight {
@@ -62,6 +90,7 @@ struct oq_weight {
 struct oq_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    oq_context* ctx = nullptr;  // the context it was captured on (null once that is destroyed)
 };
 
 namespace {
@@ -147,44 +176,36 @@ int check_weight(oq_context* ctx, const oq_weight* w) {
     return OQ_OK;
 }
 
+void device_free(void* p) { (void)hipFree(p); }
+
+// Grows a context workspace; allocations that a live graph may still replay are kept until the
+// context's last graph is destroyed (oq_workspace.h).
+int ensure_workspace(oq_context* ctx, oq::Workspace& ws, uint64_t bytes, const char* what) {
+    hipError_t err = hipSuccess;
+    const oq::GrowResult r = ws.ensure(
+        bytes, ctx->capturing, (int)ctx->graphs.size(),
+        [&](uint64_t n) -> void* {
+            void* p = nullptr;
+            err = hipMalloc(&p, n);
+            return err == hipSuccess ? p : nullptr;
+        },
+        device_free, [&] { return (err = hipStreamSynchronize(ctx->stream)) == hipSuccess; });
+    switch (r) {
+        case oq::GrowResult::kOk: return OQ_OK;
+        case oq::GrowResult::kCapturing:
+            return fail(ctx, OQ_INVALID_ARGUMENT,
+                        std::string(what) + " must be sized before graph capture (run the call once first)");
+        default: return hip_fail(ctx, err, what);
+    }
+}
+
 int ensure_scratch(oq_context* ctx, uint64_t bytes) {
-    if (ctx->scratch_bytes >= bytes) return OQ_OK;
-    if (ctx->capturing) {
-        return fail(ctx, OQ_INVALID_ARGUMENT,
-                    "activation staging buffer must be sized before graph capture (run the call once first)");
-    }
-    if (ctx->scratch) {
-        OQ_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-        OQ_HIP(ctx, hipFree(ctx->scratch), "hipFree");
-        ctx->scratch = nullptr;
-        ctx->scratch_bytes = 0;
-    }
-    OQ_HIP(ctx, hipMalloc(&ctx->scratch, bytes), "hipMalloc(activation staging)");
-    ctx->scratch_bytes = bytes;
-    return OQ_OK;
+    return ensure_workspace(ctx, ctx->scratch, bytes, "activation staging buffer");
 }
 
-int ensure_work(oq_context* ctx, uint64_t bytes) {
-    if (ctx->work_bytes >= bytes) return OQ_OK;
-    if (ctx->capturing) {
-        return fail(ctx, OQ_INVALID_ARGUMENT,
-                    "block workspace must be sized before graph capture (run the call once first)");
-    }
-    if (ctx->work) {
-        OQ_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-        OQ_HIP(ctx, hipFree(ctx->work), "hipFree");
-        ctx->work = nullptr;
-        ctx->work_bytes = 0;
-    }
-    OQ_HIP(ctx, hipMalloc(&ctx->work, bytes), "hipMalloc(block workspace)");
-    ctx->work_bytes = bytes;
-    return OQ_OK;
-}
+int ensure_work(oq_context* ctx, uint64_t bytes) { return ensure_workspace(ctx, ctx->work, bytes, "block workspace"); }
 
-bool env_flag(const char* name, bool fallback) {
-    const char* v = getenv(name);
-    return v ? atoi(v) != 0 : fallback;
-}
+bool knob_flag(oq::Knob k, bool fallback) { return oq::knob(k, fallback ? 1 : 0) != 0; }
 
 int upload_common(oq_context* ctx, uint32_t type, uint64_t ne0, uint64_t ne1, const void* bytes,
                   uint64_t nbytes, bool from_device, oq_weight** out) {
@@ -316,7 +337,7 @@ int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, f
         total += (sizes[i] + 63) & ~uint64_t(63);
     }
     if (int rc = ensure_work(ctx, total * sizeof(float))) return rc;
-    float* ws = static_cast<float*>(ctx->work);
+    float* ws = static_cast<float*>(ctx->work.ptr);
     float *qkv = ws + off[0], *z = ws + off[1], *beta = ws + off[2], *alpha = ws + off[3], *conv = ws + off[4],
           *rec = ws + off[5], *gated = ws + off[6], *branch = ws + off[7], *resid = ws + off[8], *post = ws + off[9],
           *gate = ws + off[10], *up = ws + off[11], *act = ws + off[12], *ffn = ws + off[13], *beta_s = ws + off[14],
@@ -378,7 +399,7 @@ int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, f
     down.add = resid;
     down.sum_out = y;
     const bool even = C % 2 == 0 && V % 2 == 0 && Hv % 2 == 0 && E % 2 == 0;
-    const bool fused = env_flag("OQ_BLOCK_FUSED", true) && even && aligned(x, 16) && oq::gemv_block_supported(in) &&
+    const bool fused = knob_flag(oq::kBlockFused, true) && even && aligned(x, 16) && oq::gemv_block_supported(in) &&
                        oq::gemv_block_supported(outp) && oq::gemv_block_supported(ffn_in) &&
                        oq::gemv_block_supported(down);
     if (fused) {
@@ -409,7 +430,7 @@ int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, f
     }
     if (e == hipSuccess && trace) {
         uint64_t t = 0;
-        for (int i = 0; i < 14 && e == hipSuccess; ++i) {
+        for (int i = 0; i < 16 && e == hipSuccess; ++i) {
             e = hipMemcpyAsync(trace + t, ws + off[i], sizes[i] * sizeof(float), hipMemcpyDeviceToDevice, s);
             t += sizes[i];
         }
@@ -457,6 +478,7 @@ int oq_context_create(int device, oq_context** out) {
     }
     e = hipSetDevice(device);
     if (e != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
+    if (!oq::g_knobs_loaded) oq::load_knobs();
     oq_context* ctx = new oq_context;
     ctx->device = device;
     e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
@@ -476,8 +498,9 @@ void oq_context_destroy(oq_context* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->scratch) (void)hipFree(ctx->scratch);
-    if (ctx->work) (void)hipFree(ctx->work);
+    for (oq_graph* g : ctx->graphs) g->ctx = nullptr;
+    ctx->scratch.release_all(device_free);
+    ctx->work.release_all(device_free);
     if (ctx->argmax_parts) (void)hipFree(ctx->argmax_parts);
     if (ctx->t0) (void)hipEventDestroy(ctx->t0);
     if (ctx->t1) (void)hipEventDestroy(ctx->t1);
@@ -486,6 +509,8 @@ void oq_context_destroy(oq_context* ctx) {
 }
 
 const char* oq_last_error(const oq_context* ctx) { return ctx ? ctx->error.c_str() : g_error.c_str(); }
+
+void oq_reload_options(void) { oq::load_knobs(); }
 
 int oq_synchronize(oq_context* ctx) {
     if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
@@ -612,17 +637,17 @@ int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, f
         if (!oq::gemv_kquant_supported(w->m)) {
             return fail(ctx, OQ_INVALID_ARGUMENT, "K-quant rows longer than 16384 elements are not supported yet");
         }
-        if (oq::gemm_mfma_supported(w->m, (int)m) && env_flag("OQ_GEMM_MFMA", true)) {
+        if (oq::gemm_mfma_supported(w->m, (int)m) && knob_flag(oq::kGemmMfma, true)) {
             if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
-            return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, x, nullptr, y, ctx->scratch, ctx->stream),
+            return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, x, nullptr, y, ctx->scratch.ptr, ctx->stream),
                              "matmul");
         }
         // one row: every workgroup quantizes x itself (saves a launch); several rows: quantize
         // once and let the workgroups copy the Q8_K blocks
-        if (!env_flag("OQ_FUSED_QUANT", m == 1)) {
+        if (!knob_flag(oq::kFusedQuant, m == 1)) {
             const uint64_t q8bytes = (m * (w->m.k / oq::kQK) * oq::kQ8KBytes + 255) & ~uint64_t(255);
             if (int rc = ensure_scratch(ctx, q8bytes)) return rc;
-            uint8_t* q8 = static_cast<uint8_t*>(ctx->scratch);
+            uint8_t* q8 = static_cast<uint8_t*>(ctx->scratch.ptr);
             hipError_t e = oq::launch_quantize_q8k(x, m, w->m.k, q8, ctx->stream);
             if (e == hipSuccess) e = oq::launch_gemv_kquant(w->m, (int)m, nullptr, q8, y, ctx->stream);
             return launch_rc(ctx, e, "matmul");
@@ -650,9 +675,9 @@ int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q
         return fail(ctx, OQ_INVALID_ARGUMENT, "K-quant rows longer than 16384 elements are not supported yet");
     }
     const uint8_t* q8 = static_cast<const uint8_t*>(q8k);
-    if (oq::gemm_mfma_supported(w->m, (int)m) && env_flag("OQ_GEMM_MFMA", true)) {
+    if (oq::gemm_mfma_supported(w->m, (int)m) && knob_flag(oq::kGemmMfma, true)) {
         if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
-        return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, nullptr, q8, y, ctx->scratch, ctx->stream),
+        return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, nullptr, q8, y, ctx->scratch.ptr, ctx->stream),
                          "matmul_q8k");
     }
     return launch_rc(ctx, oq::launch_gemv_kquant(w->m, (int)m, nullptr, q8, y, ctx->stream), "matmul_q8k");
@@ -700,6 +725,8 @@ int oq_capture_end(oq_context* ctx, oq_graph** out) {
     oq_graph* gr = new oq_graph;
     gr->graph = g;
     gr->exec = ex;
+    gr->ctx = ctx;
+    ctx->graphs.push_back(gr);
     *out = gr;
     return OQ_OK;
 }
@@ -712,6 +739,15 @@ int oq_graph_launch(oq_context* ctx, oq_graph* g) {
 
 void oq_graph_destroy(oq_graph* g) {
     if (!g) return;
+    if (oq_context* ctx = g->ctx) {
+        // a replay may still be running on the context's stream
+        (void)hipStreamSynchronize(ctx->stream);
+        ctx->graphs.erase(std::remove(ctx->graphs.begin(), ctx->graphs.end(), g), ctx->graphs.end());
+        if (ctx->graphs.empty()) {
+            ctx->scratch.release_retired(device_free);
+            ctx->work.release_retired(device_free);
+        }
+    }
     if (g->exec) (void)hipGraphExecDestroy(g->exec);
     if (g->graph) (void)hipGraphDestroy(g->graph);
     delete g;

@@ -839,7 +839,7 @@ Plan make_plan(const DeviceMatrix& w, int m) {
     const uint64_t tiles = (uint64_t)p.tiles_n * p.tiles_m;
     const uint32_t nsb = (uint32_t)(w.k / kQK);
     uint64_t s = ((uint64_t)cu_count() + tiles / 2) / tiles;
-    int forced = env_int("OQ_GEMM_SPLITS", 0);
+    int forced = knob(kGemmSplits, 0);
     if (forced > 0) s = (uint64_t)forced;
     if (s < 1) s = 1;
     if (s > kMaxSplits) s = kMaxSplits;
@@ -877,8 +877,8 @@ hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const float* x, co
         hipLaunchKernelGGL(q8k_to_f16_kernel, dim3(qgrid), dim3(256), 0, s, q8k, nblocks, a16);
     }
     const unsigned wgs = p.tiles_n * p.tiles_m * p.splits;
-    const bool fast = w.k >= kFastMinK && env_int("OQ_GEMM_EXACT_DEQUANT", 0) == 0;
-    if (env_int("OQ_GEMM_WS", 1) != 0) {
+    const bool fast = w.k >= kFastMinK && knob(kGemmExactDequant, 0) == 0;
+    if (knob(kGemmWs, 1) != 0) {
         float* dst = p.splits > 1 ? part : y;
         if (fast) {
             static bool attr = false;

@@ -188,7 +188,7 @@ __global__ __launch_bounds__(kThreads) void gemv_plain_kernel(DeviceMatrix w, in
 
 unsigned grid_for(uint64_t work_items, int per_wg_items) {
     const uint64_t want = (work_items + per_wg_items - 1) / per_wg_items;
-    const uint64_t cap = (uint64_t)env_int("OQ_GEMV_MAX_WG", 1 << 20);
+    const uint64_t cap = (uint64_t)knob(kGemvMaxWg, 1 << 20);
     return (unsigned)(want < cap ? (want ? want : 1) : cap);
 }
 
@@ -203,7 +203,7 @@ hipError_t launch_q8_0_rows(const DeviceMatrix& w, const float* x, float* y, hip
 
 template <int MT>
 hipError_t launch_q8_0_mt(const DeviceMatrix& w, int m, const float* x, float* y, hipStream_t s) {
-    if (MT == 1 && w.k % 1024 == 0 && env_int("OQ_Q8_0_ROWS", 1) != 0) {
+    if (MT == 1 && w.k % 1024 == 0 && knob(kQ80Rows, 1) != 0) {
         switch (w.k / 1024) {
             case 1: return launch_q8_0_rows<1>(w, x, y, s);
             case 2: return launch_q8_0_rows<2>(w, x, y, s);

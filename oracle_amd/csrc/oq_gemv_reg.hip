@@ -741,7 +741,7 @@ hipError_t launch_full(const DeviceMatrix& w, int m, const float* x, const uint8
     const uint64_t groups = (w.n + R - 1) / R;
     const uint64_t lds = act_lds_bytes(w.k, MT);
     // two workgroups per CU where both fit (more would only repeat the activation staging)
-    int wg_per_cu = env_int("OQ_GEMV_WG_PER_CU", 2);
+    int wg_per_cu = knob(kGemvWgPerCu, 2);
     if (wg_per_cu < 1) wg_per_cu = 1;
     const int resident = resident_per_cu<TYPE, ITERS, R, MT, FUSED, WAVES, FULL>(lds);
     if (wg_per_cu > resident) wg_per_cu = resident;
@@ -773,7 +773,7 @@ hipError_t launch_stream(const DeviceMatrix& w, const float* x, const uint8_t* q
     }
     // sixteen waves per CU: ~37 KiB of weights in flight per CU, and each CU stages the
     // activation row once per sixteen waves
-    int wg_per_cu = env_int("OQ_STREAM_WG_PER_CU", 16 / WAVES);
+    int wg_per_cu = knob(kStreamWgPerCu, 16 / WAVES);
     wg_per_cu = wg_per_cu < 1 ? 1 : (wg_per_cu > resident ? resident : wg_per_cu);
     uint64_t wgs = (uint64_t)cu_count() * (uint64_t)wg_per_cu;
     const uint64_t need = (w.n + WAVES - 1) / WAVES;
@@ -800,9 +800,9 @@ hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8
         // Streamed kernel: measured faster than issuing every row of a wave at once (below) for
         // 2048 to 151936 rows of 2048 to 12288 columns (0.8 to 1.2 us less on 2048 to 12288 q4_K
         // rows of 4096); the batched kernel stays selectable with OQ_GEMV_STREAM=0.
-        if (env_int("OQ_GEMV_STREAM", 1) != 0) {
+        if (knob(kGemvStream, 1) != 0) {
             const bool full = (w.k / kQK) % 16 == 0;
-            if (env_int("OQ_STREAM_WAVES", 16) >= 16) {
+            if (knob(kStreamWaves, 16) >= 16) {
                 return full ? launch_stream<TYPE, ITERS, FUSED, 16, true>(w, x, q8k, y, s)
                             : launch_stream<TYPE, ITERS, FUSED, 16, false>(w, x, q8k, y, s);
             }
@@ -814,13 +814,13 @@ hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8
         // small batches (from Q8_K blocks, or F32 rows quantized in the staging): streamed, one
         // pass in flight
         // (q5_K with eight rows would spill within the 128 registers of a 16-wave workgroup)
-        if (act_lds_bytes(w.k, MT) <= kLdsBudget && env_int("OQ_GEMV_STREAM_MT", 1) != 0) {
+        if (act_lds_bytes(w.k, MT) <= kLdsBudget && knob(kGemvStreamMt, 1) != 0) {
             return (w.k / kQK) % 16 == 0 ? launch_stream_mt<TYPE, ITERS, MT, FUSED, true>(w, m, x, q8k, y, s)
                                          : launch_stream_mt<TYPE, ITERS, MT, FUSED, false>(w, m, x, q8k, y, s);
         }
     }
-    const int rows = env_int("OQ_GEMV_ROWS", MT == 1 && ITERS <= 2 ? 2 : 1);
-    const int waves = env_int("OQ_GEMV_WAVES", 8);
+    const int rows = knob(kGemvRows, MT == 1 && ITERS <= 2 ? 2 : 1);
+    const int waves = knob(kGemvWaves, 8);
     if constexpr (MT == 1 && ITERS <= 3) {  // two rows per wave would spill beyond 3 passes
         if (rows >= 2) {
             if constexpr (ITERS == 1) {
@@ -832,7 +832,7 @@ hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8
     // small batches: two rows per wave use every activation slice read from LDS twice (Q5_K's
     // extra high-bit words do not fit two rows of three slots for eight columns without spilling)
     if constexpr (MT > 1 && ITERS <= 3 && !(TYPE == 13 && ITERS * MT > 16)) {
-        if (env_int("OQ_GEMV_ROWS_MT", 2) >= 2) return launch_one<TYPE, ITERS, 2, MT, FUSED, 8>(w, m, x, q8k, y, s);
+        if (knob(kGemvRowsMt, 2) >= 2) return launch_one<TYPE, ITERS, 2, MT, FUSED, 8>(w, m, x, q8k, y, s);
     }
     return launch_one<TYPE, ITERS, 1, MT, FUSED, 8>(w, m, x, q8k, y, s);
 }
@@ -1206,7 +1206,7 @@ hipError_t launch_block_full(const BlockGemv& a, hipStream_t s) {
     if constexpr (MODE == kBlockAdd) {
         // the residual projections without a normalising prologue stream like the plain decode
         // GEMV (FFN down 4096 x 12288: 9.3 us against 11.1 us in the structure below)
-        if (a.norm_w == nullptr && env_int("OQ_BLOCK_STREAM", 1) != 0)
+        if (a.norm_w == nullptr && knob(kBlockStream, 1) != 0)
             return launch_block_add_stream<TYPE, ITERS, FULL>(a, s);
     }
     const uint64_t groups = MODE == kBlockFfn ? a.mat[0].n : ((uint64_t)a.row_end[a.nmat - 1] + 1) / 2;

@@ -31,7 +31,30 @@ struct DeviceMatrix {
 uint64_t device_pitch(uint32_t type, uint64_t k);
 
 // ---- oq_api.cpp
-int env_int(const char* name, int fallback);  // integer launch knob; fallback when unset
+// Launch options (OQ_* environment variables), read once when the first context is created and
+// again by oq_reload_options(); never per launch.
+enum Knob : int {
+    kGemmSplits,  // OQ_GEMM_SPLITS
+    kGemmExactDequant,  // OQ_GEMM_EXACT_DEQUANT
+    kGemmWs,  // OQ_GEMM_WS
+    kGemvMaxWg,  // OQ_GEMV_MAX_WG
+    kQ80Rows,  // OQ_Q8_0_ROWS
+    kGemvWgPerCu,  // OQ_GEMV_WG_PER_CU
+    kStreamWgPerCu,  // OQ_STREAM_WG_PER_CU
+    kGemvStream,  // OQ_GEMV_STREAM
+    kStreamWaves,  // OQ_STREAM_WAVES
+    kGemvStreamMt,  // OQ_GEMV_STREAM_MT
+    kGemvRows,  // OQ_GEMV_ROWS
+    kGemvWaves,  // OQ_GEMV_WAVES
+    kGemvRowsMt,  // OQ_GEMV_ROWS_MT
+    kBlockStream,  // OQ_BLOCK_STREAM
+    kBlockFused,  // OQ_BLOCK_FUSED
+    kGemmMfma,  // OQ_GEMM_MFMA
+    kFusedQuant,  // OQ_FUSED_QUANT
+    kKnobCount
+};
+int knob(Knob k, int fallback);  // the option's value, or fallback when it is unset
+void load_knobs();
 int cu_count();                               // compute units of the current device (cached)
 
 // ---- oq_decode.hip

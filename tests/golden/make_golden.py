@@ -12,6 +12,16 @@
    convolution step and gated delta rule step (src/runtime/reference_kernels.cpp:197-335,
    compiled into the same library), several steps in a row with the state carried.
 
+4. ref_block.npz -- seeded Gated DeltaNet decode blocks run through the reference's own
+   execute_qwen35_recurrent_block_reference (src/runtime/qwen35_block.cpp:406-605) on in-memory
+   tensor views, as the reference's block test drives it (tests/test_phase2c.cpp:72-213), three
+   steps with the state and convolution history carried:
+   - "plain": projections stored as F32, F16, BF16 and Q8_0 (the reference multiplies them with
+     the F32 activation, as the oracle does), no overrides;
+   - "kq": q4_K projections with a q6_K output projection; the reference's matvec override
+     bridge (Qwen35MatvecOverrides) takes the oracle's projection outputs, so every other stage
+     is the reference's own arithmetic.
+
 Run from the repository root after `make -C oracle all ref`:  python tests/golden/make_golden.py
 """
 from __future__ import annotations
@@ -69,6 +79,17 @@ def kat() -> dict:
                           "eps": 1e-12},
                 "delta_eps": {"q": [1e-4, 0.0], "k": [1e-4, 0.0], "v": [2.0], "beta": 1.0, "log_decay": 0.0,
                               "eps": 1e-6, "expected": 1.4142135623730951, "tol": 2e-6}},
+        # reference tests/test_phase2c.cpp: manifest :49-71, recurrent block weights :146-181 (all
+        # F32; unlisted matrices are zero), assertions :215-260
+        "block": {"dims": {"embedding": 4, "key_heads": 2, "value_heads": 4, "key_dim": 1, "value_dim": 1,
+                           "conv_kernel": 2, "ffn": 4, "eps": 1e-6},
+                  "input": [1.0, -2.0, 3.0, 4.0],
+                  "qkv_ones": [[0, 0], [1, 1], [2, 0], [3, 1], [4, 0], [5, 1], [6, 2], [7, 3]],
+                  "conv_tap_one": 1, "dt_bias": [0.0, 0.0, 0.0, 0.0], "decay": [-1.0, -1.0, -1.0, -1.0],
+                  "out": "identity", "norms": "ones",
+                  "expect": {"output_equals_input": True, "beta_sigmoid0": 0.5, "gate0": -0.6931471805599453,
+                             "tol": 1e-6, "q_predelta_signs": [1, -1, 1, -1], "state_before_zero": True,
+                             "state_after_nonzero": True}},
     }
 
 
@@ -154,13 +175,94 @@ def deltanet_vectors() -> dict[str, np.ndarray]:
     return out
 
 
+BLOCK_PLAIN_DIMS = dict(embedding=64, key_heads=2, value_heads=4, key_dim=8, value_dim=16, conv_kernel=4,
+                        ffn=96, eps=1e-6)
+BLOCK_KQ_DIMS = dict(embedding=256, key_heads=1, value_heads=2, key_dim=32, value_dim=128, conv_kernel=4,
+                     ffn=256, eps=1e-6)
+# storage type per projection (0 f32, 1 f16, 30 bf16, 8 q8_0, 12 q4_K, 14 q6_K)
+BLOCK_PLAIN_TYPES = dict(qkv=8, z=1, beta=30, alpha=0, out=8, gate=0, up=1, down=8)
+BLOCK_KQ_TYPES = dict(qkv=12, z=12, beta=12, alpha=12, out=14, gate=12, up=12, down=12)
+
+
+def block_inputs(rng: np.random.Generator, dims: dict, types: dict):
+    """Seeded block inputs: (weights {name: (type, bytes)}, vectors, conv history, state, xs[3])."""
+    E, F = dims["embedding"], dims["ffn"]
+    Hk, Hv, dk, dv, K = (dims[k] for k in ("key_heads", "value_heads", "key_dim", "value_dim", "conv_kernel"))
+    C, V = 2 * Hk * dk + Hv * dv, Hv * dv
+    shapes = {"qkv": (C, E), "z": (V, E), "beta": (Hv, E), "alpha": (Hv, E), "out": (E, V), "gate": (F, E),
+              "up": (F, E), "down": (E, F)}
+    w = {}
+    for n, (rows, cols) in shapes.items():
+        t = types[n]
+        if t in (12, 13, 14, 8):
+            w[n] = (t, synth.weights(t, rng, rows, cols))
+        else:
+            vals = (0.05 * rng.standard_normal(rows * cols)).astype(np.float32)
+            if t == 0:
+                data = vals.view(np.uint8)
+            elif t == 1:
+                data = vals.astype(np.float16).view(np.uint8)
+            else:  # bf16: the upper half of the F32 pattern
+                data = (vals.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
+            w[n] = (t, data.copy())
+    vec = {
+        "input_norm": (1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32),
+        "conv_weight": (0.5 * rng.standard_normal(C * K)).astype(np.float32),
+        "dt_bias": rng.standard_normal(Hv).astype(np.float32),
+        "decay": (-np.exp(0.5 * rng.standard_normal(Hv))).astype(np.float32),
+        "out_norm": (1.0 + 0.1 * rng.standard_normal(dv)).astype(np.float32),
+        "post_norm": (1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32),
+    }
+    hist = rng.standard_normal((C, K)).astype(np.float32)
+    state = (0.01 * rng.standard_normal((Hv, dk, dv))).astype(np.float32)
+    xs = rng.standard_normal((3, E)).astype(np.float32)
+    return w, vec, hist, state, xs
+
+
+def block_vectors() -> dict[str, np.ndarray]:
+    out: dict[str, np.ndarray] = {}
+    for case, dims, types, seed in (("plain", BLOCK_PLAIN_DIMS, BLOCK_PLAIN_TYPES, 20261203),
+                                    ("kq", BLOCK_KQ_DIMS, BLOCK_KQ_TYPES, 20261204)):
+        w, vec, hist, state, xs = block_inputs(np.random.default_rng(seed), dims, types)
+        for n, (t, data) in w.items():
+            out[f"{case}_w_{n}"] = data
+            out[f"{case}_t_{n}"] = np.array([t])
+        for n, v in vec.items():
+            out[f"{case}_v_{n}"] = v
+        out[f"{case}_history0"] = hist.copy()
+        out[f"{case}_state0"] = state.copy()
+        out[f"{case}_x"] = xs
+        out[f"{case}_ffn"] = np.array([dims["ffn"]])
+        ys, traces, projs = [], [], []
+        oh, os_ = hist.copy(), state.copy()
+        for i in range(xs.shape[0]):
+            overrides = None
+            if case == "kq":
+                # the oracle's projections of this step (its own state carried alongside)
+                _, tr = oracle.deltanet_step(dims, w, vec, oh, os_, xs[i], threads=1, trace=True)
+                overrides = {"qkv": tr["qkv"], "z": tr["z"], "beta": tr["beta"], "alpha": tr["alpha"],
+                             "out": tr["branch"], "gate": tr["gate"], "up": tr["up"], "down": tr["ffn"]}
+                projs.append(np.concatenate([overrides[n] for n in oracle.DN_WEIGHTS]))
+            y, tr = oracle.ref_recurrent_block(dims, w, vec, hist, state, xs[i], overrides=overrides)
+            ys.append(y)
+            traces.append(np.concatenate([tr[n] for n in oracle.DN_TRACE]))
+        out[f"{case}_y_bits"] = np.stack(ys).view(np.uint32)
+        out[f"{case}_trace_bits"] = np.stack(traces).view(np.uint32)
+        out[f"{case}_history_bits"] = hist.view(np.uint32)
+        out[f"{case}_state_bits"] = state.view(np.uint32)
+        if projs:
+            out[f"{case}_proj_bits"] = np.stack(projs).view(np.uint32)
+    return out
+
+
 def main() -> None:
     if not oracle.ref_available():
         raise SystemExit("oracle/_ref/libref.so is not built: run `make -C oracle ref` first")
     (OUT / "ref_kat.json").write_text(json.dumps(kat(), indent=1) + "\n")
     np.savez_compressed(OUT / "ref_random.npz", **random_vectors())
     np.savez_compressed(OUT / "ref_deltanet.npz", **deltanet_vectors())
-    print("wrote", OUT / "ref_kat.json", OUT / "ref_random.npz", OUT / "ref_deltanet.npz")
+    np.savez_compressed(OUT / "ref_block.npz", **block_vectors())
+    print("wrote", OUT / "ref_kat.json", OUT / "ref_random.npz", OUT / "ref_deltanet.npz", OUT / "ref_block.npz")
 
 
 if __name__ == "__main__":

@@ -5,7 +5,6 @@ Bars: dequantized rows and Q8_K blocks bit-exact; products within
 where y_ref is the reference's sequential F32 dot (oracle) of the decoded row with xhat, the F32
 activation (q8_0 and plain rows) or the dequantized Q8_K activation (K-quant rows).
 """
-import os
 
 import numpy as np
 import pytest
@@ -251,10 +250,7 @@ def test_matrix_cores_q8k_input_and_split_counts(ctx, splits):
     data = synth.q4_k(rng, rows, cols)
     x = rng.standard_normal((m, cols)).astype(np.float32)
     w = ctx.upload(12, cols, rows, data)
-    old = os.environ.get("OQ_GEMM_SPLITS")
-    if splits is not None:
-        os.environ["OQ_GEMM_SPLITS"] = splits
-    try:
+    with oracle_amd.launch_options({} if splits is None else {"OQ_GEMM_SPLITS": splits}):
         y = gpu_matmul(ctx, w, x, rows)
         xb = ctx.to_device(x)
         qb = ctx.alloc(m * (cols // 256) * 292)
@@ -264,11 +260,6 @@ def test_matrix_cores_q8k_input_and_split_counts(ctx, splits):
         y_q8k = yb.download(np.float32, m * rows).reshape(m, rows)
         for b in (xb, qb, yb):
             b.free()
-    finally:
-        if old is None:
-            os.environ.pop("OQ_GEMM_SPLITS", None)
-        else:
-            os.environ["OQ_GEMM_SPLITS"] = old
     assert np.array_equal(y.view(np.uint32), y_q8k.view(np.uint32))
     y_ref, norm = reference_products(12, rows, cols, data, x)
     worst = check_close(y, y_ref, norm)
@@ -286,16 +277,9 @@ def test_matrix_core_kernels_agree(ctx, cols):
     x = rng.standard_normal((m, cols)).astype(np.float32)
     w = ctx.upload(12, cols, rows, data)
     ys = {}
-    old = os.environ.get("OQ_GEMM_WS")
-    try:
-        for v in ("1", "0"):
-            os.environ["OQ_GEMM_WS"] = v
+    for v in ("1", "0"):
+        with oracle_amd.launch_options({"OQ_GEMM_WS": v}):
             ys[v] = gpu_matmul(ctx, w, x, rows)
-    finally:
-        if old is None:
-            os.environ.pop("OQ_GEMM_WS", None)
-        else:
-            os.environ["OQ_GEMM_WS"] = old
     assert np.array_equal(ys["1"].view(np.uint32), ys["0"].view(np.uint32))
     y_ref, norm = reference_products(12, rows, cols, data, x)
     check_close(ys["1"], y_ref, norm)
@@ -330,16 +314,8 @@ def test_launch_variants_agree(ctx, env):
         x = rng.standard_normal((3, cols)).astype(np.float32)
         w = ctx.upload(t, cols, rows, data)
         base = gpu_matmul(ctx, w, x, rows)
-        old = {k: os.environ.get(k) for k in env}
-        os.environ.update(env)
-        try:
+        with oracle_amd.launch_options(env):
             var = gpu_matmul(ctx, w, x, rows)
-        finally:
-            for k, v in old.items():
-                if v is None:
-                    os.environ.pop(k, None)
-                else:
-                    os.environ[k] = v
         y_ref, norm = reference_products(t, rows, cols, data, x)
         check_close(var, y_ref, norm)
         results[t] = np.max(np.abs(var - base))
@@ -359,17 +335,10 @@ def test_q8_0_decode_gemv(ctx, rows, cols):
     yb = ctx.alloc(rows * 4)
     runs = []
     for flag in ("1", "0"):
-        old = os.environ.get("OQ_Q8_0_ROWS")
-        os.environ["OQ_Q8_0_ROWS"] = flag
-        try:
+        with oracle_amd.launch_options({"OQ_Q8_0_ROWS": flag}):
             yb.upload(np.full(rows, np.nan, np.float32))
             ctx.matvec(w, xb, yb)
             ctx.sync()
-        finally:
-            if old is None:
-                os.environ.pop("OQ_Q8_0_ROWS", None)
-            else:
-                os.environ["OQ_Q8_0_ROWS"] = old
         runs.append(yb.download(np.float32, rows))
     y_ref, norm = reference_products(8, rows, cols, data, x)
     for r in runs:
@@ -396,18 +365,10 @@ def test_small_batch_streamed_kernel(ctx, t, rows, cols, m):
     # streamed, batched, and streamed with the quantization inside the kernel's staging
     for env in ({"OQ_GEMV_STREAM_MT": "1"}, {"OQ_GEMV_STREAM_MT": "0"},
                 {"OQ_GEMV_STREAM_MT": "1", "OQ_FUSED_QUANT": "1"}):
-        old = {k: os.environ.get(k) for k in env}
-        os.environ.update(env)
-        try:
+        with oracle_amd.launch_options(env):
             yb.upload(np.full(m * rows, np.nan, np.float32))
             ctx.matmul(w, m, xb, yb)
             ctx.sync()
-        finally:
-            for k, v in old.items():
-                if v is None:
-                    os.environ.pop(k, None)
-                else:
-                    os.environ[k] = v
         runs.append(yb.download(np.float32, m * rows).reshape(m, rows))
     for r in runs[1:]:
         assert np.array_equal(runs[0].view(np.uint32), r.view(np.uint32))
@@ -446,18 +407,10 @@ def test_decode_gemv_many_rows_per_wave(ctx, t, rows, cols):
     runs = []
     for env in ({}, {"OQ_GEMV_STREAM": "1"}, {"OQ_GEMV_STREAM": "0"}, {"OQ_GEMV_STREAM": "1"},
                 {"OQ_GEMV_STREAM": "0", "OQ_GEMV_ROWS": "1"}):
-        old = {k: os.environ.get(k) for k in env}
-        os.environ.update(env)
-        try:
+        with oracle_amd.launch_options(env):
             yb.upload(np.full(rows, np.nan, np.float32))
             ctx.matvec(w, xb, yb)
             ctx.sync()
-        finally:
-            for k, v in old.items():
-                if v is None:
-                    os.environ.pop(k, None)
-                else:
-                    os.environ[k] = v
         runs.append(yb.download(np.float32, rows))
     for r in runs[1:]:
         assert np.array_equal(r.view(np.uint32), runs[0].view(np.uint32))
@@ -562,3 +515,39 @@ def test_graph_replay_matches_eager(ctx):
         b.free()
     for w in ws:
         w.release()
+
+
+def test_graph_replay_after_workspace_growth(ctx):
+    """A graph keeps replaying the staging buffer it captured after an eager call grew the
+    context's buffer (the old allocation is retired, not freed, while the graph lives)."""
+    rng = np.random.default_rng(6060)
+    rows, cols, m = 640, 4096, 4
+    data = synth.q4_k(rng, rows, cols)
+    w = ctx.upload(12, cols, rows, data)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    xb, yb = ctx.to_device(x), ctx.alloc(m * rows * 4)
+    ctx.matmul(w, m, xb, yb)  # sizes the small staging buffer
+    ctx.sync()
+    eager = yb.download(np.float32, m * rows)
+    ctx.capture_begin()
+    ctx.matmul(w, m, xb, yb)
+    g = ctx.capture_end()
+    big = 256  # the matrix-core path needs a much larger buffer: the context grows it
+    xbig = ctx.to_device(rng.standard_normal((big, cols)).astype(np.float32))
+    ybig = ctx.alloc(big * rows * 4)
+    ctx.matmul(w, big, xbig, ybig)
+    ctx.sync()
+    for _ in range(3):
+        yb.upload(np.full(m * rows, np.nan, np.float32))
+        g.launch()
+        ctx.sync()
+        assert np.array_equal(yb.download(np.float32, m * rows).view(np.uint32), eager.view(np.uint32))
+        ctx.matmul(w, big, xbig, ybig)  # eager work on the grown buffer between replays
+        ctx.sync()
+    g.destroy()
+    ctx.matmul(w, m, xb, yb)
+    ctx.sync()
+    assert np.array_equal(yb.download(np.float32, m * rows).view(np.uint32), eager.view(np.uint32))
+    for b in (xb, yb, xbig, ybig):
+        b.free()
+    w.release()
