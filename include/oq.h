@@ -199,6 +199,17 @@ typedef struct oq_deltanet_block {
 int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* block, float* conv_history_dev,
                      float* state_dev, const float* x_dev, float* y_dev, float* trace_dev);
 
+/* No counterpart in the reference.  oq_deltanet_step for callers that cannot allocate device
+   memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+   same arguments, checks, kernels and results, but it allocates nothing -- the block's
+   workspace is a fixed per-GPU device array of oq_deltanet_noalloc_capacity() bytes (4 MiB;
+   a hidden-4096, FFN-12288 block needs about 440 KiB), held for the life of the process.  A
+   block whose workspace would exceed it gets OQ_INVALID_ARGUMENT.  Every call on one GPU
+   shares that array: calls that overlap on one GPU (several streams or threads) race. */
+int oq_deltanet_step_noalloc(oq_context* ctx, const oq_deltanet_block* block, float* conv_history_dev,
+                             float* state_dev, const float* x_dev, float* y_dev, float* trace_dev);
+uint64_t oq_deltanet_noalloc_capacity(void);
+
 /* ------------------------------------------------------------------ timing / graphs */
 
 /* HIP events on the context's stream, for timing the kernels launched there. */

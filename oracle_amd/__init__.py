@@ -271,6 +271,13 @@ class Context:
         self._call(self.lib.oq_deltanet_step, self.h, C.byref(block.desc), conv_history.ptr, state.ptr, x.ptr, y.ptr,
                    trace.ptr if trace is not None else None)
 
+    def deltanet_step_noalloc(self, block: "DeltaNetBlockWeights", conv_history: DeviceBuffer, state: DeviceBuffer,
+                              x: DeviceBuffer, y: DeviceBuffer, trace: DeviceBuffer | None = None) -> None:
+        """oq_deltanet_step_noalloc: the same step on the library's fixed per-GPU workspace (no
+        device allocation; calls overlapping on one GPU race)."""
+        self._call(self.lib.oq_deltanet_step_noalloc, self.h, C.byref(block.desc), conv_history.ptr, state.ptr,
+                   x.ptr, y.ptr, trace.ptr if trace is not None else None)
+
     # timing / graphs
     def timer_start(self) -> None:
         self._call(self.lib.oq_timer_start, self.h)

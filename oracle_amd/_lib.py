@@ -50,6 +50,8 @@ SIGNATURES = [
     ("oq_matmul", C.c_int, [_P, _P, _U64, _P, _P]),
     ("oq_matmul_q8k", C.c_int, [_P, _P, _U64, _P, _P]),
     ("oq_deltanet_step", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
+    ("oq_deltanet_step_noalloc", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
+    ("oq_deltanet_noalloc_capacity", _U64, []),
     ("oq_timer_start", C.c_int, [_P]),
     ("oq_timer_stop", C.c_int, [_P, C.POINTER(C.c_float)]),
     ("oq_capture_begin", C.c_int, [_P]),

@@ -292,12 +292,30 @@ int check_block_weight(oq_context* ctx, const oq_weight* w, uint64_t ne0, uint64
     return OQ_OK;
 }
 
-}  // namespace
+// Workspace of one block step: the trace fields, then beta_s, log_decay and the normalised input,
+// each padded to 64 floats so every projection input is 256-byte aligned.
+struct BlockLayout {
+    uint64_t sizes[17];
+    uint64_t off[17];
+    uint64_t total_floats;
+};
 
-extern "C" {
+BlockLayout block_layout(const oq_deltanet_block* b) {
+    const uint64_t E = b->embedding, Hk = b->key_heads, Hv = b->value_heads, dk = b->key_dim, dv = b->value_dim,
+                   F = b->ffn;
+    const uint64_t V = Hv * dv, C = 2 * Hk * dk + V;
+    BlockLayout l{{C, V, Hv, Hv, C, V, V, E, E, E, F, F, F, E, Hv, Hv, E}, {}, 0};
+    for (int i = 0; i < 17; ++i) {
+        l.off[i] = l.total_floats;
+        l.total_floats += (l.sizes[i] + 63) & ~uint64_t(63);
+    }
+    return l;
+}
 
-int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, float* state, const float* x,
-                     float* y, float* trace) {
+// The block step's checks and launches.  ws: caller-provided workspace of ws_bytes, or null to
+// use (and grow) the context's own.
+int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, float* state, const float* x, float* y,
+                  float* trace, float* ext_ws, uint64_t ext_ws_bytes) {
     if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
     if (!b || !hist || !state || !x || !y) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
     const uint64_t E = b->embedding, Hk = b->key_heads, Hv = b->value_heads, dk = b->key_dim, dv = b->value_dim,
@@ -314,6 +332,13 @@ int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, f
     }
     if (E > 0x7FFFFFFF || F > 0x7FFFFFFF || Hv * dv > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "block too large");
     const uint64_t V = Hv * dv, C = 2 * Hk * dk + V;
+    const BlockLayout lay = block_layout(b);
+    if (ext_ws != nullptr && lay.total_floats * sizeof(float) > ext_ws_bytes) {
+        return fail(ctx, OQ_INVALID_ARGUMENT,
+                    "DeltaNet block workspace of " + std::to_string(lay.total_floats * sizeof(float)) +
+                        " bytes exceeds the allocation-free entry point's fixed " + std::to_string(ext_ws_bytes) +
+                        " bytes");
+    }
     if (int rc = check_block_weight(ctx, b->qkv, E, C, "qkv")) return rc;
     if (int rc = check_block_weight(ctx, b->z, E, V, "z")) return rc;
     if (int rc = check_block_weight(ctx, b->beta, E, Hv, "beta")) return rc;
@@ -328,16 +353,13 @@ int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, f
     if (!aligned(x, 4) || !aligned(y, 4) || !aligned(hist, 4) || !aligned(state, 4)) {
         return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer");
     }
-    // workspace: the trace fields, then beta_s, log_decay and the normalised input, each padded
-    // to 64 floats so every projection input is 256-byte aligned
-    const uint64_t sizes[17] = {C, V, Hv, Hv, C, V, V, E, E, E, F, F, F, E, Hv, Hv, E};
-    uint64_t off[17], total = 0;
-    for (int i = 0; i < 17; ++i) {
-        off[i] = total;
-        total += (sizes[i] + 63) & ~uint64_t(63);
+    const uint64_t* sizes = lay.sizes;
+    const uint64_t* off = lay.off;
+    float* ws = ext_ws;
+    if (ws == nullptr) {
+        if (int rc = ensure_work(ctx, lay.total_floats * sizeof(float))) return rc;
+        ws = static_cast<float*>(ctx->work.ptr);
     }
-    if (int rc = ensure_work(ctx, total * sizeof(float))) return rc;
-    float* ws = static_cast<float*>(ctx->work.ptr);
     float *qkv = ws + off[0], *z = ws + off[1], *beta = ws + off[2], *alpha = ws + off[3], *conv = ws + off[4],
           *rec = ws + off[5], *gated = ws + off[6], *branch = ws + off[7], *resid = ws + off[8], *post = ws + off[9],
           *gate = ws + off[10], *up = ws + off[11], *act = ws + off[12], *ffn = ws + off[13], *beta_s = ws + off[14],
@@ -438,6 +460,29 @@ int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, f
     return launch_rc(ctx, e, "deltanet_step");
 }
 
+}  // namespace
+
+namespace oq {
+
+int deltanet_step_into(oq_context* ctx, const oq_deltanet_block* b, float* hist, float* state, const float* x,
+                       float* y, float* trace, float* ws, uint64_t ws_bytes) {
+    if (ws == nullptr) return fail(ctx, OQ_DEVICE_ERROR, "allocation-free workspace is not set up on this device");
+    return deltanet_step(ctx, b, hist, state, x, y, trace, ws, ws_bytes);
+}
+
+int context_device(const oq_context* ctx) { return ctx->device; }
+
+int set_error(oq_context* ctx, int code, const char* msg) { return fail(ctx, code, msg); }
+
+}  // namespace oq
+
+extern "C" {
+
+int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, float* state, const float* x,
+                     float* y, float* trace) {
+    return deltanet_step(ctx, b, hist, state, x, y, trace, nullptr, 0);
+}
+
 }  // extern "C"
 
 namespace {
@@ -479,6 +524,7 @@ int oq_context_create(int device, oq_context** out) {
     e = hipSetDevice(device);
     if (e != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
     if (!oq::g_knobs_loaded) oq::load_knobs();
+    oq::noalloc_setup(device);  // its failure is reported by the allocation-free entry point
     oq_context* ctx = new oq_context;
     ctx->device = device;
     e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);

@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+struct oq_context;
+struct oq_deltanet_block;
+
 namespace oq {
 
 constexpr int kQK = 256;          // K-quant super-block
@@ -130,5 +133,14 @@ struct BlockGemv {
 };
 bool gemv_block_supported(const BlockGemv& a);
 hipError_t launch_gemv_block(int mode, const BlockGemv& a, hipStream_t s);
+
+// ---- oq_api.cpp: the block step on a caller-provided workspace (validation, capacity check, launches)
+int deltanet_step_into(oq_context* ctx, const oq_deltanet_block* b, float* hist, float* state, const float* x,
+                       float* y, float* trace, float* ws, uint64_t ws_bytes);
+int context_device(const oq_context* ctx);
+int set_error(oq_context* ctx, int code, const char* msg);
+
+// ---- oq_noalloc.hip: the allocation-free entry point's per-device workspace
+void noalloc_setup(int device);  // device must be current; once per device
 
 }  // namespace oq
