@@ -180,8 +180,8 @@ int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q
      qkv[C] z[Hv*dv] beta[Hv] alpha[Hv] conv[C] out[Hv*dv] gated[Hv*dv] branch[E] resid[E]
      post[E] gate[F] up[F] act[F] ffn[E] beta_s[Hv] log_decay[Hv]      with C = 2*Hk*dk + Hv*dv,
      beta_s = sigmoid(beta), log_decay = softplus(alpha + dt_bias) * decay.
-   Device path limits: dk in {32, 64, 128}, dv in {64, 128, 192, 256}, conv_kernel <= 16, K-quant rows
-   <= 16384; otherwise OQ_INVALID_ARGUMENT.  Weight shape mismatches -> OQ_INVALID_ARGUMENT. */
+   Device path limits: dk in {32, 64, 128}, dv in {64, 128, 192, 256}, conv_kernel <= 16; otherwise
+   OQ_INVALID_ARGUMENT.  Weight shape mismatches -> OQ_INVALID_ARGUMENT. */
 typedef struct oq_deltanet_block {
     uint64_t embedding;   /* E */
     uint64_t key_heads;   /* Hk */

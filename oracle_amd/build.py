@@ -42,22 +42,49 @@ def _run(cmd: list[str]) -> None:
             sys.stderr.write(line + "\n")
 
 
-def sources() -> list[Path]:
-    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
+# Sources compiled more than once, with different macro definitions: one object per entry.
+# oq_gemv_inst.hip holds the K-quant GEMV instantiations of one (weight type, activation form).
+VARIANTS = {
+    "oq_gemv_inst.hip": [
+        (f"t{t}_{'f32' if fused else 'q8k'}", [f"-DOQ_KQ_TYPE={t}", f"-DOQ_KQ_FUSED={int(fused)}"])
+        for t in (12, 13, 14) for fused in (True, False)
+    ],
+}
 
 
-def build(jobs: int = 8) -> Path:
+def units() -> list[tuple[Path, Path, list[str]]]:
+    """(source, object, extra flags) for every object of liboq.so."""
+    out = []
+    for src in sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp")):
+        for tag, flags in VARIANTS.get(src.name, [("", [])]):
+            name = src.name + (f".{tag}" if tag else "") + ".o"
+            out.append((src, OBJ / name, flags))
+    return out
+
+
+def _stale(obj: Path, src: Path) -> bool:
+    if not obj.exists():
+        return True
+    deps = [src, *CSRC.glob("*.h"), ROOT / "include" / "oq.h", Path(__file__)]
+    return any(d.stat().st_mtime > obj.stat().st_mtime for d in deps)
+
+
+def build(jobs: int = 8, force: bool = True) -> Path:
+    """Compile every translation unit (force=False: only objects older than their sources or
+    any header) and link liboq.so."""
     OBJ.mkdir(exist_ok=True)
-    srcs = sources()
-    objs = [OBJ / (s.name + ".o") for s in srcs]
+    todo = [u for u in units() if force or _stale(u[1], u[0])]
+    objs = [u[1] for u in units()]
 
-    def compile_one(pair):
-        src, obj = pair
+    def compile_one(unit):
+        src, obj, flags = unit
         lang = ["-x", "hip"] if src.suffix == ".hip" else []
-        _run([HIPCC, *DEVICE_FLAGS, *lang, "-c", str(src), "-o", str(obj)])
+        _run([HIPCC, *DEVICE_FLAGS, *flags, *lang, "-c", str(src), "-o", str(obj)])
 
-    with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as pool:
-        list(pool.map(compile_one, zip(srcs, objs)))
+    # the longest units first
+    todo.sort(key=lambda u: (u[0].name != "oq_gemv_inst.hip", u[0].name != "oq_gemv_block.hip"))
+    with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(todo) or 1))) as pool:
+        list(pool.map(compile_one, todo))
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
@@ -65,4 +92,4 @@ def build(jobs: int = 8) -> Path:
 
 
 if __name__ == "__main__":
-    print(build())
+    print(build(force="--incremental" not in sys.argv))

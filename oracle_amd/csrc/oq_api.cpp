@@ -286,9 +286,6 @@ int check_block_weight(oq_context* ctx, const oq_weight* w, uint64_t ne0, uint64
                     std::string("DeltaNet block weight ") + name + " has shape [" + std::to_string(w->m.k) + ", " +
                         std::to_string(w->m.n) + "], expected [" + std::to_string(ne0) + ", " + std::to_string(ne1) + "]");
     }
-    if (is_kquant(w->m.type) && !oq::gemv_kquant_supported(w->m)) {
-        return fail(ctx, OQ_INVALID_ARGUMENT, std::string("DeltaNet block weight ") + name + ": K-quant rows longer than 16384 elements are not supported yet");
-    }
     return OQ_OK;
 }
 
@@ -680,9 +677,6 @@ int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, f
         return fail(ctx, OQ_INVALID_ARGUMENT, "activation / output buffers are misaligned");
     }
     if (is_kquant(t)) {
-        if (!oq::gemv_kquant_supported(w->m)) {
-            return fail(ctx, OQ_INVALID_ARGUMENT, "K-quant rows longer than 16384 elements are not supported yet");
-        }
         if (oq::gemm_mfma_supported(w->m, (int)m) && knob_flag(oq::kGemmMfma, true)) {
             if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
             return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, x, nullptr, y, ctx->scratch.ptr, ctx->stream),
@@ -717,9 +711,6 @@ int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q
     if (m > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "matmul batch too large");
     if (!q8k || !y) return fail(ctx, OQ_INVALID_ARGUMENT, "null buffer");
     if (!aligned(q8k, 4) || !aligned(y, 4)) return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer");
-    if (!oq::gemv_kquant_supported(w->m)) {
-        return fail(ctx, OQ_INVALID_ARGUMENT, "K-quant rows longer than 16384 elements are not supported yet");
-    }
     const uint8_t* q8 = static_cast<const uint8_t*>(q8k);
     if (oq::gemm_mfma_supported(w->m, (int)m) && knob_flag(oq::kGemmMfma, true)) {
         if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
@@ -764,7 +755,11 @@ int oq_capture_end(oq_context* ctx, oq_graph** out) {
     OQ_HIP(ctx, hipStreamEndCapture(ctx->stream, &g), "hipStreamEndCapture");
     hipGraphExec_t ex = nullptr;
     hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    // upload the executable graph now, so that its first launch does not pay for it
+    if (e == hipSuccess) e = hipGraphUpload(ex, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
+        if (ex) (void)hipGraphExecDestroy(ex);
         (void)hipGraphDestroy(g);
         return hip_fail(ctx, e, "hipGraphInstantiate");
     }

@@ -1,0 +1,415 @@
+// The m = 1 decode GEMV of oq_gemv_kq.h with the small operations of a Gated DeltaNet decode
+// block folded into its prologue and epilogue (see the comment below and oq_deltanet.hip).
+#include "oq_gemv_kq.h"
+
+namespace oq {
+
+namespace {
+
+using namespace kq;
+
+// ---------------------------------------------------------------- fused decode-block GEMV
+//
+// The m = 1 kernel above with the small operations of a Gated DeltaNet block folded in (see
+// oq_deltanet.hip for the block order), two rows per wave, 8 waves per workgroup:
+//   prologue  (IN, FFN): x' = (x * inverse_rms(x)) * norm_w before the Q8_K staging; every
+//             workgroup reduces sum x^2 over the whole row itself (double), workgroup 0 also
+//             stores x' (norm_out)
+//   rows      IN: the concatenation of up to four matrices sharing K and type (row pairs never
+//             straddle two); FFN: pair g = (row g of mat[0], row g of mat[1]); ADD: one matrix
+//   epilogue  IN: raw outputs; rows of mat[0] (qkv) run their channel's causal convolution step
+//             and SiLU, rows of mat[2] (beta) the sigmoid, rows of mat[3] (alpha) softplus(a +
+//             dt_bias) * decay; ADD: sum_out[n] = add[n] + y[n]; FFN: act[g] = SiLU(gate) * up.
+namespace blk {
+
+OQ_DEVICE float sigmoid_ref(float v) {
+#pragma clang fp contract(off)
+    if (v >= 0.0f) {
+        const float e = expf(-v);
+        return 1.0f / (1.0f + e);
+    }
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+
+OQ_DEVICE float softplus_ref(float v) {
+    if (v > 20.0f) return v;
+    if (v < -20.0f) return expf(v);
+    return log1pf(expf(v));
+}
+
+OQ_DEVICE float silu_ref(float v) {
+#pragma clang fp contract(off)
+    return v * sigmoid_ref(v);
+}
+
+OQ_DEVICE double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+}  // namespace blk
+
+template <uint32_t TYPE, int ITERS, int MODE, bool FULL>
+OQ_DEVICE void blk_load_group(typename WRegs<TYPE>::type (&W)[2][ITERS], const BlockGemv& a, uint64_t grp, int lane) {
+    const uint32_t nsb = (uint32_t)(a.mat[0].k / kQK);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        uint32_t mi, local;
+        if constexpr (MODE == kBlockFfn) {
+            mi = (uint32_t)r;
+            local = (uint32_t)grp;
+        } else {
+            const uint32_t row = (uint32_t)grp * 2u + (uint32_t)r;
+            mi = 0;
+#pragma unroll
+            for (int i = 0; i < 3; ++i)
+                if ((uint32_t)i + 1 < a.nmat && row >= a.row_end[i]) mi = (uint32_t)i + 1;
+            local = row - (mi ? a.row_end[mi - 1] : 0u);
+        }
+        mi = __builtin_amdgcn_readfirstlane(mi);
+        local = __builtin_amdgcn_readfirstlane(local);
+        const DeviceMatrix& w = a.mat[mi];
+        const uint32_t lrow = local < (uint32_t)w.n ? local : (uint32_t)w.n - 1;
+        const uint8_t* base = w.base + (uint64_t)lrow * w.pitch;
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) load_w<TYPE>(W[r][it], base, nsb, it, lane);
+    }
+}
+
+template <int MODE>
+OQ_DEVICE void blk_epilogue(const BlockGemv& a, uint64_t grp, int lane, float v, float other) {
+    if constexpr (MODE == kBlockFfn) {
+        // lane 0: gate row grp, lane 1: up row grp (other = the up value in lane 0)
+        if (lane == 0) {
+#pragma clang fp contract(off)
+            a.raw[0][grp] = v;
+            a.act[grp] = blk::silu_ref(v) * other;
+        } else if (lane == 1) {
+            a.raw[1][grp] = v;
+        }
+    } else if constexpr (MODE == kBlockAdd) {
+        const uint64_t row = grp * 2 + lane;
+        if (lane < 2 && row < a.mat[0].n) {
+            a.raw[0][row] = v;
+            a.sum_out[row] = a.add[row] + v;
+        }
+    } else {
+        const uint32_t row = (uint32_t)grp * 2u + (uint32_t)lane;
+        if (lane >= 2 || row >= a.row_end[a.nmat - 1]) return;
+        uint32_t mi = 0;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+            if ((uint32_t)i + 1 < a.nmat && row >= a.row_end[i]) mi = (uint32_t)i + 1;
+        const uint32_t l = row - (mi ? a.row_end[mi - 1] : 0u);
+        a.raw[mi][l] = v;
+        if (mi == 0) {
+            // causal depthwise convolution step of channel l (reference_kernels.cpp:197-225) + SiLU
+            float* h = a.history + (uint64_t)l * a.conv_kernel;
+            const float* wc = a.conv_w + (uint64_t)l * a.conv_kernel;
+            double sum = 0.0;
+            for (uint32_t i = 0; i < a.conv_kernel; ++i) {
+#pragma clang fp contract(off)
+                const float t = i + 1 < a.conv_kernel ? h[i + 1] : v;
+                h[i] = t;
+                sum += (double)t * (double)wc[i];
+            }
+            a.conv_out[l] = blk::silu_ref((float)sum);
+        } else if (mi == 2) {
+            a.beta_s[l] = blk::sigmoid_ref(v);
+        } else if (mi == 3) {
+#pragma clang fp contract(off)
+            a.log_decay[l] = blk::softplus_ref(v + a.dt_bias[l]) * a.decay[l];
+        }
+    }
+}
+
+template <uint32_t TYPE, int ITERS, int MODE, bool FULL>
+__global__ __launch_bounds__(512) void gemv_block_kernel(BlockGemv a) {
+    using WR = typename WRegs<TYPE>::type;
+    constexpr int WAVES = 8, R = 2;
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ double red[WAVES];
+    const int lane = threadIdx.x & 63;
+    const int wave_in_wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint64_t wave = (uint64_t)blockIdx.x * WAVES + wave_in_wg;
+    const uint64_t nw = (uint64_t)gridDim.x * WAVES;
+    const uint64_t k = a.mat[0].k;
+    const uint64_t nsb = k / kQK;
+    const uint64_t groups = MODE == kBlockFfn ? a.mat[0].n : ((uint64_t)a.row_end[a.nmat - 1] + 1) / 2;
+    const ActLds s{smem, k};
+    const bool active = wave < groups;
+    WR A[R][ITERS];
+
+    constexpr int SBW = (ITERS * 16 + WAVES - 1) / WAVES;
+    // the norm weights are requested with x (up to two blocks per wave): otherwise their load is
+    // one more round trip after the sum-of-squares barrier
+    constexpr bool kNormEarly = SBW <= 2;
+    float4 xv[SBW], nv[kNormEarly ? SBW : 1];
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        b = b < nsb ? b : nsb - 1;
+        xv[j] = reinterpret_cast<const float4*>(a.x + b * kQK)[lane];
+        if constexpr (kNormEarly) {
+            if (a.norm_w) nv[j] = reinterpret_cast<const float4*>(a.norm_w + b * kQK)[lane];
+        }
+    }
+    asm volatile("" ::: "memory");
+    blk_load_group<TYPE, ITERS, MODE, FULL>(A, a, active ? wave : groups - 1, lane);
+    if (a.norm_w) {
+        // RMSNorm (qwen35_block.cpp:161-186): sum of squares in double over the whole row
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < SBW; ++j) {
+            const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+            if (b < nsb) {
+                ss += (double)xv[j].x * (double)xv[j].x + (double)xv[j].y * (double)xv[j].y +
+                      (double)xv[j].z * (double)xv[j].z + (double)xv[j].w * (double)xv[j].w;
+            }
+        }
+        ss = blk::wave_sum_f64(ss);
+        if (lane == 0) red[wave_in_wg] = ss;
+        __syncthreads();
+        double tot = 0.0;
+#pragma unroll
+        for (int i = 0; i < WAVES; ++i) tot += red[i];
+        const float inv = (float)(1.0 / sqrt(tot / (double)k + (double)a.eps));
+#pragma unroll
+        for (int j = 0; j < SBW; ++j) {
+            const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+            if (b >= nsb) break;
+            float4 w4;
+            if constexpr (kNormEarly) w4 = nv[j];
+            else w4 = reinterpret_cast<const float4*>(a.norm_w + b * kQK)[lane];
+            {
+#pragma clang fp contract(off)
+                xv[j].x = xv[j].x * inv * w4.x;
+                xv[j].y = xv[j].y * inv * w4.y;
+                xv[j].z = xv[j].z * inv * w4.z;
+                xv[j].w = xv[j].w * inv * w4.w;
+            }
+            if (blockIdx.x == 0 && a.norm_out) reinterpret_cast<float4*>(a.norm_out + b * kQK)[lane] = xv[j];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        if (b >= nsb) break;
+        uint32_t qw;
+        int bs;
+        float d;
+        quantize_block(xv[j], lane, qw, bs, d);
+        store_block<TYPE>(s, 0, b, lane, qw, bs, d);
+    }
+    __syncthreads();
+    if (!active) return;
+
+    Act act[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const uint64_t sb = 16u * it + (lane >> 2);
+        if (sb < nsb) slice_from_lds<TYPE>(act[it], s, 0, sb, lane & 3);
+    }
+    const int q = lane & 3;
+    const ScaleSel ss = scale_sel(q);
+    uint64_t grp = wave;
+    while (true) {
+        float acc[R] = {0.0f, 0.0f};
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const uint64_t sb = 16u * it + (lane >> 2);
+            if (!FULL && sb >= nsb) continue;
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] += lane_dot(decode_w<TYPE>(A[r][it], ss, q), act[it]);
+        }
+        float out = 0.0f, other = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = wave_sum_uniform(acc[r]);
+            out = lane == r ? v : out;
+            if (r == 1) other = v;
+        }
+        // the next group's weights go out before the epilogue, whose own loads (convolution
+        // history and taps) then wait behind them instead of delaying them
+        const uint64_t next = grp + nw;
+        if (next < groups) blk_load_group<TYPE, ITERS, MODE, FULL>(A, a, next, lane);
+        blk_epilogue<MODE>(a, grp, lane, out, other);
+        grp = next;
+        if (grp >= groups) break;
+    }
+}
+
+// The residual (ADD) projections of the block -- out projection and FFN down, one matrix each --
+// streamed: x staged as Q8_K in LDS by 16-wave workgroups, then the rows walked as in
+// gemv_stream_kernel (wave i of workgroup b owns rows b * 16 + i + j * (waves in the grid), one
+// pass of one row in flight).  Lane (done % 64) keeps the done-th finished row; every 64 rows, and
+// at the end, each lane writes its row's raw output and residual sum.  Per-lane sums and row
+// reductions as gemv_block_kernel: the same bits.
+template <uint32_t TYPE, int ITERS, bool FULL>
+__global__ __launch_bounds__(1024) void gemv_block_add_stream_kernel(BlockGemv a) {
+    constexpr int WAVES = 16;
+    using WR = typename WRegs<TYPE>::type;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave_in_wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = gridDim.x * WAVES;
+    const DeviceMatrix& w = a.mat[0];
+    const uint32_t nsb = (uint32_t)(w.k / kQK);
+    const uint32_t n = (uint32_t)w.n;
+    const ActLds s{smem, w.k};
+    const uint32_t first = blockIdx.x * WAVES + (uint32_t)wave_in_wg;
+    auto row_base = [&](uint32_t row) {
+        row = row < n ? row : n - 1;  // a wave without rows reads row n-1
+        return w.base + (uint64_t)__builtin_amdgcn_readfirstlane(row) * w.pitch;
+    };
+
+    WR buf[2];
+    stage_one_row<TYPE, ITERS, true, WAVES>(s, a.x, nullptr, nsb, wave_in_wg, lane, [] {});
+    load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane);
+    __syncthreads();
+    if (first >= n) return;
+
+    const int q = lane & 3;
+    const ScaleSel ss = scale_sel(q);
+    constexpr bool kActRegs = ITERS <= 2;
+    Act act[kActRegs ? ITERS : 1];
+    if constexpr (kActRegs) {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const uint32_t sb = 16u * it + (lane >> 2);
+            if (sb < nsb) slice_from_lds<TYPE>(act[it], s, 0, sb, q);
+        }
+    }
+    float acc = 0.0f, out = 0.0f;
+    uint32_t out_row = 0, done = 0;
+    uint32_t row = first, it = 0;  // the unit whose loads are in flight
+    bool more = true;
+    while (more) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int its = ITERS == 1 ? 0 : (ITERS == 2 ? j : (int)it);
+            asm volatile("s_waitcnt vmcnt(0)" : "+v"(acc), "+v"(out)::"memory");
+            uint32_t nrow = row, nit = it + 1;
+            if (nit == ITERS) {
+                nrow = row + nw < row ? n : row + nw;
+                nit = 0;
+            }
+            more = nrow < n;
+            load_w<TYPE>(buf[(j + 1) & 1], row_base(more ? nrow : row), nsb, (int)(more ? nit : it), lane);
+            hold<TYPE>(buf[j & 1]);
+            const uint32_t sb = 16u * (uint32_t)its + (lane >> 2);
+            if (FULL || sb < nsb) {
+                if constexpr (kActRegs) {
+                    acc += lane_dot(decode_w<TYPE>(buf[j & 1], ss, q), act[its]);
+                } else {
+                    Act av;
+                    slice_from_lds<TYPE>(av, s, 0, sb, q);
+                    acc += lane_dot(decode_w<TYPE>(buf[j & 1], ss, q), av);
+                }
+            }
+            if (it == ITERS - 1) {
+                const float v = wave_sum_uniform(acc);
+                const bool mine = lane == (int)(done & 63u);
+                out = mine ? v : out;
+                out_row = mine ? row : out_row;
+                acc = 0.0f;
+                ++done;
+                if ((done & 63u) == 0u) {
+                    a.raw[0][out_row] = out;
+                    a.sum_out[out_row] = a.add[out_row] + out;
+                }
+            }
+            row = nrow;
+            it = nit;
+            if (!more) break;
+        }
+    }
+    if ((uint32_t)lane < (done & 63u)) {
+        a.raw[0][out_row] = out;
+        a.sum_out[out_row] = a.add[out_row] + out;
+    }
+}
+
+template <uint32_t TYPE, int ITERS, bool FULL>
+hipError_t launch_block_add_stream(const BlockGemv& a, hipStream_t s) {
+    const uint64_t lds = act_lds_bytes(a.mat[0].k, 1);
+    uint64_t wgs = (uint64_t)cu_count();
+    const uint64_t need = (a.mat[0].n + 15) / 16;
+    if (wgs > need) wgs = need;
+    hipLaunchKernelGGL((gemv_block_add_stream_kernel<TYPE, ITERS, FULL>), dim3((unsigned)wgs), dim3(1024), lds, s, a);
+    return hipGetLastError();
+}
+
+template <uint32_t TYPE, int ITERS, int MODE, bool FULL>
+hipError_t launch_block_full(const BlockGemv& a, hipStream_t s) {
+    if constexpr (MODE == kBlockAdd) {
+        // the residual projections without a normalising prologue stream like the plain decode
+        // GEMV (FFN down 4096 x 12288: 9.3 us against 11.1 us in the structure below)
+        if (a.norm_w == nullptr && knob(kBlockStream, 1) != 0)
+            return launch_block_add_stream<TYPE, ITERS, FULL>(a, s);
+    }
+    const uint64_t groups = MODE == kBlockFfn ? a.mat[0].n : ((uint64_t)a.row_end[a.nmat - 1] + 1) / 2;
+    const uint64_t lds = act_lds_bytes(a.mat[0].k, 1);
+    static int resident = 0;
+    if (resident == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_block_kernel<TYPE, ITERS, MODE, FULL>, 512, lds) !=
+                hipSuccess || n < 1) {
+            n = 1;
+        }
+        resident = n;
+    }
+    uint64_t wgs = (uint64_t)cu_count() * (uint64_t)(resident < 2 ? resident : 2);
+    const uint64_t need = (groups + 7) / 8;
+    if (wgs > need) wgs = need;
+    hipLaunchKernelGGL((gemv_block_kernel<TYPE, ITERS, MODE, FULL>), dim3((unsigned)wgs), dim3(512), lds, s, a);
+    return hipGetLastError();
+}
+
+template <uint32_t TYPE, int MODE>
+hipError_t launch_block_type(const BlockGemv& a, hipStream_t s) {
+    const uint64_t nsb = a.mat[0].k / kQK;
+    const bool full = nsb % 16 == 0;
+    switch ((nsb + 15) / 16) {
+        case 1: return full ? launch_block_full<TYPE, 1, MODE, true>(a, s) : launch_block_full<TYPE, 1, MODE, false>(a, s);
+        case 2: return full ? launch_block_full<TYPE, 2, MODE, true>(a, s) : launch_block_full<TYPE, 2, MODE, false>(a, s);
+        case 3: return full ? launch_block_full<TYPE, 3, MODE, true>(a, s) : launch_block_full<TYPE, 3, MODE, false>(a, s);
+        default: return hipErrorNotSupported;
+    }
+}
+
+template <int MODE>
+hipError_t launch_block_mode(const BlockGemv& a, hipStream_t s) {
+    switch (a.mat[0].type) {
+        case 12: return launch_block_type<12, MODE>(a, s);
+        case 14: return launch_block_type<14, MODE>(a, s);
+        default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace
+
+bool gemv_block_supported(const BlockGemv& a) {
+    if (a.nmat < 1 || a.nmat > 4) return false;
+    const DeviceMatrix& w0 = a.mat[0];
+    if ((w0.type != 12 && w0.type != 14) || w0.k % kQK != 0 || (w0.k / kQK + 15) / 16 > 3) return false;
+    if (act_lds_bytes(w0.k, 1) > kLdsBudget) return false;
+    for (uint32_t i = 1; i < a.nmat; ++i) {
+        if (a.mat[i].type != w0.type || a.mat[i].k != w0.k || a.mat[i].pitch != w0.pitch) return false;
+    }
+    return true;
+}
+
+hipError_t launch_gemv_block(int mode, const BlockGemv& a, hipStream_t s) {
+    if (!gemv_block_supported(a)) return hipErrorNotSupported;
+    switch (mode) {
+        case kBlockIn: return launch_block_mode<kBlockIn>(a, s);
+        case kBlockAdd: return launch_block_mode<kBlockAdd>(a, s);
+        case kBlockFfn: return launch_block_mode<kBlockFfn>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace oq

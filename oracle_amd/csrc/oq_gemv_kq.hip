@@ -1,0 +1,97 @@
+// Dispatch of the K-quant (q4_K, q5_K, q6_K) decode GEMV and small-batch products
+// (oq_gemv_kq.h; instantiated per type and activation form in oq_gemv_inst.hip).
+//
+// Rows of up to 16384 elements whose Q8_K image fits the LDS budget run the compile-time kernels
+// (activation slices in registers, every pass unrolled), at most 8 activation rows per launch.
+// Longer rows run the windowed kernel: consecutive launches over windows of passes, each adding
+// its partial sums to y, at most two activation rows per launch.
+#include "oq_gemv_kq.h"
+
+namespace oq {
+
+namespace {
+
+template <bool FUSED>
+hipError_t launch_type(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+    switch (w.type) {
+        case 12: return launch_kq<12, FUSED>(w, m, x, q8k, y, s);
+        case 13: return launch_kq<13, FUSED>(w, m, x, q8k, y, s);
+        case 14: return launch_kq<14, FUSED>(w, m, x, q8k, y, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <bool FUSED>
+hipError_t launch_type_window(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
+                              uint32_t pass0, uint32_t npass, int accumulate, hipStream_t s) {
+    switch (w.type) {
+        case 12: return launch_kq_window<12, FUSED>(w, m, x, q8k, y, pass0, npass, accumulate, s);
+        case 13: return launch_kq_window<13, FUSED>(w, m, x, q8k, y, pass0, npass, accumulate, s);
+        case 14: return launch_kq_window<14, FUSED>(w, m, x, q8k, y, pass0, npass, accumulate, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool short_rows(const DeviceMatrix& w) {
+    return (w.k / kQK + 15) / 16 <= (uint64_t)kq::kMaxIters && kq::act_lds_bytes(w.k, 1) <= kq::kLdsBudget;
+}
+
+}  // namespace
+
+int gemv_max_m() { return 8; }
+
+bool gemv_kquant_supported(const DeviceMatrix& w) {
+    return (w.type == 12 || w.type == 13 || w.type == 14) && w.k > 0 && w.k % kQK == 0;
+}
+
+uint32_t gemv_window_passes(const DeviceMatrix& w, int m) {
+    if (short_rows(w)) return 0;
+    const int rows = m >= 2 ? 2 : 1;
+    const uint64_t per_pass = kq::act_lds_bytes(16 * kQK, rows);  // LDS image of one pass of `rows` rows
+    const uint64_t win = kq::kLdsBudget / per_pass;
+    return (uint32_t)(win < 1 ? 1 : win);
+}
+
+hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
+                              hipStream_t s) {
+    if (!gemv_kquant_supported(w)) return hipErrorNotSupported;
+    const uint64_t nsb = w.k / kQK;
+    if (short_rows(w)) {
+        // activation rows per launch: what fits the LDS budget, at most 8
+        int chunk = 8;
+        while (chunk > 1 && kq::act_lds_bytes(w.k, chunk) > kq::kLdsBudget) chunk >>= 1;
+        for (int m0 = 0; m0 < m; m0 += chunk) {
+            const int mc = m - m0 < chunk ? m - m0 : chunk;
+            hipError_t e;
+            if (x != nullptr) {
+                e = launch_type<true>(w, mc, x + (uint64_t)m0 * w.k, nullptr, y + (uint64_t)m0 * w.n, s);
+            } else {
+                e = launch_type<false>(w, mc, nullptr, q8k + (uint64_t)m0 * nsb * kQ8KBytes, y + (uint64_t)m0 * w.n,
+                                       s);
+            }
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    const uint32_t passes = (uint32_t)((nsb + 15) / 16);
+    const uint32_t win = gemv_window_passes(w, m);
+    const int chunk = 2;
+    for (int m0 = 0; m0 < m; m0 += chunk) {
+        const int mc = m - m0 < chunk ? m - m0 : chunk;
+        for (uint32_t p0 = 0; p0 < passes; p0 += win) {
+            const uint32_t np = passes - p0 < win ? passes - p0 : win;
+            hipError_t e;
+            if (x != nullptr) {
+                e = launch_type_window<true>(w, mc, x + (uint64_t)m0 * w.k, nullptr, y + (uint64_t)m0 * w.n, p0, np,
+                                             p0 > 0, s);
+            } else {
+                e = launch_type_window<false>(w, mc, nullptr, q8k + (uint64_t)m0 * nsb * kQ8KBytes,
+                                              y + (uint64_t)m0 * w.n, p0, np, p0 > 0, s);
+            }
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
+}  // namespace oq

@@ -68,13 +68,23 @@ hipError_t launch_dequantize(const DeviceMatrix& w, uint64_t row0, uint64_t nrow
 hipError_t launch_quantize_q8k(const float* x, uint64_t m, uint64_t k, uint8_t* q8k,
                                hipStream_t s);
 
-// ---- oq_gemv_reg.hip  (K-quant weights, m <= 8 activation rows per launch, weights streamed once)
+// ---- oq_gemv_kq.hip  (K-quant weights, m <= 8 activation rows per launch, weights streamed once)
 // Q8_K activations given as blocks (q8k) or as F32 (x, quantized by every workgroup into LDS;
 // bit-identical to launch_quantize_q8k).
 bool gemv_kquant_supported(const DeviceMatrix& w);
 hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k,
                               float* y, hipStream_t s);
 int gemv_max_m();
+// passes per launch of the windowed long-row kernel for m activation rows (0: the row fits the
+// compile-time kernels)
+uint32_t gemv_window_passes(const DeviceMatrix& w, int m);
+
+// ---- oq_gemv_inst.hip  (one instantiation set per weight type and activation form)
+template <uint32_t TYPE, bool FUSED>
+hipError_t launch_kq(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s);
+template <uint32_t TYPE, bool FUSED>
+hipError_t launch_kq_window(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
+                            uint32_t pass0, uint32_t npass, int accumulate, hipStream_t s);
 
 // ---- oq_gemv.hip  (q8_0 / f32 / f16 / bf16 weights against F32 activations)
 hipError_t launch_gemv_f32act(const DeviceMatrix& w, int m, const float* x, float* y,
@@ -108,7 +118,7 @@ hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_he
 hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s);
 hipError_t launch_add(const float* a, const float* b, uint64_t n, float* out, hipStream_t s);
 
-// ---- oq_gemv_reg.hip  (fused m = 1 GEMV of the DeltaNet decode block; see the kernel comment)
+// ---- oq_gemv_block.hip  (fused m = 1 GEMV of the DeltaNet decode block; see the kernel comment)
 enum : int { kBlockIn = 0, kBlockAdd = 1, kBlockFfn = 2 };
 struct BlockGemv {
     DeviceMatrix mat[4];   // same type, K and pitch

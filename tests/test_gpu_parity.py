@@ -551,3 +551,41 @@ def test_graph_replay_after_workspace_growth(ctx):
     for b in (xb, yb, xbig, ybig):
         b.free()
     w.release()
+
+
+@pytest.mark.parametrize("t,rows,cols,m", [
+    (12, 700, 17408, 1), (12, 300, 17408, 3), (13, 257, 24576, 1), (14, 333, 24576, 2), (12, 130, 65536, 1),
+    (14, 90, 65536, 5), (13, 64, 17408, 8), (12, 4096, 17408, 1)])
+def test_long_rows(ctx, t, rows, cols, m):
+    """K-quant rows longer than 16384 elements (the reference's dot has no length limit,
+    src/backend/cpu/quantized_reference.cpp:128-162): windows of passes multiplied by consecutive
+    launches, each adding its partial sums; F32 and Q8_K activations give the same bits."""
+    rng = np.random.default_rng(7000 + t + cols + m)
+    data = synth.weights(t, rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(t, cols, rows, data)
+    y = gpu_matmul(ctx, w, x, rows)
+    xb, qb, yb = ctx.to_device(x), ctx.alloc(m * (cols // 256) * 292), ctx.alloc(m * rows * 4)
+    ctx.quantize_q8k(xb, m, cols, qb)
+    yb.upload(np.full(m * rows, np.nan, np.float32))
+    ctx.matmul_q8k(w, m, qb, yb)
+    y_q8k = yb.download(np.float32, m * rows).reshape(m, rows)
+    for b in (xb, qb, yb):
+        b.free()
+    assert np.array_equal(y.view(np.uint32), y_q8k.view(np.uint32))
+    y_ref, norm = reference_products(t, rows, cols, data, x)
+    check_close(y, y_ref, norm)
+    w.release()
+
+
+def test_long_rows_matrix_cores(ctx):
+    """The M >= 16 q4_K product on matrix cores with K = 17408 (not a multiple of 4096)."""
+    rng = np.random.default_rng(7171)
+    rows, cols, m = 256, 17408, 32
+    data = synth.q4_k(rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(12, cols, rows, data)
+    y = gpu_matmul(ctx, w, x, rows)
+    y_ref, norm = reference_products(12, rows, cols, data, x)
+    check_close(y, y_ref, norm)
+    w.release()
