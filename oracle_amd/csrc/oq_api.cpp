@@ -292,8 +292,8 @@ int check_block_weight(oq_context* ctx, const oq_weight* w, uint64_t ne0, uint64
 // Workspace of one block step: the trace fields, then beta_s, log_decay and the normalised input,
 // each padded to 64 floats so every projection input is 256-byte aligned.
 struct BlockLayout {
-    uint64_t sizes[17];
-    uint64_t off[17];
+    uint64_t sizes[18];
+    uint64_t off[18];
     uint64_t total_floats;
 };
 
@@ -301,8 +301,9 @@ BlockLayout block_layout(const oq_deltanet_block* b) {
     const uint64_t E = b->embedding, Hk = b->key_heads, Hv = b->value_heads, dk = b->key_dim, dv = b->value_dim,
                    F = b->ffn;
     const uint64_t V = Hv * dv, C = 2 * Hk * dk + V;
-    BlockLayout l{{C, V, Hv, Hv, C, V, V, E, E, E, F, F, F, E, Hv, Hv, E}, {}, 0};
-    for (int i = 0; i < 17; ++i) {
+    // the last field: the delta rule's per-chunk double sums of squares (2 floats each)
+    BlockLayout l{{C, V, Hv, Hv, C, V, V, E, E, E, F, F, F, E, Hv, Hv, E, 2 * Hv * oq::delta_chunks(dv)}, {}, 0};
+    for (int i = 0; i < 18; ++i) {
         l.off[i] = l.total_floats;
         l.total_floats += (l.sizes[i] + 63) & ~uint64_t(63);
     }
@@ -361,6 +362,7 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
           *rec = ws + off[5], *gated = ws + off[6], *branch = ws + off[7], *resid = ws + off[8], *post = ws + off[9],
           *gate = ws + off[10], *up = ws + off[11], *act = ws + off[12], *ffn = ws + off[13], *beta_s = ws + off[14],
           *log_decay = ws + off[15], *normed = ws + off[16];
+    double* head_ss = reinterpret_cast<double*>(ws + off[17]);
     hipStream_t s = ctx->stream;
     hipError_t e = hipSuccess;
     // Fused path: five launches (normed in-projections with the convolution and gates, the delta
@@ -398,6 +400,17 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
     outp.raw[0] = branch;
     outp.add = x;
     outp.sum_out = resid;
+    outp.eps = b->eps;
+    if (oq::gemv_block_add_streams(outp)) {
+        // the out projection forms the gated activation in its staging (and stores it)
+        outp.rec = rec;
+        outp.head_ss = head_ss;
+        outp.z = z;
+        outp.out_norm = b->out_norm;
+        outp.dv = (uint32_t)dv;
+        outp.dchunks = (uint32_t)oq::delta_chunks(dv);
+        outp.gated_out = gated;
+    }
     ffn_in.nmat = 2;
     ffn_in.mat[0] = b->gate->m;
     ffn_in.mat[1] = b->up->m;
@@ -423,8 +436,9 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
                        oq::gemv_block_supported(down);
     if (fused) {
         e = oq::launch_gemv_block(oq::kBlockIn, in, s);
-        if (e == hipSuccess)
-            e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, z, b->out_norm, rec, gated, s);
+        if (e == hipSuccess) e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, rec, head_ss, s);
+        if (e == hipSuccess && outp.rec == nullptr)
+            e = oq::launch_gated_norm(rec, head_ss, z, b->out_norm, Hv, dv, b->eps, gated, s);
         if (e == hipSuccess) e = oq::launch_gemv_block(oq::kBlockAdd, outp, s);
         if (e == hipSuccess) e = oq::launch_gemv_block(oq::kBlockFfn, ffn_in, s);
         if (e == hipSuccess) e = oq::launch_gemv_block(oq::kBlockAdd, down, s);
@@ -437,8 +451,8 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
         if (e == hipSuccess)
             e = oq::launch_conv_gates(qkv, b->conv_weight, hist, C, K, beta, alpha, b->dt_bias, b->decay, Hv, conv, beta_s,
                                       log_decay, s);
-        if (e == hipSuccess)
-            e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, z, b->out_norm, rec, gated, s);
+        if (e == hipSuccess) e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, rec, head_ss, s);
+        if (e == hipSuccess) e = oq::launch_gated_norm(rec, head_ss, z, b->out_norm, Hv, dv, b->eps, gated, s);
         if (e == hipSuccess) e = block_project(b->out, gated, branch, s);
         if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s);
         if (e == hipSuccess) e = block_project(b->gate, post, gate, s);

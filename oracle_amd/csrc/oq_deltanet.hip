@@ -110,92 +110,118 @@ __global__ __launch_bounds__(256) void conv_gates_kernel(const float* __restrict
     conv_out[c] = silu_ref((float)sum);
 }
 
-// One value head per workgroup, one value column per thread (blockDim.x = dv): the gated delta
-// rule step (reference_kernels.cpp:227-335) on the state [head][key][value] with the head's
-// query/key taken from key head h % Hk (repeat_heads_tiled, qwen35_block.cpp:233-251), then the
-// head's RMSNorm with weight out_norm gated by SiLU(z) (qwen35_block.cpp:579-588).
-// Thread v keeps state column v (DK values) in registers: the DK loads are issued together, then
-// the column is decayed and reduced in key order, updated, stored and reduced again: one read
-// and one write of the state.  dv is 64, 128, 192 or 256.
+// The gated delta rule step (reference_kernels.cpp:227-335) on the state [head][key][value],
+// one workgroup per (value head h, chunk of 32 value columns), 256 threads = 8 key slices x 32
+// columns: thread (slice, column) keeps the DK/8 state values of its column and key slice in
+// registers, so the head's state is read once and written once by DK/8-deep chains spread over
+// Hv * dv/32 workgroups.  The head's query/key come from key head h % Hk (repeat_heads_tiled,
+// qwen35_block.cpp:233-251), L2-normalised by the first wave (double sums of squares, the scale
+// 1/max(norm, eps) rounded to F32, q also by 1/sqrt(DK)).  Per column: the decayed state's memory
+// sum_k S k is formed in F32 per key slice in key order, then over the slices in key order;
+// delta = (v - memory) * beta; the updated column's output sum_k S q in double the same way.
+// Outputs: rec_out[h][v] and, per (head, chunk), the double sum of the chunk's rec_out^2 in
+// head_ss[h * chunks + chunk] -- the head's gated RMSNorm (qwen35_block.cpp:579-588) is applied
+// where rec_out is consumed (gated_norm_kernel, or the out projection's activation staging).
+constexpr int kDeltaCols = 32;
+constexpr int kDeltaSlices = 8;
+
 template <int DK>
 __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ conv, uint32_t key_heads, uint32_t dv,
                                                     const float* __restrict__ beta_s, const float* __restrict__ log_decay,
-                                                    float eps, float* __restrict__ state, const float* __restrict__ z,
-                                                    const float* __restrict__ out_norm, float* __restrict__ rec_out,
-                                                    float* __restrict__ gated) {
+                                                    float eps, float* __restrict__ state, float* __restrict__ rec_out,
+                                                    double* __restrict__ head_ss) {
+    constexpr int KS = DK / kDeltaSlices;  // keys per thread
     __shared__ __align__(16) float nq[DK];
     __shared__ __align__(16) float nk[DK];
-    __shared__ double red[16];
-    const uint32_t h = blockIdx.x, v = threadIdx.x;
-    float* col = state + (uint64_t)h * DK * dv + v;
+    __shared__ float mem_part[kDeltaSlices][kDeltaCols];
+    __shared__ double out_part[kDeltaSlices][kDeltaCols];
+    const uint32_t chunks = dv / kDeltaCols;
+    const uint32_t h = blockIdx.x / chunks, chunk = blockIdx.x % chunks;
+    const uint32_t col = threadIdx.x % kDeltaCols, slice = threadIdx.x / kDeltaCols;
+    const uint32_t v = chunk * kDeltaCols + col;
+    const uint32_t d0 = slice * KS;
+    float* scol = state + ((uint64_t)h * DK + d0) * dv + v;
     const uint32_t kw = key_heads * DK;
-    // every input is requested here, before the first barrier: a load issued after a barrier
-    // would add one more memory round trip to the kernel's chain
-    const float vv = conv[2u * kw + (uint64_t)h * dv + v];
-    const float zv = z[(uint64_t)h * dv + v];
-    const float onw = out_norm[v];
-    const float ldh = log_decay[h];
-    const float beta = beta_s[h];
-    float s[DK];
-#pragma unroll
-    for (int d = 0; d < DK; ++d) s[d] = col[(uint64_t)d * dv];
-
     const float* q = conv + (uint64_t)(h % key_heads) * DK;
     const float* k = conv + kw + (uint64_t)(h % key_heads) * DK;
-    double qs = 0.0, ks = 0.0;
-    for (uint32_t d = v; d < DK; d += blockDim.x) {
-        qs += (double)q[d] * (double)q[d];
-        ks += (double)k[d] * (double)k[d];
-    }
-    qs = block_sum_f64(qs, red);
-    ks = block_sum_f64(ks, red);
-    const double ql = sqrt(qs), kl = sqrt(ks);
-    const float iq = (float)(1.0 / (ql > (double)eps ? ql : (double)eps));
-    const float ik = (float)(1.0 / (kl > (double)eps ? kl : (double)eps));
-    const float query_scale = 1.0f / sqrtf((float)DK);
-    for (uint32_t d = v; d < DK; d += blockDim.x) {
-        nq[d] = q[d] * iq * query_scale;
-        nk[d] = k[d] * ik;
+    // every input is requested before the first barrier
+    float s[KS];
+#pragma unroll
+    for (int i = 0; i < KS; ++i) s[i] = scol[(uint64_t)i * dv];
+    const float vv = conv[2u * kw + (uint64_t)h * dv + v];
+    const float ldh = log_decay[h];
+    const float beta = beta_s[h];
+    if (threadIdx.x < 64) {
+        // the first wave: L2 norms of the head's query and key (DK <= 128: two values per lane)
+        const int lane = threadIdx.x;
+        const float q0 = lane < DK ? q[lane] : 0.0f, k0 = lane < DK ? k[lane] : 0.0f;
+        const float q1 = lane + 64 < DK ? q[lane + 64] : 0.0f, k1 = lane + 64 < DK ? k[lane + 64] : 0.0f;
+        const double qs = wave_sum_f64((double)q0 * (double)q0 + (double)q1 * (double)q1);
+        const double ks = wave_sum_f64((double)k0 * (double)k0 + (double)k1 * (double)k1);
+        const double ql = sqrt(qs), kl = sqrt(ks);
+        const float iq = (float)(1.0 / (ql > (double)eps ? ql : (double)eps));
+        const float ik = (float)(1.0 / (kl > (double)eps ? kl : (double)eps));
+        const float query_scale = 1.0f / sqrtf((float)DK);
+        if (lane < DK) {
+            nq[lane] = q0 * iq * query_scale;
+            nk[lane] = k0 * ik;
+        }
+        if (lane + 64 < DK) {
+            nq[lane + 64] = q1 * iq * query_scale;
+            nk[lane + 64] = k1 * ik;
+        }
     }
     __syncthreads();
 
     const float decay = expf(ldh);
-    const float4* nk4 = reinterpret_cast<const float4*>(nk);
-    const float4* nq4 = reinterpret_cast<const float4*>(nq);
-    // the empty asm statements keep each chunk's LDS reads next to their use, so the unrolled
-    // loops hold the state column and only four keys in registers
     float mem = 0.0f;
 #pragma unroll
-    for (int d = 0; d < DK; d += 4) {
-        asm volatile("" ::: "memory");
-        const float4 kk = nk4[d / 4];
-        const float kv[4] = {kk.x, kk.y, kk.z, kk.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            s[d + i] = s[d + i] * decay;
-            mem = mem + s[d + i] * kv[i];
-        }
+    for (int i = 0; i < KS; ++i) {
+        s[i] = s[i] * decay;
+        mem = mem + s[i] * nk[d0 + i];
     }
-    const float delta = (vv - mem) * beta;
+    mem_part[slice][col] = mem;
+    __syncthreads();
+    float memory = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kDeltaSlices; ++j) memory = memory + mem_part[j][col];
+    const float delta = (vv - memory) * beta;
     double o = 0.0;
 #pragma unroll
-    for (int d = 0; d < DK; d += 4) {
-        asm volatile("" ::: "memory");
-        const float4 kk = nk4[d / 4], qq = nq4[d / 4];
-        const float kv[4] = {kk.x, kk.y, kk.z, kk.w}, qv[4] = {qq.x, qq.y, qq.z, qq.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            s[d + i] = s[d + i] + kv[i] * delta;
-            col[(uint64_t)(d + i) * dv] = s[d + i];
-            o = o + (double)s[d + i] * (double)qv[i];
-        }
+    for (int i = 0; i < KS; ++i) {
+        s[i] = s[i] + nk[d0 + i] * delta;
+        scol[(uint64_t)i * dv] = s[i];
+        o = o + (double)s[i] * (double)nq[d0 + i];
     }
-    const float of = (float)o;
-    rec_out[(uint64_t)h * dv + v] = of;
-    const double ss = block_sum_f64((double)of * (double)of, red);
+    out_part[slice][col] = o;
+    __syncthreads();
+    if (slice == 0) {
+        double out = 0.0;
+#pragma unroll
+        for (int j = 0; j < kDeltaSlices; ++j) out = out + out_part[j][col];
+        const float of = (float)out;
+        rec_out[(uint64_t)h * dv + v] = of;
+        // the chunk's sum of squares, over the 32 lanes of this half wave (lanes 0..31 of wave 0)
+        double sq = (double)of * (double)of;
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) sq += __shfl_xor(sq, off, 64);
+        if (col == 0) head_ss[(uint64_t)h * chunks + chunk] = sq;
+    }
+}
+
+// gated[h][v] = RMSNorm(rec[h])[v] * out_norm[v] * SiLU(z[h][v]) (qwen35_block.cpp:579-588), the
+// head's sum of squares taken from the delta kernel's per-chunk partials (added in chunk order).
+__global__ __launch_bounds__(256) void gated_norm_kernel(const float* __restrict__ rec, const double* __restrict__ head_ss,
+                                                         const float* __restrict__ z, const float* __restrict__ out_norm,
+                                                         uint32_t heads, uint32_t dv, float eps,
+                                                         float* __restrict__ gated) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= heads * dv) return;
+    const uint32_t h = i / dv, v = i % dv, chunks = dv / kDeltaCols;
+    double ss = 0.0;
+    for (uint32_t c = 0; c < chunks; ++c) ss += head_ss[(uint64_t)h * chunks + c];
     const float inv = (float)(1.0 / sqrt(ss / (double)dv + (double)eps));
-    const float g = silu_ref(zv);
-    gated[(uint64_t)h * dv + v] = of * inv * onw * g;
+    gated[i] = rec[i] * inv * out_norm[v] * silu_ref(z[i]);
 }
 
 // act = silu(gate) * up (qwen35_block.cpp:313-316)
@@ -240,27 +266,37 @@ hipError_t launch_conv_gates(const float* qkv, const float* conv_w, float* histo
 }
 
 hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_heads, uint64_t dk, uint64_t dv,
-                        const float* beta_s, const float* log_decay, float eps, float* state, const float* z,
-                        const float* out_norm, float* rec_out, float* gated, hipStream_t s) {
-    const dim3 grid((unsigned)value_heads), block((unsigned)dv);
+                        const float* beta_s, const float* log_decay, float eps, float* state, float* rec_out,
+                        double* head_ss, hipStream_t s) {
+    if (dv % kDeltaCols != 0) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(value_heads * (dv / kDeltaCols))), block(kDeltaCols * kDeltaSlices);
     switch (dk) {
         case 32:
             hipLaunchKernelGGL(delta_kernel<32>, grid, block, 0, s, conv, (uint32_t)key_heads, (uint32_t)dv, beta_s,
-                               log_decay, eps, state, z, out_norm, rec_out, gated);
+                               log_decay, eps, state, rec_out, head_ss);
             break;
         case 64:
             hipLaunchKernelGGL(delta_kernel<64>, grid, block, 0, s, conv, (uint32_t)key_heads, (uint32_t)dv, beta_s,
-                               log_decay, eps, state, z, out_norm, rec_out, gated);
+                               log_decay, eps, state, rec_out, head_ss);
             break;
         case 128:
             hipLaunchKernelGGL(delta_kernel<128>, grid, block, 0, s, conv, (uint32_t)key_heads, (uint32_t)dv, beta_s,
-                               log_decay, eps, state, z, out_norm, rec_out, gated);
+                               log_decay, eps, state, rec_out, head_ss);
             break;
         default:
             return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
+
+hipError_t launch_gated_norm(const float* rec, const double* head_ss, const float* z, const float* out_norm,
+                             uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s) {
+    hipLaunchKernelGGL(gated_norm_kernel, dim3(blocks_of(heads * dv, 256)), dim3(256), 0, s, rec, head_ss, z, out_norm,
+                       (uint32_t)heads, (uint32_t)dv, eps, gated);
+    return hipGetLastError();
+}
+
+uint64_t delta_chunks(uint64_t dv) { return dv / kDeltaCols; }
 
 hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s) {
     hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_of(n, 256)), dim3(256), 0, s, gate, up, (uint32_t)n, act);

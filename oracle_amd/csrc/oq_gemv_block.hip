@@ -247,6 +247,48 @@ __global__ __launch_bounds__(512) void gemv_block_kernel(BlockGemv a) {
 // pass of one row in flight).  Lane (done % 64) keeps the done-th finished row; every 64 rows, and
 // at the end, each lane writes its row's raw output and residual sum.  Per-lane sums and row
 // reductions as gemv_block_kernel: the same bits.
+// Stages the recurrent block's gated output as the activation row (Q8_K in LDS): value i of head
+// h = i / dv is ((rec[i] * inv_rms(h)) * out_norm[i % dv]) * SiLU(z[i]) (qwen35_block.cpp:579-588),
+// inv_rms(h) = 1 / sqrt(ss_h / dv + eps) with ss_h the delta rule's per-chunk sums of squares
+// added in chunk order.  dv is a multiple of 32, so a lane's four values share one head.
+template <uint32_t TYPE, int ITERS, int WAVES>
+OQ_DEVICE void stage_gated_row(const ActLds& s, const BlockGemv& a, uint64_t nsb, int wave_in_wg, int lane) {
+#pragma clang fp contract(off)
+    constexpr int SBW = (ITERS * 16 + WAVES - 1) / WAVES;
+    float4 rv[SBW], zv[SBW], wv[SBW];
+    double ssv[SBW];
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        b = b < nsb ? b : nsb - 1;
+        const uint64_t i = b * kQK + 4u * (uint32_t)lane;
+        rv[j] = *reinterpret_cast<const float4*>(a.rec + i);
+        zv[j] = *reinterpret_cast<const float4*>(a.z + i);
+        wv[j] = *reinterpret_cast<const float4*>(a.out_norm + i % a.dv);
+        const double* hs = a.head_ss + (i / a.dv) * a.dchunks;
+        double ss = 0.0;
+        for (uint32_t c = 0; c < a.dchunks; ++c) ss += hs[c];
+        ssv[j] = ss;
+    }
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        if (b >= nsb) break;
+        const float inv = (float)(1.0 / sqrt(ssv[j] / (double)a.dv + (double)a.eps));
+        float4 g;
+        g.x = rv[j].x * inv * wv[j].x * blk::silu_ref(zv[j].x);
+        g.y = rv[j].y * inv * wv[j].y * blk::silu_ref(zv[j].y);
+        g.z = rv[j].z * inv * wv[j].z * blk::silu_ref(zv[j].z);
+        g.w = rv[j].w * inv * wv[j].w * blk::silu_ref(zv[j].w);
+        if (blockIdx.x == 0) reinterpret_cast<float4*>(a.gated_out + b * kQK)[lane] = g;
+        uint32_t qw;
+        int bs;
+        float d;
+        quantize_block(g, lane, qw, bs, d);
+        store_block<TYPE>(s, 0, b, lane, qw, bs, d);
+    }
+}
+
 template <uint32_t TYPE, int ITERS, bool FULL>
 __global__ __launch_bounds__(1024) void gemv_block_add_stream_kernel(BlockGemv a) {
     constexpr int WAVES = 16;
@@ -266,7 +308,11 @@ __global__ __launch_bounds__(1024) void gemv_block_add_stream_kernel(BlockGemv a
     };
 
     WR buf[2];
-    stage_one_row<TYPE, ITERS, true, WAVES>(s, a.x, nullptr, nsb, wave_in_wg, lane, [] {});
+    if (a.rec != nullptr) {
+        stage_gated_row<TYPE, ITERS, WAVES>(s, a, nsb, wave_in_wg, lane);
+    } else {
+        stage_one_row<TYPE, ITERS, true, WAVES>(s, a.x, nullptr, nsb, wave_in_wg, lane, [] {});
+    }
     load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane);
     __syncthreads();
     if (first >= n) return;
@@ -347,8 +393,8 @@ hipError_t launch_block_full(const BlockGemv& a, hipStream_t s) {
     if constexpr (MODE == kBlockAdd) {
         // the residual projections without a normalising prologue stream like the plain decode
         // GEMV (FFN down 4096 x 12288: 9.3 us against 11.1 us in the structure below)
-        if (a.norm_w == nullptr && knob(kBlockStream, 1) != 0)
-            return launch_block_add_stream<TYPE, ITERS, FULL>(a, s);
+        if (gemv_block_add_streams(a)) return launch_block_add_stream<TYPE, ITERS, FULL>(a, s);
+        if (a.rec != nullptr) return hipErrorInvalidValue;  // only the streamed kernel forms the gated row
     }
     const uint64_t groups = MODE == kBlockFfn ? a.mat[0].n : ((uint64_t)a.row_end[a.nmat - 1] + 1) / 2;
     const uint64_t lds = act_lds_bytes(a.mat[0].k, 1);
@@ -390,6 +436,8 @@ hipError_t launch_block_mode(const BlockGemv& a, hipStream_t s) {
 }
 
 }  // namespace
+
+bool gemv_block_add_streams(const BlockGemv& a) { return a.norm_w == nullptr && knob(kBlockStream, 1) != 0; }
 
 bool gemv_block_supported(const BlockGemv& a) {
     if (a.nmat < 1 || a.nmat > 4) return false;

@@ -112,9 +112,14 @@ hipError_t launch_conv_gates(const float* qkv, const float* conv_w, float* histo
                              uint64_t kernel, const float* beta, const float* alpha, const float* dt_bias,
                              const float* decay, uint64_t heads, float* conv_out, float* beta_s, float* log_decay,
                              hipStream_t s);
+// the delta rule over Hv * dv/32 workgroups: rec_out[Hv][dv] and head_ss[Hv][dv/32], the per-chunk double
+// sums of rec_out^2 that the head's gated RMSNorm takes (launch_gated_norm, or the out projection's staging)
 hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_heads, uint64_t dk, uint64_t dv,
-                        const float* beta_s, const float* log_decay, float eps, float* state, const float* z,
-                        const float* out_norm, float* rec_out, float* gated, hipStream_t s);
+                        const float* beta_s, const float* log_decay, float eps, float* state, float* rec_out,
+                        double* head_ss, hipStream_t s);
+hipError_t launch_gated_norm(const float* rec, const double* head_ss, const float* z, const float* out_norm,
+                             uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s);
+uint64_t delta_chunks(uint64_t dv);  // head_ss entries per head
 hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s);
 hipError_t launch_add(const float* a, const float* b, uint64_t n, float* out, hipStream_t s);
 
@@ -140,8 +145,21 @@ struct BlockGemv {
     const float* add;      // ADD: sum_out = add + y
     float* sum_out;
     float* act;            // FFN: SiLU(gate) * up
+    // ADD, streamed: when rec is not null the activation is the recurrent block's gated output,
+    // formed in the staging from the delta rule's output: x = RMSNorm_head(rec) * out_norm *
+    // SiLU(z) with each head's sum of squares from head_ss[h * dchunks ...] (eps as above);
+    // workgroup 0 stores it to gated_out
+    const float* rec;
+    const double* head_ss;
+    const float* z;
+    const float* out_norm;
+    uint32_t dv, dchunks;
+    float* gated_out;
 };
 bool gemv_block_supported(const BlockGemv& a);
+// whether launch_gemv_block(kBlockAdd, a) runs the streamed kernel (the one that can form the
+// gated activation itself)
+bool gemv_block_add_streams(const BlockGemv& a);
 hipError_t launch_gemv_block(int mode, const BlockGemv& a, hipStream_t s);
 
 // ---- oq_api.cpp: the block step on a caller-provided workspace (validation, capacity check, launches)
