@@ -122,23 +122,25 @@ __global__ __launch_bounds__(256) void conv_gates_kernel(const float* __restrict
 // Outputs: rec_out[h][v] and, per (head, chunk), the double sum of the chunk's rec_out^2 in
 // head_ss[h * chunks + chunk] -- the head's gated RMSNorm (qwen35_block.cpp:579-588) is applied
 // where rec_out is consumed (gated_norm_kernel, or the out projection's activation staging).
+// value columns per workgroup of the delta rule and per head_ss entry (16 measured slower:
+// more workgroups, each with a shorter chain, 49.9 against 48.6 us per block)
 constexpr int kDeltaCols = 32;
-constexpr int kDeltaSlices = 8;
 
-template <int DK>
+template <int DK, int COLS>
 __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ conv, uint32_t key_heads, uint32_t dv,
                                                     const float* __restrict__ beta_s, const float* __restrict__ log_decay,
                                                     float eps, float* __restrict__ state, float* __restrict__ rec_out,
                                                     double* __restrict__ head_ss) {
-    constexpr int KS = DK / kDeltaSlices;  // keys per thread
+    constexpr int SLICES = 256 / COLS;
+    constexpr int KS = DK / SLICES;  // keys per thread
     __shared__ __align__(16) float nq[DK];
     __shared__ __align__(16) float nk[DK];
-    __shared__ float mem_part[kDeltaSlices][kDeltaCols];
-    __shared__ double out_part[kDeltaSlices][kDeltaCols];
-    const uint32_t chunks = dv / kDeltaCols;
+    __shared__ float mem_part[SLICES][COLS];
+    __shared__ double out_part[SLICES][COLS];
+    const uint32_t chunks = dv / COLS;
     const uint32_t h = blockIdx.x / chunks, chunk = blockIdx.x % chunks;
-    const uint32_t col = threadIdx.x % kDeltaCols, slice = threadIdx.x / kDeltaCols;
-    const uint32_t v = chunk * kDeltaCols + col;
+    const uint32_t col = threadIdx.x % COLS, slice = threadIdx.x / COLS;
+    const uint32_t v = chunk * COLS + col;
     const uint32_t d0 = slice * KS;
     float* scol = state + ((uint64_t)h * DK + d0) * dv + v;
     const uint32_t kw = key_heads * DK;
@@ -184,7 +186,7 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
     __syncthreads();
     float memory = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kDeltaSlices; ++j) memory = memory + mem_part[j][col];
+    for (int j = 0; j < SLICES; ++j) memory = memory + mem_part[j][col];
     const float delta = (vv - memory) * beta;
     double o = 0.0;
 #pragma unroll
@@ -198,13 +200,13 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
     if (slice == 0) {
         double out = 0.0;
 #pragma unroll
-        for (int j = 0; j < kDeltaSlices; ++j) out = out + out_part[j][col];
+        for (int j = 0; j < SLICES; ++j) out = out + out_part[j][col];
         const float of = (float)out;
         rec_out[(uint64_t)h * dv + v] = of;
-        // the chunk's sum of squares, over the 32 lanes of this half wave (lanes 0..31 of wave 0)
+        // the chunk's sum of squares over its COLS columns (the first COLS lanes of wave 0)
         double sq = (double)of * (double)of;
 #pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) sq += __shfl_xor(sq, off, 64);
+        for (int off = COLS / 2; off >= 1; off >>= 1) sq += __shfl_xor(sq, off, 64);
         if (col == 0) head_ss[(uint64_t)h * chunks + chunk] = sq;
     }
 }
@@ -213,11 +215,11 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
 // head's sum of squares taken from the delta kernel's per-chunk partials (added in chunk order).
 __global__ __launch_bounds__(256) void gated_norm_kernel(const float* __restrict__ rec, const double* __restrict__ head_ss,
                                                          const float* __restrict__ z, const float* __restrict__ out_norm,
-                                                         uint32_t heads, uint32_t dv, float eps,
+                                                         uint32_t heads, uint32_t dv, uint32_t chunks, float eps,
                                                          float* __restrict__ gated) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i >= heads * dv) return;
-    const uint32_t h = i / dv, v = i % dv, chunks = dv / kDeltaCols;
+    const uint32_t h = i / dv, v = i % dv;
     double ss = 0.0;
     for (uint32_t c = 0; c < chunks; ++c) ss += head_ss[(uint64_t)h * chunks + c];
     const float inv = (float)(1.0 / sqrt(ss / (double)dv + (double)eps));
@@ -269,19 +271,19 @@ hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_he
                         const float* beta_s, const float* log_decay, float eps, float* state, float* rec_out,
                         double* head_ss, hipStream_t s) {
     if (dv % kDeltaCols != 0) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(value_heads * (dv / kDeltaCols))), block(kDeltaCols * kDeltaSlices);
+    const dim3 grid((unsigned)(value_heads * (dv / kDeltaCols))), block(256);
     switch (dk) {
         case 32:
-            hipLaunchKernelGGL(delta_kernel<32>, grid, block, 0, s, conv, (uint32_t)key_heads, (uint32_t)dv, beta_s,
-                               log_decay, eps, state, rec_out, head_ss);
+            hipLaunchKernelGGL((delta_kernel<32, kDeltaCols>), grid, block, 0, s, conv, (uint32_t)key_heads,
+                               (uint32_t)dv, beta_s, log_decay, eps, state, rec_out, head_ss);
             break;
         case 64:
-            hipLaunchKernelGGL(delta_kernel<64>, grid, block, 0, s, conv, (uint32_t)key_heads, (uint32_t)dv, beta_s,
-                               log_decay, eps, state, rec_out, head_ss);
+            hipLaunchKernelGGL((delta_kernel<64, kDeltaCols>), grid, block, 0, s, conv, (uint32_t)key_heads,
+                               (uint32_t)dv, beta_s, log_decay, eps, state, rec_out, head_ss);
             break;
         case 128:
-            hipLaunchKernelGGL(delta_kernel<128>, grid, block, 0, s, conv, (uint32_t)key_heads, (uint32_t)dv, beta_s,
-                               log_decay, eps, state, rec_out, head_ss);
+            hipLaunchKernelGGL((delta_kernel<128, kDeltaCols>), grid, block, 0, s, conv, (uint32_t)key_heads,
+                               (uint32_t)dv, beta_s, log_decay, eps, state, rec_out, head_ss);
             break;
         default:
             return hipErrorInvalidValue;
@@ -292,7 +294,7 @@ hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_he
 hipError_t launch_gated_norm(const float* rec, const double* head_ss, const float* z, const float* out_norm,
                              uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s) {
     hipLaunchKernelGGL(gated_norm_kernel, dim3(blocks_of(heads * dv, 256)), dim3(256), 0, s, rec, head_ss, z, out_norm,
-                       (uint32_t)heads, (uint32_t)dv, eps, gated);
+                       (uint32_t)heads, (uint32_t)dv, (uint32_t)delta_chunks(dv), eps, gated);
     return hipGetLastError();
 }
 
