@@ -2,9 +2,10 @@
 
 Default workload: Q4_K FFN gate/up decode GEMV, 12288 rows x 4096 columns, batch 1; F32
 activation ~N(0,1) quantized to Q8_K on the device inside the same kernel.  One step = one
-matvec (F32 x in HBM -> F32 y in HBM).  K steps are captured into one HIP graph and replayed
-between two HIP events on the library's stream; steps cycle over >= 512 MiB of distinct weight
-copies so the 256 MiB Infinity Cache cannot serve them.  `value` = weight bytes / step time.
+matvec (F32 x in HBM -> F32 y in HBM).  K steps are launched back to back between two HIP events
+on the library's stream, right behind the W warmup steps (timed_steps); steps cycle over
+>= 512 MiB of distinct weight copies so the 256 MiB Infinity Cache cannot serve them.  `value` =
+weight bytes / step time.
 
 Also reported: the M=512 Q4_K prefill GEMM (4096 x 12288) in TOPS when the matrix-core path is
 available, the roofline of the dominant kernel, and the reference CPU algorithm (the oracle's
@@ -15,6 +16,7 @@ restatement, single thread) timed on a bounded sample on this host.
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import math
 import os
@@ -50,6 +52,26 @@ def weight_bytes(t, n, k):
     return synth.row_bytes(t, k) * n
 
 
+def timed_steps(ctx, step, steps, warmup):
+    """W warmup steps, then exactly K timed steps; returns the K steps' milliseconds.
+
+    Steps are launched eagerly through the C ABI (about 3 us of host time per launch, less than
+    a step, so the GPU never waits for the host).  After a host synchronization the W warmup
+    steps are launched and, right behind them on the same stream, the HIP event pair around the
+    K timed steps: the events measure the K steps back to back.  A host synchronization closes
+    the timed region.  (HIP graphs were measured too: a graph's first launch adds ~15-20 us of
+    host set-up that the GPU waits for, 0.7-1 us per step at K = 20.)"""
+    ctx.sync()
+    for i in range(warmup):
+        step(i)
+    ctx.timer_start()
+    for i in range(steps):
+        step(i)
+    ms = ctx.timer_stop()
+    ctx.sync()
+    return ms
+
+
 def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
     t, n, k, m, desc = WORKLOADS[name]
     rng = np.random.default_rng(SEED + list(WORKLOADS).index(name))
@@ -63,29 +85,20 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
     xb = ctx.to_device(x)
     yb = ctx.alloc(m * n * 4)
 
-    def step(i):
-        if m == 1:
-            ctx.matvec(ws[i % ncopies], xb, yb)
-        else:
-            ctx.matmul(ws[i % ncopies], m, xb, yb)
+    lib, h, xp, yp, whs = ctx.lib, ctx.h, xb.ptr, yb.ptr, [w.h for w in ws]
 
-    step(0)  # sizes any staging buffer before capture
+    def step(i):
+        # direct C-ABI calls: the least host time per launch
+        rc = lib.oq_matvec(h, whs[i % ncopies], xp, yp) if m == 1 else lib.oq_matmul(h, whs[i % ncopies], m, xp, yp)
+        if rc != 0:
+            raise RuntimeError(f"step {i}: {lib.oq_last_error(h).decode()}")
+
+    if m == 1:
+        ctx.matvec(ws[0], xb, yb)  # checked call; sizes any staging buffer
+    else:
+        ctx.matmul(ws[0], m, xb, yb)
     ctx.sync()
-    ctx.capture_begin()
-    for i in range(warmup):
-        step(i)
-    g_warm = ctx.capture_end()
-    ctx.capture_begin()
-    for i in range(steps):
-        step(i)
-    g = ctx.capture_end()
-    g_warm.launch()
-    ctx.sync()
-    ctx.timer_start()
-    g.launch()
-    ms = ctx.timer_stop()
-    g.destroy()
-    g_warm.destroy()
+    ms = timed_steps(ctx, step, steps, warmup)
     ms_step = ms / steps
     xbytes = m * k * 4
     ybytes = m * n * 4
@@ -102,16 +115,11 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
         tb, vb = ctx.alloc(4), ctx.alloc(4)
         ctx.argmax(yb, n, tb, vb)
         ctx.sync()
-        ctx.capture_begin()
-        for _ in range(steps):
-            ctx.argmax(yb, n, tb, vb)
-        ga = ctx.capture_end()
-        ga.launch()
-        ctx.sync()
-        ctx.timer_start()
-        ga.launch()
-        res["greedy_token_us"] = ctx.timer_stop() * 1e3 / steps
-        ga.destroy()
+        def argmax_step(i):
+            if ctx.lib.oq_argmax(ctx.h, yb.ptr, n, tb.ptr, vb.ptr) != 0:
+                raise RuntimeError("argmax failed")
+
+        res["greedy_token_us"] = timed_steps(ctx, argmax_step, steps, warmup) * 1e3 / steps
         tb.free()
         vb.free()
     for w in ws:
@@ -134,26 +142,17 @@ def run_deltanet(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
     hb, sb, xb = ctx.to_device(hist), ctx.to_device(st), ctx.to_device(x)
     yb = ctx.alloc(d["embedding"] * 4)
 
-    def step(i):
-        ctx.deltanet_step(blocks[i % ncopies], hb, sb, xb, yb)
+    lib, h = ctx.lib, ctx.h
+    descs = [C.byref(b.desc) for b in blocks]
+    hp, sp, xp, yp = hb.ptr, sb.ptr, xb.ptr, yb.ptr
 
-    step(0)  # sizes the block workspace before capture
+    def step(i):
+        if lib.oq_deltanet_step(h, descs[i % ncopies], hp, sp, xp, yp, None) != 0:
+            raise RuntimeError(f"step {i}: {lib.oq_last_error(h).decode()}")
+
+    ctx.deltanet_step(blocks[0], hb, sb, xb, yb)  # checked call; sizes the block workspace
     ctx.sync()
-    ctx.capture_begin()
-    for i in range(warmup):
-        step(i)
-    g_warm = ctx.capture_end()
-    ctx.capture_begin()
-    for i in range(steps):
-        step(i)
-    g = ctx.capture_end()
-    g_warm.launch()
-    ctx.sync()
-    ctx.timer_start()
-    g.launch()
-    ms = ctx.timer_stop()
-    g.destroy()
-    g_warm.destroy()
+    ms = timed_steps(ctx, step, steps, warmup)
     for b in blocks:
         b.release()
     for buf in (hb, sb, xb, yb):
@@ -189,9 +188,24 @@ def committed_traffic(name):
     return json.loads(p.read_text())["traffic_bytes"]
 
 
-def cpu_baseline(name, budget_s=12.0):
-    """The reference's CPU algorithm (oracle restatement: decode block, sequential F32 dot) on
-    the same workload, single thread, repeated until ~budget_s seconds; plus all host cores."""
+def _timed(fn, budget_s, max_reps):
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= max_reps:
+            return reps, el
+
+
+def cpu_baseline(name, budget_s=10.0):
+    """The reference CPU algorithm on the workload, timed on this host (a baseline, not the target).
+
+    value: the oracle's restatement of reference_storage_matvec (decode block, sequential F32 dot,
+    -O2 -ffp-contract=off) on the workload itself, one thread ("port": the reference has no Q4_K
+    decoder).  Beside it: the same on the process's CPU share, and the reference's own code compiled
+    from its sources (oracle/_ref/libref.so: reference_storage_dot over row ranges) on the nearest
+    path it runs, Q5_K at the same shape, on one thread and on the CPU share."""
     import oracle
 
     t, n, k, m, _ = WORKLOADS[name]
@@ -203,30 +217,31 @@ def cpu_baseline(name, budget_s=12.0):
     if t == 14:  # bound the 151936-row head: time a contiguous slice
         rows = 16384
     sample = data[: rows * synth.row_bytes(t, k)]
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        oracle.storage_matvec(t, rows, k, sample, xhat, threads=1)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 1000:
-            break
+    threads = oracle.default_threads()
+    host_cpus = os.cpu_count() or 1
+    reps, el = _timed(lambda: oracle.storage_matvec(t, rows, k, sample, xhat, threads=1), budget_s, 1000)
     single = sample.nbytes * reps / el / 1e9
-    threads = min(oracle.default_threads(), 16)
-    reps2, t0 = 0, time.perf_counter()
-    while True:
-        oracle.storage_matvec(t, rows, k, sample, xhat, threads=threads)
-        reps2 += 1
-        el2 = time.perf_counter() - t0
-        if el2 >= budget_s / 3 or reps2 >= 2000:
-            break
+    reps2, el2 = _timed(lambda: oracle.storage_matvec(t, rows, k, sample, xhat, threads=threads), budget_s / 4, 2000)
     multi = sample.nbytes * reps2 / el2 / 1e9
-    return {
+    out = {
         "value": single, "unit": "GB/s", "cores": 1, "kind": "port",
         "sample": f"{reps} x {rows}x{k} type-{t} matvec (oracle restatement of reference_storage_matvec, "
-                  f"-O2 -ffp-contract=off), {el:.1f} s",
+                  f"-O2 -ffp-contract=off), {el:.1f} s, 1 thread",
+        "host_cpus": host_cpus,
         "us_per_matvec_1core": el / reps * 1e6 * (n / rows),
         "all_cores": {"value": multi, "cores": threads, "us_per_matvec": el2 / reps2 * 1e6 * (n / rows)},
     }
+    if oracle.ref_available():
+        q5 = synth.weights(13, np.random.default_rng(SEED + 50), rows, k)
+        r1, e1 = _timed(lambda: oracle.ref_storage_matvec_threads(13, rows, k, q5, x, 1), budget_s / 2, 1000)
+        rN, eN = _timed(lambda: oracle.ref_storage_matvec_threads(13, rows, k, q5, x, threads), budget_s / 4, 2000)
+        out["reference_q5_k"] = {
+            "kind": "reference", "unit": "GB/s",
+            "sample": f"{rows}x{k} Q5_K matvec, the reference's reference_storage_dot compiled from its sources",
+            "value_1core": q5.nbytes * r1 / e1 / 1e9, "us_per_matvec_1core": e1 / r1 * 1e6 * (n / rows),
+            "value_all_cores": q5.nbytes * rN / eN / 1e9, "cores": threads,
+            "us_per_matvec_all_cores": eN / rN * 1e6 * (n / rows)}
+    return out
 
 
 def main():

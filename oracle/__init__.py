@@ -253,6 +253,27 @@ def ref_storage_matvec(type_id: int, rows: int, cols: int, data: np.ndarray, x: 
     return y
 
 
+def ref_storage_matvec_threads(type_id: int, rows: int, cols: int, data: np.ndarray, x: np.ndarray,
+                               threads: int) -> np.ndarray:
+    """The reference's reference_storage_dot over row ranges on `threads` host threads (ctypes
+    releases the GIL for the call), for timing its CPU path on several cores."""
+    from concurrent.futures import ThreadPoolExecutor
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(rows, dtype=np.float32)
+    rb = d.nbytes // rows
+    bounds = [rows * i // threads for i in range(threads + 1)]
+
+    def run(i):
+        return ref().ref_storage_matvec_rows(type_id, cols, _ptr(d), rb, bounds[i], bounds[i + 1], _ptr(xv), _ptr(y))
+
+    with ThreadPoolExecutor(max_workers=threads) as pool:
+        codes = list(pool.map(run, range(threads)))
+    for c in codes:
+        _chk(c, ref(), "ref_last_error")
+    return y
+
+
 def ref_conv_step(history: np.ndarray, weights: np.ndarray, x: np.ndarray, apply_silu: bool = False) -> np.ndarray:
     """One step of the reference's causal depthwise convolution; updates `history` in place."""
     ch, kern = history.shape
@@ -279,6 +300,11 @@ def ref_status(fn: str, *args) -> int:
 
 
 def default_threads() -> int:
+    """Host threads for the oracle's parallel loops: the process's CPU share -- OMP_NUM_THREADS
+    when the environment sets it, else the CPUs this process may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
     try:
         return max(1, len(os.sched_getaffinity(0)))
     except AttributeError:
