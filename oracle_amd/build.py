@@ -69,6 +69,18 @@ def _stale(obj: Path, src: Path) -> bool:
     return any(d.stat().st_mtime > obj.stat().st_mtime for d in deps)
 
 
+CALIBRATION = PKG / "calibration"
+
+
+def _build_calibration(force: bool) -> None:
+    """The HBM read-floor program (calibration/read_floor.hip), a standalone executable."""
+    src = CALIBRATION / "read_floor.hip"
+    exe = CALIBRATION / "read_floor"
+    if not force and exe.exists() and exe.stat().st_mtime >= src.stat().st_mtime:
+        return
+    _run([HIPCC, *DEVICE_FLAGS, "-x", "hip", str(src), "-o", str(exe)])
+
+
 def build(jobs: int = 8, force: bool = True) -> Path:
     """Compile every translation unit (force=False: only objects older than their sources or
     any header) and link liboq.so."""
@@ -85,6 +97,7 @@ def build(jobs: int = 8, force: bool = True) -> Path:
     todo.sort(key=lambda u: (u[0].name != "oq_gemv_inst.hip", u[0].name != "oq_gemv_block.hip"))
     with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(todo) or 1))) as pool:
         list(pool.map(compile_one, todo))
+    _build_calibration(force)
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
