@@ -27,7 +27,7 @@ constexpr const char* kKnobNames[kKnobCount] = {
     "OQ_GEMM_SPLITS",   "OQ_GEMM_EXACT_DEQUANT", "OQ_GEMM_WS",     "OQ_GEMV_MAX_WG",   "OQ_Q8_0_ROWS",
     "OQ_GEMV_WG_PER_CU", "OQ_STREAM_WG_PER_CU",  "OQ_GEMV_STREAM", "OQ_STREAM_WAVES",  "OQ_GEMV_STREAM_MT",
     "OQ_GEMV_ROWS",     "OQ_GEMV_WAVES",         "OQ_GEMV_ROWS_MT", "OQ_BLOCK_STREAM", "OQ_BLOCK_FUSED",
-    "OQ_GEMM_MFMA",     "OQ_FUSED_QUANT",
+    "OQ_GEMM_MFMA",     "OQ_FUSED_QUANT",        "OQ_GEMM_INT8",
 };
 
 struct KnobTable {
@@ -691,6 +691,11 @@ int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, f
         return fail(ctx, OQ_INVALID_ARGUMENT, "activation / output buffers are misaligned");
     }
     if (is_kquant(t)) {
+        if (oq::gemm_i8_supported(w->m, (int)m) && knob_flag(oq::kGemmInt8, false)) {
+            if (int rc = ensure_scratch(ctx, oq::gemm_i8_scratch_bytes(w->m, (int)m))) return rc;
+            return launch_rc(ctx, oq::launch_gemm_q4k_i8(w->m, (int)m, x, nullptr, y, ctx->scratch.ptr, ctx->stream),
+                             "matmul");
+        }
         if (oq::gemm_mfma_supported(w->m, (int)m) && knob_flag(oq::kGemmMfma, true)) {
             if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
             return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, x, nullptr, y, ctx->scratch.ptr, ctx->stream),
@@ -726,6 +731,11 @@ int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q
     if (!q8k || !y) return fail(ctx, OQ_INVALID_ARGUMENT, "null buffer");
     if (!aligned(q8k, 4) || !aligned(y, 4)) return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer");
     const uint8_t* q8 = static_cast<const uint8_t*>(q8k);
+    if (oq::gemm_i8_supported(w->m, (int)m) && knob_flag(oq::kGemmInt8, false)) {
+        if (int rc = ensure_scratch(ctx, oq::gemm_i8_scratch_bytes(w->m, (int)m))) return rc;
+        return launch_rc(ctx, oq::launch_gemm_q4k_i8(w->m, (int)m, nullptr, q8, y, ctx->scratch.ptr, ctx->stream),
+                         "matmul_q8k");
+    }
     if (oq::gemm_mfma_supported(w->m, (int)m) && knob_flag(oq::kGemmMfma, true)) {
         if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
         return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, nullptr, q8, y, ctx->scratch.ptr, ctx->stream),

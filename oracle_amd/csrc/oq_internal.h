@@ -54,6 +54,7 @@ enum Knob : int {
     kBlockFused,  // OQ_BLOCK_FUSED
     kGemmMfma,  // OQ_GEMM_MFMA
     kFusedQuant,  // OQ_FUSED_QUANT
+    kGemmInt8,  // OQ_GEMM_INT8
     kKnobCount
 };
 int knob(Knob k, int fallback);  // the option's value, or fallback when it is unset
@@ -103,6 +104,13 @@ bool gemm_mfma_supported(const DeviceMatrix& w, int m);
 uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m);  // planar Q8_K image + split partials
 hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
                                 void* scratch, hipStream_t s);
+
+// ---- oq_gemm_i8.hip  (m >= 16, q4_K: int8 matrix cores on Q8_K x nibbles, per-sub-block integer
+// rescale; the alternative to the f16 kernel, selected with OQ_GEMM_INT8=1)
+bool gemm_i8_supported(const DeviceMatrix& w, int m);
+uint64_t gemm_i8_scratch_bytes(const DeviceMatrix& w, int m);  // int8 image, scales, f16 partial sums
+hipError_t launch_gemm_q4k_i8(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
+                              void* scratch, hipStream_t s);
 
 // ---- oq_deltanet.hip  (Gated DeltaNet decode block: kernels between the projections)
 bool deltanet_dims_supported(uint64_t key_dim, uint64_t value_dim, uint64_t conv_kernel);

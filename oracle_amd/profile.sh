@@ -7,7 +7,8 @@
 #   OUT/<workload>_counters.json      with a fourth argument "mfma": MFMA and LDS counters of
 #                                     KERNEL (two counter passes) and the MFMA-busy fraction
 #
-#   bash oracle_amd/profile.sh WORKLOAD KERNEL_SUBSTRING [OUT] [mfma]  (OUT defaults to prof_out)
+#   bash oracle_amd/profile.sh WORKLOAD KERNEL_SUBSTRING [OUT] [mfma] [TAG]  (OUT defaults to prof_out;
+#   TAG is appended to the output names, e.g. _int8 for a run with OQ_GEMM_INT8=1 exported)
 #
 # Every rocprofv3 run has a time limit of its own; counters are collected one per run, with no
 # trace domain beside them.
@@ -15,11 +16,12 @@ set -euo pipefail
 WL=$1
 KERN=$2
 OUT=${3:-prof_out}
+TAG=${5:-}
 ROOT=$(cd "$(dirname "$0")/.." && pwd)
 cd /tmp && export TMPDIR=/tmp
 cd "$ROOT"
 mkdir -p "$OUT"
-RAW="$OUT/raw_$WL"
+RAW="$OUT/raw_$WL$TAG"
 COPY_BYTES=28311552
 SECONDARY=""
 [ "$WL" = "q4k_gemv" ] && SECONDARY="--no-secondary"
@@ -36,19 +38,20 @@ for C in FETCH_SIZE WRITE_SIZE; do
 done
 
 {
-    echo "# rocprofv3 kernel statistics, workload $WL"
-    echo "# recipe: bash oracle_amd/profile.sh $WL '$KERN' <out>"
+    echo "# rocprofv3 kernel statistics, workload $WL$TAG"
+    [ -n "$TAG" ] && echo "# launch options: $(env | grep '^OQ_' | tr '\n' ' ')"
+    echo "# recipe: bash oracle_amd/profile.sh $WL '$KERN' <out> ${4:-} $TAG"
     echo "# command: (cd \$REPO && ${TRACE_CMD//$OUT/<out>})   (<out>: the OUT argument)"
     echo "# bench line of that run:"
     grep '^{' "$RAW.trace.log" | tail -1 | sed 's/^/#   /'
     python3 -m oracle_amd.profsum stats "$RAW/trace"
-} > "$OUT/${WL}_kernel_stats.txt"
+} > "$OUT/${WL}${TAG}_kernel_stats.txt"
 python3 -m oracle_amd.profsum traffic --kernel "$KERN" --fetch "$RAW/FETCH_SIZE" --write "$RAW/WRITE_SIZE" \
     --copy-fetch "$RAW/copy_FETCH_SIZE" --copy-write "$RAW/copy_WRITE_SIZE" --copy-bytes $COPY_BYTES \
-    > "$OUT/${WL}_traffic.json"
-echo "wrote $OUT/${WL}_kernel_stats.txt $OUT/${WL}_traffic.json"
+    > "$OUT/${WL}${TAG}_traffic.json"
+echo "wrote $OUT/${WL}${TAG}_kernel_stats.txt $OUT/${WL}${TAG}_traffic.json"
 if [ "${4:-}" = "mfma" ]; then
-    P1="SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 GRBM_GUI_ACTIVE SQ_INSTS_MFMA SQ_INSTS_VALU SQ_WAVE_CYCLES SQ_INSTS_LDS"
+    P1="SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_I8 GRBM_GUI_ACTIVE SQ_INSTS_MFMA SQ_INSTS_VALU SQ_WAVE_CYCLES"
     P2="SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_LDS SQ_WAIT_INST_LDS SQ_LDS_DATA_FIFO_FULL SQ_LDS_CMD_FIFO_FULL SQ_WAIT_ANY SQ_ACTIVE_INST_VALU SQ_VALU_MFMA_COEXEC_CYCLES"
     for PASS in 1 2; do
         if [ $PASS = 1 ]; then C=$P1; else C=$P2; fi
@@ -56,6 +59,6 @@ if [ "${4:-}" = "mfma" ]; then
         timeout -s KILL 90 rocprofv3 --pmc $C --output-format csv -d "$RAW/mfma$PASS" -o run -- \
             python3 bench.py --workload "$WL" --steps 10 --warmup 2 --no-cpu $SECONDARY > "$RAW.mfma$PASS.log" 2>&1
     done
-    python3 -m oracle_amd.profsum counters --kernel "$KERN" "$RAW/mfma1" "$RAW/mfma2" > "$OUT/${WL}_counters.json"
-    echo "wrote $OUT/${WL}_counters.json"
+    python3 -m oracle_amd.profsum counters --kernel "$KERN" "$RAW/mfma1" "$RAW/mfma2" > "$OUT/${WL}${TAG}_counters.json"
+    echo "wrote $OUT/${WL}${TAG}_counters.json"
 fi

@@ -91,6 +91,11 @@ def counters(kernel: str, dirs: list[str], cus: int, simds_per_cu: int, xcds: in
         if "SQ_INSTS_VALU_MFMA_MOPS_F16" in med:
             # one MOPS unit = 512 flop; rate at the cycles of the dispatch (clock not assumed)
             out["mfma_f16_flop_per_cycle_per_cu"] = med["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512.0 / (cycles * cus)
+        if "SQ_INSTS_VALU_MFMA_MOPS_I8" in med:
+            out["mfma_i8_op_per_cycle_per_cu"] = med["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512.0 / (cycles * cus)
+    if med.get("SQ_INSTS_MFMA"):
+        # vector (non-MFMA) instructions issued per MFMA instruction
+        out["valu_per_mfma"] = (med.get("SQ_INSTS_VALU", 0.0) - med["SQ_INSTS_MFMA"]) / med["SQ_INSTS_MFMA"]
     return out
 
 

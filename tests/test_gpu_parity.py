@@ -589,3 +589,42 @@ def test_long_rows_matrix_cores(ctx):
     y_ref, norm = reference_products(12, rows, cols, data, x)
     check_close(y, y_ref, norm)
     w.release()
+
+
+@pytest.mark.parametrize("m,rows,cols", [(16, 256, 4096), (37, 300, 4096), (64, 130, 12288), (200, 128, 8192),
+                                         (19, 70, 17408)])
+def test_matmul_int8_matrix_cores(ctx, m, rows, cols):
+    """The int8 MFMA alternative (OQ_GEMM_INT8=1): Q8_K x nibble sub-block products rescaled in
+    int32, min correction on f16 matrix cores; F32 and Q8_K activations give the same bits."""
+    rng = np.random.default_rng(8100 + m + rows + cols)
+    data = synth.q4_k(rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(12, cols, rows, data)
+    with oracle_amd.launch_options({"OQ_GEMM_INT8": "1"}):
+        y = gpu_matmul(ctx, w, x, rows)
+        xb, qb, yb = ctx.to_device(x), ctx.alloc(m * (cols // 256) * 292), ctx.alloc(m * rows * 4)
+        ctx.quantize_q8k(xb, m, cols, qb)
+        ctx.matmul_q8k(w, m, qb, yb)
+        y_q8k = yb.download(np.float32, m * rows).reshape(m, rows)
+        for b in (xb, qb, yb):
+            b.free()
+    assert np.array_equal(y.view(np.uint32), y_q8k.view(np.uint32))
+    y_ref, norm = reference_products(12, rows, cols, data, x)
+    worst = check_close(y, y_ref, norm)
+    # the products are exact integers scaled in F32: far inside the bar
+    assert worst < 1e-5, worst
+    w.release()
+
+
+def test_matmul_int8_full_size_sampled_rows(ctx):
+    rng = np.random.default_rng(4243)
+    rows, cols, m = 4096, 12288, 512
+    data = synth.q4_k(rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(12, cols, rows, data)
+    with oracle_amd.launch_options({"OQ_GEMM_INT8": "1"}):
+        y = gpu_matmul(ctx, w, x, rows)
+    pick = np.array(sorted(set([0, 1, 127, 128, 511] + list(rng.integers(0, m, 11)))))
+    y_ref, norm = reference_products(12, rows, cols, data, x[pick])
+    check_close(y[pick], y_ref, norm)
+    w.release()
