@@ -34,7 +34,8 @@ typedef enum oq_status {
     OQ_UNSUPPORTED_TYPE = -4, /* reference: std::runtime_error("unsupported GGML tensor type") */
     OQ_DEVICE_ERROR = -5,     /* HIP runtime failure */
     OQ_OUT_OF_MEMORY = -6,    /* device allocation failure */
-    OQ_LOGIC_ERROR = -7       /* reference: std::logic_error (bad row geometry) */
+    OQ_LOGIC_ERROR = -7,      /* reference: std::logic_error (bad row geometry) */
+    OQ_RUNTIME_ERROR = -8     /* reference: std::runtime_error (malformed model payload) */
 } oq_status;
 
 /* GGML type ids, as registered in the reference (src/model/ggml_type.cpp:12-54) */
@@ -109,6 +110,54 @@ int oq_weight_upload_device(oq_context* ctx, uint32_t type, uint64_t ne0, uint64
 void oq_weight_release(oq_weight* w);
 int oq_weight_info(const oq_weight* w, uint32_t* type, uint64_t* ne0, uint64_t* ne1,
                    uint64_t* device_bytes);
+
+/* ------------------------------------------------------------------ whole-model upload */
+
+/* One tensor of a GGUF payload: GgufTensorInfo (include/oracle/model/gguf.hpp:77-82) with its
+   byte offset in the payload passed to oq_model_upload (GgufTensorView::absolute_offset when the
+   payload is the whole mapped file, MappedGgufModel::mapping()). */
+typedef struct oq_tensor_desc {
+    const char* name;
+    uint32_t type;     /* GGML type id */
+    uint32_t n_dims;   /* 1..4 */
+    uint64_t dims[4];  /* dims[0] contiguous (GGUF dimensions) */
+    uint64_t offset;   /* byte offset in the payload */
+} oq_tensor_desc;
+
+typedef struct oq_model oq_model;
+
+/* Checks a tensor table against a payload of payload_bytes the way the reference's GGUF reader
+   and MappedGgufModel do (src/model/gguf.cpp:457-497, src/model/mapped_gguf.cpp:124-203), in
+   their order: unique names, dimension count and non-zero dimensions, offsets inside the payload
+   (OQ_RUNTIME_ERROR); then per tensor its registered type (OQ_UNSUPPORTED_TYPE), byte size
+   (ggml_tensor_byte_size, src/model/ggml_type.cpp:96-118: ragged rows, overflow) and payload
+   end (OQ_RUNTIME_ERROR); then overlapping payloads (OQ_RUNTIME_ERROR).  Tensors of more than
+   four dimensions are refused (OQ_INVALID_ARGUMENT).  Host only, needs no device. */
+int oq_model_validate(uint64_t payload_bytes, const oq_tensor_desc* tensors, uint64_t count);
+
+/* Replaces the per-call use of mapped tensor views with one upload of the whole model: validates
+   as oq_model_validate, then copies the payload to HBM once (in payload order, through a staging
+   buffer of max(256 MiB, largest tensor)).  Rank-2 tensors of a type oq_type_supported accepts
+   become weights (as oq_weight_upload: device row layout, ready for oq_matvec / oq_matmul);
+   every other tensor keeps its GGML bytes in HBM.  The host payload may be released afterwards. */
+int oq_model_upload(oq_context* ctx, const void* payload, uint64_t payload_bytes, const oq_tensor_desc* tensors,
+                    uint64_t count, oq_model** out);
+void oq_model_release(oq_model* m);
+uint64_t oq_model_tensor_count(const oq_model* m);
+/* MappedGgufModel::find_tensor / tensor (src/model/mapped_gguf.cpp:211-222): index of the tensor
+   called `name`; OQ_OUT_OF_RANGE ("GGUF tensor not found") if there is none. */
+int oq_model_find(const oq_model* m, const char* name, uint64_t* index);
+typedef struct oq_model_tensor_info {
+    const char* name;        /* valid while the model lives */
+    uint32_t type, n_dims;
+    uint64_t dims[4];
+    uint64_t nbytes;          /* GGML bytes */
+    const oq_weight* weight;  /* the uploaded weight, or NULL */
+    const void* data_dev;     /* the GGML bytes in HBM when weight is NULL, else NULL */
+} oq_model_tensor_info;
+int oq_model_tensor(const oq_model* m, uint64_t index, oq_model_tensor_info* info);
+/* HBM held by the model (weights in device layout plus raw tensors). */
+uint64_t oq_model_device_bytes(const oq_model* m);
 
 /* ------------------------------------------------------------------ decode */
 

@@ -67,6 +67,9 @@ _REF_SIGS = [
     ("ref_gated_delta_step", C.c_int, [_U64, _U64, _U64, _P, _P, _P, _P, _P, C.c_float, _P, _P]),
     ("ref_recurrent_block", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     ("ref_block_trace_value", C.c_int64, [C.c_char_p, _P, _U64]),
+    ("ref_gguf_open", C.c_int, [C.c_char_p, C.POINTER(_U64)]),
+    ("ref_gguf_tensor", C.c_int, [_U64, C.c_char_p, C.c_int, C.POINTER(_U32), C.POINTER(_U32), C.POINTER(_U64),
+                                  C.POINTER(_U64), C.POINTER(_U64)]),
 ]
 
 
@@ -483,4 +486,21 @@ def ref_block_trace_value(name: str) -> np.ndarray:
         raise KeyError(name)
     out = np.empty(n, dtype=np.float32)
     ref().ref_block_trace_value(name.encode(), _ptr(out), n)
+    return out
+
+
+def ref_gguf_tensors(path) -> list[dict]:
+    """The tensor table the reference's MappedGgufModel builds for a GGUF file (raises OracleError
+    with the reference's message when it rejects the file)."""
+    n = C.c_uint64()
+    _chk(ref().ref_gguf_open(str(path).encode(), C.byref(n)), ref(), "ref_last_error")
+    out = []
+    for i in range(n.value):
+        name = C.create_string_buffer(512)
+        t, nd, off, nb = C.c_uint32(), C.c_uint32(), C.c_uint64(), C.c_uint64()
+        dims = (C.c_uint64 * 4)()
+        _chk(ref().ref_gguf_tensor(i, name, 512, C.byref(t), C.byref(nd), dims, C.byref(off), C.byref(nb)), ref(),
+             "ref_last_error")
+        out.append({"name": name.value.decode(), "type": t.value, "dims": list(dims[:nd.value]),
+                    "absolute_offset": off.value, "nbytes": nb.value})
     return out

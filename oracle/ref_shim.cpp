@@ -340,3 +340,41 @@ std::int64_t ref_block_trace_value(const char* name, float* out, std::uint64_t c
     return -1;
 }
 }  // extern "C"
+
+// ---------------------------------------------------------------- the reference's GGUF mapping
+//
+// MappedGgufModel (src/model/mapped_gguf.cpp:124-203) over a file: ref_gguf_open maps it (or
+// returns the reference's error), ref_gguf_tensor reads entry `index` of its tensor table.
+#include <memory>
+
+namespace {
+std::unique_ptr<oracle::model::MappedGgufModel> g_model;
+}
+
+extern "C" {
+
+int ref_gguf_open(const char* path, std::uint64_t* count) {
+    return guarded([&] {
+        g_model.reset();
+        g_model = std::make_unique<oracle::model::MappedGgufModel>(path);
+        *count = g_model->tensors().size();
+    });
+}
+
+int ref_gguf_tensor(std::uint64_t index, char* name, int name_cap, std::uint32_t* type, std::uint32_t* n_dims,
+                    std::uint64_t* dims, std::uint64_t* absolute_offset, std::uint64_t* nbytes) {
+    return guarded([&] {
+        if (!g_model || index >= g_model->tensors().size()) throw std::out_of_range("tensor index");
+        const auto& t = g_model->tensors()[static_cast<std::size_t>(index)];
+        std::snprintf(name, static_cast<std::size_t>(name_cap), "%.*s", static_cast<int>(t.name().size()),
+                      t.name().data());
+        *type = t.layout().type;
+        const auto d = t.dimensions();
+        *n_dims = static_cast<std::uint32_t>(d.size());
+        for (std::size_t i = 0; i < d.size() && i < 4; ++i) dims[i] = d[i];
+        *absolute_offset = t.absolute_offset();
+        *nbytes = t.bytes().size();
+    });
+}
+
+}  // extern "C"

@@ -166,9 +166,10 @@ class DeviceBuffer:
 class Weight:
     """A GGML tensor uploaded once to HBM (oq_weight)."""
 
-    def __init__(self, ctx: "Context", handle: int, type_id: int, ne0: int, ne1: int):
+    def __init__(self, ctx: "Context", handle: int, type_id: int, ne0: int, ne1: int, owned_by_model: bool = False):
         self.ctx, self.h = ctx, handle
         self.type, self.ne0, self.ne1 = type_id, ne0, ne1
+        self.owned_by_model = owned_by_model  # released with its Model, not by release()
 
     @property
     def device_bytes(self) -> int:
@@ -177,9 +178,9 @@ class Weight:
         return db.value
 
     def release(self) -> None:
-        if self.h:
+        if self.h and not self.owned_by_model:
             self.ctx.lib.oq_weight_release(self.h)
-            self.h = None
+        self.h = None
 
 
 class Graph:
@@ -391,3 +392,81 @@ class DeltaNetBlockWeights:
             w.release()
         for v in self.vectors.values():
             v.free()
+
+
+# ---------------------------------------------------------------- whole-model upload
+
+@dataclass(frozen=True)
+class ModelTensor:
+    name: str
+    type: int
+    dims: tuple
+    nbytes: int
+    weight: "Weight | None"
+    data_dev: int | None
+
+
+def model_tensor_descs(tensors) -> tuple:
+    """oq_tensor_desc array for (name, dims, GGML type, payload offset) entries; returns the array
+    and the encoded names (which must outlive the call)."""
+    from ._lib import TensorDesc
+    arr = (TensorDesc * len(tensors))()
+    names = []
+    for d, (name, dims, t, off) in zip(arr, tensors):
+        nb = name.encode()
+        names.append(nb)
+        d.name = nb
+        d.type = t
+        d.n_dims = len(dims)
+        for i, v in enumerate(dims):
+            d.dims[i] = v
+        d.offset = off
+    return arr, names
+
+
+def model_validate(payload_bytes: int, tensors) -> None:
+    """oq_model_validate: the reference's MappedGgufModel checks on a tensor table (no device)."""
+    lib = _lib.load()
+    arr, _names = model_tensor_descs(tensors)
+    _check(lib.oq_model_validate(payload_bytes, arr, len(tensors)))
+
+
+class Model:
+    """A whole GGUF payload uploaded once (oq_model_upload), tensors looked up by name."""
+
+    def __init__(self, ctx: "Context", payload: np.ndarray, tensors):
+        lib = _lib.load()
+        payload = np.ascontiguousarray(payload, dtype=np.uint8)
+        arr, _names = model_tensor_descs(tensors)
+        h = C.c_void_p()
+        _check(lib.oq_model_upload(ctx.h, payload.ctypes.data, payload.nbytes, arr, len(tensors), C.byref(h)), ctx.h)
+        self.ctx, self.lib, self.h = ctx, lib, h
+
+    @classmethod
+    def from_gguf(cls, ctx: "Context", gguf_file) -> "Model":
+        """Upload every tensor of a GGUF file read by oracle_amd.gguf.read (payload = the mmap'd file)."""
+        tensors = [(t.name, t.dims, t.type, t.absolute_offset) for t in gguf_file.tensors]
+        return cls(ctx, gguf_file.payload(), tensors)
+
+    def __len__(self) -> int:
+        return int(self.lib.oq_model_tensor_count(self.h))
+
+    def device_bytes(self) -> int:
+        return int(self.lib.oq_model_device_bytes(self.h))
+
+    def tensor(self, name: str) -> ModelTensor:
+        from ._lib import ModelTensorInfo
+        idx = C.c_uint64()
+        _check(self.lib.oq_model_find(self.h, name.encode(), C.byref(idx)))
+        info = ModelTensorInfo()
+        _check(self.lib.oq_model_tensor(self.h, idx.value, C.byref(info)))
+        w = None
+        if info.weight:
+            w = Weight(self.ctx, info.weight, info.type, info.dims[0], info.dims[1], owned_by_model=True)
+        return ModelTensor(info.name.decode(), info.type, tuple(info.dims[:info.n_dims]), info.nbytes, w,
+                           info.data_dev)
+
+    def release(self) -> None:
+        if self.h:
+            self.lib.oq_model_release(self.h)
+            self.h = None

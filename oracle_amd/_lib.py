@@ -18,6 +18,7 @@ OQ_UNSUPPORTED_TYPE = -4
 OQ_DEVICE_ERROR = -5
 OQ_OUT_OF_MEMORY = -6
 OQ_LOGIC_ERROR = -7
+OQ_RUNTIME_ERROR = -8
 
 # (name, restype, argtypes) for every entry point declared in include/oq.h
 _P = C.c_void_p
@@ -42,6 +43,13 @@ SIGNATURES = [
     ("oq_weight_upload_device", C.c_int, [_P, _U32, _U64, _U64, _P, _U64, C.POINTER(_P)]),
     ("oq_weight_release", None, [_P]),
     ("oq_weight_info", C.c_int, [_P, C.POINTER(_U32), C.POINTER(_U64), C.POINTER(_U64), C.POINTER(_U64)]),
+    ("oq_model_validate", C.c_int, [_U64, _P, _U64]),
+    ("oq_model_upload", C.c_int, [_P, _P, _U64, _P, _U64, C.POINTER(_P)]),
+    ("oq_model_release", None, [_P]),
+    ("oq_model_tensor_count", _U64, [_P]),
+    ("oq_model_find", C.c_int, [_P, C.c_char_p, C.POINTER(_U64)]),
+    ("oq_model_tensor", C.c_int, [_P, _U64, _P]),
+    ("oq_model_device_bytes", _U64, [_P]),
     ("oq_dequantize_rows", C.c_int, [_P, _P, _U64, _U64, _P]),
     ("oq_quantize_q8k", C.c_int, [_P, _P, _U64, _U64, _P]),
     ("oq_argmax", C.c_int, [_P, _P, _U64, _P, _P]),
@@ -68,6 +76,18 @@ class DeltaNetBlock(C.Structure):
                                           "conv_kernel", "ffn")] + [("eps", C.c_float)] + \
                [(n, C.c_void_p) for n in ("qkv", "z", "beta", "alpha", "out", "gate", "up", "down")] + \
                [(n, C.c_void_p) for n in ("input_norm", "conv_weight", "dt_bias", "decay", "out_norm", "post_norm")]
+
+
+class TensorDesc(C.Structure):
+    """oq_tensor_desc (include/oq.h)."""
+    _fields_ = [("name", C.c_char_p), ("type", C.c_uint32), ("n_dims", C.c_uint32), ("dims", C.c_uint64 * 4),
+                ("offset", C.c_uint64)]
+
+
+class ModelTensorInfo(C.Structure):
+    """oq_model_tensor_info (include/oq.h)."""
+    _fields_ = [("name", C.c_char_p), ("type", C.c_uint32), ("n_dims", C.c_uint32), ("dims", C.c_uint64 * 4),
+                ("nbytes", C.c_uint64), ("weight", C.c_void_p), ("data_dev", C.c_void_p)]
 
 
 _lib: C.CDLL | None = None

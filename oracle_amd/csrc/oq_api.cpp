@@ -241,12 +241,16 @@ int upload_common(oq_context* ctx, uint32_t type, uint64_t ne0, uint64_t ne1, co
     } else {
         const void* src = bytes;
         void* staging = nullptr;
-        if (!from_device) {
+        // the relayout reads 16-byte pieces of q4_K / q5_K blocks: device sources off that
+        // alignment are copied to an aligned buffer first
+        if (!from_device || !aligned(bytes, 16)) {
             e = hipMalloc(&staging, nbytes);
-            if (e == hipSuccess) e = hipMemcpyAsync(staging, bytes, nbytes, hipMemcpyHostToDevice, ctx->stream);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(staging, bytes, nbytes, from_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                   ctx->stream);
             src = staging;
         }
-        if (e == hipSuccess) e = hipMemsetAsync(dst, 0, dbytes, ctx->stream);
+        if (e == hipSuccess && dbytes != nbytes) e = hipMemsetAsync(dst, 0, dbytes, ctx->stream);
         if (e == hipSuccess)
             e = oq::launch_relayout(type, ne0, ne1, static_cast<const uint8_t*>(src),
                                     static_cast<uint8_t*>(dst), pitch, ctx->stream);

@@ -28,59 +28,123 @@ uint64_t device_pitch(uint32_t type, uint64_t k) {
 // GGML rows (contiguous, row_bytes each) -> device rows at `pitch`.  Plain types keep their
 // bytes; quantized blocks are split into per-row planes, so that every plane starts 16-byte
 // aligned (210- and 34-byte blocks are not) and a wave streaming a row reads contiguous bytes.
-__global__ void relayout_kernel(uint32_t type, uint64_t k, uint64_t n, const uint8_t* __restrict__ src,
-                                uint8_t* __restrict__ dst, uint64_t row_bytes, uint64_t pitch) {
-    const uint64_t total = n * row_bytes;
-    for (uint64_t t = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; t < total;
-         t += (uint64_t)gridDim.x * blockDim.x) {
-        const uint64_t r = t / row_bytes, off = t % row_bytes;
-        uint64_t o;
-        if (type == 14) {
-            const uint64_t nsb = k / kQK, sb = off / kQ6KBytes;
-            const uint32_t b = (uint32_t)(off % kQ6KBytes);
-            if (b < 128) o = q6_ql_offset(nsb, sb, b);
-            else if (b < 192) o = 128 * nsb + sb * 64 + (b - 128);
-            else if (b < 208) o = 192 * nsb + sb * 16 + q6_sc_offset(b - 192);
-            else o = 208 * nsb + sb * 2 + (b - 208);
-        } else if (type == 8) {
-            const uint64_t nb = k / 32, blk = off / kQ80Bytes, b = off % kQ80Bytes;
-            o = b < 2 ? 32 * nb + blk * 2 + b : blk * 32 + (b - 2);
-        } else if (type == 12) {
-            const uint64_t nsb = k / kQK, sb = off / kQ4KBytes;
-            const uint32_t b = (uint32_t)(off % kQ4KBytes);
-            o = b < 16 ? 128 * nsb + sb * 16 + b : q45_qs_offset(nsb, sb, b - 16);
-        } else if (type == 13) {
-            const uint64_t nsb = k / kQK, sb = off / kQ5KBytes;
-            const uint32_t b = (uint32_t)(off % kQ5KBytes);
-            if (b < 16) o = 160 * nsb + sb * 16 + b;
-            else if (b < 48) o = 128 * nsb + sb * 32 + (b - 16);
-            else o = q45_qs_offset(nsb, sb, b - 48);
+//
+// One thread per 16-byte piece of the destination row (a header, a quant chunk, a high-bit
+// chunk, regrouped q6_K scales) or per 2-byte q6_K / q8_0 scale: the piece's source bytes are
+// contiguous in the GGML block (q6_K scales: a permutation of 16 contiguous bytes), read with
+// the widest loads their alignment allows.  Row and block indices are 32-bit.
+OQ_DEVICE uint32_t ld_u16a(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+
+// 16 source bytes at a 2-byte aligned address
+OQ_DEVICE uint4 ld16_a2(const uint8_t* p) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = ld_u16a(p + 4 * i) | (ld_u16a(p + 4 * i + 2) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <uint32_t TYPE>
+__global__ __launch_bounds__(256) void relayout_kernel(uint32_t nsb, uint32_t n, const uint8_t* __restrict__ src,
+                                                       uint8_t* __restrict__ dst, uint64_t row_bytes, uint64_t pitch) {
+    // pieces per block: q4_K 9 (header, 8 quant chunks); q5_K 11 (header, 2 fifth-bit chunks, 8
+    // quant chunks); q6_K 14 (8 ql chunks, 4 qh chunks, scales, d); q8_0 3 (2 quant halves, d)
+    constexpr uint32_t P = TYPE == 12 ? 9 : (TYPE == 13 ? 11 : (TYPE == 14 ? 14 : 3));
+    constexpr uint32_t BB = TYPE == 12 ? kQ4KBytes : (TYPE == 13 ? kQ5KBytes : (TYPE == 14 ? kQ6KBytes : kQ80Bytes));
+    const uint64_t per_row = (uint64_t)nsb * P;
+    const uint64_t total = per_row * n;
+    for (uint64_t t = blockIdx.x * 256ull + threadIdx.x; t < total; t += (uint64_t)gridDim.x * 256u) {
+        const uint32_t r = (uint32_t)(t / per_row);
+        const uint32_t rem = (uint32_t)(t - (uint64_t)r * per_row);
+        const uint32_t sb = rem / P, piece = rem % P;
+        const uint8_t* blk = src + (uint64_t)r * row_bytes + (uint64_t)sb * BB;
+        uint8_t* row = dst + (uint64_t)r * pitch;
+        if constexpr (TYPE == 12) {
+            // 144-byte blocks: 16-byte aligned when the tensor is
+            const uint4 v = reinterpret_cast<const uint4*>(blk)[piece];
+            const uint64_t o = piece == 0 ? 128ull * nsb + 16ull * sb : 16ull * perm_chunk(nsb, sb, (piece - 1) / 2, (piece - 1) % 2);
+            *reinterpret_cast<uint4*>(row + o) = v;
+        } else if constexpr (TYPE == 13) {
+            const uint4 v = reinterpret_cast<const uint4*>(blk)[piece];
+            uint64_t o;
+            if (piece == 0) o = 160ull * nsb + 16ull * sb;
+            else if (piece < 3) o = 128ull * nsb + 32ull * sb + 16ull * (piece - 1);
+            else o = 16ull * perm_chunk(nsb, sb, (piece - 3) / 2, (piece - 3) % 2);
+            *reinterpret_cast<uint4*>(row + o) = v;
+        } else if constexpr (TYPE == 14) {
+            // 210-byte blocks: 2-byte aligned
+            if (piece < 8) {
+                const uint32_t c = piece, h = c / 4, p2 = (c / 2) % 2, hf = c % 2;
+                *reinterpret_cast<uint4*>(row + 16ull * perm_chunk(nsb, sb, 2 * h + hf, p2)) = ld16_a2(blk + 16 * c);
+            } else if (piece < 12) {
+                *reinterpret_cast<uint4*>(row + 128ull * nsb + 64ull * sb + 16ull * (piece - 8)) =
+                    ld16_a2(blk + 128 + 16 * (piece - 8));
+            } else if (piece == 12) {
+                const uint4 v = ld16_a2(blk + 192);
+                const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+                uint32_t out[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (uint32_t j = 0; j < 16; ++j) {
+                    const uint32_t byte = (in[j / 4] >> (8 * (j % 4))) & 0xFFu;
+                    const uint32_t o = q6_sc_offset(j);
+                    out[o / 4] |= byte << (8 * (o % 4));
+                }
+                *reinterpret_cast<uint4*>(row + 192ull * nsb + 16ull * sb) = make_uint4(out[0], out[1], out[2], out[3]);
+            } else {
+                *reinterpret_cast<uint16_t*>(row + 208ull * nsb + 2ull * sb) = (uint16_t)ld_u16a(blk + 208);
+            }
         } else {
-            o = off;
+            // q8_0, 34-byte blocks (nsb = blocks of 32 per row): 2-byte aligned
+            if (piece < 2) *reinterpret_cast<uint4*>(row + 32ull * sb + 16ull * piece) = ld16_a2(blk + 2 + 16 * piece);
+            else *reinterpret_cast<uint16_t*>(row + 32ull * nsb + 2ull * sb) = (uint16_t)ld_u16a(blk);
         }
-        dst[r * pitch + o] = src[t];
+    }
+}
+
+// plain rows: bytes copied to the pitched rows, 4 bytes per thread (row_bytes is even; f16/bf16
+// rows of odd length end in a 2-byte tail)
+__global__ __launch_bounds__(256) void relayout_plain_kernel(uint32_t n, const uint8_t* __restrict__ src,
+                                                             uint8_t* __restrict__ dst, uint64_t row_bytes,
+                                                             uint64_t pitch) {
+    const uint64_t per_row = (row_bytes + 3) / 4;
+    const uint64_t total = per_row * n;
+    for (uint64_t t = blockIdx.x * 256ull + threadIdx.x; t < total; t += (uint64_t)gridDim.x * 256u) {
+        const uint64_t r = t / per_row, w = t - r * per_row;
+        const uint8_t* s = src + r * row_bytes + 4 * w;
+        uint8_t* d = dst + r * pitch + 4 * w;
+        if (4 * w + 4 <= row_bytes) {
+            *reinterpret_cast<uint32_t*>(d) = ld_u16a(s) | (ld_u16a(s + 2) << 16);
+        } else {
+            *reinterpret_cast<uint16_t*>(d) = (uint16_t)ld_u16a(s);
+        }
     }
 }
 
 hipError_t launch_relayout(uint32_t type, uint64_t k, uint64_t n, const uint8_t* src,
                            uint8_t* dst, uint64_t pitch, hipStream_t s) {
-    uint64_t row_bytes = 0;
+    uint64_t row_bytes = 0, pieces = 0, nblk = 0;
     switch (type) {
         case 0: row_bytes = k * 4; break;
         case 1:
         case 30: row_bytes = k * 2; break;
-        case 8: row_bytes = k / 32 * kQ80Bytes; break;
-        case 12: row_bytes = k / kQK * kQ4KBytes; break;
-        case 13: row_bytes = k / kQK * kQ5KBytes; break;
-        case 14: row_bytes = k / kQK * kQ6KBytes; break;
+        case 8: row_bytes = k / 32 * kQ80Bytes; nblk = k / 32; pieces = 3; break;
+        case 12: row_bytes = k / kQK * kQ4KBytes; nblk = k / kQK; pieces = 9; break;
+        case 13: row_bytes = k / kQK * kQ5KBytes; nblk = k / kQK; pieces = 11; break;
+        case 14: row_bytes = k / kQK * kQ6KBytes; nblk = k / kQK; pieces = 14; break;
         default: return hipErrorInvalidValue;
     }
-    const uint64_t total = n * row_bytes;
+    if (n == 0 || row_bytes == 0) return hipSuccess;
+    if (n > 0xFFFFFFFFull || nblk > 0xFFFFFFFFull) return hipErrorInvalidValue;
+    const uint64_t total = pieces ? n * nblk * pieces : n * ((row_bytes + 3) / 4);
     uint64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(relayout_kernel, dim3((unsigned)blocks), dim3(256), 0, s, type, k, n, src,
-                       dst, row_bytes, pitch);
+    const dim3 grid((unsigned)blocks), block(256);
+    switch (type) {
+        case 8: hipLaunchKernelGGL(relayout_kernel<8>, grid, block, 0, s, (uint32_t)nblk, (uint32_t)n, src, dst, row_bytes, pitch); break;
+        case 12: hipLaunchKernelGGL(relayout_kernel<12>, grid, block, 0, s, (uint32_t)nblk, (uint32_t)n, src, dst, row_bytes, pitch); break;
+        case 13: hipLaunchKernelGGL(relayout_kernel<13>, grid, block, 0, s, (uint32_t)nblk, (uint32_t)n, src, dst, row_bytes, pitch); break;
+        case 14: hipLaunchKernelGGL(relayout_kernel<14>, grid, block, 0, s, (uint32_t)nblk, (uint32_t)n, src, dst, row_bytes, pitch); break;
+        default: hipLaunchKernelGGL(relayout_plain_kernel, grid, block, 0, s, (uint32_t)n, src, dst, row_bytes, pitch); break;
+    }
     return hipGetLastError();
 }
 

@@ -47,9 +47,11 @@ struct View {
     std::vector<std::uint64_t> dims;
     std::span<const std::byte> data;
     Layout lay;
+    std::string nm = "fixture.weight";
     std::span<const std::uint64_t> dimensions() const { return dims; }
     std::span<const std::byte> bytes() const { return data; }
     const Layout& layout() const { return lay; }
+    std::string_view name() const { return nm; }
 };
 
 std::span<const std::byte> as_bytes(const std::vector<std::uint8_t>& v) {
@@ -252,6 +254,115 @@ void test_greedy_token(QuantizedDevice& dev) {
     require(dev.greedy_token(v) == best, "greedy token matches the reference loop");
 }
 
+// raw caller-owned bytes are not cached: a buffer reused with new contents gives new results
+void test_raw_spans_follow_their_bytes(QuantizedDevice& dev) {
+    const std::size_t rows = 8, cols = 256;
+    std::vector<std::uint8_t> data(rows * 144);
+    std::vector<float> x(cols, 1.0F), y(rows);
+    for (int round = 0; round < 2; ++round) {
+        for (auto& b : data) b = static_cast<std::uint8_t>(next_u64());
+        for (std::size_t r = 0; r < rows; ++r) {
+            put16(data, r * 144, 0x2000);
+            put16(data, r * 144 + 2, 0x1800);
+        }
+        const std::size_t before = dev.resident_count();
+        dev.storage_matvec(12, rows, cols, as_bytes(data), x, y);
+        require(dev.resident_count() == before, "raw spans are not kept resident");
+        std::vector<float> xhat(cols);
+        std::vector<std::uint8_t> q8(292);
+        orc_quantize_row_q8_k(x.data(), cols, q8.data());
+        orc_dequantize_row_q8_k(q8.data(), cols, xhat.data());
+        for (std::size_t r = 0; r < rows; ++r) {
+            double dot = 0, ab = 0;
+            orc_storage_dot_stats(12, cols, data.data() + r * 144, 144, xhat.data(), &dot, &ab);
+            require(std::fabs(static_cast<double>(y[r]) - dot) <= 1e-4 * ab, "reused buffer: new contents multiplied");
+        }
+    }
+}
+
+// A model with MappedGgufModel's accessors: tensors() of views with name() and
+// absolute_offset(), mapping() with data() and size().
+struct ModelView {
+    std::string nm;
+    std::vector<std::uint64_t> dims;
+    std::span<const std::byte> data;
+    Layout lay;
+    std::uint64_t abs;
+    std::string_view name() const { return nm; }
+    std::span<const std::uint64_t> dimensions() const { return dims; }
+    std::span<const std::byte> bytes() const { return data; }
+    const Layout& layout() const { return lay; }
+    std::uint64_t absolute_offset() const { return abs; }
+};
+struct Mapping {
+    const std::byte* p;
+    std::size_t n;
+    const std::byte* data() const { return p; }
+    std::size_t size() const { return n; }
+};
+struct FakeModel {
+    std::vector<ModelView> views;
+    Mapping map;
+    const std::vector<ModelView>& tensors() const { return views; }
+    const Mapping& mapping() const { return map; }
+};
+
+void test_model_upload(QuantizedDevice& dev) {
+    // payload: a 64-byte header, then a q4_K matrix (40 x 512), a q6_K matrix (12 x 256), an F32 vector
+    const std::size_t r1 = 40, c1 = 512, r2 = 12, c2 = 256;
+    std::vector<std::uint8_t> payload(64 + r1 * 2 * 144 + r2 * 210 + 64 + 256 * 4, 0);
+    for (std::size_t i = 64; i < payload.size(); ++i) payload[i] = static_cast<std::uint8_t>(next_u64());
+    const std::size_t o1 = 64, o2 = o1 + r1 * 2 * 144, o3 = (o2 + r2 * 210 + 63) / 64 * 64;
+    for (std::size_t b = 0; b < r1 * 2; ++b) {
+        put16(payload, o1 + b * 144, 0x2000);
+        put16(payload, o1 + b * 144 + 2, 0x1800);
+    }
+    for (std::size_t b = 0; b < r2; ++b) put16(payload, o2 + b * 210 + 208, 0x2000);
+    const std::byte* base = reinterpret_cast<const std::byte*>(payload.data());
+    FakeModel m{{{"blk.0.ffn_up.weight", {c1, r1}, {base + o1, r1 * 2 * 144}, {12}, o1},
+                 {"blk.0.attn_output.weight", {c2, r2}, {base + o2, r2 * 210}, {14}, o2},
+                 {"blk.0.attn_norm.weight", {256}, {base + o3, 1024}, {0}, o3}},
+                {base, payload.size()}};
+    const std::size_t resident_before = dev.resident_count();
+    dev.upload_model(m);
+    require(dev.model() != nullptr && oq_model_tensor_count(dev.model()) == 3, "model registered");
+    for (int t = 0; t < 2; ++t) {
+        const ModelView& v = m.views[t];
+        const std::size_t rows = v.dims[1], cols = v.dims[0];
+        const std::uint64_t rb = v.data.size() / rows;
+        std::vector<float> x(cols), y(rows);
+        for (auto& e : x) e = static_cast<float>(static_cast<std::int64_t>(next_u64() % 2001) - 1000) / 500.0F;
+        dev.mapped_tensor_matvec(v, x, y);
+        std::vector<float> xhat(cols);
+        std::vector<std::uint8_t> q8(cols / 256 * 292);
+        orc_quantize_row_q8_k(x.data(), cols, q8.data());
+        orc_dequantize_row_q8_k(q8.data(), cols, xhat.data());
+        const auto* raw = reinterpret_cast<const std::uint8_t*>(v.data.data());
+        for (std::size_t r = 0; r < rows; ++r) {
+            double dot = 0, ab = 0;
+            orc_storage_dot_stats(v.lay.type, cols, raw + r * rb, rb, xhat.data(), &dot, &ab);
+            require(std::fabs(static_cast<double>(y[r]) - dot) <= 1e-4 * ab, "model weight multiplies like the oracle");
+        }
+        // the same product with activations and outputs in device memory
+        void *xd = nullptr, *yd = nullptr;
+        require(oq_device_alloc(dev.context(), cols * 4, &xd) == 0 && oq_device_alloc(dev.context(), rows * 4, &yd) == 0,
+                "device buffers");
+        require(oq_copy_to_device(dev.context(), xd, x.data(), cols * 4) == 0, "upload x");
+        dev.mapped_tensor_matmul_device(v, 1, static_cast<const float*>(xd), static_cast<float*>(yd));
+        dev.synchronize();
+        std::vector<float> yd_host(rows);
+        require(oq_copy_to_host(dev.context(), yd_host.data(), yd, rows * 4) == 0, "download y");
+        require(std::memcmp(yd_host.data(), y.data(), rows * 4) == 0, "device-pointer product equals the host form");
+        oq_device_free(dev.context(), xd);
+        oq_device_free(dev.context(), yd);
+    }
+    require(dev.resident_count() == resident_before, "model tensors are served from the model, not uploaded again");
+    // a malformed model fails like MappedGgufModel: overlapping payloads
+    FakeModel bad{{m.views[0], m.views[1]}, m.map};
+    bad.views[1].abs = o1 + 16;
+    require_throws<std::runtime_error>([&] { dev.upload_model(bad); }, "overlapping payloads");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -265,7 +376,9 @@ int main(int argc, char** argv) {
             test_against_oracle(dev, 14, 130, 2048);
             test_against_oracle(dev, 8, 200, 4096);
             test_greedy_token(dev);
-            require(dev.resident_count() == 3 + 4, "one resident copy per distinct tensor");
+            require(dev.resident_count() == 2 + 3, "one resident copy per distinct mapped tensor");
+            test_raw_spans_follow_their_bytes(dev);
+            test_model_upload(dev);
         }
         std::cout << "host adapter tests passed (" << (gpu ? "gpu" : "cpu") << ")\n";
     } catch (const std::exception& e) {

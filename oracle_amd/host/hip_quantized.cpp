@@ -15,6 +15,7 @@ void throw_on_status(int status, const std::string& message) {
         case OQ_OVERFLOW: throw std::overflow_error(message);
         case OQ_UNSUPPORTED_TYPE: throw std::runtime_error(message);
         case OQ_LOGIC_ERROR: throw std::logic_error(message);
+        case OQ_RUNTIME_ERROR: throw std::runtime_error(message);
         default: throw std::runtime_error("HIP device failure: " + message);
     }
 }
@@ -47,6 +48,38 @@ oq_context* QuantizedDevice::context() {
 void QuantizedDevice::evict_all() noexcept {
     for (auto& kv : weights_) oq_weight_release(kv.second);
     weights_.clear();
+    oq_model_release(model_);
+    model_ = nullptr;
+    model_base_ = nullptr;
+    model_bytes_ = 0;
+}
+
+void QuantizedDevice::check_status(int status) { check(status, ctx_); }
+
+void QuantizedDevice::synchronize() { check(oq_synchronize(context()), ctx_); }
+
+void QuantizedDevice::load_model(const void* payload, std::size_t payload_bytes,
+                                 const std::vector<oq_tensor_desc>& tensors) {
+    check(oq_model_validate(payload_bytes, tensors.data(), tensors.size()), nullptr);
+    oq_model* m = nullptr;
+    check(oq_model_upload(context(), payload, payload_bytes, tensors.data(), tensors.size(), &m), ctx_);
+    oq_model_release(model_);
+    model_ = m;
+    model_base_ = static_cast<const std::byte*>(payload);
+    model_bytes_ = payload_bytes;
+}
+
+const oq_weight* QuantizedDevice::model_weight(const std::string& name, std::uint32_t type, std::size_t rows,
+                                               std::size_t cols) {
+    std::uint64_t index = 0;
+    if (oq_model_find(model_, name.c_str(), &index) != OQ_OK) return nullptr;
+    oq_model_tensor_info info{};
+    check(oq_model_tensor(model_, index, &info), nullptr);
+    if (info.weight == nullptr || info.type != type || info.n_dims != 2 || info.dims[0] != cols ||
+        info.dims[1] != rows) {
+        return nullptr;
+    }
+    return info.weight;
 }
 
 // The checks reference_storage_matvec makes before its row loop, in its order
@@ -101,16 +134,23 @@ float* QuantizedDevice::device_floats(void*& buffer, std::size_t& capacity, std:
     return static_cast<float*>(buffer);
 }
 
-void QuantizedDevice::storage_matmul(std::uint32_t type, std::size_t rows, std::size_t cols,
-                                     std::span<const std::byte> matrix_bytes, std::size_t m,
-                                     std::span<const float> vectors, std::span<float> outputs) {
-    validate(type, rows, cols, matrix_bytes, m, vectors.size(), outputs.size());
-    const oq_weight* w = resident(type, rows, cols, matrix_bytes);
+void QuantizedDevice::run_matmul(const oq_weight* w, std::size_t m, std::span<const float> vectors,
+                                 std::span<float> outputs) {
     float* x = device_floats(x_dev_, x_cap_, vectors.size());
     float* y = device_floats(y_dev_, y_cap_, outputs.size());
     check(oq_copy_to_device(ctx_, x, vectors.data(), vectors.size_bytes()), ctx_);
     check(m == 1 ? oq_matvec(ctx_, w, x, y) : oq_matmul(ctx_, w, m, x, y), ctx_);
     check(oq_copy_to_host(ctx_, outputs.data(), y, outputs.size_bytes()), ctx_);
+}
+
+void QuantizedDevice::storage_matmul(std::uint32_t type, std::size_t rows, std::size_t cols,
+                                     std::span<const std::byte> matrix_bytes, std::size_t m,
+                                     std::span<const float> vectors, std::span<float> outputs) {
+    validate(type, rows, cols, matrix_bytes, m, vectors.size(), outputs.size());
+    // caller-owned bytes: uploaded for this call only
+    Transient t;
+    check(oq_weight_upload(context(), type, cols, rows, matrix_bytes.data(), matrix_bytes.size(), &t.w), ctx_);
+    run_matmul(t.w, m, vectors, outputs);
 }
 
 void QuantizedDevice::storage_matvec(std::uint32_t type, std::size_t rows, std::size_t cols,
@@ -119,21 +159,22 @@ void QuantizedDevice::storage_matvec(std::uint32_t type, std::size_t rows, std::
     storage_matmul(type, rows, cols, matrix_bytes, 1, vector, output);
 }
 
-float QuantizedDevice::storage_dot(StorageRowView row, std::span<const float> vector) {
+float QuantizedDevice::row_dot(std::uint32_t type, std::size_t element_count, std::span<const std::byte> bytes,
+                               std::span<const float> vector) {
     // make_storage_row_view's checks (byte size, then whitelist), then the vector length
     // (src/backend/cpu/quantized_reference.cpp:25-29)
     std::uint64_t expected = 0;
-    check(oq_row_byte_size(row.element_count, row.type, &expected), nullptr);
-    if (row.bytes.size() != expected) {
+    check(oq_row_byte_size(element_count, type, &expected), nullptr);
+    if (bytes.size() != expected) {
         throw std::invalid_argument("storage row byte size mismatch: expected " + std::to_string(expected) +
-                                    ", received " + std::to_string(row.bytes.size()));
+                                    ", received " + std::to_string(bytes.size()));
     }
-    if (!oq_type_supported(row.type)) {
-        throw std::invalid_argument("storage decoder does not support GGML type " + std::to_string(row.type));
+    if (!oq_type_supported(type)) {
+        throw std::invalid_argument("storage decoder does not support GGML type " + std::to_string(type));
     }
-    if (vector.size() != row.element_count) throw std::invalid_argument("reference dot vector length mismatch");
+    if (vector.size() != element_count) throw std::invalid_argument("reference dot vector length mismatch");
     float out = 0.0F;
-    storage_matvec(row.type, 1, row.element_count, row.bytes, vector, std::span<float>(&out, 1));
+    storage_matvec(type, 1, element_count, bytes, vector, std::span<float>(&out, 1));
     return out;
 }
 
@@ -173,9 +214,10 @@ void QuantizedDevice::decode_rows(std::uint32_t type, std::size_t rows, std::siz
         throw std::overflow_error("mapped tensor element count overflow");
     }
     if (output.size() != rows * cols) throw std::invalid_argument("mapped tensor decode output length mismatch");
-    const oq_weight* w = resident(type, rows, cols, matrix_bytes);
+    Transient t;
+    check(oq_weight_upload(context(), type, cols, rows, matrix_bytes.data(), matrix_bytes.size(), &t.w), ctx_);
     float* out = device_floats(y_dev_, y_cap_, output.size());
-    check(oq_dequantize_rows(ctx_, w, 0, rows, out), ctx_);
+    check(oq_dequantize_rows(ctx_, t.w, 0, rows, out), ctx_);
     check(oq_copy_to_host(ctx_, output.data(), out, output.size_bytes()), ctx_);
 }
 

@@ -6,13 +6,20 @@
 // the reference) and throws the same exception types for the same conditions, in the same order
 // (src/backend/cpu/quantized_reference.cpp:107-153, src/model/ggml_type.cpp:77-94,
 // src/model/storage_decode.cpp:182-198).  The difference is where the arithmetic runs: weights
-// are uploaded once to HBM through liboq.so's C ABI (include/oq.h) and stay resident, keyed by
-// the address and geometry of the mapped bytes, so a GgufTensorView's mmap'd payload is copied
-// straight to the device the first time it is used and never again.
+// live in HBM, uploaded through liboq.so's C ABI (include/oq.h):
+//   - upload_model(model) takes a whole MappedGgufModel once (oq_model_upload) and serves every
+//     later mapped_tensor_* call on one of its tensors from HBM, looked up by name;
+//   - a mapped tensor outside such a model is uploaded on first use and stays resident, keyed by
+//     the address and geometry of its (immutable, mmap'd) bytes;
+//   - raw spans (storage_matvec, storage_matmul, storage_dot, decode_rows) are uploaded for the
+//     call only: their memory belongs to the caller and may change between calls.
 //
 // Tensor views are taken generically: anything with dimensions() (a range of uint64_t),
-// bytes() (std::span<const std::byte>) and layout().type works, which includes
-// oracle::model::GgufTensorView (include/oracle/model/mapped_gguf.hpp:18-41).
+// bytes() (std::span<const std::byte>), layout().type and name() works, which includes
+// oracle::model::GgufTensorView (include/oracle/model/mapped_gguf.hpp:18-41); a model is anything
+// with tensors() (such views, each with absolute_offset()) and mapping() (data(), size()), which
+// includes oracle::model::MappedGgufModel (:53-78).  Row views: any type with the fields of
+// oracle::model::StorageRowView (include/oracle/model/storage_decode.hpp:24-28).
 //
 // Threading: one QuantizedDevice owns one oq_context (one HIP stream) and is not thread-safe,
 // matching the reference's single-threaded use.  Validation runs before any device work, so
@@ -26,7 +33,9 @@
 #include <span>
 #include <stdexcept>
 #include <string>
+#include <string_view>
 #include <tuple>
+#include <vector>
 
 #include "oq.h"
 
@@ -61,23 +70,74 @@ public:
                         std::span<const std::byte> matrix_bytes, std::size_t m,
                         std::span<const float> vectors, std::span<float> outputs);
 
-    // reference_storage_dot (src/backend/cpu/quantized_reference.cpp:24-82): one row.
-    [[nodiscard]] float storage_dot(StorageRowView row, std::span<const float> vector);
+    // reference_storage_dot (src/backend/cpu/quantized_reference.cpp:24-82): one row, given as
+    // oracle::model::StorageRowView (or the mirror above, or any type with its three fields).
+    template <typename RowView>
+    [[nodiscard]] float storage_dot(const RowView& row, std::span<const float> vector) {
+        return row_dot(row.type, row.element_count, row.bytes, vector);
+    }
+    [[nodiscard]] float storage_dot(const StorageRowView& row, std::span<const float> vector) {
+        return row_dot(row.type, row.element_count, row.bytes, vector);
+    }
 
     // reference_mapped_tensor_matvec (src/backend/cpu/quantized_reference.cpp:107-126)
     template <typename TensorView>
     void mapped_tensor_matvec(const TensorView& tensor, std::span<const float> vector,
                               std::span<float> output) {
-        const auto [rows, cols] = rank2(tensor);
-        storage_matvec(tensor.layout().type, rows, cols, tensor.bytes(), vector, output);
+        mapped_tensor_matmul(tensor, 1, vector, output);
     }
 
     template <typename TensorView>
     void mapped_tensor_matmul(const TensorView& tensor, std::size_t m,
                               std::span<const float> vectors, std::span<float> outputs) {
         const auto [rows, cols] = rank2(tensor);
-        storage_matmul(tensor.layout().type, rows, cols, tensor.bytes(), m, vectors, outputs);
+        const std::uint32_t type = tensor.layout().type;
+        validate(type, rows, cols, tensor.bytes(), m, vectors.size(), outputs.size());
+        run_matmul(mapped_weight(tensor, type, rows, cols), m, vectors, outputs);
     }
+
+    // The same products with activations and outputs already in device memory (x_dev [m][cols],
+    // y_dev [m][rows], F32): for callers that chain projections in HBM (mapped_matvec,
+    // src/runtime/qwen35_block.cpp:108-119, without a host round trip per projection).
+    // Asynchronous on the device's stream (context()); synchronize() waits.
+    template <typename TensorView>
+    void mapped_tensor_matmul_device(const TensorView& tensor, std::size_t m, const float* x_dev, float* y_dev) {
+        (void)context();
+        const auto [rows, cols] = rank2(tensor);
+        const std::uint32_t type = tensor.layout().type;
+        validate(type, rows, cols, tensor.bytes(), m, cols * m, rows * m);
+        const oq_weight* w = mapped_weight(tensor, type, rows, cols);
+        check_status(m == 1 ? oq_matvec(ctx_, w, x_dev, y_dev) : oq_matmul(ctx_, w, m, x_dev, y_dev));
+    }
+    void synchronize();
+
+    // One-time upload of a whole mapped model (oq_model_upload): every tensor validated as
+    // MappedGgufModel does, copied to HBM once; its rank-2 tensors of the supported types become
+    // resident weights, found by name by the mapped_tensor_* calls.  Replaces a previous model.
+    template <typename Model>
+    void upload_model(const Model& model) {
+        std::vector<std::string> names;
+        std::vector<oq_tensor_desc> descs;
+        names.reserve(model.tensors().size());
+        descs.reserve(model.tensors().size());
+        for (const auto& t : model.tensors()) {
+            names.emplace_back(t.name());
+            oq_tensor_desc d{};
+            d.type = t.layout().type;
+            const auto dims = t.dimensions();
+            if (dims.size() > 4) throw std::invalid_argument("tensors of more than four dimensions are not supported");
+            d.n_dims = static_cast<std::uint32_t>(dims.size());
+            std::uint32_t i = 0;
+            for (const std::uint64_t v : dims) d.dims[i++] = v;
+            d.offset = t.absolute_offset();
+            descs.push_back(d);
+        }
+        for (std::size_t i = 0; i < descs.size(); ++i) descs[i].name = names[i].c_str();
+        const auto& map = model.mapping();
+        load_model(map.data(), map.size(), descs);
+    }
+    void load_model(const void* payload, std::size_t payload_bytes, const std::vector<oq_tensor_desc>& tensors);
+    [[nodiscard]] const oq_model* model() const noexcept { return model_; }
 
     // reference_decode_mapped_tensor (src/backend/cpu/quantized_reference.cpp:85-105): every row
     // of the tensor decoded to F32, bit-identical to the reference's decoders.
@@ -108,11 +168,12 @@ public:
     // oq_argmax is called on them directly).
     [[nodiscard]] std::uint32_t greedy_token(std::span<const float> logits);
 
-    // Device-resident access for callers that keep activations in HBM (chained layers).
+    // The resident weight of a mapped tensor's bytes (immutable for the model's lifetime),
+    // uploaded on first use.
     const oq_weight* resident(std::uint32_t type, std::size_t row_count, std::size_t column_count,
                               std::span<const std::byte> matrix_bytes);
     [[nodiscard]] std::size_t resident_count() const noexcept { return weights_.size(); }
-    void evict_all() noexcept;
+    void evict_all() noexcept;  // also releases an uploaded model
     oq_context* context();  // created on first use
     [[nodiscard]] std::string_view name() const noexcept { return "hip"; }
 
@@ -128,15 +189,42 @@ private:
         return {static_cast<std::size_t>(d1), static_cast<std::size_t>(d0)};
     }
 
+    // the model's weight for a tensor of this name and geometry whose bytes lie in the model's
+    // payload, else the address-keyed resident upload
+    template <typename TensorView>
+    const oq_weight* mapped_weight(const TensorView& tensor, std::uint32_t type, std::size_t rows, std::size_t cols) {
+        if (model_ != nullptr) {
+            const std::byte* p = tensor.bytes().data();
+            if (p >= model_base_ && p < model_base_ + model_bytes_) {
+                if (const oq_weight* w = model_weight(std::string(tensor.name()), type, rows, cols)) return w;
+            }
+        }
+        return resident(type, rows, cols, tensor.bytes());
+    }
+    const oq_weight* model_weight(const std::string& name, std::uint32_t type, std::size_t rows, std::size_t cols);
+
     void validate(std::uint32_t type, std::size_t rows, std::size_t cols,
                   std::span<const std::byte> matrix_bytes, std::size_t m, std::size_t vector_len,
                   std::size_t output_len);
+    float row_dot(std::uint32_t type, std::size_t element_count, std::span<const std::byte> bytes,
+                  std::span<const float> vector);
+    void run_matmul(const oq_weight* w, std::size_t m, std::span<const float> vectors, std::span<float> outputs);
+    void check_status(int status);
     float* device_floats(void*& buffer, std::size_t& capacity, std::size_t count);
+
+    // a weight uploaded for one call (raw caller-owned bytes), released by the destructor
+    struct Transient {
+        oq_weight* w = nullptr;
+        ~Transient() { oq_weight_release(w); }
+    };
 
     using Key = std::tuple<const std::byte*, std::size_t, std::uint32_t, std::size_t>;
     int device_;
     oq_context* ctx_ = nullptr;
     std::map<Key, oq_weight*> weights_;
+    oq_model* model_ = nullptr;
+    const std::byte* model_base_ = nullptr;
+    std::size_t model_bytes_ = 0;
     void* x_dev_ = nullptr;
     std::size_t x_cap_ = 0;
     void* y_dev_ = nullptr;

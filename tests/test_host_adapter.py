@@ -22,3 +22,19 @@ def test_adapter_validation_without_gpu():
 @pytest.mark.gpu
 def test_adapter_on_gpu():
     run("gpu")
+
+
+REFERENCE_INCLUDE = "/root/reference/include"
+
+
+@pytest.mark.skipif(not __import__("os").path.isdir(REFERENCE_INCLUDE), reason="reference headers not present")
+def test_adapter_compiles_against_reference_types(tmp_path):
+    """hip_quantized.hpp instantiated on the reference's GgufTensorView, StorageRowView and
+    MappedGgufModel, from the reference's own headers (compile only)."""
+    import subprocess
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    cmd = ["g++", "-std=c++20", "-fsyntax-only", "-Wall", "-Wextra", f"-I{REFERENCE_INCLUDE}",
+           f"-I{root / 'include'}", f"-I{root / 'oracle_amd' / 'host'}", str(root / "tests" / "adapter_reference_compile.cpp")]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-4000:]
