@@ -50,6 +50,10 @@ _ORC_SIGS = [
     ("orc_gated_delta_step", C.c_int, [_P, _P, _P, _P, _P, _U64, _U64, _U64, C.c_float, _P, _P]),
     ("orc_deltanet_trace_size", _U64, [_P]),
     ("orc_deltanet_step", C.c_int, [_P, _P, _P, _P, _P, _P, C.c_int]),
+    ("orc_rope", C.c_int, [_P, _U64, _U64, _U64, _P, C.c_float, _P]),
+    ("orc_attention_step", C.c_int, [_P, _U64, _P, _P, _P, _P]),
+    ("orc_attention_trace_size", _U64, [_P]),
+    ("orc_attention_block_step", C.c_int, [_P, _P, _P, _P, _P, _P, C.c_int]),
 ]
 
 _REF_SIGS = [
@@ -68,6 +72,9 @@ _REF_SIGS = [
     ("ref_recurrent_block", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     ("ref_block_trace_value", C.c_int64, [C.c_char_p, _P, _U64]),
     ("ref_gguf_open", C.c_int, [C.c_char_p, C.POINTER(_U64)]),
+    ("ref_rope", C.c_int, [_P, _U64, _U64, _U64, _P, C.c_float, _P]),
+    ("ref_attention_step", C.c_int, [_P, _U64, _P, _P, _P, _P]),
+    ("ref_attention_block", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     ("ref_gguf_tensor", C.c_int, [_U64, C.c_char_p, C.c_int, C.POINTER(_U32), C.POINTER(_U32), C.POINTER(_U64),
                                   C.POINTER(_U64), C.POINTER(_U64)]),
 ]
@@ -504,3 +511,173 @@ def ref_gguf_tensors(path) -> list[dict]:
         out.append({"name": name.value.decode(), "type": t.value, "dims": list(dims[:nd.value]),
                     "absolute_offset": off.value, "nbytes": nb.value})
     return out
+
+
+# ---------------------------------------------------------------- full-attention decode
+
+class KvCache:
+    """KV cache in the reference's layout (hybrid_cache.cpp:131-207): keys [capacity][kv_heads][key_dim],
+    values [capacity][kv_heads][value_dim], F32, `length` tokens stored."""
+
+    def __init__(self, capacity: int, kv_heads: int, key_dim: int, value_dim: int):
+        self.keys = np.zeros((capacity, kv_heads, key_dim), dtype=np.float32)
+        self.values = np.zeros((capacity, kv_heads, value_dim), dtype=np.float32)
+        self.length = 0
+
+    @property
+    def capacity(self) -> int:
+        return self.keys.shape[0]
+
+    def copy(self) -> "KvCache":
+        c = KvCache(*self.keys.shape, self.values.shape[2])
+        c.keys[:] = self.keys
+        c.values[:] = self.values
+        c.length = self.length
+        return c
+
+    def _struct(self):
+        s = _KvCacheStruct()
+        s.capacity, s.kv_heads, s.key_dim = self.keys.shape
+        s.value_dim = self.values.shape[2]
+        s.length = self.length
+        s.keys = self.keys.ctypes.data
+        s.values = self.values.ctypes.data
+        return s
+
+
+class _KvCacheStruct(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("capacity", "kv_heads", "key_dim", "value_dim", "length")] + \
+               [("keys", C.c_void_p), ("values", C.c_void_p)]
+
+
+def _rope_args(sections, position):
+    sec = (C.c_int32 * 4)(*[int(v) for v in sections])
+    pos = (C.c_uint64 * 3)(*[int(v) for v in position])
+    return sec, pos
+
+
+def rope(heads: np.ndarray, rotary_dim: int, sections, base: float, position, reference: bool = False) -> np.ndarray:
+    """apply_qwen35_rope on a copy of heads [n][head_dim]; position = (temporal, height, width)."""
+    out = np.array(heads, dtype=np.float32, order="C", copy=True)
+    sec, pos = _rope_args(sections, position)
+    lb, fn, err = (ref(), "ref_rope", "ref_last_error") if reference else (lib(), "orc_rope", "orc_last_error")
+    _chk(getattr(lb, fn)(_ptr(out), out.shape[0], out.shape[1], int(rotary_dim), sec, float(base), pos), lb, err)
+    return out
+
+
+def attention_step(q: np.ndarray, k: np.ndarray, v: np.ndarray, cache: KvCache, reference: bool = False) -> np.ndarray:
+    """causal_attention_step: appends k [kv_heads][key_dim] and v to `cache` (in place) and returns
+    the output [q_heads][value_dim] of q [q_heads][key_dim]."""
+    qv, kv, vv = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v))
+    out = np.empty((qv.shape[0], cache.values.shape[2]), dtype=np.float32)
+    st = cache._struct()
+    lb, fn, err = (ref(), "ref_attention_step", "ref_last_error") if reference else \
+        (lib(), "orc_attention_step", "orc_last_error")
+    _chk(getattr(lb, fn)(_ptr(qv), qv.shape[0], _ptr(kv), _ptr(vv), C.byref(st), _ptr(out)), lb, err)
+    cache.length = int(st.length)
+    return out
+
+
+ATTN_WEIGHTS = ("q", "k", "v", "out", "gate", "up", "down")
+ATTN_VECTORS = ("input_norm", "q_norm", "k_norm", "post_norm")
+ATTN_TRACE = ("qfull", "k", "v", "qcur", "kcur", "pregate", "gate_s", "gated", "branch", "resid", "post", "gate", "up",
+              "act", "ffn")
+ATTN_DIMS = ("embedding", "q_heads", "kv_heads", "head_dim", "ffn", "rope_dim")
+
+
+class _AttnBlock(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ATTN_DIMS] + \
+               [("rope_sections", C.c_int32 * 4), ("rope_base", C.c_float), ("eps", C.c_float)] + \
+               [(n + "_type", C.c_uint32) for n in ATTN_WEIGHTS] + \
+               [(n, C.c_void_p) for n in ATTN_WEIGHTS] + \
+               [(n, C.c_void_p) for n in ATTN_VECTORS]
+
+
+class _RefAttnBlock(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ATTN_DIMS] + \
+               [("rope_sections", C.c_int32 * 4), ("rope_base", C.c_float), ("eps", C.c_float)] + \
+               [("types", C.c_uint32 * 7), ("weights", C.c_void_p * 7)] + \
+               [(n, C.c_void_p) for n in ATTN_VECTORS]
+
+
+def attention_trace_sizes(dims: dict) -> dict:
+    Q = dims["q_heads"] * dims["head_dim"]
+    KV = dims["kv_heads"] * dims["head_dim"]
+    E, F = dims["embedding"], dims["ffn"]
+    return dict(zip(ATTN_TRACE, (2 * Q, KV, KV, Q, KV, Q, Q, Q, E, E, E, F, F, F, E)))
+
+
+def _attn_struct(cls, dims, weights, vectors, keep, ref_layout):
+    b = cls()
+    for n in ATTN_DIMS:
+        setattr(b, n, int(dims[n]))
+    for i, v in enumerate(dims["rope_sections"]):
+        b.rope_sections[i] = int(v)
+    b.rope_base = float(dims["rope_base"])
+    b.eps = float(dims["eps"])
+    for i, n in enumerate(ATTN_WEIGHTS):
+        t, data = weights[n]
+        a = np.ascontiguousarray(data, dtype=np.uint8)
+        keep.append(a)
+        if ref_layout:
+            b.types[i] = int(t)
+            b.weights[i] = a.ctypes.data
+        else:
+            setattr(b, n + "_type", int(t))
+            setattr(b, n, a.ctypes.data)
+    for n in ATTN_VECTORS:
+        a = np.ascontiguousarray(vectors[n], dtype=np.float32)
+        keep.append(a)
+        setattr(b, n, a.ctypes.data)
+    return b
+
+
+def _split_trace(dims, tr):
+    out, off = {}, 0
+    for n, sz in attention_trace_sizes(dims).items():
+        out[n] = tr[off:off + sz]
+        off += sz
+    return out
+
+
+def attention_block_step(dims: dict, weights: dict, vectors: dict, cache: KvCache, position, x: np.ndarray,
+                         threads: int | None = None):
+    """Restated attention block step (dims: ATTN_DIMS + rope_sections, rope_base, eps; weights[name] =
+    (ggml type, uint8 bytes)).  Appends to `cache` in place.  Returns (y, trace dict)."""
+    keep = []
+    b = _attn_struct(_AttnBlock, dims, weights, vectors, keep, False)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(int(dims["embedding"]), dtype=np.float32)
+    tr = np.empty(int(lib().orc_attention_trace_size(C.byref(b))), dtype=np.float32)
+    st = cache._struct()
+    pos = (C.c_uint64 * 3)(*[int(v) for v in position])
+    _chk(lib().orc_attention_block_step(C.byref(b), C.byref(st), pos, _ptr(xv), _ptr(y), _ptr(tr),
+                                        threads or default_threads()), lib(), "orc_last_error")
+    cache.length = int(st.length)
+    return y, _split_trace(dims, tr)
+
+
+def ref_attention_block(dims: dict, weights: dict, vectors: dict, cache: KvCache, position, x: np.ndarray,
+                        overrides: dict | None = None):
+    """The reference's own attention block (execute_qwen35_attention_block_reference) on in-memory
+    views; same arguments as attention_block_step, overrides maps ATTN_WEIGHTS names to F32
+    projection outputs.  Appends to `cache` in place.  Returns (y, trace dict)."""
+    keep = []
+    b = _attn_struct(_RefAttnBlock, dims, weights, vectors, keep, True)
+    ov = None
+    if overrides:
+        ov = (C.c_void_p * 7)()
+        for i, n in enumerate(ATTN_WEIGHTS):
+            if n in overrides:
+                a = np.ascontiguousarray(overrides[n], dtype=np.float32)
+                keep.append(a)
+                ov[i] = a.ctypes.data
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(int(dims["embedding"]), dtype=np.float32)
+    tr = np.empty(sum(attention_trace_sizes(dims).values()), dtype=np.float32)
+    st = cache._struct()
+    pos = (C.c_uint64 * 3)(*[int(v) for v in position])
+    _chk(ref().ref_attention_block(C.byref(b), C.byref(st), pos, _ptr(xv), _ptr(y), _ptr(tr), ov), ref(),
+         "ref_last_error")
+    cache.length = int(st.length)
+    return y, _split_trace(dims, tr)

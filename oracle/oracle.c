@@ -18,6 +18,15 @@
  *                         bsums, |d q - x| <= |d|/2, zero block, first-index tie break)
  *   orc_vec_dot_q8_k       algebraic identity with orc_storage_dot on the dequantized Q8_K
  *                         row (tolerance) + brute-force integer sums on tiny rows
+ *   orc_rope              reference KATs (tests/test_phase1e.cpp:92-142) + the compiled
+ *                         reference on seeded heads at text, multimodal and far positions, bit
+ *                         for bit + identity at position 0 and per-pair norm preservation
+ *   orc_attention_step    reference KATs (test_phase1e.cpp:144-186) + the compiled reference
+ *                         over multi-step caches, bit for bit + one-token / equal-key / float64
+ *                         softmax checks and the query-head to KV-head map
+ *   orc_attention_block_step  the compiled reference block (qwen35_block.cpp:607-756) on
+ *                         in-memory views, bit for bit (K-quant projections through its override
+ *                         bridge) + the block KAT of test_phase2c.cpp:284-310
  */
 #include "oracle.h"
 
@@ -813,6 +822,154 @@ int orc_deltanet_step(const orc_deltanet_block* b, float* conv_history, float* s
     if (rc == ORC_OK) {
         for (uint64_t i = 0; i < E; ++i) y[i] = resid[i] + ffn[i];
         if (trace) memcpy(trace, buf, orc_deltanet_trace_size(b) * sizeof(float));
+    }
+    free(buf);
+    return rc;
+}
+
+/* ---------------------------------------------------------------- full-attention decode */
+
+/* reference_kernels.cpp:28-40: frequency f takes the height coordinate when f % 3 == 1 and
+   f / 3 < sections[1], the width coordinate when f % 3 == 2 and f / 3 < sections[2], else the
+   temporal one */
+static uint64_t rope_coordinate(uint64_t f, const uint64_t position[3], const int32_t sections[4]) {
+    if (f % 3 == 1 && f / 3 < (uint64_t)sections[1]) return position[1];
+    if (f % 3 == 2 && f / 3 < (uint64_t)sections[2]) return position[2];
+    return position[0];
+}
+
+/* reference_kernels.cpp:77-125 */
+int orc_rope(float* heads, uint64_t n_heads, uint64_t head_dim, uint64_t rotary_dim, const int32_t sections[4],
+             float base, const uint64_t position[3]) {
+    if (rotary_dim == 0 || rotary_dim % 2 != 0 || rotary_dim > head_dim)
+        return fail(ORC_INVALID_ARGUMENT, "RoPE dimension must be non-zero, even, and within head width");
+    if (!(base > 0.0f) || !isfinite(base))
+        return fail(ORC_INVALID_ARGUMENT, "RoPE frequency base must be positive and finite");
+    int64_t total = 0;
+    for (int i = 0; i < 4; ++i) {
+        if (sections[i] < 0) return fail(ORC_INVALID_ARGUMENT, "RoPE dimension sections must be non-negative");
+        total += sections[i];
+    }
+    if (total != (int64_t)(rotary_dim / 2))
+        return fail(ORC_INVALID_ARGUMENT, "RoPE dimension sections must sum to half the rotary dimension");
+    const uint64_t half = rotary_dim / 2;
+    for (uint64_t h = 0; h < n_heads; ++h) {
+        float* x = heads + h * head_dim;
+        for (uint64_t f = 0; f < half; ++f) {
+            const double exponent = (2.0 * (double)f) / (double)rotary_dim;
+            const double inv_freq = 1.0 / pow((double)base, exponent);
+            const double angle = (double)rope_coordinate(f, position, sections) * inv_freq;
+            const float c = (float)cos(angle), s = (float)sin(angle);
+            const float a = x[f], b = x[half + f];
+            x[f] = a * c - b * s;
+            x[half + f] = b * c + a * s;
+        }
+    }
+    return ORC_OK;
+}
+
+/* reference_kernels.cpp:127-195 with KvCache::append (hybrid_cache.cpp:154-169) */
+int orc_attention_step(const float* q, uint64_t q_heads, const float* k, const float* v, orc_kv_cache* c,
+                       float* out) {
+    const uint64_t Hkv = c->kv_heads, dk = c->key_dim, dv = c->value_dim;
+    if (Hkv == 0 || q_heads % Hkv != 0) return fail(ORC_INVALID_ARGUMENT, "causal_attention_step dimensions are incompatible");
+    if (c->length >= c->capacity) return fail(ORC_OVERFLOW, "KV cache capacity exceeded");
+    memcpy(c->keys + c->length * Hkv * dk, k, Hkv * dk * sizeof(float));
+    memcpy(c->values + c->length * Hkv * dv, v, Hkv * dv * sizeof(float));
+    c->length += 1;
+    const uint64_t T = c->length, rep = q_heads / Hkv;
+    const float scale = 1.0f / sqrtf((float)dk);
+    float* scores = (float*)malloc(T * sizeof(float));
+    if (!scores) return fail(ORC_RUNTIME_ERROR, "out of memory");
+    for (uint64_t i = 0; i < q_heads * dv; ++i) out[i] = 0.0f;
+    int rc = ORC_OK;
+    for (uint64_t h = 0; h < q_heads && rc == ORC_OK; ++h) {
+        const uint64_t g = h / rep;
+        const float* qh = q + h * dk;
+        float maximum = -INFINITY;
+        for (uint64_t t = 0; t < T; ++t) {
+            const float* kt = c->keys + (t * Hkv + g) * dk;
+            double dot = 0.0;
+            for (uint64_t d = 0; d < dk; ++d) dot += (double)qh[d] * (double)kt[d];
+            scores[t] = (float)dot * scale;
+            if (scores[t] > maximum) maximum = scores[t];
+        }
+        double denominator = 0.0;
+        for (uint64_t t = 0; t < T; ++t) {
+            scores[t] = expf(scores[t] - maximum);
+            denominator += (double)scores[t];
+        }
+        if (!(denominator > 0.0) || !isfinite(denominator)) {
+            rc = fail(ORC_RUNTIME_ERROR, "causal attention softmax normalization failed");
+            break;
+        }
+        float* oh = out + h * dv;
+        for (uint64_t t = 0; t < T; ++t) {
+            const float p = (float)((double)scores[t] / denominator);
+            const float* vt = c->values + (t * Hkv + g) * dv;
+            for (uint64_t d = 0; d < dv; ++d) oh[d] += p * vt[d];
+        }
+    }
+    free(scores);
+    return rc;
+}
+
+uint64_t orc_attention_trace_size(const orc_attention_block* b) {
+    const uint64_t Q = b->q_heads * b->head_dim, KV = b->kv_heads * b->head_dim;
+    return 6 * Q + 3 * KV + 4 * b->embedding + 3 * b->ffn;
+}
+
+/* qwen35_block.cpp:607-756 (attention block), :326-352 (finish_block), :296-324 (MLP) */
+int orc_attention_block_step(const orc_attention_block* b, orc_kv_cache* cache, const uint64_t position[3],
+                             const float* x, float* y, float* trace, int threads) {
+    const uint64_t E = b->embedding, Hq = b->q_heads, Hkv = b->kv_heads, D = b->head_dim, F = b->ffn;
+    if (E == 0 || Hq == 0 || Hkv == 0 || D == 0 || F == 0)
+        return fail(ORC_INVALID_ARGUMENT, "Qwen3.5 attention block dimensions are incompatible");
+    if (cache->kv_heads != Hkv || cache->key_dim != D || cache->value_dim != D)
+        return fail(ORC_INVALID_ARGUMENT, "Qwen3.5 attention cache dimensions do not match the manifest");
+    const uint64_t Q = Hq * D, KV = Hkv * D;
+    float* buf = (float*)calloc(orc_attention_trace_size(b) + E, sizeof(float));
+    if (!buf) return fail(ORC_RUNTIME_ERROR, "out of memory");
+    float *qfull = buf, *kp = qfull + 2 * Q, *vp = kp + KV, *qcur = vp + KV, *kcur = qcur + Q, *pregate = kcur + KV,
+          *gate_s = pregate + Q, *gated = gate_s + Q, *branch = gated + Q, *resid = branch + E, *post = resid + E,
+          *gate = post + E, *up = gate + F, *act = up + F, *ffn = act + F, *normed = ffn + E;
+    int rc = orc_rms_norm_rows(x, b->input_norm, E, E, b->eps, normed);
+    if (rc == ORC_OK) rc = block_matvec(b->q_type, b->q, 2 * Q, E, normed, qfull, threads);
+    if (rc == ORC_OK) rc = block_matvec(b->k_type, b->k, KV, E, normed, kp, threads);
+    if (rc == ORC_OK) rc = block_matvec(b->v_type, b->v, KV, E, normed, vp, threads);
+    if (rc == ORC_OK) {
+        /* per head: D query values, then D gate values (qwen35_block.cpp:671-685) */
+        for (uint64_t h = 0; h < Hq; ++h) {
+            memcpy(qcur + h * D, qfull + h * 2 * D, D * sizeof(float));
+            memcpy(gate_s + h * D, qfull + h * 2 * D + D, D * sizeof(float));
+        }
+        rc = orc_rms_norm_rows(qcur, b->q_norm, Q, D, b->eps, qcur);
+    }
+    if (rc == ORC_OK) rc = orc_rms_norm_rows(kp, b->k_norm, KV, D, b->eps, kcur);
+    if (rc == ORC_OK) rc = orc_rope(qcur, Hq, D, b->rope_dim, b->rope_sections, b->rope_base, position);
+    if (rc == ORC_OK) rc = orc_rope(kcur, Hkv, D, b->rope_dim, b->rope_sections, b->rope_base, position);
+    if (rc == ORC_OK) rc = orc_attention_step(qcur, Hq, kcur, vp, cache, pregate);
+    if (rc == ORC_OK) {
+        for (uint64_t i = 0; i < Q; ++i) {
+            const float g = orc_sigmoid(gate_s[i]);
+            gate_s[i] = g;
+            gated[i] = pregate[i] * g;
+        }
+        rc = block_matvec(b->out_type, b->out, E, Q, gated, branch, threads);
+    }
+    if (rc == ORC_OK) {
+        for (uint64_t i = 0; i < E; ++i) resid[i] = x[i] + branch[i];
+        rc = orc_rms_norm_rows(resid, b->post_norm, E, E, b->eps, post);
+    }
+    if (rc == ORC_OK) rc = block_matvec(b->gate_type, b->gate, F, E, post, gate, threads);
+    if (rc == ORC_OK) rc = block_matvec(b->up_type, b->up, F, E, post, up, threads);
+    if (rc == ORC_OK) {
+        for (uint64_t i = 0; i < F; ++i) act[i] = orc_silu(gate[i]) * up[i];
+        rc = block_matvec(b->down_type, b->down, E, F, act, ffn, threads);
+    }
+    if (rc == ORC_OK) {
+        for (uint64_t i = 0; i < E; ++i) y[i] = resid[i] + ffn[i];
+        if (trace) memcpy(trace, buf, orc_attention_trace_size(b) * sizeof(float));
     }
     free(buf);
     return rc;

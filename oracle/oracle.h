@@ -152,6 +152,53 @@ uint64_t orc_deltanet_trace_size(const orc_deltanet_block* b);
 int orc_deltanet_step(const orc_deltanet_block* b, float* conv_history, float* state,
                       const float* x, float* y, float* trace, int threads);
 
+/* ---------------------------------------------------------------- full-attention decode
+ * Restatement of the reference's attention block at batch 1:
+ *   orc_rope                  reference_kernels.cpp:77-125 (+ position_for_frequency :28-40):
+ *                             angles in double (base^(2f/R), coordinate * 1/that), cos and sin
+ *                             rounded to F32, pairs (f, R/2 + f) rotated with separate F32
+ *                             multiplies and adds
+ *   orc_kv_cache              KvCache (hybrid_cache.cpp:131-207): keys [capacity][kv_heads][key_dim],
+ *                             values [capacity][kv_heads][value_dim], F32, caller-owned arrays
+ *   orc_attention_step        reference_kernels.cpp:127-195: append, then per query head
+ *                             (kv head = head / (q_heads / kv_heads)) double-accumulated dots
+ *                             times 1/sqrt(key_dim) in F32, max, expf, double denominator,
+ *                             F32 probabilities, F32 weighted sum in token order
+ *   orc_attention_block_step  qwen35_block.cpp:607-756 + finish_block :326-352 + execute_mlp
+ *                             :296-324, projections with orc_deltanet_step's semantics
+ */
+typedef struct orc_kv_cache {
+    uint64_t capacity, kv_heads, key_dim, value_dim, length;
+    float *keys, *values;
+} orc_kv_cache;
+/* heads [n_heads][head_dim] rotated in place; position = {temporal, height, width} */
+int orc_rope(float* heads, uint64_t n_heads, uint64_t head_dim, uint64_t rotary_dim, const int32_t sections[4],
+             float base, const uint64_t position[3]);
+/* q [q_heads][key_dim], k [kv_heads][key_dim], v [kv_heads][value_dim] -> out [q_heads][value_dim] */
+int orc_attention_step(const float* q, uint64_t q_heads, const float* k, const float* v, orc_kv_cache* cache,
+                       float* out);
+
+typedef struct orc_attention_block {
+    uint64_t embedding, q_heads, kv_heads, head_dim, ffn, rope_dim;
+    int32_t rope_sections[4];
+    float rope_base, eps;
+    /* GGML weights: q [E -> 2*Hq*D] (per head: D query values then D gate values),
+       k [E -> Hkv*D], v [E -> Hkv*D], out [Hq*D -> E], gate/up [E -> F], down [F -> E] */
+    uint32_t q_type, k_type, v_type, out_type, gate_type, up_type, down_type;
+    const uint8_t *q, *k, *v, *out, *gate, *up, *down;
+    /* F32 vectors: input_norm[E], q_norm[D], k_norm[D], post_norm[E] */
+    const float *input_norm, *q_norm, *k_norm, *post_norm;
+} orc_attention_block;
+
+/* trace layout (Q = Hq*D, KV = Hkv*D): qfull[2Q] k[KV] v[KV] qcur[Q] kcur[KV] pregate[Q]
+   gate_s[Q] gated[Q] branch[E] resid[E] post[E] gate[F] up[F] act[F] ffn[E]  -- the reference's
+   Qcur_full Kcur_projected Vcur_projected Qcur Kcur attn_pregate gate_sigmoid attn_gated
+   attn_output attn_residual attn_post_norm ffn_gate ffn_up ffn_swiglu ffn_out */
+enum { ORC_ATTN_TRACE_FIELDS = 15 };
+uint64_t orc_attention_trace_size(const orc_attention_block* b);
+int orc_attention_block_step(const orc_attention_block* b, orc_kv_cache* cache, const uint64_t position[3],
+                             const float* x, float* y, float* trace, int threads);
+
 /* FNV-1a 64 over raw bytes (the reference fingerprints F32 bit patterns the same way,
    qwen35_block.cpp:354-364) */
 uint64_t orc_fnv1a64(const void* data, uint64_t nbytes);

@@ -378,3 +378,156 @@ int ref_gguf_tensor(std::uint64_t index, char* name, int name_cap, std::uint32_t
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- the reference's attention path
+//
+// apply_qwen35_rope (src/runtime/reference_kernels.cpp:77-125), causal_attention_step (:127-195)
+// and execute_qwen35_attention_block_reference (src/runtime/qwen35_block.cpp:607-756) on the
+// caller's arrays.  The KV cache crosses the boundary as the oracle's orc_kv_cache arrays: a
+// KvCache of the same capacity is rebuilt by appending the `length` stored tokens in order
+// (KvCache::append copies, so the rebuilt cache holds the same bits), the call runs, and the
+// cache's rows are copied back.
+struct RefKvCache {
+    std::uint64_t capacity, kv_heads, key_dim, value_dim, length;
+    float *keys, *values;
+};
+
+struct RefAttentionBlock {
+    std::uint64_t embedding, q_heads, kv_heads, head_dim, ffn, rope_dim;
+    std::int32_t rope_sections[4];
+    float rope_base, eps;
+    std::uint32_t types[7];  // q k v out gate up down
+    const std::uint8_t* weights[7];
+    const float *input_norm, *q_norm, *k_norm, *post_norm;
+};
+
+namespace {
+
+oracle::runtime::KvCache rebuild(const RefKvCache& c) {
+    oracle::runtime::KvCache cache(static_cast<std::size_t>(c.capacity), static_cast<std::size_t>(c.kv_heads),
+                                   static_cast<std::size_t>(c.key_dim), static_cast<std::size_t>(c.value_dim));
+    const std::size_t kw = static_cast<std::size_t>(c.kv_heads * c.key_dim);
+    const std::size_t vw = static_cast<std::size_t>(c.kv_heads * c.value_dim);
+    for (std::uint64_t t = 0; t < c.length; ++t) {
+        cache.append(std::span<const float>(c.keys + t * kw, kw), std::span<const float>(c.values + t * vw, vw));
+    }
+    return cache;
+}
+
+void store(const oracle::runtime::KvCache& cache, RefKvCache& c) {
+    c.length = cache.size();
+    for (std::size_t t = 0; t < cache.size(); ++t) {
+        for (std::size_t h = 0; h < cache.key_value_heads(); ++h) {
+            const auto k = cache.key(t, h);
+            const auto v = cache.value(t, h);
+            std::copy(k.begin(), k.end(), c.keys + (t * cache.key_value_heads() + h) * cache.key_dimension());
+            std::copy(v.begin(), v.end(), c.values + (t * cache.key_value_heads() + h) * cache.value_dimension());
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ref_rope(float* heads, std::uint64_t n_heads, std::uint64_t head_dim, std::uint64_t rotary_dim,
+             const std::int32_t* sections, float base, const std::uint64_t* position) {
+    return guarded([&] {
+        oracle::core::Tensor t({static_cast<std::size_t>(n_heads), static_cast<std::size_t>(head_dim)});
+        std::copy(heads, heads + n_heads * head_dim, t.data().begin());
+        oracle::runtime::apply_qwen35_rope(t, {position[0], position[1], position[2]},
+                                           static_cast<std::size_t>(rotary_dim),
+                                           {sections[0], sections[1], sections[2], sections[3]}, base);
+        std::copy(t.data().begin(), t.data().end(), heads);
+    });
+}
+
+int ref_attention_step(const float* q, std::uint64_t q_heads, const float* k, const float* v, RefKvCache* c,
+                       float* out) {
+    return guarded([&] {
+        auto cache = rebuild(*c);
+        const auto Hq = static_cast<std::size_t>(q_heads), Hkv = static_cast<std::size_t>(c->kv_heads),
+                   dk = static_cast<std::size_t>(c->key_dim), dv = static_cast<std::size_t>(c->value_dim);
+        oracle::core::Tensor tq({Hq, dk}), tk({Hkv, dk}), tv({Hkv, dv}), to({Hq, dv});
+        std::copy(q, q + Hq * dk, tq.data().begin());
+        std::copy(k, k + Hkv * dk, tk.data().begin());
+        std::copy(v, v + Hkv * dv, tv.data().begin());
+        oracle::runtime::causal_attention_step(tq, tk, tv, cache, to);
+        std::copy(to.data().begin(), to.data().end(), out);
+        store(cache, *c);
+    });
+}
+
+int ref_attention_block(const RefAttentionBlock* b, RefKvCache* c, const std::uint64_t* position, const float* x,
+                        float* y, float* trace, const float* const* overrides) {
+    return guarded([&] {
+        const std::uint64_t E = b->embedding, Hq = b->q_heads, Hkv = b->kv_heads, D = b->head_dim, F = b->ffn;
+        const std::uint64_t Q = Hq * D, KV = Hkv * D;
+        oracle::model::Qwen35Manifest m;
+        m.architecture = "qwen35";
+        m.embedding_length = static_cast<std::uint32_t>(E);
+        m.feed_forward_length = static_cast<std::uint32_t>(F);
+        m.attention_rms_epsilon = b->eps;
+        m.attention_head_count = static_cast<std::uint32_t>(Hq);
+        m.attention_head_count_kv = static_cast<std::uint32_t>(Hkv);
+        m.attention_key_length = static_cast<std::uint32_t>(D);
+        m.attention_value_length = static_cast<std::uint32_t>(D);
+        m.rope_dimension_count = static_cast<std::uint32_t>(b->rope_dim);
+        m.rope_dimension_sections = {b->rope_sections[0], b->rope_sections[1], b->rope_sections[2],
+                                     b->rope_sections[3]};
+        m.rope_frequency_base = b->rope_base;
+        ViewStore vs;
+        const std::uint64_t cols[7] = {E, E, E, Q, E, E, F};
+        const std::uint64_t rows[7] = {2 * Q, KV, KV, E, F, F, E};
+        const char* names[7] = {"attn_q", "attn_k", "attn_v", "attn_output", "gate", "up", "down"};
+        const oracle::model::GgufTensorView* w[7];
+        for (int i = 0; i < 7; ++i) w[i] = vs.add(names[i], {cols[i], rows[i]}, b->types[i], b->weights[i]);
+        oracle::model::Qwen35BackboneBlockWeights blk;
+        blk.index = 3;
+        blk.kind = oracle::model::Qwen35BlockKind::full_attention;
+        blk.input_norm = vs.add("input_norm", {E}, 0, b->input_norm);
+        blk.post_attention_norm = vs.add("post_norm", {E}, 0, b->post_norm);
+        blk.mlp.gate = w[4];
+        blk.mlp.up = w[5];
+        blk.mlp.down = w[6];
+        oracle::model::Qwen35AttentionWeights aw;
+        aw.query = w[0];
+        aw.key = w[1];
+        aw.value = w[2];
+        aw.output = w[3];
+        aw.query_norm = vs.add("attn_q_norm", {D}, 0, b->q_norm);
+        aw.key_norm = vs.add("attn_k_norm", {D}, 0, b->k_norm);
+        blk.attention = aw;
+
+        auto cache = rebuild(*c);
+        oracle::runtime::Qwen35MatvecOverrides ov;
+        if (overrides != nullptr) {
+            const char* trace_names[7] = {"Qcur_full", "Kcur_projected", "Vcur_projected", "attn_output",
+                                          "ffn_gate", "ffn_up", "ffn_out"};
+            for (int i = 0; i < 7; ++i) {
+                if (overrides[i] == nullptr) continue;
+                ov.tensors.push_back({trace_names[i], std::vector<float>(overrides[i], overrides[i] + rows[i])});
+            }
+        }
+        auto res = oracle::runtime::execute_qwen35_attention_block_reference(
+            m, blk, std::span<const float>(x, static_cast<std::size_t>(E)), cache,
+            {position[0], position[1], position[2]}, true, overrides != nullptr ? &ov : nullptr);
+        std::copy(res.output.begin(), res.output.end(), y);
+        store(cache, *c);
+        g_trace = res.trace.tensors;
+        if (trace != nullptr) {
+            const char* fields[15] = {"Qcur_full", "Kcur_projected", "Vcur_projected", "Qcur", "Kcur",
+                                      "attn_pregate", "gate_sigmoid", "attn_gated", "attn_output", "attn_residual",
+                                      "attn_post_norm", "ffn_gate", "ffn_up", "ffn_swiglu", "ffn_out"};
+            std::uint64_t off = 0;
+            for (const char* f : fields) {
+                const auto* t = res.trace.find(f);
+                if (t == nullptr) throw std::runtime_error(std::string("reference trace lacks ") + f);
+                std::copy(t->values.begin(), t->values.end(), trace + off);
+                off += t->values.size();
+            }
+        }
+    });
+}
+
+}  // extern "C"

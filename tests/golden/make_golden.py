@@ -90,6 +90,30 @@ def kat() -> dict:
                   "expect": {"output_equals_input": True, "beta_sigmoid0": 0.5, "gate0": -0.6931471805599453,
                              "tol": 1e-6, "q_predelta_signs": [1, -1, 1, -1], "state_before_zero": True,
                              "state_after_nonzero": True}},
+        # reference tests/test_phase1e.cpp:92-142 (RoPE, MRoPE) and :144-186 (KV cache + attention)
+        "rope": {"head": [1.0, 2.0, 3.0, 4.0], "position": [1, 1, 1], "rotary_dim": 4, "sections": [2, 0, 0, 0],
+                 "base": 1.0, "expected_of": "1cos1-3sin1, 2cos1-4sin1, 3cos1+1sin1, 4cos1+2sin1",
+                 "norm": 30.0, "tol": 1e-6},
+        "mrope": {"head": [1.0, 1.0, 1.0, 0.0, 0.0, 0.0], "position": [1, 2, 3], "rotary_dim": 6,
+                  "sections": [1, 1, 1, 0], "base": 1.0,
+                  "expected_of": "cos1 cos2 cos3 sin1 sin2 sin3", "tol": 1e-6},
+        "attention": {"capacity": 2, "kv_heads": 1, "key_dim": 2, "value_dim": 2, "q_heads": 2,
+                      "steps": [{"q": [1.0, 0.0, 1.0, 0.0], "k": [1.0, 0.0], "v": [2.0, 3.0],
+                                 "expected": [2.0, 3.0, 2.0, 3.0]},
+                                {"q": [0.0, 1.0, 0.0, 1.0], "k": [0.0, 1.0], "v": [4.0, 5.0],
+                                 "expected_of": "p_new = e^(1/sqrt2) / (1 + e^(1/sqrt2)); p_old 2 + p_new 4, "
+                                                "p_old 3 + p_new 5"}],
+                      "tol": 1e-6, "third_step": "overflow"},
+        # reference tests/test_phase2c.cpp: manifest :44-71, attention block weights :182-213 (all
+        # F32, MLP zero), assertions :284-310
+        "attention_block": {"dims": {"embedding": 4, "q_heads": 2, "kv_heads": 1, "head_dim": 2, "ffn": 4,
+                                     "rope_dim": 2, "rope_sections": [1, 0, 0, 0], "rope_base": 10000.0,
+                                     "eps": 1e-6},
+                            "input": [1.0, 2.0, 3.0, 4.0],
+                            "q_ones": [[0, 0], [1, 1], [4, 2], [5, 3]], "k_ones": [[0, 0], [1, 1]],
+                            "v_ones": [[0, 2], [1, 3]], "out": "identity", "norms": "ones",
+                            "expected_of": "x[i] + 0.5 * x[2 + i % 2] / sqrt(7.5 + eps)", "tol": 1e-5,
+                            "cache_after": 1},
     }
 
 
@@ -255,6 +279,102 @@ def block_vectors() -> dict[str, np.ndarray]:
     return out
 
 
+ATTN_PLAIN_DIMS = dict(embedding=64, q_heads=4, kv_heads=2, head_dim=32, ffn=96, rope_dim=16,
+                       rope_sections=[3, 3, 2, 0], rope_base=10000.0, eps=1e-6)
+ATTN_KQ_DIMS = dict(embedding=256, q_heads=4, kv_heads=1, head_dim=64, ffn=256, rope_dim=32,
+                    rope_sections=[6, 5, 5, 0], rope_base=1e7, eps=1e-6)
+ATTN_PLAIN_TYPES = dict(q=8, k=1, v=0, out=8, gate=0, up=1, down=8)
+ATTN_KQ_TYPES = dict(q=12, k=12, v=12, out=14, gate=12, up=12, down=12)
+# positions (temporal, height, width) of the three block steps after five cached tokens; the last
+# one multimodal
+ATTN_POSITIONS = ((5, 5, 5), (6, 6, 6), (7, 3, 11))
+
+
+def _weight(rng, t, rows, cols):
+    if t in (12, 13, 14, 8):
+        return t, synth.weights(t, rng, rows, cols)
+    vals = (0.05 * rng.standard_normal(rows * cols)).astype(np.float32)
+    if t == 0:
+        data = vals.view(np.uint8)
+    elif t == 1:
+        data = vals.astype(np.float16).view(np.uint8)
+    else:
+        data = (vals.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
+    return t, data.copy()
+
+
+def attention_inputs(rng: np.random.Generator, dims: dict, types: dict, cached: int = 5):
+    """Seeded attention-block inputs: (weights, vectors, cache with `cached` tokens, xs[3])."""
+    E, F, Hq, Hkv, D = (dims[k] for k in ("embedding", "ffn", "q_heads", "kv_heads", "head_dim"))
+    Q, KV = Hq * D, Hkv * D
+    shapes = {"q": (2 * Q, E), "k": (KV, E), "v": (KV, E), "out": (E, Q), "gate": (F, E), "up": (F, E),
+              "down": (E, F)}
+    w = {n: _weight(rng, types[n], r, c) for n, (r, c) in shapes.items()}
+    vec = {
+        "input_norm": (1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32),
+        "q_norm": (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32),
+        "k_norm": (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32),
+        "post_norm": (1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32),
+    }
+    cache = oracle.KvCache(cached + 4, Hkv, D, D)
+    cache.keys[:cached] = rng.standard_normal((cached, Hkv, D)).astype(np.float32)
+    cache.values[:cached] = rng.standard_normal((cached, Hkv, D)).astype(np.float32)
+    cache.length = cached
+    xs = rng.standard_normal((3, E)).astype(np.float32)
+    return w, vec, cache, xs
+
+
+def attention_vectors() -> dict[str, np.ndarray]:
+    out: dict[str, np.ndarray] = {}
+    # RoPE and the attention step alone, 8 query heads over 2 KV heads of 256 (the 2B model's
+    # attention geometry), 12 steps from an empty cache
+    rng = np.random.default_rng(20261205)
+    heads = rng.standard_normal((16, 256)).astype(np.float32)
+    out["rope_in"] = heads
+    for name, pos in (("text", (37, 37, 37)), ("mm", (37, 4, 19)), ("far", (262143, 262143, 262143))):
+        out[f"rope_{name}_pos"] = np.array(pos, dtype=np.uint64)
+        out[f"rope_{name}_bits"] = oracle.rope(heads, 64, [11, 11, 10, 0], 1e7, pos, reference=True).view(np.uint32)
+    cache = oracle.KvCache(16, 2, 256, 256)
+    qs = rng.standard_normal((12, 8, 256)).astype(np.float32)
+    ks = rng.standard_normal((12, 2, 256)).astype(np.float32)
+    vs = rng.standard_normal((12, 2, 256)).astype(np.float32)
+    ys = [oracle.attention_step(qs[i], ks[i], vs[i], cache, reference=True) for i in range(12)]
+    out["attn_q"], out["attn_k"], out["attn_v"] = qs, ks, vs
+    out["attn_y_bits"] = np.stack(ys).view(np.uint32)
+    for case, dims, types, seed in (("plain", ATTN_PLAIN_DIMS, ATTN_PLAIN_TYPES, 20261206),
+                                    ("kq", ATTN_KQ_DIMS, ATTN_KQ_TYPES, 20261207)):
+        w, vec, cache, xs = attention_inputs(np.random.default_rng(seed), dims, types)
+        for n, (t, data) in w.items():
+            out[f"{case}_w_{n}"] = data
+            out[f"{case}_t_{n}"] = np.array([t])
+        for n, v in vec.items():
+            out[f"{case}_v_{n}"] = v
+        out[f"{case}_keys0"] = cache.keys.copy()
+        out[f"{case}_values0"] = cache.values.copy()
+        out[f"{case}_length0"] = np.array([cache.length])
+        out[f"{case}_x"] = xs
+        ys, traces, projs = [], [], []
+        own = cache.copy()
+        for i in range(xs.shape[0]):
+            overrides = None
+            if case == "kq":
+                # the oracle's projections of this step (its own cache carried alongside)
+                _, tr = oracle.attention_block_step(dims, w, vec, own, ATTN_POSITIONS[i], xs[i], threads=1)
+                overrides = {"q": tr["qfull"], "k": tr["k"], "v": tr["v"], "out": tr["branch"], "gate": tr["gate"],
+                             "up": tr["up"], "down": tr["ffn"]}
+                projs.append(np.concatenate([overrides[n] for n in oracle.ATTN_WEIGHTS]))
+            y, tr = oracle.ref_attention_block(dims, w, vec, cache, ATTN_POSITIONS[i], xs[i], overrides=overrides)
+            ys.append(y)
+            traces.append(np.concatenate([tr[n] for n in oracle.ATTN_TRACE]))
+        out[f"{case}_y_bits"] = np.stack(ys).view(np.uint32)
+        out[f"{case}_trace_bits"] = np.stack(traces).view(np.uint32)
+        out[f"{case}_keys_bits"] = cache.keys.view(np.uint32)
+        out[f"{case}_values_bits"] = cache.values.view(np.uint32)
+        if projs:
+            out[f"{case}_proj_bits"] = np.stack(projs).view(np.uint32)
+    return out
+
+
 def main() -> None:
     if not oracle.ref_available():
         raise SystemExit("oracle/_ref/libref.so is not built: run `make -C oracle ref` first")
@@ -262,7 +382,9 @@ def main() -> None:
     np.savez_compressed(OUT / "ref_random.npz", **random_vectors())
     np.savez_compressed(OUT / "ref_deltanet.npz", **deltanet_vectors())
     np.savez_compressed(OUT / "ref_block.npz", **block_vectors())
-    print("wrote", OUT / "ref_kat.json", OUT / "ref_random.npz", OUT / "ref_deltanet.npz", OUT / "ref_block.npz")
+    np.savez_compressed(OUT / "ref_attention.npz", **attention_vectors())
+    print("wrote", OUT / "ref_kat.json", OUT / "ref_random.npz", OUT / "ref_deltanet.npz", OUT / "ref_block.npz",
+          OUT / "ref_attention.npz")
 
 
 if __name__ == "__main__":
