@@ -248,6 +248,91 @@ typedef struct oq_deltanet_block {
 int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* block, float* conv_history_dev,
                      float* state_dev, const float* x_dev, float* y_dev, float* trace_dev);
 
+/* ------------------------------------------------------------------ full attention (decode) */
+/* A device KV cache in the reference's layout and semantics (oracle::runtime::KvCache,
+   include/oracle/runtime/hybrid_cache.hpp:37-74, src/runtime/hybrid_cache.cpp:131-207): keys
+   [capacity][kv_heads][key_dim] and values [capacity][kv_heads][value_dim], F32, in HBM; `size`
+   tokens are stored, appends write row `size`.  The length is kept on the host: a step enqueued
+   on a context counts as appended when it returns OQ_OK.
+   Create: zero capacity / heads / dimensions -> OQ_INVALID_ARGUMENT ("KV cache capacity must be
+   non-zero", "KV head count ...", "KV key dimension ...", "KV value dimension ...", :139-142);
+   the arrays are allocated and zeroed.  The cache belongs to the creating context. */
+typedef struct oq_kv_cache oq_kv_cache;
+int oq_kv_cache_create(oq_context* ctx, uint64_t capacity, uint64_t kv_heads, uint64_t key_dim,
+                       uint64_t value_dim, oq_kv_cache** out);
+void oq_kv_cache_release(oq_kv_cache* cache);
+uint64_t oq_kv_cache_size(const oq_kv_cache* cache);      /* KvCache::size */
+uint64_t oq_kv_cache_capacity(const oq_kv_cache* cache);  /* KvCache::capacity */
+/* KvCache::reset (hybrid_cache.cpp:171-175): length 0, arrays zeroed (on the context's stream) */
+int oq_kv_cache_reset(oq_kv_cache* cache);
+/* KvCache::truncate (:177-182): new_length > size -> OQ_INVALID_ARGUMENT ("KV cache truncate
+   must not grow state") */
+int oq_kv_cache_truncate(oq_kv_cache* cache, uint64_t new_length);
+/* No counterpart in the reference (its cache only grows by append): stores `length` token rows
+   [length][kv_heads][dim] from host memory and sets the length, e.g. to resume from keys and
+   values computed elsewhere.  length > capacity -> OQ_OVERFLOW ("KV cache capacity exceeded"). */
+int oq_kv_cache_load(oq_kv_cache* cache, const float* keys_host, const float* values_host, uint64_t length);
+/* the device arrays (row t, head h of keys at keys_dev + (t * kv_heads + h) * key_dim) */
+int oq_kv_cache_arrays(const oq_kv_cache* cache, float** keys_dev, float** values_dev);
+
+/* oracle::runtime::apply_qwen35_rope (src/runtime/reference_kernels.cpp:77-125) on
+   heads_dev [n_heads][head_dim] in place: frequency f < rotary_dim/2 turns the pair
+   (f, rotary_dim/2 + f) by coordinate * base^(-2f/rotary_dim), the coordinate being
+   position[1] (height) when f % 3 == 1 and f / 3 < sections[1], position[2] (width) when
+   f % 3 == 2 and f / 3 < sections[2], else position[0] (temporal).  Angles in double, cos and
+   sin rounded to F32, separate F32 multiplies and adds, as the reference.  The reference's checks
+   and messages (OQ_INVALID_ARGUMENT): rotary_dim non-zero, even, <= head_dim; base positive and
+   finite; sections non-negative and summing to rotary_dim / 2.  position: 3 values. */
+int oq_rope(oq_context* ctx, float* heads_dev, uint64_t n_heads, uint64_t head_dim, uint64_t rotary_dim,
+            const int32_t sections[4], float base, const uint64_t position[3]);
+
+/* oracle::runtime::causal_attention_step (src/runtime/reference_kernels.cpp:127-195): appends
+   k_dev [kv_heads][key_dim] and v_dev [kv_heads][value_dim] to the cache, then for every query
+   head h of q_dev [q_heads][key_dim] (KV head h / (q_heads / kv_heads)) writes to
+   out_dev [q_heads][value_dim] the softmax(q . k_t / sqrt(key_dim)) weighted sum of the cached
+   values, t over every stored token.  Checks as the reference: dimensions ("causal_attention_step
+   dimensions are incompatible", OQ_INVALID_ARGUMENT), then capacity ("KV cache capacity
+   exceeded", OQ_OVERFLOW), both before any device work.  F32 arithmetic split over token chunks
+   and merged with the usual max rescaling: outputs agree with the reference within 1e-4 of
+   sum_t p_t |v_t| (the reference sums doubles for the dot products and the denominator).  A
+   non-finite score yields non-finite outputs where the reference throws.  Device path limits:
+   key_dim == value_dim in {64, 128, 256}, q_heads / kv_heads <= 8; else OQ_INVALID_ARGUMENT. */
+int oq_attention_step(oq_context* ctx, const float* q_dev, uint64_t q_heads, const float* k_dev,
+                      const float* v_dev, oq_kv_cache* cache, float* out_dev);
+
+/* One Qwen3.5 full-attention decoder block at batch 1, chained on the device.  Replaces
+   oracle::runtime::execute_qwen35_attention_block_reference (src/runtime/qwen35_block.cpp:607-756,
+   with finish_block :326-352 and execute_mlp :296-324):
+     normed = RMSNorm(x) * input_norm
+     qfull, k, v = projections of normed        (qfull: per head D query values, D gate values)
+     q = rope(RMSNorm_head(query) * q_norm),  k = rope(RMSNorm_head(k) * k_norm)
+     pregate = causal attention step of (q, k, v) over the cache (appends k, v)
+     gated = pregate * sigmoid(gate);  branch = out_proj(gated);  resid = x + branch
+     y = resid + down(SiLU(gate(post)) * up(post)),  post = RMSNorm(resid) * post_norm
+   Projections as oq_deltanet_step's.  trace_dev, if not NULL, receives (F32, packed; Q = Hq*D,
+   KV = Hkv*D): qfull[2Q] k[KV] v[KV] qcur[Q] kcur[KV] pregate[Q] gate_s[Q] gated[Q] branch[E]
+   resid[E] post[E] gate[F] up[F] act[F] ffn[E] -- the reference's trace tensors Qcur_full,
+   Kcur_projected, Vcur_projected, Qcur, Kcur, attn_pregate, gate_sigmoid, attn_gated,
+   attn_output, attn_residual, attn_post_norm, ffn_gate, ffn_up, ffn_swiglu, ffn_out.
+   Checks: dimensions, cache geometry ("Qwen3.5 attention cache dimensions do not match the
+   manifest"), the RoPE checks above, weight shapes, capacity -- before any device work. */
+typedef struct oq_attention_block {
+    uint64_t embedding; /* E */
+    uint64_t q_heads;   /* Hq, a multiple of kv_heads */
+    uint64_t kv_heads;  /* Hkv */
+    uint64_t head_dim;  /* D = key_length = value_length */
+    uint64_t ffn;       /* F */
+    uint64_t rope_dim;  /* rotary dimension (<= D) */
+    int32_t rope_sections[4];
+    float rope_base;
+    float eps;          /* manifest attention_rms_epsilon */
+    const oq_weight *q, *k, *v, *out, *gate, *up, *down;
+    /* F32 device vectors: input_norm[E], q_norm[D], k_norm[D], post_norm[E] */
+    const float *input_norm, *q_norm, *k_norm, *post_norm;
+} oq_attention_block;
+int oq_attention_block_step(oq_context* ctx, const oq_attention_block* block, oq_kv_cache* cache,
+                            const uint64_t position[3], const float* x_dev, float* y_dev, float* trace_dev);
+
 /* No counterpart in the reference.  oq_deltanet_step for callers that cannot allocate device
    memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
    same arguments, checks, kernels and results, but it allocates nothing -- the block's

@@ -280,6 +280,31 @@ class Context:
                    x.ptr, y.ptr, trace.ptr if trace is not None else None)
 
     # timing / graphs
+    def kv_cache(self, capacity: int, kv_heads: int, key_dim: int, value_dim: int) -> "KvCache":
+        """A device KV cache (oq_kv_cache_create)."""
+        h = C.c_void_p()
+        self._call(self.lib.oq_kv_cache_create, self.h, capacity, kv_heads, key_dim, value_dim, C.byref(h))
+        return KvCache(self, h.value)
+
+    def rope(self, heads: DeviceBuffer, n_heads: int, head_dim: int, rotary_dim: int, sections, base: float,
+             position) -> None:
+        """apply_qwen35_rope on heads [n_heads][head_dim] in place (oq_rope)."""
+        sec = (C.c_int32 * 4)(*[int(v) for v in sections])
+        pos = (C.c_uint64 * 3)(*[int(v) for v in position])
+        self._call(self.lib.oq_rope, self.h, heads.ptr, n_heads, head_dim, rotary_dim, sec, float(base), pos)
+
+    def attention_step(self, q: DeviceBuffer, q_heads: int, k: DeviceBuffer, v: DeviceBuffer, cache: "KvCache",
+                       out: DeviceBuffer) -> None:
+        """causal_attention_step: appends (k, v) to the cache and attends (oq_attention_step)."""
+        self._call(self.lib.oq_attention_step, self.h, q.ptr, q_heads, k.ptr, v.ptr, cache.h, out.ptr)
+
+    def attention_block_step(self, block: "AttentionBlockWeights", cache: "KvCache", position, x: DeviceBuffer,
+                             y: DeviceBuffer, trace: DeviceBuffer | None = None) -> None:
+        """One full-attention decode block step (oq_attention_block_step); appends to the cache."""
+        pos = (C.c_uint64 * 3)(*[int(v) for v in position])
+        self._call(self.lib.oq_attention_block_step, self.h, C.byref(block.desc), cache.h, pos, x.ptr, y.ptr,
+                   trace.ptr if trace is not None else None)
+
     def timer_start(self) -> None:
         self._call(self.lib.oq_timer_start, self.h)
 
@@ -385,6 +410,92 @@ class DeltaNetBlockWeights:
 
     def weight_bytes(self) -> int:
         """GGML bytes of the eight projections (what one block step streams)."""
+        return sum(ggml_row_byte_size(w.ne0, w.type) * w.ne1 for w in self.weights.values())
+
+    def release(self) -> None:
+        for w in self.weights.values():
+            w.release()
+        for v in self.vectors.values():
+            v.free()
+
+
+class KvCache:
+    """A device KV cache in the reference's layout (oq_kv_cache): keys [capacity][kv_heads][key_dim],
+    values [capacity][kv_heads][value_dim], F32 in HBM."""
+
+    def __init__(self, ctx: Context, handle: int):
+        self.ctx = ctx
+        self.h = handle
+        self.capacity = int(ctx.lib.oq_kv_cache_capacity(handle))
+        k, v = C.c_void_p(), C.c_void_p()
+        ctx._call(ctx.lib.oq_kv_cache_arrays, handle, C.byref(k), C.byref(v))
+        self.keys_ptr, self.values_ptr = k.value, v.value
+
+    def __len__(self) -> int:
+        return int(self.ctx.lib.oq_kv_cache_size(self.h))
+
+    def reset(self) -> None:
+        self.ctx._call(self.ctx.lib.oq_kv_cache_reset, self.h)
+
+    def truncate(self, new_length: int) -> None:
+        self.ctx._call(self.ctx.lib.oq_kv_cache_truncate, self.h, new_length)
+
+    def _view(self, ptr: int, width: int) -> DeviceBuffer:
+        b = DeviceBuffer.__new__(DeviceBuffer)  # a view: never freed through this object
+        b.ctx, b.ptr, b.nbytes = self.ctx, ptr, self.capacity * width * 4
+        return b
+
+    def download(self, kv_heads: int, key_dim: int, value_dim: int) -> tuple[np.ndarray, np.ndarray]:
+        """(keys, values) as [capacity][kv_heads][dim] arrays."""
+        kb = self._view(self.keys_ptr, kv_heads * key_dim).download(np.float32)
+        vb = self._view(self.values_ptr, kv_heads * value_dim).download(np.float32)
+        return kb.reshape(self.capacity, kv_heads, key_dim), vb.reshape(self.capacity, kv_heads, value_dim)
+
+    def load(self, keys: np.ndarray, values: np.ndarray, length: int) -> None:
+        """Stores the first `length` token rows of keys / values and sets the length (oq_kv_cache_load)."""
+        k = np.ascontiguousarray(keys, dtype=np.float32)
+        v = np.ascontiguousarray(values, dtype=np.float32)
+        self.ctx._call(self.ctx.lib.oq_kv_cache_load, self.h, k.ctypes.data, v.ctypes.data, length)
+
+    def release(self) -> None:
+        if self.h:
+            self.ctx.lib.oq_kv_cache_release(self.h)
+            self.h = None
+
+
+ATTENTION_WEIGHTS = ("q", "k", "v", "out", "gate", "up", "down")
+ATTENTION_VECTORS = ("input_norm", "q_norm", "k_norm", "post_norm")
+
+
+class AttentionBlockWeights:
+    """Device-resident weights of one full-attention block: the seven projections uploaded once
+    (weights[name] = (ggml type, host bytes)) and the F32 vectors copied to HBM."""
+
+    def __init__(self, ctx: Context, dims: dict, weights: dict, vectors: dict):
+        from ._lib import AttentionBlock
+        E, F, Hq, Hkv, D = (int(dims[k]) for k in ("embedding", "ffn", "q_heads", "kv_heads", "head_dim"))
+        Q, KV = Hq * D, Hkv * D
+        shapes = {"q": (E, 2 * Q), "k": (E, KV), "v": (E, KV), "out": (Q, E), "gate": (E, F), "up": (E, F),
+                  "down": (F, E)}
+        self.weights = {n: ctx.upload(weights[n][0], shapes[n][0], shapes[n][1], weights[n][1])
+                        for n in ATTENTION_WEIGHTS}
+        self.vectors = {n: ctx.to_device(np.ascontiguousarray(vectors[n], dtype=np.float32))
+                        for n in ATTENTION_VECTORS}
+        d = AttentionBlock()
+        for k in ("embedding", "q_heads", "kv_heads", "head_dim", "ffn", "rope_dim"):
+            setattr(d, k, int(dims[k]))
+        for i, v in enumerate(dims["rope_sections"]):
+            d.rope_sections[i] = int(v)
+        d.rope_base = float(dims["rope_base"])
+        d.eps = float(dims["eps"])
+        for n in ATTENTION_WEIGHTS:
+            setattr(d, n, self.weights[n].h)
+        for n in ATTENTION_VECTORS:
+            setattr(d, n, self.vectors[n].ptr)
+        self.desc = d
+        self.dims = dict(dims)
+
+    def weight_bytes(self) -> int:
         return sum(ggml_row_byte_size(w.ne0, w.type) * w.ne1 for w in self.weights.values())
 
     def release(self) -> None:

@@ -60,6 +60,17 @@ SIGNATURES = [
     ("oq_deltanet_step", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     ("oq_deltanet_step_noalloc", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     ("oq_deltanet_noalloc_capacity", _U64, []),
+    ("oq_kv_cache_create", C.c_int, [_P, _U64, _U64, _U64, _U64, C.POINTER(_P)]),
+    ("oq_kv_cache_release", None, [_P]),
+    ("oq_kv_cache_size", _U64, [_P]),
+    ("oq_kv_cache_capacity", _U64, [_P]),
+    ("oq_kv_cache_reset", C.c_int, [_P]),
+    ("oq_kv_cache_truncate", C.c_int, [_P, _U64]),
+    ("oq_kv_cache_arrays", C.c_int, [_P, C.POINTER(_P), C.POINTER(_P)]),
+    ("oq_kv_cache_load", C.c_int, [_P, _P, _P, _U64]),
+    ("oq_rope", C.c_int, [_P, _P, _U64, _U64, _U64, _P, C.c_float, _P]),
+    ("oq_attention_step", C.c_int, [_P, _P, _U64, _P, _P, _P, _P]),
+    ("oq_attention_block_step", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     ("oq_timer_start", C.c_int, [_P]),
     ("oq_timer_stop", C.c_int, [_P, C.POINTER(C.c_float)]),
     ("oq_capture_begin", C.c_int, [_P]),
@@ -76,6 +87,14 @@ class DeltaNetBlock(C.Structure):
                                           "conv_kernel", "ffn")] + [("eps", C.c_float)] + \
                [(n, C.c_void_p) for n in ("qkv", "z", "beta", "alpha", "out", "gate", "up", "down")] + \
                [(n, C.c_void_p) for n in ("input_norm", "conv_weight", "dt_bias", "decay", "out_norm", "post_norm")]
+
+
+class AttentionBlock(C.Structure):
+    """oq_attention_block (include/oq.h)."""
+    _fields_ = [(n, C.c_uint64) for n in ("embedding", "q_heads", "kv_heads", "head_dim", "ffn", "rope_dim")] + \
+               [("rope_sections", C.c_int32 * 4), ("rope_base", C.c_float), ("eps", C.c_float)] + \
+               [(n, C.c_void_p) for n in ("q", "k", "v", "out", "gate", "up", "down")] + \
+               [(n, C.c_void_p) for n in ("input_norm", "q_norm", "k_norm", "post_norm")]
 
 
 class TensorDesc(C.Structure):

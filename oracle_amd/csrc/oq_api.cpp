@@ -823,3 +823,394 @@ void oq_graph_destroy(oq_graph* g) {
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- full attention (decode)
+
+struct oq_kv_cache {
+    oq_context* ctx = nullptr;
+    int device = 0;
+    uint64_t capacity = 0, kv_heads = 0, key_dim = 0, value_dim = 0, length = 0;
+    float* keys = nullptr;
+    float* values = nullptr;
+};
+
+namespace {
+
+// apply_qwen35_rope's checks (reference_kernels.cpp:80-99), in its order
+int rope_params(oq_context* ctx, uint64_t head_dim, uint64_t rotary_dim, const int32_t* sections, float base,
+                const uint64_t* position, oq::RopeParams& p) {
+    if (!sections || !position) return fail(ctx, OQ_INVALID_ARGUMENT, "null RoPE sections or position");
+    if (rotary_dim == 0 || rotary_dim % 2 != 0 || rotary_dim > head_dim) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "RoPE dimension must be non-zero, even, and within head width");
+    }
+    if (!(base > 0.0f) || !std::isfinite(base)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "RoPE frequency base must be positive and finite");
+    }
+    int64_t sum = 0;
+    for (int i = 0; i < 4; ++i) {
+        if (sections[i] < 0) return fail(ctx, OQ_INVALID_ARGUMENT, "RoPE dimension sections must be non-negative");
+        sum += sections[i];
+    }
+    if (sum != (int64_t)(rotary_dim / 2)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "RoPE dimension sections must sum to half the rotary dimension");
+    }
+    if (rotary_dim > 0xFFFFFFFFull) return fail(ctx, OQ_OVERFLOW, "RoPE dimension too large");
+    p.rotary_dim = (uint32_t)rotary_dim;
+    p.sec1 = (uint32_t)sections[1];
+    p.sec2 = (uint32_t)sections[2];
+    p.base = base;
+    p.pos[0] = position[0];
+    p.pos[1] = position[1];
+    p.pos[2] = position[2];
+    return OQ_OK;
+}
+
+int check_cache(oq_context* ctx, const oq_kv_cache* c) {
+    if (!c) return fail(ctx, OQ_INVALID_ARGUMENT, "null KV cache");
+    if (c->device != ctx->device) return fail(ctx, OQ_INVALID_ARGUMENT, "KV cache lives on another device");
+    return OQ_OK;
+}
+
+// the attention launch over a cache whose new token (index T - 1 = cache->length) is given by
+// new_k / new_v, or already stored (both null); the partials go to `part`
+int attention_shape(oq_context* ctx, const oq_kv_cache* c, uint64_t q_heads, oq::AttnLaunch& L) {
+    const uint64_t rep = q_heads / c->kv_heads;
+    if (c->key_dim != c->value_dim || !oq::attention_dims_supported(c->key_dim, rep)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT,
+                    "attention device path needs key_dim == value_dim in {64, 128, 256} and at most 8 query heads per "
+                    "KV head");
+    }
+    const uint64_t T = c->length + 1;
+    uint32_t chunk = 0, nchunks = 0;
+    oq::attention_plan(T, c->kv_heads, chunk, nchunks);
+    if (nchunks > oq::kAttnMaxChunks || T > 0xFFFFFFFFull || c->kv_heads > 0xFFFF) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "attention device path supports at most 8388608 cached tokens");
+    }
+    L.T = (uint32_t)T;
+    L.Hkv = (uint32_t)c->kv_heads;
+    L.rep = (uint32_t)rep;
+    L.D = (uint32_t)c->key_dim;
+    L.chunk = chunk;
+    L.nchunks = nchunks;
+    L.scale = 1.0f / std::sqrt((float)c->key_dim);  // reference_kernels.cpp:158
+    L.keys = c->keys;
+    L.values = c->values;
+    return OQ_OK;
+}
+
+// Workspace of one attention block step: the 15 trace fields, the normalised input and the
+// attention partials, each padded to 64 floats.
+struct AttnLayout {
+    uint64_t sizes[17];
+    uint64_t off[17];
+    uint64_t total_floats;
+};
+
+AttnLayout attn_layout(const oq_attention_block* b, uint32_t nchunks) {
+    const uint64_t E = b->embedding, D = b->head_dim, F = b->ffn, Q = b->q_heads * D, KV = b->kv_heads * D;
+    const uint64_t P = oq::attention_partial_floats(b->kv_heads, b->q_heads / b->kv_heads, D, nchunks);
+    AttnLayout l{{2 * Q, KV, KV, Q, KV, Q, Q, Q, E, E, E, F, F, F, E, E, P}, {}, 0};
+    for (int i = 0; i < 17; ++i) {
+        l.off[i] = l.total_floats;
+        l.total_floats += (l.sizes[i] + 63) & ~uint64_t(63);
+    }
+    return l;
+}
+
+int check_attn_weight(oq_context* ctx, const oq_weight* w, uint64_t ne0, uint64_t ne1, const char* name) {
+    if (int rc = check_weight(ctx, w)) return fail(ctx, rc, std::string("attention block weight ") + name + ": " + ctx->error);
+    if (w->m.k != ne0 || w->m.n != ne1) {
+        return fail(ctx, OQ_INVALID_ARGUMENT,
+                    std::string("attention block weight ") + name + " has shape [" + std::to_string(w->m.k) + ", " +
+                        std::to_string(w->m.n) + "], expected [" + std::to_string(ne0) + ", " + std::to_string(ne1) + "]");
+    }
+    return OQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int oq_kv_cache_create(oq_context* ctx, uint64_t capacity, uint64_t kv_heads, uint64_t key_dim, uint64_t value_dim,
+                       oq_kv_cache** out) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (!out) return fail(ctx, OQ_INVALID_ARGUMENT, "null output handle");
+    *out = nullptr;
+    // KvCache::KvCache (hybrid_cache.cpp:131-152)
+    if (capacity == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "KV cache capacity must be non-zero");
+    if (kv_heads == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "KV head count must be non-zero");
+    if (key_dim == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "KV key dimension must be non-zero");
+    if (value_dim == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "KV value dimension must be non-zero");
+    const uint64_t lim = UINT64_MAX / sizeof(float);
+    if (kv_heads > lim / capacity || key_dim > lim / (capacity * kv_heads) ||
+        value_dim > lim / (capacity * kv_heads)) {
+        return fail(ctx, OQ_OVERFLOW, "KV cache size overflow");
+    }
+    if (ctx->capturing) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be created during graph capture");
+    const uint64_t kb = capacity * kv_heads * key_dim * sizeof(float);
+    const uint64_t vb = capacity * kv_heads * value_dim * sizeof(float);
+    OQ_HIP(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    oq_kv_cache* c = new oq_kv_cache;
+    c->ctx = ctx;
+    c->device = ctx->device;
+    c->capacity = capacity;
+    c->kv_heads = kv_heads;
+    c->key_dim = key_dim;
+    c->value_dim = value_dim;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&c->keys), kb);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->values), vb);
+    if (e == hipSuccess) e = hipMemsetAsync(c->keys, 0, kb, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->values, 0, vb, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        const int rc = hip_fail(ctx, e, "KV cache allocation");
+        oq_kv_cache_release(c);
+        return rc;
+    }
+    *out = c;
+    return OQ_OK;
+}
+
+void oq_kv_cache_release(oq_kv_cache* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->ctx && c->ctx->stream) (void)hipStreamSynchronize(c->ctx->stream);
+    if (c->keys) (void)hipFree(c->keys);
+    if (c->values) (void)hipFree(c->values);
+    delete c;
+}
+
+uint64_t oq_kv_cache_size(const oq_kv_cache* c) { return c ? c->length : 0; }
+uint64_t oq_kv_cache_capacity(const oq_kv_cache* c) { return c ? c->capacity : 0; }
+
+int oq_kv_cache_reset(oq_kv_cache* c) {
+    if (!c) return fail(nullptr, OQ_INVALID_ARGUMENT, "null KV cache");
+    oq_context* ctx = c->ctx;
+    if (ctx->capturing) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be reset during graph capture");
+    c->length = 0;
+    OQ_HIP(ctx, hipMemsetAsync(c->keys, 0, c->capacity * c->kv_heads * c->key_dim * sizeof(float), ctx->stream),
+           "KV cache reset");
+    OQ_HIP(ctx, hipMemsetAsync(c->values, 0, c->capacity * c->kv_heads * c->value_dim * sizeof(float), ctx->stream),
+           "KV cache reset");
+    return OQ_OK;
+}
+
+int oq_kv_cache_truncate(oq_kv_cache* c, uint64_t new_length) {
+    if (!c) return fail(nullptr, OQ_INVALID_ARGUMENT, "null KV cache");
+    if (new_length > c->length) return fail(c->ctx, OQ_INVALID_ARGUMENT, "KV cache truncate must not grow state");
+    c->length = new_length;
+    return OQ_OK;
+}
+
+int oq_kv_cache_load(oq_kv_cache* c, const float* keys, const float* values, uint64_t length) {
+    if (!c) return fail(nullptr, OQ_INVALID_ARGUMENT, "null KV cache");
+    oq_context* ctx = c->ctx;
+    if (length > c->capacity) return fail(ctx, OQ_OVERFLOW, "KV cache capacity exceeded");
+    if (length > 0 && (!keys || !values)) return fail(ctx, OQ_INVALID_ARGUMENT, "null cache rows");
+    if (ctx->capturing) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be loaded during graph capture");
+    if (length > 0) {
+        OQ_HIP(ctx, hipMemcpyAsync(c->keys, keys, length * c->kv_heads * c->key_dim * sizeof(float),
+                                   hipMemcpyHostToDevice, ctx->stream), "KV cache load");
+        OQ_HIP(ctx, hipMemcpyAsync(c->values, values, length * c->kv_heads * c->value_dim * sizeof(float),
+                                   hipMemcpyHostToDevice, ctx->stream), "KV cache load");
+        OQ_HIP(ctx, hipStreamSynchronize(ctx->stream), "KV cache load");
+    }
+    c->length = length;
+    return OQ_OK;
+}
+
+int oq_kv_cache_arrays(const oq_kv_cache* c, float** keys_dev, float** values_dev) {
+    if (!c) return fail(nullptr, OQ_INVALID_ARGUMENT, "null KV cache");
+    if (keys_dev) *keys_dev = c->keys;
+    if (values_dev) *values_dev = c->values;
+    return OQ_OK;
+}
+
+int oq_rope(oq_context* ctx, float* heads, uint64_t n_heads, uint64_t head_dim, uint64_t rotary_dim,
+            const int32_t sections[4], float base, const uint64_t position[3]) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    oq::RopeParams p{};
+    if (int rc = rope_params(ctx, head_dim, rotary_dim, sections, base, position, p)) return rc;
+    if (n_heads == 0) return OQ_OK;
+    if (!heads) return fail(ctx, OQ_INVALID_ARGUMENT, "null heads");
+    if (!aligned(heads, 4)) return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer");
+    if (n_heads > 0x7FFFFFFF || head_dim > 0xFFFFFFFFull) return fail(ctx, OQ_OVERFLOW, "RoPE tensor too large");
+    return launch_rc(ctx, oq::launch_rope(heads, n_heads, head_dim, p, ctx->stream), "rope");
+}
+
+int oq_attention_step(oq_context* ctx, const float* q, uint64_t q_heads, const float* k, const float* v,
+                      oq_kv_cache* cache, float* out) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (int rc = check_cache(ctx, cache)) return rc;
+    if (!q || !k || !v || !out) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    // causal_attention_step (reference_kernels.cpp:139-150), then KvCache::append's capacity check
+    if (q_heads == 0 || q_heads % cache->kv_heads != 0) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "causal_attention_step dimensions are incompatible");
+    }
+    if (cache->length >= cache->capacity) return fail(ctx, OQ_OVERFLOW, "KV cache capacity exceeded");
+    oq::AttnLaunch L{};
+    if (int rc = attention_shape(ctx, cache, q_heads, L)) return rc;
+    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "attention buffers must be 16-byte aligned");
+    }
+    const uint64_t pf = oq::attention_partial_floats(L.Hkv, L.rep, L.D, L.nchunks);
+    if (int rc = ensure_scratch(ctx, pf * sizeof(float))) return rc;
+    L.q = q;
+    L.new_k = k;
+    L.new_v = v;
+    L.part = static_cast<float*>(ctx->scratch.ptr);
+    L.out = out;
+    const int rc = launch_rc(ctx, oq::launch_attention(L, ctx->stream), "attention_step");
+    if (rc == OQ_OK) cache->length += 1;
+    return rc;
+}
+
+int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_cache* cache,
+                            const uint64_t position[3], const float* x, float* y, float* trace) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (!b || !x || !y) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    if (int rc = check_cache(ctx, cache)) return rc;
+    const uint64_t E = b->embedding, Hq = b->q_heads, Hkv = b->kv_heads, D = b->head_dim, F = b->ffn;
+    if (E == 0 || Hq == 0 || Hkv == 0 || D == 0 || F == 0 || Hq % Hkv != 0) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 attention block dimensions are incompatible");
+    }
+    // execute_qwen35_attention_block_reference (qwen35_block.cpp:621-625)
+    if (cache->kv_heads != Hkv || cache->key_dim != D || cache->value_dim != D) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 attention cache dimensions do not match the manifest");
+    }
+    if (!(b->eps > 0.0f) || !std::isfinite(b->eps)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 RMSNorm epsilon must be positive and finite");
+    }
+    oq::RopeParams rp{};
+    if (int rc = rope_params(ctx, D, b->rope_dim, b->rope_sections, b->rope_base, position, rp)) return rc;
+    if (E > 0x7FFFFFFF || F > 0x7FFFFFFF || Hq * D > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "block too large");
+    const uint64_t Q = Hq * D, KV = Hkv * D;
+    if (int rc = check_attn_weight(ctx, b->q, E, 2 * Q, "q")) return rc;
+    if (int rc = check_attn_weight(ctx, b->k, E, KV, "k")) return rc;
+    if (int rc = check_attn_weight(ctx, b->v, E, KV, "v")) return rc;
+    if (int rc = check_attn_weight(ctx, b->out, Q, E, "out")) return rc;
+    if (int rc = check_attn_weight(ctx, b->gate, E, F, "gate")) return rc;
+    if (int rc = check_attn_weight(ctx, b->up, E, F, "up")) return rc;
+    if (int rc = check_attn_weight(ctx, b->down, F, E, "down")) return rc;
+    if (!b->input_norm || !b->q_norm || !b->k_norm || !b->post_norm) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "null block vector");
+    }
+    if (!aligned(x, 16) || !aligned(y, 4)) return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer");
+    if (cache->length >= cache->capacity) return fail(ctx, OQ_OVERFLOW, "KV cache capacity exceeded");
+    oq::AttnLaunch L{};
+    if (int rc = attention_shape(ctx, cache, Hq, L)) return rc;
+    const AttnLayout lay = attn_layout(b, L.nchunks);
+    if (int rc = ensure_work(ctx, lay.total_floats * sizeof(float))) return rc;
+    float* ws = static_cast<float*>(ctx->work.ptr);
+    const uint64_t* off = lay.off;
+    float *qfull = ws + off[0], *kp = ws + off[1], *vp = ws + off[2], *qcur = ws + off[3], *kcur = ws + off[4],
+          *pregate = ws + off[5], *gate_s = ws + off[6], *gated = ws + off[7], *branch = ws + off[8],
+          *resid = ws + off[9], *post = ws + off[10], *gate = ws + off[11], *up = ws + off[12], *act = ws + off[13],
+          *ffn = ws + off[14], *normed = ws + off[15], *part = ws + off[16];
+    hipStream_t s = ctx->stream;
+    hipError_t e = hipSuccess;
+
+    oq::BlockGemv in{}, outp{}, ffn_in{}, down{};
+    in.nmat = 3;
+    in.mat[0] = b->q->m;
+    in.mat[1] = b->k->m;
+    in.mat[2] = b->v->m;
+    in.row_end[0] = (uint32_t)(2 * Q);
+    in.row_end[1] = (uint32_t)(2 * Q + KV);
+    in.row_end[2] = (uint32_t)(2 * Q + 2 * KV);
+    in.x = x;
+    in.norm_w = b->input_norm;
+    in.eps = b->eps;
+    in.raw[0] = qfull;
+    in.raw[1] = kp;
+    in.raw[2] = vp;
+    outp.nmat = 1;
+    outp.mat[0] = b->out->m;
+    outp.row_end[0] = (uint32_t)E;
+    outp.x = gated;
+    outp.raw[0] = branch;
+    outp.add = x;
+    outp.sum_out = resid;
+    ffn_in.nmat = 2;
+    ffn_in.mat[0] = b->gate->m;
+    ffn_in.mat[1] = b->up->m;
+    ffn_in.row_end[0] = (uint32_t)F;
+    ffn_in.row_end[1] = (uint32_t)(2 * F);
+    ffn_in.x = resid;
+    ffn_in.norm_w = b->post_norm;
+    ffn_in.eps = b->eps;
+    ffn_in.norm_out = post;
+    ffn_in.raw[0] = gate;
+    ffn_in.raw[1] = up;
+    ffn_in.act = act;
+    down.nmat = 1;
+    down.mat[0] = b->down->m;
+    down.row_end[0] = (uint32_t)E;
+    down.x = act;
+    down.raw[0] = ffn;
+    down.add = resid;
+    down.sum_out = y;
+
+    oq::AttnPrep prep{};
+    prep.qfull = qfull;
+    prep.kp = kp;
+    prep.vp = vp;
+    prep.q_norm = b->q_norm;
+    prep.k_norm = b->k_norm;
+    prep.eps = b->eps;
+    prep.Hq = (uint32_t)Hq;
+    prep.Hkv = (uint32_t)Hkv;
+    prep.D = (uint32_t)D;
+    prep.rope = rp;
+    prep.qcur = qcur;
+    prep.kcur = kcur;
+    prep.key_slot = cache->keys + cache->length * KV;
+    prep.value_slot = cache->values + cache->length * KV;
+    L.q = qcur;
+    L.part = part;
+    L.out = pregate;
+    L.gate = qfull + D;
+    L.gate_stride = (uint32_t)(2 * D);
+    L.gate_s = gate_s;
+    L.gated = gated;
+
+    const bool even = E % 2 == 0 && F % 2 == 0;
+    const bool fused_in = knob_flag(oq::kBlockFused, true) && even && oq::gemv_block_supported(in);
+    const bool fused_tail = knob_flag(oq::kBlockFused, true) && even && oq::gemv_block_supported(outp) &&
+                            oq::gemv_block_supported(ffn_in) && oq::gemv_block_supported(down);
+    if (fused_in) {
+        e = oq::launch_gemv_block(oq::kBlockIn, in, s);
+    } else {
+        e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s);
+        if (e == hipSuccess) e = block_project(b->q, normed, qfull, s);
+        if (e == hipSuccess) e = block_project(b->k, normed, kp, s);
+        if (e == hipSuccess) e = block_project(b->v, normed, vp, s);
+    }
+    if (e == hipSuccess) e = oq::launch_attention_prep(prep, s);
+    if (e == hipSuccess) e = oq::launch_attention(L, s);
+    if (fused_tail) {
+        if (e == hipSuccess) e = oq::launch_gemv_block(oq::kBlockAdd, outp, s);
+        if (e == hipSuccess) e = oq::launch_gemv_block(oq::kBlockFfn, ffn_in, s);
+        if (e == hipSuccess) e = oq::launch_gemv_block(oq::kBlockAdd, down, s);
+    } else {
+        if (e == hipSuccess) e = block_project(b->out, gated, branch, s);
+        if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s);
+        if (e == hipSuccess) e = block_project(b->gate, post, gate, s);
+        if (e == hipSuccess) e = block_project(b->up, post, up, s);
+        if (e == hipSuccess) e = oq::launch_swiglu(gate, up, F, act, s);
+        if (e == hipSuccess) e = block_project(b->down, act, ffn, s);
+        if (e == hipSuccess) e = oq::launch_add(resid, ffn, E, y, s);
+    }
+    if (e == hipSuccess && trace) {
+        uint64_t t = 0;
+        for (int i = 0; i < 15 && e == hipSuccess; ++i) {
+            e = hipMemcpyAsync(trace + t, ws + off[i], lay.sizes[i] * sizeof(float), hipMemcpyDeviceToDevice, s);
+            t += lay.sizes[i];
+        }
+    }
+    const int rc = launch_rc(ctx, e, "attention_block_step");
+    if (rc == OQ_OK) cache->length += 1;
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,489 @@
+// Full-attention decode for gfx950: RoPE / MRoPE, the attention block's per-head preparation and
+// single-token GQA attention over an F32 KV cache in HBM.
+//
+// Attention (reference_kernels.cpp:127-195) is split over the token axis, flash-decoding style:
+//   chunk kernel   one workgroup per (KV head g, chunk of tokens), 4 waves.  All rep = q_heads /
+//                  kv_heads query heads of g share each key and value row, so K and V are read
+//                  from HBM once per step whatever the group size.
+//                  scores: 16 lanes per token, each lane holding D/16 key values (four 16-lane
+//                    groups per wave, 256 contiguous bytes per group and load); the rep query
+//                    heads' matching slices sit in registers; F32 products reduced over the 16
+//                    lanes; s = dot * 1/sqrt(D) kept in LDS
+//                  softmax: per head the chunk's max m_c, p = exp(s - m_c) in place, l_c = sum p
+//                  values: each wave takes every fourth token, lane i owning D/64 value columns,
+//                    o[h] += p[h][t] * v_t for the rep heads; the four waves' sums are added in LDS
+//                  -> o_c [rep][D], (m_c, l_c) [rep] for the chunk
+//   merge kernel   one 1024-thread workgroup per query head: M = max_c m_c, w_c = exp(m_c - M),
+//                  out = sum_c w_c o_c / sum_c w_c l_c; for the decoder block also the output gate
+//                  (gate_s = sigmoid(gate), gated = out * gate_s, qwen35_block.cpp:734-741)
+// The reference sums the dot products and the softmax denominator in double and the weighted
+// values in F32 in token order; here everything is F32 in the order above, so results agree
+// within a small multiple of F32 rounding (tested against 1e-4 of sum_t p_t |v_t|).
+//
+// The append (KvCache::append, hybrid_cache.cpp:154-169) is folded in: when new_k / new_v are
+// given, the workgroup whose chunk holds the new token reads it from there and stores it into
+// cache row T - 1; nothing else reads that row during the step.
+#include "oq_common.h"
+
+namespace oq {
+
+namespace {
+
+constexpr int kAttnWaves = 4;
+constexpr int kAttnThreads = kAttnWaves * 64;
+constexpr uint32_t kTokStep = kAttnWaves * 4;  // tokens per workgroup pass in the score phase
+constexpr uint32_t kMaxChunk = 1024;
+constexpr int kMergeThreads = 1024;
+
+struct ChunkArgs {
+    const float* q;       // [Hq][D]
+    float* keys;          // [capacity][Hkv][D]
+    float* values;        // [capacity][Hkv][D]
+    const float* new_k;   // [Hkv][D] or null
+    const float* new_v;
+    uint32_t T, Hkv, rep, chunk, nchunks;
+    float scale;
+    float* part_o;        // [Hkv][nchunks][rep][D]
+    float* part_ml;       // [Hkv][nchunks][rep][2]
+};
+
+struct MergeArgs {
+    const float* part_o;
+    const float* part_ml;
+    uint32_t Hkv, rep, nchunks;
+    float* out;           // [Hq][D]
+    const float* gate;    // gate of head h at gate + h * gate_stride, or null
+    uint32_t gate_stride;
+    float* gate_s;        // [Hq][D]
+    float* gated;         // [Hq][D]
+};
+
+template <int N>
+struct Vec;
+template <>
+struct Vec<1> {
+    using type = float;
+    OQ_DEVICE static void unpack(type v, float* o) { o[0] = v; }
+};
+template <>
+struct Vec<2> {
+    using type = float2;
+    OQ_DEVICE static void unpack(type v, float* o) {
+        o[0] = v.x;
+        o[1] = v.y;
+    }
+};
+template <>
+struct Vec<4> {
+    using type = float4;
+    OQ_DEVICE static void unpack(type v, float* o) {
+        o[0] = v.x;
+        o[1] = v.y;
+        o[2] = v.z;
+        o[3] = v.w;
+    }
+};
+
+OQ_DEVICE float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <int D, int REP>
+__global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs a) {
+    constexpr int NV = D / 64;  // float4 of one key row per lane (16 lanes per row)
+    constexpr int VW = D / 64;  // value columns per lane (64 lanes per row)
+    using VT = typename Vec<VW>::type;
+    extern __shared__ __align__(16) float lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t g = blockIdx.x / a.nchunks;
+    const uint32_t c = blockIdx.x - g * a.nchunks;
+    const uint32_t c0 = c * a.chunk;
+    const uint32_t c1 = min(c0 + a.chunk, a.T);
+    const uint32_t n = c1 - c0;
+    const uint32_t rep = a.rep;
+    const uint32_t last = a.T - 1;
+    float* sc = lds;  // [rep][chunk] scores, then probabilities
+
+    auto key_row = [&](uint32_t t) -> const float* {
+        if (a.new_k != nullptr && t == last) return a.new_k + (uint64_t)g * D;
+        return a.keys + ((uint64_t)t * a.Hkv + g) * D;
+    };
+    auto value_row = [&](uint32_t t) -> const float* {
+        if (a.new_v != nullptr && t == last) return a.new_v + (uint64_t)g * D;
+        return a.values + ((uint64_t)t * a.Hkv + g) * D;
+    };
+
+    // the append: the chunk holding the new token stores its key and value row
+    if (a.new_k != nullptr && c1 == a.T) {
+        for (uint32_t i = threadIdx.x; i < (uint32_t)D; i += kAttnThreads) {
+            a.keys[((uint64_t)last * a.Hkv + g) * D + i] = a.new_k[(uint64_t)g * D + i];
+            a.values[((uint64_t)last * a.Hkv + g) * D + i] = a.new_v[(uint64_t)g * D + i];
+        }
+    }
+
+    // ---- scores
+    const int l16 = lane & 15;
+    float4 qr[REP][NV];
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+        const uint32_t hh = (uint32_t)h < rep ? (uint32_t)h : 0u;
+        const float4* qp = reinterpret_cast<const float4*>(a.q + ((uint64_t)g * rep + hh) * D);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) qr[h][j] = qp[j * 16 + l16];
+    }
+    {
+        uint32_t t = c0 + (uint32_t)wave * 4u + (uint32_t)(lane >> 4);
+        float4 kv[NV];
+        {
+            const float4* kp = reinterpret_cast<const float4*>(key_row(t < c1 ? t : c1 - 1));
+#pragma unroll
+            for (int j = 0; j < NV; ++j) kv[j] = kp[j * 16 + l16];
+        }
+        for (uint32_t base = c0 + (uint32_t)wave * 4u; base < c1; base += kTokStep) {
+            // next pass's row first, so its load overlaps this pass's arithmetic
+            const uint32_t tn = t + kTokStep;
+            float4 kn[NV];
+            {
+                const float4* kp = reinterpret_cast<const float4*>(key_row(tn < c1 ? tn : c1 - 1));
+#pragma unroll
+                for (int j = 0; j < NV; ++j) kn[j] = kp[j * 16 + l16];
+            }
+            float acc[REP];
+#pragma unroll
+            for (int h = 0; h < REP; ++h) {
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NV; ++j) {
+                    s += qr[h][j].x * kv[j].x;
+                    s += qr[h][j].y * kv[j].y;
+                    s += qr[h][j].z * kv[j].z;
+                    s += qr[h][j].w * kv[j].w;
+                }
+#pragma unroll
+                for (int off = 8; off >= 1; off >>= 1) s += __shfl_xor(s, off, 16);
+                acc[h] = s;
+            }
+            if (t < c1 && (uint32_t)l16 < rep) {
+                float v = acc[0];
+#pragma unroll
+                for (int h = 1; h < REP; ++h) v = l16 == h ? acc[h] : v;
+                sc[(uint32_t)l16 * a.chunk + (t - c0)] = v * a.scale;
+            }
+#pragma unroll
+            for (int j = 0; j < NV; ++j) kv[j] = kn[j];
+            t = tn;
+        }
+    }
+    __syncthreads();
+
+    // ---- softmax over the chunk, one wave per head
+    for (uint32_t h = (uint32_t)wave; h < rep; h += kAttnWaves) {
+        float* s = sc + h * a.chunk;
+        float m = -INFINITY;
+        for (uint32_t i = (uint32_t)lane; i < n; i += 64) m = fmaxf(m, s[i]);
+        m = wave_max(m);
+        float l = 0.0f;
+        for (uint32_t i = (uint32_t)lane; i < n; i += 64) {
+            const float p = expf(s[i] - m);
+            s[i] = p;
+            l += p;
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+            float* ml = a.part_ml + (((uint64_t)g * a.nchunks + c) * rep + h) * 2;
+            ml[0] = m;
+            ml[1] = l;
+        }
+    }
+    __syncthreads();
+
+    // ---- weighted values: wave w takes tokens c0 + w, c0 + w + 4, ...; four rows in flight
+    float o[REP][VW];
+#pragma unroll
+    for (int h = 0; h < REP; ++h)
+#pragma unroll
+        for (int e = 0; e < VW; ++e) o[h][e] = 0.0f;
+    for (uint32_t i0 = (uint32_t)wave; i0 < n; i0 += 4u * kAttnWaves) {
+        VT vr[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t i = i0 + (uint32_t)u * kAttnWaves;
+            vr[u] = reinterpret_cast<const VT*>(value_row(c0 + (i < n ? i : n - 1)))[lane];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t i = i0 + (uint32_t)u * kAttnWaves;
+            if (i >= n) break;
+            float v[VW];
+            Vec<VW>::unpack(vr[u], v);
+#pragma unroll
+            for (int h = 0; h < REP; ++h) {
+                if ((uint32_t)h >= rep) break;
+                const float p = sc[(uint32_t)h * a.chunk + i];
+#pragma unroll
+                for (int e = 0; e < VW; ++e) o[h][e] += p * v[e];
+            }
+        }
+    }
+    __syncthreads();  // the probabilities are no longer read: reuse the LDS for the wave sums
+    float* red = lds;  // [wave][rep][D]
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+        if ((uint32_t)h >= rep) break;
+#pragma unroll
+        for (int e = 0; e < VW; ++e) red[((uint32_t)wave * rep + (uint32_t)h) * D + (uint32_t)lane * VW + e] = o[h][e];
+    }
+    __syncthreads();
+    float* po = a.part_o + ((uint64_t)g * a.nchunks + c) * rep * D;
+    for (uint32_t i = threadIdx.x; i < rep * (uint32_t)D; i += kAttnThreads) {
+        float s = red[i];
+#pragma unroll
+        for (int w = 1; w < kAttnWaves; ++w) s += red[(uint32_t)w * rep * D + i];
+        po[i] = s;
+    }
+}
+
+OQ_DEVICE float sigmoid_ref(float v) {
+#pragma clang fp contract(off)
+    if (v >= 0.0f) {
+        const float e = expf(-v);
+        return 1.0f / (1.0f + e);
+    }
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+
+template <int D>
+__global__ __launch_bounds__(kMergeThreads) void attention_merge_kernel(MergeArgs a) {
+    constexpr int COLS = D / 4;                   // float4 columns of a head
+    constexpr int GROUPS = kMergeThreads / COLS;  // chunk groups
+    extern __shared__ __align__(16) float lds[];  // w_c [nchunks], then GROUPS x D partial sums
+    __shared__ float red[kMergeThreads / 64];
+    __shared__ float stat[2];
+    const uint32_t h = blockIdx.x;
+    const uint32_t g = h / a.rep, r = h - g * a.rep;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    auto ml = [&](uint32_t c) { return a.part_ml + (((uint64_t)g * a.nchunks + c) * a.rep + r) * 2; };
+
+    float m = -INFINITY;
+    for (uint32_t c = threadIdx.x; c < a.nchunks; c += kMergeThreads) m = fmaxf(m, ml(c)[0]);
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float mm = red[0];
+        for (int w = 1; w < kMergeThreads / 64; ++w) mm = fmaxf(mm, red[w]);
+        stat[0] = mm;
+    }
+    __syncthreads();
+    const float M = stat[0];
+    float l = 0.0f;
+    for (uint32_t c = threadIdx.x; c < a.nchunks; c += kMergeThreads) {
+        const float* p = ml(c);
+        const float w = expf(p[0] - M);
+        lds[c] = w;
+        l += w * p[1];
+    }
+    l = wave_sum(l);
+    __syncthreads();  // red is reused
+    if (lane == 0) red[wave] = l;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float s = 0.0f;
+        for (int w = 0; w < kMergeThreads / 64; ++w) s += red[w];
+        stat[1] = s;
+    }
+    const int col = threadIdx.x % COLS, grp = threadIdx.x / COLS;
+    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t c = (uint32_t)grp; c < a.nchunks; c += GROUPS) {
+        const float w = lds[c];
+        const float4 v = reinterpret_cast<const float4*>(a.part_o + (((uint64_t)g * a.nchunks + c) * a.rep + r) * D)[col];
+        acc.x += w * v.x;
+        acc.y += w * v.y;
+        acc.z += w * v.z;
+        acc.w += w * v.w;
+    }
+    float4* part = reinterpret_cast<float4*>(lds + ((a.nchunks + 3u) & ~3u));
+    part[grp * COLS + col] = acc;
+    __syncthreads();
+    if (threadIdx.x < COLS) {
+        float4 s = part[col];
+        for (int i = 1; i < GROUPS; ++i) {
+            const float4 v = part[i * COLS + col];
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        }
+        const float inv_l = stat[1];
+        float o[4] = {s.x / inv_l, s.y / inv_l, s.z / inv_l, s.w / inv_l};
+        const uint64_t base = (uint64_t)h * D + (uint64_t)col * 4;
+        reinterpret_cast<float4*>(a.out + base)[0] = make_float4(o[0], o[1], o[2], o[3]);
+        if (a.gate != nullptr) {
+            const float4 gv = reinterpret_cast<const float4*>(a.gate + (uint64_t)h * a.gate_stride)[col];
+            const float gs[4] = {sigmoid_ref(gv.x), sigmoid_ref(gv.y), sigmoid_ref(gv.z), sigmoid_ref(gv.w)};
+            reinterpret_cast<float4*>(a.gate_s + base)[0] = make_float4(gs[0], gs[1], gs[2], gs[3]);
+            reinterpret_cast<float4*>(a.gated + base)[0] =
+                make_float4(o[0] * gs[0], o[1] * gs[1], o[2] * gs[2], o[3] * gs[3]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- RoPE
+
+// cos and sin of frequency f's angle, as apply_qwen35_rope (reference_kernels.cpp:105-115):
+// base^(2f/R) and the angle in double, the coordinate chosen as position_for_frequency (:28-40)
+OQ_DEVICE void rope_cs(uint32_t f, const RopeParams& p, float& c, float& s) {
+    const double exponent = (2.0 * (double)f) / (double)p.rotary_dim;
+    const double inv_freq = 1.0 / pow((double)p.base, exponent);
+    uint64_t coord = p.pos[0];
+    if (f % 3u == 1u && f / 3u < p.sec1) coord = p.pos[1];
+    else if (f % 3u == 2u && f / 3u < p.sec2) coord = p.pos[2];
+    const double angle = (double)coord * inv_freq;
+    c = (float)cos(angle);
+    s = (float)sin(angle);
+}
+
+OQ_DEVICE void rope_pair(float* x, uint32_t f, uint32_t half, const RopeParams& p) {
+#pragma clang fp contract(off)
+    float c, s;
+    rope_cs(f, p, c, s);
+    const float a = x[f], b = x[half + f];
+    x[f] = a * c - b * s;
+    x[half + f] = b * c + a * s;
+}
+
+__global__ __launch_bounds__(256) void rope_kernel(float* heads, uint32_t head_dim, RopeParams p) {
+    float* x = heads + (uint64_t)blockIdx.x * head_dim;
+    const uint32_t half = p.rotary_dim / 2;
+    for (uint32_t f = threadIdx.x; f < half; f += blockDim.x) rope_pair(x, f, half, p);
+}
+
+// The attention block's per-head preparation (qwen35_block.cpp:671-711), one workgroup per head:
+// query heads (b < Hq) take D query values of qfull, RMSNorm with q_norm, rotate -> qcur;
+// key heads RMSNorm with k_norm, rotate -> kcur and cache row T - 1, whose value row receives v.
+__global__ __launch_bounds__(256) void attention_prep_kernel(AttnPrep a) {
+#pragma clang fp contract(off)
+    __shared__ float y[256];
+    __shared__ double red[4];
+    const uint32_t b = blockIdx.x, i = threadIdx.x, D = a.D;
+    const bool is_q = b < a.Hq;
+    const uint32_t head = is_q ? b : b - a.Hq;
+    const float* src = is_q ? a.qfull + (uint64_t)head * 2 * D : a.kp + (uint64_t)head * D;
+    const float* w = is_q ? a.q_norm : a.k_norm;
+    const float x = i < D ? src[i] : 0.0f;
+    double ss = (double)x * (double)x;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if ((i & 63) == 0) red[i >> 6] = ss;
+    __syncthreads();
+    const double tot = red[0] + red[1] + red[2] + red[3];
+    const float inv = (float)(1.0 / sqrt(tot / (double)D + (double)a.eps));
+    if (i < D) y[i] = x * inv * w[i];
+    __syncthreads();
+    const uint32_t half = a.rope.rotary_dim / 2;
+    if (i < half) rope_pair(y, i, half, a.rope);
+    __syncthreads();
+    if (i < D) {
+        if (is_q) {
+            a.qcur[(uint64_t)head * D + i] = y[i];
+        } else {
+            a.kcur[(uint64_t)head * D + i] = y[i];
+            a.key_slot[(uint64_t)head * D + i] = y[i];
+            a.value_slot[(uint64_t)head * D + i] = a.vp[(uint64_t)head * D + i];
+        }
+    }
+}
+
+template <int D, int REP>
+hipError_t launch_chunks(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
+    hipLaunchKernelGGL((attention_chunk_kernel<D, REP>), dim3(a.Hkv * a.nchunks), dim3(kAttnThreads), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_d(const AttnLaunch& L, hipStream_t s) {
+    ChunkArgs a{};
+    a.q = L.q;
+    a.keys = L.keys;
+    a.values = L.values;
+    a.new_k = L.new_k;
+    a.new_v = L.new_v;
+    a.T = L.T;
+    a.Hkv = L.Hkv;
+    a.rep = L.rep;
+    a.chunk = L.chunk;
+    a.nchunks = L.nchunks;
+    a.scale = L.scale;
+    a.part_o = L.part;
+    a.part_ml = L.part + (uint64_t)L.Hkv * L.nchunks * L.rep * D;
+    const uint64_t lds = (uint64_t)std::max(L.rep * L.chunk, (uint32_t)kAttnWaves * L.rep * D) * sizeof(float);
+    hipError_t e;
+    if (L.rep == 1) e = launch_chunks<D, 1>(a, lds, s);
+    else if (L.rep == 2) e = launch_chunks<D, 2>(a, lds, s);
+    else if (L.rep <= 4) e = launch_chunks<D, 4>(a, lds, s);
+    else e = launch_chunks<D, 8>(a, lds, s);
+    if (e != hipSuccess) return e;
+    MergeArgs m{};
+    m.part_o = a.part_o;
+    m.part_ml = a.part_ml;
+    m.Hkv = L.Hkv;
+    m.rep = L.rep;
+    m.nchunks = L.nchunks;
+    m.out = L.out;
+    m.gate = L.gate;
+    m.gate_stride = L.gate_stride;
+    m.gate_s = L.gate_s;
+    m.gated = L.gated;
+    const uint64_t mlds = (((uint64_t)L.nchunks + 3) & ~uint64_t(3)) * sizeof(float) +
+                          (uint64_t)(kMergeThreads / (D / 4)) * D * sizeof(float);
+    hipLaunchKernelGGL((attention_merge_kernel<D>), dim3(L.Hkv * L.rep), dim3(kMergeThreads), mlds, s, m);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool attention_dims_supported(uint64_t head_dim, uint64_t rep) {
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && rep >= 1 && rep <= 8;
+}
+
+void attention_plan(uint64_t T, uint64_t Hkv, uint32_t& chunk, uint32_t& nchunks) {
+    // about two chunk workgroups per compute unit, chunks a multiple of the score pass
+    const uint64_t target = std::max<uint64_t>(1, (2 * (uint64_t)cu_count()) / std::max<uint64_t>(Hkv, 1));
+    uint64_t c = (T + target - 1) / target;
+    c = (c + kTokStep - 1) / kTokStep * kTokStep;
+    c = std::min<uint64_t>(std::max<uint64_t>(c, kTokStep), kMaxChunk);
+    chunk = (uint32_t)c;
+    nchunks = (uint32_t)((T + c - 1) / c);
+}
+
+uint64_t attention_partial_floats(uint64_t Hkv, uint64_t rep, uint64_t head_dim, uint32_t nchunks) {
+    return Hkv * (uint64_t)nchunks * rep * (head_dim + 2);
+}
+
+hipError_t launch_attention(const AttnLaunch& L, hipStream_t s) {
+    switch (L.D) {
+        case 64: return launch_d<64>(L, s);
+        case 128: return launch_d<128>(L, s);
+        case 256: return launch_d<256>(L, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_rope(float* heads, uint64_t n_heads, uint64_t head_dim, const RopeParams& p, hipStream_t s) {
+    if (n_heads == 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)n_heads), dim3(std::min<uint32_t>(256u, std::max(64u, p.rotary_dim / 2))),
+                       0, s, heads, (uint32_t)head_dim, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_prep(const AttnPrep& a, hipStream_t s) {
+    if (a.D > 256) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(attention_prep_kernel, dim3(a.Hq + a.Hkv), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace oq

@@ -19,7 +19,9 @@ using namespace kq;
 //             straddle two); FFN: pair g = (row g of mat[0], row g of mat[1]); ADD: one matrix
 //   epilogue  IN: raw outputs; rows of mat[0] (qkv) run their channel's causal convolution step
 //             and SiLU, rows of mat[2] (beta) the sigmoid, rows of mat[3] (alpha) softplus(a +
-//             dt_bias) * decay; ADD: sum_out[n] = add[n] + y[n]; FFN: act[g] = SiLU(gate) * up.
+//             dt_bias) * decay -- each only when its output is given (the attention block's
+//             q / k / v projections take raw outputs only); ADD: sum_out[n] = add[n] + y[n];
+//             FFN: act[g] = SiLU(gate) * up.
 namespace blk {
 
 OQ_DEVICE float sigmoid_ref(float v) {
@@ -104,7 +106,7 @@ OQ_DEVICE void blk_epilogue(const BlockGemv& a, uint64_t grp, int lane, float v,
             if ((uint32_t)i + 1 < a.nmat && row >= a.row_end[i]) mi = (uint32_t)i + 1;
         const uint32_t l = row - (mi ? a.row_end[mi - 1] : 0u);
         a.raw[mi][l] = v;
-        if (mi == 0) {
+        if (mi == 0 && a.conv_w != nullptr) {
             // causal depthwise convolution step of channel l (reference_kernels.cpp:197-225) + SiLU
             float* h = a.history + (uint64_t)l * a.conv_kernel;
             const float* wc = a.conv_w + (uint64_t)l * a.conv_kernel;
@@ -116,9 +118,9 @@ OQ_DEVICE void blk_epilogue(const BlockGemv& a, uint64_t grp, int lane, float v,
                 sum += (double)t * (double)wc[i];
             }
             a.conv_out[l] = blk::silu_ref((float)sum);
-        } else if (mi == 2) {
+        } else if (mi == 2 && a.beta_s != nullptr) {
             a.beta_s[l] = blk::sigmoid_ref(v);
-        } else if (mi == 3) {
+        } else if (mi == 3 && a.log_decay != nullptr) {
 #pragma clang fp contract(off)
             a.log_decay[l] = blk::softplus_ref(v + a.dt_bias[l]) * a.decay[l];
         }

@@ -131,6 +131,44 @@ uint64_t delta_chunks(uint64_t dv);  // head_ss entries per head
 hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s);
 hipError_t launch_add(const float* a, const float* b, uint64_t n, float* out, hipStream_t s);
 
+// ---- oq_attention.hip  (full-attention decode: RoPE, the block's head preparation, attention)
+struct RopeParams {
+    uint32_t rotary_dim, sec1, sec2;  // sections[1] (height) and sections[2] (width)
+    float base;
+    uint64_t pos[3];  // temporal, height, width
+};
+struct AttnLaunch {
+    const float* q;            // [Hkv * rep][D]
+    float* keys;               // cache [capacity][Hkv][D]
+    float* values;
+    const float* new_k;        // token T-1's key/value rows [Hkv][D], stored into the cache; or null
+    const float* new_v;        //   when the cache already holds them
+    uint32_t T, Hkv, rep, D, chunk, nchunks;
+    float scale;               // 1 / sqrt(D)
+    float* part;               // attention_partial_floats(Hkv, rep, D, nchunks) floats
+    float* out;                // [Hkv * rep][D]
+    const float* gate;         // raw output gate of head h at gate + h * gate_stride, or null
+    uint32_t gate_stride;
+    float* gate_s;             // sigmoid(gate) [Hq][D] and out * sigmoid(gate), when gate is given
+    float* gated;
+};
+struct AttnPrep {
+    const float *qfull, *kp, *vp;  // projections: [Hq][2D], [Hkv][D], [Hkv][D]
+    const float *q_norm, *k_norm;
+    float eps;
+    uint32_t Hq, Hkv, D;
+    RopeParams rope;
+    float *qcur, *kcur;           // [Hq][D], [Hkv][D]
+    float *key_slot, *value_slot;  // cache row T-1
+};
+bool attention_dims_supported(uint64_t head_dim, uint64_t rep);
+void attention_plan(uint64_t T, uint64_t Hkv, uint32_t& chunk, uint32_t& nchunks);
+uint64_t attention_partial_floats(uint64_t Hkv, uint64_t rep, uint64_t head_dim, uint32_t nchunks);
+constexpr uint32_t kAttnMaxChunks = 8192;
+hipError_t launch_attention(const AttnLaunch& a, hipStream_t s);
+hipError_t launch_rope(float* heads, uint64_t n_heads, uint64_t head_dim, const RopeParams& p, hipStream_t s);
+hipError_t launch_attention_prep(const AttnPrep& a, hipStream_t s);
+
 // ---- oq_gemv_block.hip  (fused m = 1 GEMV of the DeltaNet decode block; see the kernel comment)
 enum : int { kBlockIn = 0, kBlockAdd = 1, kBlockFfn = 2 };
 struct BlockGemv {

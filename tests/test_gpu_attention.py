@@ -1,0 +1,385 @@
+"""GPU parity of the full-attention decode path against the oracle's restatement of the
+reference (reference_kernels.cpp:77-195, qwen35_block.cpp:607-756) on identical seeded inputs.
+
+- RoPE (oq_rope): within 2^-21 of |a| + |b| of the rotated pair (cos and sin in double on the
+  device, from glibc in the reference; the F32 rotation itself is the reference's), exact for
+  almost every element;
+- attention (oq_attention_step): |out - ref| <= 1e-4 * sum_t p_t |v_t| per output (F32 chunked
+  sums against the reference's double dot products and token-order F32 sum); the appended cache
+  rows bit for bit;
+- the block (oq_attention_block_step) stage by stage, each stage from the device's own inputs to
+  it as in the DeltaNet block tests, and end to end as a wiring check.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+import oracle_amd
+from oracle_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+ATTN_TOL = 1e-4     # attention outputs, normalised by sum_t p_t |v_t|
+TOL = 1e-4          # projections, normalised by sum |w xhat|
+STAGE_TOL = 2e-6    # elementwise / per-head stages, relative to the stage's max |value|
+CHAIN_TOL = 5e-2    # end-to-end y, relative to max |y| (wiring check)
+THREADS = min(16, oracle.default_threads())
+KQ = (12, 13, 14)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = oracle_amd.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def attn_golden():
+    from conftest import GOLDEN
+    with np.load(GOLDEN / "ref_attention.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def attention_bar(q, keys, values, length):
+    """sum_t p_t |v_t| per output [Hq][D] in float64 (q [Hq][D], keys/values [T][Hkv][D])."""
+    hq, d = q.shape
+    hkv = keys.shape[1]
+    rep = hq // hkv
+    out = np.empty((hq, values.shape[2]))
+    for h in range(hq):
+        k = keys[:length, h // rep].astype(np.float64)
+        s = k @ q[h].astype(np.float64) / math.sqrt(d)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        out[h] = p @ np.abs(values[:length, h // rep].astype(np.float64))
+    return out
+
+
+def check_attention(got, want, bar, what):
+    err = float(np.max(np.abs(got.astype(np.float64) - want) / np.maximum(bar, 1e-30)))
+    assert err <= ATTN_TOL, f"{what}: normalised error {err:.3e}"
+    return err
+
+
+# ---------------------------------------------------------------- RoPE
+
+def rope_close(got, want, x, half):
+    a = np.abs(x[:, :half]) + np.abs(x[:, half:2 * half])
+    scale = np.concatenate([a, a, np.abs(x[:, 2 * half:])], axis=1)
+    err = np.abs(got.astype(np.float64) - want)
+    assert np.all(err <= 2.0 ** -21 * scale + 1e-30), float(np.max(err / (scale + 1e-30)))
+    return float(np.mean(got == want))
+
+
+def test_rope_matches_reference_fixture(ctx, attn_golden):
+    g = attn_golden
+    x = g["rope_in"]
+    buf = ctx.alloc(x.nbytes)
+    try:
+        for name in ("text", "mm", "far"):
+            buf.upload(x)
+            ctx.rope(buf, x.shape[0], x.shape[1], 64, [11, 11, 10, 0], 1e7, tuple(int(v) for v in g[f"rope_{name}_pos"]))
+            got = buf.download(np.float32, x.size).reshape(x.shape)
+            exact = rope_close(got, g[f"rope_{name}_bits"].view(np.float32), x, 32)
+            assert exact >= 0.99, f"{name}: only {exact:.4f} of the elements bit-exact"
+    finally:
+        buf.free()
+
+
+def test_rope_known_answers_and_sizes(ctx, kat):
+    r = kat["rope"]
+    for spec in (r, kat["mrope"]):
+        x = np.array([spec["head"]], np.float32)
+        buf = ctx.to_device(x)
+        ctx.rope(buf, 1, x.shape[1], spec["rotary_dim"], spec["sections"], spec["base"], spec["position"])
+        got = buf.download(np.float32, x.size)
+        buf.free()
+        want = oracle.rope(x, spec["rotary_dim"], spec["sections"], spec["base"], spec["position"])[0]
+        assert np.allclose(got, want, atol=spec["tol"], rtol=0)
+    rng = np.random.default_rng(3)
+    for n, hd, rd, sec in ((3, 128, 128, [22, 21, 21, 0]), (40, 256, 64, [11, 11, 10, 0]), (1, 2, 2, [1, 0, 0, 0]),
+                           (7, 96, 48, [8, 8, 8, 0])):
+        x = rng.standard_normal((n, hd)).astype(np.float32)
+        pos = (int(rng.integers(0, 300000)), int(rng.integers(0, 64)), int(rng.integers(0, 64)))
+        buf = ctx.to_device(x)
+        ctx.rope(buf, n, hd, rd, sec, 1e6, pos)
+        got = buf.download(np.float32, x.size).reshape(x.shape)
+        buf.free()
+        rope_close(got, oracle.rope(x, rd, sec, 1e6, pos), x, rd // 2)
+
+
+def test_rope_errors(ctx):
+    buf = ctx.alloc(64)
+    try:
+        for rd, sec, base, msg in ((0, [0, 0, 0, 0], 1.0, "RoPE dimension must be non-zero, even, and within head width"),
+                                   (6, [3, 0, 0, 0], 1.0, "RoPE dimension must be non-zero, even, and within head width"),
+                                   (4, [2, 0, 0, 0], -1.0, "RoPE frequency base must be positive and finite"),
+                                   (4, [3, -1, 0, 0], 1.0, "RoPE dimension sections must be non-negative"),
+                                   (4, [1, 0, 0, 0], 1.0, "RoPE dimension sections must sum to half the rotary dimension")):
+            with pytest.raises(oracle_amd.InvalidArgument, match=msg):
+                ctx.rope(buf, 1, 4, rd, sec, base, (1, 1, 1))
+    finally:
+        buf.free()
+
+
+# ---------------------------------------------------------------- attention step
+
+def test_attention_step_matches_reference_fixture(ctx, attn_golden):
+    g = attn_golden
+    steps, hq, d = g["attn_q"].shape
+    hkv = g["attn_k"].shape[1]
+    cache = ctx.kv_cache(16, hkv, d, d)
+    qb, kb, vb, ob = ctx.alloc(hq * d * 4), ctx.alloc(hkv * d * 4), ctx.alloc(hkv * d * 4), ctx.alloc(hq * d * 4)
+    try:
+        for i in range(steps):
+            qb.upload(g["attn_q"][i])
+            kb.upload(g["attn_k"][i])
+            vb.upload(g["attn_v"][i])
+            ctx.attention_step(qb, hq, kb, vb, cache, ob)
+            got = ob.download(np.float32, hq * d).reshape(hq, d)
+            assert len(cache) == i + 1
+            bar = attention_bar(g["attn_q"][i], g["attn_k"][:i + 1], g["attn_v"][:i + 1], i + 1)
+            check_attention(got, g["attn_y_bits"][i].view(np.float32), bar, f"step {i}")
+        keys, values = cache.download(hkv, d, d)
+        assert np.array_equal(keys[:steps], g["attn_k"]) and np.array_equal(values[:steps], g["attn_v"])
+        assert not np.any(keys[steps:]) and not np.any(values[steps:])
+    finally:
+        for b in (qb, kb, vb, ob):
+            b.free()
+        cache.release()
+
+
+# (q_heads, kv_heads, head_dim, tokens after the step): group sizes 1-8, chunk edges, long caches
+CASES = [(8, 2, 256, 1), (8, 2, 256, 17), (16, 4, 256, 4097), (8, 2, 256, 20000), (8, 1, 128, 777),
+         (4, 4, 64, 300), (6, 2, 128, 301), (24, 4, 256, 3000), (16, 2, 256, 50), (16, 4, 256, 65537)]
+
+
+@pytest.mark.parametrize("hq,hkv,d,T", CASES, ids=[f"h{a}_{b}_d{c}_T{t}" for a, b, c, t in CASES])
+def test_attention_step_sizes(ctx, hq, hkv, d, T):
+    print(f"attention step hq={hq} hkv={hkv} d={d} T={T}", flush=True)
+    rng = np.random.default_rng(1000 + T + hq)
+    keys = rng.standard_normal((T, hkv, d)).astype(np.float32)
+    values = rng.standard_normal((T, hkv, d)).astype(np.float32)
+    q = (2.0 * rng.standard_normal((hq, d))).astype(np.float32)
+    ref_cache = oracle.KvCache(T + 1, hkv, d, d)
+    ref_cache.keys[:T - 1] = keys[:T - 1]
+    ref_cache.values[:T - 1] = values[:T - 1]
+    ref_cache.length = T - 1
+    want = oracle.attention_step(q, keys[T - 1], values[T - 1], ref_cache)
+    cache = ctx.kv_cache(T + 1, hkv, d, d)
+    bufs = [ctx.to_device(q), ctx.to_device(keys[T - 1]), ctx.to_device(values[T - 1]), ctx.alloc(hq * d * 4)]
+    try:
+        cache.load(keys[:T - 1], values[:T - 1], T - 1)
+        ctx.attention_step(bufs[0], hq, bufs[1], bufs[2], cache, bufs[3])
+        got = bufs[3].download(np.float32, hq * d).reshape(hq, d)
+        check_attention(got, want, attention_bar(q, keys, values, T), f"T={T}")
+        assert len(cache) == T
+        k_dev, v_dev = cache.download(hkv, d, d)
+        assert np.array_equal(k_dev[T - 1], keys[T - 1]) and np.array_equal(v_dev[T - 1], values[T - 1])
+        assert np.array_equal(k_dev[:T - 1], keys[:T - 1])
+    finally:
+        for b in bufs:
+            b.free()
+        cache.release()
+
+
+def test_attention_step_errors(ctx):
+    cache = ctx.kv_cache(2, 2, 64, 64)
+    q, k, v, o = ctx.alloc(6 * 64 * 4), ctx.alloc(2 * 64 * 4), ctx.alloc(2 * 64 * 4), ctx.alloc(6 * 64 * 4)
+    try:
+        with pytest.raises(oracle_amd.InvalidArgument, match="causal_attention_step dimensions are incompatible"):
+            ctx.attention_step(q, 3, k, v, cache, o)
+        cache.load(np.zeros((2, 2, 64), np.float32), np.zeros((2, 2, 64), np.float32), 2)
+        with pytest.raises(oracle_amd.Overflow, match="KV cache capacity exceeded"):
+            ctx.attention_step(q, 6, k, v, cache, o)
+        assert len(cache) == 2
+        with pytest.raises(oracle_amd.InvalidArgument, match="KV cache truncate must not grow state"):
+            cache.truncate(3)
+        cache.truncate(1)
+        assert len(cache) == 1
+        cache.reset()
+        assert len(cache) == 0
+        keys, values = cache.download(2, 64, 64)
+        assert not np.any(keys) and not np.any(values)
+        with pytest.raises(oracle_amd.InvalidArgument, match="KV cache capacity must be non-zero"):
+            ctx.kv_cache(0, 1, 64, 64)
+        odd = ctx.kv_cache(4, 1, 64, 32)
+        try:
+            with pytest.raises(oracle_amd.InvalidArgument, match="attention device path"):
+                ctx.attention_step(q, 1, k, v, odd, o)
+        finally:
+            odd.release()
+    finally:
+        for b in (q, k, v, o):
+            b.free()
+        cache.release()
+
+
+# ---------------------------------------------------------------- the block
+
+def run_block(ctx, d, w, vec, cache_np, positions, xs):
+    """Device steps; per step: y, trace and the cache arrays before the step."""
+    blk = oracle_amd.AttentionBlockWeights(ctx, d, w, vec)
+    hkv, D = d["kv_heads"], d["head_dim"]
+    cache = ctx.kv_cache(cache_np.capacity, hkv, D, D)
+    try:
+        cache.load(cache_np.keys, cache_np.values, cache_np.length)
+        sizes = oracle.attention_trace_sizes(d)
+        tb = ctx.alloc(sum(sizes.values()) * 4)
+        yb = ctx.alloc(d["embedding"] * 4)
+        steps = []
+        for x, pos in zip(xs, positions):
+            k0, v0 = cache.download(hkv, D, D)
+            n0 = len(cache)
+            xb = ctx.to_device(x)
+            ctx.attention_block_step(blk, cache, pos, xb, yb, tb)
+            ctx.sync()
+            flat = tb.download(np.float32, sum(sizes.values()))
+            tr, off = {}, 0
+            for n, sz in sizes.items():
+                tr[n] = flat[off:off + sz]
+                off += sz
+            k1, v1 = cache.download(hkv, D, D)
+            steps.append({"x": x, "pos": pos, "y": yb.download(np.float32, d["embedding"]), "trace": tr,
+                          "keys0": k0, "values0": v0, "len0": n0, "keys1": k1, "values1": v1, "len1": len(cache)})
+            xb.free()
+        tb.free()
+        yb.free()
+        return steps
+    finally:
+        cache.release()
+        blk.release()
+
+
+def project(w, name, inp, rows, cols):
+    t, data = w[name]
+    xhat = oracle.dequantize_q8k(oracle.quantize_q8k(inp), cols) if t in KQ else inp
+    y = oracle.storage_matvec(t, rows, cols, data, xhat, threads=THREADS)
+    return y, oracle.matvec_stats(t, rows, cols, data, xhat, threads=THREADS)[1]
+
+
+def close(name, got, want, worst):
+    scale = float(np.max(np.abs(want))) or 1.0
+    worst[name] = float(np.max(np.abs(got.astype(np.float64) - want))) / scale
+    assert worst[name] <= STAGE_TOL, f"{name}: error {worst[name]:.3e} of scale"
+
+
+def check_block_stages(d, w, vec, step):
+    E, F, Hq, Hkv, D, eps = (d[k] for k in ("embedding", "ffn", "q_heads", "kv_heads", "head_dim", "eps"))
+    Q, KV = Hq * D, Hkv * D
+    g, x = step["trace"], step["x"]
+    worst = {}
+    normed = oracle.rms_norm_rows(x, vec["input_norm"], E, eps)
+    projections = {"qfull": ("q", normed, 2 * Q, E), "k": ("k", normed, KV, E), "v": ("v", normed, KV, E),
+                   "branch": ("out", g["gated"], E, Q), "gate": ("gate", g["post"], F, E),
+                   "up": ("up", g["post"], F, E), "ffn": ("down", g["act"], E, F)}
+    for n, (wn, inp, rows, cols) in projections.items():
+        y, norm = project(w, wn, inp, rows, cols)
+        worst[n] = float(np.max(np.abs(g[n].astype(np.float64) - y) / np.maximum(norm, 1e-30)))
+        assert worst[n] <= TOL, f"{n}: normalised error {worst[n]:.3e}"
+    qf = g["qfull"].reshape(Hq, 2 * D)
+    rd, sec, base = d["rope_dim"], d["rope_sections"], d["rope_base"]
+    qn = oracle.rms_norm_rows(qf[:, :D].reshape(-1), vec["q_norm"], D, eps).reshape(Hq, D)
+    kn = oracle.rms_norm_rows(g["k"], vec["k_norm"], D, eps).reshape(Hkv, D)
+    close("qcur", g["qcur"], oracle.rope(qn, rd, sec, base, step["pos"]).reshape(-1), worst)
+    close("kcur", g["kcur"], oracle.rope(kn, rd, sec, base, step["pos"]).reshape(-1), worst)
+    n0 = step["len0"]
+    c = oracle.KvCache(step["keys0"].shape[0], Hkv, D, D)
+    c.keys[:] = step["keys0"]
+    c.values[:] = step["values0"]
+    c.length = n0
+    q = g["qcur"].reshape(Hq, D)
+    att = oracle.attention_step(q, g["kcur"].reshape(Hkv, D), g["v"].reshape(Hkv, D), c)
+    bar = attention_bar(q, c.keys, c.values, n0 + 1)
+    worst["pregate"] = check_attention(g["pregate"].reshape(Hq, D), att, bar, "pregate")
+    gs = np.array([oracle.sigmoid(v) for v in qf[:, D:].reshape(-1)], np.float32)
+    close("gate_s", g["gate_s"], gs, worst)
+    close("gated", g["gated"], g["pregate"] * g["gate_s"], worst)
+    close("resid", g["resid"], x + g["branch"], worst)
+    close("post", g["post"], oracle.rms_norm_rows(g["resid"], vec["post_norm"], E, eps), worst)
+    close("act", g["act"], np.array([oracle.silu(a) for a in g["gate"]], np.float32) * g["up"], worst)
+    close("y", step["y"], g["resid"] + g["ffn"], worst)
+    # the append: row n0 holds the rotated key and the value; nothing else changed
+    assert step["len1"] == n0 + 1
+    assert np.array_equal(step["keys1"][n0].reshape(-1), g["kcur"])
+    assert np.array_equal(step["values1"][n0].reshape(-1), g["v"])
+    assert np.array_equal(step["keys1"][:n0], step["keys0"][:n0])
+    return worst
+
+
+def test_attention_block_reference_fixture_stages(ctx, attn_golden):
+    """The committed kq block case (q4_K / q6_K projections, one multimodal position)."""
+    from golden.make_golden import ATTN_KQ_DIMS, ATTN_POSITIONS
+    g = attn_golden
+    d = ATTN_KQ_DIMS
+    w = {n: (int(g[f"kq_t_{n}"][0]), g[f"kq_w_{n}"]) for n in oracle.ATTN_WEIGHTS}
+    vec = {n: g[f"kq_v_{n}"] for n in oracle.ATTN_VECTORS}
+    c = oracle.KvCache(*g["kq_keys0"].shape, g["kq_values0"].shape[2])
+    c.keys[:] = g["kq_keys0"]
+    c.values[:] = g["kq_values0"]
+    c.length = int(g["kq_length0"][0])
+    steps = run_block(ctx, d, w, vec, c, ATTN_POSITIONS, g["kq_x"])
+    for i, st in enumerate(steps):
+        check_block_stages(d, w, vec, st)
+        want = g["kq_y_bits"][i].view(np.float32)
+        assert float(np.max(np.abs(st["y"] - want))) <= CHAIN_TOL * float(np.max(np.abs(want)))
+
+
+BLOCKS = {
+    # the 2B checkpoint's attention geometry (8 query heads over 2 KV heads of 256, MRoPE 64)
+    "e2048": (dict(embedding=2048, q_heads=8, kv_heads=2, head_dim=256, ffn=6144, rope_dim=64,
+                   rope_sections=[11, 11, 10, 0], rope_base=1e7, eps=1e-6),
+              dict(q=12, k=12, v=12, out=14, gate=12, up=12, down=14), 1000),
+    # hidden 4096: 16 query heads over 4 KV heads
+    "e4096": (dict(embedding=4096, q_heads=16, kv_heads=4, head_dim=256, ffn=12288, rope_dim=64,
+                   rope_sections=[11, 11, 10, 0], rope_base=1e7, eps=1e-6),
+              dict(q=12, k=12, v=12, out=12, gate=12, up=12, down=12), 4000),
+    # mixed storage types: the unfused projection path
+    "mixed": (dict(embedding=512, q_heads=4, kv_heads=2, head_dim=128, ffn=1024, rope_dim=32,
+                   rope_sections=[6, 5, 5, 0], rope_base=1e6, eps=1e-6),
+              dict(q=13, k=8, v=0, out=14, gate=13, up=1, down=8), 37),
+}
+
+
+@pytest.mark.parametrize("name", list(BLOCKS))
+def test_attention_block_stages(ctx, name):
+    from golden.make_golden import attention_inputs
+    d, types, cached = BLOCKS[name]
+    print(f"attention block {name} cached={cached}", flush=True)
+    w, vec, c, xs = attention_inputs(np.random.default_rng(4242), d, types, cached=cached)
+    positions = [(cached + i, cached + i, cached + i) for i in range(2)] + [(cached + 2, 7, 19)]
+    steps = run_block(ctx, d, w, vec, c, positions, xs)
+    own = c.copy()
+    for st in steps:
+        check_block_stages(d, w, vec, st)
+        y, _ = oracle.attention_block_step(d, w, vec, own, st["pos"], st["x"], threads=THREADS)
+        assert float(np.max(np.abs(st["y"] - y))) <= CHAIN_TOL * float(np.max(np.abs(y)))
+
+
+def test_attention_block_errors(ctx):
+    from golden.make_golden import ATTN_KQ_DIMS, ATTN_KQ_TYPES, attention_inputs
+    d = dict(ATTN_KQ_DIMS)
+    w, vec, c, xs = attention_inputs(np.random.default_rng(5), d, ATTN_KQ_TYPES)
+    blk = oracle_amd.AttentionBlockWeights(ctx, d, w, vec)
+    wrong = ctx.kv_cache(4, 2, 64, 64)
+    full = ctx.kv_cache(1, 1, 64, 64)
+    xb, yb = ctx.to_device(xs[0]), ctx.alloc(d["embedding"] * 4)
+    try:
+        with pytest.raises(oracle_amd.InvalidArgument, match="cache dimensions do not match the manifest"):
+            ctx.attention_block_step(blk, wrong, (0, 0, 0), xb, yb)
+        full.load(np.zeros((1, 1, 64), np.float32), np.zeros((1, 1, 64), np.float32), 1)
+        with pytest.raises(oracle_amd.Overflow, match="KV cache capacity exceeded"):
+            ctx.attention_block_step(blk, full, (0, 0, 0), xb, yb)
+        blk.desc.rope_sections[0] = 7
+        with pytest.raises(oracle_amd.InvalidArgument, match="sum to half the rotary dimension"):
+            ctx.attention_block_step(blk, full, (0, 0, 0), xb, yb)
+        assert len(full) == 1
+    finally:
+        xb.free()
+        yb.free()
+        wrong.release()
+        full.release()
+        blk.release()
