@@ -163,6 +163,54 @@ def run_deltanet(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
             "state_bytes": 2 * st.nbytes, "dims": d}
 
 
+ATTN_GEOMETRY = dict(q_heads=16, kv_heads=4, head_dim=256, tokens=32768)
+
+
+def run_attention(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, **geometry):
+    """Single-token GQA attention (oq_attention_step): 16 query heads over 4 KV heads of 256 with
+    32768 tokens cached (F32 keys and values, 256 MiB); steps cycle over caches totalling >= 512
+    MiB.  Each step appends one token; the cache is truncated back (host-side bookkeeping only)
+    so every step attends over the same number of tokens."""
+    g = dict(ATTN_GEOMETRY, **geometry)
+    hq, hkv, d, T = g["q_heads"], g["kv_heads"], g["head_dim"], g["tokens"]
+    rng = np.random.default_rng(SEED + 200)
+    kv_bytes = 2 * T * hkv * d * 4
+    ncopies = max(1, math.ceil(copies_min_bytes / kv_bytes))
+    keys = rng.standard_normal((T, hkv, d)).astype(np.float32)
+    values = rng.standard_normal((T, hkv, d)).astype(np.float32)
+    caches = []
+    for _ in range(ncopies):
+        c = ctx.kv_cache(T + 1, hkv, d, d)
+        c.load(keys, values, T - 1)
+        caches.append(c)
+    del keys, values
+    qb = ctx.to_device((2.0 * rng.standard_normal((hq, d))).astype(np.float32))
+    kb = ctx.to_device(rng.standard_normal((hkv, d)).astype(np.float32))
+    vb = ctx.to_device(rng.standard_normal((hkv, d)).astype(np.float32))
+    ob = ctx.alloc(hq * d * 4)
+    lib, h = ctx.lib, ctx.h
+    hs = [c.h for c in caches]
+
+    def step(i):
+        c = hs[i % ncopies]
+        if lib.oq_attention_step(h, qb.ptr, hq, kb.ptr, vb.ptr, c, ob.ptr) != 0 or \
+                lib.oq_kv_cache_truncate(c, T - 1) != 0:
+            raise RuntimeError(f"step {i}: {lib.oq_last_error(h).decode()}")
+
+    step(0)  # sizes the partial-sum buffer
+    ctx.sync()
+    ms = timed_steps(ctx, step, steps, warmup)
+    for c in caches:
+        c.release()
+    for b in (qb, kb, vb, ob):
+        b.free()
+    ms_step = ms / steps
+    alg = kv_bytes + 2 * hq * d * 4 + 2 * hkv * d * 4
+    return {"workload": "attention_decode", "ms_per_step": ms_step, "us_per_step": ms_step * 1e3,
+            "kv_bytes": kv_bytes, "algorithmic_bytes": alg, "gbs": alg / (ms_step * 1e-3) / 1e9,
+            "copies": ncopies, "geometry": g}
+
+
 def run_copy_calibration(ctx, steps, nbytes=28311552):
     """Device-to-device copies of a known size: the FETCH_SIZE / WRITE_SIZE counters of this
     dispatch calibrate the same counters read on the GEMV kernels."""
@@ -250,7 +298,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="q4k_gemv",
-                    choices=sorted(WORKLOADS) + ["copy_calibration", "deltanet_block"])
+                    choices=sorted(WORKLOADS) + ["copy_calibration", "deltanet_block", "attention_decode"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     args = ap.parse_args()
@@ -280,11 +328,26 @@ def main():
             "us_per_block": round(r["us_per_block"], 2),
             "hbm_frac_weight_bytes": round(r["weight_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
         return
+    if args.workload == "attention_decode":
+        r = run_attention(ctx, args.steps, args.warmup)
+        ctx.close()
+        print(json.dumps({
+            "metric": "GQA decode attention GB/s of KV cache", "value": round(r["gbs"], 2), "unit": "GB/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (keys, values, k, v ~ N(0,1), q ~ N(0,4))",
+            "config": {"workload": "single-token GQA attention over an F32 KV cache", **r["geometry"],
+                       "kv_bytes": r["kv_bytes"], "caches_cycled": r["copies"]},
+            "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": committed_traffic("attention_decode")},
+            "us_per_step": round(r["us_per_step"], 2)}), flush=True)
+        return
     main_res = run_gpu(ctx, args.workload, args.steps, args.warmup)
-    secondary = block = None
+    secondary = block = attn = None
     if not args.no_secondary and args.workload == "q4k_gemv":
         secondary = run_gpu(ctx, "q4k_down_m512", max(5, args.steps // 20), max(2, args.warmup // 5))
         block = run_deltanet(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
+        attn = run_attention(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
     ctx.close()
 
     t, n, k, m, desc = WORKLOADS[args.workload]
@@ -319,6 +382,9 @@ def main():
         out["deltanet_block"] = {"us": round(block["us_per_block"], 2), "weight_gbs": round(block["weight_gbs"], 1),
                                  "hbm_frac": round(block["weight_gbs"] / HBM_PEAK_GBS, 4),
                                  "weight_bytes": block["weight_bytes"]}
+    if attn is not None:
+        out["attention_decode"] = {"us": round(attn["us_per_step"], 2), "kv_gbs": round(attn["gbs"], 1),
+                                   "hbm_frac": round(attn["gbs"] / HBM_PEAK_GBS, 4), **attn["geometry"]}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.workload)
     print(json.dumps(out), flush=True)

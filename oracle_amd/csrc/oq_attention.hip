@@ -13,9 +13,12 @@
 //                  values: each wave takes every fourth token, lane i owning D/64 value columns,
 //                    o[h] += p[h][t] * v_t for the rep heads; the four waves' sums are added in LDS
 //                  -> o_c [rep][D], (m_c, l_c) [rep] for the chunk
-//   merge kernel   one 1024-thread workgroup per query head: M = max_c m_c, w_c = exp(m_c - M),
-//                  out = sum_c w_c o_c / sum_c w_c l_c; for the decoder block also the output gate
-//                  (gate_s = sigmoid(gate), gated = out * gate_s, qwen35_block.cpp:734-741)
+//   merge kernel   one workgroup per (query head, 64 output columns), 16 chunk groups x 16 float4
+//                  columns: each thread folds its chunks into a running (m, l, o) with the usual
+//                  rescaling (every load issued before the first use), the 16 groups are folded in
+//                  LDS the same way: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.  For the
+//                  decoder block also the output gate (gate_s = sigmoid(gate), gated = out * gate_s,
+//                  qwen35_block.cpp:734-741)
 // The reference sums the dot products and the softmax denominator in double and the weighted
 // values in F32 in token order; here everything is F32 in the order above, so results agree
 // within a small multiple of F32 rounding (tested against 1e-4 of sum_t p_t |v_t|).
@@ -33,7 +36,8 @@ constexpr int kAttnWaves = 4;
 constexpr int kAttnThreads = kAttnWaves * 64;
 constexpr uint32_t kTokStep = kAttnWaves * 4;  // tokens per workgroup pass in the score phase
 constexpr uint32_t kMaxChunk = 1024;
-constexpr int kMergeThreads = 1024;
+constexpr int kMergeGroups = 16;  // chunk groups of the merge kernel
+constexpr int kMergeUnroll = 8;   // chunks in flight per merge thread
 
 struct ChunkArgs {
     const float* q;       // [Hq][D]
@@ -43,8 +47,8 @@ struct ChunkArgs {
     const float* new_v;
     uint32_t T, Hkv, rep, chunk, nchunks;
     float scale;
-    float* part_o;        // [Hkv][nchunks][rep][D]
-    float* part_ml;       // [Hkv][nchunks][rep][2]
+    float* part_o;        // [Hkv][rep][D/64][nchunks][64]: one head slice's chunks contiguous
+    float* part_ml;       // [Hkv][rep][nchunks][2]
 };
 
 struct MergeArgs {
@@ -84,13 +88,7 @@ struct Vec<4> {
     }
 };
 
-OQ_DEVICE float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-template <int D, int REP>
+template <int D, int REP, int NB>
 __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs a) {
     constexpr int NV = D / 64;  // float4 of one key row per lane (16 lanes per row)
     constexpr int VW = D / 64;  // value columns per lane (64 lanes per row)
@@ -124,7 +122,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
         }
     }
 
-    // ---- scores
+    // ---- scores: NB passes of 16 tokens in flight per wave, buffers rotated by unrolling (a copy
+    // between buffers would wait for the loads it copies)
     const int l16 = lane & 15;
     float4 qr[REP][NV];
 #pragma unroll
@@ -134,98 +133,107 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
 #pragma unroll
         for (int j = 0; j < NV; ++j) qr[h][j] = qp[j * 16 + l16];
     }
+    const uint32_t first = c0 + (uint32_t)wave * 4u;  // this wave's first pass (wave-uniform)
+    auto load_keys = [&](float4 (&dst)[NV], uint32_t pass_base) {
+        const uint32_t t = pass_base + (uint32_t)(lane >> 4);
+        const float4* kp = reinterpret_cast<const float4*>(key_row(t < c1 ? t : c1 - 1));
+#pragma unroll
+        for (int j = 0; j < NV; ++j) dst[j] = kp[j * 16 + l16];
+    };
     {
-        uint32_t t = c0 + (uint32_t)wave * 4u + (uint32_t)(lane >> 4);
-        float4 kv[NV];
-        {
-            const float4* kp = reinterpret_cast<const float4*>(key_row(t < c1 ? t : c1 - 1));
+        float4 kb[NB][NV];
 #pragma unroll
-            for (int j = 0; j < NV; ++j) kv[j] = kp[j * 16 + l16];
-        }
-        for (uint32_t base = c0 + (uint32_t)wave * 4u; base < c1; base += kTokStep) {
-            // next pass's row first, so its load overlaps this pass's arithmetic
-            const uint32_t tn = t + kTokStep;
-            float4 kn[NV];
-            {
-                const float4* kp = reinterpret_cast<const float4*>(key_row(tn < c1 ? tn : c1 - 1));
+        for (int b = 0; b < NB; ++b) load_keys(kb[b], first + (uint32_t)b * kTokStep);
+        for (uint32_t base = first; base < c1; base += NB * kTokStep) {
 #pragma unroll
-                for (int j = 0; j < NV; ++j) kn[j] = kp[j * 16 + l16];
-            }
-            float acc[REP];
+            for (int b = 0; b < NB; ++b) {
+                const uint32_t pb = base + (uint32_t)b * kTokStep;
+                const uint32_t t = pb + (uint32_t)(lane >> 4);
+                float acc[REP];
 #pragma unroll
-            for (int h = 0; h < REP; ++h) {
-                float s = 0.0f;
+                for (int h = 0; h < REP; ++h) {
+                    float sum = 0.0f;
 #pragma unroll
-                for (int j = 0; j < NV; ++j) {
-                    s += qr[h][j].x * kv[j].x;
-                    s += qr[h][j].y * kv[j].y;
-                    s += qr[h][j].z * kv[j].z;
-                    s += qr[h][j].w * kv[j].w;
+                    for (int j = 0; j < NV; ++j) {
+                        sum += qr[h][j].x * kb[b][j].x;
+                        sum += qr[h][j].y * kb[b][j].y;
+                        sum += qr[h][j].z * kb[b][j].z;
+                        sum += qr[h][j].w * kb[b][j].w;
+                    }
+                    acc[h] = row16_sum(sum);
                 }
+                if (t < c1 && (uint32_t)l16 < rep) {
+                    float v = acc[0];
 #pragma unroll
-                for (int off = 8; off >= 1; off >>= 1) s += __shfl_xor(s, off, 16);
-                acc[h] = s;
+                    for (int h = 1; h < REP; ++h) v = l16 == h ? acc[h] : v;
+                    sc[(uint32_t)l16 * a.chunk + (t - c0)] = v * a.scale;
+                }
+                load_keys(kb[b], pb + NB * kTokStep);
             }
-            if (t < c1 && (uint32_t)l16 < rep) {
-                float v = acc[0];
-#pragma unroll
-                for (int h = 1; h < REP; ++h) v = l16 == h ? acc[h] : v;
-                sc[(uint32_t)l16 * a.chunk + (t - c0)] = v * a.scale;
-            }
-#pragma unroll
-            for (int j = 0; j < NV; ++j) kv[j] = kn[j];
-            t = tn;
         }
     }
+    // this wave's first value rows go out before the softmax (they do not depend on it): NB groups
+    // of four rows, rotated like the keys
+    VT vb[NB][4];
+    auto load_values = [&](VT (&dst)[4], uint32_t i0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t i = i0 + (uint32_t)u * kAttnWaves;
+            dst[u] = reinterpret_cast<const VT*>(value_row(c0 + (i < n ? i : n - 1)))[lane];
+        }
+    };
+    constexpr uint32_t kGroup = 4u * kAttnWaves;  // tokens per value group of the workgroup
+#pragma unroll
+    for (int b = 0; b < NB; ++b) load_values(vb[b], (uint32_t)wave + (uint32_t)b * kGroup);
     __syncthreads();
 
     // ---- softmax over the chunk, one wave per head
     for (uint32_t h = (uint32_t)wave; h < rep; h += kAttnWaves) {
-        float* s = sc + h * a.chunk;
+        float* sh = sc + h * a.chunk;
         float m = -INFINITY;
-        for (uint32_t i = (uint32_t)lane; i < n; i += 64) m = fmaxf(m, s[i]);
+        for (uint32_t i = (uint32_t)lane; i < n; i += 64) m = fmaxf(m, sh[i]);
         m = wave_max(m);
         float l = 0.0f;
         for (uint32_t i = (uint32_t)lane; i < n; i += 64) {
-            const float p = expf(s[i] - m);
-            s[i] = p;
+            const float p = expf(sh[i] - m);
+            sh[i] = p;
             l += p;
         }
         l = wave_sum(l);
         if (lane == 0) {
-            float* ml = a.part_ml + (((uint64_t)g * a.nchunks + c) * rep + h) * 2;
+            float* ml = a.part_ml + (((uint64_t)g * rep + h) * a.nchunks + c) * 2;
             ml[0] = m;
             ml[1] = l;
         }
     }
     __syncthreads();
 
-    // ---- weighted values: wave w takes tokens c0 + w, c0 + w + 4, ...; four rows in flight
+    // ---- weighted values: wave w takes tokens c0 + w, c0 + w + 4, ...
     float o[REP][VW];
 #pragma unroll
     for (int h = 0; h < REP; ++h)
 #pragma unroll
         for (int e = 0; e < VW; ++e) o[h][e] = 0.0f;
-    for (uint32_t i0 = (uint32_t)wave; i0 < n; i0 += 4u * kAttnWaves) {
-        VT vr[4];
+    for (uint32_t i0 = (uint32_t)wave; i0 < n; i0 += NB * kGroup) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t i = i0 + (uint32_t)u * kAttnWaves;
-            vr[u] = reinterpret_cast<const VT*>(value_row(c0 + (i < n ? i : n - 1)))[lane];
-        }
+        for (int b = 0; b < NB; ++b) {
+            const uint32_t ib = i0 + (uint32_t)b * kGroup;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t i = i0 + (uint32_t)u * kAttnWaves;
-            if (i >= n) break;
-            float v[VW];
-            Vec<VW>::unpack(vr[u], v);
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t i = ib + (uint32_t)u * kAttnWaves;
+                // rows past the chunk are clamped loads with weight 0
+                const uint32_t ic = i < n ? i : n - 1;
+                float v[VW];
+                Vec<VW>::unpack(vb[b][u], v);
 #pragma unroll
-            for (int h = 0; h < REP; ++h) {
-                if ((uint32_t)h >= rep) break;
-                const float p = sc[(uint32_t)h * a.chunk + i];
+                for (int h = 0; h < REP; ++h) {
+                    if ((uint32_t)h >= rep) break;
+                    const float p = i < n ? sc[(uint32_t)h * a.chunk + ic] : 0.0f;
 #pragma unroll
-                for (int e = 0; e < VW; ++e) o[h][e] += p * v[e];
+                    for (int e = 0; e < VW; ++e) o[h][e] += p * v[e];
+                }
             }
+            load_values(vb[b], ib + NB * kGroup);
         }
     }
     __syncthreads();  // the probabilities are no longer read: reuse the LDS for the wave sums
@@ -237,12 +245,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
         for (int e = 0; e < VW; ++e) red[((uint32_t)wave * rep + (uint32_t)h) * D + (uint32_t)lane * VW + e] = o[h][e];
     }
     __syncthreads();
-    float* po = a.part_o + ((uint64_t)g * a.nchunks + c) * rep * D;
     for (uint32_t i = threadIdx.x; i < rep * (uint32_t)D; i += kAttnThreads) {
         float s = red[i];
 #pragma unroll
         for (int w = 1; w < kAttnWaves; ++w) s += red[(uint32_t)w * rep * D + i];
-        po[i] = s;
+        const uint32_t h = i / D, slice = (i % D) / 64;
+        a.part_o[((((uint64_t)g * rep + h) * (D / 64) + slice) * a.nchunks + c) * 64 + (i % 64)] = s;
     }
 }
 
@@ -256,79 +264,71 @@ OQ_DEVICE float sigmoid_ref(float v) {
     return e / (1.0f + e);
 }
 
-template <int D>
-__global__ __launch_bounds__(kMergeThreads) void attention_merge_kernel(MergeArgs a) {
-    constexpr int COLS = D / 4;                   // float4 columns of a head
-    constexpr int GROUPS = kMergeThreads / COLS;  // chunk groups
-    extern __shared__ __align__(16) float lds[];  // w_c [nchunks], then GROUPS x D partial sums
-    __shared__ float red[kMergeThreads / 64];
-    __shared__ float stat[2];
-    const uint32_t h = blockIdx.x;
-    const uint32_t g = h / a.rep, r = h - g * a.rep;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    auto ml = [&](uint32_t c) { return a.part_ml + (((uint64_t)g * a.nchunks + c) * a.rep + r) * 2; };
+OQ_DEVICE void fold(float& m, float& l, float4& o, float mc, float lc, float4 oc) {
+    const float mn = fmaxf(m, mc);
+    const float a = expf(m - mn), b = expf(mc - mn);  // m = -inf (nothing folded yet): a = 0
+    l = l * a + lc * b;
+    o.x = o.x * a + oc.x * b;
+    o.y = o.y * a + oc.y * b;
+    o.z = o.z * a + oc.z * b;
+    o.w = o.w * a + oc.w * b;
+    m = mn;
+}
 
-    float m = -INFINITY;
-    for (uint32_t c = threadIdx.x; c < a.nchunks; c += kMergeThreads) m = fmaxf(m, ml(c)[0]);
-    m = wave_max(m);
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float mm = red[0];
-        for (int w = 1; w < kMergeThreads / 64; ++w) mm = fmaxf(mm, red[w]);
-        stat[0] = mm;
-    }
-    __syncthreads();
-    const float M = stat[0];
-    float l = 0.0f;
-    for (uint32_t c = threadIdx.x; c < a.nchunks; c += kMergeThreads) {
-        const float* p = ml(c);
-        const float w = expf(p[0] - M);
-        lds[c] = w;
-        l += w * p[1];
-    }
-    l = wave_sum(l);
-    __syncthreads();  // red is reused
-    if (lane == 0) red[wave] = l;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float s = 0.0f;
-        for (int w = 0; w < kMergeThreads / 64; ++w) s += red[w];
-        stat[1] = s;
-    }
-    const int col = threadIdx.x % COLS, grp = threadIdx.x / COLS;
-    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t c = (uint32_t)grp; c < a.nchunks; c += GROUPS) {
-        const float w = lds[c];
-        const float4 v = reinterpret_cast<const float4*>(a.part_o + (((uint64_t)g * a.nchunks + c) * a.rep + r) * D)[col];
-        acc.x += w * v.x;
-        acc.y += w * v.y;
-        acc.z += w * v.z;
-        acc.w += w * v.w;
-    }
-    float4* part = reinterpret_cast<float4*>(lds + ((a.nchunks + 3u) & ~3u));
-    part[grp * COLS + col] = acc;
-    __syncthreads();
-    if (threadIdx.x < COLS) {
-        float4 s = part[col];
-        for (int i = 1; i < GROUPS; ++i) {
-            const float4 v = part[i * COLS + col];
-            s.x += v.x;
-            s.y += v.y;
-            s.z += v.z;
-            s.w += v.w;
+template <int D>
+__global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
+    constexpr int SLICES = D / 64;
+    __shared__ float4 s_o[kMergeGroups][16];
+    __shared__ float s_m[kMergeGroups], s_l[kMergeGroups];
+    const uint32_t h = blockIdx.x / SLICES, slice = blockIdx.x - h * SLICES;
+    const uint32_t g = h / a.rep, r = h - g * a.rep;
+    const int col = threadIdx.x & 15, grp = threadIdx.x >> 4;
+    const float* mlp = a.part_ml + ((uint64_t)g * a.rep + r) * a.nchunks * 2;           // [nchunks][2]
+    const float* op = a.part_o + (((uint64_t)g * a.rep + r) * SLICES + slice) * a.nchunks * 64;  // [nchunks][64]
+    float m = -INFINITY, l = 0.0f;
+    float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t c0 = (uint32_t)grp; c0 < a.nchunks; c0 += kMergeGroups * kMergeUnroll) {
+        float2 ml[kMergeUnroll];
+        float4 oc[kMergeUnroll];
+#pragma unroll
+        for (int u = 0; u < kMergeUnroll; ++u) {
+            uint32_t c = c0 + (uint32_t)u * kMergeGroups;
+            c = c < a.nchunks ? c : a.nchunks - 1;
+            ml[u] = *reinterpret_cast<const float2*>(mlp + (uint64_t)c * 2);
+            oc[u] = reinterpret_cast<const float4*>(op + (uint64_t)c * 64)[col];
         }
-        const float inv_l = stat[1];
-        float o[4] = {s.x / inv_l, s.y / inv_l, s.z / inv_l, s.w / inv_l};
-        const uint64_t base = (uint64_t)h * D + (uint64_t)col * 4;
-        reinterpret_cast<float4*>(a.out + base)[0] = make_float4(o[0], o[1], o[2], o[3]);
-        if (a.gate != nullptr) {
-            const float4 gv = reinterpret_cast<const float4*>(a.gate + (uint64_t)h * a.gate_stride)[col];
-            const float gs[4] = {sigmoid_ref(gv.x), sigmoid_ref(gv.y), sigmoid_ref(gv.z), sigmoid_ref(gv.w)};
-            reinterpret_cast<float4*>(a.gate_s + base)[0] = make_float4(gs[0], gs[1], gs[2], gs[3]);
-            reinterpret_cast<float4*>(a.gated + base)[0] =
-                make_float4(o[0] * gs[0], o[1] * gs[1], o[2] * gs[2], o[3] * gs[3]);
+        asm volatile("" ::: "memory");  // all loads of the pass issued before the first fold
+        // every fold unconditional (a branch would let the compiler sink each load behind the
+        // previous fold): chunks past the end fold in as (m = -inf, l = 0), which leaves the
+        // running values unchanged once chunk c0 (always present) is in
+#pragma unroll
+        for (int u = 0; u < kMergeUnroll; ++u) {
+            const bool in = c0 + (uint32_t)u * kMergeGroups < a.nchunks;
+            fold(m, l, o, in ? ml[u].x : -INFINITY, in ? ml[u].y : 0.0f, oc[u]);
         }
+    }
+    s_o[grp][col] = o;
+    if (col == 0) {
+        s_m[grp] = m;
+        s_l[grp] = l;
+    }
+    __syncthreads();
+    if (grp != 0) return;
+    float M = -INFINITY, L = 0.0f;
+    float4 O = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < kMergeGroups; ++i) {
+        if (s_m[i] == -INFINITY) continue;  // a group without chunks
+        fold(M, L, O, s_m[i], s_l[i], s_o[i][col]);
+    }
+    const float out[4] = {O.x / L, O.y / L, O.z / L, O.w / L};
+    const uint64_t base = (uint64_t)h * D + slice * 64 + (uint64_t)col * 4;
+    *reinterpret_cast<float4*>(a.out + base) = make_float4(out[0], out[1], out[2], out[3]);
+    if (a.gate != nullptr) {
+        const float4 gv = *reinterpret_cast<const float4*>(a.gate + (uint64_t)h * a.gate_stride + slice * 64 + col * 4);
+        const float gs[4] = {sigmoid_ref(gv.x), sigmoid_ref(gv.y), sigmoid_ref(gv.z), sigmoid_ref(gv.w)};
+        *reinterpret_cast<float4*>(a.gate_s + base) = make_float4(gs[0], gs[1], gs[2], gs[3]);
+        *reinterpret_cast<float4*>(a.gated + base) = make_float4(out[0] * gs[0], out[1] * gs[1], out[2] * gs[2],
+                                                                 out[3] * gs[3]);
     }
 }
 
@@ -400,7 +400,9 @@ __global__ __launch_bounds__(256) void attention_prep_kernel(AttnPrep a) {
 
 template <int D, int REP>
 hipError_t launch_chunks(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
-    hipLaunchKernelGGL((attention_chunk_kernel<D, REP>), dim3(a.Hkv * a.nchunks), dim3(kAttnThreads), lds, s, a);
+    // two passes in flight per wave: measured 56.1 us per step (chunk + merge, 16 query heads over
+    // 4 KV heads of 256, 32768 tokens) against 57.2 with one and 62.4 with three
+    hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 2>), dim3(a.Hkv * a.nchunks), dim3(kAttnThreads), lds, s, a);
     return hipGetLastError();
 }
 
@@ -438,9 +440,7 @@ hipError_t launch_d(const AttnLaunch& L, hipStream_t s) {
     m.gate_stride = L.gate_stride;
     m.gate_s = L.gate_s;
     m.gated = L.gated;
-    const uint64_t mlds = (((uint64_t)L.nchunks + 3) & ~uint64_t(3)) * sizeof(float) +
-                          (uint64_t)(kMergeThreads / (D / 4)) * D * sizeof(float);
-    hipLaunchKernelGGL((attention_merge_kernel<D>), dim3(L.Hkv * L.rep), dim3(kMergeThreads), mlds, s, m);
+    hipLaunchKernelGGL((attention_merge_kernel<D>), dim3(L.Hkv * L.rep * (D / 64)), dim3(256), 0, s, m);
     return hipGetLastError();
 }
 
@@ -451,8 +451,10 @@ bool attention_dims_supported(uint64_t head_dim, uint64_t rep) {
 }
 
 void attention_plan(uint64_t T, uint64_t Hkv, uint32_t& chunk, uint32_t& nchunks) {
-    // about two chunk workgroups per compute unit, chunks a multiple of the score pass
-    const uint64_t target = std::max<uint64_t>(1, (2 * (uint64_t)cu_count()) / std::max<uint64_t>(Hkv, 1));
+    // about two chunk workgroups per compute unit (OQ_ATTN_WG_PER_CU), chunks a multiple of the
+    // score pass
+    const uint64_t per_cu = (uint64_t)std::max(1, knob(kAttnWgPerCu, 2));
+    const uint64_t target = std::max<uint64_t>(1, (per_cu * (uint64_t)cu_count()) / std::max<uint64_t>(Hkv, 1));
     uint64_t c = (T + target - 1) / target;
     c = (c + kTokStep - 1) / kTokStep * kTokStep;
     c = std::min<uint64_t>(std::max<uint64_t>(c, kTokStep), kMaxChunk);

@@ -55,6 +55,7 @@ enum Knob : int {
     kGemmMfma,  // OQ_GEMM_MFMA
     kFusedQuant,  // OQ_FUSED_QUANT
     kGemmInt8,  // OQ_GEMM_INT8
+    kAttnWgPerCu,  // OQ_ATTN_WG_PER_CU
     kKnobCount
 };
 int knob(Knob k, int fallback);  // the option's value, or fallback when it is unset
