@@ -44,6 +44,9 @@ WORKLOADS = {
     "q4k_down_m1": (12, 4096, 12288, 1, "Q4_K down-projection GEMV 4096x12288, batch 1, Q8_K activations"),
     "q4k_down_m4": (12, 4096, 12288, 4, "Q4_K down-projection GEMM 4096x12288, M=4, Q8_K activations"),
     "q4k_down_m512": (12, 4096, 12288, 512, "Q4_K down-projection GEMM 4096x12288, M=512, Q8_K activations"),
+    "q5k_down_m512": (13, 4096, 12288, 512, "Q5_K down-projection GEMM 4096x12288, M=512, Q8_K activations"),
+    "q6k_down_m512": (14, 4096, 12288, 512, "Q6_K down-projection GEMM 4096x12288, M=512, Q8_K activations"),
+    "q5k_gemv": (13, 12288, 4096, 1, "Q5_K FFN gate/up decode GEMV 12288x4096, batch 1, Q8_K activations"),
 }
 SEED = 20261201
 
@@ -353,8 +356,10 @@ def main():
     t, n, k, m, desc = WORKLOADS[args.workload]
     gbs = main_res["weight_gbs"]
     achieved = main_res["algorithmic_bytes"] / (main_res["ms_per_step"] * 1e-3) / 1e9
+    metric = ("Q4_K GEMV weight GB/s (% of HBM peak); M=512 Q4_K GEMM TOPS (% MFMA)" if args.workload == "q4k_gemv"
+              else f"{desc}: weight GB/s")
     out = {
-        "metric": "Q4_K GEMV weight GB/s (% of HBM peak); M=512 Q4_K GEMM TOPS (% MFMA)",
+        "metric": metric,
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -371,6 +376,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(args.workload)},
         "us_per_gemv": round(main_res["us_per_step"], 3),
+        **({"tflops": round(main_res["tops"], 2)} if m > 1 else {}),
         **({"greedy_token_us": round(main_res["greedy_token_us"], 3)} if "greedy_token_us" in main_res else {}),
         "hbm_frac_weight_bytes": round(gbs / HBM_PEAK_GBS, 4),
     }

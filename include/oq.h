@@ -100,8 +100,9 @@ int oq_copy_device(oq_context* ctx, void* dst_dev, const void* src_dev, uint64_t
    ne1 = N rows (dimensions[1]), `host_bytes` = GgufTensorView::bytes() (zero-copy: the mmap
    pointer is copied straight to HBM).  Validates exactly what reference_storage_matvec
    validates before its loop (src/backend/cpu/quantized_reference.cpp:134-153) plus the decoder
-   whitelist (src/model/storage_decode.cpp:192-193, extended by q4_K).  Q8_0 and Q6_K rows are
-   re-laid out on the device into aligned planes; the values they decode to are unchanged. */
+   whitelist (src/model/storage_decode.cpp:192-193, extended by q4_K).  Quantized rows (q8_0,
+   q4_K, q5_K, q6_K) are re-laid out on the device into aligned planes; the values they decode to
+   are unchanged. */
 int oq_weight_upload(oq_context* ctx, uint32_t type, uint64_t ne0, uint64_t ne1,
                      const void* host_bytes, uint64_t nbytes, oq_weight** out);
 /* Same, from bytes already in device memory (e.g. a whole GGUF payload uploaded once). */
@@ -204,7 +205,9 @@ int oq_matvec_q8k(oq_context* ctx, const oq_weight* w, const void* q8k_dev, floa
 /* M activation rows: x_dev [m][ne0] -> y_dev [m][ne1].  The reference has no M>1 kernel; its
    multi-token evaluation is M independent matvecs (src/runtime/qwen35_target_multi.cpp:14-25),
    which is the semantics here.  Small m streams the weights once with register reuse;
-   m >= 16 on q4_K uses matrix cores (fp16 MFMA on exact small-integer tiles). */
+   m >= 16 on q4_K, q5_K and q6_K with K >= 4096 uses matrix cores: both operands rounded once
+   to f16 (weights decoded as the reference, Q8_K activations dequantized), F32 accumulation,
+   within the product bar (1e-4 of sum |w * xhat| per output). */
 int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x_dev, float* y_dev);
 int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q8k_dev,
                   float* y_dev);

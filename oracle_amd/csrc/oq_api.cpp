@@ -702,7 +702,7 @@ int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, f
         }
         if (oq::gemm_mfma_supported(w->m, (int)m) && knob_flag(oq::kGemmMfma, true)) {
             if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
-            return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, x, nullptr, y, ctx->scratch.ptr, ctx->stream),
+            return launch_rc(ctx, oq::launch_gemm_mfma(w->m, (int)m, x, nullptr, y, ctx->scratch.ptr, ctx->stream),
                              "matmul");
         }
         // one row: every workgroup quantizes x itself (saves a launch); several rows: quantize
@@ -742,7 +742,7 @@ int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q
     }
     if (oq::gemm_mfma_supported(w->m, (int)m) && knob_flag(oq::kGemmMfma, true)) {
         if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
-        return launch_rc(ctx, oq::launch_gemm_q4k_mfma(w->m, (int)m, nullptr, q8, y, ctx->scratch.ptr, ctx->stream),
+        return launch_rc(ctx, oq::launch_gemm_mfma(w->m, (int)m, nullptr, q8, y, ctx->scratch.ptr, ctx->stream),
                          "matmul_q8k");
     }
     return launch_rc(ctx, oq::launch_gemv_kquant(w->m, (int)m, nullptr, q8, y, ctx->stream), "matmul_q8k");

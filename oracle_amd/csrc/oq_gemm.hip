@@ -1,8 +1,11 @@
-// Prefill / verify GEMM for q4_K weights (m >= 16 activation rows) on gfx950 matrix cores.
+// Prefill / verify GEMM for K-quant weights (m >= 16 activation rows) on gfx950 matrix cores.
 //
 // Y[m][n] = sum_k Xhat[m][k] * W[n][k] with Xhat the dequantized Q8_K activations (d*q) and W
-// the reference's decoded weights ((d*sc)*q - dmin*m, src/model/storage_decode.cpp:63-94 applied
-// to GGML q4_K).  Both operands are rounded once to binary16 and multiplied on
+// the reference's decoded weights ((d*sc)*q - dmin*m for q4_K / q5_K, src/model/storage_decode.cpp
+// :63-94; (d*sc)*q for q6_K, :96-125).  q4_K runs the kernels below whose MFMA waves convert the
+// weights in registers (gemm_q4k_ws_kernel by default: 64.7 us at M = 512, 4096 x 12288, against
+// 80.6 us for the kernel further down); q5_K and q6_K run gemm_kq_kernel, whose load waves convert
+// each step's weights into an f16 B tile in LDS.  Both operands are rounded once to binary16 and multiplied on
 // v_mfma_f32_32x32x16_f16 with F32 accumulation.  The rounding is relative 2^-11 per operand;
 // over K >= 4096 terms its effect on an output stays below 1e-4 * sum_k |w_k * xhat_k| with a
 // wide margin (checked by the parity tests), so the path is enabled only for K >= 4096.
@@ -797,6 +800,341 @@ __global__ __launch_bounds__(kWsThreads) void gemm_q4k_ws_kernel(DeviceMatrix w,
     }
 }
 
+// ---------------------------------------------------------------- B tiles converted by the load waves
+//
+// The producer/consumer workgroup with the weights converted by the load waves: every 64-k step
+// the producers turn the step's quants into the f16 B tile of the MFMAs in LDS, so the MFMA waves
+// only read LDS and multiply, whatever the weight type (q4_K, q5_K, q6_K).
+//
+// LDS (dynamic, 128 KB):
+//   A ring  4 x 16 KB  activation tile of step s in buffer s % 4 (layout as above)
+//   B ring  2 x 32 KB  weight tile of step s in buffer s % 2: slice ks, row n (0..255), lane half
+//                      hb: the 8 f16 of the MFMA B operand at 8192 ks + 32 n + 16 hb
+// Producer p: activation rows 32 p .. 32 p + 31 of each tile (as in the kernel above) and weight
+// rows 64 p .. 64 p + 63 in two passes of 32 rows; lane = 2 r + hb works on row 32 pass + r,
+// operand half hb, so its four 16-byte stores per pass (one per slice) are contiguous over the
+// wave.  Its quants for step s + 1 were loaded at step s - 2 (four register sets, one per step of
+// a super-block), converted during step s and stored into B buffer (s + 1) % 2, whose last reader
+// was step s - 1.  One barrier per step.
+//
+// Which quants make the B operand of slice ks, half hb, element i at step G of a super-block
+// (k = 32 (ks & 1) + 16 hb + 8 (ks >> 1) + i within the step, the k order of a_chunk):
+//   q4_K / q5_K: chunk (group G, half hb), byte 8 (ks >> 1) + i, low nibble for even ks (sub-block
+//                2G), high for odd (2G + 1); q5_K's fifth bit is bit 2G + (ks & 1) of qh byte
+//                16 hb + 8 (ks >> 1) + i;
+//   q6_K      : chunk (group 2 (G / 2) + hb, half ks & 1), byte 8 (ks >> 1) + i, low nibble for
+//                even G, high for odd; high bits from qh byte 32 (G / 2) + 16 hb + 8 (ks >> 1) + i
+//                shifted by 2 seg, seg = 2 (G % 2) + (ks & 1); scale sc[8 (G / 2) + hb + 2 seg]
+//                (src/model/storage_decode.cpp:96-125: element 128 half + 32 seg + lane).
+constexpr uint32_t kKqThreads = 512;
+constexpr uint32_t kKqBTile = 32768;
+constexpr uint32_t kKqLds = 4 * kTileBytes + 2 * kKqBTile;
+
+template <uint32_t TYPE>
+struct KqRaw;
+template <>
+struct KqRaw<12> {
+    uint4 q[2], hdr[2];
+};
+template <>
+struct KqRaw<13> {
+    uint4 q[2], hdr[2], qh[2];
+};
+template <>
+struct KqRaw<14> {
+    uint4 q0[2], q1[2], qh[2];
+    uint32_t sc[2], d[2];
+};
+
+// quant chunk (group g, half e) of super-block sb: offset within the row
+OQ_DEVICE uint32_t kq_chunk_off(uint32_t nsb, uint32_t sb, uint32_t g, uint32_t e) {
+    const uint32_t pass = sb / 16u;
+    const uint32_t mp = nsb - 16u * pass < 16u ? nsb - 16u * pass : 16u;
+    return 16u * (128u * pass + e * 4u * mp + 4u * (sb % 16u) + g);
+}
+
+template <uint32_t TYPE, int G>
+OQ_DEVICE void kq_load(KqRaw<TYPE>& r, const uint8_t* wb, const uint32_t (&row_off)[2], uint32_t nsb, uint32_t sb,
+                       uint32_t hb) {
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+        const uint8_t* row = wb + row_off[pp];
+        if constexpr (TYPE == 14) {
+            const uint32_t g = 2u * (G / 2) + hb;
+            r.q0[pp] = *reinterpret_cast<const uint4*>(row + kq_chunk_off(nsb, sb, g, 0));
+            r.q1[pp] = *reinterpret_cast<const uint4*>(row + kq_chunk_off(nsb, sb, g, 1));
+            r.qh[pp] = *reinterpret_cast<const uint4*>(row + 128u * nsb + 64u * sb + 16u * g);
+            r.sc[pp] = *reinterpret_cast<const uint32_t*>(row + 192u * nsb + 16u * sb + 4u * g);
+            r.d[pp] = *reinterpret_cast<const uint16_t*>(row + 208u * nsb + 2u * sb);
+        } else {
+            r.q[pp] = *reinterpret_cast<const uint4*>(row + kq_chunk_off(nsb, sb, (uint32_t)G, hb));
+            r.hdr[pp] = *reinterpret_cast<const uint4*>(row + (TYPE == 13 ? 160u : 128u) * nsb + 16u * sb);
+            if constexpr (TYPE == 13) r.qh[pp] = *reinterpret_cast<const uint4*>(row + 128u * nsb + 32u * sb + 16u * hb);
+        }
+    }
+}
+
+OQ_DEVICE uint32_t dword_of(uint4 v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
+
+// Bytes (2P, 2P+1) of a word of quant values (below 1024) as the f16 pair {1024 + q0, 1024 + q1}.
+template <int P>
+OQ_DEVICE half2v f16_1024_pair(uint32_t v) {
+    const uint32_t sel = P ? 0x0C030C02u : 0x0C010C00u;
+    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0u, v, sel) | 0x64006400u);
+}
+
+// Two weights (bytes 2P, 2P+1 of the word of 5-bit quants q) of a q5_K sub-block: (d sc) q - dmin m.
+template <bool FAST, int P>
+OQ_DEVICE uint32_t q5_pair(uint32_t q, const ScaleT<FAST>& s) {
+    if constexpr (FAST) {
+        const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const half2v x = f16_1024_pair<P>(q) - k1024;  // exact integers 0..31
+        const half2v sv = __builtin_bit_cast(half2v, s.v);
+        const half2v r = __builtin_elementwise_fma(x, __builtin_shufflevector(sv, sv, 0, 0),
+                                                   __builtin_shufflevector(sv, sv, 1, 1));
+        return __builtin_bit_cast(uint32_t, r);
+    } else {
+        const float a = (float)((q >> (16 * P)) & 0xFFu), b = (float)((q >> (16 * P + 8)) & 0xFFu);
+        return pack_f16(__builtin_fmaf(a, s.ds, -s.dm), __builtin_fmaf(b, s.ds, -s.dm));
+    }
+}
+
+// Two weights of a q6_K sub-block from the word of 6-bit codes u (q = u - 32): (d sc) q.
+//   FAST : ds = f16(d * sc) (d * sc is exact in F32), x = q exactly, one v_pk_mul_f16;
+//   exact: F32 (d * sc) * q as the reference, rounded to f16.
+template <bool FAST, int P>
+OQ_DEVICE uint32_t q6_pair(uint32_t u, float ds) {
+    if constexpr (FAST) {
+        const half2v k1056 = {(_Float16)1056.0f, (_Float16)1056.0f};
+        const half2v x = f16_1024_pair<P>(u) - k1056;  // exact integers -32..31
+        const _Float16 h = (_Float16)ds;
+        const half2v dv = {h, h};
+        return __builtin_bit_cast(uint32_t, x * dv);
+    } else {
+#pragma clang fp contract(off)
+        const float a = (float)((int)((u >> (16 * P)) & 0xFFu) - 32), b = (float)((int)((u >> (16 * P + 8)) & 0xFFu) - 32);
+        return pack_f16(ds * a, ds * b);
+    }
+}
+
+// Converts the quants of one step (G) of a super-block into the four 16-byte B operand pieces of
+// each pass and stores them.
+template <uint32_t TYPE, bool FAST, int G>
+OQ_DEVICE void kq_convert(const KqRaw<TYPE>& r, uint8_t* bdst, const uint32_t (&wr_off)[2]) {
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+        uint32_t out[4][4];
+        if constexpr (TYPE == 14) {
+            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.d[pp] & 0xFFFFu));
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const int e = ks & 1, seg = 2 * (G & 1) + e;
+                const uint4 src = e ? r.q1[pp] : r.q0[pp];
+                const float ds = d * (float)(int8_t)((r.sc[pp] >> (8 * seg)) & 0xFFu);
+#pragma unroll
+                for (int wd = 0; wd < 2; ++wd) {
+                    const uint32_t lo = (dword_of(src, 2 * (ks >> 1) + wd) >> (4 * (G & 1))) & 0x0F0F0F0Fu;
+                    const uint32_t hi = (dword_of(r.qh[pp], 2 * (ks >> 1) + wd) >> (2 * seg)) & 0x03030303u;
+                    const uint32_t u = lo | (hi << 4);
+                    out[ks][2 * wd] = q6_pair<FAST, 0>(u, ds);
+                    out[ks][2 * wd + 1] = q6_pair<FAST, 1>(u, ds);
+                }
+            }
+        } else {
+            ScaleT<FAST> sc[2];
+            scale_pairs<FAST, G>(r.hdr[pp], sc);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+                for (int wd = 0; wd < 2; ++wd) {
+                    const uint32_t dw = dword_of(r.q[pp], 2 * (ks >> 1) + wd);
+                    const uint32_t nib = (ks & 1) ? (dw >> 4) & 0x0F0F0F0Fu : dw & 0x0F0F0F0Fu;
+                    if constexpr (TYPE == 13) {
+                        const uint32_t hb5 = (dword_of(r.qh[pp], 2 * (ks >> 1) + wd) >> (2 * G + (ks & 1))) & 0x01010101u;
+                        const uint32_t q = nib | (hb5 << 4);
+                        out[ks][2 * wd] = q5_pair<FAST, 0>(q, sc[ks & 1]);
+                        out[ks][2 * wd + 1] = q5_pair<FAST, 1>(q, sc[ks & 1]);
+                    } else {
+                        out[ks][2 * wd] = weight_pair<FAST, 0>(nib, sc[ks & 1]);
+                        out[ks][2 * wd + 1] = weight_pair<FAST, 1>(nib, sc[ks & 1]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            *reinterpret_cast<uint4*>(bdst + 8192u * ks + wr_off[pp]) = make_uint4(out[ks][0], out[ks][1], out[ks][2], out[ks][3]);
+    }
+}
+
+template <uint32_t TYPE, bool FAST>
+__global__ __launch_bounds__(kKqThreads) void gemm_kq_kernel(DeviceMatrix w, int m, const _Float16* a16,
+                                                             uint32_t tiles_n, uint32_t tiles_m, uint32_t splits,
+                                                             float* __restrict__ out) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint8_t* const bring = lds + 4 * kTileBytes;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nsb = (uint32_t)(w.k / kQK);
+    const Unit un = unit_of(blockIdx.x, tiles_n, tiles_m, splits);
+    const uint32_t z = un.z;
+    const uint64_t n0 = (uint64_t)un.nt * kBN, m0 = (uint64_t)un.mt * kBM;
+    Split sp;
+    sp.sb0 = (uint32_t)((uint64_t)z * nsb / splits);
+    const uint32_t sb1 = (uint32_t)((uint64_t)(z + 1) * nsb / splits);
+    sp.nsbu = sb1 - sp.sb0;  // >= 1: splits <= nsb
+    sp.nsb = nsb;
+    sp.last_step = 4 * sp.nsbu - 1;
+    sp.hdr_base = 0;
+    sp.wbase = w.base;
+    sp.a16 = reinterpret_cast<const uint8_t*>(a16) + 2ull * kQK * sp.sb0;
+    const uint32_t nsteps = 4 * sp.nsbu;
+
+    if (wave >= 4) {
+        // ------------------------------------------------------------ producer
+        const int pw = wave - 4;
+        uint32_t act_off[4];
+        const uint32_t krow = (uint32_t)(w.k * 2);
+        const uint32_t rb = 32u * pw + 2u * ((uint32_t)lane >> 3), c8 = (uint32_t)lane & 7;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint64_t row = m0 + rb + (uint32_t)(j & 1) + 16u * (uint32_t)(j >> 1);
+            row = row < (uint64_t)m ? row : (uint64_t)m - 1;
+            act_off[j] = (uint32_t)row * krow + 16u * c8;
+        }
+        const uint32_t act_st = 128u * rb + 16u * (c8 ^ ((rb >> 1) & 7));
+        auto act_load = [&](uint32_t t, uint4 (&v)[4]) {
+            const uint32_t st = t < sp.last_step ? t : sp.last_step;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = load_u4(sp.a16 + 128u * st, act_off[j]);
+        };
+        auto act_store = [&](uint32_t buf, const uint4 (&v)[4]) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<uint4*>(lds + buf * kTileBytes + act_st + 128u * (j & 1) + 2048u * (j >> 1)) = v[j];
+        };
+        // weight rows of the two passes, B store offsets
+        const uint32_t r = (uint32_t)lane >> 1, hb = (uint32_t)lane & 1;
+        uint32_t row_off[2], wr_off[2];
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+            const uint32_t nl = 64u * pw + 32u * pp + r;
+            uint64_t n = n0 + nl;
+            n = n < w.n ? n : w.n - 1;
+            row_off[pp] = (uint32_t)(n * w.pitch);
+            wr_off[pp] = 32u * nl + 16u * hb;
+        }
+        KqRaw<TYPE> raw[4];
+        // prologue: activation tiles 0..2 stored, 3 and 4 in flight; quants of steps 0..2 loaded,
+        // step 0 converted into B buffer 0
+        {
+            uint4 t0[4], t1[4], t2[4];
+            act_load(0, t0);
+            act_load(1, t1);
+            act_load(2, t2);
+            const uint32_t sb = split_sb(sp, 0);
+            kq_load<TYPE, 0>(raw[0], sp.wbase, row_off, nsb, sb, hb);
+            kq_load<TYPE, 1>(raw[1], sp.wbase, row_off, nsb, sb, hb);
+            kq_load<TYPE, 2>(raw[2], sp.wbase, row_off, nsb, sb, hb);
+            act_store(0, t0);
+            act_store(1, t1);
+            act_store(2, t2);
+            kq_convert<TYPE, FAST, 0>(raw[0], bring, wr_off);
+        }
+        uint4 av[2][4];
+        act_load(3, av[1]);
+        act_load(4, av[0]);
+        lds_barrier();
+        for (uint32_t s = 0; s < nsteps; s += 4) {
+            const uint32_t i = s / 4;
+            const uint32_t sbn = split_sb(sp, i + 1);
+            const uint32_t sbc = split_sb(sp, i);
+            // step s + g: store tile s + g + 3, load tile s + g + 5; convert step s + g + 1 into B
+            // buffer (g + 1) % 2; load the quants of step s + g + 3
+            act_store(3, av[1]);
+            act_load(s + 5, av[1]);
+            kq_load<TYPE, 3>(raw[3], sp.wbase, row_off, nsb, sbc, hb);
+            kq_convert<TYPE, FAST, 1>(raw[1], bring + kKqBTile, wr_off);
+            lds_barrier();
+            act_store(0, av[0]);
+            act_load(s + 6, av[0]);
+            kq_load<TYPE, 0>(raw[0], sp.wbase, row_off, nsb, sbn, hb);
+            kq_convert<TYPE, FAST, 2>(raw[2], bring, wr_off);
+            lds_barrier();
+            act_store(1, av[1]);
+            act_load(s + 7, av[1]);
+            kq_load<TYPE, 1>(raw[1], sp.wbase, row_off, nsb, sbn, hb);
+            kq_convert<TYPE, FAST, 3>(raw[3], bring + kKqBTile, wr_off);
+            lds_barrier();
+            act_store(2, av[0]);
+            act_load(s + 8, av[0]);
+            kq_load<TYPE, 2>(raw[2], sp.wbase, row_off, nsb, sbn, hb);
+            kq_convert<TYPE, FAST, 0>(raw[0], bring, wr_off);
+            lds_barrier();
+        }
+        return;
+    }
+
+    // ---------------------------------------------------------------- consumer
+    const int h = lane >> 5, r0 = lane & 31;
+    uint32_t rd_off[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) rd_off[ks] = 128u * (uint32_t)r0 + 16u * (uint32_t)(a_chunk(ks, h) ^ ((r0 >> 1) & 7));
+    // B operand of n-subtile j: row 64 wave + 32 j + r0, half h
+    const uint32_t b_off = 32u * (64u * (uint32_t)wave + (uint32_t)r0) + 16u * (uint32_t)h;
+    float16v acc[4][2] = {};
+    lds_barrier();  // the producers' prologue
+    half8 a[4], b[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = lds_read(lds, 4096u * i + rd_off[0]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) b[j] = lds_read(bring, 1024u * j + b_off);
+    for (uint32_t s = 0; s < nsteps; ++s) {
+        const uint32_t abuf = s & 3, bbuf = s & 1;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            half8 an[4], bn[2];
+            if (ks < 3) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) an[i] = lds_read(lds, abuf * kTileBytes + 4096u * i + rd_off[ks + 1]);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) bn[j] = lds_read(bring, bbuf * kKqBTile + 8192u * (ks + 1) + 1024u * j + b_off);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int i = q >> 1, j = q & 1;
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+            }
+            if (ks < 3) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[i] = an[i];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) b[j] = bn[j];
+            }
+        }
+        lds_barrier();
+        const uint32_t na = (s + 1) & 3, nb = (s + 1) & 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = lds_read(lds, na * kTileBytes + 4096u * i + rd_off[0]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) b[j] = lds_read(bring, nb * kKqBTile + 1024u * j + b_off);
+    }
+    float* o = out + (uint64_t)z * (uint64_t)m * w.n;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint64_t col = n0 + 64 * wave + 32 * j + r0;
+        if (col >= w.n) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int rr = 0; rr < 16; ++rr) {
+                const uint64_t row = m0 + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
+                if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][rr];
+            }
+        }
+    }
+}
+
 // y[i] = sum over splits s (in order) of partial[s][i]; count4 = outputs / 4
 __global__ __launch_bounds__(256) void reduce_splits_kernel(const float4* __restrict__ part, uint64_t count4,
                                                             uint32_t splits, float4* __restrict__ y) {
@@ -853,7 +1191,7 @@ Plan make_plan(const DeviceMatrix& w, int m) {
 }  // namespace
 
 bool gemm_mfma_supported(const DeviceMatrix& w, int m) {
-    return w.type == 12 && m >= 16 && w.k >= kMinK && w.k % kQK == 0;
+    return (w.type == 12 || w.type == 13 || w.type == 14) && m >= 16 && w.k >= kMinK && w.k % kQK == 0;
 }
 
 uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m) {
@@ -861,7 +1199,19 @@ uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m) {
     return p.a16_bytes + p.part_bytes;
 }
 
-hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
+template <uint32_t TYPE, bool FAST>
+void launch_kq(const DeviceMatrix& w, int m, const _Float16* a16, const Plan& p, float* dst, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_kq_kernel<TYPE, FAST>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kKqLds);
+        attr = true;
+    }
+    hipLaunchKernelGGL((gemm_kq_kernel<TYPE, FAST>), dim3(p.tiles_n * p.tiles_m * p.splits), dim3(kKqThreads), kKqLds, s,
+                       w, m, a16, p.tiles_n, p.tiles_m, p.splits, dst);
+}
+
+hipError_t launch_gemm_mfma(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
                                 void* scratch, hipStream_t s) {
     if (!gemm_mfma_supported(w, m) || (x == nullptr) == (q8k == nullptr)) return hipErrorNotSupported;
     const Plan p = make_plan(w, m);
@@ -878,7 +1228,13 @@ hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const float* x, co
     }
     const unsigned wgs = p.tiles_n * p.tiles_m * p.splits;
     const bool fast = w.k >= kFastMinK && knob(kGemmExactDequant, 0) == 0;
-    if (knob(kGemmWs, 1) != 0) {
+    if (w.type != 12 || knob(kGemmWs, 1) == 2) {
+        // the weights converted by the load waves (every type; q4_K with OQ_GEMM_WS=2)
+        float* dst = p.splits > 1 ? part : y;
+        if (w.type == 12) fast ? launch_kq<12, true>(w, m, a16, p, dst, s) : launch_kq<12, false>(w, m, a16, p, dst, s);
+        else if (w.type == 13) fast ? launch_kq<13, true>(w, m, a16, p, dst, s) : launch_kq<13, false>(w, m, a16, p, dst, s);
+        else fast ? launch_kq<14, true>(w, m, a16, p, dst, s) : launch_kq<14, false>(w, m, a16, p, dst, s);
+    } else if (knob(kGemmWs, 1) != 0) {
         float* dst = p.splits > 1 ? part : y;
         if (fast) {
             static bool attr = false;

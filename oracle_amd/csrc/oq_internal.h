@@ -98,12 +98,12 @@ constexpr uint32_t kArgmaxParts = 256;
 hipError_t launch_argmax(const float* logits, uint64_t n, uint32_t* token, float* value, void* partials,
                          hipStream_t s);
 
-// ---- oq_gemm.hip  (m >= 16, q4_K, K >= 4096: F16 matrix cores on F16-rounded operands)
+// ---- oq_gemm.hip  (m >= 16, q4_K / q5_K / q6_K, K >= 4096: F16 matrix cores on F16-rounded operands)
 // Activations are given either as F32 (x; quantized to Q8_K inside, bit-identical to
 // launch_quantize_q8k) or as Q8_K blocks (q8k); exactly one of the two is non-null.
 bool gemm_mfma_supported(const DeviceMatrix& w, int m);
 uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m);  // planar Q8_K image + split partials
-hipError_t launch_gemm_q4k_mfma(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
+hipError_t launch_gemm_mfma(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
                                 void* scratch, hipStream_t s);
 
 // ---- oq_gemm_i8.hip  (m >= 16, q4_K: int8 matrix cores on Q8_K x nibbles, per-sub-block integer

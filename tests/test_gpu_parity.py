@@ -277,12 +277,54 @@ def test_matrix_core_kernels_agree(ctx, cols):
     x = rng.standard_normal((m, cols)).astype(np.float32)
     w = ctx.upload(12, cols, rows, data)
     ys = {}
-    for v in ("1", "0"):
+    for v in ("1", "0", "2"):
         with oracle_amd.launch_options({"OQ_GEMM_WS": v}):
             ys[v] = gpu_matmul(ctx, w, x, rows)
     assert np.array_equal(ys["1"].view(np.uint32), ys["0"].view(np.uint32))
+    # the kernel whose load waves convert the weights into LDS B tiles (the q5_K / q6_K path)
+    assert np.array_equal(ys["1"].view(np.uint32), ys["2"].view(np.uint32))
     y_ref, norm = reference_products(12, rows, cols, data, x)
     check_close(ys["1"], y_ref, norm)
+    w.release()
+
+
+@pytest.mark.parametrize("t", [13, 14])
+@pytest.mark.parametrize("m,rows,cols", [(16, 256, 4096), (37, 300, 4096), (64, 130, 12288), (200, 128, 8192),
+                                         (19, 70, 17408), (130, 513, 4352)])
+def test_matmul_matrix_cores_q5_q6(ctx, t, m, rows, cols):
+    """m >= 16 q5_K / q6_K products on the f16 MFMA path (weights converted by the load waves);
+    Q8_K and F32 activations give the same bits."""
+    rng = np.random.default_rng(9500 + 7 * t + m + rows + cols)
+    data = synth.weights(t, rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(t, cols, rows, data)
+    y = gpu_matmul(ctx, w, x, rows)
+    xb, qb, yb = ctx.to_device(x), ctx.alloc(m * (cols // 256) * 292), ctx.alloc(m * rows * 4)
+    ctx.quantize_q8k(xb, m, cols, qb)
+    ctx.matmul_q8k(w, m, qb, yb)
+    y_q8k = yb.download(np.float32, m * rows).reshape(m, rows)
+    for b in (xb, qb, yb):
+        b.free()
+    assert np.array_equal(y.view(np.uint32), y_q8k.view(np.uint32))
+    y_ref, norm = reference_products(t, rows, cols, data, x)
+    worst = check_close(y, y_ref, norm)
+    assert worst < 0.5 * TOL, f"MFMA path margin too thin: {worst:.2e}"
+    w.release()
+
+
+@pytest.mark.parametrize("t", [13, 14])
+def test_prefill_gemm_q5_q6_full_size_sampled_rows(ctx, t):
+    """4096 x 12288 q5_K / q6_K down projections at M = 512, 24 sampled activation rows."""
+    rng = np.random.default_rng(4244 + t)
+    rows, cols, m = 4096, 12288, 512
+    data = synth.weights(t, rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(t, cols, rows, data)
+    y = gpu_matmul(ctx, w, x, rows)
+    pick = np.array(sorted(set([0, 1, 255, 256, 511] + list(rng.integers(0, m, 19)))))
+    y_ref, norm = reference_products(t, rows, cols, data, x[pick])
+    check_close(y[pick], y_ref, norm)
+    assert np.all(np.isfinite(y))
     w.release()
 
 
