@@ -806,16 +806,18 @@ __global__ __launch_bounds__(kWsThreads) void gemm_q4k_ws_kernel(DeviceMatrix w,
 // the producers turn the step's quants into the f16 B tile of the MFMAs in LDS, so the MFMA waves
 // only read LDS and multiply, whatever the weight type (q4_K, q5_K, q6_K).
 //
-// LDS (dynamic, 128 KB):
-//   A ring  4 x 16 KB  activation tile of step s in buffer s % 4 (layout as above)
-//   B ring  2 x 32 KB  weight tile of step s in buffer s % 2: slice ks, row n (0..255), lane half
+// LDS (dynamic, 144 KB):
+//   A ring  3 x 16 KB  activation tile of step s in buffer s % 3 (layout as above)
+//   B ring  3 x 32 KB  weight tile of step s in buffer s % 3: slice ks, row n (0..255), lane half
 //                      hb: the 8 f16 of the MFMA B operand at 8192 ks + 32 n + 16 hb
-// Producer p: activation rows 32 p .. 32 p + 31 of each tile (as in the kernel above) and weight
-// rows 64 p .. 64 p + 63 in two passes of 32 rows; lane = 2 r + hb works on row 32 pass + r,
+// Producer p: activation rows 32 p .. 32 p + 31 of each tile (four 16-byte chunks per lane) and
+// weight rows 64 p .. 64 p + 63 in two passes of 32 rows; lane = 2 r + hb works on row 32 pass + r,
 // operand half hb, so its four 16-byte stores per pass (one per slice) are contiguous over the
-// wave.  Its quants for step s + 1 were loaded at step s - 2 (four register sets, one per step of
-// a super-block), converted during step s and stored into B buffer (s + 1) % 2, whose last reader
-// was step s - 1.  One barrier per step.
+// wave.  During step s it stores activation tile s + 2 (loaded at step s - 2) and converts the
+// quants of step s + 2 (loaded at step s - 2; two register sets, alternating by step) into B
+// buffer (s + 2) % 3, both buffers last read at step s - 1.  The MFMA waves read the
+// operands of step s + 1 during the last slice of step s (both tiles complete since the barrier
+// ending step s - 1), so no LDS latency is exposed at a step boundary.  One barrier per step.
 //
 // Which quants make the B operand of slice ks, half hb, element i at step G of a super-block
 // (k = 32 (ks & 1) + 16 hb + 8 (ks >> 1) + i within the step, the k order of a_chunk):
@@ -828,7 +830,7 @@ __global__ __launch_bounds__(kWsThreads) void gemm_q4k_ws_kernel(DeviceMatrix w,
 //                (src/model/storage_decode.cpp:96-125: element 128 half + 32 seg + lane).
 constexpr uint32_t kKqThreads = 512;
 constexpr uint32_t kKqBTile = 32768;
-constexpr uint32_t kKqLds = 4 * kTileBytes + 2 * kKqBTile;
+constexpr uint32_t kKqLds = 3 * kTileBytes + 3 * kKqBTile;
 
 template <uint32_t TYPE>
 struct KqRaw;
@@ -972,7 +974,7 @@ __global__ __launch_bounds__(kKqThreads) void gemm_kq_kernel(DeviceMatrix w, int
                                                              uint32_t tiles_n, uint32_t tiles_m, uint32_t splits,
                                                              float* __restrict__ out) {
     extern __shared__ __align__(16) uint8_t lds[];
-    uint8_t* const bring = lds + 4 * kTileBytes;
+    uint8_t* const bring = lds + 3 * kTileBytes;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nsb = (uint32_t)(w.k / kQK);
@@ -1024,52 +1026,58 @@ __global__ __launch_bounds__(kKqThreads) void gemm_kq_kernel(DeviceMatrix w, int
             row_off[pp] = (uint32_t)(n * w.pitch);
             wr_off[pp] = 32u * nl + 16u * hb;
         }
-        KqRaw<TYPE> raw[4];
-        // prologue: activation tiles 0..2 stored, 3 and 4 in flight; quants of steps 0..2 loaded,
-        // step 0 converted into B buffer 0
+        KqRaw<TYPE> raw[2];
+        uint4 av[2][4];
+        // prologue: activation tiles 0, 1 stored, 2 and 3 in flight (sets 0, 1); quants of steps 0
+        // and 1 converted into B buffers 0 and 1, those of steps 2 and 3 in flight (sets 0, 1)
         {
-            uint4 t0[4], t1[4], t2[4];
+            uint4 t0[4], t1[4];
             act_load(0, t0);
             act_load(1, t1);
-            act_load(2, t2);
             const uint32_t sb = split_sb(sp, 0);
             kq_load<TYPE, 0>(raw[0], sp.wbase, row_off, nsb, sb, hb);
             kq_load<TYPE, 1>(raw[1], sp.wbase, row_off, nsb, sb, hb);
-            kq_load<TYPE, 2>(raw[2], sp.wbase, row_off, nsb, sb, hb);
+            act_load(2, av[0]);
+            act_load(3, av[1]);
             act_store(0, t0);
             act_store(1, t1);
-            act_store(2, t2);
             kq_convert<TYPE, FAST, 0>(raw[0], bring, wr_off);
+            kq_load<TYPE, 2>(raw[0], sp.wbase, row_off, nsb, sb, hb);
+            kq_convert<TYPE, FAST, 1>(raw[1], bring + kKqBTile, wr_off);
+            kq_load<TYPE, 3>(raw[1], sp.wbase, row_off, nsb, sb, hb);
         }
-        uint4 av[2][4];
-        act_load(3, av[1]);
-        act_load(4, av[0]);
         lds_barrier();
+        uint32_t buf2 = 2;  // (s + 2) % 3
         for (uint32_t s = 0; s < nsteps; s += 4) {
             const uint32_t i = s / 4;
             const uint32_t sbn = split_sb(sp, i + 1);
-            const uint32_t sbc = split_sb(sp, i);
-            // step s + g: store tile s + g + 3, load tile s + g + 5; convert step s + g + 1 into B
-            // buffer (g + 1) % 2; load the quants of step s + g + 3
-            act_store(3, av[1]);
-            act_load(s + 5, av[1]);
-            kq_load<TYPE, 3>(raw[3], sp.wbase, row_off, nsb, sbc, hb);
-            kq_convert<TYPE, FAST, 1>(raw[1], bring + kKqBTile, wr_off);
-            lds_barrier();
-            act_store(0, av[0]);
-            act_load(s + 6, av[0]);
+            // step s + g: store tile s + g + 2 (set g % 2) into buffer (s + g + 2) % 3 and load tile
+            // s + g + 4 into the set; convert the quants of step s + g + 2 (set g % 2) into B
+            // buffer (s + g + 2) % 3 and reload the set with step s + g + 4
+            auto next_buf = [&] { buf2 = buf2 == 2 ? 0 : buf2 + 1; };
+            act_store(buf2, av[0]);
+            act_load(s + 4, av[0]);
+            kq_convert<TYPE, FAST, 2>(raw[0], bring + buf2 * kKqBTile, wr_off);
             kq_load<TYPE, 0>(raw[0], sp.wbase, row_off, nsb, sbn, hb);
-            kq_convert<TYPE, FAST, 2>(raw[2], bring, wr_off);
+            next_buf();
             lds_barrier();
-            act_store(1, av[1]);
-            act_load(s + 7, av[1]);
+            act_store(buf2, av[1]);
+            act_load(s + 5, av[1]);
+            kq_convert<TYPE, FAST, 3>(raw[1], bring + buf2 * kKqBTile, wr_off);
             kq_load<TYPE, 1>(raw[1], sp.wbase, row_off, nsb, sbn, hb);
-            kq_convert<TYPE, FAST, 3>(raw[3], bring + kKqBTile, wr_off);
+            next_buf();
             lds_barrier();
-            act_store(2, av[0]);
-            act_load(s + 8, av[0]);
-            kq_load<TYPE, 2>(raw[2], sp.wbase, row_off, nsb, sbn, hb);
-            kq_convert<TYPE, FAST, 0>(raw[0], bring, wr_off);
+            act_store(buf2, av[0]);
+            act_load(s + 6, av[0]);
+            kq_convert<TYPE, FAST, 0>(raw[0], bring + buf2 * kKqBTile, wr_off);
+            kq_load<TYPE, 2>(raw[0], sp.wbase, row_off, nsb, sbn, hb);
+            next_buf();
+            lds_barrier();
+            act_store(buf2, av[1]);
+            act_load(s + 7, av[1]);
+            kq_convert<TYPE, FAST, 1>(raw[1], bring + buf2 * kKqBTile, wr_off);
+            kq_load<TYPE, 3>(raw[1], sp.wbase, row_off, nsb, sbn, hb);
+            next_buf();
             lds_barrier();
         }
         return;
@@ -1083,41 +1091,44 @@ __global__ __launch_bounds__(kKqThreads) void gemm_kq_kernel(DeviceMatrix w, int
     // B operand of n-subtile j: row 64 wave + 32 j + r0, half h
     const uint32_t b_off = 32u * (64u * (uint32_t)wave + (uint32_t)r0) + 16u * (uint32_t)h;
     float16v acc[4][2] = {};
-    lds_barrier();  // the producers' prologue
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();  // the producers' prologue
     half8 a[4], b[2];
 #pragma unroll
     for (int i = 0; i < 4; ++i) a[i] = lds_read(lds, 4096u * i + rd_off[0]);
 #pragma unroll
     for (int j = 0; j < 2; ++j) b[j] = lds_read(bring, 1024u * j + b_off);
+    uint32_t buf = 0;  // s % 3
     for (uint32_t s = 0; s < nsteps; ++s) {
-        const uint32_t abuf = s & 3, bbuf = s & 1;
+        const uint32_t nbuf = buf == 2 ? 0 : buf + 1;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
+            // the next slice's operands (of the next step after slice 3) are requested before this
+            // slice's MFMAs, which then cover their latency
             half8 an[4], bn[2];
-            if (ks < 3) {
+            const uint32_t ab = (ks < 3 ? buf : nbuf) * kTileBytes, bb = (ks < 3 ? buf : nbuf) * kKqBTile;
+            const int nks = (ks + 1) & 3;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) an[i] = lds_read(lds, abuf * kTileBytes + 4096u * i + rd_off[ks + 1]);
+            for (int i = 0; i < 4; ++i) an[i] = lds_read(lds, ab + 4096u * i + rd_off[nks]);
 #pragma unroll
-                for (int j = 0; j < 2; ++j) bn[j] = lds_read(bring, bbuf * kKqBTile + 8192u * (ks + 1) + 1024u * j + b_off);
-            }
+            for (int j = 0; j < 2; ++j) bn[j] = lds_read(bring, bb + 8192u * nks + 1024u * j + b_off);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
                 const int i = q >> 1, j = q & 1;
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
             }
-            if (ks < 3) {
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) a[i] = an[i];
+            for (int i = 0; i < 4; ++i) a[i] = an[i];
 #pragma unroll
-                for (int j = 0; j < 2; ++j) b[j] = bn[j];
-            }
+            for (int j = 0; j < 2; ++j) b[j] = bn[j];
         }
-        lds_barrier();
-        const uint32_t na = (s + 1) & 3, nb = (s + 1) & 1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = lds_read(lds, na * kTileBytes + 4096u * i + rd_off[0]);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) b[j] = lds_read(bring, nb * kKqBTile + 1024u * j + b_off);
+        // the barrier with a wait the compiler sees (the inline-asm one is opaque to its wait
+        // counting, which then waits for the next step's fresh reads before its first MFMA)
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        buf = nbuf;
     }
     float* o = out + (uint64_t)z * (uint64_t)m * w.n;
 #pragma unroll

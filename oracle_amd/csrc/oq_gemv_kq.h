@@ -640,6 +640,51 @@ OQ_DEVICE void stage_rows(const ActLds& s, int m, const float* x, const uint8_t*
     }
 }
 
+// The m activation rows staged in one round: every block a wave stages (at most MT * ITERS * 16 /
+// WAVES of them) is requested before the first store, then `issue` (the first weight loads), then
+// the stores.  (A loop over rounds of a few blocks costs one memory round trip per round.)
+template <uint32_t TYPE, int ITERS, int MT, bool FUSED, int WAVES, typename Issue>
+OQ_DEVICE void stage_rows_once(const ActLds& s, int m, const float* x, const uint8_t* q8k, uint64_t nsb, uint64_t k,
+                               int wave_in_wg, int lane, Issue&& issue) {
+    constexpr int SBW = (MT * ITERS * 16 + WAVES - 1) / WAVES;
+    const uint64_t nblk = (uint64_t)m * nsb;
+    float4 xv[FUSED ? SBW : 1];
+    uint32_t qv[FUSED ? 1 : SBW], bv[FUSED ? 1 : SBW];
+    float dv[FUSED ? 1 : SBW];
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        b = b < nblk ? b : nblk - 1;
+        if constexpr (FUSED) {
+            const uint64_t mi = b / nsb, sb = b % nsb;
+            xv[j] = reinterpret_cast<const float4*>(x + mi * k + sb * kQK)[lane];
+        } else {
+            const uint8_t* blk = q8k + b * kQ8KBytes;
+            qv[j] = ldg32(blk + 4 + 4 * lane);
+            bv[j] = ldg32(blk + 260 + 4 * (lane & 7));
+            dv[j] = __uint_as_float(ldg32(blk));
+        }
+    }
+    asm volatile("" ::: "memory");
+    issue();
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        if (b >= nblk) break;
+        const int mi = (int)(b / nsb);
+        const uint64_t sb = b % nsb;
+        if constexpr (FUSED) {
+            uint32_t qw;
+            int bs;
+            float d;
+            quantize_block(xv[j], lane, qw, bs, d);
+            store_block<TYPE>(s, mi, sb, lane, qw, bs, d);
+        } else {
+            copy_block_store<TYPE>(s, mi, sb, lane, qv[j], bv[j], dv[j]);
+        }
+    }
+}
+
 // Small-batch product (2 <= m <= MT activation rows), streamed like gemv_stream_kernel: 16-wave
 // workgroups stage the m rows' Q8_K blocks in LDS once, a wave walks its weight rows one pass at
 // a time with one pass in flight, decodes each pass once and multiplies it with the m activation
@@ -664,8 +709,16 @@ __global__ __launch_bounds__(1024) void gemv_stream_mt_kernel(DeviceMatrix w, in
     };
 
     WR buf[2];
-    stage_rows<TYPE, FUSED, WAVES>(s, m, x, q8k, nsb, w.k, wave_in_wg, lane);
-    load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane);
+    // one staging round (the first pass's weights requested between its loads and its stores)
+    // while the per-wave block count stays small; several rounds beyond
+    constexpr bool kOnce = (MT * ITERS * 16 + WAVES - 1) / WAVES <= (FUSED ? 8 : 12);
+    if constexpr (kOnce) {
+        stage_rows_once<TYPE, ITERS, MT, FUSED, WAVES>(s, m, x, q8k, nsb, w.k, wave_in_wg, lane,
+                                                       [&] { load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane); });
+    } else {
+        stage_rows<TYPE, FUSED, WAVES>(s, m, x, q8k, nsb, w.k, wave_in_wg, lane);
+        load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane);
+    }
     __syncthreads();
     if (first >= n) return;
 
