@@ -123,6 +123,13 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
                 raise RuntimeError("argmax failed")
 
         res["greedy_token_us"] = timed_steps(ctx, argmax_step, steps, warmup) * 1e3 / steps
+
+        # the head with the greedy token in its epilogue (oq_matvec_argmax), per step
+        def fused_step(i):
+            if ctx.lib.oq_matvec_argmax(ctx.h, whs[i % ncopies], xp, yp, tb.ptr, vb.ptr) != 0:
+                raise RuntimeError("matvec_argmax failed")
+
+        res["head_and_token_us"] = timed_steps(ctx, fused_step, steps, warmup) * 1e3 / steps
         tb.free()
         vb.free()
     for w in ws:
@@ -377,7 +384,8 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(args.workload)},
         "us_per_gemv": round(main_res["us_per_step"], 3),
         **({"tflops": round(main_res["tops"], 2)} if m > 1 else {}),
-        **({"greedy_token_us": round(main_res["greedy_token_us"], 3)} if "greedy_token_us" in main_res else {}),
+        **({"greedy_token_us": round(main_res["greedy_token_us"], 3),
+            "head_and_token_us": round(main_res["head_and_token_us"], 3)} if "greedy_token_us" in main_res else {}),
         "hbm_frac_weight_bytes": round(gbs / HBM_PEAK_GBS, 4),
     }
     if secondary is not None:

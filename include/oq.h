@@ -190,6 +190,16 @@ int oq_quantize_q8k(oq_context* ctx, const float* x_dev, uint64_t m, uint64_t k,
    buffers. */
 int oq_argmax(oq_context* ctx, const float* logits_dev, uint64_t n, uint32_t* token_dev, float* value_dev);
 
+/* The output head and its greedy token in one call: oq_matvec(w, x) into logits y_dev (ne1
+   values), then oq_argmax over them -- the head matvec and sampler of the reference's decode step
+   (src/runtime/qwen35_forward.cpp:450-465 with Sampler::sample at temperature 0,
+   src/runtime/sampler.cpp:22-44; MTP: src/runtime/qwen35_mtp.cpp:292-308).  For K-quant weights the
+   decode GEMV reduces the logits it writes to one partial per workgroup and a single small kernel
+   combines them (no pass over the logits); other types run the two calls.  Same results as the
+   two calls: token = first index of the maximum, 0xFFFFFFFF if a logit is NaN. */
+int oq_matvec_argmax(oq_context* ctx, const oq_weight* w, const float* x_dev, float* y_dev, uint32_t* token_dev,
+                     float* value_dev);
+
 /* ------------------------------------------------------------------ products */
 
 /* Replaces oracle::backend::cpu::reference_mapped_tensor_matvec / reference_storage_matvec

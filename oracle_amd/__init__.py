@@ -257,6 +257,10 @@ class Context:
     def matvec(self, w: Weight, x: DeviceBuffer, y: DeviceBuffer) -> None:
         self._call(self.lib.oq_matvec, self.h, w.h, x.ptr, y.ptr)
 
+    def matvec_argmax(self, w: Weight, x: DeviceBuffer, y: DeviceBuffer, token: DeviceBuffer, value: DeviceBuffer) -> None:
+        """Head matvec and its greedy token in one call (oq_matvec_argmax)."""
+        self._call(self.lib.oq_matvec_argmax, self.h, w.h, x.ptr, y.ptr, token.ptr, value.ptr)
+
     def matvec_q8k(self, w: Weight, q8k: DeviceBuffer, y: DeviceBuffer) -> None:
         self._call(self.lib.oq_matvec_q8k, self.h, w.h, q8k.ptr, y.ptr)
 

@@ -54,6 +54,7 @@ SIGNATURES = [
     ("oq_quantize_q8k", C.c_int, [_P, _P, _U64, _U64, _P]),
     ("oq_argmax", C.c_int, [_P, _P, _U64, _P, _P]),
     ("oq_matvec", C.c_int, [_P, _P, _P, _P]),
+    ("oq_matvec_argmax", C.c_int, [_P, _P, _P, _P, _P, _P]),
     ("oq_matvec_q8k", C.c_int, [_P, _P, _P, _P]),
     ("oq_matmul", C.c_int, [_P, _P, _U64, _P, _P]),
     ("oq_matmul_q8k", C.c_int, [_P, _P, _U64, _P, _P]),

@@ -76,7 +76,7 @@ struct oq_context {
     bool capturing = false;
     oq::Workspace scratch;  // Q8_K staging (small batches) or the GEMM's activation image + split partials
     oq::Workspace work;     // intermediates of the DeltaNet block step
-    void* argmax_parts = nullptr;  // per-slice results of oq_argmax (kArgmaxParts * 12 bytes)
+    void* argmax_parts = nullptr;  // per-slice results of oq_argmax (kArgmaxParts ArgmaxPart)
     std::vector<oq_graph*> graphs;  // live graphs captured on this context
 };
 
@@ -545,7 +545,7 @@ int oq_context_create(int device, oq_context** out) {
     e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&ctx->t0);
     if (e == hipSuccess) e = hipEventCreate(&ctx->t1);
-    if (e == hipSuccess) e = hipMalloc(&ctx->argmax_parts, oq::kArgmaxParts * 12u);
+    if (e == hipSuccess) e = hipMalloc(&ctx->argmax_parts, oq::kArgmaxParts * sizeof(oq::ArgmaxPart));
     if (e != hipSuccess) {
         const int rc = hip_fail(nullptr, e, "context creation");
         oq_context_destroy(ctx);
@@ -722,6 +722,30 @@ int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, f
 
 int oq_matvec(oq_context* ctx, const oq_weight* w, const float* x, float* y) {
     return oq_matmul(ctx, w, 1, x, y);
+}
+
+int oq_matvec_argmax(oq_context* ctx, const oq_weight* w, const float* x, float* y, uint32_t* token, float* value) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (int rc = check_weight(ctx, w)) return rc;
+    if (!x || !y || !token || !value) return fail(ctx, OQ_INVALID_ARGUMENT, "null buffer");
+    if (w->m.n > 0xFFFFFFFEull) return fail(ctx, OQ_OVERFLOW, "argmax over more than 2^32 - 1 logits");
+    if (!aligned(token, 4) || !aligned(value, 4)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "argmax buffers must be 4-byte aligned");
+    }
+    if (is_kquant(w->m.type) && aligned(x, 16) && aligned(y, 4)) {
+        // the decode GEMV reduces its own outputs: one partial per workgroup, then one small
+        // kernel combines them
+        uint32_t nparts = 0;
+        auto* parts = static_cast<oq::ArgmaxPart*>(ctx->argmax_parts);
+        hipError_t e = oq::launch_gemv_kquant_argmax(w->m, x, nullptr, y, parts, oq::kArgmaxParts, &nparts, ctx->stream);
+        if (e == hipSuccess) {
+            return launch_rc(ctx, oq::launch_argmax_final(parts, nparts, token, value, ctx->stream), "matvec_argmax");
+        }
+        if (e != hipErrorNotSupported) return launch_rc(ctx, e, "matvec_argmax");
+        (void)hipGetLastError();
+    }
+    if (int rc = oq_matmul(ctx, w, 1, x, y)) return rc;
+    return oq_argmax(ctx, y, w->m.n, token, value);
 }
 
 int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q8k, float* y) {

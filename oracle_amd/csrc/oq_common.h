@@ -104,6 +104,25 @@ OQ_DEVICE float row16_sum(float v) {
     return v;
 }
 
+// Greedy-token combination: keeps the larger value and, on equal values, the smaller index, so
+// any order of combination yields the first index of the maximum; index 0xFFFFFFFF: no element;
+// NaN values are never taken (the caller records them separately).
+OQ_DEVICE void argmax_take(float& best, uint32_t& bi, float ov, uint32_t oi) {
+    const bool take = oi != 0xFFFFFFFFu && (bi == 0xFFFFFFFFu || ov > best || (ov == best && oi < bi));
+    best = take ? ov : best;
+    bi = take ? oi : bi;
+}
+
+OQ_DEVICE void argmax_wave(float& best, uint32_t& bi, uint32_t& nan) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const uint32_t oi = __shfl_xor(bi, off, 64);
+        nan |= __shfl_xor(nan, off, 64);
+        argmax_take(best, bi, ov, oi);
+    }
+}
+
 OQ_DEVICE float readlane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }

@@ -276,30 +276,12 @@ namespace {
 
 constexpr int kArgmaxThreads = 256;
 
-struct ArgmaxPart {
-    float value;
-    uint32_t index;  // 0xFFFFFFFF: no element
-    uint32_t nan;
-};
-
-OQ_DEVICE void argmax_take(float& best, uint32_t& bi, float ov, uint32_t oi) {
-    const bool take = oi != 0xFFFFFFFFu && (bi == 0xFFFFFFFFu || ov > best || (ov == best && oi < bi));
-    best = take ? ov : best;
-    bi = take ? oi : bi;
-}
-
 // workgroup reduction of (best, bi, nan); the result is valid in thread 0
 OQ_DEVICE void argmax_block(float& best, uint32_t& bi, uint32_t& nan) {
     __shared__ float sv[kArgmaxThreads / 64];
     __shared__ uint32_t si[kArgmaxThreads / 64];
     __shared__ uint32_t sn[kArgmaxThreads / 64];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(best, off, 64);
-        const uint32_t oi = __shfl_xor(bi, off, 64);
-        nan |= __shfl_xor(nan, off, 64);
-        argmax_take(best, bi, ov, oi);
-    }
+    argmax_wave(best, bi, nan);
     const uint32_t t = threadIdx.x;
     if ((t & 63) == 0) {
         sv[t >> 6] = best;
@@ -363,6 +345,12 @@ hipError_t launch_argmax(const float* logits, uint64_t n, uint32_t* token, float
     hipLaunchKernelGGL(argmax_slice_kernel, dim3((unsigned)parts), dim3(kArgmaxThreads), 0, s, logits, (uint32_t)n,
                        (uint32_t)slice, part);
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, part, (uint32_t)parts, token, value);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_final(const ArgmaxPart* parts, uint32_t nparts, uint32_t* token, float* value,
+                               hipStream_t s) {
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, parts, nparts, token, value);
     return hipGetLastError();
 }
 

@@ -16,6 +16,12 @@ hipError_t launch_kq(const DeviceMatrix& w, int m, const float* x, const uint8_t
 }
 
 template <uint32_t TYPE, bool FUSED>
+hipError_t launch_kq_argmax(const DeviceMatrix& w, const float* x, const uint8_t* q8k, float* y, ArgmaxPart* parts,
+                            uint32_t max_parts, uint32_t* nparts, hipStream_t s) {
+    return kq::launch_argmax_iters<TYPE, FUSED>(w, x, q8k, y, parts, max_parts, nparts, s);
+}
+
+template <uint32_t TYPE, bool FUSED>
 hipError_t launch_kq_window(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
                             uint32_t pass0, uint32_t npass, int accumulate, hipStream_t s) {
     if (m <= 1) return kq::launch_window<TYPE, 1, FUSED>(w, m, x, q8k, y, pass0, npass, accumulate, s);
@@ -25,6 +31,9 @@ hipError_t launch_kq_window(const DeviceMatrix& w, int m, const float* x, const 
 
 template hipError_t launch_kq<OQ_KQ_TYPE, (OQ_KQ_FUSED != 0)>(const DeviceMatrix&, int, const float*, const uint8_t*,
                                                                float*, hipStream_t);
+template hipError_t launch_kq_argmax<OQ_KQ_TYPE, (OQ_KQ_FUSED != 0)>(const DeviceMatrix&, const float*,
+                                                                      const uint8_t*, float*, ArgmaxPart*, uint32_t,
+                                                                      uint32_t*, hipStream_t);
 template hipError_t launch_kq_window<OQ_KQ_TYPE, (OQ_KQ_FUSED != 0)>(const DeviceMatrix&, int, const float*,
                                                                       const uint8_t*, float*, uint32_t, uint32_t, int,
                                                                       hipStream_t);

@@ -506,7 +506,7 @@ OQ_DEVICE void hold(W6& r) {
 // gemv_kq_kernel, so both kernels give the same bits.
 template <uint32_t TYPE, int ITERS, bool FUSED, int WAVES, bool FULL>
 __global__ __launch_bounds__(64 * WAVES) void gemv_stream_kernel(DeviceMatrix w, const float* x, const uint8_t* q8k,
-                                                                 float* __restrict__ y) {
+                                                                 float* __restrict__ y, ArgmaxPart* amax) {
     using WR = typename WRegs<TYPE>::type;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -527,8 +527,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_stream_kernel(DeviceMatrix w,
     stage_one_row<TYPE, ITERS, FUSED, WAVES>(s, x, q8k, nsb, wave_in_wg, lane, [] {});
     load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane);
     __syncthreads();
-    if (first >= n) return;
-
+    // greedy-token epilogue (amax set): the lane's first maximum over the rows it stores
+    float best = -__builtin_inff();
+    uint32_t bi = 0xFFFFFFFFu, nan = 0;
+    if (first < n) {
     const int q = lane & 3;
     const ScaleSel ss = scale_sel(q);
     // up to two passes the lane's activation slices stay in registers; longer rows read the
@@ -586,14 +588,45 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_stream_kernel(DeviceMatrix w,
                 out_row = mine ? row : out_row;
                 acc = 0.0f;
                 ++done;
-                if ((done & 63u) == 0u) y[out_row] = out;
+                if ((done & 63u) == 0u) {
+                    y[out_row] = out;
+                    if (amax != nullptr) {
+                        nan |= out != out ? 1u : 0u;
+                        argmax_take(best, bi, out, out_row);
+                    }
+                }
             }
             row = nrow;
             it = nit;
             if (!more) break;
         }
     }
-    if ((uint32_t)lane < (done & 63u)) y[out_row] = out;
+    if ((uint32_t)lane < (done & 63u)) {
+        y[out_row] = out;
+        if (amax != nullptr) {
+            nan |= out != out ? 1u : 0u;
+            argmax_take(best, bi, out, out_row);
+        }
+    }
+    }  // first < n
+    if (amax != nullptr) {
+        __shared__ float sv[WAVES];
+        __shared__ uint32_t si[WAVES], sn[WAVES];
+        argmax_wave(best, bi, nan);
+        if (lane == 0) {
+            sv[wave_in_wg] = best;
+            si[wave_in_wg] = bi;
+            sn[wave_in_wg] = nan;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int i = 1; i < WAVES; ++i) {
+                nan |= sn[i];
+                argmax_take(best, bi, sv[i], si[i]);
+            }
+            amax[blockIdx.x] = ArgmaxPart{best, bi, nan};
+        }
+    }
 }
 
 // Stages the Q8_K form of m activation rows in LDS (row mi at s.q(mi)...), wave w taking the
@@ -980,7 +1013,8 @@ hipError_t launch_one(const DeviceMatrix& w, int m, const float* x, const uint8_
 }
 
 template <uint32_t TYPE, int ITERS, bool FUSED, int WAVES, bool FULL>
-hipError_t launch_stream(const DeviceMatrix& w, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+hipError_t launch_stream(const DeviceMatrix& w, const float* x, const uint8_t* q8k, float* y, hipStream_t s,
+                         ArgmaxPart* amax = nullptr, uint32_t max_parts = 0, uint32_t* nparts = nullptr) {
     const uint64_t lds = act_lds_bytes(w.k, 1);
     static int resident = 0;
     if (resident == 0) {
@@ -998,9 +1032,32 @@ hipError_t launch_stream(const DeviceMatrix& w, const float* x, const uint8_t* q
     uint64_t wgs = (uint64_t)cu_count() * (uint64_t)wg_per_cu;
     const uint64_t need = (w.n + WAVES - 1) / WAVES;
     if (wgs > need) wgs = need;
+    if (amax != nullptr) {
+        if (wgs > max_parts) return hipErrorNotSupported;
+        *nparts = (uint32_t)wgs;
+    }
     hipLaunchKernelGGL((gemv_stream_kernel<TYPE, ITERS, FUSED, WAVES, FULL>), dim3((unsigned)wgs), dim3(64 * WAVES),
-                       lds, s, w, x, q8k, y);
+                       lds, s, w, x, q8k, y, amax);
     return hipGetLastError();
+}
+
+// the m = 1 streamed GEMV with the greedy-token epilogue (16-wave workgroups)
+template <uint32_t TYPE, bool FUSED>
+hipError_t launch_argmax_iters(const DeviceMatrix& w, const float* x, const uint8_t* q8k, float* y, ArgmaxPart* amax,
+                               uint32_t max_parts, uint32_t* nparts, hipStream_t s) {
+    const bool full = (w.k / kQK) % 16 == 0;
+    switch ((w.k / kQK + 15) / 16) {
+#define OQ_ARGMAX_CASE(IT)                                                                                        \
+    case IT:                                                                                                      \
+        return full ? launch_stream<TYPE, IT, FUSED, 16, true>(w, x, q8k, y, s, amax, max_parts, nparts)          \
+                    : launch_stream<TYPE, IT, FUSED, 16, false>(w, x, q8k, y, s, amax, max_parts, nparts);
+        OQ_ARGMAX_CASE(1)
+        OQ_ARGMAX_CASE(2)
+        OQ_ARGMAX_CASE(3)
+        OQ_ARGMAX_CASE(4)
+#undef OQ_ARGMAX_CASE
+        default: return hipErrorNotSupported;
+    }
 }
 
 template <uint32_t TYPE, int ITERS, int MT, bool FUSED, bool FULL>

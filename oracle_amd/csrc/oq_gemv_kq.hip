@@ -52,6 +52,21 @@ uint32_t gemv_window_passes(const DeviceMatrix& w, int m) {
     return (uint32_t)(win < 1 ? 1 : win);
 }
 
+hipError_t launch_gemv_kquant_argmax(const DeviceMatrix& w, const float* x, const uint8_t* q8k, float* y,
+                                     ArgmaxPart* parts, uint32_t max_parts, uint32_t* nparts, hipStream_t s) {
+    if (!gemv_kquant_supported(w) || !short_rows(w)) return hipErrorNotSupported;
+    const bool fused = x != nullptr;
+    switch (w.type) {
+        case 12: return fused ? launch_kq_argmax<12, true>(w, x, q8k, y, parts, max_parts, nparts, s)
+                              : launch_kq_argmax<12, false>(w, x, q8k, y, parts, max_parts, nparts, s);
+        case 13: return fused ? launch_kq_argmax<13, true>(w, x, q8k, y, parts, max_parts, nparts, s)
+                              : launch_kq_argmax<13, false>(w, x, q8k, y, parts, max_parts, nparts, s);
+        case 14: return fused ? launch_kq_argmax<14, true>(w, x, q8k, y, parts, max_parts, nparts, s)
+                              : launch_kq_argmax<14, false>(w, x, q8k, y, parts, max_parts, nparts, s);
+        default: return hipErrorNotSupported;
+    }
+}
+
 hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
                               hipStream_t s) {
     if (!gemv_kquant_supported(w)) return hipErrorNotSupported;

@@ -33,6 +33,8 @@ struct DeviceMatrix {
 
 uint64_t device_pitch(uint32_t type, uint64_t k);
 
+struct ArgmaxPart;  // one slice's greedy-token result (below)
+
 // ---- oq_api.cpp
 // Launch options (OQ_* environment variables), read once when the first context is created and
 // again by oq_reload_options(); never per launch.
@@ -80,10 +82,18 @@ int gemv_max_m();
 // passes per launch of the windowed long-row kernel for m activation rows (0: the row fits the
 // compile-time kernels)
 uint32_t gemv_window_passes(const DeviceMatrix& w, int m);
+// m = 1 decode GEMV that also reduces its outputs to one greedy-token partial per workgroup
+// (parts[0..*nparts)); hipErrorNotSupported when the row does not fit the streamed kernel or the
+// grid would exceed max_parts workgroups
+hipError_t launch_gemv_kquant_argmax(const DeviceMatrix& w, const float* x, const uint8_t* q8k, float* y,
+                                     ArgmaxPart* parts, uint32_t max_parts, uint32_t* nparts, hipStream_t s);
 
 // ---- oq_gemv_inst.hip  (one instantiation set per weight type and activation form)
 template <uint32_t TYPE, bool FUSED>
 hipError_t launch_kq(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s);
+template <uint32_t TYPE, bool FUSED>
+hipError_t launch_kq_argmax(const DeviceMatrix& w, const float* x, const uint8_t* q8k, float* y, ArgmaxPart* parts,
+                            uint32_t max_parts, uint32_t* nparts, hipStream_t s);
 template <uint32_t TYPE, bool FUSED>
 hipError_t launch_kq_window(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
                             uint32_t pass0, uint32_t npass, int accumulate, hipStream_t s);
@@ -93,10 +103,18 @@ hipError_t launch_gemv_f32act(const DeviceMatrix& w, int m, const float* x, floa
                               hipStream_t s);
 
 // greedy token: first index of the maximum of logits[0..n) (n >= 1), its value; 0xFFFFFFFF on NaN.
-// partials: kArgmaxParts * 12 bytes of device memory (per-slice results; no initial contents)
-constexpr uint32_t kArgmaxParts = 256;
+// partials: kArgmaxParts ArgmaxPart of device memory (per-slice results; no initial contents)
+struct ArgmaxPart {
+    float value;
+    uint32_t index;  // 0xFFFFFFFF: no element
+    uint32_t nan;
+};
+constexpr uint32_t kArgmaxParts = 1024;
 hipError_t launch_argmax(const float* logits, uint64_t n, uint32_t* token, float* value, void* partials,
                          hipStream_t s);
+// the combination of nparts slice results (from launch_argmax's first kernel or a GEMV epilogue)
+hipError_t launch_argmax_final(const ArgmaxPart* parts, uint32_t nparts, uint32_t* token, float* value,
+                               hipStream_t s);
 
 // ---- oq_gemm.hip  (m >= 16, q4_K / q5_K / q6_K, K >= 4096: F16 matrix cores on F16-rounded operands)
 // Activations are given either as F32 (x; quantized to Q8_K inside, bit-identical to

@@ -107,3 +107,64 @@ def test_argmax_in_graph(ctx):
     g.destroy()
     for b in (lb, tb, vb):
         b.free()
+
+
+def fused_head(ctx, w, x, rows):
+    """oq_matvec_argmax: (logits, token, value) downloaded."""
+    xb, yb, tb, vb = ctx.to_device(np.ascontiguousarray(x, np.float32)), ctx.alloc(rows * 4), ctx.alloc(4), ctx.alloc(4)
+    try:
+        ctx.matvec_argmax(w, xb, yb, tb, vb)
+        return (yb.download(np.float32, rows), int(tb.download(np.uint32, 1)[0]),
+                float(vb.download(np.float32, 1)[0]))
+    finally:
+        for b in (xb, yb, tb, vb):
+            b.free()
+
+
+@pytest.mark.parametrize("t,rows,cols", [(14, 20000, 1024), (12, 4099, 4096), (13, 777, 2048), (14, 151936, 4096),
+                                         (12, 33, 12288), (8, 3000, 1024), (14, 5, 256)])
+def test_matvec_argmax_equals_two_calls(ctx, t, rows, cols):
+    """The head with the greedy token in its epilogue (K-quant weights; other types run the two
+    calls): logits bit-identical to oq_matvec, token the first index of their maximum."""
+    rng = np.random.default_rng(310 + t + rows)
+    data = synth.weights(t, rng, rows, cols)
+    w = ctx.upload(t, cols, rows, data)
+    x = rng.standard_normal(cols).astype(np.float32)
+    y, tok, val = fused_head(ctx, w, x, rows)
+    xb, yb = ctx.to_device(x), ctx.alloc(rows * 4)
+    ctx.matvec(w, xb, yb)
+    y2 = yb.download(np.float32, rows)
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+    assert (tok, val) == oracle.greedy_token(y2)
+    assert oracle_amd.greedy_token(ctx, yb, rows) == (tok, val)
+    for b in (xb, yb):
+        b.free()
+    w.release()
+
+
+def test_matvec_argmax_ties_and_nan(ctx):
+    """Duplicated maximal rows far apart (different workgroups): the first index wins; a NaN
+    logit (a weight row with a NaN scale) gives the NaN token."""
+    rng = np.random.default_rng(320)
+    rows, cols = 40000, 1024
+    rb = synth.row_bytes(14, cols)
+    data = synth.weights(14, rng, rows, cols).reshape(rows, rb)
+    x = rng.standard_normal(cols).astype(np.float32)
+    w = ctx.upload(14, cols, rows, data.ravel())
+    y, tok, _ = fused_head(ctx, w, x, rows)
+    w.release()
+    for dup in (tok + 1, rows - 1, 17):
+        d2 = data.copy()
+        d2[dup] = d2[tok]
+        w = ctx.upload(14, cols, rows, d2.ravel())
+        y2, tok2, val2 = fused_head(ctx, w, x, rows)
+        assert (tok2, val2) == oracle.greedy_token(y2)
+        assert tok2 == min(tok, dup)
+        w.release()
+    d3 = data.copy()
+    # q6_K block: ... f16 d at byte 208 of each 210-byte block: NaN scale in row 12345
+    d3[12345, 208:210] = np.array([0x00, 0x7E], np.uint8)
+    w = ctx.upload(14, cols, rows, d3.ravel())
+    y3, tok3, _ = fused_head(ctx, w, x, rows)
+    assert np.isnan(y3[12345]) and tok3 == 0xFFFFFFFF
+    w.release()

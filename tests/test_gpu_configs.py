@@ -52,6 +52,13 @@ def test_q6k_head_151936x4096_and_greedy_token(ctx):
     tok, val = oracle_amd.greedy_token(ctx, yb, rows)
     # the device's choice over its own logits is exact: first index of the maximum
     assert (tok, val) == oracle.greedy_token(y)
+    # the head with the greedy token in its epilogue: the same logits and token
+    xb, y2b, tb, vb = ctx.to_device(synth.activations(np.random.default_rng(SEED + 2), 1, 4096)[0]), \
+        ctx.alloc(rows * 4), ctx.alloc(4), ctx.alloc(4)
+    ctx.matvec_argmax(w, xb, y2b, tb, vb)
+    assert int(tb.download(np.uint32, 1)[0]) == oracle.greedy_token(y2b.download(np.float32, rows))[0]
+    for b in (xb, y2b, tb, vb):
+        b.free()
     # against the oracle's logits: the same token unless the two leading logits are closer than
     # the products' tolerance allows them to be ordered
     tok_ref, _ = oracle.greedy_token(y_ref)
