@@ -221,6 +221,49 @@ def run_attention(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, **geom
             "copies": ncopies, "geometry": g}
 
 
+def run_attention_block(ctx, steps, warmup, cached=4096, copies_min_bytes=MALL_DEFEAT_BYTES):
+    """One full-attention decode block (hidden 4096, 16 query heads over 4 KV heads of 256, FFN
+    12288) over 4096 cached tokens per step (oq_attention_block_step); steps cycle over block
+    copies (weights + cache) totalling >= 512 MiB; the cache is truncated back after each step."""
+    rng = np.random.default_rng(SEED + 300)
+    d, w, vec, keys, values, x = synth.attention_block(rng, cached=cached)
+    first = oracle_amd.AttentionBlockWeights(ctx, d, w, vec)
+    wb = first.weight_bytes()
+    kvb = keys.nbytes + values.nbytes
+    ncopies = max(1, math.ceil(copies_min_bytes / (wb + kvb)))
+    blocks = [first] + [oracle_amd.AttentionBlockWeights(ctx, d, w, vec) for _ in range(ncopies - 1)]
+    caches = []
+    for _ in range(ncopies):
+        c = ctx.kv_cache(cached + 1, d["kv_heads"], d["head_dim"], d["head_dim"])
+        c.load(keys, values, cached)
+        caches.append(c)
+    xb, yb = ctx.to_device(x), ctx.alloc(d["embedding"] * 4)
+    lib, h = ctx.lib, ctx.h
+    descs = [C.byref(b.desc) for b in blocks]
+    hs = [c.h for c in caches]
+    pos = (C.c_uint64 * 3)(cached, cached, cached)
+
+    def step(i):
+        c = hs[i % ncopies]
+        if lib.oq_attention_block_step(h, descs[i % ncopies], c, pos, xb.ptr, yb.ptr, None) != 0 or \
+                lib.oq_kv_cache_truncate(c, cached) != 0:
+            raise RuntimeError(f"step {i}: {lib.oq_last_error(h).decode()}")
+
+    step(0)  # checked call; sizes the block workspace
+    ctx.sync()
+    ms = timed_steps(ctx, step, steps, warmup)
+    for b in blocks:
+        b.release()
+    for c in caches:
+        c.release()
+    for buf in (xb, yb):
+        buf.free()
+    ms_step = ms / steps
+    return {"workload": "attention_block", "weight_bytes": wb, "kv_bytes": kvb, "copies": ncopies,
+            "ms_per_step": ms_step, "us_per_block": ms_step * 1e3,
+            "gbs": (wb + kvb) / (ms_step * 1e-3) / 1e9, "dims": {k: v for k, v in d.items()}, "cached": cached}
+
+
 def run_copy_calibration(ctx, steps, nbytes=28311552):
     """Device-to-device copies of a known size: the FETCH_SIZE / WRITE_SIZE counters of this
     dispatch calibrate the same counters read on the GEMV kernels."""
@@ -308,7 +351,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="q4k_gemv",
-                    choices=sorted(WORKLOADS) + ["copy_calibration", "deltanet_block", "attention_decode"])
+                    choices=sorted(WORKLOADS) + ["copy_calibration", "deltanet_block", "attention_decode",
+                                                 "attention_block"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     args = ap.parse_args()
@@ -338,6 +382,19 @@ def main():
             "us_per_block": round(r["us_per_block"], 2),
             "hbm_frac_weight_bytes": round(r["weight_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
         return
+    if args.workload == "attention_block":
+        r = run_attention_block(ctx, args.steps, args.warmup)
+        ctx.close()
+        print(json.dumps({
+            "metric": "attention decode block GB/s (weights + KV cache)", "value": round(r["gbs"], 2), "unit": "GB/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8xu4 dot (i32) + f32",
+            "data": "synthetic (seeded block weights, keys/values/x ~ N(0,1))",
+            "config": {"workload": "Qwen3.5 full-attention decode block, batch 1", **r["dims"],
+                       "cached_tokens": r["cached"], "weight_bytes": r["weight_bytes"], "kv_bytes": r["kv_bytes"],
+                       "block_copies_cycled": r["copies"]},
+            "us_per_block": round(r["us_per_block"], 2), "hbm_frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
+        return
     if args.workload == "attention_decode":
         r = run_attention(ctx, args.steps, args.warmup)
         ctx.close()
@@ -353,11 +410,12 @@ def main():
             "us_per_step": round(r["us_per_step"], 2)}), flush=True)
         return
     main_res = run_gpu(ctx, args.workload, args.steps, args.warmup)
-    secondary = block = attn = None
+    secondary = block = attn = attn_block = None
     if not args.no_secondary and args.workload == "q4k_gemv":
         secondary = run_gpu(ctx, "q4k_down_m512", max(5, args.steps // 20), max(2, args.warmup // 5))
         block = run_deltanet(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
         attn = run_attention(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
+        attn_block = run_attention_block(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
     ctx.close()
 
     t, n, k, m, desc = WORKLOADS[args.workload]
@@ -396,6 +454,11 @@ def main():
         out["deltanet_block"] = {"us": round(block["us_per_block"], 2), "weight_gbs": round(block["weight_gbs"], 1),
                                  "hbm_frac": round(block["weight_gbs"] / HBM_PEAK_GBS, 4),
                                  "weight_bytes": block["weight_bytes"]}
+    if attn_block is not None:
+        out["attention_block"] = {"us": round(attn_block["us_per_block"], 2), "gbs": round(attn_block["gbs"], 1),
+                                  "hbm_frac": round(attn_block["gbs"] / HBM_PEAK_GBS, 4),
+                                  "weight_bytes": attn_block["weight_bytes"], "kv_bytes": attn_block["kv_bytes"],
+                                  "cached_tokens": attn_block["cached"]}
     if attn is not None:
         out["attention_decode"] = {"us": round(attn["us_per_step"], 2), "kv_gbs": round(attn["gbs"], 1),
                                    "hbm_frac": round(attn["gbs"] / HBM_PEAK_GBS, 4), **attn["geometry"]}

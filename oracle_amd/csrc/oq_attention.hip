@@ -456,6 +456,8 @@ void attention_plan(uint64_t T, uint64_t Hkv, uint32_t& chunk, uint32_t& nchunks
     const uint64_t per_cu = (uint64_t)std::max(1, knob(kAttnWgPerCu, 2));
     const uint64_t target = std::max<uint64_t>(1, (per_cu * (uint64_t)cu_count()) / std::max<uint64_t>(Hkv, 1));
     uint64_t c = (T + target - 1) / target;
+    const uint64_t min_chunk = (uint64_t)std::max(1, knob(kAttnMinChunk, (int)kTokStep));
+    c = std::max<uint64_t>(c, min_chunk);
     c = (c + kTokStep - 1) / kTokStep * kTokStep;
     c = std::min<uint64_t>(std::max<uint64_t>(c, kTokStep), kMaxChunk);
     chunk = (uint32_t)c;

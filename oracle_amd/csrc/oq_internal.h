@@ -58,6 +58,7 @@ enum Knob : int {
     kFusedQuant,  // OQ_FUSED_QUANT
     kGemmInt8,  // OQ_GEMM_INT8
     kAttnWgPerCu,  // OQ_ATTN_WG_PER_CU
+    kAttnMinChunk,  // OQ_ATTN_MIN_CHUNK
     kKnobCount
 };
 int knob(Knob k, int fallback);  // the option's value, or fallback when it is unset

@@ -127,3 +127,30 @@ def deltanet_block(rng: np.random.Generator, dims: dict | None = None):
     state = (0.01 * rng.standard_normal((Hv, dk, dv))).astype(np.float32)
     x = rng.standard_normal(E).astype(np.float32)
     return d, w, vec, conv_history, state, x
+
+
+# hidden 4096, 16 query heads over 4 KV heads of 256 (MRoPE over 64 dimensions), FFN 12288
+ATTENTION_DIMS = dict(embedding=4096, q_heads=16, kv_heads=4, head_dim=256, ffn=12288, rope_dim=64,
+                      rope_sections=[11, 11, 10, 0], rope_base=1e7, eps=1e-6)
+
+
+def attention_block(rng: np.random.Generator, dims: dict | None = None, cached: int = 4096):
+    """(dims, weights {name: (type, bytes)}, vectors {name: F32}, keys, values, x): q4_K
+    projections (out and down q6_K / q4_K as in the DeltaNet block) and `cached` tokens of keys
+    and values [cached][kv_heads][head_dim]."""
+    d = dict(ATTENTION_DIMS if dims is None else dims)
+    E, F, Hq, Hkv, D = d["embedding"], d["ffn"], d["q_heads"], d["kv_heads"], d["head_dim"]
+    Q, KV = Hq * D, Hkv * D
+    shapes = {"q": (Q4_K, 2 * Q, E), "k": (Q4_K, KV, E), "v": (Q4_K, KV, E), "out": (Q6_K, E, Q),
+              "gate": (Q4_K, F, E), "up": (Q4_K, F, E), "down": (Q4_K, E, F)}
+    w = {n: (t, weights(t, rng, rows, cols)) for n, (t, rows, cols) in shapes.items()}
+    vec = {
+        "input_norm": (1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32),
+        "q_norm": (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32),
+        "k_norm": (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32),
+        "post_norm": (1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32),
+    }
+    keys = rng.standard_normal((cached, Hkv, D)).astype(np.float32)
+    values = rng.standard_normal((cached, Hkv, D)).astype(np.float32)
+    x = rng.standard_normal(E).astype(np.float32)
+    return d, w, vec, keys, values, x
