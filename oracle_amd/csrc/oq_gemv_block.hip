@@ -53,9 +53,31 @@ OQ_DEVICE double wave_sum_f64(double v) {
 
 }  // namespace blk
 
+// IN: matrix index and local row of row `row` of the concatenation (wave-uniform)
+OQ_DEVICE void blk_in_row(const BlockGemv& a, uint32_t row, uint32_t& mi, uint32_t& local) {
+    mi = 0;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        if ((uint32_t)i + 1 < a.nmat && row >= a.row_end[i]) mi = (uint32_t)i + 1;
+    local = row - (mi ? a.row_end[mi - 1] : 0u);
+    mi = __builtin_amdgcn_readfirstlane(mi);
+    local = __builtin_amdgcn_readfirstlane(local);
+}
+
+// IN: the epilogue's operands of a group, requested with its weights (behind them: they are
+// needed only after the weights): lane 16 r + i of a convolution row r holds the channel's history
+// value i + 1 (v[0]; unused for the last tap) and tap i (v[1]); lane 16 r of an alpha row holds
+// dt_bias (v[0]) and decay (v[1]).  Loaded in the epilogue instead, they would cost the last group
+// of every wave one dependent round trip per tap.
+struct EpiPf {
+    float v[2];
+};
+
 template <uint32_t TYPE, int ITERS, int MODE, bool FULL>
-OQ_DEVICE void blk_load_group(typename WRegs<TYPE>::type (&W)[2][ITERS], const BlockGemv& a, uint64_t grp, int lane) {
+OQ_DEVICE void blk_load_group(typename WRegs<TYPE>::type (&W)[2][ITERS], EpiPf& pf, const BlockGemv& a, uint64_t grp,
+                              int lane) {
     const uint32_t nsb = (uint32_t)(a.mat[0].k / kQK);
+    uint32_t mis[2], locals[2];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         uint32_t mi, local;
@@ -63,66 +85,96 @@ OQ_DEVICE void blk_load_group(typename WRegs<TYPE>::type (&W)[2][ITERS], const B
             mi = (uint32_t)r;
             local = (uint32_t)grp;
         } else {
-            const uint32_t row = (uint32_t)grp * 2u + (uint32_t)r;
-            mi = 0;
-#pragma unroll
-            for (int i = 0; i < 3; ++i)
-                if ((uint32_t)i + 1 < a.nmat && row >= a.row_end[i]) mi = (uint32_t)i + 1;
-            local = row - (mi ? a.row_end[mi - 1] : 0u);
+            blk_in_row(a, (uint32_t)grp * 2u + (uint32_t)r, mi, local);
         }
-        mi = __builtin_amdgcn_readfirstlane(mi);
-        local = __builtin_amdgcn_readfirstlane(local);
+        mis[r] = mi;
+        locals[r] = local;
         const DeviceMatrix& w = a.mat[mi];
         const uint32_t lrow = local < (uint32_t)w.n ? local : (uint32_t)w.n - 1;
         const uint8_t* base = w.base + (uint64_t)lrow * w.pitch;
 #pragma unroll
         for (int it = 0; it < ITERS; ++it) load_w<TYPE>(W[r][it], base, nsb, it, lane);
     }
+    if constexpr (MODE == kBlockIn) {
+        const uint32_t nrows = a.row_end[a.nmat - 1];
+        const uint32_t r = (uint32_t)lane >> 4, i = (uint32_t)lane & 15u;
+        const uint32_t mi = r == 0 ? mis[0] : mis[1], l = r == 0 ? locals[0] : locals[1];
+        const bool row_ok = lane < 32 && (uint32_t)grp * 2u + r < nrows;
+        const uint32_t K = a.conv_kernel;
+        // one load per register, its address chosen per lane: two loads into one register on
+        // paths of different lanes would make the second wait for every load in flight (the
+        // group's weights included)
+        const bool conv = row_ok && mi == 0 && a.conv_w != nullptr && i < K;
+        const bool alpha = row_ok && mi == 3 && a.log_decay != nullptr && i == 0;
+        const float* p0 = conv ? a.history + (uint64_t)l * K + i + 1 : a.dt_bias + l;
+        const float* p1 = conv ? a.conv_w + (uint64_t)l * K + i : a.decay + l;
+        if ((conv && i + 1 < K) || alpha) pf.v[0] = *p0;
+        if (conv || alpha) pf.v[1] = *p1;
+    }
 }
 
+OQ_DEVICE double readlane_f64(double v, int src) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, src);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), src);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// v0, v1: the group's two row outputs (wave-uniform); pf: its prefetched epilogue operands
 template <int MODE>
-OQ_DEVICE void blk_epilogue(const BlockGemv& a, uint64_t grp, int lane, float v, float other) {
+OQ_DEVICE void blk_epilogue(const BlockGemv& a, uint64_t grp, int lane, float v0, float v1, const EpiPf& pf) {
     if constexpr (MODE == kBlockFfn) {
-        // lane 0: gate row grp, lane 1: up row grp (other = the up value in lane 0)
+        // lane 0: gate row grp, lane 1: up row grp
         if (lane == 0) {
 #pragma clang fp contract(off)
-            a.raw[0][grp] = v;
-            a.act[grp] = blk::silu_ref(v) * other;
+            a.raw[0][grp] = v0;
+            a.act[grp] = blk::silu_ref(v0) * v1;
         } else if (lane == 1) {
-            a.raw[1][grp] = v;
+            a.raw[1][grp] = v1;
         }
     } else if constexpr (MODE == kBlockAdd) {
         const uint64_t row = grp * 2 + lane;
         if (lane < 2 && row < a.mat[0].n) {
+            const float v = lane == 0 ? v0 : v1;
             a.raw[0][row] = v;
             a.sum_out[row] = a.add[row] + v;
         }
     } else {
-        const uint32_t row = (uint32_t)grp * 2u + (uint32_t)lane;
-        if (lane >= 2 || row >= a.row_end[a.nmat - 1]) return;
-        uint32_t mi = 0;
+        const uint32_t nrows = a.row_end[a.nmat - 1];
 #pragma unroll
-        for (int i = 0; i < 3; ++i)
-            if ((uint32_t)i + 1 < a.nmat && row >= a.row_end[i]) mi = (uint32_t)i + 1;
-        const uint32_t l = row - (mi ? a.row_end[mi - 1] : 0u);
-        a.raw[mi][l] = v;
-        if (mi == 0 && a.conv_w != nullptr) {
-            // causal depthwise convolution step of channel l (reference_kernels.cpp:197-225) + SiLU
-            float* h = a.history + (uint64_t)l * a.conv_kernel;
-            const float* wc = a.conv_w + (uint64_t)l * a.conv_kernel;
-            double sum = 0.0;
-            for (uint32_t i = 0; i < a.conv_kernel; ++i) {
+        for (int r = 0; r < 2; ++r) {
+            const uint32_t row = (uint32_t)grp * 2u + (uint32_t)r;
+            if (row >= nrows) break;
+            uint32_t mi, l;
+            blk_in_row(a, row, mi, l);
+            const float v = r == 0 ? v0 : v1;
+            if (lane == r) a.raw[mi][l] = v;
+            if (mi == 0 && a.conv_w != nullptr) {
+                // causal depthwise convolution step of channel l (reference_kernels.cpp:197-225) +
+                // SiLU: the history shifts by one (tap i takes value i + 1, the last tap the new
+                // output), then the taps are summed in tap order, in double, as the reference does
+                const uint32_t K = a.conv_kernel, i = (uint32_t)lane - 16u * (uint32_t)r;
+                const bool mine = i < K;  // lanes 16 r .. 16 r + K - 1
+                const float t = i + 1 < K ? pf.v[0] : v;
+                double p = 0.0;
+                if (mine) {
+                    a.history[(uint64_t)l * K + i] = t;
+                    p = (double)t * (double)pf.v[1];
+                }
+                double sum = 0.0;
+                for (uint32_t j = 0; j < K; ++j) {
 #pragma clang fp contract(off)
-                const float t = i + 1 < a.conv_kernel ? h[i + 1] : v;
-                h[i] = t;
-                sum += (double)t * (double)wc[i];
+                    sum += readlane_f64(p, 16 * r + (int)j);
+                }
+                if (lane == r) a.conv_out[l] = blk::silu_ref((float)sum);
+            } else if (mi == 2 && a.beta_s != nullptr) {
+                if (lane == r) a.beta_s[l] = blk::sigmoid_ref(v);
+            } else if (mi == 3 && a.log_decay != nullptr) {
+                if (lane == 16 * r) {
+#pragma clang fp contract(off)
+                    a.log_decay[l] = blk::softplus_ref(v + pf.v[0]) * pf.v[1];
+                }
             }
-            a.conv_out[l] = blk::silu_ref((float)sum);
-        } else if (mi == 2 && a.beta_s != nullptr) {
-            a.beta_s[l] = blk::sigmoid_ref(v);
-        } else if (mi == 3 && a.log_decay != nullptr) {
-#pragma clang fp contract(off)
-            a.log_decay[l] = blk::softplus_ref(v + a.dt_bias[l]) * a.decay[l];
         }
     }
 }
@@ -159,7 +211,8 @@ __global__ __launch_bounds__(512) void gemv_block_kernel(BlockGemv a) {
         }
     }
     asm volatile("" ::: "memory");
-    blk_load_group<TYPE, ITERS, MODE, FULL>(A, a, active ? wave : groups - 1, lane);
+    EpiPf pf[2] = {};
+    blk_load_group<TYPE, ITERS, MODE, FULL>(A, pf[0], a, active ? wave : groups - 1, lane);
     if (a.norm_w) {
         // RMSNorm (qwen35_block.cpp:161-186): sum of squares in double over the whole row
         double ss = 0.0;
@@ -226,18 +279,12 @@ __global__ __launch_bounds__(512) void gemv_block_kernel(BlockGemv a) {
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] += lane_dot(decode_w<TYPE>(A[r][it], ss, q), act[it]);
         }
-        float out = 0.0f, other = 0.0f;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float v = wave_sum_uniform(acc[r]);
-            out = lane == r ? v : out;
-            if (r == 1) other = v;
-        }
-        // the next group's weights go out before the epilogue, whose own loads (convolution
-        // history and taps) then wait behind them instead of delaying them
+        const float v0 = wave_sum_uniform(acc[0]), v1 = wave_sum_uniform(acc[1]);
+        // the next group's weights and epilogue operands go out before this group's epilogue
         const uint64_t next = grp + nw;
-        if (next < groups) blk_load_group<TYPE, ITERS, MODE, FULL>(A, a, next, lane);
-        blk_epilogue<MODE>(a, grp, lane, out, other);
+        pf[1] = pf[0];
+        if (next < groups) blk_load_group<TYPE, ITERS, MODE, FULL>(A, pf[0], a, next, lane);
+        blk_epilogue<MODE>(a, grp, lane, v0, v1, pf[1]);
         grp = next;
         if (grp >= groups) break;
     }
