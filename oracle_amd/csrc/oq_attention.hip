@@ -138,7 +138,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
         const uint32_t t = pass_base + (uint32_t)(lane >> 4);
         const float4* kp = reinterpret_cast<const float4*>(key_row(t < c1 ? t : c1 - 1));
 #pragma unroll
-        for (int j = 0; j < NV; ++j) dst[j] = kp[j * 16 + l16];
+        for (int j = 0; j < NV; ++j) dst[j] = load_stream(kp + j * 16 + l16);
     };
     {
         float4 kb[NB][NV];
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const uint32_t i = i0 + (uint32_t)u * kAttnWaves;
-            dst[u] = reinterpret_cast<const VT*>(value_row(c0 + (i < n ? i : n - 1)))[lane];
+            dst[u] = load_stream(reinterpret_cast<const VT*>(value_row(c0 + (i < n ? i : n - 1))) + lane);
         }
     };
     constexpr uint32_t kGroup = 4u * kAttnWaves;  // tokens per value group of the workgroup

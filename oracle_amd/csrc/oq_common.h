@@ -18,6 +18,28 @@ namespace oq {
 
 OQ_DEVICE float bits_f32(uint32_t u) { return __uint_as_float(u); }
 
+// Loads of data read once per launch (weights, cached keys and values), marked non-temporal:
+// streamed through the caches at the lowest retention, they do not evict the activation rows that
+// every workgroup reads (measured: 12288 x 4096 q4_K GEMV 7.23 -> 7.07 us, 151936 x 4096 q6_K
+// head 87.7 -> 79.5 us).
+OQ_DEVICE uint32_t load_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+OQ_DEVICE float load_stream(const float* p) { return __builtin_nontemporal_load(p); }
+OQ_DEVICE float2 load_stream(const float2* p) {
+    typedef float v2 __attribute__((ext_vector_type(2)));
+    const v2 v = __builtin_nontemporal_load(reinterpret_cast<const v2*>(p));
+    return make_float2(v.x, v.y);
+}
+OQ_DEVICE float4 load_stream(const float4* p) {
+    typedef float v4 __attribute__((ext_vector_type(4)));
+    const v4 v = __builtin_nontemporal_load(reinterpret_cast<const v4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+OQ_DEVICE uint4 load_stream(const uint4* p) {
+    typedef unsigned v4 __attribute__((ext_vector_type(4)));
+    const v4 v = __builtin_nontemporal_load(reinterpret_cast<const v4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Exact binary16 -> binary32 that keeps NaN payloads bit for bit (the hardware conversion
 // quiets signalling NaNs; the reference's f16_to_f32, src/model/storage_decode.cpp:150-176,
 // does not).  Subnormals: value = mantissa * 2^-24, exact in F32.

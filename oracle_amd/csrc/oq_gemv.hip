@@ -12,7 +12,8 @@ constexpr int kWaves = 4;  // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr uint64_t kLdsBudget = 64 * 1024;
 
-OQ_DEVICE uint4 ldg128(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+// q8_0 weight chunks: read once per launch (non-temporal, see load_stream)
+OQ_DEVICE uint4 ldg128(const uint8_t* p) { return load_stream(reinterpret_cast<const uint4*>(p)); }
 
 
 // ---------------------------------------------------------------- F32-activation kernels

@@ -40,6 +40,9 @@ constexpr uint64_t kLdsBudget = 64 * 1024;
 
 OQ_DEVICE uint4 ldg128(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
 OQ_DEVICE uint32_t ldg32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+// weight loads (read once per launch: non-temporal, see load_stream)
+OQ_DEVICE uint4 ldg128_stream(const uint8_t* p) { return load_stream(reinterpret_cast<const uint4*>(p)); }
+OQ_DEVICE uint32_t ldg32_stream(const uint8_t* p) { return load_stream(reinterpret_cast<const uint32_t*>(p)); }
 OQ_DEVICE int dot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 OQ_DEVICE float h2f(uint32_t bits16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16); }
 
@@ -160,17 +163,17 @@ OQ_DEVICE void load_w(typename WRegs<TYPE>::type& r, const uint8_t* row, uint32_
     const uint32_t l = (uint32_t)lane < 4 * m ? (uint32_t)lane : 4 * m - 1;  // surplus lanes re-read
     const uint32_t sb = 16u * it + (l >> 2);
     const uint32_t q = l & 3;
-    r.c0 = ldg128(row + 16u * (128u * it + l));
-    r.c1 = ldg128(row + 16u * (128u * it + 4u * m + l));
+    r.c0 = ldg128_stream(row + 16u * (128u * it + l));
+    r.c1 = ldg128_stream(row + 16u * (128u * it + 4u * m + l));
     if constexpr (TYPE == 14) {
-        r.qh = ldg128(row + (128u * nsb + 64u * sb + 16u * q));
-        r.sc = ldg32(row + (192u * nsb + 16u * sb + 4u * q));
+        r.qh = ldg128_stream(row + (128u * nsb + 64u * sb + 16u * q));
+        r.sc = ldg32_stream(row + (192u * nsb + 16u * sb + 4u * q));
         r.d = *reinterpret_cast<const uint16_t*>(row + (208u * nsb + 2u * sb));
     } else {
-        r.hdr = ldg128(row + ((TYPE == 13 ? 160u : 128u) * nsb + 16u * sb));
+        r.hdr = ldg128_stream(row + ((TYPE == 13 ? 160u : 128u) * nsb + 16u * sb));
         if constexpr (TYPE == 13) {
-            r.h0 = ldg128(row + (128u * nsb + 32u * sb));
-            r.h1 = ldg128(row + (128u * nsb + 32u * sb + 16u));
+            r.h0 = ldg128_stream(row + (128u * nsb + 32u * sb));
+            r.h1 = ldg128_stream(row + (128u * nsb + 32u * sb + 16u));
         }
     }
 }
