@@ -277,7 +277,7 @@ __global__ __launch_bounds__(512) void gemv_block_kernel(BlockGemv a) {
             const uint64_t sb = 16u * it + (lane >> 2);
             if (!FULL && sb >= nsb) continue;
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] += lane_dot(decode_w<TYPE>(A[r][it], ss, q), act[it]);
+            for (int r = 0; r < R; ++r) acc[r] = lane_fma(decode_w<TYPE>(A[r][it], ss, q), act[it], acc[r]);
         }
         const float v0 = wave_sum_uniform(acc[0]), v1 = wave_sum_uniform(acc[1]);
         // the next group's weights and epilogue operands go out before this group's epilogue
@@ -397,11 +397,11 @@ __global__ __launch_bounds__(1024) void gemv_block_add_stream_kernel(BlockGemv a
             const uint32_t sb = 16u * (uint32_t)its + (lane >> 2);
             if (FULL || sb < nsb) {
                 if constexpr (kActRegs) {
-                    acc += lane_dot(decode_w<TYPE>(buf[j & 1], ss, q), act[its]);
+                    acc = lane_fma(decode_w<TYPE>(buf[j & 1], ss, q), act[its], acc);
                 } else {
                     Act av;
                     slice_from_lds<TYPE>(av, s, 0, sb, q);
-                    acc += lane_dot(decode_w<TYPE>(buf[j & 1], ss, q), av);
+                    acc = lane_fma(decode_w<TYPE>(buf[j & 1], ss, q), av, acc);
                 }
             }
             if (it == ITERS - 1) {

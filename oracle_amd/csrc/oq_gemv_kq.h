@@ -257,7 +257,10 @@ OQ_DEVICE int dot16(const uint32_t* w, const uint4 x, int acc) {
     return acc;
 }
 
-OQ_DEVICE float lane_dot(const Dec45& w, const Act& a) {
+// A lane's share of one pass: the activation block's scale times lane_inner, accumulated as one
+// fused multiply-add (lane_fma) in every kernel, so that kernels splitting the passes of a row
+// differently give the same bits.
+OQ_DEVICE float lane_inner(const Dec45& w, const Act& a) {
     int slo = dot16(w.lo, a.x0, 0);
     slo = dot16(w.lo + 4, a.x1, slo);
     int shi = dot16(w.hi, a.x2, 0);
@@ -266,17 +269,22 @@ OQ_DEVICE float lane_dot(const Dec45& w, const Act& a) {
     // 24-bit multiplies are exact here
     const int isum = __mul24(w.sc0, slo) + __mul24(w.sc1, shi);
     const int imin = __mul24(w.mn0, a.b[0] + a.b[1]) + __mul24(w.mn1, a.b[2] + a.b[3]);
-    return a.d * (w.d * (float)isum - w.dmin * (float)imin);
+    return w.d * (float)isum - w.dmin * (float)imin;
 }
 
-OQ_DEVICE float lane_dot(const Dec6& w, const Act& a) {
+OQ_DEVICE float lane_inner(const Dec6& w, const Act& a) {
     const int p0 = dot16(w.s[0], a.x0, 0) - 32 * a.b[0];
     const int p1 = dot16(w.s[1], a.x1, 0) - 32 * a.b[1];
     const int p2 = dot16(w.s[2], a.x2, 0) - 32 * a.b[2];
     const int p3 = dot16(w.s[3], a.x3, 0) - 32 * a.b[3];
     // |p_i| <= 16*63*127 + 32*16*127, |sc| <= 128: exact in 24-bit multiplies
     const int isum = __mul24(w.sc[0], p0) + __mul24(w.sc[1], p1) + __mul24(w.sc[2], p2) + __mul24(w.sc[3], p3);
-    return a.d * (w.d * (float)isum);
+    return w.d * (float)isum;
+}
+
+template <typename Dec>
+OQ_DEVICE float lane_fma(const Dec& w, const Act& a, float acc) {
+    return __builtin_fmaf(a.d, lane_inner(w, a), acc);
 }
 
 // ---------------------------------------------------------------- kernel
@@ -314,7 +322,7 @@ OQ_DEVICE void finish_group(const typename WRegs<TYPE>::type (&W)[R][ITERS], con
         if (!FULL && sb >= nsb) continue;  // FULL: K is a multiple of 4096, every lane has a slot
         if constexpr (MT == 1) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r][0] += lane_dot(decode_w<TYPE>(W[r][it], ss, q), act[it]);
+            for (int r = 0; r < R; ++r) acc[r][0] = lane_fma(decode_w<TYPE>(W[r][it], ss, q), act[it], acc[r][0]);
         } else {
             // each activation slice is read from LDS once for the R rows
             decltype(decode_w<TYPE>(W[0][it], ss, q)) dec[R];
@@ -326,7 +334,7 @@ OQ_DEVICE void finish_group(const typename WRegs<TYPE>::type (&W)[R][ITERS], con
                     Act a;
                     slice_from_lds<TYPE>(a, s, mi, sb, q);
 #pragma unroll
-                    for (int r = 0; r < R; ++r) acc[r][mi] += lane_dot(dec[r], a);
+                    for (int r = 0; r < R; ++r) acc[r][mi] = lane_fma(dec[r], a, acc[r][mi]);
                 }
             }
         }
@@ -577,11 +585,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_stream_kernel(DeviceMatrix w,
             const uint32_t sb = 16u * (uint32_t)its + (lane >> 2);
             if (FULL || sb < nsb) {
                 if constexpr (kActRegs) {
-                    acc += lane_dot(decode_w<TYPE>(buf[j & 1], ss, q), act[its]);
+                    acc = lane_fma(decode_w<TYPE>(buf[j & 1], ss, q), act[its], acc);
                 } else {
                     Act a;
                     slice_from_lds<TYPE>(a, s, 0, sb, q);
-                    acc += lane_dot(decode_w<TYPE>(buf[j & 1], ss, q), a);
+                    acc = lane_fma(decode_w<TYPE>(buf[j & 1], ss, q), a, acc);
                 }
             }
             if (it == ITERS - 1) {
@@ -786,7 +794,7 @@ __global__ __launch_bounds__(1024) void gemv_stream_mt_kernel(DeviceMatrix w, in
                     if (mi < m) {
                         Act a;
                         slice_from_lds<TYPE>(a, s, mi, sb, q);
-                        acc[mi] += lane_dot(dec, a);
+                        acc[mi] = lane_fma(dec, a, acc[mi]);
                     }
                 }
             }
@@ -937,7 +945,7 @@ __global__ __launch_bounds__(1024) void gemv_stream_win_kernel(DeviceMatrix w, i
                     if (mi < m) {
                         Act a;
                         slice_from_lds<TYPE>(a, s, mi, sb - sb0, q);
-                        acc[mi] += lane_dot(dec, a);
+                        acc[mi] = lane_fma(dec, a, acc[mi]);
                     }
                 }
             }
