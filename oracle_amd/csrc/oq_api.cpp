@@ -293,11 +293,12 @@ int check_block_weight(oq_context* ctx, const oq_weight* w, uint64_t ne0, uint64
     return OQ_OK;
 }
 
-// Workspace of one block step: the trace fields, then beta_s, log_decay and the normalised input,
-// each padded to 64 floats so every projection input is 256-byte aligned.
+// Workspace of one block step: the trace fields, then beta_s, log_decay, the normalised input, the
+// delta rule's per-chunk sums of squares and SiLU(z), each padded to 64 floats so every projection
+// input is 256-byte aligned.
 struct BlockLayout {
-    uint64_t sizes[18];
-    uint64_t off[18];
+    uint64_t sizes[19];
+    uint64_t off[19];
     uint64_t total_floats;
 };
 
@@ -306,8 +307,8 @@ BlockLayout block_layout(const oq_deltanet_block* b) {
                    F = b->ffn;
     const uint64_t V = Hv * dv, C = 2 * Hk * dk + V;
     // the last field: the delta rule's per-chunk double sums of squares (2 floats each)
-    BlockLayout l{{C, V, Hv, Hv, C, V, V, E, E, E, F, F, F, E, Hv, Hv, E, 2 * Hv * oq::delta_chunks(dv)}, {}, 0};
-    for (int i = 0; i < 18; ++i) {
+    BlockLayout l{{C, V, Hv, Hv, C, V, V, E, E, E, F, F, F, E, Hv, Hv, E, 2 * Hv * oq::delta_chunks(dv), V}, {}, 0};
+    for (int i = 0; i < 19; ++i) {
         l.off[i] = l.total_floats;
         l.total_floats += (l.sizes[i] + 63) & ~uint64_t(63);
     }
@@ -367,6 +368,7 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
           *gate = ws + off[10], *up = ws + off[11], *act = ws + off[12], *ffn = ws + off[13], *beta_s = ws + off[14],
           *log_decay = ws + off[15], *normed = ws + off[16];
     double* head_ss = reinterpret_cast<double*>(ws + off[17]);
+    float* z_silu = ws + off[18];
     hipStream_t s = ctx->stream;
     hipError_t e = hipSuccess;
     // Fused path: five launches (normed in-projections with the convolution and gates, the delta
@@ -406,10 +408,11 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
     outp.sum_out = resid;
     outp.eps = b->eps;
     if (oq::gemv_block_add_streams(outp)) {
-        // the out projection forms the gated activation in its staging (and stores it)
+        // the out projection forms the gated activation in its staging (and stores it), from
+        // SiLU(z) formed by the delta rule's launch
         outp.rec = rec;
         outp.head_ss = head_ss;
-        outp.z = z;
+        outp.z = z_silu;
         outp.out_norm = b->out_norm;
         outp.dv = (uint32_t)dv;
         outp.dchunks = (uint32_t)oq::delta_chunks(dv);
@@ -440,7 +443,9 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
                        oq::gemv_block_supported(down);
     if (fused) {
         e = oq::launch_gemv_block(oq::kBlockIn, in, s);
-        if (e == hipSuccess) e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, rec, head_ss, s);
+        if (e == hipSuccess)
+            e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, rec, head_ss,
+                                 outp.rec != nullptr ? z : nullptr, outp.rec != nullptr ? z_silu : nullptr, s);
         if (e == hipSuccess && outp.rec == nullptr)
             e = oq::launch_gated_norm(rec, head_ss, z, b->out_norm, Hv, dv, b->eps, gated, s);
         if (e == hipSuccess) e = oq::launch_gemv_block(oq::kBlockAdd, outp, s);
@@ -455,7 +460,9 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
         if (e == hipSuccess)
             e = oq::launch_conv_gates(qkv, b->conv_weight, hist, C, K, beta, alpha, b->dt_bias, b->decay, Hv, conv, beta_s,
                                       log_decay, s);
-        if (e == hipSuccess) e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, rec, head_ss, s);
+        if (e == hipSuccess)
+            e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, rec, head_ss, nullptr, nullptr,
+                                 s);
         if (e == hipSuccess) e = oq::launch_gated_norm(rec, head_ss, z, b->out_norm, Hv, dv, b->eps, gated, s);
         if (e == hipSuccess) e = block_project(b->out, gated, branch, s);
         if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s);

@@ -299,7 +299,9 @@ __global__ __launch_bounds__(512) void gemv_block_kernel(BlockGemv a) {
 // Stages the recurrent block's gated output as the activation row (Q8_K in LDS): value i of head
 // h = i / dv is ((rec[i] * inv_rms(h)) * out_norm[i % dv]) * SiLU(z[i]) (qwen35_block.cpp:579-588),
 // inv_rms(h) = 1 / sqrt(ss_h / dv + eps) with ss_h the delta rule's per-chunk sums of squares
-// added in chunk order.  dv is a multiple of 32, so a lane's four values share one head.
+// added in chunk order, SiLU(z[i]) as the delta rule's launch stored it (a.z).  dv is a multiple of
+// 32, so a lane's four values share one head.
+constexpr uint32_t kMaxHeadChunks = 8;  // value_dim <= 256 in chunks of 32 columns
 template <uint32_t TYPE, int ITERS, int WAVES>
 OQ_DEVICE void stage_gated_row(const ActLds& s, const BlockGemv& a, uint64_t nsb, int wave_in_wg, int lane) {
 #pragma clang fp contract(off)
@@ -314,9 +316,15 @@ OQ_DEVICE void stage_gated_row(const ActLds& s, const BlockGemv& a, uint64_t nsb
         rv[j] = *reinterpret_cast<const float4*>(a.rec + i);
         zv[j] = *reinterpret_cast<const float4*>(a.z + i);
         wv[j] = *reinterpret_cast<const float4*>(a.out_norm + i % a.dv);
+        // the head's chunk sums, requested together (at most kMaxHeadChunks), then added in order
         const double* hs = a.head_ss + (i / a.dv) * a.dchunks;
+        double hv[kMaxHeadChunks];
+#pragma unroll
+        for (uint32_t c = 0; c < kMaxHeadChunks; ++c) hv[c] = c < a.dchunks ? hs[c] : 0.0;
         double ss = 0.0;
-        for (uint32_t c = 0; c < a.dchunks; ++c) ss += hs[c];
+#pragma unroll
+        for (uint32_t c = 0; c < kMaxHeadChunks; ++c)
+            if (c < a.dchunks) ss += hv[c];
         ssv[j] = ss;
     }
 #pragma unroll
@@ -325,10 +333,10 @@ OQ_DEVICE void stage_gated_row(const ActLds& s, const BlockGemv& a, uint64_t nsb
         if (b >= nsb) break;
         const float inv = (float)(1.0 / sqrt(ssv[j] / (double)a.dv + (double)a.eps));
         float4 g;
-        g.x = rv[j].x * inv * wv[j].x * blk::silu_ref(zv[j].x);
-        g.y = rv[j].y * inv * wv[j].y * blk::silu_ref(zv[j].y);
-        g.z = rv[j].z * inv * wv[j].z * blk::silu_ref(zv[j].z);
-        g.w = rv[j].w * inv * wv[j].w * blk::silu_ref(zv[j].w);
+        g.x = rv[j].x * inv * wv[j].x * zv[j].x;
+        g.y = rv[j].y * inv * wv[j].y * zv[j].y;
+        g.z = rv[j].z * inv * wv[j].z * zv[j].z;
+        g.w = rv[j].w * inv * wv[j].w * zv[j].w;
         if (blockIdx.x == 0) reinterpret_cast<float4*>(a.gated_out + b * kQK)[lane] = g;
         uint32_t qw;
         int bs;

@@ -142,9 +142,11 @@ hipError_t launch_conv_gates(const float* qkv, const float* conv_w, float* histo
                              hipStream_t s);
 // the delta rule over Hv * dv/32 workgroups: rec_out[Hv][dv] and head_ss[Hv][dv/32], the per-chunk double
 // sums of rec_out^2 that the head's gated RMSNorm takes (launch_gated_norm, or the out projection's staging)
+// z / z_silu: when not null, the launch also stores SiLU(z) of the block's gate row (the value
+// heads' columns, [Hv][dv]) for the out projection's staging
 hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_heads, uint64_t dk, uint64_t dv,
                         const float* beta_s, const float* log_decay, float eps, float* state, float* rec_out,
-                        double* head_ss, hipStream_t s);
+                        double* head_ss, const float* z, float* z_silu, hipStream_t s);
 hipError_t launch_gated_norm(const float* rec, const double* head_ss, const float* z, const float* out_norm,
                              uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s);
 uint64_t delta_chunks(uint64_t dv);  // head_ss entries per head
@@ -213,11 +215,11 @@ struct BlockGemv {
     float* act;            // FFN: SiLU(gate) * up
     // ADD, streamed: when rec is not null the activation is the recurrent block's gated output,
     // formed in the staging from the delta rule's output: x = RMSNorm_head(rec) * out_norm *
-    // SiLU(z) with each head's sum of squares from head_ss[h * dchunks ...] (eps as above);
-    // workgroup 0 stores it to gated_out
+    // SiLU(z) with each head's sum of squares from head_ss[h * dchunks ...] (eps as above) and
+    // z_silu = SiLU(z) as the delta rule's launch stores it; workgroup 0 stores x to gated_out
     const float* rec;
     const double* head_ss;
-    const float* z;
+    const float* z;        // SiLU(z), [Hv][dv]
     const float* out_norm;
     uint32_t dv, dchunks;
     float* gated_out;
