@@ -2,30 +2,30 @@
 //
 // Y[m][n] = sum_k Xhat[m][k] * W[n][k] with Xhat the dequantized Q8_K activations (d*q) and W
 // the reference's decoded weights ((d*sc)*q - dmin*m for q4_K / q5_K, src/model/storage_decode.cpp
-// :63-94; (d*sc)*q for q6_K, :96-125).  q4_K runs the kernels below whose MFMA waves convert the
-// weights in registers (gemm_q4k_ws_kernel by default: 64.7 us at M = 512, 4096 x 12288, against
-// 80.6 us for the kernel further down); q5_K and q6_K run gemm_kq_kernel, whose load waves convert
-// each step's weights into an f16 B tile in LDS.  Both operands are rounded once to binary16 and multiplied on
-// v_mfma_f32_32x32x16_f16 with F32 accumulation.  The rounding is relative 2^-11 per operand;
-// over K >= 4096 terms its effect on an output stays below 1e-4 * sum_k |w_k * xhat_k| with a
-// wide margin (checked by the parity tests), so the path is enabled only for K >= 4096.
+// :63-94; (d*sc)*q for q6_K, :96-125).  q4_K and q5_K run gemm_ws_kernel, whose MFMA waves convert
+// the weights in registers while load waves stage every tile in LDS (q4_K 64.7 us at M = 512,
+// 4096 x 12288); q6_K runs gemm_kq_kernel, whose load waves convert each step's weights into an
+// f16 B tile in LDS (q4_K through it: 80.6 us).  Both operands are rounded once to binary16 and
+// multiplied on v_mfma_f32_32x32x16_f16 with F32 accumulation.  The rounding is relative 2^-11
+// per operand; over K >= 4096 terms its effect on an output stays below 1e-4 * sum_k |w_k * xhat_k|
+// with a wide margin (checked by the parity tests), so the path is enabled only for K >= 4096.
+// Every kernel of a weight type forms the same f16 operands and adds the products in the same
+// order, so they agree bit for bit.
 //
 // Data flow (one call):
 //   1. activations -> F16 image Xhat[m][K] in scratch.  From F32 x the Q8_K quantization is
 //      the one of quantize_q8k (bit-identical q and d) and Xhat = f16(d*q); caller-supplied
 //      Q8_K blocks are converted the same way.
-//   2. GEMM: a 128 (m) x 256 (n) output tile per 256-thread workgroup (one wave per SIMD)
-//      over one K-split of whole super-blocks, in steps of 64 k.  Wave w owns all 128 rows and
-//      64 columns (4 x 2 accumulators of 32 x 32).  It dequantizes its own weight columns
-//      straight into MFMA B operands in registers (no LDS), while the activation tiles are
-//      shared through a ring of three LDS buffers.  A wave can retire only about one 1 KB LDS
-//      read per 50 cycles, so the LDS traffic is what limits a GEMM with one wave per SIMD;
-//      keeping the weights out of LDS leaves 16 operand reads + 4 stores per wave per step.
+//   2. GEMM: a 128 (m) x 256 (n) output tile per workgroup over one K-split of whole
+//      super-blocks, in steps of 64 k.  MFMA wave w owns all 128 rows and 64 columns (4 x 2
+//      accumulators of 32 x 32).
 //   3. with more than one K-split, partial tiles go to scratch and a reduction kernel adds
 //      them in split order (deterministic).
 //
-// Weight dequantization: a nibble goes to F32 exactly (v_cvt_f32_ubyte), one F32 fma applies
-// the scale and the min, and v_cvt_pk_f16_f32 rounds two weights to f16 (nearest even); the
+// Weight dequantization (FAST, K >= 8192): a quant pair becomes exact f16 integers (a nibble read
+// as fp8 e4m3 and converted with scale 2^9; a 5- or 6-bit value by a byte permute under the f16
+// exponent of 1024, minus 1024) and one packed f16 fma applies the f16-rounded scale and min.
+// Below K = 8192 the scale and min are applied in F32 and the result rounded to f16 once.  The
 // conversion instructions are interleaved with the MFMAs, which execute asynchronously.
 #include <type_traits>
 
@@ -212,6 +212,47 @@ OQ_DEVICE uint32_t weight_pair(uint32_t nib, const ScaleT<FAST>& s) {
         const float2v f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(nib, 512.0f, P != 0);
         return pack_f16(__builtin_fmaf(f.x, s.ds, -s.dm), __builtin_fmaf(f.y, s.ds, -s.dm));
     }
+}
+
+OQ_DEVICE uint32_t dword_of(uint4 v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
+
+// Bytes (2P, 2P+1) of a word of quant values (below 256) as the f16 pair {1024 + q0, 1024 + q1}:
+// one byte permute that puts 0x64 (the high byte of f16 1024) above each quant byte.
+template <int P>
+OQ_DEVICE half2v f16_1024_pair(uint32_t v) {
+    const uint32_t sel = P ? 0x04030402u : 0x04010400u;
+    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, v, sel));
+}
+
+// Two weights (bytes 2P, 2P+1 of the word of 5-bit quants q) of a q5_K sub-block: (d sc) q - dmin m,
+// with the same scale state and rounding as weight_pair.
+template <bool FAST, int P>
+OQ_DEVICE uint32_t q5_pair(uint32_t q, const ScaleT<FAST>& s) {
+    if constexpr (FAST) {
+        const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const half2v x = f16_1024_pair<P>(q) - k1024;  // exact integers 0..31
+        const half2v sv = __builtin_bit_cast(half2v, s.v);
+        const half2v r = __builtin_elementwise_fma(x, __builtin_shufflevector(sv, sv, 0, 0),
+                                                   __builtin_shufflevector(sv, sv, 1, 1));
+        return __builtin_bit_cast(uint32_t, r);
+    } else {
+        const float a = (float)((q >> (16 * P)) & 0xFFu), b = (float)((q >> (16 * P + 8)) & 0xFFu);
+        return pack_f16(__builtin_fmaf(a, s.ds, -s.dm), __builtin_fmaf(b, s.ds, -s.dm));
+    }
+}
+
+// q4_K (TYPE 12) or q5_K (13) weight pair from a word of quant bytes (nibbles, or 5-bit values)
+template <uint32_t TYPE, bool FAST, int P>
+OQ_DEVICE uint32_t k_pair(uint32_t q, const ScaleT<FAST>& s) {
+    if constexpr (TYPE == 13) return q5_pair<FAST, P>(q, s);
+    else return weight_pair<FAST, P>(q, s);
+}
+
+// The fifth bits of q5_K slice ks of group g for bytes 4e .. 4e + 3 of a lane's chunk half, moved
+// to bit 4 of each byte: byte l of the lane's 16-byte high-bit half holds bit 2g + (ks & 1) for
+// element l of that half (GGML block_q5_K qh, src/model/storage_decode.cpp:63-94).
+OQ_DEVICE uint32_t q5_high(uint4 qh, int ks, int g, int e) {
+    return ((dword_of(qh, 2 * (ks >> 1) + e) >> (2 * g + (ks & 1))) & 0x01010101u) << 4;
 }
 
 // ---------------------------------------------------------------- wave state
@@ -511,41 +552,51 @@ __global__ __launch_bounds__(kThreads) void gemm_q4k_f16_kernel(DeviceMatrix w, 
 // LDS reads, conversions and MFMAs: no global load latency reaches them through the in-order
 // load counter.
 //
-// LDS (dynamic, 136 KB):
+// LDS (dynamic, 136 KB; 152 KB for q5_K):
 //   A ring   4 x 16 KB  activation tile of step s in buffer s % 4 (layout as above)
 //   W ring   2 x 32 KB  the quant chunks of super-block i in slot i % 2: group g, row n, half e
 //                       at g * 8 KB + ((32 n + 16 e) ^ (64 g))
 //   H ring   2 x  4 KB  the headers of super-block i in slot i % 2: row n at 16 n
+//   Q ring   2 x  8 KB  q5_K only: the 32-byte high-bit planes of super-block i in slot i % 2,
+//                       half e of row n at 4096 e + 16 n (a half-wave reads 512 contiguous bytes)
 // Producer p: activation rows 32 p .. 32 p + 31 of each tile (four 16-byte chunks per lane, eight
 // rows of 128 bytes per load instruction) and weight rows 64 p .. 64 p + 63: per super-block 8 KB
 // of quants, loaded as 16 row pieces of 64 contiguous bytes per instruction (four lanes per
-// piece), and one 16-byte header per lane.
+// piece), one 16-byte header per lane and, for q5_K, the lane row's 32-byte high-bit plane.
 // Timing, step s = 4 i + g of the split:
 //   producer: stores tile s + 3 (loaded at step s - 2) into buffer (s + 3) % 4 and loads tile
 //             s + 5; at g = 0 stores super-block i + 1 (loaded during super-block i - 1) into W/H
 //             slot (i + 1) % 2, whose last reader was super-block i - 1, and loads super-block i + 2;
 //   consumer: multiplies step s; during it reads the next step's quant chunks (and at g = 3 the
-//             next super-block's headers) from LDS;
+//             next super-block's headers and high-bit halves) from LDS;
 //   all 8 waves: one barrier per step.
 constexpr uint32_t kWsThreads = 512;
 constexpr uint32_t kWsA = 4 * kTileBytes;   // 64 KB
 constexpr uint32_t kWsWSlot = 32768;
 constexpr uint32_t kWsHSlot = 4096;
+constexpr uint32_t kWsQSlot = 8192;
 constexpr uint32_t kWsLds = kWsA + 2 * kWsWSlot + 2 * kWsHSlot;
+template <uint32_t TYPE>
+constexpr uint32_t ws_lds_bytes() { return kWsLds + (TYPE == 13 ? 2 * kWsQSlot : 0u); }
 
 OQ_DEVICE uint32_t ws_w_off(uint32_t slot, uint32_t g, uint32_t n, uint32_t e) {
     return kWsA + slot * kWsWSlot + g * 8192u + ((32u * n + 16u * e) ^ (64u * g));
 }
 OQ_DEVICE uint32_t ws_h_off(uint32_t slot, uint32_t n) { return kWsA + 2 * kWsWSlot + slot * kWsHSlot + 16u * n; }
+OQ_DEVICE uint32_t ws_q_off(uint32_t slot, uint32_t n, uint32_t e) {
+    return kWsLds + slot * kWsQSlot + 4096u * e + 16u * n;
+}
 
 // consumer: one step (see wave_step); W chunks of this step in wc[j], of the next step in wn[j]
 // (read here from LDS at slice 1), scale state as there; headers of this super-block in hdr,
-// of the next one in hdrn (read at g = 3).
-template <bool FAST, int G>
+// of the next one in hdrn (read at g = 3); for q5_K the lane's high-bit halves of this
+// super-block in qh, of the next one in qhn (read at g = 3).
+template <uint32_t TYPE, bool FAST, int G>
 OQ_DEVICE void ws_consumer_step(const uint8_t* lds, const uint32_t (&rd_off)[4], uint32_t wslot, uint32_t wslot_next,
                                 uint32_t hslot_next, uint32_t n_lane0, uint32_t h, float16v (&acc)[4][2],
                                 half8 (&a)[4], uint32_t (&b)[2][4], const uint4 (&wc)[2], uint4 (&wn)[2],
-                                const uint4 (&hdr)[2], uint4 (&hdrn)[2], ScaleT<FAST> (&sc)[2][2][2]) {
+                                const uint4 (&hdr)[2], uint4 (&hdrn)[2], const uint4 (&qh)[2], uint4 (&qhn)[2],
+                                ScaleT<FAST> (&sc)[2][2][2]) {
     constexpr int G1 = (G + 1) & 3;
     constexpr int P = G & 1;
 #pragma unroll
@@ -581,8 +632,15 @@ OQ_DEVICE void ws_consumer_step(const uint8_t* lds, const uint32_t (&rd_off)[4],
                     nw[jj][0] = nib_word<3>(src, 0);
                     nw[jj][1] = nib_word<3>(src, 1);
                 }
+                if constexpr (TYPE == 13) {
+                    // the next slice's group: G, or G + 1 (of the next super-block when G = 3)
+                    const uint4 qsrc = ks < 3 || G < 3 ? qh[jj] : qhn[jj];
+                    const int grp = ks < 3 ? G : G1;
+                    nw[jj][0] |= q5_high(qsrc, nks, grp, 0);
+                    nw[jj][1] |= q5_high(qsrc, nks, grp, 1);
+                }
             }
-            bn[jj][pp] = (pp & 1) ? weight_pair<FAST, 1>(nw[jj][pp >> 1], scl) : weight_pair<FAST, 0>(nw[jj][pp >> 1], scl);
+            bn[jj][pp] = (pp & 1) ? k_pair<TYPE, FAST, 1>(nw[jj][pp >> 1], scl) : k_pair<TYPE, FAST, 0>(nw[jj][pp >> 1], scl);
             if (ks == 0 && q < 2) {
                 // quant chunks of the next step: group G + 1 of this super-block, or group 0 of the next
                 const uint32_t slot = G < 3 ? wslot : wslot_next;
@@ -590,6 +648,9 @@ OQ_DEVICE void ws_consumer_step(const uint8_t* lds, const uint32_t (&rd_off)[4],
             }
             if (G == 3 && ks == 0 && (q == 2 || q == 3)) {
                 hdrn[q - 2] = *reinterpret_cast<const uint4*>(lds + ws_h_off(hslot_next, n_lane0 + 32u * (q - 2)));
+            }
+            if (TYPE == 13 && G == 3 && ks == 0 && (q == 4 || q == 5)) {
+                qhn[q - 4] = *reinterpret_cast<const uint4*>(lds + ws_q_off(hslot_next, n_lane0 + 32u * (q - 4), h));
             }
             if (ks == 1 && q == 4) {
                 if (G < 3) scale_pairs<FAST, G1>(hdr[0], sc[P ^ 1][0]);
@@ -621,26 +682,43 @@ struct Producer {
     uint32_t hrow_off;     // row * pitch of the lane's header row
 };
 
-OQ_DEVICE void ws_load_sb(const Split& sp, const Producer& pr, uint32_t sb, int lane, uint4 (&wq)[8], uint4& hq) {
+template <uint32_t TYPE>
+OQ_DEVICE void ws_load_sb(const Split& sp, const Producer& pr, uint32_t sb, int lane, uint4 (&wq)[8], uint4& hq,
+                          uint4 (&qq)[2]) {
     const uint32_t pass = sb / 16u, s16 = sb % 16u;
     const uint32_t mp = sp.nsb - 16u * pass < 16u ? sp.nsb - 16u * pass : 16u;
     const uint8_t* qbase = sp.wbase + 16u * (128u * pass + 4u * s16 + (uint32_t)(lane & 3));
 #pragma unroll
     for (int t = 0; t < 8; ++t) wq[t] = load_u4(qbase, pr.wrow_off[t] + pr.w_e[t] * 64u * mp);
     hq = load_u4(sp.wbase + sp.hdr_base + 16u * sb, pr.hrow_off);
+    if constexpr (TYPE == 13) {
+        // the high-bit plane: 32 bytes per super-block after the 128 * nsb quant bytes of the row
+        const uint8_t* qh = sp.wbase + 128u * sp.nsb + 32u * sb;
+        qq[0] = load_u4(qh, pr.hrow_off);
+        qq[1] = load_u4(qh + 16, pr.hrow_off);
+    }
 }
 
-OQ_DEVICE void ws_store_sb(uint8_t* lds, const Producer& pr, uint32_t slot, const uint4 (&wq)[8], uint4 hq, int pw,
-                           int lane) {
+template <uint32_t TYPE>
+OQ_DEVICE void ws_store_sb(uint8_t* lds, const Producer& pr, uint32_t slot, const uint4 (&wq)[8], uint4 hq,
+                           const uint4 (&qq)[2], int pw, int lane) {
 #pragma unroll
     for (int t = 0; t < 8; ++t) *reinterpret_cast<uint4*>(lds + kWsA + slot * kWsWSlot + pr.w_st[t]) = wq[t];
-    *reinterpret_cast<uint4*>(lds + ws_h_off(slot, 64u * (uint32_t)pw + (uint32_t)lane)) = hq;
+    const uint32_t n = 64u * (uint32_t)pw + (uint32_t)lane;
+    *reinterpret_cast<uint4*>(lds + ws_h_off(slot, n)) = hq;
+    if constexpr (TYPE == 13) {
+        *reinterpret_cast<uint4*>(lds + ws_q_off(slot, n, 0)) = qq[0];
+        *reinterpret_cast<uint4*>(lds + ws_q_off(slot, n, 1)) = qq[1];
+    }
 }
 
-template <bool FAST>
-__global__ __launch_bounds__(kWsThreads) void gemm_q4k_ws_kernel(DeviceMatrix w, int m, const _Float16* a16,
-                                                                 uint32_t tiles_n, uint32_t tiles_m, uint32_t splits,
-                                                                 float* __restrict__ out) {
+// q4_K (TYPE 12) and q5_K (13): the same tiles, steps and k order; q5_K adds the high-bit plane
+// (staged beside the headers) to each nibble word before the conversion.
+template <uint32_t TYPE, bool FAST>
+__global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(DeviceMatrix w, int m, const _Float16* a16,
+                                                             uint32_t tiles_n, uint32_t tiles_m, uint32_t splits,
+                                                             float* __restrict__ out) {
+    static_assert(TYPE == 12 || TYPE == 13, "q4_K or q5_K");
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -654,7 +732,7 @@ __global__ __launch_bounds__(kWsThreads) void gemm_q4k_ws_kernel(DeviceMatrix w,
     sp.nsbu = sb1 - sp.sb0;  // >= 1: splits <= nsb
     sp.nsb = nsb;
     sp.last_step = 4 * sp.nsbu - 1;
-    sp.hdr_base = 128u * nsb;
+    sp.hdr_base = (TYPE == 13 ? 160u : 128u) * nsb;
     sp.wbase = w.base;
     sp.a16 = reinterpret_cast<const uint8_t*>(a16) + 2ull * kQK * sp.sb0;
     const uint32_t nsteps = 4 * sp.nsbu;
@@ -699,24 +777,24 @@ __global__ __launch_bounds__(kWsThreads) void gemm_q4k_ws_kernel(DeviceMatrix w,
             for (int j = 0; j < 4; ++j)
                 *reinterpret_cast<uint4*>(lds + buf * kTileBytes + pr.act_st + 128u * (j & 1) + 2048u * (j >> 1)) = v[j];
         };
-        uint4 av[2][4], wq[8], hq;
+        uint4 av[2][4], wq[8], hq, qq[2];
         // prologue: tiles 0..2, super-block 0 into slot 0; tiles 3, 4 and super-block 1 in flight
         {
             uint4 t0[4], t1[4], t2[4];
             act_load(0, t0);
             act_load(1, t1);
             act_load(2, t2);
-            ws_load_sb(sp, pr, split_sb(sp, 0), lane, wq, hq);
+            ws_load_sb<TYPE>(sp, pr, split_sb(sp, 0), lane, wq, hq, qq);
             act_store(0, t0);
             act_store(1, t1);
             act_store(2, t2);
-            ws_store_sb(lds, pr, 0, wq, hq, pw, lane);
+            ws_store_sb<TYPE>(lds, pr, 0, wq, hq, qq, pw, lane);
         }
         // Issued in the order of a loop trip (tile of set 1, then of set 0), each group whole: the
         // compiler's wait counts at the loop head merge this path with the loop's back edge, and
         // interleaved prologue loads would leave a tile with fewer younger loads here than in the
         // loop, so that every trip would wait for the loads of the step before.
-        ws_load_sb(sp, pr, split_sb(sp, 1), lane, wq, hq);
+        ws_load_sb<TYPE>(sp, pr, split_sb(sp, 1), lane, wq, hq, qq);
         asm volatile("" ::: "memory");
         act_load(3, av[1]);
         asm volatile("" ::: "memory");
@@ -730,8 +808,8 @@ __global__ __launch_bounds__(kWsThreads) void gemm_q4k_ws_kernel(DeviceMatrix w,
                 act_store((uint32_t)((g + 3) & 3), av[as]);
                 act_load(s + g + 5, av[as]);
                 if (g == 0) {
-                    ws_store_sb(lds, pr, (i + 1) & 1, wq, hq, pw, lane);
-                    ws_load_sb(sp, pr, split_sb(sp, i + 2), lane, wq, hq);
+                    ws_store_sb<TYPE>(lds, pr, (i + 1) & 1, wq, hq, qq, pw, lane);
+                    ws_load_sb<TYPE>(sp, pr, split_sb(sp, i + 2), lane, wq, hq, qq);
                 }
                 lds_barrier();
             }
@@ -748,13 +826,16 @@ __global__ __launch_bounds__(kWsThreads) void gemm_q4k_ws_kernel(DeviceMatrix w,
 
     float16v acc[4][2] = {};
     lds_barrier();  // the producers' prologue
-    uint4 wcur[2], wnext[2], hdr[2], hdrn[2];
+    uint4 wcur[2], wnext[2], hdr[2], hdrn[2], qh[2], qhn[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         wcur[j] = *reinterpret_cast<const uint4*>(lds + ws_w_off(0, 0, n_lane0 + 32u * j, h));
         hdr[j] = *reinterpret_cast<const uint4*>(lds + ws_h_off(0, n_lane0 + 32u * j));
         hdrn[j] = hdr[j];
         wnext[j] = wcur[j];
+        if constexpr (TYPE == 13) qh[j] = *reinterpret_cast<const uint4*>(lds + ws_q_off(0, n_lane0 + 32u * j, h));
+        else qh[j] = make_uint4(0u, 0u, 0u, 0u);
+        qhn[j] = qh[j];
     }
     ScaleT<FAST> sc[2][2][2];
     scale_pairs<FAST, 0>(hdr[0], sc[0][0]);
@@ -765,24 +846,34 @@ __global__ __launch_bounds__(kWsThreads) void gemm_q4k_ws_kernel(DeviceMatrix w,
     for (int i = 0; i < 4; ++i) a[i] = lds_read(lds, 4096u * i + rd_off[0]);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const uint32_t w0 = nib_word<0>(wcur[j], 0), w1 = nib_word<0>(wcur[j], 1);
-        b[j][0] = weight_pair<FAST, 0>(w0, sc[0][j][0]);
-        b[j][1] = weight_pair<FAST, 1>(w0, sc[0][j][0]);
-        b[j][2] = weight_pair<FAST, 0>(w1, sc[0][j][0]);
-        b[j][3] = weight_pair<FAST, 1>(w1, sc[0][j][0]);
+        uint32_t w0 = nib_word<0>(wcur[j], 0), w1 = nib_word<0>(wcur[j], 1);
+        if constexpr (TYPE == 13) {
+            w0 |= q5_high(qh[j], 0, 0, 0);
+            w1 |= q5_high(qh[j], 0, 0, 1);
+        }
+        b[j][0] = k_pair<TYPE, FAST, 0>(w0, sc[0][j][0]);
+        b[j][1] = k_pair<TYPE, FAST, 1>(w0, sc[0][j][0]);
+        b[j][2] = k_pair<TYPE, FAST, 0>(w1, sc[0][j][0]);
+        b[j][3] = k_pair<TYPE, FAST, 1>(w1, sc[0][j][0]);
     }
     for (uint32_t s = 0; s < nsteps; s += 4) {
         const uint32_t i = s / 4, slot = i & 1, slot1 = (i + 1) & 1;
-        ws_consumer_step<FAST, 0>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wcur, wnext, hdr, hdrn, sc);
+        ws_consumer_step<TYPE, FAST, 0>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wcur, wnext, hdr, hdrn,
+                                        qh, qhn, sc);
         lds_barrier();
-        ws_consumer_step<FAST, 1>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wnext, wcur, hdr, hdrn, sc);
+        ws_consumer_step<TYPE, FAST, 1>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wnext, wcur, hdr, hdrn,
+                                        qh, qhn, sc);
         lds_barrier();
-        ws_consumer_step<FAST, 2>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wcur, wnext, hdr, hdrn, sc);
+        ws_consumer_step<TYPE, FAST, 2>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wcur, wnext, hdr, hdrn,
+                                        qh, qhn, sc);
         lds_barrier();
-        ws_consumer_step<FAST, 3>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wnext, wcur, hdr, hdrn, sc);
+        ws_consumer_step<TYPE, FAST, 3>(lds, rd_off, slot, slot1, slot1, n_lane0, h, acc, a, b, wnext, wcur, hdr, hdrn,
+                                        qh, qhn, sc);
         lds_barrier();
         hdr[0] = hdrn[0];
         hdr[1] = hdrn[1];
+        qh[0] = qhn[0];
+        qh[1] = qhn[1];
     }
     float* o = out + (uint64_t)z * (uint64_t)m * w.n;
 #pragma unroll
@@ -876,31 +967,6 @@ OQ_DEVICE void kq_load(KqRaw<TYPE>& r, const uint8_t* wb, const uint32_t (&row_o
     }
 }
 
-OQ_DEVICE uint32_t dword_of(uint4 v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
-
-// Bytes (2P, 2P+1) of a word of quant values (below 1024) as the f16 pair {1024 + q0, 1024 + q1}.
-template <int P>
-OQ_DEVICE half2v f16_1024_pair(uint32_t v) {
-    const uint32_t sel = P ? 0x0C030C02u : 0x0C010C00u;
-    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0u, v, sel) | 0x64006400u);
-}
-
-// Two weights (bytes 2P, 2P+1 of the word of 5-bit quants q) of a q5_K sub-block: (d sc) q - dmin m.
-template <bool FAST, int P>
-OQ_DEVICE uint32_t q5_pair(uint32_t q, const ScaleT<FAST>& s) {
-    if constexpr (FAST) {
-        const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-        const half2v x = f16_1024_pair<P>(q) - k1024;  // exact integers 0..31
-        const half2v sv = __builtin_bit_cast(half2v, s.v);
-        const half2v r = __builtin_elementwise_fma(x, __builtin_shufflevector(sv, sv, 0, 0),
-                                                   __builtin_shufflevector(sv, sv, 1, 1));
-        return __builtin_bit_cast(uint32_t, r);
-    } else {
-        const float a = (float)((q >> (16 * P)) & 0xFFu), b = (float)((q >> (16 * P + 8)) & 0xFFu);
-        return pack_f16(__builtin_fmaf(a, s.ds, -s.dm), __builtin_fmaf(b, s.ds, -s.dm));
-    }
-}
-
 // Two weights of a q6_K sub-block from the word of 6-bit codes u (q = u - 32): (d sc) q.
 //   FAST : ds = f16(d * sc) (d * sc is exact in F32), x = q exactly, one v_pk_mul_f16;
 //   exact: F32 (d * sc) * q as the reference, rounded to f16.
@@ -952,8 +1018,7 @@ OQ_DEVICE void kq_convert(const KqRaw<TYPE>& r, uint8_t* bdst, const uint32_t (&
                     const uint32_t dw = dword_of(r.q[pp], 2 * (ks >> 1) + wd);
                     const uint32_t nib = (ks & 1) ? (dw >> 4) & 0x0F0F0F0Fu : dw & 0x0F0F0F0Fu;
                     if constexpr (TYPE == 13) {
-                        const uint32_t hb5 = (dword_of(r.qh[pp], 2 * (ks >> 1) + wd) >> (2 * G + (ks & 1))) & 0x01010101u;
-                        const uint32_t q = nib | (hb5 << 4);
+                        const uint32_t q = nib | q5_high(r.qh[pp], ks, G, wd);
                         out[ks][2 * wd] = q5_pair<FAST, 0>(q, sc[ks & 1]);
                         out[ks][2 * wd + 1] = q5_pair<FAST, 1>(q, sc[ks & 1]);
                     } else {
@@ -1222,6 +1287,18 @@ void launch_kq(const DeviceMatrix& w, int m, const _Float16* a16, const Plan& p,
                        w, m, a16, p.tiles_n, p.tiles_m, p.splits, dst);
 }
 
+template <uint32_t TYPE, bool FAST>
+void launch_ws(const DeviceMatrix& w, int m, const _Float16* a16, const Plan& p, float* dst, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_ws_kernel<TYPE, FAST>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)ws_lds_bytes<TYPE>());
+        attr = true;
+    }
+    hipLaunchKernelGGL((gemm_ws_kernel<TYPE, FAST>), dim3(p.tiles_n * p.tiles_m * p.splits), dim3(kWsThreads),
+                       ws_lds_bytes<TYPE>(), s, w, m, a16, p.tiles_n, p.tiles_m, p.splits, dst);
+}
+
 hipError_t launch_gemm_mfma(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
                                 void* scratch, hipStream_t s) {
     if (!gemm_mfma_supported(w, m) || (x == nullptr) == (q8k == nullptr)) return hipErrorNotSupported;
@@ -1239,33 +1316,16 @@ hipError_t launch_gemm_mfma(const DeviceMatrix& w, int m, const float* x, const 
     }
     const unsigned wgs = p.tiles_n * p.tiles_m * p.splits;
     const bool fast = w.k >= kFastMinK && knob(kGemmExactDequant, 0) == 0;
-    if (w.type != 12 || knob(kGemmWs, 1) == 2) {
-        // the weights converted by the load waves (every type; q4_K with OQ_GEMM_WS=2)
+    if (w.type == 14 || knob(kGemmWs, 1) == 2) {
+        // the weights converted by the load waves (q6_K; every type with OQ_GEMM_WS=2)
         float* dst = p.splits > 1 ? part : y;
         if (w.type == 12) fast ? launch_kq<12, true>(w, m, a16, p, dst, s) : launch_kq<12, false>(w, m, a16, p, dst, s);
         else if (w.type == 13) fast ? launch_kq<13, true>(w, m, a16, p, dst, s) : launch_kq<13, false>(w, m, a16, p, dst, s);
         else fast ? launch_kq<14, true>(w, m, a16, p, dst, s) : launch_kq<14, false>(w, m, a16, p, dst, s);
-    } else if (knob(kGemmWs, 1) != 0) {
+    } else if (knob(kGemmWs, 1) != 0 || w.type == 13) {
         float* dst = p.splits > 1 ? part : y;
-        if (fast) {
-            static bool attr = false;
-            if (!attr) {
-                (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_q4k_ws_kernel<true>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWsLds);
-                attr = true;
-            }
-            hipLaunchKernelGGL(gemm_q4k_ws_kernel<true>, dim3(wgs), dim3(kWsThreads), kWsLds, s, w, m, a16, p.tiles_n,
-                               p.tiles_m, p.splits, dst);
-        } else {
-            static bool attr = false;
-            if (!attr) {
-                (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_q4k_ws_kernel<false>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWsLds);
-                attr = true;
-            }
-            hipLaunchKernelGGL(gemm_q4k_ws_kernel<false>, dim3(wgs), dim3(kWsThreads), kWsLds, s, w, m, a16, p.tiles_n,
-                               p.tiles_m, p.splits, dst);
-        }
+        if (w.type == 13) fast ? launch_ws<13, true>(w, m, a16, p, dst, s) : launch_ws<13, false>(w, m, a16, p, dst, s);
+        else fast ? launch_ws<12, true>(w, m, a16, p, dst, s) : launch_ws<12, false>(w, m, a16, p, dst, s);
     } else if (fast) {
         hipLaunchKernelGGL(gemm_q4k_f16_kernel<true>, dim3(wgs), dim3(kThreads), 0, s, w, m, a16, p.tiles_n,
                            p.tiles_m, p.splits, p.splits > 1 ? part : y);
