@@ -14,9 +14,10 @@
 //                    o[h] += p[h][t] * v_t for the rep heads; the four waves' sums are added in LDS
 //                  -> o_c [rep][D], (m_c, l_c) [rep] for the chunk
 //   merge kernel   one workgroup per (query head, 64 output columns), 16 chunk groups x 16 float4
-//                  columns: each thread folds its chunks into a running (m, l, o) with the usual
-//                  rescaling (every load issued before the first use), the 16 groups are folded in
-//                  LDS the same way: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.  For the
+//                  columns, every load issued before the first use: the largest chunk maximum M
+//                  (over the groups through LDS), then each chunk weighted on its own,
+//                  out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, the groups' sums added in
+//                  LDS (no running rescale: one exp per chunk and no chain of them).  For the
 //                  decoder block also the output gate (gate_s = sigmoid(gate), gated = out * gate_s,
 //                  qwen35_block.cpp:734-741)
 // The reference sums the dot products and the softmax denominator in double and the weighted
@@ -264,17 +265,6 @@ OQ_DEVICE float sigmoid_ref(float v) {
     return e / (1.0f + e);
 }
 
-OQ_DEVICE void fold(float& m, float& l, float4& o, float mc, float lc, float4 oc) {
-    const float mn = fmaxf(m, mc);
-    const float a = expf(m - mn), b = expf(mc - mn);  // m = -inf (nothing folded yet): a = 0
-    l = l * a + lc * b;
-    o.x = o.x * a + oc.x * b;
-    o.y = o.y * a + oc.y * b;
-    o.z = o.z * a + oc.z * b;
-    o.w = o.w * a + oc.w * b;
-    m = mn;
-}
-
 template <int D>
 __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
     constexpr int SLICES = D / 64;
@@ -285,46 +275,82 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
     const int col = threadIdx.x & 15, grp = threadIdx.x >> 4;
     const float* mlp = a.part_ml + ((uint64_t)g * a.rep + r) * a.nchunks * 2;           // [nchunks][2]
     const float* op = a.part_o + (((uint64_t)g * a.rep + r) * SLICES + slice) * a.nchunks * 64;  // [nchunks][64]
-    float m = -INFINITY, l = 0.0f;
+    constexpr uint32_t kPass = kMergeGroups * kMergeUnroll;  // chunks per pass of the workgroup
+    const uint64_t base = (uint64_t)h * D + slice * 64 + (uint64_t)col * 4;
+    // the block's output gate, needed last, requested first
+    float4 gv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.gate != nullptr && grp == 0)
+        gv = *reinterpret_cast<const float4*>(a.gate + (uint64_t)h * a.gate_stride + slice * 64 + col * 4);
+    // the first pass's chunk maxima and sums, then its value slices, all requested before any
+    // use (loads complete in order: M waits only for the maxima)
+    float2 ml[kMergeUnroll];
+    float4 oc[kMergeUnroll];
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+        uint32_t c = (uint32_t)grp + (uint32_t)u * kMergeGroups;
+        c = c < a.nchunks ? c : a.nchunks - 1;
+        ml[u] = *reinterpret_cast<const float2*>(mlp + (uint64_t)c * 2);
+    }
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+        uint32_t c = (uint32_t)grp + (uint32_t)u * kMergeGroups;
+        c = c < a.nchunks ? c : a.nchunks - 1;
+        oc[u] = reinterpret_cast<const float4*>(op + (uint64_t)c * 64)[col];
+    }
+    // 1. M = the largest chunk maximum (every chunk holds at least one token: m_c is finite);
+    //    clamped repeats of the last chunk do not change a maximum
+    float m = ml[0].x;
+#pragma unroll
+    for (int u = 1; u < kMergeUnroll; ++u) m = fmaxf(m, ml[u].x);
+    for (uint32_t c = (uint32_t)grp + kPass; c < a.nchunks; c += kMergeGroups)
+        m = fmaxf(m, mlp[(uint64_t)c * 2]);
+    if (col == 0) s_m[grp] = m;
+    __syncthreads();
+    float M = s_m[0];
+#pragma unroll
+    for (int i = 1; i < kMergeGroups; ++i) M = fmaxf(M, s_m[i]);
+    // 2. out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c: each chunk's weight on its own, the
+    //    sums in chunk order within a group, then over the groups in group order
+    float l = 0.0f;
     float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t c0 = (uint32_t)grp; c0 < a.nchunks; c0 += kMergeGroups * kMergeUnroll) {
-        float2 ml[kMergeUnroll];
-        float4 oc[kMergeUnroll];
 #pragma unroll
-        for (int u = 0; u < kMergeUnroll; ++u) {
-            uint32_t c = c0 + (uint32_t)u * kMergeGroups;
-            c = c < a.nchunks ? c : a.nchunks - 1;
-            ml[u] = *reinterpret_cast<const float2*>(mlp + (uint64_t)c * 2);
-            oc[u] = reinterpret_cast<const float4*>(op + (uint64_t)c * 64)[col];
-        }
-        asm volatile("" ::: "memory");  // all loads of the pass issued before the first fold
-        // every fold unconditional (a branch would let the compiler sink each load behind the
-        // previous fold): chunks past the end fold in as (m = -inf, l = 0), which leaves the
-        // running values unchanged once chunk c0 (always present) is in
-#pragma unroll
-        for (int u = 0; u < kMergeUnroll; ++u) {
-            const bool in = c0 + (uint32_t)u * kMergeGroups < a.nchunks;
-            fold(m, l, o, in ? ml[u].x : -INFINITY, in ? ml[u].y : 0.0f, oc[u]);
-        }
+    for (int u = 0; u < kMergeUnroll; ++u) {
+        const bool in = (uint32_t)grp + (uint32_t)u * kMergeGroups < a.nchunks;
+        const float wgt = in ? expf(ml[u].x - M) : 0.0f;
+        l = fmaf(wgt, ml[u].y, l);
+        o.x = fmaf(wgt, oc[u].x, o.x);
+        o.y = fmaf(wgt, oc[u].y, o.y);
+        o.z = fmaf(wgt, oc[u].z, o.z);
+        o.w = fmaf(wgt, oc[u].w, o.w);
+    }
+    for (uint32_t c = (uint32_t)grp + kPass; c < a.nchunks; c += kMergeGroups) {
+        const float2 v = *reinterpret_cast<const float2*>(mlp + (uint64_t)c * 2);
+        const float4 ov = reinterpret_cast<const float4*>(op + (uint64_t)c * 64)[col];
+        const float wgt = expf(v.x - M);
+        l = fmaf(wgt, v.y, l);
+        o.x = fmaf(wgt, ov.x, o.x);
+        o.y = fmaf(wgt, ov.y, o.y);
+        o.z = fmaf(wgt, ov.z, o.z);
+        o.w = fmaf(wgt, ov.w, o.w);
     }
     s_o[grp][col] = o;
-    if (col == 0) {
-        s_m[grp] = m;
-        s_l[grp] = l;
-    }
+    if (col == 0) s_l[grp] = l;
     __syncthreads();
     if (grp != 0) return;
-    float M = -INFINITY, L = 0.0f;
-    float4 O = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int i = 0; i < kMergeGroups; ++i) {
-        if (s_m[i] == -INFINITY) continue;  // a group without chunks
-        fold(M, L, O, s_m[i], s_l[i], s_o[i][col]);
+    float L = s_l[0];
+    float4 O = s_o[0][col];
+#pragma unroll
+    for (int i = 1; i < kMergeGroups; ++i) {
+        L += s_l[i];
+        const float4 v = s_o[i][col];
+        O.x += v.x;
+        O.y += v.y;
+        O.z += v.z;
+        O.w += v.w;
     }
     const float out[4] = {O.x / L, O.y / L, O.z / L, O.w / L};
-    const uint64_t base = (uint64_t)h * D + slice * 64 + (uint64_t)col * 4;
     *reinterpret_cast<float4*>(a.out + base) = make_float4(out[0], out[1], out[2], out[3]);
     if (a.gate != nullptr) {
-        const float4 gv = *reinterpret_cast<const float4*>(a.gate + (uint64_t)h * a.gate_stride + slice * 64 + col * 4);
         const float gs[4] = {sigmoid_ref(gv.x), sigmoid_ref(gv.y), sigmoid_ref(gv.z), sigmoid_ref(gv.w)};
         *reinterpret_cast<float4*>(a.gate_s + base) = make_float4(gs[0], gs[1], gs[2], gs[3]);
         *reinterpret_cast<float4*>(a.gated + base) = make_float4(out[0] * gs[0], out[1] * gs[1], out[2] * gs[2],
