@@ -373,13 +373,17 @@ OQ_DEVICE void rope_cs(uint32_t f, const RopeParams& p, float& c, float& s) {
     s = (float)sin(angle);
 }
 
-OQ_DEVICE void rope_pair(float* x, uint32_t f, uint32_t half, const RopeParams& p) {
+OQ_DEVICE void rotate_pair(float* x, uint32_t f, uint32_t half, float c, float s) {
 #pragma clang fp contract(off)
-    float c, s;
-    rope_cs(f, p, c, s);
     const float a = x[f], b = x[half + f];
     x[f] = a * c - b * s;
     x[half + f] = b * c + a * s;
+}
+
+OQ_DEVICE void rope_pair(float* x, uint32_t f, uint32_t half, const RopeParams& p) {
+    float c, s;
+    rope_cs(f, p, c, s);
+    rotate_pair(x, f, half, c, s);
 }
 
 __global__ __launch_bounds__(256) void rope_kernel(float* heads, uint32_t head_dim, RopeParams p) {
@@ -401,6 +405,10 @@ __global__ __launch_bounds__(256) void attention_prep_kernel(AttnPrep a) {
     const float* src = is_q ? a.qfull + (uint64_t)head * 2 * D : a.kp + (uint64_t)head * D;
     const float* w = is_q ? a.q_norm : a.k_norm;
     const float x = i < D ? src[i] : 0.0f;
+    // the rotation's cos and sin (double arithmetic, independent of the data) while x arrives
+    const uint32_t half = a.rope.rotary_dim / 2;
+    float rc = 1.0f, rs = 0.0f;
+    if (i < half) rope_cs(i, a.rope, rc, rs);
     double ss = (double)x * (double)x;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
@@ -410,8 +418,7 @@ __global__ __launch_bounds__(256) void attention_prep_kernel(AttnPrep a) {
     const float inv = (float)(1.0 / sqrt(tot / (double)D + (double)a.eps));
     if (i < D) y[i] = x * inv * w[i];
     __syncthreads();
-    const uint32_t half = a.rope.rotary_dim / 2;
-    if (i < half) rope_pair(y, i, half, a.rope);
+    if (i < half) rotate_pair(y, i, half, rc, rs);
     __syncthreads();
     if (i < D) {
         if (is_q) {
