@@ -41,7 +41,7 @@ struct ArgmaxPart;  // one slice's greedy-token result (below)
 enum Knob : int {
     kGemmSplits,  // OQ_GEMM_SPLITS
     kGemmExactDequant,  // OQ_GEMM_EXACT_DEQUANT
-    kGemmWs,  // OQ_GEMM_WS
+    kGemmWs,  // OQ_GEMM_WS: 1 (default) weights converted in the MFMA waves (q4_K, q5_K), 0 the four-wave kernel (q4_K), 2 converted by the load waves (every type; q6_K always)
     kGemvMaxWg,  // OQ_GEMV_MAX_WG
     kQ80Rows,  // OQ_Q8_0_ROWS
     kGemvWgPerCu,  // OQ_GEMV_WG_PER_CU
