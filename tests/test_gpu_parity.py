@@ -241,15 +241,17 @@ def test_matmul_matrix_cores(ctx, m, rows, cols):
     w.release()
 
 
+@pytest.mark.parametrize("t", [12, 13])
 @pytest.mark.parametrize("splits", [None, "1", "3", "8"])
-def test_matrix_cores_q8k_input_and_split_counts(ctx, splits):
-    """The MFMA path from caller-supplied Q8_K blocks equals the path from F32 activations bit
-    for bit (same planar image), and every K-split count stays within the tolerance."""
-    rng = np.random.default_rng(31337)
+def test_matrix_cores_q8k_input_and_split_counts(ctx, t, splits):
+    """The MFMA path (q4_K and q5_K: weights converted in the MFMA waves) from caller-supplied
+    Q8_K blocks equals the path from F32 activations bit for bit (same planar image), and every
+    K-split count stays within the tolerance."""
+    rng = np.random.default_rng(31337 + t)
     m, rows, cols = 70, 520, 8192
-    data = synth.q4_k(rng, rows, cols)
+    data = synth.weights(t, rng, rows, cols)
     x = rng.standard_normal((m, cols)).astype(np.float32)
-    w = ctx.upload(12, cols, rows, data)
+    w = ctx.upload(t, cols, rows, data)
     with oracle_amd.launch_options({} if splits is None else {"OQ_GEMM_SPLITS": splits}):
         y = gpu_matmul(ctx, w, x, rows)
         xb = ctx.to_device(x)
@@ -261,7 +263,7 @@ def test_matrix_cores_q8k_input_and_split_counts(ctx, splits):
         for b in (xb, qb, yb):
             b.free()
     assert np.array_equal(y.view(np.uint32), y_q8k.view(np.uint32))
-    y_ref, norm = reference_products(12, rows, cols, data, x)
+    y_ref, norm = reference_products(t, rows, cols, data, x)
     worst = check_close(y, y_ref, norm)
     assert worst < 0.5 * TOL, f"MFMA path margin too thin: {worst:.2e}"
     w.release()
