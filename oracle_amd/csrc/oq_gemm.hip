@@ -241,6 +241,24 @@ OQ_DEVICE uint32_t q5_pair(uint32_t q, const ScaleT<FAST>& s) {
     }
 }
 
+// Two weights of a q6_K sub-block from the word of 6-bit codes u (q = u - 32): (d sc) q.
+//   FAST : ds = f16(d * sc) (d * sc is exact in F32), x = q exactly, one v_pk_mul_f16;
+//   exact: F32 (d * sc) * q as the reference, rounded to f16.
+template <bool FAST, int P>
+OQ_DEVICE uint32_t q6_pair(uint32_t u, float ds) {
+    if constexpr (FAST) {
+        const half2v k1056 = {(_Float16)1056.0f, (_Float16)1056.0f};
+        const half2v x = f16_1024_pair<P>(u) - k1056;  // exact integers -32..31
+        const _Float16 h = (_Float16)ds;
+        const half2v dv = {h, h};
+        return __builtin_bit_cast(uint32_t, x * dv);
+    } else {
+#pragma clang fp contract(off)
+        const float a = (float)((int)((u >> (16 * P)) & 0xFFu) - 32), b = (float)((int)((u >> (16 * P + 8)) & 0xFFu) - 32);
+        return pack_f16(ds * a, ds * b);
+    }
+}
+
 // q4_K (TYPE 12) or q5_K (13) weight pair from a word of quant bytes (nibbles, or 5-bit values)
 template <uint32_t TYPE, bool FAST, int P>
 OQ_DEVICE uint32_t k_pair(uint32_t q, const ScaleT<FAST>& s) {
@@ -891,6 +909,321 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(DeviceMatrix w, int
     }
 }
 
+// ---------------------------------------------------------------- q6_K with weights in registers
+//
+// gemm_ws_kernel's tiles, steps, wave roles and k order for q6_K, with gemm_kq_kernel's element
+// map (so the two kernels form the same operands): step G of a super-block is half G / 2 of it
+// (low nibbles of the 6-bit codes for even G, high for odd), slice ks of step G is segment
+// 2 (G & 1) + (ks & 1), and lane half h takes group g = 2 (G / 2) + h: both halves of its quant
+// chunk, its high-bit chunk, its scale word (segments 0..3) and the block's d.  Both steps of a
+// half use the same data, so the load waves stage half a super-block at a time ("half-unit" u:
+// super-block u / 2, half u % 2) in a two-slot ring, and each MFMA wave reads a half-unit once,
+// during the step before the half-unit's first step.
+//
+// LDS (dynamic, 117 KB):
+//   A ring    4 x 16 KB    as gemm_ws_kernel
+//   Q6 ring   2 x 26.5 KB  half-unit u in slot u % 2: quant chunk (group 2 (u % 2) + gl, half e)
+//                          of row n at 4096 (2 gl + e) + 16 n; high-bit chunk gl at
+//                          16 KB + 4096 gl + 16 n; the two scale words at 24 KB + 8 n; d at
+//                          26 KB + 2 n (a half-wave reads 512 contiguous bytes of each array)
+// Timing, step t = 2 u + b (b = 0, 1) of the split:
+//   load waves: the activation tiles as gemm_ws_kernel; at b = 0 store half-unit u + 1 (loaded
+//               at step t - 4) into slot (u + 1) % 2, whose last reader was step t - 1, and load
+//               half-unit u + 3 into the same registers;
+//   MFMA waves: multiply step t; at b = 1 read half-unit u + 1 from its slot (chunk half 1 at the
+//               last slice, when half-unit u's chunks are no longer read).
+constexpr uint32_t kQ6Slot = 27136;
+constexpr uint32_t kQ6Lds = kWsA + 2 * kQ6Slot;
+
+OQ_DEVICE uint32_t q6_ql_off(uint32_t slot, uint32_t gl, uint32_t e, uint32_t n) {
+    return kWsA + slot * kQ6Slot + 4096u * (2u * gl + e) + 16u * n;
+}
+OQ_DEVICE uint32_t q6_qh_off(uint32_t slot, uint32_t gl, uint32_t n) {
+    return kWsA + slot * kQ6Slot + 16384u + 4096u * gl + 16u * n;
+}
+OQ_DEVICE uint32_t q6_sc_off(uint32_t slot, uint32_t n) { return kWsA + slot * kQ6Slot + 24576u + 8u * n; }
+OQ_DEVICE uint32_t q6_d_off(uint32_t slot, uint32_t n) { return kWsA + slot * kQ6Slot + 26624u + 2u * n; }
+
+// one half-unit of one weight row, as an MFMA lane holds it
+struct Q6Half {
+    uint4 ql[2];  // quant chunk halves e = 0, 1 of the lane's group
+    uint4 qh;     // high-bit chunk of the group
+    uint32_t sc;  // int8 scales of segments 0..3
+    uint32_t d;   // f16 bits of the block's d
+};
+
+// what slice 0 of a half-unit needs (quant chunk half 0, high bits, scales, d), and chunk half 1
+OQ_DEVICE void q6_read_head(const uint8_t* lds, uint32_t slot, uint32_t n, uint32_t h, Q6Half& r) {
+    r.ql[0] = *reinterpret_cast<const uint4*>(lds + q6_ql_off(slot, h, 0, n));
+    r.qh = *reinterpret_cast<const uint4*>(lds + q6_qh_off(slot, h, n));
+    r.sc = *reinterpret_cast<const uint32_t*>(lds + q6_sc_off(slot, n) + 4u * h);
+    r.d = *reinterpret_cast<const uint16_t*>(lds + q6_d_off(slot, n));
+}
+OQ_DEVICE void q6_read_ql1(const uint8_t* lds, uint32_t slot, uint32_t n, uint32_t h, Q6Half& r) {
+    r.ql[1] = *reinterpret_cast<const uint4*>(lds + q6_ql_off(slot, h, 1, n));
+}
+
+// The two 4-code words and the scale of slice ks (of a step with half-parity par = G & 1) of a
+// lane's half-unit: codes u = low nibble | high bits << 4 (0..63, q = u - 32), ds = d * sc as F32
+OQ_DEVICE void q6_words(const Q6Half& r, int ks, int par, uint32_t (&u)[2], float& ds) {
+    const int e = ks & 1, seg = 2 * par + e;
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.d & 0xFFFFu));
+    ds = d * (float)(int8_t)((r.sc >> (8 * seg)) & 0xFFu);
+#pragma unroll
+    for (int wd = 0; wd < 2; ++wd) {
+        const uint32_t lo = (dword_of(r.ql[e], 2 * (ks >> 1) + wd) >> (4 * par)) & 0x0F0F0F0Fu;
+        const uint32_t hi = (dword_of(r.qh, 2 * (ks >> 1) + wd) >> (2 * seg)) & 0x03030303u;
+        u[wd] = lo | (hi << 4);
+    }
+}
+
+// MFMA wave, one step G: multiplies it (A of slice ks in a, B in b) while converting the next
+// slice's B operands, one weight pair after each MFMA (from cur, or at the last slice of an odd
+// step from nxt, the next half-unit) and, at odd G, reading the next half-unit from slot nslot
+// into nxt.
+template <bool FAST, int G>
+OQ_DEVICE void ws6_consumer_step(const uint8_t* lds, const uint32_t (&rd_off)[4], uint32_t nslot, uint32_t n_lane0,
+                                 uint32_t h, float16v (&acc)[4][2], half8 (&a)[4], uint32_t (&b)[2][4],
+                                 const Q6Half (&cur)[2], Q6Half (&nxt)[2]) {
+    constexpr int G1 = (G + 1) & 3;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const int nks = (ks + 1) & 3;
+        const uint32_t nbuf = ks < 3 ? (uint32_t)G : (uint32_t)G1;
+        const int npar = ks < 3 ? (G & 1) : (G1 & 1);  // half-parity of the next slice's step
+        half8 an[4];
+        uint32_t bn[2][4];
+        uint32_t uw[2][2];
+        float ds[2];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int i = q >> 1, j = q & 1;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], as_b_operand(b[j]), acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (q == 0) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) an[ii] = lds_read(lds, nbuf * kTileBytes + 4096u * ii + rd_off[nks]);
+            }
+            // the next half-unit: what its first slice needs at slice 0, chunk half 1 (first used
+            // by the next step's slice 1) at slice 3, once this half-unit's chunks are dead
+            if ((G & 1) && ks == 0 && (q == 2 || q == 3)) q6_read_head(lds, nslot, n_lane0 + 32u * (q - 2), h, nxt[q - 2]);
+            if ((G & 1) && ks == 3 && (q == 1 || q == 2)) q6_read_ql1(lds, nslot, n_lane0 + 32u * (q - 1), h, nxt[q - 1]);
+            const int jj = q >> 2, pp = q & 3;
+            if (pp == 0) q6_words(ks == 3 && (G & 1) ? nxt[jj] : cur[jj], nks, npar, uw[jj], ds[jj]);
+            bn[jj][pp] = (pp & 1) ? q6_pair<FAST, 1>(uw[jj][pp >> 1], ds[jj]) : q6_pair<FAST, 0>(uw[jj][pp >> 1], ds[jj]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) a[ii] = an[ii];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) b[j][e] = bn[j][e];
+    }
+}
+
+// load waves' registers for one half-unit: quant pieces (see ws6 producer), the lane row's
+// high-bit chunks, scale words and d
+struct Q6Raw {
+    uint4 ql[4], qh[2];
+    uint2 sc;
+    uint32_t d;
+};
+
+template <bool FAST>
+__global__ __launch_bounds__(kWsThreads) void gemm_ws6_kernel(DeviceMatrix w, int m, const _Float16* a16,
+                                                              uint32_t tiles_n, uint32_t tiles_m, uint32_t splits,
+                                                              float* __restrict__ out) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nsb = (uint32_t)(w.k / kQK);
+    const Unit un = unit_of(blockIdx.x, tiles_n, tiles_m, splits);
+    const uint32_t z = un.z;
+    const uint64_t n0 = (uint64_t)un.nt * kBN, m0 = (uint64_t)un.mt * kBM;
+    Split sp;
+    sp.sb0 = (uint32_t)((uint64_t)z * nsb / splits);
+    const uint32_t sb1 = (uint32_t)((uint64_t)(z + 1) * nsb / splits);
+    sp.nsbu = sb1 - sp.sb0;  // >= 1: splits <= nsb
+    sp.nsb = nsb;
+    sp.last_step = 4 * sp.nsbu - 1;
+    sp.hdr_base = 0;
+    sp.wbase = w.base;
+    sp.a16 = reinterpret_cast<const uint8_t*>(a16) + 2ull * kQK * sp.sb0;
+    const uint32_t nsteps = 4 * sp.nsbu;
+
+    if (wave >= 4) {
+        // ------------------------------------------------------------ load waves
+        const int pw = wave - 4;
+        const uint32_t krow = (uint32_t)(w.k * 2);
+        uint32_t act_off[4];
+        const uint32_t rb = 32u * pw + 2u * ((uint32_t)lane >> 3), c8 = (uint32_t)lane & 7;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint64_t row = m0 + rb + (uint32_t)(j & 1) + 16u * (uint32_t)(j >> 1);
+            row = row < (uint64_t)m ? row : (uint64_t)m - 1;
+            act_off[j] = (uint32_t)row * krow + 16u * c8;
+        }
+        const uint32_t act_st = 128u * rb + 16u * (c8 ^ ((rb >> 1) & 7));
+        auto act_load = [&](uint32_t t, uint4 (&v)[4]) {
+            const uint32_t st = t < sp.last_step ? t : sp.last_step;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = load_u4(sp.a16 + 128u * st, act_off[j]);
+        };
+        auto act_store = [&](uint32_t buf, const uint4 (&v)[4]) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<uint4*>(lds + buf * kTileBytes + act_st + 128u * (j & 1) + 2048u * (j >> 1)) = v[j];
+        };
+        // quant pieces: load t takes piece 32 t + lane / 2 = (row 16 t + lane / 4, half e = lane / 2 % 2)
+        // and chunk gl = lane % 2 of the half-unit's two groups: each lane pair reads 32 bytes
+        uint32_t prow_off[4], pst[4], pe[4];
+        const uint32_t gl = (uint32_t)lane & 1;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t piece = 32u * t + ((uint32_t)lane >> 1);
+            const uint32_t nl = 64u * pw + (piece >> 1), e = piece & 1;
+            uint64_t n = n0 + nl;
+            n = n < w.n ? n : w.n - 1;
+            prow_off[t] = (uint32_t)(n * w.pitch);
+            pe[t] = e;
+            pst[t] = q6_ql_off(0, gl, e, nl) - kWsA;
+        }
+        const uint32_t nrow = 64u * pw + (uint32_t)lane;  // the lane's row for qh, scales, d
+        uint32_t hrow_off;
+        {
+            uint64_t n = n0 + nrow;
+            n = n < w.n ? n : w.n - 1;
+            hrow_off = (uint32_t)(n * w.pitch);
+        }
+        auto half_load = [&](uint32_t u, Q6Raw& r) {
+            const uint32_t sb = split_sb(sp, u / 2), hf = u & 1;
+            const uint32_t pass = sb / 16u, s16 = sb % 16u;
+            const uint32_t mp = nsb - 16u * pass < 16u ? nsb - 16u * pass : 16u;
+            const uint8_t* qb = w.base + 16u * (128u * pass + 4u * s16 + 2u * hf + gl);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) r.ql[t] = load_u4(qb, prow_off[t] + pe[t] * 64u * mp);
+            const uint8_t* hb = w.base + 128u * nsb + 64u * sb + 32u * hf;
+            r.qh[0] = load_u4(hb, hrow_off);
+            r.qh[1] = load_u4(hb + 16, hrow_off);
+            r.sc = *reinterpret_cast<const uint2*>(w.base + 192u * nsb + 16u * sb + 8u * hf + hrow_off);
+            r.d = *reinterpret_cast<const uint16_t*>(w.base + 208u * nsb + 2u * sb + hrow_off);
+        };
+        auto half_store = [&](uint32_t slot, const Q6Raw& r) {
+            uint8_t* base = lds + kWsA + slot * kQ6Slot;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) *reinterpret_cast<uint4*>(base + pst[t]) = r.ql[t];
+            *reinterpret_cast<uint4*>(lds + q6_qh_off(slot, 0, nrow)) = r.qh[0];
+            *reinterpret_cast<uint4*>(lds + q6_qh_off(slot, 1, nrow)) = r.qh[1];
+            *reinterpret_cast<uint2*>(lds + q6_sc_off(slot, nrow)) = r.sc;
+            *reinterpret_cast<uint16_t*>(lds + q6_d_off(slot, nrow)) = (uint16_t)r.d;
+        };
+        uint4 av[2][4];
+        Q6Raw hr[2];
+        // prologue: tiles 0..2 and half-unit 0 stored; half-units 1 (set 1) and 2 (set 0), tiles
+        // 3 and 4 in flight
+        {
+            uint4 t0[4], t1[4], t2[4];
+            Q6Raw h0;
+            act_load(0, t0);
+            act_load(1, t1);
+            act_load(2, t2);
+            half_load(0, h0);
+            act_store(0, t0);
+            act_store(1, t1);
+            act_store(2, t2);
+            half_store(0, h0);
+        }
+        // (the order keeps as many younger loads behind each set as a loop trip does, so that the
+        // wait counts the compiler merges at the loop head are the loop's own)
+        half_load(1, hr[1]);
+        asm volatile("" ::: "memory");
+        act_load(3, av[1]);
+        asm volatile("" ::: "memory");
+        act_load(4, av[0]);
+        asm volatile("" ::: "memory");
+        half_load(2, hr[0]);
+        lds_barrier();
+        for (uint32_t s = 0; s < nsteps; s += 4) {
+            const uint32_t i = s / 4;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int as = (g + 1) & 1;
+                act_store((uint32_t)((g + 3) & 3), av[as]);
+                act_load(s + g + 5, av[as]);
+                if (g == 0) {
+                    half_store(1, hr[1]);
+                    half_load(2 * i + 3, hr[1]);
+                } else if (g == 2) {
+                    half_store(0, hr[0]);
+                    half_load(2 * i + 4, hr[0]);
+                }
+                lds_barrier();
+            }
+        }
+        return;
+    }
+
+    // ---------------------------------------------------------------- MFMA waves
+    const int h = lane >> 5, r0 = lane & 31;
+    uint32_t rd_off[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) rd_off[ks] = 128u * (uint32_t)r0 + 16u * (uint32_t)(a_chunk(ks, h) ^ ((r0 >> 1) & 7));
+    const uint32_t n_lane0 = 64u * (uint32_t)wave + (uint32_t)r0;  // row of n-subtile j: + 32 j
+
+    float16v acc[4][2] = {};
+    lds_barrier();  // the load waves' prologue
+    Q6Half cur[2], nxt[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        q6_read_head(lds, 0, n_lane0 + 32u * j, (uint32_t)h, cur[j]);
+        q6_read_ql1(lds, 0, n_lane0 + 32u * j, (uint32_t)h, cur[j]);
+        nxt[j] = cur[j];
+    }
+    half8 a[4];
+    uint32_t b[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = lds_read(lds, 4096u * i + rd_off[0]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        uint32_t uw[2];
+        float ds;
+        q6_words(cur[j], 0, 0, uw, ds);
+        b[j][0] = q6_pair<FAST, 0>(uw[0], ds);
+        b[j][1] = q6_pair<FAST, 1>(uw[0], ds);
+        b[j][2] = q6_pair<FAST, 0>(uw[1], ds);
+        b[j][3] = q6_pair<FAST, 1>(uw[1], ds);
+    }
+    for (uint32_t s = 0; s < nsteps; s += 4) {
+        ws6_consumer_step<FAST, 0>(lds, rd_off, 1, n_lane0, h, acc, a, b, cur, nxt);
+        lds_barrier();
+        ws6_consumer_step<FAST, 1>(lds, rd_off, 1, n_lane0, h, acc, a, b, cur, nxt);
+        lds_barrier();
+        cur[0] = nxt[0];
+        cur[1] = nxt[1];
+        ws6_consumer_step<FAST, 2>(lds, rd_off, 0, n_lane0, h, acc, a, b, cur, nxt);
+        lds_barrier();
+        ws6_consumer_step<FAST, 3>(lds, rd_off, 0, n_lane0, h, acc, a, b, cur, nxt);
+        lds_barrier();
+        cur[0] = nxt[0];
+        cur[1] = nxt[1];
+    }
+    float* o = out + (uint64_t)z * (uint64_t)m * w.n;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint64_t col = n0 + 64 * wave + 32 * j + r0;
+        if (col >= w.n) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int rr = 0; rr < 16; ++rr) {
+                const uint64_t row = m0 + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
+                if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][rr];
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- B tiles converted by the load waves
 //
 // The producer/consumer workgroup with the weights converted by the load waves: every 64-k step
@@ -964,24 +1297,6 @@ OQ_DEVICE void kq_load(KqRaw<TYPE>& r, const uint8_t* wb, const uint32_t (&row_o
             r.hdr[pp] = *reinterpret_cast<const uint4*>(row + (TYPE == 13 ? 160u : 128u) * nsb + 16u * sb);
             if constexpr (TYPE == 13) r.qh[pp] = *reinterpret_cast<const uint4*>(row + 128u * nsb + 32u * sb + 16u * hb);
         }
-    }
-}
-
-// Two weights of a q6_K sub-block from the word of 6-bit codes u (q = u - 32): (d sc) q.
-//   FAST : ds = f16(d * sc) (d * sc is exact in F32), x = q exactly, one v_pk_mul_f16;
-//   exact: F32 (d * sc) * q as the reference, rounded to f16.
-template <bool FAST, int P>
-OQ_DEVICE uint32_t q6_pair(uint32_t u, float ds) {
-    if constexpr (FAST) {
-        const half2v k1056 = {(_Float16)1056.0f, (_Float16)1056.0f};
-        const half2v x = f16_1024_pair<P>(u) - k1056;  // exact integers -32..31
-        const _Float16 h = (_Float16)ds;
-        const half2v dv = {h, h};
-        return __builtin_bit_cast(uint32_t, x * dv);
-    } else {
-#pragma clang fp contract(off)
-        const float a = (float)((int)((u >> (16 * P)) & 0xFFu) - 32), b = (float)((int)((u >> (16 * P + 8)) & 0xFFu) - 32);
-        return pack_f16(ds * a, ds * b);
     }
 }
 
@@ -1299,6 +1614,18 @@ void launch_ws(const DeviceMatrix& w, int m, const _Float16* a16, const Plan& p,
                        ws_lds_bytes<TYPE>(), s, w, m, a16, p.tiles_n, p.tiles_m, p.splits, dst);
 }
 
+template <bool FAST>
+void launch_ws6(const DeviceMatrix& w, int m, const _Float16* a16, const Plan& p, float* dst, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_ws6_kernel<FAST>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ6Lds);
+        attr = true;
+    }
+    hipLaunchKernelGGL((gemm_ws6_kernel<FAST>), dim3(p.tiles_n * p.tiles_m * p.splits), dim3(kWsThreads), kQ6Lds, s,
+                       w, m, a16, p.tiles_n, p.tiles_m, p.splits, dst);
+}
+
 hipError_t launch_gemm_mfma(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
                                 void* scratch, hipStream_t s) {
     if (!gemm_mfma_supported(w, m) || (x == nullptr) == (q8k == nullptr)) return hipErrorNotSupported;
@@ -1316,12 +1643,15 @@ hipError_t launch_gemm_mfma(const DeviceMatrix& w, int m, const float* x, const 
     }
     const unsigned wgs = p.tiles_n * p.tiles_m * p.splits;
     const bool fast = w.k >= kFastMinK && knob(kGemmExactDequant, 0) == 0;
-    if (w.type == 14 || knob(kGemmWs, 1) == 2) {
-        // the weights converted by the load waves (q6_K; every type with OQ_GEMM_WS=2)
+    if (knob(kGemmWs, 1) == 2) {
+        // the weights converted by the load waves (every type with OQ_GEMM_WS=2)
         float* dst = p.splits > 1 ? part : y;
         if (w.type == 12) fast ? launch_kq<12, true>(w, m, a16, p, dst, s) : launch_kq<12, false>(w, m, a16, p, dst, s);
         else if (w.type == 13) fast ? launch_kq<13, true>(w, m, a16, p, dst, s) : launch_kq<13, false>(w, m, a16, p, dst, s);
         else fast ? launch_kq<14, true>(w, m, a16, p, dst, s) : launch_kq<14, false>(w, m, a16, p, dst, s);
+    } else if (w.type == 14) {
+        float* dst = p.splits > 1 ? part : y;
+        fast ? launch_ws6<true>(w, m, a16, p, dst, s) : launch_ws6<false>(w, m, a16, p, dst, s);
     } else if (knob(kGemmWs, 1) != 0 || w.type == 13) {
         float* dst = p.splits > 1 ? part : y;
         if (w.type == 13) fast ? launch_ws<13, true>(w, m, a16, p, dst, s) : launch_ws<13, false>(w, m, a16, p, dst, s);

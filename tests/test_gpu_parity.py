@@ -241,10 +241,10 @@ def test_matmul_matrix_cores(ctx, m, rows, cols):
     w.release()
 
 
-@pytest.mark.parametrize("t", [12, 13])
+@pytest.mark.parametrize("t", [12, 13, 14])
 @pytest.mark.parametrize("splits", [None, "1", "3", "8"])
 def test_matrix_cores_q8k_input_and_split_counts(ctx, t, splits):
-    """The MFMA path (q4_K and q5_K: weights converted in the MFMA waves) from caller-supplied
+    """The MFMA path (every K-quant type: weights converted in the MFMA waves) from caller-supplied
     Q8_K blocks equals the path from F32 activations bit for bit (same planar image), and every
     K-split count stays within the tolerance."""
     rng = np.random.default_rng(31337 + t)
@@ -290,23 +290,24 @@ def test_matrix_core_kernels_agree(ctx, cols):
     w.release()
 
 
+@pytest.mark.parametrize("t", [13, 14])
 @pytest.mark.parametrize("cols", [4096, 8192])
-def test_q5_matrix_core_kernels_agree(ctx, cols):
-    """q5_K: the kernel whose MFMA waves convert the weights in registers (default) and the one
-    whose load waves convert them into LDS B tiles (OQ_GEMM_WS=2) form the same f16 operands and
-    add them in the same order: identical outputs, bit for bit, on both dequantization paths
-    (F32 scales below K = 8192, packed f16 from 8192)."""
-    rng = np.random.default_rng(5150 + cols)
+def test_q5_q6_matrix_core_kernels_agree(ctx, t, cols):
+    """q5_K and q6_K: the kernel whose MFMA waves convert the weights in registers (default) and
+    the one whose load waves convert them into LDS B tiles (OQ_GEMM_WS=2) form the same f16
+    operands and add them in the same order: identical outputs, bit for bit, on both
+    dequantization paths (F32 scales below K = 8192, packed f16 from 8192)."""
+    rng = np.random.default_rng(5150 + 7 * t + cols)
     m, rows = 70, 520
-    data = synth.weights(13, rng, rows, cols)
+    data = synth.weights(t, rng, rows, cols)
     x = rng.standard_normal((m, cols)).astype(np.float32)
-    w = ctx.upload(13, cols, rows, data)
+    w = ctx.upload(t, cols, rows, data)
     ys = {}
     for v in ("1", "2"):
         with oracle_amd.launch_options({"OQ_GEMM_WS": v}):
             ys[v] = gpu_matmul(ctx, w, x, rows)
     assert np.array_equal(ys["1"].view(np.uint32), ys["2"].view(np.uint32))
-    y_ref, norm = reference_products(13, rows, cols, data, x)
+    y_ref, norm = reference_products(t, rows, cols, data, x)
     check_close(ys["1"], y_ref, norm)
     w.release()
 
@@ -315,8 +316,8 @@ def test_q5_matrix_core_kernels_agree(ctx, cols):
 @pytest.mark.parametrize("m,rows,cols", [(16, 256, 4096), (37, 300, 4096), (64, 130, 12288), (200, 128, 8192),
                                          (19, 70, 17408), (130, 513, 4352)])
 def test_matmul_matrix_cores_q5_q6(ctx, t, m, rows, cols):
-    """m >= 16 q5_K / q6_K products on the f16 MFMA path (q5_K converted in the MFMA waves'
-    registers, q6_K by the load waves); Q8_K and F32 activations give the same bits."""
+    """m >= 16 q5_K / q6_K products on the f16 MFMA path (weights converted in the MFMA waves'
+    registers); Q8_K and F32 activations give the same bits."""
     rng = np.random.default_rng(9500 + 7 * t + m + rows + cols)
     data = synth.weights(t, rng, rows, cols)
     x = rng.standard_normal((m, cols)).astype(np.float32)
