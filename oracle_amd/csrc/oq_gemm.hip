@@ -6,10 +6,10 @@
 // MFMA waves convert the weights in registers while load waves stage every tile in LDS (q4_K
 // 64.7 us at M = 512, 4096 x 12288).  gemm_kq_kernel, whose load waves convert each step's weights
 // into an f16 B tile in LDS, stays selectable (q4_K through it: 80.6 us).  Both operands are
-// rounded once to binary16 and
-// multiplied on v_mfma_f32_32x32x16_f16 with F32 accumulation.  The rounding is relative 2^-11
-// per operand; over K >= 4096 terms its effect on an output stays below 1e-4 * sum_k |w_k * xhat_k|
-// with a wide margin (checked by the parity tests), so the path is enabled only for K >= 4096.
+// rounded once to binary16 and multiplied on v_mfma_f32_32x32x16_f16 with F32 accumulation.  The
+// rounding is relative 2^-11 per operand; over K >= 4096 terms its effect on an output stays below
+// 1e-4 * sum_k |w_k * xhat_k| with a wide margin (checked by the parity tests), so the path is
+// enabled only for K >= 4096.
 // Every kernel of a weight type forms the same f16 operands and adds the products in the same
 // order, so they agree bit for bit.
 //
