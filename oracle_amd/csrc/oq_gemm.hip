@@ -924,7 +924,7 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(DeviceMatrix w, int
 // LDS (dynamic, 117 KB):
 //   A ring    4 x 16 KB    as gemm_ws_kernel
 //   Q6 ring   2 x 26.5 KB  half-unit u in slot u % 2: quant chunk (group 2 (u % 2) + gl, half e)
-//                          of row n at 4096 (2 gl + e) + 16 n; high-bit chunk gl at
+//                          of row n at 4096 c + 16 ((n + 4 c) % 256), c = 2 gl + e; high-bit chunk gl at
 //                          16 KB + 4096 gl + 16 n; the two scale words at 24 KB + 8 n; d at
 //                          26 KB + 2 n (a half-wave reads 512 contiguous bytes of each array)
 // Timing, step t = 2 u + b (b = 0, 1) of the split:
@@ -936,8 +936,12 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(DeviceMatrix w, int
 constexpr uint32_t kQ6Slot = 27136;
 constexpr uint32_t kQ6Lds = kWsA + 2 * kQ6Slot;
 
+// chunk array c = 2 gl + e holds row n at position (n + 4 c) % 256: the load waves' stores (lanes
+// 4 r + c of a 16-lane pass: rows r, arrays c) then fall on 16 distinct bank groups, and a
+// half-wave's reads (32 consecutive rows of one array) stay contiguous modulo 4 KB
 OQ_DEVICE uint32_t q6_ql_off(uint32_t slot, uint32_t gl, uint32_t e, uint32_t n) {
-    return kWsA + slot * kQ6Slot + 4096u * (2u * gl + e) + 16u * n;
+    const uint32_t c = 2u * gl + e;
+    return kWsA + slot * kQ6Slot + 4096u * c + 16u * ((n + 4u * c) & 255u);
 }
 OQ_DEVICE uint32_t q6_qh_off(uint32_t slot, uint32_t gl, uint32_t n) {
     return kWsA + slot * kQ6Slot + 16384u + 4096u * gl + 16u * n;
