@@ -943,8 +943,9 @@ OQ_DEVICE uint32_t q6_ql_off(uint32_t slot, uint32_t gl, uint32_t e, uint32_t n)
     const uint32_t c = 2u * gl + e;
     return kWsA + slot * kQ6Slot + 4096u * c + 16u * ((n + 4u * c) & 255u);
 }
+// (high-bit chunk array gl holds row n at (n + 8 gl) % 256, for the same reason)
 OQ_DEVICE uint32_t q6_qh_off(uint32_t slot, uint32_t gl, uint32_t n) {
-    return kWsA + slot * kQ6Slot + 16384u + 4096u * gl + 16u * n;
+    return kWsA + slot * kQ6Slot + 16384u + 4096u * gl + 16u * ((n + 8u * gl) & 255u);
 }
 OQ_DEVICE uint32_t q6_sc_off(uint32_t slot, uint32_t n) { return kWsA + slot * kQ6Slot + 24576u + 8u * n; }
 OQ_DEVICE uint32_t q6_d_off(uint32_t slot, uint32_t n) { return kWsA + slot * kQ6Slot + 26624u + 2u * n; }
@@ -1030,7 +1031,7 @@ OQ_DEVICE void ws6_consumer_step(const uint8_t* lds, const uint32_t (&rd_off)[4]
 // load waves' registers for one half-unit: quant pieces (see ws6 producer), the lane row's
 // high-bit chunks, scale words and d
 struct Q6Raw {
-    uint4 ql[4], qh[2];
+    uint4 ql[4], qh[2];  // qh[t]: chunk (lane % 2) of row 32 t + lane / 2
     uint2 sc;
     uint32_t d;
 };
@@ -1094,12 +1095,19 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws6_kernel(DeviceMatrix w, in
             pe[t] = e;
             pst[t] = q6_ql_off(0, gl, e, nl) - kWsA;
         }
-        const uint32_t nrow = 64u * pw + (uint32_t)lane;  // the lane's row for qh, scales, d
-        uint32_t hrow_off;
+        const uint32_t nrow = 64u * pw + (uint32_t)lane;  // the lane's row for scales and d
+        uint32_t hrow_off, qrow_off[2];
         {
             uint64_t n = n0 + nrow;
             n = n < w.n ? n : w.n - 1;
             hrow_off = (uint32_t)(n * w.pitch);
+        }
+        // high bits: lane pairs read a row's 32 contiguous bytes, rows 32 t + lane / 2
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            uint64_t n = n0 + 64u * pw + 32u * t + ((uint32_t)lane >> 1);
+            n = n < w.n ? n : w.n - 1;
+            qrow_off[t] = (uint32_t)(n * w.pitch) + 16u * gl;
         }
         auto half_load = [&](uint32_t u, Q6Raw& r) {
             const uint32_t sb = split_sb(sp, u / 2), hf = u & 1;
@@ -1109,8 +1117,8 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws6_kernel(DeviceMatrix w, in
 #pragma unroll
             for (int t = 0; t < 4; ++t) r.ql[t] = load_u4(qb, prow_off[t] + pe[t] * 64u * mp);
             const uint8_t* hb = w.base + 128u * nsb + 64u * sb + 32u * hf;
-            r.qh[0] = load_u4(hb, hrow_off);
-            r.qh[1] = load_u4(hb + 16, hrow_off);
+            r.qh[0] = load_u4(hb, qrow_off[0]);
+            r.qh[1] = load_u4(hb, qrow_off[1]);
             r.sc = *reinterpret_cast<const uint2*>(w.base + 192u * nsb + 16u * sb + 8u * hf + hrow_off);
             r.d = *reinterpret_cast<const uint16_t*>(w.base + 208u * nsb + 2u * sb + hrow_off);
         };
@@ -1118,8 +1126,9 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws6_kernel(DeviceMatrix w, in
             uint8_t* base = lds + kWsA + slot * kQ6Slot;
 #pragma unroll
             for (int t = 0; t < 4; ++t) *reinterpret_cast<uint4*>(base + pst[t]) = r.ql[t];
-            *reinterpret_cast<uint4*>(lds + q6_qh_off(slot, 0, nrow)) = r.qh[0];
-            *reinterpret_cast<uint4*>(lds + q6_qh_off(slot, 1, nrow)) = r.qh[1];
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                *reinterpret_cast<uint4*>(lds + q6_qh_off(slot, gl, 64u * pw + 32u * t + ((uint32_t)lane >> 1))) = r.qh[t];
             *reinterpret_cast<uint2*>(lds + q6_sc_off(slot, nrow)) = r.sc;
             *reinterpret_cast<uint16_t*>(lds + q6_d_off(slot, nrow)) = (uint16_t)r.d;
         };
