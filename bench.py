@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes as C
+import hashlib
 import json
 import math
 import os
@@ -108,6 +109,9 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
     ybytes = m * n * 4
     res = {
         "workload": name, "desc": desc, "type": t, "rows": n, "cols": k, "m": m,
+        # the exact input bytes (weights as the reference stores them, and x), for reproduction
+        "weights_sha256": hashlib.sha256(data.tobytes()).hexdigest()[:16],
+        "x_sha256": hashlib.sha256(x.tobytes()).hexdigest()[:16],
         "weight_bytes": wb, "copies": ncopies, "ms_per_step": ms_step,
         "us_per_step": ms_step * 1e3,
         "weight_gbs": wb / (ms_step * 1e-3) / 1e9,
@@ -447,7 +451,8 @@ def main():
         "dtype": "f16 MFMA (f32 accumulate)" if mfma else "int8xu4 dot (i32) + f32 scales",
         "data": "synthetic (seeded: weights per workload distributions, x ~ N(0,1))",
         "config": {"workload": desc, "rows": n, "cols": k, "batch": m, "weight_type": TYPE_NAMES[t],
-                   "weight_copies_cycled": main_res["copies"], "seed": SEED},
+                   "weight_copies_cycled": main_res["copies"], "seed": SEED,
+                   "weights_sha256": main_res["weights_sha256"], "x_sha256": main_res["x_sha256"]},
         "roofline": roofline,
         "us_per_gemv": round(main_res["us_per_step"], 3),
         **({"tflops": round(main_res["tops"], 2)} if m > 1 else {}),
