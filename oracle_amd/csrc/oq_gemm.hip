@@ -924,9 +924,10 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(DeviceMatrix w, int
 // LDS (dynamic, 117 KB):
 //   A ring    4 x 16 KB    as gemm_ws_kernel
 //   Q6 ring   2 x 26.5 KB  half-unit u in slot u % 2: quant chunk (group 2 (u % 2) + gl, half e)
-//                          of row n at 4096 c + 16 ((n + 4 c) % 256), c = 2 gl + e; high-bit chunk gl at
-//                          16 KB + 4096 gl + 16 n; the two scale words at 24 KB + 8 n; d at
-//                          26 KB + 2 n (a half-wave reads 512 contiguous bytes of each array)
+//                          of row n at 4096 c + 16 ((n + 4 c) % 256), c = 2 gl + e; high-bit
+//                          chunk gl at 16 KB + 4096 gl + 16 ((n + 8 gl) % 256); the two scale
+//                          words at 24 KB + 8 n; d at 26 KB + 2 n (a half-wave reads 512 bytes,
+//                          contiguous modulo 4 KB, of each array)
 // Timing, step t = 2 u + b (b = 0, 1) of the split:
 //   load waves: the activation tiles as gemm_ws_kernel; at b = 0 store half-unit u + 1 (loaded
 //               at step t - 4) into slot (u + 1) % 2, whose last reader was step t - 1, and load
