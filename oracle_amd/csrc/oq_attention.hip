@@ -434,7 +434,9 @@ __global__ __launch_bounds__(256) void attention_prep_kernel(AttnPrep a) {
 template <int D, int REP>
 hipError_t launch_chunks(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
     // two passes in flight per wave: measured 56.1 us per step (chunk + merge, 16 query heads over
-    // 4 KV heads of 256, 32768 tokens) against 57.2 with one and 62.4 with three
+    // 4 KV heads of 256, 32768 tokens) against 57.2 with one and 62.4 with three; the attention
+    // block at 4096 tokens (64-token chunks) also takes longest with more: 56.1 against 56.9 and
+    // 58.7 us with three and four
     hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 2>), dim3(a.Hkv * a.nchunks), dim3(kAttnThreads), lds, s, a);
     return hipGetLastError();
 }
