@@ -1189,15 +1189,10 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_
     prep.q_norm = b->q_norm;
     prep.k_norm = b->k_norm;
     prep.eps = b->eps;
-    prep.Hq = (uint32_t)Hq;
-    prep.Hkv = (uint32_t)Hkv;
-    prep.D = (uint32_t)D;
     prep.rope = rp;
     prep.qcur = qcur;
     prep.kcur = kcur;
-    prep.key_slot = cache->keys + cache->length * KV;
-    prep.value_slot = cache->values + cache->length * KV;
-    L.q = qcur;
+    L.prep = &prep;
     L.part = part;
     L.out = pregate;
     L.gate = qfull + D;
@@ -1217,7 +1212,6 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_
         if (e == hipSuccess) e = block_project(b->k, normed, kp, s);
         if (e == hipSuccess) e = block_project(b->v, normed, vp, s);
     }
-    if (e == hipSuccess) e = oq::launch_attention_prep(prep, s);
     if (e == hipSuccess) e = oq::launch_attention(L, s);
     if (fused_tail) {
         if (e == hipSuccess) e = oq::launch_gemv_block(oq::kBlockAdd, outp, s);

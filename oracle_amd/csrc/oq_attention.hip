@@ -27,6 +27,13 @@
 // The append (KvCache::append, hybrid_cache.cpp:154-169) is folded in: when new_k / new_v are
 // given, the workgroup whose chunk holds the new token reads it from there and stores it into
 // cache row T - 1; nothing else reads that row during the step.
+//
+// For the decoder block the per-head preparation (qwen35_block.cpp:671-711: RMSNorm of each query
+// head with q_norm and of each key head with k_norm, then the rotation) is folded in as well, so
+// the block has no separate preparation launch: every chunk workgroup of KV head g normalises and
+// rotates g's rep query heads itself, in LDS, while its first key rows are in flight, and the
+// workgroup whose chunk holds the new token also prepares the new key, scores that token from LDS
+// (the key loads issued before it was ready skip it) and stores it into the cache.
 #include "oq_common.h"
 
 namespace oq {
@@ -50,6 +57,16 @@ struct ChunkArgs {
     float scale;
     float* part_o;        // [Hkv][rep][D/64][nchunks][64]: one head slice's chunks contiguous
     float* part_ml;       // [Hkv][rep][nchunks][2]
+    // the block's preparation (PREP kernels); new_k is null and new_v the value projection
+    const float* qfull;   // [Hq][2D]: query values, then the output gate
+    const float* kp;      // [Hkv][D] key projection
+    const float* q_norm;  // [D]
+    const float* k_norm;  // [D]
+    float eps;
+    RopeParams rope;
+    float* qcur;          // [Hq][D], written by each KV head's chunk 0
+    float* kcur;          // [Hkv][D], written by the chunk holding the new token
+    uint32_t stage;       // float offset of the preparation's LDS: [rep + 1][D] rows, cos/sin [2][128]
 };
 
 struct MergeArgs {
@@ -89,7 +106,49 @@ struct Vec<4> {
     }
 };
 
-template <int D, int REP, int NB>
+// cos and sin of frequency f's angle, as apply_qwen35_rope (reference_kernels.cpp:105-115):
+// base^(2f/R) and the angle in double, the coordinate chosen as position_for_frequency (:28-40)
+OQ_DEVICE void rope_cs(uint32_t f, const RopeParams& p, float& c, float& s) {
+    const double exponent = (2.0 * (double)f) / (double)p.rotary_dim;
+    const double inv_freq = 1.0 / pow((double)p.base, exponent);
+    uint64_t coord = p.pos[0];
+    if (f % 3u == 1u && f / 3u < p.sec1) coord = p.pos[1];
+    else if (f % 3u == 2u && f / 3u < p.sec2) coord = p.pos[2];
+    const double angle = (double)coord * inv_freq;
+    c = (float)cos(angle);
+    s = (float)sin(angle);
+}
+
+OQ_DEVICE void rotate_pair(float* x, uint32_t f, uint32_t half, float c, float s) {
+#pragma clang fp contract(off)
+    const float a = x[f], b = x[half + f];
+    x[f] = a * c - b * s;
+    x[half + f] = b * c + a * s;
+}
+
+OQ_DEVICE double wave_sum_f64(double v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// One row of the block's preparation in wave registers (lane i holding elements i*VW ..): the
+// RMSNorm of rms_norm_rows (qwen35_block.cpp:161-189, sum of squares in double; called at :691-698)
+// with weight w, written to LDS row y for the rotation
+template <int D>
+OQ_DEVICE void prep_row_norm(const float* x, const float* w, float eps, int lane, float* y) {
+#pragma clang fp contract(off)
+    constexpr int VW = D / 64;
+    double ss = 0.0;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) ss += (double)x[e] * (double)x[e];
+    ss = wave_sum_f64(ss);
+    const float inv = (float)(1.0 / sqrt(ss / (double)D + (double)eps));
+#pragma unroll
+    for (int e = 0; e < VW; ++e) y[lane * VW + e] = x[e] * inv * w[e];
+}
+
+template <int D, int REP, int NB, bool PREP>
 __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs a) {
     constexpr int NV = D / 64;  // float4 of one key row per lane (16 lanes per row)
     constexpr int VW = D / 64;  // value columns per lane (64 lanes per row)
@@ -127,12 +186,34 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
     // between buffers would wait for the loads it copies)
     const int l16 = lane & 15;
     float4 qr[REP][NV];
+    // the preparation's rows: query heads of g as rows 0 .. rep-1, the new key as row rep; wave w
+    // takes rows w, w + 4, ..  Their loads go out before the key rows, so waiting for them does not
+    // wait for the keys.
+    constexpr int kPrepRows = PREP ? (REP + kAttnWaves) / kAttnWaves : 1;
+    const bool holds_new = c1 == a.T;
+    const uint32_t prep_rows = rep + (holds_new ? 1u : 0u);
+    float px[kPrepRows][VW], pw[kPrepRows][VW];
+    if constexpr (PREP) {
 #pragma unroll
-    for (int h = 0; h < REP; ++h) {
-        const uint32_t hh = (uint32_t)h < rep ? (uint32_t)h : 0u;
-        const float4* qp = reinterpret_cast<const float4*>(a.q + ((uint64_t)g * rep + hh) * D);
+        for (int r = 0; r < kPrepRows; ++r) {
+            const uint32_t row = (uint32_t)wave + (uint32_t)r * kAttnWaves;
+            if (row < prep_rows) {
+                const bool is_q = row < rep;
+                const float* src = is_q ? a.qfull + ((uint64_t)g * rep + row) * 2 * D : a.kp + (uint64_t)g * D;
+                const float* w = is_q ? a.q_norm : a.k_norm;
+                Vec<VW>::unpack(*reinterpret_cast<const VT*>(src + lane * VW), px[r]);
 #pragma unroll
-        for (int j = 0; j < NV; ++j) qr[h][j] = qp[j * 16 + l16];
+                for (int e = 0; e < VW; ++e) pw[r][e] = w[lane * VW + e];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < REP; ++h) {
+            const uint32_t hh = (uint32_t)h < rep ? (uint32_t)h : 0u;
+            const float4* qp = reinterpret_cast<const float4*>(a.q + ((uint64_t)g * rep + hh) * D);
+#pragma unroll
+            for (int j = 0; j < NV; ++j) qr[h][j] = qp[j * 16 + l16];
+        }
     }
     const uint32_t first = c0 + (uint32_t)wave * 4u;  // this wave's first pass (wave-uniform)
     auto load_keys = [&](float4 (&dst)[NV], uint32_t pass_base) {
@@ -145,6 +226,43 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
         float4 kb[NB][NV];
 #pragma unroll
         for (int b = 0; b < NB; ++b) load_keys(kb[b], first + (uint32_t)b * kTokStep);
+        if constexpr (PREP) {
+            // normalise (each wave its rows), then rotate (the workgroup over every row's frequency
+            // pairs), while the key rows arrive
+            float* stage = lds + a.stage;
+            float* rc = stage + (rep + 1) * D;  // cos [128], sin [128]
+            const uint32_t half = a.rope.rotary_dim / 2;
+            if (threadIdx.x < half) rope_cs(threadIdx.x, a.rope, rc[threadIdx.x], rc[128 + threadIdx.x]);
+#pragma unroll
+            for (int r = 0; r < kPrepRows; ++r) {
+                const uint32_t row = (uint32_t)wave + (uint32_t)r * kAttnWaves;
+                if (row < prep_rows) prep_row_norm<D>(px[r], pw[r], a.eps, lane, stage + row * D);
+            }
+            __syncthreads();
+            for (uint32_t i = threadIdx.x; i < prep_rows * half; i += kAttnThreads) {
+                const uint32_t row = i / half, f = i - row * half;
+                rotate_pair(stage + row * D, f, half, rc[f], rc[128 + f]);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int h = 0; h < REP; ++h) {
+                const uint32_t hh = (uint32_t)h < rep ? (uint32_t)h : 0u;
+#pragma unroll
+                for (int j = 0; j < NV; ++j) qr[h][j] = *reinterpret_cast<const float4*>(stage + hh * D + 4 * (j * 16 + l16));
+            }
+            // the trace's copies, and the append of the new key and value rows
+            if (c == 0) {
+                for (uint32_t i = threadIdx.x; i < rep * D; i += kAttnThreads) a.qcur[(uint64_t)g * rep * D + i] = stage[i];
+            }
+            if (holds_new) {
+                for (uint32_t i = threadIdx.x; i < (uint32_t)D; i += kAttnThreads) {
+                    const float k = stage[rep * D + i];
+                    a.kcur[(uint64_t)g * D + i] = k;
+                    a.keys[((uint64_t)last * a.Hkv + g) * D + i] = k;
+                    a.values[((uint64_t)last * a.Hkv + g) * D + i] = a.new_v[(uint64_t)g * D + i];
+                }
+            }
+        }
         for (uint32_t base = first; base < c1; base += NB * kTokStep) {
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
@@ -163,13 +281,28 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                     }
                     acc[h] = row16_sum(sum);
                 }
-                if (t < c1 && (uint32_t)l16 < rep) {
+                // (with the preparation folded in, the new token's cache row was loaded before
+                // it was written: its score comes from LDS below)
+                if (t < c1 && (uint32_t)l16 < rep && !(PREP && t == last)) {
                     float v = acc[0];
 #pragma unroll
                     for (int h = 1; h < REP; ++h) v = l16 == h ? acc[h] : v;
                     sc[(uint32_t)l16 * a.chunk + (t - c0)] = v * a.scale;
                 }
                 load_keys(kb[b], pb + NB * kTokStep);
+            }
+        }
+    }
+    if constexpr (PREP) {
+        if (holds_new) {
+            const float* stage = lds + a.stage;
+            const float* kn = stage + rep * D;
+            for (uint32_t h = (uint32_t)wave; h < rep; h += kAttnWaves) {
+                float s = 0.0f;
+#pragma unroll
+                for (int e = 0; e < VW; ++e) s += stage[h * D + (uint32_t)lane * VW + e] * kn[(uint32_t)lane * VW + e];
+                s = wave_sum(s);
+                if (lane == 0) sc[h * a.chunk + (last - c0)] = s * a.scale;
             }
         }
     }
@@ -360,26 +493,6 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
 
 // ---------------------------------------------------------------- RoPE
 
-// cos and sin of frequency f's angle, as apply_qwen35_rope (reference_kernels.cpp:105-115):
-// base^(2f/R) and the angle in double, the coordinate chosen as position_for_frequency (:28-40)
-OQ_DEVICE void rope_cs(uint32_t f, const RopeParams& p, float& c, float& s) {
-    const double exponent = (2.0 * (double)f) / (double)p.rotary_dim;
-    const double inv_freq = 1.0 / pow((double)p.base, exponent);
-    uint64_t coord = p.pos[0];
-    if (f % 3u == 1u && f / 3u < p.sec1) coord = p.pos[1];
-    else if (f % 3u == 2u && f / 3u < p.sec2) coord = p.pos[2];
-    const double angle = (double)coord * inv_freq;
-    c = (float)cos(angle);
-    s = (float)sin(angle);
-}
-
-OQ_DEVICE void rotate_pair(float* x, uint32_t f, uint32_t half, float c, float s) {
-#pragma clang fp contract(off)
-    const float a = x[f], b = x[half + f];
-    x[f] = a * c - b * s;
-    x[half + f] = b * c + a * s;
-}
-
 OQ_DEVICE void rope_pair(float* x, uint32_t f, uint32_t half, const RopeParams& p) {
     float c, s;
     rope_cs(f, p, c, s);
@@ -392,52 +505,18 @@ __global__ __launch_bounds__(256) void rope_kernel(float* heads, uint32_t head_d
     for (uint32_t f = threadIdx.x; f < half; f += blockDim.x) rope_pair(x, f, half, p);
 }
 
-// The attention block's per-head preparation (qwen35_block.cpp:671-711), one workgroup per head:
-// query heads (b < Hq) take D query values of qfull, RMSNorm with q_norm, rotate -> qcur;
-// key heads RMSNorm with k_norm, rotate -> kcur and cache row T - 1, whose value row receives v.
-__global__ __launch_bounds__(256) void attention_prep_kernel(AttnPrep a) {
-#pragma clang fp contract(off)
-    __shared__ float y[256];
-    __shared__ double red[4];
-    const uint32_t b = blockIdx.x, i = threadIdx.x, D = a.D;
-    const bool is_q = b < a.Hq;
-    const uint32_t head = is_q ? b : b - a.Hq;
-    const float* src = is_q ? a.qfull + (uint64_t)head * 2 * D : a.kp + (uint64_t)head * D;
-    const float* w = is_q ? a.q_norm : a.k_norm;
-    const float x = i < D ? src[i] : 0.0f;
-    // the rotation's cos and sin (double arithmetic, independent of the data) while x arrives
-    const uint32_t half = a.rope.rotary_dim / 2;
-    float rc = 1.0f, rs = 0.0f;
-    if (i < half) rope_cs(i, a.rope, rc, rs);
-    double ss = (double)x * (double)x;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-    if ((i & 63) == 0) red[i >> 6] = ss;
-    __syncthreads();
-    const double tot = red[0] + red[1] + red[2] + red[3];
-    const float inv = (float)(1.0 / sqrt(tot / (double)D + (double)a.eps));
-    if (i < D) y[i] = x * inv * w[i];
-    __syncthreads();
-    if (i < half) rotate_pair(y, i, half, rc, rs);
-    __syncthreads();
-    if (i < D) {
-        if (is_q) {
-            a.qcur[(uint64_t)head * D + i] = y[i];
-        } else {
-            a.kcur[(uint64_t)head * D + i] = y[i];
-            a.key_slot[(uint64_t)head * D + i] = y[i];
-            a.value_slot[(uint64_t)head * D + i] = a.vp[(uint64_t)head * D + i];
-        }
-    }
-}
-
 template <int D, int REP>
 hipError_t launch_chunks(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
+    const dim3 grid(a.Hkv * a.nchunks);
     // two passes in flight per wave: measured 56.1 us per step (chunk + merge, 16 query heads over
     // 4 KV heads of 256, 32768 tokens) against 57.2 with one and 62.4 with three; the attention
     // block at 4096 tokens (64-token chunks) also takes longest with more: 56.1 against 56.9 and
     // 58.7 us with three and four
-    hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 2>), dim3(a.Hkv * a.nchunks), dim3(kAttnThreads), lds, s, a);
+    if (a.qfull != nullptr) {
+        hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 2, true>), grid, dim3(kAttnThreads), lds, s, a);
+    } else {
+        hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 2, false>), grid, dim3(kAttnThreads), lds, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -457,7 +536,24 @@ hipError_t launch_d(const AttnLaunch& L, hipStream_t s) {
     a.scale = L.scale;
     a.part_o = L.part;
     a.part_ml = L.part + (uint64_t)L.Hkv * L.nchunks * L.rep * D;
-    const uint64_t lds = (uint64_t)std::max(L.rep * L.chunk, (uint32_t)kAttnWaves * L.rep * D) * sizeof(float);
+    a.stage = std::max(L.rep * L.chunk, (uint32_t)kAttnWaves * L.rep * D);
+    uint64_t lds = a.stage;
+    if (L.prep != nullptr) {
+        const AttnPrep& p = *L.prep;
+        a.q = nullptr;
+        a.new_k = nullptr;
+        a.new_v = p.vp;
+        a.qfull = p.qfull;
+        a.kp = p.kp;
+        a.q_norm = p.q_norm;
+        a.k_norm = p.k_norm;
+        a.eps = p.eps;
+        a.rope = p.rope;
+        a.qcur = p.qcur;
+        a.kcur = p.kcur;
+        lds += (uint64_t)(L.rep + 1) * D + 256;  // the preparation's rows and cos / sin
+    }
+    lds *= sizeof(float);
     hipError_t e;
     if (L.rep == 1) e = launch_chunks<D, 1>(a, lds, s);
     else if (L.rep == 2) e = launch_chunks<D, 2>(a, lds, s);
@@ -516,12 +612,6 @@ hipError_t launch_rope(float* heads, uint64_t n_heads, uint64_t head_dim, const 
     if (n_heads == 0) return hipSuccess;
     hipLaunchKernelGGL(rope_kernel, dim3((unsigned)n_heads), dim3(std::min<uint32_t>(256u, std::max(64u, p.rotary_dim / 2))),
                        0, s, heads, (uint32_t)head_dim, p);
-    return hipGetLastError();
-}
-
-hipError_t launch_attention_prep(const AttnPrep& a, hipStream_t s) {
-    if (a.D > 256) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attention_prep_kernel, dim3(a.Hq + a.Hkv), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -159,6 +159,16 @@ struct RopeParams {
     float base;
     uint64_t pos[3];  // temporal, height, width
 };
+// The decoder block's per-head preparation (qwen35_block.cpp:671-711), done by the attention
+// chunk kernel: RMSNorm of the query heads (q_norm) and of the new key (k_norm), rotation, the
+// append of the new key and value rows, and the trace's copies qcur / kcur.
+struct AttnPrep {
+    const float *qfull, *kp, *vp;  // projections: [Hq][2D], [Hkv][D], [Hkv][D]
+    const float *q_norm, *k_norm;
+    float eps;
+    RopeParams rope;
+    float *qcur, *kcur;           // [Hq][D], [Hkv][D]
+};
 struct AttnLaunch {
     const float* q;            // [Hkv * rep][D]
     float* keys;               // cache [capacity][Hkv][D]
@@ -173,15 +183,7 @@ struct AttnLaunch {
     uint32_t gate_stride;
     float* gate_s;             // sigmoid(gate) [Hq][D] and out * sigmoid(gate), when gate is given
     float* gated;
-};
-struct AttnPrep {
-    const float *qfull, *kp, *vp;  // projections: [Hq][2D], [Hkv][D], [Hkv][D]
-    const float *q_norm, *k_norm;
-    float eps;
-    uint32_t Hq, Hkv, D;
-    RopeParams rope;
-    float *qcur, *kcur;           // [Hq][D], [Hkv][D]
-    float *key_slot, *value_slot;  // cache row T-1
+    const AttnPrep* prep;      // or null; when given, q and new_k / new_v are not read
 };
 bool attention_dims_supported(uint64_t head_dim, uint64_t rep);
 void attention_plan(uint64_t T, uint64_t Hkv, uint32_t& chunk, uint32_t& nchunks);
@@ -189,7 +191,6 @@ uint64_t attention_partial_floats(uint64_t Hkv, uint64_t rep, uint64_t head_dim,
 constexpr uint32_t kAttnMaxChunks = 8192;
 hipError_t launch_attention(const AttnLaunch& a, hipStream_t s);
 hipError_t launch_rope(float* heads, uint64_t n_heads, uint64_t head_dim, const RopeParams& p, hipStream_t s);
-hipError_t launch_attention_prep(const AttnPrep& a, hipStream_t s);
 
 // ---- oq_gemv_block.hip  (fused m = 1 GEMV of the DeltaNet decode block; see the kernel comment)
 enum : int { kBlockIn = 0, kBlockAdd = 1, kBlockFfn = 2 };

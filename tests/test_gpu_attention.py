@@ -341,6 +341,11 @@ BLOCKS = {
     "mixed": (dict(embedding=512, q_heads=4, kv_heads=2, head_dim=128, ffn=1024, rope_dim=32,
                    rope_sections=[6, 5, 5, 0], rope_base=1e6, eps=1e-6),
               dict(q=13, k=8, v=0, out=14, gate=13, up=1, down=8), 37),
+    # from an empty cache (the first step's only token is the new one), 8 query heads per KV head,
+    # rotation over the whole head
+    "empty_rep8": (dict(embedding=512, q_heads=8, kv_heads=1, head_dim=128, ffn=1024, rope_dim=128,
+                        rope_sections=[22, 21, 21, 0], rope_base=1e6, eps=1e-6),
+                   dict(q=12, k=12, v=12, out=14, gate=12, up=12, down=12), 0),
 }
 
 
