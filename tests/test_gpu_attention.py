@@ -346,6 +346,11 @@ BLOCKS = {
     "empty_rep8": (dict(embedding=512, q_heads=8, kv_heads=1, head_dim=128, ffn=1024, rope_dim=128,
                         rope_sections=[22, 21, 21, 0], rope_base=1e6, eps=1e-6),
                    dict(q=12, k=12, v=12, out=14, gate=12, up=12, down=12), 0),
+    # one query head per KV head, heads of 64 rotated whole, 16-token chunks: the first step's
+    # new token closes a full chunk, the next two open one
+    "rep1_d64": (dict(embedding=256, q_heads=4, kv_heads=4, head_dim=64, ffn=512, rope_dim=64,
+                      rope_sections=[11, 11, 10, 0], rope_base=1e4, eps=1e-6),
+                 dict(q=12, k=12, v=12, out=12, gate=12, up=12, down=14), 47),
 }
 
 
