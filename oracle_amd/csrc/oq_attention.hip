@@ -508,11 +508,19 @@ __global__ __launch_bounds__(256) void rope_kernel(float* heads, uint32_t head_d
 template <int D, int REP>
 hipError_t launch_chunks(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
     const dim3 grid(a.Hkv * a.nchunks);
-    // two passes in flight per wave: measured 56.1 us per step (chunk + merge, 16 query heads over
-    // 4 KV heads of 256, 32768 tokens) against 57.2 with one and 62.4 with three; the attention
-    // block at 4096 tokens (64-token chunks) also takes longest with more: 56.1 against 56.9 and
-    // 58.7 us with three and four
-    if (a.qfull != nullptr) {
+    // passes in flight per wave.  Long chunks: two, measured 56.1 us per step (chunk + merge, 16
+    // query heads over 4 KV heads of 256, 32768 tokens) against 57.2 with one and 62.4 with three;
+    // 64-token chunks also took longest with more (56.1 against 56.9 and 58.7 us with three and
+    // four, attention block at 4096 tokens).  Chunks of at most three passes take all of them at
+    // once, so keys and values each need one round trip: the attention block at 4097 tokens
+    // (48-token chunks) 54.3-55.2 -> 52.9-53.3 us.
+    if (a.chunk <= 3 * kTokStep) {
+        if (a.qfull != nullptr) {
+            hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 3, true>), grid, dim3(kAttnThreads), lds, s, a);
+        } else {
+            hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 3, false>), grid, dim3(kAttnThreads), lds, s, a);
+        }
+    } else if (a.qfull != nullptr) {
         hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 2, true>), grid, dim3(kAttnThreads), lds, s, a);
     } else {
         hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 2, false>), grid, dim3(kAttnThreads), lds, s, a);
