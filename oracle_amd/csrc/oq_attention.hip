@@ -510,11 +510,18 @@ hipError_t launch_chunks(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
     const dim3 grid(a.Hkv * a.nchunks);
     // passes in flight per wave.  Long chunks: two, measured 56.1 us per step (chunk + merge, 16
     // query heads over 4 KV heads of 256, 32768 tokens) against 57.2 with one and 62.4 with three;
-    // 64-token chunks also took longest with more (56.1 against 56.9 and 58.7 us with three and
-    // four, attention block at 4096 tokens).  Chunks of at most three passes take all of them at
-    // once, so keys and values each need one round trip: the attention block at 4097 tokens
-    // (48-token chunks) 54.3-55.2 -> 52.9-53.3 us.
-    if (a.chunk <= 3 * kTokStep) {
+    // four for 64-token chunks took 24.3 against 19.9 us at 8192 tokens.  A chunk of one, two or
+    // three passes keeps exactly that many in flight, so keys and values each need one round
+    // trip and no pass is a clamped copy of the chunk's last row: attention at 1024 / 2048 / 4096
+    // tokens 12.1 / 15.5 / 17.8 us with three passes in flight -> 9.45 / 12.3 / 15.6; the attention
+    // block at 4097 tokens (48-token chunks) 54.3-55.2 us with two -> 52.9-53.3 with three.
+    if (a.chunk <= kTokStep) {
+        if (a.qfull != nullptr) {
+            hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 1, true>), grid, dim3(kAttnThreads), lds, s, a);
+        } else {
+            hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 1, false>), grid, dim3(kAttnThreads), lds, s, a);
+        }
+    } else if (a.chunk > 2 * kTokStep && a.chunk <= 3 * kTokStep) {
         if (a.qfull != nullptr) {
             hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 3, true>), grid, dim3(kAttnThreads), lds, s, a);
         } else {
