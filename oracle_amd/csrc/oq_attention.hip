@@ -148,7 +148,9 @@ OQ_DEVICE void prep_row_norm(const float* x, const float* w, float eps, int lane
     for (int e = 0; e < VW; ++e) y[lane * VW + e] = x[e] * inv * w[e];
 }
 
-template <int D, int REP, int NB, bool PREP>
+// ONE: the chunk fits the NB passes in flight (chunk <= 16 NB tokens), so each loop below runs at
+// most once and requests nothing for a next iteration
+template <int D, int REP, int NB, bool PREP, bool ONE>
 __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs a) {
     constexpr int NV = D / 64;  // float4 of one key row per lane (16 lanes per row)
     constexpr int VW = D / 64;  // value columns per lane (64 lanes per row)
@@ -289,7 +291,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                     for (int h = 1; h < REP; ++h) v = l16 == h ? acc[h] : v;
                     sc[(uint32_t)l16 * a.chunk + (t - c0)] = v * a.scale;
                 }
-                load_keys(kb[b], pb + NB * kTokStep);
+                if constexpr (!ONE) load_keys(kb[b], pb + NB * kTokStep);
             }
         }
     }
@@ -367,7 +369,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                     for (int e = 0; e < VW; ++e) o[h][e] += p * v[e];
                 }
             }
-            load_values(vb[b], ib + NB * kGroup);
+            if constexpr (!ONE) load_values(vb[b], ib + NB * kGroup);
         }
     }
     __syncthreads();  // the probabilities are no longer read: reuse the LDS for the wave sums
@@ -505,9 +507,19 @@ __global__ __launch_bounds__(256) void rope_kernel(float* heads, uint32_t head_d
     for (uint32_t f = threadIdx.x; f < half; f += blockDim.x) rope_pair(x, f, half, p);
 }
 
+template <int D, int REP, int NB, bool ONE>
+hipError_t launch_nb(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
+    const dim3 grid(a.Hkv * a.nchunks);
+    if (a.qfull != nullptr) {
+        hipLaunchKernelGGL((attention_chunk_kernel<D, REP, NB, true, ONE>), grid, dim3(kAttnThreads), lds, s, a);
+    } else {
+        hipLaunchKernelGGL((attention_chunk_kernel<D, REP, NB, false, ONE>), grid, dim3(kAttnThreads), lds, s, a);
+    }
+    return hipGetLastError();
+}
+
 template <int D, int REP>
 hipError_t launch_chunks(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
-    const dim3 grid(a.Hkv * a.nchunks);
     // passes in flight per wave.  Long chunks: two, measured 56.1 us per step (chunk + merge, 16
     // query heads over 4 KV heads of 256, 32768 tokens) against 57.2 with one and 62.4 with three;
     // four for 64-token chunks took 24.3 against 19.9 us at 8192 tokens.  A chunk of one, two or
@@ -515,24 +527,10 @@ hipError_t launch_chunks(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
     // trip and no pass is a clamped copy of the chunk's last row: attention at 1024 / 2048 / 4096
     // tokens 12.1 / 15.5 / 17.8 us with three passes in flight -> 9.45 / 12.3 / 15.6; the attention
     // block at 4097 tokens (48-token chunks) 54.3-55.2 us with two -> 52.9-53.3 with three.
-    if (a.chunk <= kTokStep) {
-        if (a.qfull != nullptr) {
-            hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 1, true>), grid, dim3(kAttnThreads), lds, s, a);
-        } else {
-            hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 1, false>), grid, dim3(kAttnThreads), lds, s, a);
-        }
-    } else if (a.chunk > 2 * kTokStep && a.chunk <= 3 * kTokStep) {
-        if (a.qfull != nullptr) {
-            hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 3, true>), grid, dim3(kAttnThreads), lds, s, a);
-        } else {
-            hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 3, false>), grid, dim3(kAttnThreads), lds, s, a);
-        }
-    } else if (a.qfull != nullptr) {
-        hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 2, true>), grid, dim3(kAttnThreads), lds, s, a);
-    } else {
-        hipLaunchKernelGGL((attention_chunk_kernel<D, REP, 2, false>), grid, dim3(kAttnThreads), lds, s, a);
-    }
-    return hipGetLastError();
+    if (a.chunk <= kTokStep) return launch_nb<D, REP, 1, true>(a, lds, s);
+    if (a.chunk <= 2 * kTokStep) return launch_nb<D, REP, 2, true>(a, lds, s);
+    if (a.chunk <= 3 * kTokStep) return launch_nb<D, REP, 3, true>(a, lds, s);
+    return launch_nb<D, REP, 2, false>(a, lds, s);
 }
 
 template <int D>
