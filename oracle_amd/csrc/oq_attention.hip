@@ -148,8 +148,9 @@ OQ_DEVICE void prep_row_norm(const float* x, const float* w, float eps, int lane
     for (int e = 0; e < VW; ++e) y[lane * VW + e] = x[e] * inv * w[e];
 }
 
-// ONE: the chunk fits the NB passes in flight (chunk <= 16 NB tokens), so each loop below runs at
-// most once and requests nothing for a next iteration
+// Both phases run in blocks of NB passes (keys) or NB groups (values); every block but the last
+// requests the next block's rows as it consumes its own, and the last requests nothing.  ONE: the
+// chunk fits the NB passes in flight (chunk <= 16 NB tokens), so the last block is the only one.
 template <int D, int REP, int NB, bool PREP, bool ONE>
 __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs a) {
     constexpr int NV = D / 64;  // float4 of one key row per lane (16 lanes per row)
@@ -265,7 +266,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                 }
             }
         }
-        for (uint32_t base = first; base < c1; base += NB * kTokStep) {
+        auto score_block = [&](uint32_t base, auto reload) {
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 const uint32_t pb = base + (uint32_t)b * kTokStep;
@@ -291,9 +292,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                     for (int h = 1; h < REP; ++h) v = l16 == h ? acc[h] : v;
                     sc[(uint32_t)l16 * a.chunk + (t - c0)] = v * a.scale;
                 }
-                if constexpr (!ONE) load_keys(kb[b], pb + NB * kTokStep);
+                if constexpr (decltype(reload)::value) load_keys(kb[b], pb + NB * kTokStep);
             }
+        };
+        uint32_t base = first;
+        if constexpr (!ONE) {
+            for (; base + NB * kTokStep < c1; base += NB * kTokStep) score_block(base, std::true_type{});
         }
+        if (base < c1) score_block(base, std::false_type{});
     }
     if constexpr (PREP) {
         if (holds_new) {
@@ -350,7 +356,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
     for (int h = 0; h < REP; ++h)
 #pragma unroll
         for (int e = 0; e < VW; ++e) o[h][e] = 0.0f;
-    for (uint32_t i0 = (uint32_t)wave; i0 < n; i0 += NB * kGroup) {
+    auto value_block = [&](uint32_t i0, auto reload) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const uint32_t ib = i0 + (uint32_t)b * kGroup;
@@ -369,9 +375,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                     for (int e = 0; e < VW; ++e) o[h][e] += p * v[e];
                 }
             }
-            if constexpr (!ONE) load_values(vb[b], ib + NB * kGroup);
+            if constexpr (decltype(reload)::value) load_values(vb[b], ib + NB * kGroup);
         }
+    };
+    uint32_t i0 = (uint32_t)wave;
+    if constexpr (!ONE) {
+        for (; i0 + NB * kGroup < n; i0 += NB * kGroup) value_block(i0, std::true_type{});
     }
+    if (i0 < n) value_block(i0, std::false_type{});
     __syncthreads();  // the probabilities are no longer read: reuse the LDS for the wave sums
     float* red = lds;  // [wave][rep][D]
 #pragma unroll
