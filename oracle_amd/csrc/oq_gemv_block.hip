@@ -435,6 +435,159 @@ __global__ __launch_bounds__(1024) void gemv_block_add_stream_kernel(BlockGemv a
     }
 }
 
+// The normalised in-projection without per-row epilogue (the attention block's q / k / v: raw
+// outputs only) streamed like the residual projections.  Staging: each wave requests its x
+// blocks and their norm weights, then its first row's weights; RMSNorm (qwen35_block.cpp:161-189,
+// sum of squares in double, the 16 waves' sums added in wave order); x' quantized to Q8_K in LDS.
+// Rows of the concatenation mat[0] | mat[1] | .. are walked as in gemv_block_add_stream_kernel.
+template <uint32_t TYPE, int ITERS, bool FULL>
+__global__ __launch_bounds__(1024) void gemv_block_in_stream_kernel(BlockGemv a) {
+    constexpr int WAVES = 16;
+    constexpr int SBW = (ITERS * 16 + WAVES - 1) / WAVES;
+    using WR = typename WRegs<TYPE>::type;
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ double red[WAVES];
+    const int lane = threadIdx.x & 63;
+    const int wave_in_wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = gridDim.x * WAVES;
+    const uint64_t k = a.mat[0].k;
+    const uint32_t nsb = (uint32_t)(k / kQK);
+    const uint32_t n = a.row_end[a.nmat - 1];
+    const ActLds s{smem, k};
+    const uint32_t first = blockIdx.x * WAVES + (uint32_t)wave_in_wg;
+    auto row_base = [&](uint32_t row) {
+        row = row < n ? row : n - 1;  // a wave without rows reads row n-1
+        uint32_t mi, local;
+        blk_in_row(a, row, mi, local);
+        return a.mat[mi].base + (uint64_t)local * a.mat[mi].pitch;
+    };
+
+    float4 xv[SBW], nv[SBW];
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        b = b < nsb ? b : nsb - 1;
+        xv[j] = reinterpret_cast<const float4*>(a.x + b * kQK)[lane];
+        nv[j] = reinterpret_cast<const float4*>(a.norm_w + b * kQK)[lane];
+    }
+    asm volatile("" ::: "memory");
+    WR buf[2];
+    load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane);
+    {
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < SBW; ++j) {
+            const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+            if (b < nsb) {
+                ss += (double)xv[j].x * (double)xv[j].x + (double)xv[j].y * (double)xv[j].y +
+                      (double)xv[j].z * (double)xv[j].z + (double)xv[j].w * (double)xv[j].w;
+            }
+        }
+        ss = blk::wave_sum_f64(ss);
+        if (lane == 0) red[wave_in_wg] = ss;
+    }
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int i = 0; i < WAVES; ++i) tot += red[i];
+    const float inv = (float)(1.0 / sqrt(tot / (double)k + (double)a.eps));
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        if (b >= nsb) break;
+        float4 v;
+        {
+#pragma clang fp contract(off)
+            v.x = xv[j].x * inv * nv[j].x;
+            v.y = xv[j].y * inv * nv[j].y;
+            v.z = xv[j].z * inv * nv[j].z;
+            v.w = xv[j].w * inv * nv[j].w;
+        }
+        if (blockIdx.x == 0 && a.norm_out) reinterpret_cast<float4*>(a.norm_out + b * kQK)[lane] = v;
+        uint32_t qw;
+        int bs;
+        float d;
+        quantize_block(v, lane, qw, bs, d);
+        store_block<TYPE>(s, 0, b, lane, qw, bs, d);
+    }
+    __syncthreads();
+    if (first >= n) return;
+
+    // row -> (matrix, local row) per lane, for the deferred stores
+    auto store_row = [&](uint32_t row, float v) {
+        uint32_t mi = 0;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+            if ((uint32_t)i + 1 < a.nmat && row >= a.row_end[i]) mi = (uint32_t)i + 1;
+        const uint32_t local = row - (mi ? a.row_end[mi - 1] : 0u);
+        float* dst = mi == 0 ? a.raw[0] : mi == 1 ? a.raw[1] : mi == 2 ? a.raw[2] : a.raw[3];
+        dst[local] = v;
+    };
+    const int q = lane & 3;
+    const ScaleSel ss = scale_sel(q);
+    constexpr bool kActRegs = ITERS <= 2;
+    Act act[kActRegs ? ITERS : 1];
+    if constexpr (kActRegs) {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const uint32_t sb = 16u * it + (lane >> 2);
+            if (sb < nsb) slice_from_lds<TYPE>(act[it], s, 0, sb, q);
+        }
+    }
+    float acc = 0.0f, out = 0.0f;
+    uint32_t out_row = 0, done = 0;
+    uint32_t row = first, it = 0;  // the unit whose loads are in flight
+    bool more = true;
+    while (more) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int its = ITERS == 1 ? 0 : (ITERS == 2 ? j : (int)it);
+            asm volatile("s_waitcnt vmcnt(0)" : "+v"(acc), "+v"(out)::"memory");
+            uint32_t nrow = row, nit = it + 1;
+            if (nit == ITERS) {
+                nrow = row + nw < row ? n : row + nw;
+                nit = 0;
+            }
+            more = nrow < n;
+            load_w<TYPE>(buf[(j + 1) & 1], row_base(more ? nrow : row), nsb, (int)(more ? nit : it), lane);
+            hold<TYPE>(buf[j & 1]);
+            const uint32_t sb = 16u * (uint32_t)its + (lane >> 2);
+            if (FULL || sb < nsb) {
+                if constexpr (kActRegs) {
+                    acc = lane_fma(decode_w<TYPE>(buf[j & 1], ss, q), act[its], acc);
+                } else {
+                    Act av;
+                    slice_from_lds<TYPE>(av, s, 0, sb, q);
+                    acc = lane_fma(decode_w<TYPE>(buf[j & 1], ss, q), av, acc);
+                }
+            }
+            if (it == ITERS - 1) {
+                const float v = wave_sum_uniform(acc);
+                const bool mine = lane == (int)(done & 63u);
+                out = mine ? v : out;
+                out_row = mine ? row : out_row;
+                acc = 0.0f;
+                ++done;
+                if ((done & 63u) == 0u) store_row(out_row, out);
+            }
+            row = nrow;
+            it = nit;
+            if (!more) break;
+        }
+    }
+    if ((uint32_t)lane < (done & 63u)) store_row(out_row, out);
+}
+
+template <uint32_t TYPE, int ITERS, bool FULL>
+hipError_t launch_block_in_stream(const BlockGemv& a, hipStream_t s) {
+    const uint64_t lds = act_lds_bytes(a.mat[0].k, 1);
+    uint64_t wgs = (uint64_t)cu_count();
+    const uint64_t need = ((uint64_t)a.row_end[a.nmat - 1] + 15) / 16;
+    if (wgs > need) wgs = need;
+    hipLaunchKernelGGL((gemv_block_in_stream_kernel<TYPE, ITERS, FULL>), dim3((unsigned)wgs), dim3(1024), lds, s, a);
+    return hipGetLastError();
+}
+
 template <uint32_t TYPE, int ITERS, bool FULL>
 hipError_t launch_block_add_stream(const BlockGemv& a, hipStream_t s) {
     const uint64_t lds = act_lds_bytes(a.mat[0].k, 1);
@@ -452,6 +605,9 @@ hipError_t launch_block_full(const BlockGemv& a, hipStream_t s) {
         // GEMV (FFN down 4096 x 12288: 9.3 us against 11.1 us in the structure below)
         if (gemv_block_add_streams(a)) return launch_block_add_stream<TYPE, ITERS, FULL>(a, s);
         if (a.rec != nullptr) return hipErrorInvalidValue;  // only the streamed kernel forms the gated row
+    }
+    if constexpr (MODE == kBlockIn) {
+        if (gemv_block_in_streams(a)) return launch_block_in_stream<TYPE, ITERS, FULL>(a, s);
     }
     const uint64_t groups = MODE == kBlockFfn ? a.mat[0].n : ((uint64_t)a.row_end[a.nmat - 1] + 1) / 2;
     const uint64_t lds = act_lds_bytes(a.mat[0].k, 1);
@@ -495,6 +651,11 @@ hipError_t launch_block_mode(const BlockGemv& a, hipStream_t s) {
 }  // namespace
 
 bool gemv_block_add_streams(const BlockGemv& a) { return a.norm_w == nullptr && knob(kBlockStream, 1) != 0; }
+
+bool gemv_block_in_streams(const BlockGemv& a) {
+    return a.norm_w != nullptr && a.conv_w == nullptr && a.beta_s == nullptr && a.log_decay == nullptr &&
+           knob(kBlockStream, 1) != 0;
+}
 
 bool gemv_block_supported(const BlockGemv& a) {
     if (a.nmat < 1 || a.nmat > 4) return false;

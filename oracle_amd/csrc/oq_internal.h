@@ -229,6 +229,8 @@ bool gemv_block_supported(const BlockGemv& a);
 // whether launch_gemv_block(kBlockAdd, a) runs the streamed kernel (the one that can form the
 // gated activation itself)
 bool gemv_block_add_streams(const BlockGemv& a);
+// whether launch_gemv_block(kBlockIn, a) runs the streamed kernel (normalised, raw outputs only)
+bool gemv_block_in_streams(const BlockGemv& a);
 hipError_t launch_gemv_block(int mode, const BlockGemv& a, hipStream_t s);
 
 // ---- oq_api.cpp: the block step on a caller-provided workspace (validation, capacity check, launches)

@@ -136,8 +136,8 @@ SMALL = dict(synth.DELTANET_DIMS, embedding=1024, key_heads=2, value_heads=4, ff
 def test_deltanet_steps_match_oracle(ctx, dims, env):
     """Every device schedule: the fused one (five launches: normalised in-projections with the
     convolution and gates, delta rule, out projection + residual, normalised gate/up + SwiGLU,
-    down + residual; the in- and residual projections streamed, or with OQ_BLOCK_STREAM=0 in the
-    batched structure) and the one launch per stage (OQ_BLOCK_FUSED=0)."""
+    down + residual; the residual projections streamed, or with OQ_BLOCK_STREAM=0 in the batched
+    structure) and the one launch per stage (OQ_BLOCK_FUSED=0)."""
     d, w, vec, hist, st, _ = synth.deltanet_block(np.random.default_rng(21), dims)
     rng = np.random.default_rng(22)
     xs = [rng.standard_normal(d["embedding"]).astype(np.float32) for _ in range(3)]
