@@ -351,6 +351,14 @@ BLOCKS = {
     "rep1_d64": (dict(embedding=256, q_heads=4, kv_heads=4, head_dim=64, ffn=512, rope_dim=64,
                       rope_sections=[11, 11, 10, 0], rope_base=1e4, eps=1e-6),
                  dict(q=12, k=12, v=12, out=12, gate=12, up=12, down=14), 47),
+    # long activation rows: the streamed q / k / v projection walks each row in two units (8192)
+    # or three with a partial last one (8448 = 33 super-blocks)
+    "e8192": (dict(embedding=8192, q_heads=4, kv_heads=2, head_dim=64, ffn=512, rope_dim=64,
+                   rope_sections=[11, 11, 10, 0], rope_base=1e6, eps=1e-6),
+              dict(q=12, k=12, v=12, out=12, gate=12, up=12, down=12), 20),
+    "e8448": (dict(embedding=8448, q_heads=4, kv_heads=2, head_dim=64, ffn=512, rope_dim=64,
+                   rope_sections=[11, 11, 10, 0], rope_base=1e6, eps=1e-6),
+              dict(q=12, k=12, v=12, out=14, gate=12, up=12, down=12), 20),
 }
 
 
