@@ -45,7 +45,6 @@ constexpr int kAttnThreads = kAttnWaves * 64;
 constexpr uint32_t kTokStep = kAttnWaves * 4;  // tokens per workgroup pass in the score phase
 constexpr uint32_t kMaxChunk = 1024;
 constexpr int kMergeGroups = 16;  // chunk groups of the merge kernel
-constexpr int kMergeUnroll = 8;   // chunks in flight per merge thread
 
 struct ChunkArgs {
     const float* q;       // [Hq][D]
@@ -411,7 +410,7 @@ OQ_DEVICE float sigmoid_ref(float v) {
     return e / (1.0f + e);
 }
 
-template <int D>
+template <int D, int kMergeUnroll>
 __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
     constexpr int SLICES = D / 64;
     __shared__ float4 s_o[kMergeGroups][16];
@@ -595,7 +594,12 @@ hipError_t launch_d(const AttnLaunch& L, hipStream_t s) {
     m.gate_stride = L.gate_stride;
     m.gate_s = L.gate_s;
     m.gated = L.gated;
-    hipLaunchKernelGGL((attention_merge_kernel<D>), dim3(L.Hkv * L.rep * (D / 64)), dim3(256), 0, s, m);
+    // chunks in flight per merge thread: as many as the chunks need, up to 8 (no clamped repeats
+    // of the last chunk): 256 / 512 / 1024 tokens 8.87 / 8.98 / 9.34 -> 8.43 / 8.52 / 9.05 us
+    const dim3 mgrid(L.Hkv * L.rep * (D / 64));
+    if (L.nchunks <= 2 * kMergeGroups) hipLaunchKernelGGL((attention_merge_kernel<D, 2>), mgrid, dim3(256), 0, s, m);
+    else if (L.nchunks <= 4 * kMergeGroups) hipLaunchKernelGGL((attention_merge_kernel<D, 4>), mgrid, dim3(256), 0, s, m);
+    else hipLaunchKernelGGL((attention_merge_kernel<D, 8>), mgrid, dim3(256), 0, s, m);
     return hipGetLastError();
 }
 
