@@ -62,7 +62,9 @@ OQ_DEVICE uint32_t pack_f16(float a, float b) {
 // F32 x [m][K] -> f16(d * q) with the Q8_K quantization of quantize_q8k.  A wave quantizes
 // kQuantBlocksPerWave blocks (one at a time, their loads issued together); a workgroup's four waves
 // take consecutive blocks, so each load instruction of the workgroup reads 4 KiB of consecutive x.
-constexpr int kQuantBlocksPerWave = 4;
+// Two blocks per wave: 512 x 12288 took 7.4 us against 8.1 / 8.3 / 9.0 with one / four / eight
+// (the quantization arithmetic, 1.5 us of the launch with four, overlaps the loads better).
+constexpr int kQuantBlocksPerWave = 2;
 
 __global__ __launch_bounds__(256) void quantize_f16_kernel(const float* __restrict__ x, uint64_t nblocks,
                                                            _Float16* __restrict__ out) {
