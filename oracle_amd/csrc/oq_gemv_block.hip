@@ -400,7 +400,8 @@ __global__ __launch_bounds__(1024) void gemv_block_add_stream_kernel(BlockGemv a
                 nit = 0;
             }
             more = nrow < n;
-            load_w<TYPE>(buf[(j + 1) & 1], row_base(more ? nrow : row), nsb, (int)(more ? nit : it), lane);
+            // as gemv_stream_kernel: rows of one unit request nothing past the wave's last row
+            if (ITERS != 1 || more) load_w<TYPE>(buf[(j + 1) & 1], row_base(more ? nrow : row), nsb, (int)(more ? nit : it), lane);
             hold<TYPE>(buf[j & 1]);
             const uint32_t sb = 16u * (uint32_t)its + (lane >> 2);
             if (FULL || sb < nsb) {
@@ -549,7 +550,8 @@ __global__ __launch_bounds__(1024) void gemv_block_in_stream_kernel(BlockGemv a)
                 nit = 0;
             }
             more = nrow < n;
-            load_w<TYPE>(buf[(j + 1) & 1], row_base(more ? nrow : row), nsb, (int)(more ? nit : it), lane);
+            // as gemv_stream_kernel: rows of one unit request nothing past the wave's last row
+            if (ITERS != 1 || more) load_w<TYPE>(buf[(j + 1) & 1], row_base(more ? nrow : row), nsb, (int)(more ? nit : it), lane);
             hold<TYPE>(buf[j & 1]);
             const uint32_t sb = 16u * (uint32_t)its + (lane >> 2);
             if (FULL || sb < nsb) {
