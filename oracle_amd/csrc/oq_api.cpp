@@ -387,10 +387,12 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
     in.x = x;
     in.norm_w = b->input_norm;
     in.eps = b->eps;
-    in.raw[0] = qkv;
+    // the raw q/k/v, beta and alpha rows feed only the trace (the delta rule reads the
+    // convolution's output and the gates): without a trace they are not stored
+    in.raw[0] = trace ? qkv : nullptr;
     in.raw[1] = z;
-    in.raw[2] = beta;
-    in.raw[3] = alpha;
+    in.raw[2] = trace ? beta : nullptr;
+    in.raw[3] = trace ? alpha : nullptr;
     in.conv_w = b->conv_weight;
     in.history = hist;
     in.conv_kernel = (uint32_t)K;

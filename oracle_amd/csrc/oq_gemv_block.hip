@@ -148,7 +148,7 @@ OQ_DEVICE void blk_epilogue(const BlockGemv& a, uint64_t grp, int lane, float v0
             uint32_t mi, l;
             blk_in_row(a, row, mi, l);
             const float v = r == 0 ? v0 : v1;
-            if (lane == r) a.raw[mi][l] = v;
+            if (lane == r && a.raw[mi] != nullptr) a.raw[mi][l] = v;
             if (mi == 0 && a.conv_w != nullptr) {
                 // causal depthwise convolution step of channel l (reference_kernels.cpp:197-225) +
                 // SiLU: the history shifts by one (tap i takes value i + 1, the last tap the new
