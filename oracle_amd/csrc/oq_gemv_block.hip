@@ -17,11 +17,11 @@ using namespace kq;
 //             stores x' (norm_out)
 //   rows      IN: the concatenation of up to four matrices sharing K and type (row pairs never
 //             straddle two); FFN: pair g = (row g of mat[0], row g of mat[1]); ADD: one matrix
-//   epilogue  IN: raw outputs; rows of mat[0] (qkv) run their channel's causal convolution step
-//             and SiLU, rows of mat[2] (beta) the sigmoid, rows of mat[3] (alpha) softplus(a +
-//             dt_bias) * decay -- each only when its output is given (the attention block's
-//             q / k / v projections take raw outputs only); ADD: sum_out[n] = add[n] + y[n];
-//             FFN: act[g] = SiLU(gate) * up.
+//   epilogue  IN: raw outputs (of the matrices whose raw[i] is given); rows of mat[0] (qkv) run
+//             their channel's causal convolution step and SiLU, rows of mat[2] (beta) the
+//             sigmoid, rows of mat[3] (alpha) softplus(a + dt_bias) * decay -- each only when its
+//             output is given (the attention block's q / k / v projections take raw outputs
+//             only); ADD: sum_out[n] = add[n] + y[n]; FFN: act[g] = SiLU(gate) * up.
 namespace blk {
 
 OQ_DEVICE float sigmoid_ref(float v) {
