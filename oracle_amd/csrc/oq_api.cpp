@@ -405,7 +405,7 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
     outp.mat[0] = b->out->m;
     outp.row_end[0] = (uint32_t)E;
     outp.x = gated;
-    outp.raw[0] = branch;
+    outp.raw[0] = trace ? branch : nullptr;  // raw outputs and staged rows: only the trace reads them
     outp.add = x;
     outp.sum_out = resid;
     outp.eps = b->eps;
@@ -418,7 +418,7 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
         outp.out_norm = b->out_norm;
         outp.dv = (uint32_t)dv;
         outp.dchunks = (uint32_t)oq::delta_chunks(dv);
-        outp.gated_out = gated;
+        outp.gated_out = trace ? gated : nullptr;
     }
     ffn_in.nmat = 2;
     ffn_in.mat[0] = b->gate->m;
@@ -428,15 +428,15 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
     ffn_in.x = resid;
     ffn_in.norm_w = b->post_norm;
     ffn_in.eps = b->eps;
-    ffn_in.norm_out = post;
-    ffn_in.raw[0] = gate;
-    ffn_in.raw[1] = up;
+    ffn_in.norm_out = trace ? post : nullptr;
+    ffn_in.raw[0] = trace ? gate : nullptr;
+    ffn_in.raw[1] = trace ? up : nullptr;
     ffn_in.act = act;
     down.nmat = 1;
     down.mat[0] = b->down->m;
     down.row_end[0] = (uint32_t)E;
     down.x = act;
-    down.raw[0] = ffn;
+    down.raw[0] = trace ? ffn : nullptr;
     down.add = resid;
     down.sum_out = y;
     const bool even = C % 2 == 0 && V % 2 == 0 && Hv % 2 == 0 && E % 2 == 0;
@@ -1161,7 +1161,7 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_
     outp.mat[0] = b->out->m;
     outp.row_end[0] = (uint32_t)E;
     outp.x = gated;
-    outp.raw[0] = branch;
+    outp.raw[0] = trace ? branch : nullptr;  // raw outputs and per-head copies: only the trace reads them
     outp.add = x;
     outp.sum_out = resid;
     ffn_in.nmat = 2;
@@ -1172,15 +1172,15 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_
     ffn_in.x = resid;
     ffn_in.norm_w = b->post_norm;
     ffn_in.eps = b->eps;
-    ffn_in.norm_out = post;
-    ffn_in.raw[0] = gate;
-    ffn_in.raw[1] = up;
+    ffn_in.norm_out = trace ? post : nullptr;
+    ffn_in.raw[0] = trace ? gate : nullptr;
+    ffn_in.raw[1] = trace ? up : nullptr;
     ffn_in.act = act;
     down.nmat = 1;
     down.mat[0] = b->down->m;
     down.row_end[0] = (uint32_t)E;
     down.x = act;
-    down.raw[0] = ffn;
+    down.raw[0] = trace ? ffn : nullptr;
     down.add = resid;
     down.sum_out = y;
 
@@ -1192,14 +1192,14 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_
     prep.k_norm = b->k_norm;
     prep.eps = b->eps;
     prep.rope = rp;
-    prep.qcur = qcur;
-    prep.kcur = kcur;
+    prep.qcur = trace ? qcur : nullptr;
+    prep.kcur = trace ? kcur : nullptr;
     L.prep = &prep;
     L.part = part;
-    L.out = pregate;
+    L.out = trace ? pregate : nullptr;
     L.gate = qfull + D;
     L.gate_stride = (uint32_t)(2 * D);
-    L.gate_s = gate_s;
+    L.gate_s = trace ? gate_s : nullptr;
     L.gated = gated;
 
     const bool even = E % 2 == 0 && F % 2 == 0;

@@ -253,13 +253,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                 for (int j = 0; j < NV; ++j) qr[h][j] = *reinterpret_cast<const float4*>(stage + hh * D + 4 * (j * 16 + l16));
             }
             // the trace's copies, and the append of the new key and value rows
-            if (c == 0) {
+            if (c == 0 && a.qcur != nullptr) {
                 for (uint32_t i = threadIdx.x; i < rep * D; i += kAttnThreads) a.qcur[(uint64_t)g * rep * D + i] = stage[i];
             }
             if (holds_new) {
                 for (uint32_t i = threadIdx.x; i < (uint32_t)D; i += kAttnThreads) {
                     const float k = stage[rep * D + i];
-                    a.kcur[(uint64_t)g * D + i] = k;
+                    if (a.kcur != nullptr) a.kcur[(uint64_t)g * D + i] = k;
                     a.keys[((uint64_t)last * a.Hkv + g) * D + i] = k;
                     a.values[((uint64_t)last * a.Hkv + g) * D + i] = a.new_v[(uint64_t)g * D + i];
                 }
@@ -494,10 +494,10 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
         O.w += v.w;
     }
     const float out[4] = {O.x / L, O.y / L, O.z / L, O.w / L};
-    *reinterpret_cast<float4*>(a.out + base) = make_float4(out[0], out[1], out[2], out[3]);
+    if (a.out != nullptr) *reinterpret_cast<float4*>(a.out + base) = make_float4(out[0], out[1], out[2], out[3]);
     if (a.gate != nullptr) {
         const float gs[4] = {sigmoid_ref(gv.x), sigmoid_ref(gv.y), sigmoid_ref(gv.z), sigmoid_ref(gv.w)};
-        *reinterpret_cast<float4*>(a.gate_s + base) = make_float4(gs[0], gs[1], gs[2], gs[3]);
+        if (a.gate_s != nullptr) *reinterpret_cast<float4*>(a.gate_s + base) = make_float4(gs[0], gs[1], gs[2], gs[3]);
         *reinterpret_cast<float4*>(a.gated + base) = make_float4(out[0] * gs[0], out[1] * gs[1], out[2] * gs[2],
                                                                  out[3] * gs[3]);
     }

@@ -127,16 +127,16 @@ OQ_DEVICE void blk_epilogue(const BlockGemv& a, uint64_t grp, int lane, float v0
         // lane 0: gate row grp, lane 1: up row grp
         if (lane == 0) {
 #pragma clang fp contract(off)
-            a.raw[0][grp] = v0;
+            if (a.raw[0] != nullptr) a.raw[0][grp] = v0;
             a.act[grp] = blk::silu_ref(v0) * v1;
-        } else if (lane == 1) {
+        } else if (lane == 1 && a.raw[1] != nullptr) {
             a.raw[1][grp] = v1;
         }
     } else if constexpr (MODE == kBlockAdd) {
         const uint64_t row = grp * 2 + lane;
         if (lane < 2 && row < a.mat[0].n) {
             const float v = lane == 0 ? v0 : v1;
-            a.raw[0][row] = v;
+            if (a.raw[0] != nullptr) a.raw[0][row] = v;
             a.sum_out[row] = a.add[row] + v;
         }
     } else {
@@ -337,7 +337,7 @@ OQ_DEVICE void stage_gated_row(const ActLds& s, const BlockGemv& a, uint64_t nsb
         g.y = rv[j].y * inv * wv[j].y * zv[j].y;
         g.z = rv[j].z * inv * wv[j].z * zv[j].z;
         g.w = rv[j].w * inv * wv[j].w * zv[j].w;
-        if (blockIdx.x == 0) reinterpret_cast<float4*>(a.gated_out + b * kQK)[lane] = g;
+        if (blockIdx.x == 0 && a.gated_out != nullptr) reinterpret_cast<float4*>(a.gated_out + b * kQK)[lane] = g;
         uint32_t qw;
         int bs;
         float d;
@@ -421,7 +421,7 @@ __global__ __launch_bounds__(1024) void gemv_block_add_stream_kernel(BlockGemv a
                 acc = 0.0f;
                 ++done;
                 if ((done & 63u) == 0u) {
-                    a.raw[0][out_row] = out;
+                    if (a.raw[0] != nullptr) a.raw[0][out_row] = out;
                     a.sum_out[out_row] = a.add[out_row] + out;
                 }
             }
@@ -431,7 +431,7 @@ __global__ __launch_bounds__(1024) void gemv_block_add_stream_kernel(BlockGemv a
         }
     }
     if ((uint32_t)lane < (done & 63u)) {
-        a.raw[0][out_row] = out;
+        if (a.raw[0] != nullptr) a.raw[0][out_row] = out;
         a.sum_out[out_row] = a.add[out_row] + out;
     }
 }

@@ -167,7 +167,7 @@ struct AttnPrep {
     const float *q_norm, *k_norm;
     float eps;
     RopeParams rope;
-    float *qcur, *kcur;           // [Hq][D], [Hkv][D]
+    float *qcur, *kcur;           // [Hq][D], [Hkv][D], or null (not stored)
 };
 struct AttnLaunch {
     const float* q;            // [Hkv * rep][D]
@@ -178,10 +178,10 @@ struct AttnLaunch {
     uint32_t T, Hkv, rep, D, chunk, nchunks;
     float scale;               // 1 / sqrt(D)
     float* part;               // attention_partial_floats(Hkv, rep, D, nchunks) floats
-    float* out;                // [Hkv * rep][D]
+    float* out;                // [Hkv * rep][D]; with a gate, may be null (not stored)
     const float* gate;         // raw output gate of head h at gate + h * gate_stride, or null
     uint32_t gate_stride;
-    float* gate_s;             // sigmoid(gate) [Hq][D] and out * sigmoid(gate), when gate is given
+    float* gate_s;             // sigmoid(gate) [Hq][D] (or null: not stored) and out * sigmoid(gate), when gate is given
     float* gated;
     const AttnPrep* prep;      // or null; when given, q and new_k / new_v are not read
 };
@@ -202,7 +202,7 @@ struct BlockGemv {
     const float* norm_w;   // RMSNorm weight (K values) or null
     float eps;
     float* norm_out;       // the normalised activation (written by workgroup 0) or null
-    float* raw[4];         // per-matrix outputs
+    float* raw[4];         // per-matrix outputs (or null: not stored; the attention block's IN needs them)
     const float* conv_w;   // IN: convolution taps [rows of mat[0]][conv_kernel]
     float* history;        // IN: convolution history, same shape, updated in place
     uint32_t conv_kernel;
