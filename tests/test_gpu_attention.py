@@ -377,6 +377,51 @@ def test_attention_block_stages(ctx, name):
         assert float(np.max(np.abs(st["y"] - y))) <= CHAIN_TOL * float(np.max(np.abs(y)))
 
 
+@pytest.mark.parametrize("name", ["e2048", "rep1_d64"])
+def test_attention_block_trace_does_not_change_results(ctx, name):
+    """Without a trace the block skips the stores only the trace reads (qcur / kcur, the pre-gate
+    output, sigmoid(gate), the raw residual and gate/up rows): y and the cache must be the same
+    bits."""
+    from golden.make_golden import attention_inputs
+    d, types, cached = BLOCKS[name]
+    w, vec, c, xs = attention_inputs(np.random.default_rng(77), d, types, cached=cached)
+    hkv, D = d["kv_heads"], d["head_dim"]
+    blk = oracle_amd.AttentionBlockWeights(ctx, d, w, vec)
+    caches, bufs = [], []
+    try:
+        tb = ctx.alloc(sum(oracle.attention_trace_sizes(d).values()) * 4)
+        bufs.append(tb)
+        runs = []
+        for traced in (True, False):
+            cache = ctx.kv_cache(c.capacity, hkv, D, D)
+            caches.append(cache)
+            cache.load(c.keys, c.values, c.length)
+            yb = ctx.alloc(d["embedding"] * 4)
+            bufs.append(yb)
+            ys = []
+            for i, x in enumerate(xs[:2]):
+                xb = ctx.to_device(x)
+                pos = (cached + i, cached + i, cached + i)
+                if traced:
+                    ctx.attention_block_step(blk, cache, pos, xb, yb, tb)
+                else:
+                    ctx.attention_block_step(blk, cache, pos, xb, yb)
+                ctx.sync()
+                ys.append(yb.download(np.float32, d["embedding"]))
+                xb.free()
+            runs.append((ys, *cache.download(hkv, D, D)))
+        (y_t, k_t, v_t), (y_n, k_n, v_n) = runs
+        for a, b in zip(y_t, y_n):
+            assert np.array_equal(a, b)
+        assert np.array_equal(k_t, k_n) and np.array_equal(v_t, v_n)
+    finally:
+        for b in bufs:
+            b.free()
+        for cache in caches:
+            cache.release()
+        blk.release()
+
+
 def test_attention_block_errors(ctx):
     from golden.make_golden import ATTN_KQ_DIMS, ATTN_KQ_TYPES, attention_inputs
     d = dict(ATTN_KQ_DIMS)

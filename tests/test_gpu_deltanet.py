@@ -167,6 +167,45 @@ def test_deltanet_full_block_matches_oracle(ctx):
     check_history(steps[0], hist_g)
 
 
+@pytest.mark.parametrize("dims", [SMALL, dict(SMALL, conv_kernel=3)], ids=["k4", "k3"])
+@pytest.mark.parametrize("env", [{}, {"OQ_BLOCK_STREAM": "0"}], ids=["streamed", "batched"])
+def test_deltanet_trace_does_not_change_results(ctx, dims, env):
+    """Without a trace the block skips the stores only the trace reads (raw projections, the
+    normalised FFN input, the gated row): y, the state and the history must be the same bits."""
+    d, w, vec, hist, st, _ = synth.deltanet_block(np.random.default_rng(41), dims)
+    rng = np.random.default_rng(42)
+    xs = [rng.standard_normal(d["embedding"]).astype(np.float32) for _ in range(2)]
+    blk = oracle_amd.DeltaNetBlockWeights(ctx, d, w, vec)
+    bufs = []
+    try:
+        tb = ctx.alloc(sum(oracle.deltanet_trace_sizes(d).values()) * 4)
+        bufs.append(tb)
+        runs = []
+        for traced in (True, False):
+            hb, sb, yb = ctx.to_device(hist), ctx.to_device(st), ctx.alloc(d["embedding"] * 4)
+            bufs += [hb, sb, yb]
+            ys = []
+            for x in xs:
+                xb = ctx.to_device(x)
+                with oracle_amd.launch_options(env):
+                    if traced:
+                        ctx.deltanet_step(blk, hb, sb, xb, yb, tb)
+                    else:
+                        ctx.deltanet_step(blk, hb, sb, xb, yb)
+                ctx.sync()
+                ys.append(yb.download(np.float32, d["embedding"]))
+                xb.free()
+            runs.append((ys, hb.download(np.float32, hist.size), sb.download(np.float32, st.size)))
+        (y_t, h_t, s_t), (y_n, h_n, s_n) = runs
+        for a, b in zip(y_t, y_n):
+            assert np.array_equal(a, b)
+        assert np.array_equal(h_t, h_n) and np.array_equal(s_t, s_n)
+    finally:
+        for b in bufs:
+            b.free()
+        blk.release()
+
+
 def test_deltanet_rejects_bad_shapes(ctx):
     d, w, vec, hist, st, x = synth.deltanet_block(np.random.default_rng(41), SMALL)
     blk = oracle_amd.DeltaNetBlockWeights(ctx, d, w, vec)
