@@ -14,6 +14,12 @@
  *                         derived KATs (0.25 / 1.25 / -0.75) + single-hot scale packing
  *   orc_storage_dot/matvec reference KATs (4288, 8576, -192, 4480, 14, 64) + bitwise equality
  *                         with the compiled reference on random rows
+ *   orc_storage_matmul_mt  m > 1: each output row bit-equal to the matvec of that activation
+ *                         row (and to the compiled reference), for 1 and 4 threads
+ *   orc_storage_dot_stats / orc_storage_matvec_stats  numpy float64 sums of w*x and |w*x| over
+ *                         the decoded rows, every type, ragged sizes; planted wrong normalisers
+ *                         (sum|w| max|x|, |sum w x|, half a row) are rejected by the same check
+ *   orc_fnv1a64           the published FNV-1a-64 vectors ("", "a", "foobar")
  *   orc_quantize_row_q8_k  hand KATs and GGML invariants (|q| <= 127, q[argmax] = -127,
  *                         bsums, |d q - x| <= |d|/2, zero block, first-index tie break)
  *   orc_vec_dot_q8_k       algebraic identity with orc_storage_dot on the dequantized Q8_K

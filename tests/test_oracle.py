@@ -370,3 +370,110 @@ def test_live_reference_random_rows():
     y5 = oracle.ref_storage_matvec(13, rows, cols, q5.reshape(-1), x)
     y4 = oracle.storage_matvec(12, rows, cols, q4, x)
     assert np.array_equal(y5.view(np.uint32), y4.view(np.uint32))
+
+
+# ---------------------------------------------------------------- tolerance normaliser, helpers
+
+def _plain_rows(t, rng, rows, cols):
+    """Seeded rows of an unquantized type (f32 = 0, f16 = 1, bf16 = 30) as raw bytes."""
+    v = rng.standard_normal((rows, cols)).astype(np.float32) * 0.05
+    if t == 0:
+        return v.view(np.uint8).reshape(-1)
+    if t == 1:
+        return v.astype(np.float16).view(np.uint8).reshape(-1)
+    return (v.view(np.uint32) >> 16).astype("<u2").view(np.uint8).reshape(-1)
+
+
+def _normaliser_agrees(got_dot, got_abs, want_dot, want_abs):
+    """The stats agree with a float64 recomputation to 1e-12 of the row's sum |w x|."""
+    scale = np.maximum(want_abs, 1e-300)
+    return bool(np.all(np.abs(got_abs - want_abs) <= 1e-12 * scale)
+                and np.all(np.abs(got_dot - want_dot) <= 1e-12 * scale))
+
+
+@pytest.mark.parametrize("t", [0, 1, 30, 8, 12, 13, 14])
+def test_matvec_stats_is_float64_sum_over_decoded_rows(t):
+    """orc_storage_matvec_stats / orc_storage_dot_stats (the per-output bar of every product test)
+    equal numpy's float64 sum of w*x and of |w*x| over the rows decode_row gives (decode_row is
+    pinned to the compiled reference above), at ragged sizes; wrong normalisers are rejected."""
+    rng = np.random.default_rng(4100 + t)
+    block = {0: 1, 1: 1, 30: 1, 8: 32}.get(t, 256)
+    for rows, cols in ((1, block * 3), (7, 2 * 1024 + block), (33, 4096)):
+        if t in (0, 1, 30):
+            data = _plain_rows(t, rng, rows, cols + 5)
+            cols = cols + 5
+        else:
+            data = synth.weights(t, rng, rows, cols)
+        x = rng.standard_normal(cols).astype(np.float32)
+        x[rng.integers(0, cols, 3)] = 0.0
+        w = oracle.decode_matrix(t, cols, rows, data).astype(np.float64)
+        prod = w * x.astype(np.float64)[None, :]
+        want_dot, want_abs = prod.sum(axis=1), np.abs(prod).sum(axis=1)
+        for threads in (1, 3):
+            dot, ab = oracle.matvec_stats(t, rows, cols, data, x, threads=threads)
+            assert _normaliser_agrees(dot, ab, want_dot, want_abs), (t, rows, cols, threads)
+        rb = data.size // rows
+        for r in (0, rows - 1):
+            d1, a1 = C_stats_dot(t, cols, data[r * rb:(r + 1) * rb], x)
+            assert _normaliser_agrees(np.array([d1]), np.array([a1]), want_dot[r:r + 1], want_abs[r:r + 1])
+        # planted mistakes the check must reject: sum|w| * max|x|, |sum w x|, sum of |w| * |x| over
+        # only the first half of the row
+        wrong = [np.abs(w).sum(axis=1) * np.abs(x).max(), np.abs(want_dot),
+                 np.abs(prod[:, : cols // 2]).sum(axis=1)]
+        for bad in wrong:
+            assert not _normaliser_agrees(want_dot, bad, want_dot, want_abs), t
+
+
+def C_stats_dot(t, n, row, x):
+    import ctypes as C
+    d = np.ascontiguousarray(row, dtype=np.uint8)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    dot, ab = C.c_double(), C.c_double()
+    rc = oracle.lib().orc_storage_dot_stats(t, n, d.ctypes.data, d.nbytes, xv.ctypes.data, C.byref(dot), C.byref(ab))
+    assert rc == 0
+    return dot.value, ab.value
+
+
+def test_matvec_stats_errors_follow_matvec():
+    x = np.ones(256, np.float32)
+    with pytest.raises(oracle.OracleError):
+        oracle.matvec_stats(13, 2, 256, np.zeros(351, np.uint8), x)
+    with pytest.raises(oracle.OracleError):
+        oracle.matvec_stats(13, 0, 256, np.zeros(352, np.uint8), x)
+
+
+def test_fnv1a64_published_vectors():
+    """FNV-1a 64-bit: offset basis 0xcbf29ce484222325, prime 0x100000001b3 (the published
+    test vectors of the FNV reference page)."""
+    assert oracle.fnv1a64(b"") == 0xCBF29CE484222325
+    assert oracle.fnv1a64(b"a") == 0xAF63DC4C8601EC8C
+    assert oracle.fnv1a64(b"foobar") == 0x85944171F73967E8
+    # and against a direct restatement on random bytes
+    blob = np.random.default_rng(7).integers(0, 256, 1000, dtype=np.uint8).tobytes()
+    h = 0xCBF29CE484222325
+    for b in blob:
+        h = ((h ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    assert oracle.fnv1a64(blob) == h
+
+
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
+def test_storage_matmul_is_m_matvecs(t):
+    """orc_storage_matmul_mt with m > 1 is m independent reference matvecs
+    (src/runtime/qwen35_target_multi.cpp:14-25): row i of the output equals, bit for bit, the
+    matvec of activation row i (itself bit-equal to the compiled reference), for any thread count."""
+    rng = np.random.default_rng(4200 + t)
+    rows, cols, m = 11, 1024 if t != 8 else 96, 5
+    data = synth.weights(t, rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    for threads in (1, 4):
+        y = oracle.storage_matmul(t, rows, cols, data, x, threads=threads)
+        assert y.shape == (m, rows)
+        for i in range(m):
+            want = oracle.storage_matvec(t, rows, cols, data, x[i])
+            assert np.array_equal(y[i].view(np.uint32), want.view(np.uint32)), (t, threads, i)
+            if oracle.ref_available() and t != 12:
+                ref = oracle.ref_storage_matvec(t, rows, cols, data, x[i])
+                assert np.array_equal(y[i].view(np.uint32), ref.view(np.uint32))
+    # a transposed activation (columns and rows swapped) gives a different product: the check sees it
+    yt = oracle.storage_matmul(t, rows, cols, data, np.ascontiguousarray(x[::-1]))
+    assert not np.array_equal(yt[0], y[0])
