@@ -8,8 +8,10 @@ on the library's stream, right behind the W warmup steps (timed_steps); steps cy
 weight bytes / step time.
 
 Also reported: the M=512 Q4_K prefill GEMM (4096 x 12288) in TOPS when the matrix-core path is
-available, the roofline of the dominant kernel, and the reference CPU algorithm (the oracle's
-restatement, single thread) timed on a bounded sample on this host.
+available; the Q8_0 4096x4096 GEMV, the Q6_K 151936x4096 output head (with the greedy token) and
+the M=4 Q4_K 4096x12288 product, each with its own roofline; the DeltaNet and attention blocks;
+the roofline of the dominant kernel; and the reference CPU algorithm (the oracle's restatement,
+single thread) timed on a bounded sample on this host.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
 """
@@ -57,7 +59,7 @@ def weight_bytes(t, n, k):
     return synth.row_bytes(t, k) * n
 
 
-def timed_steps(ctx, step, steps, warmup):
+def timed_steps(ctx, step, steps, warmup, first=0):
     """W warmup steps, then exactly K timed steps; returns the K steps' milliseconds.
 
     Steps are launched eagerly through the C ABI (about 3 us of host time per launch, less than
@@ -65,13 +67,17 @@ def timed_steps(ctx, step, steps, warmup):
     steps are launched and, right behind them on the same stream, the HIP event pair around the
     K timed steps: the events measure the K steps back to back.  A host synchronization closes
     the timed region.  (HIP graphs were measured too: a graph's first launch adds ~15-20 us of
-    host set-up that the GPU waits for, 0.7-1 us per step at K = 20.)"""
+    host set-up that the GPU waits for, 0.7-1 us per step at K = 20.)
+
+    Step indices run on from the warmup into the timed steps (first, first + 1, ...), so with
+    steps cycling over >= 512 MiB of copies no timed step reads a copy that the previous 256 MiB
+    of reads touched (the Infinity Cache cannot serve it)."""
     ctx.sync()
     for i in range(warmup):
-        step(i)
+        step(first + i)
     ctx.timer_start()
     for i in range(steps):
-        step(i)
+        step(first + warmup + i)
     ms = ctx.timer_stop()
     ctx.sync()
     return ms
@@ -103,7 +109,7 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
     else:
         ctx.matmul(ws[0], m, xb, yb)
     ctx.sync()
-    ms = timed_steps(ctx, step, steps, warmup)
+    ms = timed_steps(ctx, step, steps, warmup, first=1)
     ms_step = ms / steps
     xbytes = m * k * 4
     ybytes = m * n * 4
@@ -117,6 +123,7 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
         "weight_gbs": wb / (ms_step * 1e-3) / 1e9,
         "algorithmic_bytes": wb + xbytes + ybytes,
         "tops": 2.0 * m * n * k / (ms_step * 1e-3) / 1e12,
+        "steps": steps,
     }
     if name == "q6k_head":
         # greedy token over the head's logits, on the device (oq_argmax), timed on its own
@@ -134,7 +141,7 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
             if ctx.lib.oq_matvec_argmax(ctx.h, whs[i % ncopies], xp, yp, tb.ptr, vb.ptr) != 0:
                 raise RuntimeError("matvec_argmax failed")
 
-        res["head_and_token_us"] = timed_steps(ctx, fused_step, steps, warmup) * 1e3 / steps
+        res["head_and_token_us"] = timed_steps(ctx, fused_step, steps, warmup, first=1 + warmup + steps) * 1e3 / steps
         tb.free()
         vb.free()
     for w in ws:
@@ -167,7 +174,7 @@ def run_deltanet(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
 
     ctx.deltanet_step(blocks[0], hb, sb, xb, yb)  # checked call; sizes the block workspace
     ctx.sync()
-    ms = timed_steps(ctx, step, steps, warmup)
+    ms = timed_steps(ctx, step, steps, warmup, first=1)
     for b in blocks:
         b.release()
     for buf in (hb, sb, xb, yb):
@@ -214,7 +221,7 @@ def run_attention(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, **geom
 
     step(0)  # sizes the partial-sum buffer
     ctx.sync()
-    ms = timed_steps(ctx, step, steps, warmup)
+    ms = timed_steps(ctx, step, steps, warmup, first=1)
     for c in caches:
         c.release()
     for b in (qb, kb, vb, ob):
@@ -256,7 +263,7 @@ def run_attention_block(ctx, steps, warmup, cached=4096, copies_min_bytes=MALL_D
 
     step(0)  # checked call; sizes the block workspace
     ctx.sync()
-    ms = timed_steps(ctx, step, steps, warmup)
+    ms = timed_steps(ctx, step, steps, warmup, first=1)
     for b in blocks:
         b.release()
     for c in caches:
@@ -416,8 +423,12 @@ def main():
         return
     main_res = run_gpu(ctx, args.workload, args.steps, args.warmup)
     secondary = block = attn = attn_block = None
+    configs = {}
     if not args.no_secondary and args.workload == "q4k_gemv":
-        secondary = run_gpu(ctx, "q4k_down_m512", max(5, args.steps // 20), max(2, args.warmup // 5))
+        secondary = run_gpu(ctx, "q4k_down_m512", max(5, args.steps // 4), max(2, args.warmup // 5))
+        # the other single-GPU configurations, each with its own roofline
+        for name in ("q8_0_gemv", "q6k_head", "q4k_down_m4"):
+            configs[name] = run_gpu(ctx, name, max(5, args.steps // 4), max(2, args.warmup // 5))
         block = run_deltanet(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
         attn = run_attention(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
         attn_block = run_attention_block(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
@@ -462,8 +473,21 @@ def main():
     }
     if secondary is not None:
         out["gemm_m512"] = {"tops": round(secondary["tops"], 2), "us": round(secondary["us_per_step"], 2),
+                            "steps": secondary["steps"], "copies": secondary["copies"],
+                            "traffic": committed_traffic("q4k_down_m512"),
                             "frac_fp16_mfma_peak": round(secondary["tops"] / MFMA_PEAK_TFLOPS["fp16"], 4),
                             "frac_int8_mfma_peak": round(secondary["tops"] / MFMA_PEAK_TFLOPS["int8"], 4)}
+    for name, r in configs.items():
+        alg = r["algorithmic_bytes"] / (r["ms_per_step"] * 1e-3) / 1e9
+        entry = {"desc": r["desc"], "us": round(r["us_per_step"], 3), "steps": r["steps"],
+                 "weight_gbs": round(r["weight_gbs"], 1), "copies": r["copies"],
+                 "roofline": {"bound": "hbm", "achieved": round(alg, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(alg / HBM_PEAK_GBS, 4), "traffic": committed_traffic(name),
+                              "algorithmic_bytes": r["algorithmic_bytes"]}}
+        if "head_and_token_us" in r:
+            entry["head_and_token_us"] = round(r["head_and_token_us"], 3)
+            entry["greedy_token_us"] = round(r["greedy_token_us"], 3)
+        out[name] = entry
     if block is not None:
         out["deltanet_block"] = {"us": round(block["us_per_block"], 2), "weight_gbs": round(block["weight_gbs"], 1),
                                  "hbm_frac": round(block["weight_gbs"] / HBM_PEAK_GBS, 4),

@@ -309,7 +309,9 @@ int oq_rope(oq_context* ctx, float* heads_dev, uint64_t n_heads, uint64_t head_d
    and merged with the usual max rescaling: outputs agree with the reference within 1e-4 of
    sum_t p_t |v_t| (the reference sums doubles for the dot products and the denominator).  A
    non-finite score yields non-finite outputs where the reference throws.  Device path limits:
-   key_dim == value_dim in {64, 128, 256}, q_heads / kv_heads <= 8; else OQ_INVALID_ARGUMENT. */
+   key_dim == value_dim in {64, 128, 256}, q_heads / kv_heads <= 8; else OQ_INVALID_ARGUMENT.
+   The cache must belong to ctx, and the step is refused while ctx's stream is being captured
+   (OQ_INVALID_ARGUMENT; both apply to oq_attention_block_step too). */
 int oq_attention_step(oq_context* ctx, const float* q_dev, uint64_t q_heads, const float* k_dev,
                       const float* v_dev, oq_kv_cache* cache, float* out_dev);
 
@@ -367,7 +369,11 @@ int oq_timer_stop(oq_context* ctx, float* elapsed_ms); /* waits for the stop eve
    captured call once eagerly first: a call that would have to grow the context's workspace
    during capture fails with OQ_INVALID_ARGUMENT.  A graph keeps the workspace it captured: when
    a later eager call grows it, the old allocation is kept until the context's last graph is
-   destroyed.  Destroy a context's graphs before the context. */
+   destroyed.  Destroy a context's graphs before the context.  Refused during any capture of the
+   context's stream (this one, or the caller's own hipStreamBeginCapture on oq_context_stream()):
+   weight and model uploads, KV cache create / reset / load, workspace growth, and the attention
+   steps (oq_attention_step, oq_attention_block_step), whose cache length advances on the host
+   when the step is issued -- OQ_INVALID_ARGUMENT. */
 int oq_capture_begin(oq_context* ctx);
 int oq_capture_end(oq_context* ctx, oq_graph** out);
 int oq_graph_launch(oq_context* ctx, oq_graph* g);

@@ -12,6 +12,9 @@
 #include <cstring>
 #include <cmath>
 #include <algorithm>
+#include <atomic>
+#include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -34,36 +37,53 @@ struct KnobTable {
     int value[kKnobCount] = {};
     bool set[kKnobCount] = {};
 };
-KnobTable g_knobs;
-bool g_knobs_loaded = false;
+// The table in force is published through an atomic pointer, so a launch on one thread may read
+// it while another thread creates a context or reloads the options.  Replaced tables are kept
+// (a reader may still hold one) and freed at exit.
+std::atomic<const KnobTable*> g_knobs{nullptr};
+std::mutex g_knob_mutex;
+std::vector<std::unique_ptr<KnobTable>> g_knob_tables;
 
 }  // namespace
 
 void load_knobs() {
-    KnobTable t;
+    auto t = std::make_unique<KnobTable>();
     for (int i = 0; i < kKnobCount; ++i) {
         const char* v = getenv(kKnobNames[i]);
-        t.set[i] = v != nullptr;
-        t.value[i] = v ? atoi(v) : 0;
+        t->set[i] = v != nullptr;
+        t->value[i] = v ? atoi(v) : 0;
     }
-    g_knobs = t;
-    g_knobs_loaded = true;
+    std::lock_guard<std::mutex> lock(g_knob_mutex);
+    g_knobs.store(t.get(), std::memory_order_release);
+    g_knob_tables.push_back(std::move(t));
 }
 
-int knob(Knob k, int fallback) { return g_knobs.set[k] ? g_knobs.value[k] : fallback; }
+void ensure_knobs() {
+    if (g_knobs.load(std::memory_order_acquire) != nullptr) return;
+    {
+        std::lock_guard<std::mutex> lock(g_knob_mutex);
+        if (g_knobs.load(std::memory_order_relaxed) != nullptr) return;
+    }
+    load_knobs();
+}
+
+int knob(Knob k, int fallback) {
+    const KnobTable* t = g_knobs.load(std::memory_order_acquire);
+    return (t && t->set[k]) ? t->value[k] : fallback;
+}
 
 int cu_count() {
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) {
-            cus = v;
-        } else {
-            cus = 256;
+    static std::atomic<int> cus{0};
+    int v = cus.load(std::memory_order_relaxed);
+    if (v == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) {
+            v = 256;
         }
+        cus.store(v, std::memory_order_relaxed);
     }
-    return cus;
+    return v;
 }
 
 }  // namespace oq
@@ -178,12 +198,25 @@ int check_weight(oq_context* ctx, const oq_weight* w) {
 
 void device_free(void* p) { (void)hipFree(p); }
 
+// The context's stream is being captured, by oq_capture_begin or by the caller's own
+// hipStreamBeginCapture on oq_context_stream().
+bool capturing_now(oq_context* ctx) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(ctx->stream, &st);
+    oq::StreamCapture q = oq::StreamCapture::kNone;
+    if (e != hipSuccess) q = oq::StreamCapture::kQueryFailed;
+    else if (st == hipStreamCaptureStatusActive) q = oq::StreamCapture::kActive;
+    else if (st == hipStreamCaptureStatusInvalidated) q = oq::StreamCapture::kInvalidated;
+    return oq::capture_in_progress(ctx->capturing, q);
+}
+
 // Grows a context workspace; allocations that a live graph may still replay are kept until the
 // context's last graph is destroyed (oq_workspace.h).
 int ensure_workspace(oq_context* ctx, oq::Workspace& ws, uint64_t bytes, const char* what) {
+    if (ws.bytes >= bytes) return OQ_OK;
     hipError_t err = hipSuccess;
     const oq::GrowResult r = ws.ensure(
-        bytes, ctx->capturing, (int)ctx->graphs.size(),
+        bytes, capturing_now(ctx), (int)ctx->graphs.size(),
         [&](uint64_t n) -> void* {
             void* p = nullptr;
             err = hipMalloc(&p, n);
@@ -221,7 +254,7 @@ int upload_common(oq_context* ctx, uint32_t type, uint64_t ne0, uint64_t ne1, co
         return fail(ctx, OQ_INVALID_ARGUMENT, "storage decoder does not support GGML type " + std::to_string(type));
     }
     if (!bytes) return fail(ctx, OQ_INVALID_ARGUMENT, "null tensor bytes");
-    if (ctx->capturing) return fail(ctx, OQ_INVALID_ARGUMENT, "weights cannot be uploaded during graph capture");
+    if (capturing_now(ctx)) return fail(ctx, OQ_INVALID_ARGUMENT, "weights cannot be uploaded during graph capture");
 
     const uint64_t pitch = oq::device_pitch(type, ne0);
     if (pitch != 0 && ne1 > UINT64_MAX / pitch) return fail(ctx, OQ_OVERFLOW, "device matrix size overflow");
@@ -547,7 +580,7 @@ int oq_context_create(int device, oq_context** out) {
     }
     e = hipSetDevice(device);
     if (e != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
-    if (!oq::g_knobs_loaded) oq::load_knobs();
+    oq::ensure_knobs();
     oq::noalloc_setup(device);  // its failure is reported by the allocation-free entry point
     oq_context* ctx = new oq_context;
     ctx->device = device;
@@ -898,9 +931,18 @@ int rope_params(oq_context* ctx, uint64_t head_dim, uint64_t rotary_dim, const i
     return OQ_OK;
 }
 
+// A step runs on the cache's own context: its stream orders the step after the cache's reset and
+// load.  The token count lives on the host and advances when the step is issued, so a step cannot
+// be recorded into a graph (a replay would attend over the recorded length and rewrite the same
+// row).
 int check_cache(oq_context* ctx, const oq_kv_cache* c) {
     if (!c) return fail(ctx, OQ_INVALID_ARGUMENT, "null KV cache");
     if (c->device != ctx->device) return fail(ctx, OQ_INVALID_ARGUMENT, "KV cache lives on another device");
+    if (c->ctx != ctx) return fail(ctx, OQ_INVALID_ARGUMENT, "KV cache belongs to another context");
+    if (capturing_now(ctx)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT,
+                    "an attention step cannot be captured into a graph (the KV cache length advances on the host)");
+    }
     return OQ_OK;
 }
 
@@ -979,7 +1021,7 @@ int oq_kv_cache_create(oq_context* ctx, uint64_t capacity, uint64_t kv_heads, ui
         value_dim > lim / (capacity * kv_heads)) {
         return fail(ctx, OQ_OVERFLOW, "KV cache size overflow");
     }
-    if (ctx->capturing) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be created during graph capture");
+    if (capturing_now(ctx)) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be created during graph capture");
     const uint64_t kb = capacity * kv_heads * key_dim * sizeof(float);
     const uint64_t vb = capacity * kv_heads * value_dim * sizeof(float);
     OQ_HIP(ctx, hipSetDevice(ctx->device), "hipSetDevice");
@@ -1019,7 +1061,7 @@ uint64_t oq_kv_cache_capacity(const oq_kv_cache* c) { return c ? c->capacity : 0
 int oq_kv_cache_reset(oq_kv_cache* c) {
     if (!c) return fail(nullptr, OQ_INVALID_ARGUMENT, "null KV cache");
     oq_context* ctx = c->ctx;
-    if (ctx->capturing) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be reset during graph capture");
+    if (capturing_now(ctx)) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be reset during graph capture");
     c->length = 0;
     OQ_HIP(ctx, hipMemsetAsync(c->keys, 0, c->capacity * c->kv_heads * c->key_dim * sizeof(float), ctx->stream),
            "KV cache reset");
@@ -1040,7 +1082,7 @@ int oq_kv_cache_load(oq_kv_cache* c, const float* keys, const float* values, uin
     oq_context* ctx = c->ctx;
     if (length > c->capacity) return fail(ctx, OQ_OVERFLOW, "KV cache capacity exceeded");
     if (length > 0 && (!keys || !values)) return fail(ctx, OQ_INVALID_ARGUMENT, "null cache rows");
-    if (ctx->capturing) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be loaded during graph capture");
+    if (capturing_now(ctx)) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be loaded during graph capture");
     if (length > 0) {
         OQ_HIP(ctx, hipMemcpyAsync(c->keys, keys, length * c->kv_heads * c->key_dim * sizeof(float),
                                    hipMemcpyHostToDevice, ctx->stream), "KV cache load");

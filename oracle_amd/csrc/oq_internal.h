@@ -62,7 +62,8 @@ enum Knob : int {
     kKnobCount
 };
 int knob(Knob k, int fallback);  // the option's value, or fallback when it is unset
-void load_knobs();
+void load_knobs();    // (re)reads every OQ_* option from the environment
+void ensure_knobs();  // load_knobs() once, unless a table is already in force
 int cu_count();                               // compute units of the current device (cached)
 
 // ---- oq_decode.hip

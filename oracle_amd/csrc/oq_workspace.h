@@ -14,6 +14,17 @@ namespace oq {
 
 enum class GrowResult { kOk, kCapturing, kAllocFailed, kSyncFailed };
 
+// What a query of the context's stream (hipStreamIsCapturing) reported.
+enum class StreamCapture { kNone, kActive, kInvalidated, kQueryFailed };
+
+// Whether a call must treat the context's stream as being captured: the library's own capture
+// (oq_capture_begin) or a caller's hipStreamBeginCapture on the same stream.  An invalidated
+// capture is still a capture, and a failed query is treated as one, so that nothing which would
+// record memsets, allocations or host-side state changes into a graph slips through.
+inline bool capture_in_progress(bool library_capture, StreamCapture stream) {
+    return library_capture || stream != StreamCapture::kNone;
+}
+
 struct Workspace {
     void* ptr = nullptr;
     uint64_t bytes = 0;

@@ -26,7 +26,13 @@ COPY_BYTES=28311552
 SECONDARY=""
 [ "$WL" = "q4k_gemv" ] && SECONDARY="--no-secondary"
 
-TRACE_CMD="rocprofv3 --kernel-trace --stats --output-format csv -d $RAW/trace -o run -- python3 bench.py --workload $WL --steps 200 --warmup 20 --no-cpu $SECONDARY"
+# the headline workload is traced in the shape the default run times it (20 steps after 5 warmup
+# steps, every secondary workload after it); the others in 200 steps after 20
+if [ "$WL" = "q4k_gemv" ]; then
+    TRACE_CMD="rocprofv3 --kernel-trace --stats --output-format csv -d $RAW/trace -o run -- python3 bench.py --workload $WL --steps 20 --warmup 5 --no-cpu"
+else
+    TRACE_CMD="rocprofv3 --kernel-trace --stats --output-format csv -d $RAW/trace -o run -- python3 bench.py --workload $WL --steps 200 --warmup 20 --no-cpu $SECONDARY"
+fi
 echo "trace: $TRACE_CMD"
 timeout -k 10 300 $TRACE_CMD > "$RAW.trace.log" 2>&1
 for C in FETCH_SIZE WRITE_SIZE; do

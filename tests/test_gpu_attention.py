@@ -446,3 +446,84 @@ def test_attention_block_errors(ctx):
         wrong.release()
         full.release()
         blk.release()
+
+
+def test_attention_steps_refused_under_capture(ctx):
+    """The KV cache's length advances on the host when a step is issued, so a captured step would
+    replay over a stale length: both attention entry points refuse a capture, and the cache is
+    left as it was."""
+    cache = ctx.kv_cache(4, 1, 64, 64)
+    q, k, v = (ctx.to_device(np.ones((1, 64), np.float32)) for _ in range(3))
+    o = ctx.alloc(64 * 4)
+    heads = ctx.to_device(np.ones((1, 64), np.float32))
+    try:
+        ctx.capture_begin()
+        try:
+            ctx.rope(heads, 1, 64, 64, (32, 0, 0, 0), 10000.0, (1, 1, 1))
+            with pytest.raises(oracle_amd.InvalidArgument, match="cannot be captured"):
+                ctx.attention_step(q, 1, k, v, cache, o)
+        finally:
+            g = ctx.capture_end()
+        g.destroy()
+        assert len(cache) == 0
+        ctx.attention_step(q, 1, k, v, cache, o)
+        ctx.sync()
+        assert len(cache) == 1
+        assert np.array_equal(o.download(np.float32, 64), np.ones(64, np.float32))
+    finally:
+        for b in (q, k, v, o, heads):
+            b.free()
+        cache.release()
+
+
+def test_attention_cache_of_another_context(ctx):
+    """A cache is ordered by its own context's stream (reset, load): another context's step is
+    refused."""
+    other = oracle_amd.Context(0)
+    q, k, v = (ctx.to_device(np.ones((1, 64), np.float32)) for _ in range(3))
+    o = ctx.alloc(64 * 4)
+    try:
+        cache = other.kv_cache(4, 1, 64, 64)
+        try:
+            with pytest.raises(oracle_amd.InvalidArgument, match="belongs to another context"):
+                ctx.attention_step(q, 1, k, v, cache, o)
+            assert len(cache) == 0
+        finally:
+            cache.release()
+    finally:
+        for b in (q, k, v, o):
+            b.free()
+        other.close()
+
+
+def test_caller_stream_capture_is_refused(ctx):
+    """A caller capturing the context's stream with its own hipStreamBeginCapture is seen too:
+    uploads, KV cache creation and attention steps refuse it, as under oq_capture_begin."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    stream = C.c_void_p(ctx.lib.oq_context_stream(ctx.h))
+    cache = ctx.kv_cache(4, 1, 64, 64)
+    q, k, v = (ctx.to_device(np.ones((1, 64), np.float32)) for _ in range(3))
+    o = ctx.alloc(64 * 4)
+    data = synth.q4_k(np.random.default_rng(3), 4, 256)
+    try:
+        assert hip.hipStreamBeginCapture(stream, 2) == 0  # hipStreamCaptureModeRelaxed
+        try:
+            with pytest.raises(oracle_amd.InvalidArgument, match="during graph capture"):
+                ctx.upload(12, 256, 4, data)
+            with pytest.raises(oracle_amd.InvalidArgument, match="during graph capture"):
+                ctx.kv_cache(4, 1, 64, 64)
+            with pytest.raises(oracle_amd.InvalidArgument, match="cannot be captured"):
+                ctx.attention_step(q, 1, k, v, cache, o)
+        finally:
+            graph = C.c_void_p()
+            assert hip.hipStreamEndCapture(stream, C.byref(graph)) == 0
+            if graph.value:
+                hip.hipGraphDestroy(graph)
+        w = ctx.upload(12, 256, 4, data)  # eager again
+        w.release()
+        assert len(cache) == 0
+    finally:
+        for b in (q, k, v, o):
+            b.free()
+        cache.release()

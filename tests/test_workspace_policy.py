@@ -1,6 +1,8 @@
 """The context workspace growth policy (oracle_amd/csrc/oq_workspace.h), host only: an allocation
 that a live captured graph may replay is retired instead of freed, growth during capture is
-refused, and retired allocations are freed with the context's last graph.  Compiled with g++
+refused, and retired allocations are freed with the context's last graph; the capture refusal
+(oq_capture_begin, or a caller's hipStreamBeginCapture on the context's stream) of
+capture_in_progress.  Compiled with g++
 against a counting allocator; no GPU."""
 import shutil
 import subprocess

@@ -65,6 +65,15 @@ int main() {
     EXPECT(ws.ensure(16, false, 0, alloc, release, sync) == oq::GrowResult::kOk);
     ws.release_all(release);
     EXPECT(live.empty() && ws.ptr == nullptr);
+    // capture refusal: the library's own capture, or any capture state the stream query reports
+    // (a caller's hipStreamBeginCapture on the context's stream), or a failed query
+    using SC = oq::StreamCapture;
+    EXPECT(!oq::capture_in_progress(false, SC::kNone));
+    EXPECT(oq::capture_in_progress(true, SC::kNone));
+    EXPECT(oq::capture_in_progress(false, SC::kActive));
+    EXPECT(oq::capture_in_progress(false, SC::kInvalidated));
+    EXPECT(oq::capture_in_progress(false, SC::kQueryFailed));
+    EXPECT(oq::capture_in_progress(true, SC::kActive));
     std::printf("workspace policy ok\n");
     return 0;
 }
