@@ -84,7 +84,8 @@ int oq_synchronize(oq_context* ctx);
 void* oq_context_stream(oq_context* ctx);
 /* Launch-shape options (environment variables OQ_GEMV_*, OQ_GEMM_*, OQ_BLOCK_*, ... selecting
    alternative kernel schedules for measurement) are read once, when the first context is
-   created; this re-reads them.  No reference counterpart.  Not thread-safe with launches. */
+   created; this re-reads them.  No reference counterpart.  The option table is replaced
+   atomically, so launches on other threads read either the old or the new one. */
 void oq_reload_options(void);
 
 /* Device memory helpers (so callers need no other GPU runtime). */
@@ -216,8 +217,16 @@ int oq_matvec_q8k(oq_context* ctx, const oq_weight* w, const void* q8k_dev, floa
    multi-token evaluation is M independent matvecs (src/runtime/qwen35_target_multi.cpp:14-25),
    which is the semantics here.  Small m streams the weights once with register reuse;
    m >= 16 on q4_K, q5_K and q6_K with K >= 4096 uses matrix cores: both operands rounded once
-   to f16 (weights decoded as the reference, Q8_K activations dequantized), F32 accumulation,
-   within the product bar (1e-4 of sum |w * xhat| per output). */
+   to f16 (weights decoded as the reference, Q8_K activations dequantized), F32 accumulation.
+   Each product is then off by at most about 2^-10 of itself, so an output is within 2^-10 of
+   sum |w * xhat| (plus F32 summation) always, and within the product bar (1e-4 of it) when the
+   sum spreads over many products (N(0,1)-like rows: 2.4e-5 to 4.3e-5 measured); a row dominated
+   by a few products can exceed 1e-4.  OQ_GEMM_MFMA=0 (read by oq_reload_options) sends every m
+   to the integer-dot path instead (exact products, F32 scales).  Each activation row is scaled by
+   a power of two into binary16's range before the rounding and scaled back in the output, so any
+   finite activation magnitude is accepted.  Weights must decode inside binary16's range
+   (|(d sc) q - dmin m| <= 65504, i.e. d <= 69 for q4_K / q5_K; GGUF checkpoints store d as f16 and
+   hold values many orders below that); a weight outside it makes that output non-finite. */
 int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x_dev, float* y_dev);
 int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q8k_dev,
                   float* y_dev);

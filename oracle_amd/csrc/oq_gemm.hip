@@ -15,8 +15,8 @@
 //
 // Data flow (one call):
 //   1. activations -> F16 image Xhat[m][K] in scratch.  From F32 x the Q8_K quantization is
-//      the one of quantize_q8k (bit-identical q and d) and Xhat = f16(d*q); caller-supplied
-//      Q8_K blocks are converted the same way.
+//      the one of quantize_q8k (bit-identical q and d) and Xhat = f16(2^e_r * d*q); caller-supplied
+//      Q8_K blocks are converted the same way.  e_r is one power-of-two exponent per row (below).
 //   2. GEMM: a 128 (m) x 256 (n) output tile per workgroup over one K-split of whole
 //      super-blocks, in steps of 64 k.  MFMA wave w owns all 128 rows and 64 columns (4 x 2
 //      accumulators of 32 x 32).
@@ -28,6 +28,7 @@
 // exponent of 1024, minus 1024) and one packed f16 fma applies the f16-rounded scale and min.
 // Below K = 8192 the scale and min are applied in F32 and the result rounded to f16 once.  The
 // conversion instructions are interleaved with the MFMAs, which execute asynchronously.
+#include <algorithm>
 #include <type_traits>
 
 #include "oq_common.h"
@@ -59,50 +60,160 @@ OQ_DEVICE uint32_t pack_f16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2v));
 }
 
-// F32 x [m][K] -> f16(d * q) with the Q8_K quantization of quantize_q8k.  A wave quantizes
-// kQuantBlocksPerWave blocks (one at a time, their loads issued together); a workgroup's four waves
-// take consecutive blocks, so each load instruction of the workgroup reads 4 KiB of consecutive x.
-// Two blocks per wave: 512 x 12288 took 7.4 us against 8.1 / 8.3 / 9.0 with one / four / eight
-// (the quantization arithmetic, 1.5 us of the launch with four, overlaps the loads better).
-constexpr int kQuantBlocksPerWave = 2;
+// Row exponents.  Row r of the image holds f16(2^e_r * d * q), e_r chosen so that the row's
+// largest value, 127 * max |d| over its blocks, lands in [2^14, 2^15): every finite activation then
+// fits binary16's range (|d q| alone can exceed 65504), and a row of small values keeps binary16's
+// full relative precision instead of falling into its subnormals.  Every GEMM epilogue multiplies
+// row r's outputs by 2^-e_r.  Scaling by a power of two commutes with each rounding on the way (the
+// f16 operands, their exact products, the F32 sums) while values stay in the normal range, so a row
+// whose values are normal with and without the scaling gives bit-identical outputs either way.
+// The exponents sit in scratch right after the image (row_exponents), padded to whole m-tiles.
+OQ_DEVICE int row_exponent(float dmax) {
+    const float amax = 127.0f * dmax;
+    if (!(amax > 0.0f) || !__builtin_isfinite(amax)) return 0;  // zero or non-finite rows stay as they are
+    int x = 0;
+    (void)frexpf(amax, &x);  // amax = f * 2^x, f in [0.5, 1)
+    return 15 - x;
+}
 
-__global__ __launch_bounds__(256) void quantize_f16_kernel(const float* __restrict__ x, uint64_t nblocks,
-                                                           _Float16* __restrict__ out) {
-    const int lane = threadIdx.x & 63;
-    const uint64_t first = blockIdx.x * (4ull * kQuantBlocksPerWave) + (threadIdx.x >> 6);
-    float4 v[kQuantBlocksPerWave];
+OQ_DEVICE uint64_t image_bytes(uint64_t m, uint64_t k) { return (m * k * 2 + 255) & ~uint64_t(255); }
+
+OQ_DEVICE const int* row_exponents(const _Float16* a16, uint64_t m, uint64_t k) {
+    return reinterpret_cast<const int*>(reinterpret_cast<const uint8_t*>(a16) + image_bytes(m, k));
+}
+
+// A row's workgroup: 16 waves, block b of the row on wave b % 16.  Blocks per wave whose Q8_K
+// words stay in registers between the two passes: 4 (rows of up to 64 blocks, K <= 16384); the
+// blocks of longer rows are quantized again in the second pass.
+constexpr int kRowWaves = 16;
+constexpr int kRowCache = 4;
+
+OQ_DEVICE float row_max_of_waves(const float* wmax) {
+    float v = wmax[0];
 #pragma unroll
-    for (int u = 0; u < kQuantBlocksPerWave; ++u) {
-        uint64_t blk = first + 4ull * u;
-        blk = blk < nblocks ? blk : nblocks - 1;
-        v[u] = reinterpret_cast<const float4*>(x + blk * kQK)[lane];
+    for (int i = 1; i < kRowWaves; ++i) v = fmaxf(v, wmax[i]);
+    return v;
+}
+
+// F32 x [m][K] -> the image, one workgroup per row.  Pass 1 quantizes every block of the row (the
+// Q8_K quantization of quantize_q8k, bit-identical q and d; all of a wave's loads issued together)
+// and reduces max |d| over the row; pass 2 writes f16(2^e d * q).
+__global__ __launch_bounds__(1024) void quantize_f16_kernel(const float* __restrict__ x, uint32_t nb,
+                                                            _Float16* __restrict__ out, int* __restrict__ rexp) {
+    __shared__ float wmax[kRowWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t row = blockIdx.x;
+    const float* xr = x + row * nb * (uint64_t)kQK;
+    _Float16* orow = out + row * nb * (uint64_t)kQK;
+    float4 v[kRowCache];
+#pragma unroll
+    for (int t = 0; t < kRowCache; ++t) {
+        const uint32_t b = (uint32_t)wave + kRowWaves * t;
+        if (b < nb) v[t] = reinterpret_cast<const float4*>(xr + (uint64_t)b * kQK)[lane];
     }
+    uint32_t qw[kRowCache];
+    float dv[kRowCache];
+    float dmax = 0.0f;
 #pragma unroll
-    for (int u = 0; u < kQuantBlocksPerWave; ++u) {
-        const uint64_t blk = first + 4ull * u;
-        if (blk >= nblocks) break;
-        const Q8KLane r = quantize_q8k_block_wave(v[u], lane);
+    for (int t = 0; t < kRowCache; ++t) {
+        const uint32_t b = (uint32_t)wave + kRowWaves * t;
+        if (b < nb) {
+            const Q8KLane r = quantize_q8k_block_wave(v[t], lane);
+            qw[t] = r.qword;
+            dv[t] = r.d;
+            dmax = fmaxf(dmax, fabsf(r.d));
+        }
+    }
+    for (uint32_t b = (uint32_t)wave + kRowWaves * kRowCache; b < nb; b += kRowWaves) {
+        const Q8KLane r = quantize_q8k_block_wave(reinterpret_cast<const float4*>(xr + (uint64_t)b * kQK)[lane], lane);
+        dmax = fmaxf(dmax, fabsf(r.d));
+    }
+    if (lane == 0) wmax[wave] = dmax;  // d is uniform across the wave
+    __syncthreads();
+    const int e = row_exponent(row_max_of_waves(wmax));
+    if (threadIdx.x == 0) rexp[row] = e;
+    auto put = [&](uint32_t b, uint32_t q, float d) {
+        const float ds = ldexpf(d, e);
         float f[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] = r.d * (float)(int8_t)(r.qword >> (8 * i));
-        *reinterpret_cast<uint2*>(out + blk * kQK + 4 * lane) =
-            make_uint2(pack_f16(f[0], f[1]), pack_f16(f[2], f[3]));
+        for (int i = 0; i < 4; ++i) f[i] = ds * (float)(int8_t)(q >> (8 * i));
+        *reinterpret_cast<uint2*>(orow + (uint64_t)b * kQK + 4 * lane) = make_uint2(pack_f16(f[0], f[1]), pack_f16(f[2], f[3]));
+    };
+#pragma unroll
+    for (int t = 0; t < kRowCache; ++t) {
+        const uint32_t b = (uint32_t)wave + kRowWaves * t;
+        if (b < nb) put(b, qw[t], dv[t]);
+    }
+    for (uint32_t b = (uint32_t)wave + kRowWaves * kRowCache; b < nb; b += kRowWaves) {
+        const Q8KLane r = quantize_q8k_block_wave(reinterpret_cast<const float4*>(xr + (uint64_t)b * kQK)[lane], lane);
+        put(b, r.qword, r.d);
     }
 }
 
-// Q8_K blocks -> f16(d * q)
-__global__ __launch_bounds__(256) void q8k_to_f16_kernel(const uint8_t* __restrict__ q8k, uint64_t nblocks,
-                                                         _Float16* __restrict__ out) {
-    const int lane = threadIdx.x & 63;
-    const uint64_t blk = blockIdx.x * 4ull + (threadIdx.x >> 6);
-    if (blk >= nblocks) return;
-    const uint8_t* b = q8k + blk * kQ8KBytes;
-    const float d = *reinterpret_cast<const float*>(b);
-    const uint32_t q = *reinterpret_cast<const uint32_t*>(b + 4 + 4 * lane);
-    float f[4];
+// Q8_K blocks [m][nb] -> the image, one workgroup per row: max |d| over the row's blocks, then
+// f16(2^e d * q) as quantize_f16_kernel.
+__global__ __launch_bounds__(1024) void q8k_to_f16_kernel(const uint8_t* __restrict__ q8k, uint32_t nb,
+                                                          _Float16* __restrict__ out, int* __restrict__ rexp) {
+    __shared__ float wmax[kRowWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t row = blockIdx.x;
+    const uint8_t* qr = q8k + row * nb * (uint64_t)kQ8KBytes;
+    _Float16* orow = out + row * nb * (uint64_t)kQK;
+    float dmax = 0.0f;
+    for (uint32_t b = threadIdx.x; b < nb; b += 64 * kRowWaves)
+        dmax = fmaxf(dmax, fabsf(*reinterpret_cast<const float*>(qr + (uint64_t)b * kQ8KBytes)));
+    dmax = __int_as_float((int)wave_max_u32((uint32_t)__float_as_int(dmax)));  // non-negative: integer order
+    if (lane == 0) wmax[wave] = dmax;
+    __syncthreads();
+    const int e = row_exponent(row_max_of_waves(wmax));
+    if (threadIdx.x == 0) rexp[row] = e;
+    for (uint32_t b = (uint32_t)wave; b < nb; b += kRowWaves) {
+        const uint8_t* blk = qr + (uint64_t)b * kQ8KBytes;
+        const float ds = ldexpf(*reinterpret_cast<const float*>(blk), e);
+        const uint32_t q = *reinterpret_cast<const uint32_t*>(blk + 4 + 4 * lane);
+        float f[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = d * (float)(int8_t)(q >> (8 * i));
-    *reinterpret_cast<uint2*>(out + blk * kQK + 4 * lane) = make_uint2(pack_f16(f[0], f[1]), pack_f16(f[2], f[3]));
+        for (int i = 0; i < 4; ++i) f[i] = ds * (float)(int8_t)(q >> (8 * i));
+        *reinterpret_cast<uint2*>(orow + (uint64_t)b * kQK + 4 * lane) = make_uint2(pack_f16(f[0], f[1]), pack_f16(f[2], f[3]));
+    }
+}
+
+// One wave's 128 x 64 output tile (accumulators acc[i][j]: m-subtile i, n-subtile j, 32 x 32 each;
+// result register r of lane l: row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32), stored to o
+// (m x n, row-major).  col0: the wave's first column.  With rexp (the last writer of the outputs:
+// a single K-split) each row is scaled back by 2^-e_row; a split's partial tile is stored as it
+// is and the split reduction scales the sums back.
+OQ_DEVICE void store_wave_tile(float* __restrict__ o, const int* __restrict__ rexp, uint64_t m0, uint64_t m,
+                               uint64_t n, uint64_t col0, int h, int r0, const float16v (&acc)[4][2]) {
+    int e[4][16] = {};
+    if (rexp != nullptr) {
+        // rows 8 g + 4 h + 0..3 of m-subtile i: four consecutive exponents per load, all 16 loads
+        // issued before the first use (the array is padded to whole m-tiles: reads stay inside it)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int4 ev = *reinterpret_cast<const int4*>(rexp + m0 + 32 * i + 8 * g + 4 * h);
+                e[i][4 * g] = ev.x;
+                e[i][4 * g + 1] = ev.y;
+                e[i][4 * g + 2] = ev.z;
+                e[i][4 * g + 3] = ev.w;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint64_t col = col0 + 32 * j + r0;
+        if (col >= n) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int rr = 0; rr < 16; ++rr) {
+                const uint64_t row = m0 + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
+                if (row < m) o[row * n + col] = rexp != nullptr ? ldexpf(acc[i][j][rr], -e[i][rr]) : acc[i][j][rr];
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------- tiles and addressing
@@ -547,21 +658,8 @@ __global__ __launch_bounds__(kThreads) void gemm_q4k_f16_kernel(DeviceMatrix w, 
         hdr[0] = hdrn[0];
         hdr[1] = hdrn[1];
     }
-    // result register r of lane l: row 8*(r/4) + 4*(l/32) + r%4, column l%32
-    float* o = out + (uint64_t)z * (uint64_t)m * w.n;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint64_t col = n0 + 64 * wave + 32 * j + r0;
-        if (col >= w.n) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int rr = 0; rr < 16; ++rr) {
-                const uint64_t row = m0 + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
-                if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][rr];
-            }
-        }
-    }
+    store_wave_tile(out + (uint64_t)z * (uint64_t)m * w.n, splits > 1 ? nullptr : row_exponents(a16, (uint64_t)m, w.k),
+                    m0, (uint64_t)m, w.n, n0 + 64 * wave, h, r0, acc);
 }
 
 // ---------------------------------------------------------------- producer / consumer variant
@@ -896,20 +994,8 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(DeviceMatrix w, int
         qh[0] = qhn[0];
         qh[1] = qhn[1];
     }
-    float* o = out + (uint64_t)z * (uint64_t)m * w.n;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint64_t col = n0 + 64 * wave + 32 * j + r0;
-        if (col >= w.n) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int rr = 0; rr < 16; ++rr) {
-                const uint64_t row = m0 + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
-                if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][rr];
-            }
-        }
-    }
+    store_wave_tile(out + (uint64_t)z * (uint64_t)m * w.n, splits > 1 ? nullptr : row_exponents(a16, (uint64_t)m, w.k),
+                    m0, (uint64_t)m, w.n, n0 + 64 * wave, h, r0, acc);
 }
 
 // ---------------------------------------------------------------- q6_K with weights in registers
@@ -1225,20 +1311,8 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws6_kernel(DeviceMatrix w, in
         cur[0] = nxt[0];
         cur[1] = nxt[1];
     }
-    float* o = out + (uint64_t)z * (uint64_t)m * w.n;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint64_t col = n0 + 64 * wave + 32 * j + r0;
-        if (col >= w.n) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int rr = 0; rr < 16; ++rr) {
-                const uint64_t row = m0 + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
-                if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][rr];
-            }
-        }
-    }
+    store_wave_tile(out + (uint64_t)z * (uint64_t)m * w.n, splits > 1 ? nullptr : row_exponents(a16, (uint64_t)m, w.k),
+                    m0, (uint64_t)m, w.n, n0 + 64 * wave, h, r0, acc);
 }
 
 // ---------------------------------------------------------------- B tiles converted by the load waves
@@ -1527,27 +1601,18 @@ __global__ __launch_bounds__(kKqThreads) void gemm_kq_kernel(DeviceMatrix w, int
         __builtin_amdgcn_s_barrier();
         buf = nbuf;
     }
-    float* o = out + (uint64_t)z * (uint64_t)m * w.n;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint64_t col = n0 + 64 * wave + 32 * j + r0;
-        if (col >= w.n) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int rr = 0; rr < 16; ++rr) {
-                const uint64_t row = m0 + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
-                if (row < (uint64_t)m) o[row * w.n + col] = acc[i][j][rr];
-            }
-        }
-    }
+    store_wave_tile(out + (uint64_t)z * (uint64_t)m * w.n, splits > 1 ? nullptr : row_exponents(a16, (uint64_t)m, w.k),
+                    m0, (uint64_t)m, w.n, n0 + 64 * wave, h, r0, acc);
 }
 
-// y[i] = sum over splits s (in order) of partial[s][i]; count4 = outputs / 4
+// y[i] = 2^-e_row * (sum over splits s, in order, of partial[s][i]); count4 = outputs / 4, n = row
+// length (a multiple of 4, so the four outputs of an index share their row)
 __global__ __launch_bounds__(256) void reduce_splits_kernel(const float4* __restrict__ part, uint64_t count4,
-                                                            uint32_t splits, float4* __restrict__ y) {
+                                                            uint32_t splits, uint64_t n, const int* __restrict__ rexp,
+                                                            float4* __restrict__ y) {
     const uint64_t stride = (uint64_t)gridDim.x * 256;
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < count4; i += stride) {
+        const int e = -rexp[4 * i / n];
         float4 s = part[i];
         for (uint32_t z = 1; z < splits; ++z) {
             const float4 p = part[(uint64_t)z * count4 + i];
@@ -1556,24 +1621,27 @@ __global__ __launch_bounds__(256) void reduce_splits_kernel(const float4* __rest
             s.z += p.z;
             s.w += p.w;
         }
-        y[i] = s;
+        y[i] = make_float4(ldexpf(s.x, e), ldexpf(s.y, e), ldexpf(s.z, e), ldexpf(s.w, e));
     }
 }
 
-// the same for outputs whose count is not a multiple of 4
+// the same for rows whose length is not a multiple of 4
 __global__ __launch_bounds__(256) void reduce_splits_scalar_kernel(const float* __restrict__ part, uint64_t count,
-                                                                   uint32_t splits, float* __restrict__ y) {
+                                                                   uint32_t splits, uint64_t n,
+                                                                   const int* __restrict__ rexp, float* __restrict__ y) {
     const uint64_t stride = (uint64_t)gridDim.x * 256;
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < count; i += stride) {
         float s = part[i];
         for (uint32_t z = 1; z < splits; ++z) s += part[(uint64_t)z * count + i];
-        y[i] = s;
+        y[i] = ldexpf(s, -rexp[i / n]);
     }
 }
 
+// Scratch of one call: the F16 image [m][K] (image_bytes), the row exponents [tiles_m * kBM] (int),
+// then the split partials [splits][m][n] (F32) when splits > 1.
 struct Plan {
     uint32_t tiles_n, tiles_m, splits;
-    uint64_t a16_bytes, part_bytes;
+    uint64_t a16_bytes, rexp_bytes, part_bytes;
 };
 
 uint64_t round256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
@@ -1592,6 +1660,7 @@ Plan make_plan(const DeviceMatrix& w, int m) {
     if (s > nsb) s = nsb;
     p.splits = (uint32_t)s;
     p.a16_bytes = round256((uint64_t)m * w.k * 2);
+    p.rexp_bytes = round256((uint64_t)p.tiles_m * kBM * 4);
     p.part_bytes = p.splits > 1 ? (uint64_t)p.splits * m * w.n * 4 : 0;
     return p;
 }
@@ -1604,7 +1673,7 @@ bool gemm_mfma_supported(const DeviceMatrix& w, int m) {
 
 uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m) {
     const Plan p = make_plan(w, m);
-    return p.a16_bytes + p.part_bytes;
+    return p.a16_bytes + p.rexp_bytes + p.part_bytes;
 }
 
 template <uint32_t TYPE, bool FAST>
@@ -1649,14 +1718,13 @@ hipError_t launch_gemm_mfma(const DeviceMatrix& w, int m, const float* x, const 
     const Plan p = make_plan(w, m);
     uint8_t* base = static_cast<uint8_t*>(scratch);
     _Float16* a16 = reinterpret_cast<_Float16*>(base);
-    float* part = reinterpret_cast<float*>(base + p.a16_bytes);
-    const uint64_t nblocks = (uint64_t)m * (w.k / kQK);
-    const unsigned qgrid = (unsigned)((nblocks + 3) / 4);
+    int* rexp = reinterpret_cast<int*>(base + p.a16_bytes);  // = row_exponents(a16, m, K)
+    float* part = reinterpret_cast<float*>(base + p.a16_bytes + p.rexp_bytes);
+    const uint32_t nb = (uint32_t)(w.k / kQK);
     if (x) {
-        const unsigned xgrid = (unsigned)((nblocks + 4 * kQuantBlocksPerWave - 1) / (4 * kQuantBlocksPerWave));
-        hipLaunchKernelGGL(quantize_f16_kernel, dim3(xgrid), dim3(256), 0, s, x, nblocks, a16);
+        hipLaunchKernelGGL(quantize_f16_kernel, dim3((unsigned)m), dim3(64 * kRowWaves), 0, s, x, nb, a16, rexp);
     } else {
-        hipLaunchKernelGGL(q8k_to_f16_kernel, dim3(qgrid), dim3(256), 0, s, q8k, nblocks, a16);
+        hipLaunchKernelGGL(q8k_to_f16_kernel, dim3((unsigned)m), dim3(64 * kRowWaves), 0, s, q8k, nb, a16, rexp);
     }
     const unsigned wgs = p.tiles_n * p.tiles_m * p.splits;
     const bool fast = w.k >= kFastMinK && knob(kGemmExactDequant, 0) == 0;
@@ -1682,17 +1750,17 @@ hipError_t launch_gemm_mfma(const DeviceMatrix& w, int m, const float* x, const 
     }
     if (p.splits > 1) {
         const uint64_t count = (uint64_t)m * w.n;
-        if (count % 4 == 0) {
+        if (w.n % 4 == 0) {
             uint64_t blocks = (count / 4 + 255) / 256;
             if (blocks > 8192) blocks = 8192;
             hipLaunchKernelGGL(reduce_splits_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
-                               reinterpret_cast<const float4*>(part), count / 4, p.splits,
+                               reinterpret_cast<const float4*>(part), count / 4, p.splits, w.n, rexp,
                                reinterpret_cast<float4*>(y));
         } else {
             uint64_t blocks = (count + 255) / 256;
             if (blocks > 8192) blocks = 8192;
             hipLaunchKernelGGL(reduce_splits_scalar_kernel, dim3((unsigned)blocks), dim3(256), 0, s, part, count,
-                               p.splits, y);
+                               p.splits, w.n, rexp, y);
         }
     }
     return hipGetLastError();

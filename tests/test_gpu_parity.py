@@ -269,6 +269,49 @@ def test_matrix_cores_q8k_input_and_split_counts(ctx, t, splits):
     w.release()
 
 
+@pytest.mark.parametrize("t", [12, 13, 14])
+@pytest.mark.parametrize("env", [{}, {"OQ_GEMM_WS": "2"}])
+def test_matrix_cores_extreme_activation_scales(ctx, t, env):
+    """The matrix-core path's f16 activation image carries one power-of-two exponent per row, so
+    rows far outside binary16's range (1e5 and 3e6 scales: |d q| > 65504) and far below it (1e-6,
+    1e-30: subnormal or zero in binary16) stay finite, from F32 and from Q8_K inputs, in every
+    kernel.  Rows whose sum spreads over many products meet the 1e-4 bar.  A row dominated by a
+    few products (one element at 3e6, one block at 1e5 times the rest) is held to the path's
+    rigorous bound instead: each operand rounded once to binary16 (relative 2^-11), so each
+    product is off by at most about 2^-10 of itself, plus F32 summation: 2e-3 of sum |w xhat|
+    (a missing or doubled row exponent would be off by a power of two)."""
+    rng = np.random.default_rng(5150 + t)
+    m, rows, cols = 24, 300, 4096
+    data = synth.weights(t, rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    x[0] *= 1e5
+    x[1] *= 1e-6
+    x[2] *= 1e-30
+    x[3, 17] = 3e6           # one huge element; the rest of the row quantizes to small integers
+    x[4] = 0.0               # an all-zero row
+    x[5, :256] *= 1e5        # one block far above the others
+    w = ctx.upload(t, cols, rows, data)
+    with oracle_amd.launch_options(env):
+        y = gpu_matmul(ctx, w, x, rows)
+        xb = ctx.to_device(x)
+        qb = ctx.alloc(m * (cols // 256) * 292)
+        yb = ctx.alloc(m * rows * 4)
+        ctx.quantize_q8k(xb, m, cols, qb)
+        ctx.matmul_q8k(w, m, qb, yb)
+        y_q8k = yb.download(np.float32, m * rows).reshape(m, rows)
+        for b in (xb, qb, yb):
+            b.free()
+    assert np.all(np.isfinite(y))
+    assert np.array_equal(y.view(np.uint32), y_q8k.view(np.uint32))
+    assert np.all(y[4] == 0.0)
+    y_ref, norm = reference_products(t, rows, cols, data, x)
+    for r in range(m):
+        if r == 4:
+            continue
+        check_close(y[r:r + 1], y_ref[r:r + 1], norm[r:r + 1], tol=2e-3 if r in (3, 5) else TOL)
+    w.release()
+
+
 @pytest.mark.parametrize("cols", [4096, 8192])
 def test_matrix_core_kernels_agree(ctx, cols):
     """The producer/consumer GEMM kernel (default) and the four-wave kernel (OQ_GEMM_WS=0)
