@@ -51,6 +51,7 @@ WORKLOADS = {
     "q5k_down_m512": (13, 4096, 12288, 512, "Q5_K down-projection GEMM 4096x12288, M=512, Q8_K activations"),
     "q6k_down_m512": (14, 4096, 12288, 512, "Q6_K down-projection GEMM 4096x12288, M=512, Q8_K activations"),
     "q5k_gemv": (13, 12288, 4096, 1, "Q5_K FFN gate/up decode GEMV 12288x4096, batch 1, Q8_K activations"),
+    "q8_0_eh_m512": (8, 4096, 8192, 512, "Q8_0 MTP hidden projection GEMM 4096x8192 (nextn.eh_proj), M=512, F32 activations"),
 }
 SEED = 20261201
 

@@ -759,6 +759,11 @@ int oq_matmul(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, f
         }
         return launch_rc(ctx, oq::launch_gemv_kquant(w->m, (int)m, x, nullptr, y, ctx->stream), "matmul");
     }
+    if (t == OQ_TYPE_Q8_0 && oq::gemm_mfma_supported(w->m, (int)m) && knob_flag(oq::kGemmMfma, true)) {
+        if (int rc = ensure_scratch(ctx, oq::gemm_scratch_bytes(w->m, (int)m))) return rc;
+        return launch_rc(ctx, oq::launch_gemm_mfma(w->m, (int)m, x, nullptr, y, ctx->scratch.ptr, ctx->stream),
+                         "matmul");
+    }
     return launch_rc(ctx, oq::launch_gemv_f32act(w->m, (int)m, x, y, ctx->stream), "matmul");
 }
 

@@ -68,8 +68,7 @@ OQ_DEVICE uint32_t pack_f16(float a, float b) {
 // f16 operands, their exact products, the F32 sums) while values stay in the normal range, so a row
 // whose values are normal with and without the scaling gives bit-identical outputs either way.
 // The exponents sit in scratch right after the image (row_exponents), padded to whole m-tiles.
-OQ_DEVICE int row_exponent(float dmax) {
-    const float amax = 127.0f * dmax;
+OQ_DEVICE int row_exponent(float amax) {
     if (!(amax > 0.0f) || !__builtin_isfinite(amax)) return 0;  // zero or non-finite rows stay as they are
     int x = 0;
     (void)frexpf(amax, &x);  // amax = f * 2^x, f in [0.5, 1)
@@ -130,7 +129,7 @@ __global__ __launch_bounds__(1024) void quantize_f16_kernel(const float* __restr
     }
     if (lane == 0) wmax[wave] = dmax;  // d is uniform across the wave
     __syncthreads();
-    const int e = row_exponent(row_max_of_waves(wmax));
+    const int e = row_exponent(127.0f * row_max_of_waves(wmax));
     if (threadIdx.x == 0) rexp[row] = e;
     auto put = [&](uint32_t b, uint32_t q, float d) {
         const float ds = ldexpf(d, e);
@@ -165,7 +164,7 @@ __global__ __launch_bounds__(1024) void q8k_to_f16_kernel(const uint8_t* __restr
     dmax = __int_as_float((int)wave_max_u32((uint32_t)__float_as_int(dmax)));  // non-negative: integer order
     if (lane == 0) wmax[wave] = dmax;
     __syncthreads();
-    const int e = row_exponent(row_max_of_waves(wmax));
+    const int e = row_exponent(127.0f * row_max_of_waves(wmax));
     if (threadIdx.x == 0) rexp[row] = e;
     for (uint32_t b = (uint32_t)wave; b < nb; b += kRowWaves) {
         const uint8_t* blk = qr + (uint64_t)b * kQ8KBytes;
@@ -176,6 +175,49 @@ __global__ __launch_bounds__(1024) void q8k_to_f16_kernel(const uint8_t* __restr
         for (int i = 0; i < 4; ++i) f[i] = ds * (float)(int8_t)(q >> (8 * i));
         *reinterpret_cast<uint2*>(orow + (uint64_t)b * kQK + 4 * lane) = make_uint2(pack_f16(f[0], f[1]), pack_f16(f[2], f[3]));
     }
+}
+
+// F32 x [m][K] -> f16(2^e x), one workgroup per row (K a multiple of 256): the image of q8_0
+// weights, whose products take the activations as they are (the reference multiplies q8_0 rows by
+// the F32 activation, src/backend/cpu/quantized_reference.cpp:50-64).  Pass 1 reduces max |x|
+// over the row, pass 2 writes; e as for the Q8_K images.
+__global__ __launch_bounds__(1024) void scale_f16_kernel(const float* __restrict__ x, uint32_t nb,
+                                                         _Float16* __restrict__ out, int* __restrict__ rexp) {
+    __shared__ float wmax[kRowWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t row = blockIdx.x;
+    const float* xr = x + row * nb * (uint64_t)kQK;
+    _Float16* orow = out + row * nb * (uint64_t)kQK;
+    float4 v[kRowCache];
+    float amax = 0.0f;
+#pragma unroll
+    for (int t = 0; t < kRowCache; ++t) {
+        const uint32_t b = (uint32_t)wave + kRowWaves * t;
+        if (b < nb) {
+            v[t] = reinterpret_cast<const float4*>(xr + (uint64_t)b * kQK)[lane];
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[t].x), fabsf(v[t].y)), fmaxf(fabsf(v[t].z), fabsf(v[t].w))));
+        }
+    }
+    for (uint32_t b = (uint32_t)wave + kRowWaves * kRowCache; b < nb; b += kRowWaves) {
+        const float4 u = reinterpret_cast<const float4*>(xr + (uint64_t)b * kQK)[lane];
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+    }
+    amax = __int_as_float((int)wave_max_u32((uint32_t)__float_as_int(amax)));  // non-negative: integer order
+    if (lane == 0) wmax[wave] = amax;
+    __syncthreads();
+    const int e = row_exponent(row_max_of_waves(wmax));
+    if (threadIdx.x == 0) rexp[row] = e;
+    auto put = [&](uint32_t b, float4 u) {
+        *reinterpret_cast<uint2*>(orow + (uint64_t)b * kQK + 4 * lane) =
+            make_uint2(pack_f16(ldexpf(u.x, e), ldexpf(u.y, e)), pack_f16(ldexpf(u.z, e), ldexpf(u.w, e)));
+    };
+#pragma unroll
+    for (int t = 0; t < kRowCache; ++t) {
+        const uint32_t b = (uint32_t)wave + kRowWaves * t;
+        if (b < nb) put(b, v[t]);
+    }
+    for (uint32_t b = (uint32_t)wave + kRowWaves * kRowCache; b < nb; b += kRowWaves)
+        put(b, reinterpret_cast<const float4*>(xr + (uint64_t)b * kQK)[lane]);
 }
 
 // One wave's 128 x 64 output tile (accumulators acc[i][j]: m-subtile i, n-subtile j, 32 x 32 each;
@@ -371,6 +413,18 @@ OQ_DEVICE uint32_t q6_pair(uint32_t u, float ds) {
         const float a = (float)((int)((u >> (16 * P)) & 0xFFu) - 32), b = (float)((int)((u >> (16 * P + 8)) & 0xFFu) - 32);
         return pack_f16(ds * a, ds * b);
     }
+}
+
+// Two weights of a q8_0 block from bytes (2P, 2P+1) of a word of int8 quants: the bytes offset to
+// unsigned (q + 128) become the exact f16 integers 1024 + q + 128, minus 1152 gives q, and one
+// v_pk_mul_f16 by the block's f16 d rounds d * q (exact in F32) once: f16(d * q).
+template <int P>
+OQ_DEVICE uint32_t q8_pair(uint32_t v, uint32_t dbits) {
+    const half2v k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const half2v x = f16_1024_pair<P>(v ^ 0x80808080u) - k1152;
+    const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)dbits);
+    const half2v dv = {dh, dh};
+    return __builtin_bit_cast(uint32_t, x * dv);
 }
 
 // q4_K (TYPE 12) or q5_K (13) weight pair from a word of quant bytes (nibbles, or 5-bit values)
@@ -1350,6 +1404,11 @@ constexpr uint32_t kKqLds = 3 * kTileBytes + 3 * kKqBTile;
 template <uint32_t TYPE>
 struct KqRaw;
 template <>
+struct KqRaw<8> {
+    uint4 q0[2], q1[2];  // bytes 16 hb .. 16 hb + 15 of the step's two blocks
+    uint32_t d[2];       // their f16 scales
+};
+template <>
 struct KqRaw<12> {
     uint4 q[2], hdr[2];
 };
@@ -1376,7 +1435,13 @@ OQ_DEVICE void kq_load(KqRaw<TYPE>& r, const uint8_t* wb, const uint32_t (&row_o
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
         const uint8_t* row = wb + row_off[pp];
-        if constexpr (TYPE == 14) {
+        if constexpr (TYPE == 8) {
+            // step G of super-block sb: q8_0 blocks 8 sb + 2 G and 8 sb + 2 G + 1 (qs[nb][32] | d[nb])
+            const uint32_t blk = 8u * sb + 2u * (uint32_t)G;
+            r.q0[pp] = *reinterpret_cast<const uint4*>(row + 32u * blk + 16u * hb);
+            r.q1[pp] = *reinterpret_cast<const uint4*>(row + 32u * blk + 32u + 16u * hb);
+            r.d[pp] = *reinterpret_cast<const uint32_t*>(row + 256u * nsb + 2u * blk);
+        } else if constexpr (TYPE == 14) {
             const uint32_t g = 2u * (G / 2) + hb;
             r.q0[pp] = *reinterpret_cast<const uint4*>(row + kq_chunk_off(nsb, sb, g, 0));
             r.q1[pp] = *reinterpret_cast<const uint4*>(row + kq_chunk_off(nsb, sb, g, 1));
@@ -1398,7 +1463,20 @@ OQ_DEVICE void kq_convert(const KqRaw<TYPE>& r, uint8_t* bdst, const uint32_t (&
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
         uint32_t out[4][4];
-        if constexpr (TYPE == 14) {
+        if constexpr (TYPE == 8) {
+            // slice ks takes block ks & 1, bytes 8 (ks >> 1) .. + 7 of the lane's half
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const uint4 src = (ks & 1) ? r.q1[pp] : r.q0[pp];
+                const uint32_t dh = (ks & 1) ? r.d[pp] >> 16 : r.d[pp] & 0xFFFFu;
+#pragma unroll
+                for (int wd = 0; wd < 2; ++wd) {
+                    const uint32_t v = dword_of(src, 2 * (ks >> 1) + wd);
+                    out[ks][2 * wd] = q8_pair<0>(v, dh);
+                    out[ks][2 * wd + 1] = q8_pair<1>(v, dh);
+                }
+            }
+        } else if constexpr (TYPE == 14) {
             const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.d[pp] & 0xFFFFu));
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
@@ -1668,7 +1746,7 @@ Plan make_plan(const DeviceMatrix& w, int m) {
 }  // namespace
 
 bool gemm_mfma_supported(const DeviceMatrix& w, int m) {
-    return (w.type == 12 || w.type == 13 || w.type == 14) && m >= 16 && w.k >= kMinK && w.k % kQK == 0;
+    return (w.type == 8 || w.type == 12 || w.type == 13 || w.type == 14) && m >= 16 && w.k >= kMinK && w.k % kQK == 0;
 }
 
 uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m) {
@@ -1721,14 +1799,21 @@ hipError_t launch_gemm_mfma(const DeviceMatrix& w, int m, const float* x, const 
     int* rexp = reinterpret_cast<int*>(base + p.a16_bytes);  // = row_exponents(a16, m, K)
     float* part = reinterpret_cast<float*>(base + p.a16_bytes + p.rexp_bytes);
     const uint32_t nb = (uint32_t)(w.k / kQK);
-    if (x) {
+    if (w.type == 8) {
+        // q8_0: the F32 activations themselves (no Q8_K), weights converted by the load waves
+        if (!x) return hipErrorNotSupported;
+        hipLaunchKernelGGL(scale_f16_kernel, dim3((unsigned)m), dim3(64 * kRowWaves), 0, s, x, nb, a16, rexp);
+        launch_kq<8, true>(w, m, a16, p, p.splits > 1 ? part : y, s);
+    } else if (x) {
         hipLaunchKernelGGL(quantize_f16_kernel, dim3((unsigned)m), dim3(64 * kRowWaves), 0, s, x, nb, a16, rexp);
     } else {
         hipLaunchKernelGGL(q8k_to_f16_kernel, dim3((unsigned)m), dim3(64 * kRowWaves), 0, s, q8k, nb, a16, rexp);
     }
     const unsigned wgs = p.tiles_n * p.tiles_m * p.splits;
     const bool fast = w.k >= kFastMinK && knob(kGemmExactDequant, 0) == 0;
-    if (knob(kGemmWs, 1) == 2) {
+    if (w.type == 8) {
+        // launched above
+    } else if (knob(kGemmWs, 1) == 2) {
         // the weights converted by the load waves (every type with OQ_GEMM_WS=2)
         float* dst = p.splits > 1 ? part : y;
         if (w.type == 12) fast ? launch_kq<12, true>(w, m, a16, p, dst, s) : launch_kq<12, false>(w, m, a16, p, dst, s);

@@ -312,6 +312,69 @@ def test_matrix_cores_extreme_activation_scales(ctx, t, env):
     w.release()
 
 
+@pytest.mark.parametrize("m,rows,cols,splits", [(70, 520, 8192, None), (16, 33, 4096, None), (130, 300, 4096, "3"),
+                                                (40, 257, 12288, "1"), (33, 64, 8192, "8")])
+def test_q8_0_matrix_cores(ctx, m, rows, cols, splits):
+    """q8_0 weights at m >= 16 run on matrix cores: the F32 activations rounded once to f16 (with
+    the row exponent), weights f16(d q), F32 accumulation; within the product bar of the
+    reference's F32 dot (src/backend/cpu/quantized_reference.cpp:50-64), tails in m and n, every
+    split count, and against the integer-free GEMV path (OQ_GEMM_MFMA=0) within the same bar."""
+    rng = np.random.default_rng(8800 + m + rows + cols)
+    data = synth.q8_0(rng, rows, cols)
+    blocks = data.reshape(-1, 34)
+    blocks[rng.integers(0, blocks.shape[0], 50), 2 + rng.integers(0, 32, 50)] = 0x80  # q = -128 too
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(8, cols, rows, data)
+    with oracle_amd.launch_options({} if splits is None else {"OQ_GEMM_SPLITS": splits}):
+        y = gpu_matmul(ctx, w, x, rows)
+    with oracle_amd.launch_options({"OQ_GEMM_MFMA": "0"}):
+        y_gemv = gpu_matmul(ctx, w, x, rows)
+    y_ref, norm = reference_products(8, rows, cols, data, x)
+    worst = check_close(y, y_ref, norm)
+    assert worst < 0.5 * TOL, f"MFMA path margin too thin: {worst:.2e}"
+    check_close(y_gemv, y_ref, norm)
+    assert not np.array_equal(y, y_gemv)  # the two paths really differ (f16 operands)
+    w.release()
+
+
+def test_q8_0_prefill_full_size_sampled_rows(ctx):
+    """The MTP hidden projection's shape (nextn.eh_proj, q8_0, 2 x 4096 -> 4096,
+    src/model/qwen35_weights.cpp:53-58) at M = 512: every output of 24 sampled activation rows."""
+    rng = np.random.default_rng(8812)
+    rows, cols, m = 4096, 8192, 512
+    data = synth.q8_0(rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    w = ctx.upload(8, cols, rows, data)
+    y = gpu_matmul(ctx, w, x, rows)
+    pick = np.array(sorted(set([0, 1, 255, 256, 511] + list(rng.integers(0, m, 19)))))
+    y_ref, norm = reference_products(8, rows, cols, data, x[pick])
+    check_close(y[pick], y_ref, norm)
+    assert np.all(np.isfinite(y))
+    w.release()
+
+
+def test_q8_0_matrix_cores_extreme_activation_scales(ctx):
+    """The q8_0 image scales each F32 row by a power of two into binary16's range: rows at 1e5
+    and 1e-30 times N(0, 1) stay finite and within the bar; a row dominated by one element is
+    held to the rigorous 2e-3 bound (see test_matrix_cores_extreme_activation_scales)."""
+    rng = np.random.default_rng(8813)
+    m, rows, cols = 20, 200, 4096
+    data = synth.q8_0(rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    x[0] *= 1e5
+    x[1] *= 1e-30
+    x[2, 5] = 7e6
+    x[3] = 0.0
+    w = ctx.upload(8, cols, rows, data)
+    y = gpu_matmul(ctx, w, x, rows)
+    assert np.all(np.isfinite(y)) and np.all(y[3] == 0.0)
+    y_ref, norm = reference_products(8, rows, cols, data, x)
+    for r in range(m):
+        if r != 3:
+            check_close(y[r:r + 1], y_ref[r:r + 1], norm[r:r + 1], tol=2e-3 if r == 2 else TOL)
+    w.release()
+
+
 @pytest.mark.parametrize("cols", [4096, 8192])
 def test_matrix_core_kernels_agree(ctx, cols):
     """The producer/consumer GEMM kernel (default) and the four-wave kernel (OQ_GEMM_WS=0)
