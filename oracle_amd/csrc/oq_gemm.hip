@@ -1746,7 +1746,10 @@ Plan make_plan(const DeviceMatrix& w, int m) {
 }  // namespace
 
 bool gemm_mfma_supported(const DeviceMatrix& w, int m) {
-    return (w.type == 8 || w.type == 12 || w.type == 13 || w.type == 14) && m >= 16 && w.k >= kMinK && w.k % kQK == 0;
+    // rows shorter than kMinK stay on the integer paths: their f16 rounding errors average over fewer
+    // products (OQ_GEMM_MIN_K lowers the limit for measurement)
+    const uint64_t min_k = (uint64_t)std::max(knob(kGemmMinK, (int)kMinK), (int)kQK);
+    return (w.type == 8 || w.type == 12 || w.type == 13 || w.type == 14) && m >= 16 && w.k >= min_k && w.k % kQK == 0;
 }
 
 uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m) {

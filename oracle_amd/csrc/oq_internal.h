@@ -59,6 +59,7 @@ enum Knob : int {
     kGemmInt8,  // OQ_GEMM_INT8
     kAttnWgPerCu,  // OQ_ATTN_WG_PER_CU
     kAttnMinChunk,  // OQ_ATTN_MIN_CHUNK
+    kGemmMinK,  // OQ_GEMM_MIN_K: shortest rows (K) of the matrix-core path (default 4096; measurement only)
     kKnobCount
 };
 int knob(Knob k, int fallback);  // the option's value, or fallback when it is unset
