@@ -152,28 +152,33 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
     return res
 
 
-def run_deltanet(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
+def run_deltanet(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, tokens=1):
     """One Gated DeltaNet decode block (hidden 4096, 32 heads of dk = dv = 128, FFN 12288) per
-    step, chained on the device (oq_deltanet_step); steps cycle over block copies whose weights
-    total >= 512 MiB, so every step streams its projections from HBM."""
+    step, chained on the device (oq_deltanet_step; with tokens > 1, oq_deltanet_steps over that
+    many consecutive tokens); steps cycle over block copies whose weights total >= 512 MiB, so every
+    step streams its projections from HBM."""
     rng = np.random.default_rng(SEED + 100)
     d, w, vec, hist, st, x = synth.deltanet_block(rng)
+    if tokens > 1:
+        x = rng.standard_normal((tokens, d["embedding"])).astype(np.float32)
     first = oracle_amd.DeltaNetBlockWeights(ctx, d, w, vec)
     wb = first.weight_bytes()
     ncopies = max(1, math.ceil(copies_min_bytes / wb))
     blocks = [first] + [oracle_amd.DeltaNetBlockWeights(ctx, d, w, vec) for _ in range(ncopies - 1)]
     hb, sb, xb = ctx.to_device(hist), ctx.to_device(st), ctx.to_device(x)
-    yb = ctx.alloc(d["embedding"] * 4)
+    yb = ctx.alloc(tokens * d["embedding"] * 4)
 
     lib, h = ctx.lib, ctx.h
     descs = [C.byref(b.desc) for b in blocks]
     hp, sp, xp, yp = hb.ptr, sb.ptr, xb.ptr, yb.ptr
 
     def step(i):
-        if lib.oq_deltanet_step(h, descs[i % ncopies], hp, sp, xp, yp, None) != 0:
+        rc = lib.oq_deltanet_step(h, descs[i % ncopies], hp, sp, xp, yp, None) if tokens == 1 else \
+            lib.oq_deltanet_steps(h, descs[i % ncopies], tokens, hp, sp, xp, yp, None)
+        if rc != 0:
             raise RuntimeError(f"step {i}: {lib.oq_last_error(h).decode()}")
 
-    ctx.deltanet_step(blocks[0], hb, sb, xb, yb)  # checked call; sizes the block workspace
+    step(0)  # checked call; sizes the block workspace
     ctx.sync()
     ms = timed_steps(ctx, step, steps, warmup, first=1)
     for b in blocks:
@@ -183,7 +188,7 @@ def run_deltanet(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
     ms_step = ms / steps
     return {"workload": "deltanet_block", "weight_bytes": wb, "copies": ncopies, "ms_per_step": ms_step,
             "us_per_block": ms_step * 1e3, "weight_gbs": wb / (ms_step * 1e-3) / 1e9,
-            "state_bytes": 2 * st.nbytes, "dims": d}
+            "state_bytes": 2 * st.nbytes, "dims": d, "tokens": tokens, "us_per_token": ms_step * 1e3 / tokens}
 
 
 ATTN_GEOMETRY = dict(q_heads=16, kv_heads=4, head_dim=256, tokens=32768)
@@ -366,6 +371,7 @@ def main():
     ap.add_argument("--workload", default="q4k_gemv",
                     choices=sorted(WORKLOADS) + ["copy_calibration", "deltanet_block", "attention_decode",
                                                  "attention_block"])
+    ap.add_argument("--tokens", type=int, default=1, help="deltanet_block: consecutive tokens per step")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     args = ap.parse_args()
@@ -383,16 +389,17 @@ def main():
         ctx.close()
         return
     if args.workload == "deltanet_block":
-        r = run_deltanet(ctx, args.steps, args.warmup)
+        r = run_deltanet(ctx, args.steps, args.warmup, tokens=args.tokens)
         ctx.close()
         print(json.dumps({
             "metric": "DeltaNet decode block weight GB/s", "value": round(r["weight_gbs"], 2), "unit": "GB/s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8xu4 dot (i32) + f32",
             "data": "synthetic (seeded block weights, state ~ N(0, 0.01), x ~ N(0,1))",
-            "config": {"workload": "Gated DeltaNet decode block, batch 1", **r["dims"],
+            "config": {"workload": "Gated DeltaNet decode block, batch 1" if r["tokens"] == 1 else
+                       f"Gated DeltaNet block, {r['tokens']} consecutive tokens per step (oq_deltanet_steps)", **r["dims"],
                        "weight_bytes": r["weight_bytes"], "block_copies_cycled": r["copies"]},
-            "us_per_block": round(r["us_per_block"], 2),
+            "us_per_block": round(r["us_per_block"], 2), "tokens": r["tokens"], "us_per_token": round(r["us_per_token"], 2),
             "hbm_frac_weight_bytes": round(r["weight_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
         return
     if args.workload == "attention_block":
@@ -423,7 +430,7 @@ def main():
             "us_per_step": round(r["us_per_step"], 2)}), flush=True)
         return
     main_res = run_gpu(ctx, args.workload, args.steps, args.warmup)
-    secondary = block = attn = attn_block = None
+    secondary = block = block4 = attn = attn_block = None
     configs = {}
     if not args.no_secondary and args.workload == "q4k_gemv":
         secondary = run_gpu(ctx, "q4k_down_m512", max(5, args.steps // 4), max(2, args.warmup // 5))
@@ -431,6 +438,7 @@ def main():
         for name in ("q8_0_gemv", "q6k_head", "q4k_down_m4"):
             configs[name] = run_gpu(ctx, name, max(5, args.steps // 4), max(2, args.warmup // 5))
         block = run_deltanet(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
+        block4 = run_deltanet(ctx, max(5, args.steps // 10), max(2, args.warmup // 5), tokens=4)
         attn = run_attention(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
         attn_block = run_attention_block(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
     ctx.close()
@@ -493,6 +501,10 @@ def main():
         out["deltanet_block"] = {"us": round(block["us_per_block"], 2), "weight_gbs": round(block["weight_gbs"], 1),
                                  "hbm_frac": round(block["weight_gbs"] / HBM_PEAK_GBS, 4),
                                  "weight_bytes": block["weight_bytes"]}
+    if block4 is not None:
+        out["deltanet_block_4_tokens"] = {"us": round(block4["us_per_block"], 2),
+                                          "us_per_token": round(block4["us_per_token"], 2),
+                                          "weight_gbs": round(block4["weight_gbs"], 1)}
     if attn_block is not None:
         out["attention_block"] = {"us": round(attn_block["us_per_block"], 2), "gbs": round(attn_block["gbs"], 1),
                                   "hbm_frac": round(attn_block["gbs"] / HBM_PEAK_GBS, 4),

@@ -270,6 +270,21 @@ typedef struct oq_deltanet_block {
 int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* block, float* conv_history_dev,
                      float* state_dev, const float* x_dev, float* y_dev, float* trace_dev);
 
+/* m consecutive tokens through the block: the same results as m oq_deltanet_step calls on the rows
+   of x_dev [m][E] in order (token t sees the convolution history and state that token t - 1 left),
+   y_dev [m][E].  Replaces the per-token loop of the reference's multi-token evaluation
+   (src/runtime/qwen35_target_multi.cpp:14-25, one execute_qwen35_recurrent_block_reference per
+   token per block; MTP verification, src/runtime/qwen35_mtp_chain_verify_batched.cpp:38-158).  Each
+   projection streams its weights once for all m tokens (m >= 16: the matrix-core path of
+   oq_matmul, with its precision contract, except the out projection, whose heavy-tailed gated
+   input keeps the integer-dot products; below 16: the small-batch integer-dot products); the
+   convolution and the delta rule run the tokens in order inside one launch each, the state read
+   and written once, every token's arithmetic that of the single step.  trace_dev, if not NULL,
+   receives m traces of oq_deltanet_step's layout, one after the other.  Checks as
+   oq_deltanet_step, plus m in 1..65535 and x_dev 16-byte aligned. */
+int oq_deltanet_steps(oq_context* ctx, const oq_deltanet_block* block, uint64_t m, float* conv_history_dev,
+                      float* state_dev, const float* x_dev, float* y_dev, float* trace_dev);
+
 /* ------------------------------------------------------------------ full attention (decode) */
 /* A device KV cache in the reference's layout and semantics (oracle::runtime::KvCache,
    include/oracle/runtime/hybrid_cache.hpp:37-74, src/runtime/hybrid_cache.cpp:131-207): keys

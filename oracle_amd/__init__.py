@@ -276,6 +276,13 @@ class Context:
         self._call(self.lib.oq_deltanet_step, self.h, C.byref(block.desc), conv_history.ptr, state.ptr, x.ptr, y.ptr,
                    trace.ptr if trace is not None else None)
 
+    def deltanet_steps(self, block: "DeltaNetBlockWeights", m: int, conv_history: DeviceBuffer, state: DeviceBuffer,
+                       x: DeviceBuffer, y: DeviceBuffer, trace: DeviceBuffer | None = None) -> None:
+        """m consecutive tokens through the block (oq_deltanet_steps): x, y [m][E]; the same results
+        as m deltanet_step calls in order; trace: m traces one after the other."""
+        self._call(self.lib.oq_deltanet_steps, self.h, C.byref(block.desc), m, conv_history.ptr, state.ptr, x.ptr,
+                   y.ptr, trace.ptr if trace is not None else None)
+
     def deltanet_step_noalloc(self, block: "DeltaNetBlockWeights", conv_history: DeviceBuffer, state: DeviceBuffer,
                               x: DeviceBuffer, y: DeviceBuffer, trace: DeviceBuffer | None = None) -> None:
         """oq_deltanet_step_noalloc: the same step on the library's fixed per-GPU workspace (no

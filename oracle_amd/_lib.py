@@ -59,6 +59,7 @@ SIGNATURES = [
     ("oq_matmul", C.c_int, [_P, _P, _U64, _P, _P]),
     ("oq_matmul_q8k", C.c_int, [_P, _P, _U64, _P, _P]),
     ("oq_deltanet_step", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
+    ("oq_deltanet_steps", C.c_int, [_P, _P, _U64, _P, _P, _P, _P, _P]),
     ("oq_deltanet_step_noalloc", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     ("oq_deltanet_noalloc_capacity", _U64, []),
     ("oq_kv_cache_create", C.c_int, [_P, _U64, _U64, _U64, _U64, C.POINTER(_P)]),

@@ -13,6 +13,7 @@
 #include <cmath>
 #include <algorithm>
 #include <atomic>
+#include <initializer_list>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -518,6 +519,149 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
     return launch_rc(ctx, e, "deltanet_step");
 }
 
+// ---------------------------------------------------------------- m consecutive tokens
+
+// Workspace of an m-token block step: every field of block_layout with m rows (a field's rows
+// consecutive, each padded to 64 floats), then the Q8_K image of one projection input (m rows of
+// the widest input).
+struct StepsLayout {
+    uint64_t row[19];   // floats per row of each field
+    uint64_t off[19];
+    uint64_t q8_off, total_floats;
+};
+
+StepsLayout steps_layout(const oq_deltanet_block* b, uint64_t m) {
+    const BlockLayout one = block_layout(b);
+    StepsLayout l{};
+    for (int i = 0; i < 19; ++i) {
+        l.row[i] = one.sizes[i];
+        l.off[i] = l.total_floats;
+        l.total_floats += (m * one.sizes[i] + 63) & ~uint64_t(63);
+    }
+    const uint64_t kmax = std::max({b->embedding, b->value_heads * b->value_dim, b->ffn});
+    l.q8_off = l.total_floats;
+    l.total_floats += (m * (kmax / oq::kQK) * oq::kQ8KBytes / sizeof(float) + 64) & ~uint64_t(63);
+    return l;
+}
+
+// m activation rows through one block projection, with the path oq_matmul takes: matrix cores for
+// m >= 16 (where `mfma` allows), else the K-quant small-batch GEMV from the Q8_K image q8
+// (quantized once per input by the caller) or the F32-activation GEMV.
+bool on_matrix_cores(const oq_weight* w, uint64_t m, bool mfma) {
+    return mfma && oq::gemm_mfma_supported(w->m, (int)m) && knob_flag(oq::kGemmMfma, true);
+}
+
+hipError_t project_rows(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, const uint8_t* q8, float* y,
+                        bool mfma = true) {
+    if (on_matrix_cores(w, m, mfma)) return oq::launch_gemm_mfma(w->m, (int)m, x, nullptr, y, ctx->scratch.ptr, ctx->stream);
+    if (is_kquant(w->m.type)) return oq::launch_gemv_kquant(w->m, (int)m, nullptr, q8, y, ctx->stream);
+    return oq::launch_gemv_f32act(w->m, (int)m, x, y, ctx->stream);
+}
+
+bool needs_q8(const oq_weight* w, uint64_t m, bool mfma = true) {
+    return is_kquant(w->m.type) && !on_matrix_cores(w, m, mfma);
+}
+
+int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, float* hist, float* state, const float* x,
+                   float* y, float* trace) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (!b || !hist || !state || !x || !y) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    if (m == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "token count must be non-zero");
+    if (m > 0xFFFF) return fail(ctx, OQ_INVALID_ARGUMENT, "at most 65535 tokens per call");
+    const uint64_t E = b->embedding, Hk = b->key_heads, Hv = b->value_heads, dk = b->key_dim, dv = b->value_dim,
+                   K = b->conv_kernel, F = b->ffn;
+    if (E == 0 || Hk == 0 || Hv == 0 || dk == 0 || dv == 0 || K == 0 || F == 0 || Hv % Hk != 0) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 recurrent block dimensions are incompatible");
+    }
+    if (!(b->eps > 0.0f) || !std::isfinite(b->eps)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 RMSNorm epsilon must be positive and finite");
+    }
+    if (!oq::deltanet_dims_supported(dk, dv, K)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT,
+                    "DeltaNet block device path needs key_dim in {32,64,128}, value_dim in {64,128,192,256}, conv_kernel <= 16");
+    }
+    const uint64_t V = Hv * dv, C = 2 * Hk * dk + V;
+    if (m * std::max({E, F, C}) > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "block too large");
+    if (int rc = check_block_weight(ctx, b->qkv, E, C, "qkv")) return rc;
+    if (int rc = check_block_weight(ctx, b->z, E, V, "z")) return rc;
+    if (int rc = check_block_weight(ctx, b->beta, E, Hv, "beta")) return rc;
+    if (int rc = check_block_weight(ctx, b->alpha, E, Hv, "alpha")) return rc;
+    if (int rc = check_block_weight(ctx, b->out, V, E, "out")) return rc;
+    if (int rc = check_block_weight(ctx, b->gate, E, F, "gate")) return rc;
+    if (int rc = check_block_weight(ctx, b->up, E, F, "up")) return rc;
+    if (int rc = check_block_weight(ctx, b->down, F, E, "down")) return rc;
+    if (!b->input_norm || !b->conv_weight || !b->dt_bias || !b->decay || !b->out_norm || !b->post_norm) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "null block vector");
+    }
+    if (!aligned(x, 16) || !aligned(y, 4) || !aligned(hist, 4) || !aligned(state, 4) || (trace && !aligned(trace, 4))) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer (x 16-byte, others 4-byte)");
+    }
+    const StepsLayout lay = steps_layout(b, m);
+    if (int rc = ensure_work(ctx, lay.total_floats * sizeof(float))) return rc;
+    uint64_t scratch = 0;
+    for (const oq_weight* w : {b->qkv, b->z, b->beta, b->alpha, b->gate, b->up, b->down}) {
+        if (oq::gemm_mfma_supported(w->m, (int)m) && knob_flag(oq::kGemmMfma, true))
+            scratch = std::max(scratch, oq::gemm_scratch_bytes(w->m, (int)m));
+    }
+    if (scratch > 0) {
+        if (int rc = ensure_scratch(ctx, scratch)) return rc;
+    }
+    float* ws = static_cast<float*>(ctx->work.ptr);
+    const uint64_t* off = lay.off;
+    float *qkv = ws + off[0], *z = ws + off[1], *beta = ws + off[2], *alpha = ws + off[3], *conv = ws + off[4],
+          *rec = ws + off[5], *gated = ws + off[6], *branch = ws + off[7], *resid = ws + off[8], *post = ws + off[9],
+          *gate = ws + off[10], *up = ws + off[11], *act = ws + off[12], *ffn = ws + off[13], *beta_s = ws + off[14],
+          *log_decay = ws + off[15], *normed = ws + off[16];
+    double* head_ss = reinterpret_cast<double*>(ws + off[17]);
+    uint8_t* q8 = reinterpret_cast<uint8_t*>(ws + lay.q8_off);
+    hipStream_t s = ctx->stream;
+    // the Q8_K image of one projection input, when a projection of it takes the small-batch GEMV
+    auto quantize = [&](const float* in, uint64_t k, std::initializer_list<const oq_weight*> ws_of_input) {
+        for (const oq_weight* w : ws_of_input)
+            if (needs_q8(w, m)) return oq::launch_quantize_q8k(in, m, k, q8, s);
+        return hipSuccess;
+    };
+    hipError_t e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m);
+    if (e == hipSuccess) e = quantize(normed, E, {b->qkv, b->z, b->beta, b->alpha});
+    if (e == hipSuccess) e = project_rows(ctx, b->qkv, m, normed, q8, qkv);
+    if (e == hipSuccess) e = project_rows(ctx, b->z, m, normed, q8, z);
+    if (e == hipSuccess) e = project_rows(ctx, b->beta, m, normed, q8, beta);
+    if (e == hipSuccess) e = project_rows(ctx, b->alpha, m, normed, q8, alpha);
+    if (e == hipSuccess)
+        e = oq::launch_conv_gates_tokens(qkv, b->conv_weight, hist, C, K, beta, alpha, b->dt_bias, b->decay, Hv, m,
+                                         conv, beta_s, log_decay, s);
+    if (e == hipSuccess)
+        e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, rec, head_ss, nullptr, nullptr, s,
+                             m);
+    if (e == hipSuccess) e = oq::launch_gated_norm(rec, head_ss, z, b->out_norm, Hv, dv, b->eps, gated, s, m);
+    // the out projection's input (RMSNorm(rec) * out_norm * SiLU(z), a product of two near-Gaussian
+    // rows) is heavy-tailed -- kurtosis 68 on the hidden-4096 block, one product up to 13 % of
+    // sum |w xhat| -- so f16 operands would reach the product bar (2.3e-4 measured at 16 tokens):
+    // it keeps the integer-dot products at every m
+    if (e == hipSuccess && is_kquant(b->out->m.type)) e = oq::launch_quantize_q8k(gated, m, V, q8, s);
+    if (e == hipSuccess) e = project_rows(ctx, b->out, m, gated, q8, branch, false);
+    if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m);
+    if (e == hipSuccess) e = quantize(post, E, {b->gate, b->up});
+    if (e == hipSuccess) e = project_rows(ctx, b->gate, m, post, q8, gate);
+    if (e == hipSuccess) e = project_rows(ctx, b->up, m, post, q8, up);
+    if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s);
+    if (e == hipSuccess) e = quantize(act, F, {b->down});
+    if (e == hipSuccess) e = project_rows(ctx, b->down, m, act, q8, ffn);
+    if (e == hipSuccess) e = oq::launch_add(resid, ffn, m * E, y, s);
+    if (e == hipSuccess && trace) {
+        // token t's trace (the 16 fields of oq_deltanet_step's trace, in order) at trace + t * size
+        uint64_t per_token = 0;
+        for (int i = 0; i < 16; ++i) per_token += lay.row[i];
+        uint64_t t = 0;
+        for (int i = 0; i < 16 && e == hipSuccess; ++i) {
+            e = hipMemcpy2DAsync(trace + t, per_token * sizeof(float), ws + off[i], lay.row[i] * sizeof(float),
+                                 lay.row[i] * sizeof(float), m, hipMemcpyDeviceToDevice, s);
+            t += lay.row[i];
+        }
+    }
+    return launch_rc(ctx, e, "deltanet_steps");
+}
+
 }  // namespace
 
 namespace oq {
@@ -539,6 +683,11 @@ extern "C" {
 int oq_deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, float* state, const float* x,
                      float* y, float* trace) {
     return deltanet_step(ctx, b, hist, state, x, y, trace, nullptr, 0);
+}
+
+int oq_deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, float* hist, float* state,
+                      const float* x, float* y, float* trace) {
+    return deltanet_steps(ctx, b, m, hist, state, x, y, trace);
 }
 
 }  // extern "C"

@@ -62,6 +62,14 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
                                                                const float* __restrict__ w, uint32_t n, float eps,
                                                                float* __restrict__ sum_out, float* __restrict__ out) {
     __shared__ double red[16];
+    // workgroup r normalises row r (rows of n values, consecutive)
+    const uint64_t row = (uint64_t)blockIdx.x * n;
+    a += row;
+    if (b) {
+        b += row;
+        sum_out += row;
+    }
+    out += row;
     double ss = 0.0;
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
         float v = a[i];
@@ -110,6 +118,36 @@ __global__ __launch_bounds__(256) void conv_gates_kernel(const float* __restrict
     conv_out[c] = silu_ref((float)sum);
 }
 
+// The same for `tokens` consecutive tokens: qkv [tokens][channels] -> conv_out [tokens][channels],
+// the history advanced once per token in token order (as `tokens` calls of the step), the gates
+// per (token, head).
+__global__ __launch_bounds__(256) void conv_gates_tokens_kernel(
+    const float* __restrict__ qkv, const float* __restrict__ conv_w, float* __restrict__ history, uint32_t channels,
+    uint32_t kernel, const float* __restrict__ beta, const float* __restrict__ alpha,
+    const float* __restrict__ dt_bias, const float* __restrict__ decay, uint32_t heads, uint32_t tokens,
+    float* __restrict__ conv_out, float* __restrict__ beta_s, float* __restrict__ log_decay) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+    if (blockIdx.x == 0) {
+        for (uint32_t i = threadIdx.x; i < heads * tokens; i += 256) {
+            const uint32_t h = i % heads;
+            beta_s[i] = sigmoid_ref(beta[i]);
+            log_decay[i] = softplus_ref(alpha[i] + dt_bias[h]) * decay[h];
+        }
+    }
+    if (c >= channels) return;
+    float* hst = history + (uint64_t)c * kernel;
+    const float* wc = conv_w + (uint64_t)c * kernel;
+    for (uint32_t t = 0; t < tokens; ++t) {
+        double sum = 0.0;
+        for (uint32_t i = 0; i < kernel; ++i) {
+            const float v = i + 1 < kernel ? hst[i + 1] : qkv[(uint64_t)t * channels + c];
+            hst[i] = v;
+            sum += (double)v * (double)wc[i];
+        }
+        conv_out[(uint64_t)t * channels + c] = silu_ref((float)sum);
+    }
+}
+
 // The gated delta rule step (reference_kernels.cpp:227-335) on the state [head][key][value],
 // one workgroup per (value head h, chunk of 32 value columns), 256 threads = 8 key slices x 32
 // columns: thread (slice, column) keeps the DK/8 state values of its column and key slice in
@@ -129,12 +167,18 @@ __global__ __launch_bounds__(256) void conv_gates_kernel(const float* __restrict
 // more workgroups, each with a shorter chain, 49.9 against 48.6 us per block)
 constexpr int kDeltaCols = 32;
 
+//
+// With tokens > 1 the launch runs `tokens` consecutive steps (token t's conv row at conv + t * C,
+// its gates at beta_s / log_decay + t * Hv, its outputs at rec_out + t * Hv * dv and head_ss +
+// t * Hv * chunks): each thread keeps its state values in registers from the first token to the
+// last, and every token's arithmetic is that of a single step, so the results equal `tokens`
+// launches bit for bit while the state is read and written once.
 template <int DK, int COLS>
 __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ conv, uint32_t key_heads, uint32_t dv,
                                                     const float* __restrict__ beta_s, const float* __restrict__ log_decay,
                                                     float eps, float* __restrict__ state, float* __restrict__ rec_out,
                                                     double* __restrict__ head_ss, const float* __restrict__ z,
-                                                    float* __restrict__ z_silu) {
+                                                    float* __restrict__ z_silu, uint32_t tokens, uint32_t value_heads) {
     constexpr int SLICES = 256 / COLS;
     constexpr int KS = DK / SLICES;  // keys per thread
     __shared__ __align__(16) float nq[DK];
@@ -148,16 +192,19 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
     const uint32_t d0 = slice * KS;
     float* scol = state + ((uint64_t)h * DK + d0) * dv + v;
     const uint32_t kw = key_heads * DK;
-    const float* q = conv + (uint64_t)(h % key_heads) * DK;
-    const float* k = conv + kw + (uint64_t)(h % key_heads) * DK;
+    const uint64_t cstride = 2ull * kw + (uint64_t)value_heads * dv;  // one token's conv row
     // every input is requested before the first barrier
     float s[KS];
 #pragma unroll
     for (int i = 0; i < KS; ++i) s[i] = scol[(uint64_t)i * dv];
-    const float vv = conv[2u * kw + (uint64_t)h * dv + v];
+    for (uint32_t t = 0; t < tokens; ++t) {
+    if (t > 0) __syncthreads();  // the previous token's reads of nq / nk and the partial sums are done
+    const float* q = conv + t * cstride + (uint64_t)(h % key_heads) * DK;
+    const float* k = conv + t * cstride + kw + (uint64_t)(h % key_heads) * DK;
+    const float vv = conv[t * cstride + 2u * kw + (uint64_t)h * dv + v];
     const float zv = z_silu != nullptr && slice == 0 ? z[(uint64_t)h * dv + v] : 0.0f;
-    const float ldh = log_decay[h];
-    const float beta = beta_s[h];
+    const float ldh = log_decay[(uint64_t)t * value_heads + h];
+    const float beta = beta_s[(uint64_t)t * value_heads + h];
     if (threadIdx.x < 64) {
         // the first wave: L2 norms of the head's query and key (DK <= 128: two values per lane)
         const int lane = threadIdx.x;
@@ -197,7 +244,6 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
 #pragma unroll
     for (int i = 0; i < KS; ++i) {
         s[i] = s[i] + nk[d0 + i] * delta;
-        scol[(uint64_t)i * dv] = s[i];
         o = o + (double)s[i] * (double)nq[d0 + i];
     }
     out_part[slice][col] = o;
@@ -207,27 +253,33 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
 #pragma unroll
         for (int j = 0; j < SLICES; ++j) out = out + out_part[j][col];
         const float of = (float)out;
-        rec_out[(uint64_t)h * dv + v] = of;
+        const uint64_t vt = (uint64_t)t * value_heads * dv;
+        rec_out[vt + (uint64_t)h * dv + v] = of;
         // the chunk's sum of squares over its COLS columns (the first COLS lanes of wave 0)
         double sq = (double)of * (double)of;
 #pragma unroll
         for (int off = COLS / 2; off >= 1; off >>= 1) sq += __shfl_xor(sq, off, 64);
-        if (col == 0) head_ss[(uint64_t)h * chunks + chunk] = sq;
+        if (col == 0) head_ss[(uint64_t)t * value_heads * chunks + (uint64_t)h * chunks + chunk] = sq;
         if (z_silu != nullptr) z_silu[(uint64_t)h * dv + v] = silu_ref(zv);
     }
+    }
+#pragma unroll
+    for (int i = 0; i < KS; ++i) scol[(uint64_t)i * dv] = s[i];
 }
 
 // gated[h][v] = RMSNorm(rec[h])[v] * out_norm[v] * SiLU(z[h][v]) (qwen35_block.cpp:579-588), the
 // head's sum of squares taken from the delta kernel's per-chunk partials (added in chunk order).
 __global__ __launch_bounds__(256) void gated_norm_kernel(const float* __restrict__ rec, const double* __restrict__ head_ss,
                                                          const float* __restrict__ z, const float* __restrict__ out_norm,
-                                                         uint32_t heads, uint32_t dv, uint32_t chunks, float eps,
+                                                         uint32_t total, uint32_t dv, uint32_t chunks, float eps,
                                                          float* __restrict__ gated) {
+    // i over tokens x heads x dv: token rows of rec / z / gated are consecutive, as are the
+    // tokens' head_ss rows
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= heads * dv) return;
-    const uint32_t h = i / dv, v = i % dv;
+    if (i >= total) return;
+    const uint32_t hv = i / dv, v = i % dv;  // hv = token * heads + head
     double ss = 0.0;
-    for (uint32_t c = 0; c < chunks; ++c) ss += head_ss[(uint64_t)h * chunks + c];
+    for (uint32_t c = 0; c < chunks; ++c) ss += head_ss[(uint64_t)hv * chunks + c];
     const float inv = (float)(1.0 / sqrt(ss / (double)dv + (double)eps));
     gated[i] = rec[i] * inv * out_norm[v] * silu_ref(z[i]);
 }
@@ -258,8 +310,19 @@ bool deltanet_dims_supported(uint64_t key_dim, uint64_t value_dim, uint64_t conv
 }
 
 hipError_t launch_rmsnorm(const float* a, const float* b, const float* w, uint64_t n, float eps, float* sum_out,
-                          float* out, hipStream_t s) {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, s, a, b, w, (uint32_t)n, eps, sum_out, out);
+                          float* out, hipStream_t s, uint64_t rows) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, s, a, b, w, (uint32_t)n, eps, sum_out,
+                       out);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv_gates_tokens(const float* qkv, const float* conv_w, float* history, uint64_t channels,
+                                    uint64_t kernel, const float* beta, const float* alpha, const float* dt_bias,
+                                    const float* decay, uint64_t heads, uint64_t tokens, float* conv_out,
+                                    float* beta_s, float* log_decay, hipStream_t s) {
+    hipLaunchKernelGGL(conv_gates_tokens_kernel, dim3(blocks_of(channels, 256)), dim3(256), 0, s, qkv, conv_w, history,
+                       (uint32_t)channels, (uint32_t)kernel, beta, alpha, dt_bias, decay, (uint32_t)heads,
+                       (uint32_t)tokens, conv_out, beta_s, log_decay);
     return hipGetLastError();
 }
 
@@ -275,22 +338,26 @@ hipError_t launch_conv_gates(const float* qkv, const float* conv_w, float* histo
 
 hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_heads, uint64_t dk, uint64_t dv,
                         const float* beta_s, const float* log_decay, float eps, float* state, float* rec_out,
-                        double* head_ss, const float* z, float* z_silu, hipStream_t s) {
+                        double* head_ss, const float* z, float* z_silu, hipStream_t s, uint64_t tokens) {
+    if (tokens > 1 && z_silu != nullptr) return hipErrorInvalidValue;  // SiLU(z) is a single-token epilogue
     if ((z == nullptr) != (z_silu == nullptr)) return hipErrorInvalidValue;
     if (dv % kDeltaCols != 0) return hipErrorInvalidValue;
     const dim3 grid((unsigned)(value_heads * (dv / kDeltaCols))), block(256);
     switch (dk) {
         case 32:
             hipLaunchKernelGGL((delta_kernel<32, kDeltaCols>), grid, block, 0, s, conv, (uint32_t)key_heads,
-                               (uint32_t)dv, beta_s, log_decay, eps, state, rec_out, head_ss, z, z_silu);
+                               (uint32_t)dv, beta_s, log_decay, eps, state, rec_out, head_ss, z, z_silu, (uint32_t)tokens,
+                               (uint32_t)value_heads);
             break;
         case 64:
             hipLaunchKernelGGL((delta_kernel<64, kDeltaCols>), grid, block, 0, s, conv, (uint32_t)key_heads,
-                               (uint32_t)dv, beta_s, log_decay, eps, state, rec_out, head_ss, z, z_silu);
+                               (uint32_t)dv, beta_s, log_decay, eps, state, rec_out, head_ss, z, z_silu, (uint32_t)tokens,
+                               (uint32_t)value_heads);
             break;
         case 128:
             hipLaunchKernelGGL((delta_kernel<128, kDeltaCols>), grid, block, 0, s, conv, (uint32_t)key_heads,
-                               (uint32_t)dv, beta_s, log_decay, eps, state, rec_out, head_ss, z, z_silu);
+                               (uint32_t)dv, beta_s, log_decay, eps, state, rec_out, head_ss, z, z_silu, (uint32_t)tokens,
+                               (uint32_t)value_heads);
             break;
         default:
             return hipErrorInvalidValue;
@@ -299,9 +366,10 @@ hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_he
 }
 
 hipError_t launch_gated_norm(const float* rec, const double* head_ss, const float* z, const float* out_norm,
-                             uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s) {
-    hipLaunchKernelGGL(gated_norm_kernel, dim3(blocks_of(heads * dv, 256)), dim3(256), 0, s, rec, head_ss, z, out_norm,
-                       (uint32_t)heads, (uint32_t)dv, (uint32_t)delta_chunks(dv), eps, gated);
+                             uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s, uint64_t tokens) {
+    const uint64_t total = tokens * heads * dv;
+    hipLaunchKernelGGL(gated_norm_kernel, dim3(blocks_of(total, 256)), dim3(256), 0, s, rec, head_ss, z, out_norm,
+                       (uint32_t)total, (uint32_t)dv, (uint32_t)delta_chunks(dv), eps, gated);
     return hipGetLastError();
 }
 

@@ -136,21 +136,27 @@ hipError_t launch_gemm_q4k_i8(const DeviceMatrix& w, int m, const float* x, cons
 
 // ---- oq_deltanet.hip  (Gated DeltaNet decode block: kernels between the projections)
 bool deltanet_dims_supported(uint64_t key_dim, uint64_t value_dim, uint64_t conv_kernel);
+// rows consecutive rows of n values (one workgroup each)
 hipError_t launch_rmsnorm(const float* a, const float* b, const float* w, uint64_t n, float eps, float* sum_out,
-                          float* out, hipStream_t s);
+                          float* out, hipStream_t s, uint64_t rows = 1);
 hipError_t launch_conv_gates(const float* qkv, const float* conv_w, float* history, uint64_t channels,
                              uint64_t kernel, const float* beta, const float* alpha, const float* dt_bias,
                              const float* decay, uint64_t heads, float* conv_out, float* beta_s, float* log_decay,
                              hipStream_t s);
+// tokens consecutive tokens: qkv / conv_out [tokens][channels], beta / alpha / beta_s / log_decay [tokens][heads]
+hipError_t launch_conv_gates_tokens(const float* qkv, const float* conv_w, float* history, uint64_t channels,
+                                    uint64_t kernel, const float* beta, const float* alpha, const float* dt_bias,
+                                    const float* decay, uint64_t heads, uint64_t tokens, float* conv_out,
+                                    float* beta_s, float* log_decay, hipStream_t s);
 // the delta rule over Hv * dv/32 workgroups: rec_out[Hv][dv] and head_ss[Hv][dv/32], the per-chunk double
 // sums of rec_out^2 that the head's gated RMSNorm takes (launch_gated_norm, or the out projection's staging)
 // z / z_silu: when not null, the launch also stores SiLU(z) of the block's gate row (the value
 // heads' columns, [Hv][dv]) for the out projection's staging
 hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_heads, uint64_t dk, uint64_t dv,
                         const float* beta_s, const float* log_decay, float eps, float* state, float* rec_out,
-                        double* head_ss, const float* z, float* z_silu, hipStream_t s);
+                        double* head_ss, const float* z, float* z_silu, hipStream_t s, uint64_t tokens = 1);
 hipError_t launch_gated_norm(const float* rec, const double* head_ss, const float* z, const float* out_norm,
-                             uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s);
+                             uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s, uint64_t tokens = 1);
 uint64_t delta_chunks(uint64_t dv);  // head_ss entries per head
 hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s);
 hipError_t launch_add(const float* a, const float* b, uint64_t n, float* out, hipStream_t s);
