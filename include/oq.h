@@ -372,6 +372,19 @@ typedef struct oq_attention_block {
 int oq_attention_block_step(oq_context* ctx, const oq_attention_block* block, oq_kv_cache* cache,
                             const uint64_t position[3], const float* x_dev, float* y_dev, float* trace_dev);
 
+/* m consecutive tokens through the block: the same results as m oq_attention_block_step calls on
+   the rows of x_dev [m][E] in order, token t at positions[3 t .. 3 t + 2] (host array), appending
+   m rows to the cache; y_dev [m][E].  Replaces the per-token loop of the reference's multi-token
+   evaluation (src/runtime/qwen35_target_multi.cpp:14-25).  The projections stream their weights
+   once for all m tokens (m >= 16: the matrix-core path of oq_matmul, with its precision contract;
+   below 16: the small-batch integer-dot products); token t's attention step appends its key and
+   value at row size + t and attends over every row up to it, as the single step does.  trace_dev,
+   if not NULL, receives m traces of oq_attention_block_step's layout, one after the other.
+   Checks as oq_attention_block_step, every position, m in 1..65535, and size + m <= capacity
+   (OQ_OVERFLOW, "KV cache capacity exceeded"), all before any device work. */
+int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* block, oq_kv_cache* cache, uint64_t m,
+                             const uint64_t* positions, const float* x_dev, float* y_dev, float* trace_dev);
+
 /* No counterpart in the reference.  oq_deltanet_step for callers that cannot allocate device
    memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
    same arguments, checks, kernels and results, but it allocates nothing -- the block's

@@ -316,6 +316,16 @@ class Context:
         self._call(self.lib.oq_attention_block_step, self.h, C.byref(block.desc), cache.h, pos, x.ptr, y.ptr,
                    trace.ptr if trace is not None else None)
 
+    def attention_block_steps(self, block: "AttentionBlockWeights", cache: "KvCache", positions, x: DeviceBuffer,
+                              y: DeviceBuffer, trace: DeviceBuffer | None = None) -> None:
+        """m consecutive tokens through the full-attention block (oq_attention_block_steps); positions:
+        m (temporal, height, width) triples; appends m rows to the cache."""
+        pos = [int(v) for p in positions for v in p]
+        m = len(pos) // 3
+        arr = (C.c_uint64 * len(pos))(*pos)
+        self._call(self.lib.oq_attention_block_steps, self.h, C.byref(block.desc), cache.h, m, arr, x.ptr, y.ptr,
+                   trace.ptr if trace is not None else None)
+
     def timer_start(self) -> None:
         self._call(self.lib.oq_timer_start, self.h)
 

@@ -73,6 +73,7 @@ SIGNATURES = [
     ("oq_rope", C.c_int, [_P, _P, _U64, _U64, _U64, _P, C.c_float, _P]),
     ("oq_attention_step", C.c_int, [_P, _P, _U64, _P, _P, _P, _P]),
     ("oq_attention_block_step", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
+    ("oq_attention_block_steps", C.c_int, [_P, _P, _P, _U64, _P, _P, _P, _P]),
     ("oq_timer_start", C.c_int, [_P]),
     ("oq_timer_stop", C.c_int, [_P, C.POINTER(C.c_float)]),
     ("oq_capture_begin", C.c_int, [_P]),

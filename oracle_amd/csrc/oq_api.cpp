@@ -1103,14 +1103,14 @@ int check_cache(oq_context* ctx, const oq_kv_cache* c) {
 
 // the attention launch over a cache whose new token (index T - 1 = cache->length) is given by
 // new_k / new_v, or already stored (both null); the partials go to `part`
-int attention_shape(oq_context* ctx, const oq_kv_cache* c, uint64_t q_heads, oq::AttnLaunch& L) {
+int attention_shape(oq_context* ctx, const oq_kv_cache* c, uint64_t q_heads, oq::AttnLaunch& L, uint64_t ahead = 0) {
     const uint64_t rep = q_heads / c->kv_heads;
     if (c->key_dim != c->value_dim || !oq::attention_dims_supported(c->key_dim, rep)) {
         return fail(ctx, OQ_INVALID_ARGUMENT,
                     "attention device path needs key_dim == value_dim in {64, 128, 256} and at most 8 query heads per "
                     "KV head");
     }
-    const uint64_t T = c->length + 1;
+    const uint64_t T = c->length + 1 + ahead;  // the token `ahead` places after the next one to append
     uint32_t chunk = 0, nchunks = 0;
     oq::attention_plan(T, c->kv_heads, chunk, nchunks);
     if (nchunks > oq::kAttnMaxChunks || T > 0xFFFFFFFFull || c->kv_heads > 0xFFFF) {
@@ -1434,6 +1434,136 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_
     }
     const int rc = launch_rc(ctx, e, "attention_block_step");
     if (rc == OQ_OK) cache->length += 1;
+    return rc;
+}
+
+int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv_cache* cache, uint64_t m,
+                             const uint64_t* positions, const float* x, float* y, float* trace) {
+    if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
+    if (!b || !x || !y || !positions) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
+    if (int rc = check_cache(ctx, cache)) return rc;
+    if (m == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "token count must be non-zero");
+    if (m > 0xFFFF) return fail(ctx, OQ_INVALID_ARGUMENT, "at most 65535 tokens per call");
+    const uint64_t E = b->embedding, Hq = b->q_heads, Hkv = b->kv_heads, D = b->head_dim, F = b->ffn;
+    if (E == 0 || Hq == 0 || Hkv == 0 || D == 0 || F == 0 || Hq % Hkv != 0) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 attention block dimensions are incompatible");
+    }
+    if (cache->kv_heads != Hkv || cache->key_dim != D || cache->value_dim != D) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 attention cache dimensions do not match the manifest");
+    }
+    if (!(b->eps > 0.0f) || !std::isfinite(b->eps)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 RMSNorm epsilon must be positive and finite");
+    }
+    std::vector<oq::RopeParams> rps(m);
+    for (uint64_t t = 0; t < m; ++t) {
+        if (int rc = rope_params(ctx, D, b->rope_dim, b->rope_sections, b->rope_base, positions + 3 * t, rps[t])) return rc;
+    }
+    const uint64_t Q = Hq * D, KV = Hkv * D;
+    if (m * std::max({E, F, 2 * Q}) > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "block too large");
+    if (int rc = check_attn_weight(ctx, b->q, E, 2 * Q, "q")) return rc;
+    if (int rc = check_attn_weight(ctx, b->k, E, KV, "k")) return rc;
+    if (int rc = check_attn_weight(ctx, b->v, E, KV, "v")) return rc;
+    if (int rc = check_attn_weight(ctx, b->out, Q, E, "out")) return rc;
+    if (int rc = check_attn_weight(ctx, b->gate, E, F, "gate")) return rc;
+    if (int rc = check_attn_weight(ctx, b->up, E, F, "up")) return rc;
+    if (int rc = check_attn_weight(ctx, b->down, F, E, "down")) return rc;
+    if (!b->input_norm || !b->q_norm || !b->k_norm || !b->post_norm) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "null block vector");
+    }
+    if (!aligned(x, 16) || !aligned(y, 4) || (trace && !aligned(trace, 4))) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer (x 16-byte, others 4-byte)");
+    }
+    if (cache->capacity - cache->length < m) return fail(ctx, OQ_OVERFLOW, "KV cache capacity exceeded");
+    // the attention launch of every token, and the partial-sum buffer the longest one needs
+    std::vector<oq::AttnLaunch> Ls(m);
+    uint64_t part_floats = 0;
+    for (uint64_t t = 0; t < m; ++t) {
+        if (int rc = attention_shape(ctx, cache, Hq, Ls[t], t)) return rc;
+        part_floats = std::max(part_floats, oq::attention_partial_floats(Hkv, Hq / Hkv, D, Ls[t].nchunks));
+    }
+    // workspace: the 15 trace fields with m rows each, the normalised input, the partial sums and
+    // one Q8_K image (m rows of the widest projection input)
+    const uint64_t row[16] = {2 * Q, KV, KV, Q, KV, Q, Q, Q, E, E, E, F, F, F, E, E};
+    uint64_t off[18], total = 0;
+    for (int i = 0; i < 16; ++i) {
+        off[i] = total;
+        total += (m * row[i] + 63) & ~uint64_t(63);
+    }
+    off[16] = total;
+    total += (part_floats + 63) & ~uint64_t(63);
+    off[17] = total;
+    total += (m * (std::max({E, Q, F}) / oq::kQK) * oq::kQ8KBytes / sizeof(float) + 64) & ~uint64_t(63);
+    if (int rc = ensure_work(ctx, total * sizeof(float))) return rc;
+    uint64_t scratch = 0;
+    for (const oq_weight* w : {b->q, b->k, b->v, b->out, b->gate, b->up, b->down}) {
+        if (on_matrix_cores(w, m, true)) scratch = std::max(scratch, oq::gemm_scratch_bytes(w->m, (int)m));
+    }
+    if (scratch > 0) {
+        if (int rc = ensure_scratch(ctx, scratch)) return rc;
+    }
+    float* ws = static_cast<float*>(ctx->work.ptr);
+    float *qfull = ws + off[0], *kp = ws + off[1], *vp = ws + off[2], *qcur = ws + off[3], *kcur = ws + off[4],
+          *pregate = ws + off[5], *gate_s = ws + off[6], *gated = ws + off[7], *branch = ws + off[8],
+          *resid = ws + off[9], *post = ws + off[10], *gate = ws + off[11], *up = ws + off[12], *act = ws + off[13],
+          *ffn = ws + off[14], *normed = ws + off[15], *part = ws + off[16];
+    uint8_t* q8 = reinterpret_cast<uint8_t*>(ws + off[17]);
+    hipStream_t s = ctx->stream;
+    auto quantize = [&](const float* in, uint64_t k, std::initializer_list<const oq_weight*> consumers) {
+        for (const oq_weight* w : consumers)
+            if (needs_q8(w, m)) return oq::launch_quantize_q8k(in, m, k, q8, s);
+        return hipSuccess;
+    };
+    hipError_t e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m);
+    if (e == hipSuccess) e = quantize(normed, E, {b->q, b->k, b->v});
+    if (e == hipSuccess) e = project_rows(ctx, b->q, m, normed, q8, qfull);
+    if (e == hipSuccess) e = project_rows(ctx, b->k, m, normed, q8, kp);
+    if (e == hipSuccess) e = project_rows(ctx, b->v, m, normed, q8, vp);
+    // the tokens' attention steps in order: token t appends its key and value at row length + t and
+    // attends over the rows before it and itself (the single step's launch, with its head preparation)
+    for (uint64_t t = 0; t < m && e == hipSuccess; ++t) {
+        oq::AttnPrep prep{};
+        prep.qfull = qfull + t * 2 * Q;
+        prep.kp = kp + t * KV;
+        prep.vp = vp + t * KV;
+        prep.q_norm = b->q_norm;
+        prep.k_norm = b->k_norm;
+        prep.eps = b->eps;
+        prep.rope = rps[t];
+        prep.qcur = trace ? qcur + t * Q : nullptr;
+        prep.kcur = trace ? kcur + t * KV : nullptr;
+        oq::AttnLaunch& L = Ls[t];
+        L.prep = &prep;
+        L.part = part;
+        L.out = trace ? pregate + t * Q : nullptr;
+        L.gate = qfull + t * 2 * Q + D;
+        L.gate_stride = (uint32_t)(2 * D);
+        L.gate_s = trace ? gate_s + t * Q : nullptr;
+        L.gated = gated + t * Q;
+        e = oq::launch_attention(L, s);
+    }
+    if (e == hipSuccess) e = quantize(gated, Q, {b->out});
+    if (e == hipSuccess) e = project_rows(ctx, b->out, m, gated, q8, branch);
+    if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m);
+    if (e == hipSuccess) e = quantize(post, E, {b->gate, b->up});
+    if (e == hipSuccess) e = project_rows(ctx, b->gate, m, post, q8, gate);
+    if (e == hipSuccess) e = project_rows(ctx, b->up, m, post, q8, up);
+    if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s);
+    if (e == hipSuccess) e = quantize(act, F, {b->down});
+    if (e == hipSuccess) e = project_rows(ctx, b->down, m, act, q8, ffn);
+    if (e == hipSuccess) e = oq::launch_add(resid, ffn, m * E, y, s);
+    if (e == hipSuccess && trace) {
+        // token t's trace (oq_attention_block_step's 15 fields, in order) at trace + t * size
+        uint64_t per_token = 0;
+        for (int i = 0; i < 15; ++i) per_token += row[i];
+        uint64_t t = 0;
+        for (int i = 0; i < 15 && e == hipSuccess; ++i) {
+            e = hipMemcpy2DAsync(trace + t, per_token * sizeof(float), ws + off[i], row[i] * sizeof(float),
+                                 row[i] * sizeof(float), m, hipMemcpyDeviceToDevice, s);
+            t += row[i];
+        }
+    }
+    const int rc = launch_rc(ctx, e, "attention_block_steps");
+    if (rc == OQ_OK) cache->length += m;
     return rc;
 }
 

@@ -267,7 +267,9 @@ def close(name, got, want, worst):
     assert worst[name] <= STAGE_TOL, f"{name}: error {worst[name]:.3e} of scale"
 
 
-def check_block_stages(d, w, vec, step):
+def check_block_stages(d, w, vec, step, proj_tol=None):
+    """Every traced stage of one block step from the device's inputs to it; proj_tol maps a
+    projection's trace name to a bound other than TOL."""
     E, F, Hq, Hkv, D, eps = (d[k] for k in ("embedding", "ffn", "q_heads", "kv_heads", "head_dim", "eps"))
     Q, KV = Hq * D, Hkv * D
     g, x = step["trace"], step["x"]
@@ -279,7 +281,7 @@ def check_block_stages(d, w, vec, step):
     for n, (wn, inp, rows, cols) in projections.items():
         y, norm = project(w, wn, inp, rows, cols)
         worst[n] = float(np.max(np.abs(g[n].astype(np.float64) - y) / np.maximum(norm, 1e-30)))
-        assert worst[n] <= TOL, f"{n}: normalised error {worst[n]:.3e}"
+        assert worst[n] <= (proj_tol or {}).get(n, TOL), f"{n}: normalised error {worst[n]:.3e}"
     qf = g["qfull"].reshape(Hq, 2 * D)
     rd, sec, base = d["rope_dim"], d["rope_sections"], d["rope_base"]
     qn = oracle.rms_norm_rows(qf[:, :D].reshape(-1), vec["q_norm"], D, eps).reshape(Hq, D)
