@@ -28,7 +28,7 @@ namespace oq {
 namespace {
 
 constexpr const char* kKnobNames[kKnobCount] = {
-    "OQ_GEMM_SPLITS",   "OQ_GEMM_EXACT_DEQUANT", "OQ_GEMM_WS",     "OQ_GEMV_MAX_WG",   "OQ_Q8_0_ROWS",
+    "OQ_GEMM_SPLITS",   "OQ_GEMM_FAST_DEQUANT",  "OQ_GEMM_WS",     "OQ_GEMV_MAX_WG",   "OQ_Q8_0_ROWS",
     "OQ_GEMV_WG_PER_CU", "OQ_STREAM_WG_PER_CU",  "OQ_GEMV_STREAM", "OQ_STREAM_WAVES",  "OQ_GEMV_STREAM_MT",
     "OQ_GEMV_ROWS",     "OQ_GEMV_WAVES",         "OQ_GEMV_ROWS_MT", "OQ_BLOCK_STREAM", "OQ_BLOCK_FUSED",
     "OQ_GEMM_MFMA",     "OQ_FUSED_QUANT",        "OQ_GEMM_INT8",   "OQ_ATTN_WG_PER_CU", "OQ_ATTN_MIN_CHUNK",

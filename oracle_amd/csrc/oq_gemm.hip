@@ -7,9 +7,10 @@
 // 64.7 us at M = 512, 4096 x 12288).  gemm_kq_kernel, whose load waves convert each step's weights
 // into an f16 B tile in LDS, stays selectable (q4_K through it: 80.6 us).  Both operands are
 // rounded once to binary16 and multiplied on v_mfma_f32_32x32x16_f16 with F32 accumulation.  The
-// rounding is relative 2^-11 per operand; over K >= 4096 terms its effect on an output stays below
-// 1e-4 * sum_k |w_k * xhat_k| with a wide margin (checked by the parity tests), so the path is
-// enabled only for K >= 4096.
+// rounding is relative 2^-11 per operand, so each product is within about 2^-10 of itself and an
+// output within 2^-10 * sum_k |w_k * xhat_k| (plus F32 summation) whatever the data; over
+// K >= 4096 terms that spread over many products the effect stays below 1e-4 of that sum with a
+// wide margin (checked by the parity tests), so the path is enabled only for K >= 4096.
 // Every kernel of a weight type forms the same f16 operands and adds the products in the same
 // order, so they agree bit for bit.
 //
@@ -23,10 +24,14 @@
 //   3. with more than one K-split, partial tiles go to scratch and a reduction kernel adds
 //      them in split order (deterministic).
 //
-// Weight dequantization (FAST, K >= 8192): a quant pair becomes exact f16 integers (a nibble read
-// as fp8 e4m3 and converted with scale 2^9; a 5- or 6-bit value by a byte permute under the f16
-// exponent of 1024, minus 1024) and one packed f16 fma applies the f16-rounded scale and min.
-// Below K = 8192 the scale and min are applied in F32 and the result rounded to f16 once.  The
+// Weight dequantization: a quant pair becomes exact f16 integers (a nibble read as fp8 e4m3 and
+// converted with scale 2^9; a 5- or 6-bit value by a byte permute under the f16 exponent of 1024,
+// minus 1024), and each weight is the F32 (d*sc)*q - dmin*m of the reference's F32 scale and min
+// rounded once to f16 (v_fma_mixlo_f16 / v_fma_mixhi_f16, two per pair).  OQ_GEMM_FAST_DEQUANT=1
+// (K >= 8192, measurement only) applies f16-rounded scale and min with one packed f16 fma per
+// pair instead: about 5% faster on q4_K, but a weight that is the small difference of its scale
+// and min terms then carries an error relative to those terms, not to itself, which breaks the
+// bound above (9e-3 of sum |w * xhat| measured on a row dominated by a few products).  The
 // conversion instructions are interleaved with the MFMAs, which execute asynchronously.
 #include <algorithm>
 #include <type_traits>
@@ -46,10 +51,7 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 constexpr int kBM = 128, kBN = 256, kBK = 64;
 constexpr int kThreads = 256;       // 4 waves, one per SIMD
 constexpr uint64_t kMinK = 4096;
-// From this K on, weights are dequantized with packed f16 arithmetic (scale and min rounded to
-// f16 per sub-block); below it, from F32.  The extra rounding roughly 1.3x the output error,
-// which the longer sums absorb: worst normalised errors measured 3.7e-5 at K = 8192 and 3.3e-5
-// at K = 12288 against the 1e-4 bar.
+// OQ_GEMM_FAST_DEQUANT=1 applies from this K on (scale and min rounded to f16 per sub-block).
 constexpr uint64_t kFastMinK = 8192;
 constexpr int kMaxSplits = 8;
 
@@ -350,23 +352,30 @@ OQ_DEVICE uint32_t nib_word(uint4 q, int half) {
     return (KS & 1) ? (d >> 4) & 0x0F0F0F0Fu : d & 0x0F0F0F0Fu;
 }
 
+// f16(fma(x_i, a, c)) for both halves of x (exact f16 integers): the F32 fma of an f16 operand
+// converted to f16, which is one v_fma_mixlo_f16 / v_fma_mixhi_f16 each (x stays packed, no
+// widening instructions).
+OQ_DEVICE uint32_t mix_pair(half2v x, float a, float c) {
+    const half2v r = {(_Float16)__builtin_fmaf((float)x[0], a, c), (_Float16)__builtin_fmaf((float)x[1], a, c)};
+    return __builtin_bit_cast(uint32_t, r);
+}
+
 // Two weights of a B operand from bytes 2p, 2p+1 of a nibble word.  A byte q in 0..15 read as
 // an fp8 e4m3 pattern is q * 2^-9 (subnormal or the first binade), so the scaled fp8 conversion
 // with scale 2^9 yields q exactly, two per instruction.
 //   FAST : one v_pk_fma_f16 with {d*sc, -(dmin*m)}: f16(d*sc*q - dmin*m) from the f16-rounded
 //          scale and min, one rounding;
-//   exact: F32 fma with the reference's F32 scale and min, then one rounding to f16.
+//   exact: the F32 fma with the reference's F32 scale and min, rounded to f16 (mix_pair).
 template <bool FAST, int P>
 OQ_DEVICE uint32_t weight_pair(uint32_t nib, const ScaleT<FAST>& s) {
+    const half2v x = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(nib, 512.0f, P != 0);
     if constexpr (FAST) {
-        const half2v x = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(nib, 512.0f, P != 0);
         const half2v sv = __builtin_bit_cast(half2v, s.v);
         const half2v r = __builtin_elementwise_fma(x, __builtin_shufflevector(sv, sv, 0, 0),
                                                    __builtin_shufflevector(sv, sv, 1, 1));
         return __builtin_bit_cast(uint32_t, r);
     } else {
-        const float2v f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(nib, 512.0f, P != 0);
-        return pack_f16(__builtin_fmaf(f.x, s.ds, -s.dm), __builtin_fmaf(f.y, s.ds, -s.dm));
+        return mix_pair(x, s.ds, -s.dm);
     }
 }
 
@@ -392,26 +401,25 @@ OQ_DEVICE uint32_t q5_pair(uint32_t q, const ScaleT<FAST>& s) {
                                                    __builtin_shufflevector(sv, sv, 1, 1));
         return __builtin_bit_cast(uint32_t, r);
     } else {
-        const float a = (float)((q >> (16 * P)) & 0xFFu), b = (float)((q >> (16 * P + 8)) & 0xFFu);
-        return pack_f16(__builtin_fmaf(a, s.ds, -s.dm), __builtin_fmaf(b, s.ds, -s.dm));
+        const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        return mix_pair(f16_1024_pair<P>(q) - k1024, s.ds, -s.dm);
     }
 }
 
 // Two weights of a q6_K sub-block from the word of 6-bit codes u (q = u - 32): (d sc) q.
 //   FAST : ds = f16(d * sc) (d * sc is exact in F32), x = q exactly, one v_pk_mul_f16;
-//   exact: F32 (d * sc) * q as the reference, rounded to f16.
+//   exact: F32 (d * sc) * q as the reference (exact in F32), rounded to f16; the F32 product is
+//          formed as fma(q, d * sc, +0), so a zero weight is +0 whatever the sign of the scale.
 template <bool FAST, int P>
 OQ_DEVICE uint32_t q6_pair(uint32_t u, float ds) {
+    const half2v k1056 = {(_Float16)1056.0f, (_Float16)1056.0f};
+    const half2v x = f16_1024_pair<P>(u) - k1056;  // exact integers -32..31
     if constexpr (FAST) {
-        const half2v k1056 = {(_Float16)1056.0f, (_Float16)1056.0f};
-        const half2v x = f16_1024_pair<P>(u) - k1056;  // exact integers -32..31
         const _Float16 h = (_Float16)ds;
         const half2v dv = {h, h};
         return __builtin_bit_cast(uint32_t, x * dv);
     } else {
-#pragma clang fp contract(off)
-        const float a = (float)((int)((u >> (16 * P)) & 0xFFu) - 32), b = (float)((int)((u >> (16 * P + 8)) & 0xFFu) - 32);
-        return pack_f16(ds * a, ds * b);
+        return mix_pair(x, ds, 0.0f);
     }
 }
 
@@ -1813,7 +1821,7 @@ hipError_t launch_gemm_mfma(const DeviceMatrix& w, int m, const float* x, const 
         hipLaunchKernelGGL(q8k_to_f16_kernel, dim3((unsigned)m), dim3(64 * kRowWaves), 0, s, q8k, nb, a16, rexp);
     }
     const unsigned wgs = p.tiles_n * p.tiles_m * p.splits;
-    const bool fast = w.k >= kFastMinK && knob(kGemmExactDequant, 0) == 0;
+    const bool fast = w.k >= kFastMinK && knob(kGemmFastDequant, 0) != 0;
     if (w.type == 8) {
         // launched above
     } else if (knob(kGemmWs, 1) == 2) {

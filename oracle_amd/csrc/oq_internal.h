@@ -40,7 +40,7 @@ struct ArgmaxPart;  // one slice's greedy-token result (below)
 // again by oq_reload_options(); never per launch.
 enum Knob : int {
     kGemmSplits,  // OQ_GEMM_SPLITS
-    kGemmExactDequant,  // OQ_GEMM_EXACT_DEQUANT
+    kGemmFastDequant,  // OQ_GEMM_FAST_DEQUANT: 1 rounds the q4_K / q5_K / q6_K scales and mins to f16 before the weights (K >= 8192; measurement only, outside the precision contract)
     kGemmWs,  // OQ_GEMM_WS: 1 (default) weights converted in the MFMA waves (q4_K, q5_K), 0 the four-wave kernel (q4_K), 2 converted by the load waves (every type; q6_K always)
     kGemvMaxWg,  // OQ_GEMV_MAX_WG
     kQ80Rows,  // OQ_Q8_0_ROWS

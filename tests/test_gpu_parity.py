@@ -312,6 +312,39 @@ def test_matrix_cores_extreme_activation_scales(ctx, t, env):
     w.release()
 
 
+@pytest.mark.parametrize("t", [12, 13, 14])
+@pytest.mark.parametrize("cols", [8192, 12288])
+@pytest.mark.parametrize("env", [{}, {"OQ_GEMM_WS": "2"}])
+def test_matrix_cores_bound_on_dominated_rows(ctx, t, cols, env):
+    """Rows that a few products dominate, at the long K of down projections: a saturated SwiGLU
+    output silu(g) * u with gate values N(-200, 80) (at least -85), rows of log-normal magnitudes
+    (log-scale deviations 10 and 20) and a row with one non-zero element per block, so that one
+    element leads each Q8_K block by a wide factor and a few blocks lead the row.  Every output
+    stays within the path's bound, about 2^-10 of sum |w xhat| (1.5e-3 here: 2^-10 plus
+    binary16-subnormal weights and F32 summation; an ideal one-rounding product reaches 2e-4 to
+    7e-4 on these rows).  Each weight is the reference's F32 value rounded once to f16: rounding
+    the q4_K / q5_K scale and min to f16 first puts the error of a weight that is the small
+    difference of its two terms relative to those terms, which such rows expose."""
+    rng = np.random.default_rng(7100 + t + cols)
+    m, rows = 16, 256
+    data = synth.weights(t, rng, rows, cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    g = np.maximum(rng.normal(-200.0, 80.0, cols), -85.0)
+    x[0] = (g / (1.0 + np.exp(-g)) * rng.standard_normal(cols) * 100.0).astype(np.float32)
+    for r, s in ((1, 10.0), (2, 20.0)):
+        x[r] = (np.exp(np.clip(s * rng.standard_normal(cols), -80.0, 60.0)) * rng.standard_normal(cols)).astype(np.float32)
+    x[3] = 0.0
+    x[3, np.arange(0, cols, 256) + rng.integers(0, 256, cols // 256)] = rng.standard_normal(cols // 256)
+    w = ctx.upload(t, cols, rows, data)
+    with oracle_amd.launch_options(env):
+        y = gpu_matmul(ctx, w, x, rows)
+    y_ref, norm = reference_products(t, rows, cols, data, x)
+    for r in range(4):
+        check_close(y[r:r + 1], y_ref[r:r + 1], norm[r:r + 1], tol=1.5e-3)
+    check_close(y[4:], y_ref[4:], norm[4:])
+    w.release()
+
+
 @pytest.mark.parametrize("m,rows,cols,splits", [(70, 520, 8192, None), (16, 33, 4096, None), (130, 300, 4096, "3"),
                                                 (40, 257, 12288, "1"), (33, 64, 8192, "8")])
 def test_q8_0_matrix_cores(ctx, m, rows, cols, splits):
