@@ -217,12 +217,15 @@ int oq_matvec_q8k(oq_context* ctx, const oq_weight* w, const void* q8k_dev, floa
    multi-token evaluation is M independent matvecs (src/runtime/qwen35_target_multi.cpp:14-25),
    which is the semantics here.  Small m streams the weights once with register reuse;
    m >= 16 on q4_K, q5_K and q6_K with K >= 4096 uses matrix cores: both operands rounded once
-   to f16 (weights decoded as the reference, Q8_K activations dequantized), F32 accumulation.
-   Each product is then off by at most about 2^-10 of itself, so an output is within 2^-10 of
-   sum |w * xhat| (plus F32 summation) always, and within the product bar (1e-4 of it) when the
-   sum spreads over many products (N(0,1)-like rows: 2.4e-5 to 4.3e-5 measured); a row dominated
-   by a few products can exceed 1e-4.  OQ_GEMM_MFMA=0 (read by oq_reload_options) sends every m
-   to the integer-dot path instead (exact products, F32 scales).  Each activation row is scaled by
+   to f16 (each weight the reference's F32 decoded value, Q8_K activations dequantized), F32
+   accumulation.  Each product is then off by at most about 2^-10 of itself (a weight below
+   2^-14 in magnitude, binary16's subnormal range, by at most 2^-25 absolute), so an output is
+   within about 2^-10 of sum |w * xhat| (plus F32 summation) whatever the data, and within the
+   product bar (1e-4 of it) when the sum spreads over many products (N(0,1)-like rows: 2.4e-5 to
+   4.3e-5 measured); a row led by a few products exceeds 1e-4 (up to 7e-4 measured on saturated
+   SwiGLU outputs).  OQ_GEMM_MFMA=0 (read by oq_reload_options) sends every m to the integer-dot
+   path instead (exact products, F32 scales).  OQ_GEMM_FAST_DEQUANT=1 (measurement only) rounds
+   the scales and mins to f16 first, which voids the per-product bound for q4_K / q5_K.  Each activation row is scaled by
    a power of two into binary16's range before the rounding and scaled back in the output, so any
    finite activation magnitude is accepted.  Weights must decode inside binary16's range
    (|(d sc) q - dmin m| <= 65504, i.e. d <= 69 for q4_K / q5_K; GGUF checkpoints store d as f16 and
@@ -333,7 +336,9 @@ int oq_rope(oq_context* ctx, float* heads_dev, uint64_t n_heads, uint64_t head_d
    and merged with the usual max rescaling: outputs agree with the reference within 1e-4 of
    sum_t p_t |v_t| (the reference sums doubles for the dot products and the denominator).  A
    non-finite score yields non-finite outputs where the reference throws.  Device path limits:
-   key_dim == value_dim in {64, 128, 256}, q_heads / kv_heads <= 8; else OQ_INVALID_ARGUMENT.
+   key_dim == value_dim in {64, 128, 256}, q_heads / kv_heads <= 256; else OQ_INVALID_ARGUMENT.
+   Up to 8 query heads per KV head read each cached row once per step; a larger group runs as
+   equal subgroups of at most 8 heads (16: two of 8), each reading the group's rows.
    The cache must belong to ctx, and the step is refused while ctx's stream is being captured
    (OQ_INVALID_ARGUMENT; both apply to oq_attention_block_step too). */
 int oq_attention_step(oq_context* ctx, const float* q_dev, uint64_t q_heads, const float* k_dev,

@@ -1107,12 +1107,12 @@ int attention_shape(oq_context* ctx, const oq_kv_cache* c, uint64_t q_heads, oq:
     const uint64_t rep = q_heads / c->kv_heads;
     if (c->key_dim != c->value_dim || !oq::attention_dims_supported(c->key_dim, rep)) {
         return fail(ctx, OQ_INVALID_ARGUMENT,
-                    "attention device path needs key_dim == value_dim in {64, 128, 256} and at most 8 query heads per "
+                    "attention device path needs key_dim == value_dim in {64, 128, 256} and at most 256 query heads per "
                     "KV head");
     }
     const uint64_t T = c->length + 1 + ahead;  // the token `ahead` places after the next one to append
     uint32_t chunk = 0, nchunks = 0;
-    oq::attention_plan(T, c->kv_heads, chunk, nchunks);
+    oq::attention_plan(T, c->kv_heads, rep, chunk, nchunks);
     if (nchunks > oq::kAttnMaxChunks || T > 0xFFFFFFFFull || c->kv_heads > 0xFFFF) {
         return fail(ctx, OQ_INVALID_ARGUMENT, "attention device path supports at most 8388608 cached tokens");
     }

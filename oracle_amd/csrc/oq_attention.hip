@@ -2,9 +2,12 @@
 // single-token GQA attention over an F32 KV cache in HBM.
 //
 // Attention (reference_kernels.cpp:127-195) is split over the token axis, flash-decoding style:
-//   chunk kernel   one workgroup per (KV head g, chunk of tokens), 4 waves.  All rep = q_heads /
-//                  kv_heads query heads of g share each key and value row, so K and V are read
-//                  from HBM once per step whatever the group size.
+//   chunk kernel   one workgroup per (KV head g, subgroup, chunk of tokens), 4 waves.  The
+//                  query heads of g (q_heads / kv_heads of them) share each key and value row; up
+//                  to 8 of them are one subgroup, whose workgroups hold every head's query slices
+//                  in registers, so K and V are read from HBM once per step for groups of up to
+//                  8 heads.  A larger group is split into equal subgroups of at most 8 heads
+//                  (16 heads: two of 8; 12: two of 6), each reading the group's rows again.
 //                  scores: 16 lanes per token, each lane holding D/16 key values (four 16-lane
 //                    groups per wave, 256 contiguous bytes per group and load); the rep query
 //                    heads' matching slices sit in registers; F32 products reduced over the 16
@@ -53,9 +56,11 @@ struct ChunkArgs {
     const float* new_k;   // [Hkv][D] or null
     const float* new_v;
     uint32_t T, Hkv, rep, chunk, nchunks;
+    uint32_t rep_all;     // query heads per KV head
+    uint32_t nsub;        // subgroups per KV head, of rep = rep_all / nsub query heads each
     float scale;
-    float* part_o;        // [Hkv][rep][D/64][nchunks][64]: one head slice's chunks contiguous
-    float* part_ml;       // [Hkv][rep][nchunks][2]
+    float* part_o;        // [Hq][D/64][nchunks][64]: one head slice's chunks contiguous
+    float* part_ml;       // [Hq][nchunks][2]
     // the block's preparation (PREP kernels); new_k is null and new_v the value projection
     const float* qfull;   // [Hq][2D]: query values, then the output gate
     const float* kp;      // [Hkv][D] key projection
@@ -63,15 +68,15 @@ struct ChunkArgs {
     const float* k_norm;  // [D]
     float eps;
     RopeParams rope;
-    float* qcur;          // [Hq][D], written by each KV head's chunk 0
-    float* kcur;          // [Hkv][D], written by the chunk holding the new token
+    float* qcur;          // [Hq][D], written by each subgroup's chunk 0
+    float* kcur;          // [Hkv][D], written by subgroup 0's chunk holding the new token
     uint32_t stage;       // float offset of the preparation's LDS: [rep + 1][D] rows, cos/sin [2][128]
 };
 
 struct MergeArgs {
     const float* part_o;
     const float* part_ml;
-    uint32_t Hkv, rep, nchunks;
+    uint32_t nchunks;
     float* out;           // [Hq][D]
     const float* gate;    // gate of head h at gate + h * gate_stride, or null
     uint32_t gate_stride;
@@ -158,8 +163,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
     extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t g = blockIdx.x / a.nchunks;
-    const uint32_t c = blockIdx.x - g * a.nchunks;
+    const uint32_t grp = blockIdx.x / a.nchunks;  // (KV head, subgroup)
+    const uint32_t c = blockIdx.x - grp * a.nchunks;
+    const uint32_t g = grp / a.nsub, sub = grp - g * a.nsub;
+    const uint64_t h0 = (uint64_t)g * a.rep_all + (uint64_t)sub * a.rep;  // the subgroup's first query head
     const uint32_t c0 = c * a.chunk;
     const uint32_t c1 = min(c0 + a.chunk, a.T);
     const uint32_t n = c1 - c0;
@@ -176,8 +183,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
         return a.values + ((uint64_t)t * a.Hkv + g) * D;
     };
 
-    // the append: the chunk holding the new token stores its key and value row
-    if (a.new_k != nullptr && c1 == a.T) {
+    // the append: subgroup 0's chunk holding the new token stores its key and value row
+    if (a.new_k != nullptr && c1 == a.T && sub == 0) {
         for (uint32_t i = threadIdx.x; i < (uint32_t)D; i += kAttnThreads) {
             a.keys[((uint64_t)last * a.Hkv + g) * D + i] = a.new_k[(uint64_t)g * D + i];
             a.values[((uint64_t)last * a.Hkv + g) * D + i] = a.new_v[(uint64_t)g * D + i];
@@ -201,7 +208,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
             const uint32_t row = (uint32_t)wave + (uint32_t)r * kAttnWaves;
             if (row < prep_rows) {
                 const bool is_q = row < rep;
-                const float* src = is_q ? a.qfull + ((uint64_t)g * rep + row) * 2 * D : a.kp + (uint64_t)g * D;
+                const float* src = is_q ? a.qfull + (h0 + row) * 2 * D : a.kp + (uint64_t)g * D;
                 const float* w = is_q ? a.q_norm : a.k_norm;
                 Vec<VW>::unpack(*reinterpret_cast<const VT*>(src + lane * VW), px[r]);
 #pragma unroll
@@ -212,7 +219,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
 #pragma unroll
         for (int h = 0; h < REP; ++h) {
             const uint32_t hh = (uint32_t)h < rep ? (uint32_t)h : 0u;
-            const float4* qp = reinterpret_cast<const float4*>(a.q + ((uint64_t)g * rep + hh) * D);
+            const float4* qp = reinterpret_cast<const float4*>(a.q + (h0 + hh) * D);
 #pragma unroll
             for (int j = 0; j < NV; ++j) qr[h][j] = qp[j * 16 + l16];
         }
@@ -254,9 +261,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
             }
             // the trace's copies, and the append of the new key and value rows
             if (c == 0 && a.qcur != nullptr) {
-                for (uint32_t i = threadIdx.x; i < rep * D; i += kAttnThreads) a.qcur[(uint64_t)g * rep * D + i] = stage[i];
+                for (uint32_t i = threadIdx.x; i < rep * D; i += kAttnThreads) a.qcur[h0 * D + i] = stage[i];
             }
-            if (holds_new) {
+            if (holds_new && sub == 0) {
                 for (uint32_t i = threadIdx.x; i < (uint32_t)D; i += kAttnThreads) {
                     const float k = stage[rep * D + i];
                     if (a.kcur != nullptr) a.kcur[(uint64_t)g * D + i] = k;
@@ -342,7 +349,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
         }
         l = wave_sum(l);
         if (lane == 0) {
-            float* ml = a.part_ml + (((uint64_t)g * rep + h) * a.nchunks + c) * 2;
+            float* ml = a.part_ml + ((h0 + h) * a.nchunks + c) * 2;
             ml[0] = m;
             ml[1] = l;
         }
@@ -396,7 +403,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
 #pragma unroll
         for (int w = 1; w < kAttnWaves; ++w) s += red[(uint32_t)w * rep * D + i];
         const uint32_t h = i / D, slice = (i % D) / 64;
-        a.part_o[((((uint64_t)g * rep + h) * (D / 64) + slice) * a.nchunks + c) * 64 + (i % 64)] = s;
+        a.part_o[(((h0 + h) * (D / 64) + slice) * a.nchunks + c) * 64 + (i % 64)] = s;
     }
 }
 
@@ -416,10 +423,9 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
     __shared__ float4 s_o[kMergeGroups][16];
     __shared__ float s_m[kMergeGroups], s_l[kMergeGroups];
     const uint32_t h = blockIdx.x / SLICES, slice = blockIdx.x - h * SLICES;
-    const uint32_t g = h / a.rep, r = h - g * a.rep;
     const int col = threadIdx.x & 15, grp = threadIdx.x >> 4;
-    const float* mlp = a.part_ml + ((uint64_t)g * a.rep + r) * a.nchunks * 2;           // [nchunks][2]
-    const float* op = a.part_o + (((uint64_t)g * a.rep + r) * SLICES + slice) * a.nchunks * 64;  // [nchunks][64]
+    const float* mlp = a.part_ml + (uint64_t)h * a.nchunks * 2;                     // [nchunks][2]
+    const float* op = a.part_o + ((uint64_t)h * SLICES + slice) * a.nchunks * 64;  // [nchunks][64]
     constexpr uint32_t kPass = kMergeGroups * kMergeUnroll;  // chunks per pass of the workgroup
     const uint64_t base = (uint64_t)h * D + slice * 64 + (uint64_t)col * 4;
     // the block's output gate, needed last, requested first
@@ -519,7 +525,7 @@ __global__ __launch_bounds__(256) void rope_kernel(float* heads, uint32_t head_d
 
 template <int D, int REP, int NB, bool ONE>
 hipError_t launch_nb(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
-    const dim3 grid(a.Hkv * a.nchunks);
+    const dim3 grid(a.Hkv * a.nsub * a.nchunks);
     if (a.qfull != nullptr) {
         hipLaunchKernelGGL((attention_chunk_kernel<D, REP, NB, true, ONE>), grid, dim3(kAttnThreads), lds, s, a);
     } else {
@@ -553,13 +559,15 @@ hipError_t launch_d(const AttnLaunch& L, hipStream_t s) {
     a.new_v = L.new_v;
     a.T = L.T;
     a.Hkv = L.Hkv;
-    a.rep = L.rep;
+    a.rep_all = L.rep;
+    a.nsub = attention_subgroups(L.rep);
+    a.rep = L.rep / a.nsub;
     a.chunk = L.chunk;
     a.nchunks = L.nchunks;
     a.scale = L.scale;
     a.part_o = L.part;
     a.part_ml = L.part + (uint64_t)L.Hkv * L.nchunks * L.rep * D;
-    a.stage = std::max(L.rep * L.chunk, (uint32_t)kAttnWaves * L.rep * D);
+    a.stage = std::max(a.rep * L.chunk, (uint32_t)kAttnWaves * a.rep * D);
     uint64_t lds = a.stage;
     if (L.prep != nullptr) {
         const AttnPrep& p = *L.prep;
@@ -574,20 +582,18 @@ hipError_t launch_d(const AttnLaunch& L, hipStream_t s) {
         a.rope = p.rope;
         a.qcur = p.qcur;
         a.kcur = p.kcur;
-        lds += (uint64_t)(L.rep + 1) * D + 256;  // the preparation's rows and cos / sin
+        lds += (uint64_t)(a.rep + 1) * D + 256;  // the preparation's rows and cos / sin
     }
     lds *= sizeof(float);
     hipError_t e;
-    if (L.rep == 1) e = launch_chunks<D, 1>(a, lds, s);
-    else if (L.rep == 2) e = launch_chunks<D, 2>(a, lds, s);
-    else if (L.rep <= 4) e = launch_chunks<D, 4>(a, lds, s);
+    if (a.rep == 1) e = launch_chunks<D, 1>(a, lds, s);
+    else if (a.rep == 2) e = launch_chunks<D, 2>(a, lds, s);
+    else if (a.rep <= 4) e = launch_chunks<D, 4>(a, lds, s);
     else e = launch_chunks<D, 8>(a, lds, s);
     if (e != hipSuccess) return e;
     MergeArgs m{};
     m.part_o = a.part_o;
     m.part_ml = a.part_ml;
-    m.Hkv = L.Hkv;
-    m.rep = L.rep;
     m.nchunks = L.nchunks;
     m.out = L.out;
     m.gate = L.gate;
@@ -606,14 +612,22 @@ hipError_t launch_d(const AttnLaunch& L, hipStream_t s) {
 }  // namespace
 
 bool attention_dims_supported(uint64_t head_dim, uint64_t rep) {
-    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && rep >= 1 && rep <= 8;
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && rep >= 1 && rep <= kAttnMaxRep;
 }
 
-void attention_plan(uint64_t T, uint64_t Hkv, uint32_t& chunk, uint32_t& nchunks) {
-    // about two chunk workgroups per compute unit (OQ_ATTN_WG_PER_CU), chunks a multiple of the
-    // score pass
+uint32_t attention_subgroups(uint32_t rep) {
+    // the fewest equal subgroups of at most 8 query heads (a prime group above 8 becomes single heads)
+    for (uint32_t n = (rep + 7) / 8; n < rep; ++n)
+        if (rep % n == 0) return n;
+    return rep;
+}
+
+void attention_plan(uint64_t T, uint64_t Hkv, uint64_t rep, uint32_t& chunk, uint32_t& nchunks) {
+    // about two chunk workgroups per compute unit (OQ_ATTN_WG_PER_CU) over the (KV head, subgroup)
+    // pairs, chunks a multiple of the score pass
     const uint64_t per_cu = (uint64_t)std::max(1, knob(kAttnWgPerCu, 2));
-    const uint64_t target = std::max<uint64_t>(1, (per_cu * (uint64_t)cu_count()) / std::max<uint64_t>(Hkv, 1));
+    const uint64_t groups = std::max<uint64_t>(Hkv, 1) * attention_subgroups((uint32_t)std::max<uint64_t>(rep, 1));
+    const uint64_t target = std::max<uint64_t>(1, (per_cu * (uint64_t)cu_count()) / groups);
     uint64_t c = (T + target - 1) / target;
     const uint64_t min_chunk = (uint64_t)std::max(1, knob(kAttnMinChunk, (int)kTokStep));
     c = std::max<uint64_t>(c, min_chunk);

@@ -193,8 +193,10 @@ struct AttnLaunch {
     float* gated;
     const AttnPrep* prep;      // or null; when given, q and new_k / new_v are not read
 };
+constexpr uint64_t kAttnMaxRep = 256;  // query heads per KV head
 bool attention_dims_supported(uint64_t head_dim, uint64_t rep);
-void attention_plan(uint64_t T, uint64_t Hkv, uint32_t& chunk, uint32_t& nchunks);
+uint32_t attention_subgroups(uint32_t rep);  // chunk workgroups per (KV head, chunk): rep / subgroups <= 8 heads each
+void attention_plan(uint64_t T, uint64_t Hkv, uint64_t rep, uint32_t& chunk, uint32_t& nchunks);
 uint64_t attention_partial_floats(uint64_t Hkv, uint64_t rep, uint64_t head_dim, uint32_t nchunks);
 constexpr uint32_t kAttnMaxChunks = 8192;
 hipError_t launch_attention(const AttnLaunch& a, hipStream_t s);

@@ -152,9 +152,12 @@ def test_attention_step_matches_reference_fixture(ctx, attn_golden):
         cache.release()
 
 
-# (q_heads, kv_heads, head_dim, tokens after the step): group sizes 1-8, chunk edges, long caches
+# (q_heads, kv_heads, head_dim, tokens after the step): group sizes 1-8, chunk edges, long caches;
+# groups above 8 query heads run as equal subgroups of at most 8: 16 (two of 8), 12 (two of 6),
+# 9 (three of 3), 11 (a prime: eleven single heads)
 CASES = [(8, 2, 256, 1), (8, 2, 256, 17), (16, 4, 256, 4097), (8, 2, 256, 20000), (8, 1, 128, 777),
-         (4, 4, 64, 300), (6, 2, 128, 301), (24, 4, 256, 3000), (16, 2, 256, 50), (16, 4, 256, 65537)]
+         (4, 4, 64, 300), (6, 2, 128, 301), (24, 4, 256, 3000), (16, 2, 256, 50), (16, 4, 256, 65537),
+         (32, 2, 256, 4097), (16, 1, 256, 1), (24, 2, 128, 301), (18, 2, 64, 300), (11, 1, 64, 77)]
 
 
 @pytest.mark.parametrize("hq,hkv,d,T", CASES, ids=[f"h{a}_{b}_d{c}_T{t}" for a, b, c, t in CASES])
@@ -212,6 +215,16 @@ def test_attention_step_errors(ctx):
                 ctx.attention_step(q, 1, k, v, odd, o)
         finally:
             odd.release()
+        one = ctx.kv_cache(4, 1, 64, 64)
+        wide_q, wide_o = ctx.alloc(257 * 64 * 4), ctx.alloc(257 * 64 * 4)
+        try:
+            with pytest.raises(oracle_amd.InvalidArgument, match="at most 256 query heads per KV head"):
+                ctx.attention_step(wide_q, 257, k, v, one, wide_o)
+            assert len(one) == 0
+        finally:
+            one.release()
+            wide_q.free()
+            wide_o.free()
     finally:
         for b in (q, k, v, o):
             b.free()
@@ -353,6 +366,10 @@ BLOCKS = {
     "rep1_d64": (dict(embedding=256, q_heads=4, kv_heads=4, head_dim=64, ffn=512, rope_dim=64,
                       rope_sections=[11, 11, 10, 0], rope_base=1e4, eps=1e-6),
                  dict(q=12, k=12, v=12, out=12, gate=12, up=12, down=14), 47),
+    # 32 query heads over 2 KV heads of 256 (two subgroups of 8 per KV head)
+    "rep16": (dict(embedding=1024, q_heads=32, kv_heads=2, head_dim=256, ffn=1024, rope_dim=64,
+                   rope_sections=[11, 11, 10, 0], rope_base=1e7, eps=1e-6),
+              dict(q=12, k=12, v=12, out=14, gate=12, up=12, down=12), 500),
     # long activation rows: the streamed q / k / v projection walks each row in two units (8192)
     # or three with a partial last one (8448 = 33 super-blocks)
     "e8192": (dict(embedding=8192, q_heads=4, kv_heads=2, head_dim=64, ffn=512, rope_dim=64,

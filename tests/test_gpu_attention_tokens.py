@@ -70,7 +70,7 @@ def run_tokens(ctx, d, w, vec, c, positions, xs, trace=True):
         blk.release()
 
 
-@pytest.mark.parametrize("name,m", [("rep1_d64", 4), ("mixed", 3), ("empty_rep8", 5), ("e2048", 2)])
+@pytest.mark.parametrize("name,m", [("rep1_d64", 4), ("mixed", 3), ("empty_rep8", 5), ("e2048", 2), ("rep16", 3)])
 def test_block_tokens_match_oracle(ctx, name, m):
     d, w, vec, c, xs, positions = inputs(name, m, 9100 + m)
     n0 = c.length
