@@ -84,7 +84,33 @@ def timed_steps(ctx, step, steps, warmup, first=0):
     return ms
 
 
-def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
+def timed_graph(ctx, step, steps, warmup, first, step_bytes):
+    """The K timed steps captured in order into one HIP graph, timed as one launch: the steps'
+    kernels run back to back with no host launch between them (what a profiler's kernel trace
+    then records is the timed configuration).  The graph's first launch (its set-up) is untimed;
+    then eager steps over the copies after the timed range, at least 256 MiB of them (and at
+    least W), so that no timed step reads a copy the Infinity Cache may still hold; then the
+    timed launch."""
+    ctx.sync()
+    ctx.capture_begin()
+    for i in range(steps):
+        step(first + warmup + i)
+    g = ctx.capture_end()
+    try:
+        g.launch()
+        eager = max(warmup, math.ceil((MALL_DEFEAT_BYTES // 2) / max(step_bytes, 1)) + 1)
+        for i in range(eager):
+            step(first + warmup + steps + i)
+        ctx.timer_start()
+        g.launch()
+        ms = ctx.timer_stop()
+        ctx.sync()
+    finally:
+        g.destroy()
+    return ms
+
+
+def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, graph=False):
     t, n, k, m, desc = WORKLOADS[name]
     rng = np.random.default_rng(SEED + list(WORKLOADS).index(name))
     data = synth.weights(t, rng, n, k)
@@ -110,7 +136,7 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES):
     else:
         ctx.matmul(ws[0], m, xb, yb)
     ctx.sync()
-    ms = timed_steps(ctx, step, steps, warmup, first=1)
+    ms = timed_graph(ctx, step, steps, warmup, 1, wb) if graph else timed_steps(ctx, step, steps, warmup, first=1)
     ms_step = ms / steps
     xbytes = m * k * 4
     ybytes = m * n * 4
@@ -374,6 +400,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=1, help="deltanet_block: consecutive tokens per step")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the workload's K steps as one captured HIP graph launch (for kernel traces)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}); the quantized matrix path is "
@@ -429,7 +457,7 @@ def main():
                          "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": committed_traffic("attention_decode")},
             "us_per_step": round(r["us_per_step"], 2)}), flush=True)
         return
-    main_res = run_gpu(ctx, args.workload, args.steps, args.warmup)
+    main_res = run_gpu(ctx, args.workload, args.steps, args.warmup, graph=args.graph)
     secondary = block = block4 = attn = attn_block = None
     configs = {}
     if not args.no_secondary and args.workload == "q4k_gemv":
@@ -472,6 +500,7 @@ def main():
         "data": "synthetic (seeded: weights per workload distributions, x ~ N(0,1))",
         "config": {"workload": desc, "rows": n, "cols": k, "batch": m, "weight_type": TYPE_NAMES[t],
                    "weight_copies_cycled": main_res["copies"], "seed": SEED,
+                   "launch": "one HIP graph of the timed steps" if args.graph else "eager C-ABI calls",
                    "weights_sha256": main_res["weights_sha256"], "x_sha256": main_res["x_sha256"]},
         "roofline": roofline,
         "us_per_gemv": round(main_res["us_per_step"], 3),

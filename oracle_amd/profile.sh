@@ -52,10 +52,32 @@ done
     grep '^{' "$RAW.trace.log" | tail -1 | sed 's/^/#   /'
     python3 -m oracle_amd.profsum stats "$RAW/trace"
 } > "$OUT/${WL}${TAG}_kernel_stats.txt"
+# the blocks' launches are summarised one by one (each kernel and grid of the step)
+PER=""
+case "$WL" in deltanet_block*|attention_block*) PER="--per-kernel" ;; esac
 python3 -m oracle_amd.profsum traffic --kernel "$KERN" --fetch "$RAW/FETCH_SIZE" --write "$RAW/WRITE_SIZE" \
-    --copy-fetch "$RAW/copy_FETCH_SIZE" --copy-write "$RAW/copy_WRITE_SIZE" --copy-bytes $COPY_BYTES \
+    --copy-fetch "$RAW/copy_FETCH_SIZE" --copy-write "$RAW/copy_WRITE_SIZE" --copy-bytes $COPY_BYTES $PER \
     > "$OUT/${WL}${TAG}_traffic.json"
 echo "wrote $OUT/${WL}${TAG}_kernel_stats.txt $OUT/${WL}${TAG}_traffic.json"
+if [ "$WL" = "q4k_gemv" ]; then
+    # the same timed steps with no host launch between them (bench.py --graph): a kernel trace
+    # delays each eager launch by several microseconds, so the GPU idles between the traced
+    # dispatches above; in a graph they run back to back, as in the untraced run
+    GRAPH_CMD="rocprofv3 --kernel-trace --stats --output-format csv -d $RAW/graph -o run -- python3 bench.py --workload $WL --steps 20 --warmup 5 --no-cpu --no-secondary --graph"
+    echo "trace: $GRAPH_CMD"
+    timeout -k 10 300 $GRAPH_CMD > "$RAW.graph.log" 2>&1
+    {
+        echo "# rocprofv3 kernel statistics, workload $WL, timed steps as one HIP graph launch"
+        echo "# recipe: bash oracle_amd/profile.sh $WL '$KERN' <out>"
+        echo "# command: (cd \$REPO && ${GRAPH_CMD//$OUT/<out>})   (<out>: the OUT argument)"
+        echo "# bench line of that run:"
+        grep '^{' "$RAW.graph.log" | tail -1 | sed 's/^/#   /'
+        python3 -m oracle_amd.profsum stats "$RAW/graph"
+        echo "# the timed graph launch's dispatches of the matching kernel (the last K of them):"
+        python3 -m oracle_amd.profsum dispatches --kernel "$KERN" --last 20 "$RAW/graph"
+    } > "$OUT/${WL}_graph_kernel_stats.txt"
+    echo "wrote $OUT/${WL}_graph_kernel_stats.txt"
+fi
 if [ "${4:-}" = "mfma" ]; then
     P1="SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_I8 GRBM_GUI_ACTIVE SQ_INSTS_MFMA SQ_INSTS_VALU SQ_WAVE_CYCLES"
     P2="SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_LDS SQ_WAIT_INST_LDS SQ_LDS_DATA_FIFO_FULL SQ_LDS_CMD_FIFO_FULL SQ_WAIT_ANY SQ_ACTIVE_INST_VALU SQ_VALU_MFMA_COEXEC_CYCLES"
