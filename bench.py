@@ -220,21 +220,22 @@ def run_deltanet(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, tokens=
 ATTN_GEOMETRY = dict(q_heads=16, kv_heads=4, head_dim=256, tokens=32768)
 
 
-def run_attention(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, **geometry):
+def run_attention(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, kv_dtype="f32", **geometry):
     """Single-token GQA attention (oq_attention_step): 16 query heads over 4 KV heads of 256 with
-    32768 tokens cached (F32 keys and values, 256 MiB); steps cycle over caches totalling >= 512
-    MiB.  Each step appends one token; the cache is truncated back (host-side bookkeeping only)
-    so every step attends over the same number of tokens."""
+    32768 tokens cached (F32 keys and values, 256 MiB; an F16 cache, kv_dtype "f16", 128 MiB);
+    steps cycle over caches totalling >= 512 MiB.  Each step appends one token; the cache is
+    truncated back (host-side bookkeeping only) so every step attends over the same number of
+    tokens."""
     g = dict(ATTN_GEOMETRY, **geometry)
     hq, hkv, d, T = g["q_heads"], g["kv_heads"], g["head_dim"], g["tokens"]
     rng = np.random.default_rng(SEED + 200)
-    kv_bytes = 2 * T * hkv * d * 4
+    kv_bytes = 2 * T * hkv * d * (2 if kv_dtype == "f16" else 4)
     ncopies = max(1, math.ceil(copies_min_bytes / kv_bytes))
     keys = rng.standard_normal((T, hkv, d)).astype(np.float32)
     values = rng.standard_normal((T, hkv, d)).astype(np.float32)
     caches = []
     for _ in range(ncopies):
-        c = ctx.kv_cache(T + 1, hkv, d, d)
+        c = ctx.kv_cache(T + 1, hkv, d, d, dtype=kv_dtype)
         c.load(keys, values, T - 1)
         caches.append(c)
     del keys, values
@@ -398,6 +399,7 @@ def main():
                     choices=sorted(WORKLOADS) + ["copy_calibration", "deltanet_block", "attention_decode",
                                                  "attention_block"])
     ap.add_argument("--tokens", type=int, default=1, help="deltanet_block: consecutive tokens per step")
+    ap.add_argument("--kv", choices=["f32", "f16"], default="f32", help="attention_decode: KV cache element type")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--graph", action="store_true",
@@ -444,21 +446,22 @@ def main():
             "us_per_block": round(r["us_per_block"], 2), "hbm_frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
         return
     if args.workload == "attention_decode":
-        r = run_attention(ctx, args.steps, args.warmup)
+        r = run_attention(ctx, args.steps, args.warmup, kv_dtype=args.kv)
         ctx.close()
         print(json.dumps({
             "metric": "GQA decode attention GB/s of KV cache", "value": round(r["gbs"], 2), "unit": "GB/s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32" if args.kv == "f32" else "f32 (f16 cache)",
             "data": "synthetic (keys, values, k, v ~ N(0,1), q ~ N(0,4))",
-            "config": {"workload": "single-token GQA attention over an F32 KV cache", **r["geometry"],
-                       "kv_bytes": r["kv_bytes"], "caches_cycled": r["copies"]},
+            "config": {"workload": f"single-token GQA attention over an {args.kv.upper()} KV cache", **r["geometry"],
+                       "kv_bytes": r["kv_bytes"], "caches_cycled": r["copies"], "kv_element": args.kv},
             "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": committed_traffic("attention_decode")},
+                         "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                         "traffic": committed_traffic("attention_decode" if args.kv == "f32" else "attention_decode_f16")},
             "us_per_step": round(r["us_per_step"], 2)}), flush=True)
         return
     main_res = run_gpu(ctx, args.workload, args.steps, args.warmup, graph=args.graph)
-    secondary = block = block4 = attn = attn_block = None
+    secondary = block = block4 = attn = attn16 = attn_block = None
     configs = {}
     if not args.no_secondary and args.workload == "q4k_gemv":
         secondary = run_gpu(ctx, "q4k_down_m512", max(5, args.steps // 4), max(2, args.warmup // 5))
@@ -468,6 +471,7 @@ def main():
         block = run_deltanet(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
         block4 = run_deltanet(ctx, max(5, args.steps // 10), max(2, args.warmup // 5), tokens=4)
         attn = run_attention(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
+        attn16 = run_attention(ctx, max(5, args.steps // 10), max(2, args.warmup // 5), kv_dtype="f16")
         attn_block = run_attention_block(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
     ctx.close()
 
@@ -542,6 +546,9 @@ def main():
     if attn is not None:
         out["attention_decode"] = {"us": round(attn["us_per_step"], 2), "kv_gbs": round(attn["gbs"], 1),
                                    "hbm_frac": round(attn["gbs"] / HBM_PEAK_GBS, 4), **attn["geometry"]}
+    if attn16 is not None:
+        out["attention_decode_f16_cache"] = {"us": round(attn16["us_per_step"], 2), "kv_gbs": round(attn16["gbs"], 1),
+                                             "hbm_frac": round(attn16["gbs"] / HBM_PEAK_GBS, 4), **attn16["geometry"]}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.workload)
     print(json.dumps(out), flush=True)

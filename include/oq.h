@@ -300,6 +300,16 @@ int oq_deltanet_steps(oq_context* ctx, const oq_deltanet_block* block, uint64_t 
 typedef struct oq_kv_cache oq_kv_cache;
 int oq_kv_cache_create(oq_context* ctx, uint64_t capacity, uint64_t kv_heads, uint64_t key_dim,
                        uint64_t value_dim, oq_kv_cache** out);
+/* No counterpart in the reference (its cache is F32): a cache whose key and value elements are of
+   `type`, OQ_TYPE_F32 (as oq_kv_cache_create) or OQ_TYPE_F16 (binary16: half the bytes that every
+   attention step reads).  An F16 cache stores each appended or loaded F32 element rounded to
+   nearest even, and attention steps read what is stored, the new token's row included: their
+   outputs are attention over the rounded rows, within the same bound as over an F32 cache, and
+   differ from an F32 cache's by that rounding (relative 2^-11 per element).  Other types ->
+   OQ_INVALID_ARGUMENT ("KV cache element type must be F32 or F16"); then as oq_kv_cache_create. */
+int oq_kv_cache_create_typed(oq_context* ctx, uint64_t capacity, uint64_t kv_heads, uint64_t key_dim,
+                             uint64_t value_dim, uint32_t type, oq_kv_cache** out);
+uint32_t oq_kv_cache_type(const oq_kv_cache* cache);  /* OQ_TYPE_F32 or OQ_TYPE_F16; 0 for NULL */
 void oq_kv_cache_release(oq_kv_cache* cache);
 uint64_t oq_kv_cache_size(const oq_kv_cache* cache);      /* KvCache::size */
 uint64_t oq_kv_cache_capacity(const oq_kv_cache* cache);  /* KvCache::capacity */
@@ -310,9 +320,13 @@ int oq_kv_cache_reset(oq_kv_cache* cache);
 int oq_kv_cache_truncate(oq_kv_cache* cache, uint64_t new_length);
 /* No counterpart in the reference (its cache only grows by append): stores `length` token rows
    [length][kv_heads][dim] from host memory and sets the length, e.g. to resume from keys and
-   values computed elsewhere.  length > capacity -> OQ_OVERFLOW ("KV cache capacity exceeded"). */
+   values computed elsewhere.  length > capacity -> OQ_OVERFLOW ("KV cache capacity exceeded").
+   The rows are F32 for either element type; an F16 cache rounds them on the device (through a
+   staging buffer of at most 64 MiB, allocated for the call). */
 int oq_kv_cache_load(oq_kv_cache* cache, const float* keys_host, const float* values_host, uint64_t length);
-/* the device arrays (row t, head h of keys at keys_dev + (t * kv_heads + h) * key_dim) */
+/* the device arrays (row t, head h of keys at element (t * kv_heads + h) * key_dim), of the
+   cache's element type: F32, or binary16 for an F16 cache (the pointers then address 2-byte
+   elements) */
 int oq_kv_cache_arrays(const oq_kv_cache* cache, float** keys_dev, float** values_dev);
 
 /* oracle::runtime::apply_qwen35_rope (src/runtime/reference_kernels.cpp:77-125) on

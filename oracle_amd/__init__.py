@@ -291,10 +291,15 @@ class Context:
                    x.ptr, y.ptr, trace.ptr if trace is not None else None)
 
     # timing / graphs
-    def kv_cache(self, capacity: int, kv_heads: int, key_dim: int, value_dim: int) -> "KvCache":
-        """A device KV cache (oq_kv_cache_create)."""
+    def kv_cache(self, capacity: int, kv_heads: int, key_dim: int, value_dim: int, dtype: str = "f32") -> "KvCache":
+        """A device KV cache (oq_kv_cache_create); dtype "f16" stores binary16 elements
+        (oq_kv_cache_create_typed)."""
+        types = {"f32": 0, "f16": 1}
+        if dtype not in types:
+            raise InvalidArgument(f"KV cache dtype must be one of {sorted(types)}")
         h = C.c_void_p()
-        self._call(self.lib.oq_kv_cache_create, self.h, capacity, kv_heads, key_dim, value_dim, C.byref(h))
+        self._call(self.lib.oq_kv_cache_create_typed, self.h, capacity, kv_heads, key_dim, value_dim, types[dtype],
+                   C.byref(h))
         return KvCache(self, h.value)
 
     def rope(self, heads: DeviceBuffer, n_heads: int, head_dim: int, rotary_dim: int, sections, base: float,
@@ -442,12 +447,13 @@ class DeltaNetBlockWeights:
 
 class KvCache:
     """A device KV cache in the reference's layout (oq_kv_cache): keys [capacity][kv_heads][key_dim],
-    values [capacity][kv_heads][value_dim], F32 in HBM."""
+    values [capacity][kv_heads][value_dim], F32 (or binary16 for an F16 cache) in HBM."""
 
     def __init__(self, ctx: Context, handle: int):
         self.ctx = ctx
         self.h = handle
         self.capacity = int(ctx.lib.oq_kv_cache_capacity(handle))
+        self.dtype = np.float16 if int(ctx.lib.oq_kv_cache_type(handle)) == 1 else np.float32
         k, v = C.c_void_p(), C.c_void_p()
         ctx._call(ctx.lib.oq_kv_cache_arrays, handle, C.byref(k), C.byref(v))
         self.keys_ptr, self.values_ptr = k.value, v.value
@@ -463,13 +469,13 @@ class KvCache:
 
     def _view(self, ptr: int, width: int) -> DeviceBuffer:
         b = DeviceBuffer.__new__(DeviceBuffer)  # a view: never freed through this object
-        b.ctx, b.ptr, b.nbytes = self.ctx, ptr, self.capacity * width * 4
+        b.ctx, b.ptr, b.nbytes = self.ctx, ptr, self.capacity * width * np.dtype(self.dtype).itemsize
         return b
 
     def download(self, kv_heads: int, key_dim: int, value_dim: int) -> tuple[np.ndarray, np.ndarray]:
-        """(keys, values) as [capacity][kv_heads][dim] arrays."""
-        kb = self._view(self.keys_ptr, kv_heads * key_dim).download(np.float32)
-        vb = self._view(self.values_ptr, kv_heads * value_dim).download(np.float32)
+        """(keys, values) as F32 [capacity][kv_heads][dim] arrays (an F16 cache's elements widened)."""
+        kb = self._view(self.keys_ptr, kv_heads * key_dim).download(self.dtype).astype(np.float32)
+        vb = self._view(self.values_ptr, kv_heads * value_dim).download(self.dtype).astype(np.float32)
         return kb.reshape(self.capacity, kv_heads, key_dim), vb.reshape(self.capacity, kv_heads, value_dim)
 
     def load(self, keys: np.ndarray, values: np.ndarray, length: int) -> None:

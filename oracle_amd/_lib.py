@@ -63,6 +63,8 @@ SIGNATURES = [
     ("oq_deltanet_step_noalloc", C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     ("oq_deltanet_noalloc_capacity", _U64, []),
     ("oq_kv_cache_create", C.c_int, [_P, _U64, _U64, _U64, _U64, C.POINTER(_P)]),
+    ("oq_kv_cache_create_typed", C.c_int, [_P, _U64, _U64, _U64, _U64, C.c_uint32, C.POINTER(_P)]),
+    ("oq_kv_cache_type", C.c_uint32, [_P]),
     ("oq_kv_cache_release", None, [_P]),
     ("oq_kv_cache_size", _U64, [_P]),
     ("oq_kv_cache_capacity", _U64, [_P]),

@@ -1050,9 +1050,11 @@ void oq_graph_destroy(oq_graph* g) {
 struct oq_kv_cache {
     oq_context* ctx = nullptr;
     int device = 0;
+    uint32_t type = OQ_TYPE_F32;  // element type: OQ_TYPE_F32 or OQ_TYPE_F16
     uint64_t capacity = 0, kv_heads = 0, key_dim = 0, value_dim = 0, length = 0;
-    float* keys = nullptr;
-    float* values = nullptr;
+    void* keys = nullptr;
+    void* values = nullptr;
+    uint64_t element_bytes() const { return type == OQ_TYPE_F16 ? 2 : 4; }
 };
 
 namespace {
@@ -1125,6 +1127,7 @@ int attention_shape(oq_context* ctx, const oq_kv_cache* c, uint64_t q_heads, oq:
     L.scale = 1.0f / std::sqrt((float)c->key_dim);  // reference_kernels.cpp:158
     L.keys = c->keys;
     L.values = c->values;
+    L.f16 = c->type == OQ_TYPE_F16;
     return OQ_OK;
 }
 
@@ -1163,6 +1166,11 @@ extern "C" {
 
 int oq_kv_cache_create(oq_context* ctx, uint64_t capacity, uint64_t kv_heads, uint64_t key_dim, uint64_t value_dim,
                        oq_kv_cache** out) {
+    return oq_kv_cache_create_typed(ctx, capacity, kv_heads, key_dim, value_dim, OQ_TYPE_F32, out);
+}
+
+int oq_kv_cache_create_typed(oq_context* ctx, uint64_t capacity, uint64_t kv_heads, uint64_t key_dim,
+                             uint64_t value_dim, uint32_t type, oq_kv_cache** out) {
     if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
     if (!out) return fail(ctx, OQ_INVALID_ARGUMENT, "null output handle");
     *out = nullptr;
@@ -1171,24 +1179,29 @@ int oq_kv_cache_create(oq_context* ctx, uint64_t capacity, uint64_t kv_heads, ui
     if (kv_heads == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "KV head count must be non-zero");
     if (key_dim == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "KV key dimension must be non-zero");
     if (value_dim == 0) return fail(ctx, OQ_INVALID_ARGUMENT, "KV value dimension must be non-zero");
-    const uint64_t lim = UINT64_MAX / sizeof(float);
+    if (type != OQ_TYPE_F32 && type != OQ_TYPE_F16) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "KV cache element type must be F32 or F16");
+    }
+    const uint64_t es = type == OQ_TYPE_F16 ? 2 : 4;
+    const uint64_t lim = UINT64_MAX / es;
     if (kv_heads > lim / capacity || key_dim > lim / (capacity * kv_heads) ||
         value_dim > lim / (capacity * kv_heads)) {
         return fail(ctx, OQ_OVERFLOW, "KV cache size overflow");
     }
     if (capturing_now(ctx)) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be created during graph capture");
-    const uint64_t kb = capacity * kv_heads * key_dim * sizeof(float);
-    const uint64_t vb = capacity * kv_heads * value_dim * sizeof(float);
+    const uint64_t kb = capacity * kv_heads * key_dim * es;
+    const uint64_t vb = capacity * kv_heads * value_dim * es;
     OQ_HIP(ctx, hipSetDevice(ctx->device), "hipSetDevice");
     oq_kv_cache* c = new oq_kv_cache;
     c->ctx = ctx;
     c->device = ctx->device;
+    c->type = type;
     c->capacity = capacity;
     c->kv_heads = kv_heads;
     c->key_dim = key_dim;
     c->value_dim = value_dim;
-    hipError_t e = hipMalloc(reinterpret_cast<void**>(&c->keys), kb);
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->values), vb);
+    hipError_t e = hipMalloc(&c->keys, kb);
+    if (e == hipSuccess) e = hipMalloc(&c->values, vb);
     if (e == hipSuccess) e = hipMemsetAsync(c->keys, 0, kb, ctx->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->values, 0, vb, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
@@ -1218,9 +1231,9 @@ int oq_kv_cache_reset(oq_kv_cache* c) {
     oq_context* ctx = c->ctx;
     if (capturing_now(ctx)) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be reset during graph capture");
     c->length = 0;
-    OQ_HIP(ctx, hipMemsetAsync(c->keys, 0, c->capacity * c->kv_heads * c->key_dim * sizeof(float), ctx->stream),
+    OQ_HIP(ctx, hipMemsetAsync(c->keys, 0, c->capacity * c->kv_heads * c->key_dim * c->element_bytes(), ctx->stream),
            "KV cache reset");
-    OQ_HIP(ctx, hipMemsetAsync(c->values, 0, c->capacity * c->kv_heads * c->value_dim * sizeof(float), ctx->stream),
+    OQ_HIP(ctx, hipMemsetAsync(c->values, 0, c->capacity * c->kv_heads * c->value_dim * c->element_bytes(), ctx->stream),
            "KV cache reset");
     return OQ_OK;
 }
@@ -1238,12 +1251,32 @@ int oq_kv_cache_load(oq_kv_cache* c, const float* keys, const float* values, uin
     if (length > c->capacity) return fail(ctx, OQ_OVERFLOW, "KV cache capacity exceeded");
     if (length > 0 && (!keys || !values)) return fail(ctx, OQ_INVALID_ARGUMENT, "null cache rows");
     if (capturing_now(ctx)) return fail(ctx, OQ_INVALID_ARGUMENT, "a KV cache cannot be loaded during graph capture");
-    if (length > 0) {
+    if (length > 0 && c->type == OQ_TYPE_F32) {
         OQ_HIP(ctx, hipMemcpyAsync(c->keys, keys, length * c->kv_heads * c->key_dim * sizeof(float),
                                    hipMemcpyHostToDevice, ctx->stream), "KV cache load");
         OQ_HIP(ctx, hipMemcpyAsync(c->values, values, length * c->kv_heads * c->value_dim * sizeof(float),
                                    hipMemcpyHostToDevice, ctx->stream), "KV cache load");
         OQ_HIP(ctx, hipStreamSynchronize(ctx->stream), "KV cache load");
+    } else if (length > 0) {
+        // F16: the F32 rows go through a bounded device staging buffer and are rounded on the device
+        // (the rounding of the attention steps' appends)
+        const uint64_t total[2] = {length * c->kv_heads * c->key_dim, length * c->kv_heads * c->value_dim};
+        const float* src[2] = {keys, values};
+        _Float16* dst[2] = {static_cast<_Float16*>(c->keys), static_cast<_Float16*>(c->values)};
+        const uint64_t chunk = std::min<uint64_t>(std::max(total[0], total[1]), uint64_t(16) << 20);  // floats
+        void* staging = nullptr;
+        OQ_HIP(ctx, hipMalloc(&staging, chunk * sizeof(float)), "KV cache load staging");
+        hipError_t e = hipSuccess;
+        for (int a = 0; a < 2 && e == hipSuccess; ++a) {
+            for (uint64_t off = 0; off < total[a] && e == hipSuccess; off += chunk) {
+                const uint64_t n = std::min(chunk, total[a] - off);
+                e = hipMemcpyAsync(staging, src[a] + off, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream);
+                if (e == hipSuccess) e = oq::launch_f32_to_f16(static_cast<const float*>(staging), dst[a] + off, n, ctx->stream);
+            }
+        }
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        (void)hipFree(staging);
+        if (e != hipSuccess) return hip_fail(ctx, e, "KV cache load");
     }
     c->length = length;
     return OQ_OK;
@@ -1251,10 +1284,12 @@ int oq_kv_cache_load(oq_kv_cache* c, const float* keys, const float* values, uin
 
 int oq_kv_cache_arrays(const oq_kv_cache* c, float** keys_dev, float** values_dev) {
     if (!c) return fail(nullptr, OQ_INVALID_ARGUMENT, "null KV cache");
-    if (keys_dev) *keys_dev = c->keys;
-    if (values_dev) *values_dev = c->values;
+    if (keys_dev) *keys_dev = static_cast<float*>(c->keys);
+    if (values_dev) *values_dev = static_cast<float*>(c->values);
     return OQ_OK;
 }
+
+uint32_t oq_kv_cache_type(const oq_kv_cache* c) { return c ? c->type : 0; }
 
 int oq_rope(oq_context* ctx, float* heads, uint64_t n_heads, uint64_t head_dim, uint64_t rotary_dim,
             const int32_t sections[4], float base, const uint64_t position[3]) {

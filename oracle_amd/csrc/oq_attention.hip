@@ -31,12 +31,22 @@
 // given, the workgroup whose chunk holds the new token reads it from there and stores it into
 // cache row T - 1; nothing else reads that row during the step.
 //
+// A cache of binary16 elements (no counterpart in the reference, whose cache is F32) halves the
+// bytes every step reads.  Its rows are the F32 rows rounded to nearest even on append, and
+// attention reads what is stored, the new token's row included: a small launch stores the new
+// row rounded before the chunk kernel (which then reads every row from the cache), and with the
+// block's preparation folded in, the new key is scored rounded and stored rounded by the
+// workgroup that prepares it.  Each lane loads the same elements as from an F32 cache (4 of a key
+// row, D / 64 of a value row), half the bytes, kept raw in registers until used.
+//
 // For the decoder block the per-head preparation (qwen35_block.cpp:671-711: RMSNorm of each query
 // head with q_norm and of each key head with k_norm, then the rotation) is folded in as well, so
 // the block has no separate preparation launch: every chunk workgroup of KV head g normalises and
 // rotates g's rep query heads itself, in LDS, while its first key rows are in flight, and the
 // workgroup whose chunk holds the new token also prepares the new key, scores that token from LDS
 // (the key loads issued before it was ready skip it) and stores it into the cache.
+#include <type_traits>
+
 #include "oq_common.h"
 
 namespace oq {
@@ -51,8 +61,8 @@ constexpr int kMergeGroups = 16;  // chunk groups of the merge kernel
 
 struct ChunkArgs {
     const float* q;       // [Hq][D]
-    float* keys;          // [capacity][Hkv][D]
-    float* values;        // [capacity][Hkv][D]
+    void* keys;           // [capacity][Hkv][D] of the cache's element type
+    void* values;         // [capacity][Hkv][D]
     const float* new_k;   // [Hkv][D] or null
     const float* new_v;
     uint32_t T, Hkv, rep, chunk, nchunks;
@@ -110,6 +120,83 @@ struct Vec<4> {
     }
 };
 
+// Binary16 values of a value row per lane (VW of them) as raw bits, and their F32 values
+template <int N>
+struct HalfVec;
+template <>
+struct HalfVec<1> {
+    using type = uint16_t;
+    OQ_DEVICE static void unpack(type v, float* o) { o[0] = (float)__builtin_bit_cast(_Float16, v); }
+};
+template <>
+struct HalfVec<2> {
+    using type = uint32_t;
+    OQ_DEVICE static void unpack(type v, float* o) {
+        o[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFFu));
+        o[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+    }
+};
+template <>
+struct HalfVec<4> {
+    using type = uint2;
+    OQ_DEVICE static void unpack(type v, float* o) {
+        HalfVec<2>::unpack(v.x, o);
+        HalfVec<2>::unpack(v.y, o + 2);
+    }
+};
+
+// Loads of cache rows of element type KT: K4 holds a lane's 4 consecutive key elements, V its VW
+// value elements, both as loaded; k4 / unpack_v convert at the point of use.  round gives the
+// value a cache element holds for an F32 value, store the element itself.
+template <typename KT, int VW>
+struct KvIo;
+template <int VW>
+struct KvIo<float, VW> {
+    using K4 = float4;
+    using V = typename Vec<VW>::type;
+    OQ_DEVICE static K4 load_k(const float* row, uint32_t i4) { return load_stream(reinterpret_cast<const float4*>(row) + i4); }
+    OQ_DEVICE static float4 k4(K4 v) { return v; }
+    OQ_DEVICE static V load_v(const float* row, int lane) { return load_stream(reinterpret_cast<const V*>(row) + lane); }
+    OQ_DEVICE static void unpack_v(V v, float* o) { Vec<VW>::unpack(v, o); }
+    OQ_DEVICE static float round(float x) { return x; }
+    OQ_DEVICE static float store(float x) { return x; }
+};
+template <int VW>
+struct KvIo<_Float16, VW> {
+    using K4 = uint2;
+    using V = typename HalfVec<VW>::type;
+    OQ_DEVICE static K4 load_k(const _Float16* row, uint32_t i4) {
+        return load_stream(reinterpret_cast<const uint2*>(row) + i4);
+    }
+    OQ_DEVICE static float4 k4(K4 v) {
+        float o[4];
+        HalfVec<4>::unpack(v, o);
+        return make_float4(o[0], o[1], o[2], o[3]);
+    }
+    OQ_DEVICE static V load_v(const _Float16* row, int lane) { return load_stream(reinterpret_cast<const V*>(row) + lane); }
+    OQ_DEVICE static void unpack_v(V v, float* o) { HalfVec<VW>::unpack(v, o); }
+    OQ_DEVICE static float round(float x) { return (float)(_Float16)x; }
+    OQ_DEVICE static _Float16 store(float x) { return (_Float16)x; }
+};
+
+// The new token's key and value rows [Hkv * D] stored into an F16 cache (rounded to nearest even)
+// before an attention launch over it; either source may be null (not stored).
+__global__ __launch_bounds__(256) void kv_append_f16_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                            _Float16* __restrict__ kd, _Float16* __restrict__ vd,
+                                                            uint32_t n) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    if (k != nullptr) kd[i] = (_Float16)k[i];
+    if (v != nullptr) vd[i] = (_Float16)v[i];
+}
+
+// F32 rows -> an F16 cache's elements, rounded to nearest even (oq_kv_cache_load)
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict__ src, _Float16* __restrict__ dst,
+                                                         uint64_t n) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256u;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += stride) dst[i] = (_Float16)src[i];
+}
+
 // cos and sin of frequency f's angle, as apply_qwen35_rope (reference_kernels.cpp:105-115):
 // base^(2f/R) and the angle in double, the coordinate chosen as position_for_frequency (:28-40)
 OQ_DEVICE void rope_cs(uint32_t f, const RopeParams& p, float& c, float& s) {
@@ -155,11 +242,14 @@ OQ_DEVICE void prep_row_norm(const float* x, const float* w, float eps, int lane
 // Both phases run in blocks of NB passes (keys) or NB groups (values); every block but the last
 // requests the next block's rows as it consumes its own, and the last requests nothing.  ONE: the
 // chunk fits the NB passes in flight (chunk <= 16 NB tokens), so the last block is the only one.
-template <int D, int REP, int NB, bool PREP, bool ONE>
+template <typename KT, int D, int REP, int NB, bool PREP, bool ONE>
 __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs a) {
-    constexpr int NV = D / 64;  // float4 of one key row per lane (16 lanes per row)
+    constexpr int NV = D / 64;  // 4-element pieces of one key row per lane (16 lanes per row)
     constexpr int VW = D / 64;  // value columns per lane (64 lanes per row)
-    using VT = typename Vec<VW>::type;
+    using IO = KvIo<KT, VW>;
+    using VT = typename IO::V;
+    KT* const keys = static_cast<KT*>(a.keys);
+    KT* const values = static_cast<KT*>(a.values);
     extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -174,20 +264,26 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
     const uint32_t last = a.T - 1;
     float* sc = lds;  // [rep][chunk] scores, then probabilities
 
-    auto key_row = [&](uint32_t t) -> const float* {
-        if (a.new_k != nullptr && t == last) return a.new_k + (uint64_t)g * D;
-        return a.keys + ((uint64_t)t * a.Hkv + g) * D;
+    // rows t of the cache; the new token's rows from new_k / new_v when given (an F32 cache only:
+    // an F16 cache holds them before the launch)
+    auto key_row = [&](uint32_t t) -> const KT* {
+        if constexpr (std::is_same_v<KT, float>) {
+            if (a.new_k != nullptr && t == last) return a.new_k + (uint64_t)g * D;
+        }
+        return keys + ((uint64_t)t * a.Hkv + g) * D;
     };
-    auto value_row = [&](uint32_t t) -> const float* {
-        if (a.new_v != nullptr && t == last) return a.new_v + (uint64_t)g * D;
-        return a.values + ((uint64_t)t * a.Hkv + g) * D;
+    auto value_row = [&](uint32_t t) -> const KT* {
+        if constexpr (std::is_same_v<KT, float>) {
+            if (a.new_v != nullptr && t == last) return a.new_v + (uint64_t)g * D;
+        }
+        return values + ((uint64_t)t * a.Hkv + g) * D;
     };
 
     // the append: subgroup 0's chunk holding the new token stores its key and value row
     if (a.new_k != nullptr && c1 == a.T && sub == 0) {
         for (uint32_t i = threadIdx.x; i < (uint32_t)D; i += kAttnThreads) {
-            a.keys[((uint64_t)last * a.Hkv + g) * D + i] = a.new_k[(uint64_t)g * D + i];
-            a.values[((uint64_t)last * a.Hkv + g) * D + i] = a.new_v[(uint64_t)g * D + i];
+            keys[((uint64_t)last * a.Hkv + g) * D + i] = IO::store(a.new_k[(uint64_t)g * D + i]);
+            values[((uint64_t)last * a.Hkv + g) * D + i] = IO::store(a.new_v[(uint64_t)g * D + i]);
         }
     }
 
@@ -210,7 +306,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                 const bool is_q = row < rep;
                 const float* src = is_q ? a.qfull + (h0 + row) * 2 * D : a.kp + (uint64_t)g * D;
                 const float* w = is_q ? a.q_norm : a.k_norm;
-                Vec<VW>::unpack(*reinterpret_cast<const VT*>(src + lane * VW), px[r]);
+                Vec<VW>::unpack(*reinterpret_cast<const typename Vec<VW>::type*>(src + lane * VW), px[r]);
 #pragma unroll
                 for (int e = 0; e < VW; ++e) pw[r][e] = w[lane * VW + e];
             }
@@ -225,14 +321,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
         }
     }
     const uint32_t first = c0 + (uint32_t)wave * 4u;  // this wave's first pass (wave-uniform)
-    auto load_keys = [&](float4 (&dst)[NV], uint32_t pass_base) {
+    auto load_keys = [&](typename IO::K4 (&dst)[NV], uint32_t pass_base) {
         const uint32_t t = pass_base + (uint32_t)(lane >> 4);
-        const float4* kp = reinterpret_cast<const float4*>(key_row(t < c1 ? t : c1 - 1));
+        const KT* kp = key_row(t < c1 ? t : c1 - 1);
 #pragma unroll
-        for (int j = 0; j < NV; ++j) dst[j] = load_stream(kp + j * 16 + l16);
+        for (int j = 0; j < NV; ++j) dst[j] = IO::load_k(kp, (uint32_t)(j * 16 + l16));
     };
     {
-        float4 kb[NB][NV];
+        typename IO::K4 kb[NB][NV];
 #pragma unroll
         for (int b = 0; b < NB; ++b) load_keys(kb[b], first + (uint32_t)b * kTokStep);
         if constexpr (PREP) {
@@ -267,8 +363,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                 for (uint32_t i = threadIdx.x; i < (uint32_t)D; i += kAttnThreads) {
                     const float k = stage[rep * D + i];
                     if (a.kcur != nullptr) a.kcur[(uint64_t)g * D + i] = k;
-                    a.keys[((uint64_t)last * a.Hkv + g) * D + i] = k;
-                    a.values[((uint64_t)last * a.Hkv + g) * D + i] = a.new_v[(uint64_t)g * D + i];
+                    keys[((uint64_t)last * a.Hkv + g) * D + i] = IO::store(k);
+                    // (an F16 cache's value row was stored before the launch: new_v is null)
+                    if (a.new_v != nullptr) values[((uint64_t)last * a.Hkv + g) * D + i] = IO::store(a.new_v[(uint64_t)g * D + i]);
                 }
             }
         }
@@ -278,15 +375,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                 const uint32_t pb = base + (uint32_t)b * kTokStep;
                 const uint32_t t = pb + (uint32_t)(lane >> 4);
                 float acc[REP];
+                float4 kf[NV];
+#pragma unroll
+                for (int j = 0; j < NV; ++j) kf[j] = IO::k4(kb[b][j]);
 #pragma unroll
                 for (int h = 0; h < REP; ++h) {
                     float sum = 0.0f;
 #pragma unroll
                     for (int j = 0; j < NV; ++j) {
-                        sum += qr[h][j].x * kb[b][j].x;
-                        sum += qr[h][j].y * kb[b][j].y;
-                        sum += qr[h][j].z * kb[b][j].z;
-                        sum += qr[h][j].w * kb[b][j].w;
+                        sum += qr[h][j].x * kf[j].x;
+                        sum += qr[h][j].y * kf[j].y;
+                        sum += qr[h][j].z * kf[j].z;
+                        sum += qr[h][j].w * kf[j].w;
                     }
                     acc[h] = row16_sum(sum);
                 }
@@ -314,7 +414,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
             for (uint32_t h = (uint32_t)wave; h < rep; h += kAttnWaves) {
                 float s = 0.0f;
 #pragma unroll
-                for (int e = 0; e < VW; ++e) s += stage[h * D + (uint32_t)lane * VW + e] * kn[(uint32_t)lane * VW + e];
+                for (int e = 0; e < VW; ++e) s += stage[h * D + (uint32_t)lane * VW + e] * IO::round(kn[(uint32_t)lane * VW + e]);
                 s = wave_sum(s);
                 if (lane == 0) sc[h * a.chunk + (last - c0)] = s * a.scale;
             }
@@ -327,7 +427,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const uint32_t i = i0 + (uint32_t)u * kAttnWaves;
-            dst[u] = load_stream(reinterpret_cast<const VT*>(value_row(c0 + (i < n ? i : n - 1))) + lane);
+            dst[u] = IO::load_v(value_row(c0 + (i < n ? i : n - 1)), lane);
         }
     };
     constexpr uint32_t kGroup = 4u * kAttnWaves;  // tokens per value group of the workgroup
@@ -372,7 +472,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                 // rows past the chunk are clamped loads with weight 0
                 const uint32_t ic = i < n ? i : n - 1;
                 float v[VW];
-                Vec<VW>::unpack(vb[b][u], v);
+                IO::unpack_v(vb[b][u], v);
 #pragma unroll
                 for (int h = 0; h < REP; ++h) {
                     if ((uint32_t)h >= rep) break;
@@ -523,18 +623,18 @@ __global__ __launch_bounds__(256) void rope_kernel(float* heads, uint32_t head_d
     for (uint32_t f = threadIdx.x; f < half; f += blockDim.x) rope_pair(x, f, half, p);
 }
 
-template <int D, int REP, int NB, bool ONE>
+template <typename KT, int D, int REP, int NB, bool ONE>
 hipError_t launch_nb(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
     const dim3 grid(a.Hkv * a.nsub * a.nchunks);
     if (a.qfull != nullptr) {
-        hipLaunchKernelGGL((attention_chunk_kernel<D, REP, NB, true, ONE>), grid, dim3(kAttnThreads), lds, s, a);
+        hipLaunchKernelGGL((attention_chunk_kernel<KT, D, REP, NB, true, ONE>), grid, dim3(kAttnThreads), lds, s, a);
     } else {
-        hipLaunchKernelGGL((attention_chunk_kernel<D, REP, NB, false, ONE>), grid, dim3(kAttnThreads), lds, s, a);
+        hipLaunchKernelGGL((attention_chunk_kernel<KT, D, REP, NB, false, ONE>), grid, dim3(kAttnThreads), lds, s, a);
     }
     return hipGetLastError();
 }
 
-template <int D, int REP>
+template <typename KT, int D, int REP>
 hipError_t launch_chunks(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
     // passes in flight per wave.  Long chunks: two, measured 56.1 us per step (chunk + merge, 16
     // query heads over 4 KV heads of 256, 32768 tokens) against 57.2 with one and 62.4 with three;
@@ -543,10 +643,18 @@ hipError_t launch_chunks(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
     // trip and no pass is a clamped copy of the chunk's last row: attention at 1024 / 2048 / 4096
     // tokens 12.1 / 15.5 / 17.8 us with three passes in flight -> 9.45 / 12.3 / 15.6; the attention
     // block at 4097 tokens (48-token chunks) 54.3-55.2 us with two -> 52.9-53.3 with three.
-    if (a.chunk <= kTokStep) return launch_nb<D, REP, 1, true>(a, lds, s);
-    if (a.chunk <= 2 * kTokStep) return launch_nb<D, REP, 2, true>(a, lds, s);
-    if (a.chunk <= 3 * kTokStep) return launch_nb<D, REP, 3, true>(a, lds, s);
-    return launch_nb<D, REP, 2, false>(a, lds, s);
+    if (a.chunk <= kTokStep) return launch_nb<KT, D, REP, 1, true>(a, lds, s);
+    if (a.chunk <= 2 * kTokStep) return launch_nb<KT, D, REP, 2, true>(a, lds, s);
+    if (a.chunk <= 3 * kTokStep) return launch_nb<KT, D, REP, 3, true>(a, lds, s);
+    return launch_nb<KT, D, REP, 2, false>(a, lds, s);
+}
+
+template <typename KT, int D>
+hipError_t launch_reps(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
+    if (a.rep == 1) return launch_chunks<KT, D, 1>(a, lds, s);
+    if (a.rep == 2) return launch_chunks<KT, D, 2>(a, lds, s);
+    if (a.rep <= 4) return launch_chunks<KT, D, 4>(a, lds, s);
+    return launch_chunks<KT, D, 8>(a, lds, s);
 }
 
 template <int D>
@@ -586,10 +694,22 @@ hipError_t launch_d(const AttnLaunch& L, hipStream_t s) {
     }
     lds *= sizeof(float);
     hipError_t e;
-    if (a.rep == 1) e = launch_chunks<D, 1>(a, lds, s);
-    else if (a.rep == 2) e = launch_chunks<D, 2>(a, lds, s);
-    else if (a.rep <= 4) e = launch_chunks<D, 4>(a, lds, s);
-    else e = launch_chunks<D, 8>(a, lds, s);
+    if (L.f16) {
+        // the new token's rows (with the preparation folded in, its value row only: the key is
+        // prepared and stored by the chunk kernel) rounded into the cache before the chunk kernel
+        if (a.new_k != nullptr || a.new_v != nullptr) {
+            const uint32_t n = L.Hkv * (uint32_t)D;
+            const uint64_t row = (uint64_t)(L.T - 1) * L.Hkv * D;
+            hipLaunchKernelGGL(kv_append_f16_kernel, dim3((n + 255) / 256), dim3(256), 0, s, a.new_k, a.new_v,
+                               static_cast<_Float16*>(L.keys) + row, static_cast<_Float16*>(L.values) + row, n);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+        a.new_k = nullptr;
+        a.new_v = nullptr;
+        e = launch_reps<_Float16, D>(a, lds, s);
+    } else {
+        e = launch_reps<float, D>(a, lds, s);
+    }
     if (e != hipSuccess) return e;
     MergeArgs m{};
     m.part_o = a.part_o;
@@ -639,6 +759,13 @@ void attention_plan(uint64_t T, uint64_t Hkv, uint64_t rep, uint32_t& chunk, uin
 
 uint64_t attention_partial_floats(uint64_t Hkv, uint64_t rep, uint64_t head_dim, uint32_t nchunks) {
     return Hkv * (uint64_t)nchunks * rep * (head_dim + 2);
+}
+
+hipError_t launch_f32_to_f16(const float* src, void* dst, uint64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, static_cast<_Float16*>(dst), n);
+    return hipGetLastError();
 }
 
 hipError_t launch_attention(const AttnLaunch& L, hipStream_t s) {

@@ -39,6 +39,12 @@ OQ_DEVICE uint4 load_stream(const uint4* p) {
     const v4 v = __builtin_nontemporal_load(reinterpret_cast<const v4*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+OQ_DEVICE uint2 load_stream(const uint2* p) {
+    typedef unsigned v2 __attribute__((ext_vector_type(2)));
+    const v2 v = __builtin_nontemporal_load(reinterpret_cast<const v2*>(p));
+    return make_uint2(v.x, v.y);
+}
+OQ_DEVICE uint16_t load_stream(const uint16_t* p) { return __builtin_nontemporal_load(p); }
 
 // Exact binary16 -> binary32 that keeps NaN payloads bit for bit (the hardware conversion
 // quiets signalling NaNs; the reference's f16_to_f32, src/model/storage_decode.cpp:150-176,

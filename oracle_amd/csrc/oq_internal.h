@@ -179,8 +179,9 @@ struct AttnPrep {
 };
 struct AttnLaunch {
     const float* q;            // [Hkv * rep][D]
-    float* keys;               // cache [capacity][Hkv][D]
-    float* values;
+    void* keys;                // cache [capacity][Hkv][D] of F32, or of binary16 when f16
+    void* values;
+    bool f16;
     const float* new_k;        // token T-1's key/value rows [Hkv][D], stored into the cache; or null
     const float* new_v;        //   when the cache already holds them
     uint32_t T, Hkv, rep, D, chunk, nchunks;
@@ -200,6 +201,7 @@ void attention_plan(uint64_t T, uint64_t Hkv, uint64_t rep, uint32_t& chunk, uin
 uint64_t attention_partial_floats(uint64_t Hkv, uint64_t rep, uint64_t head_dim, uint32_t nchunks);
 constexpr uint32_t kAttnMaxChunks = 8192;
 hipError_t launch_attention(const AttnLaunch& a, hipStream_t s);
+hipError_t launch_f32_to_f16(const float* src, void* dst, uint64_t n, hipStream_t s);  // round to nearest even
 hipError_t launch_rope(float* heads, uint64_t n_heads, uint64_t head_dim, const RopeParams& p, hipStream_t s);
 
 // ---- oq_gemv_block.hip  (fused m = 1 GEMV of the DeltaNet decode block; see the kernel comment)

@@ -10,6 +10,7 @@ reference (reference_kernels.cpp:77-195, qwen35_block.cpp:607-756) on identical 
 - the block (oq_attention_block_step) stage by stage, each stage from the device's own inputs to
   it as in the DeltaNet block tests, and end to end as a wiring check.
 """
+import ctypes as C
 import math
 
 import numpy as np
@@ -189,6 +190,72 @@ def test_attention_step_sizes(ctx, hq, hkv, d, T):
         cache.release()
 
 
+def f16(a):
+    """The value an F16 cache stores for F32 elements (round to nearest even)."""
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+F16_CASES = [(8, 2, 256, 1), (16, 4, 256, 4097), (8, 1, 128, 777), (4, 4, 64, 300), (6, 2, 128, 301),
+             (32, 2, 256, 4097), (16, 4, 256, 65537)]
+
+
+@pytest.mark.parametrize("hq,hkv,d,T", F16_CASES, ids=[f"h{a}_{b}_d{c}_T{t}" for a, b, c, t in F16_CASES])
+def test_attention_step_f16_cache(ctx, hq, hkv, d, T):
+    """An F16 cache: loaded and appended rows are the F32 rows rounded to nearest even (bit for
+    bit), and attention runs over the stored rows, the new token's included, within the same bar
+    as over an F32 cache."""
+    print(f"attention step f16 cache hq={hq} hkv={hkv} d={d} T={T}", flush=True)
+    rng = np.random.default_rng(2000 + T + hq)
+    keys = rng.standard_normal((T, hkv, d)).astype(np.float32)
+    values = rng.standard_normal((T, hkv, d)).astype(np.float32)
+    q = (2.0 * rng.standard_normal((hq, d))).astype(np.float32)
+    k16, v16 = f16(keys), f16(values)
+    ref_cache = oracle.KvCache(T + 1, hkv, d, d)
+    ref_cache.keys[:T - 1] = k16[:T - 1]
+    ref_cache.values[:T - 1] = v16[:T - 1]
+    ref_cache.length = T - 1
+    want = oracle.attention_step(q, k16[T - 1], v16[T - 1], ref_cache)
+    cache = ctx.kv_cache(T + 1, hkv, d, d, dtype="f16")
+    bufs = [ctx.to_device(q), ctx.to_device(keys[T - 1]), ctx.to_device(values[T - 1]), ctx.alloc(hq * d * 4)]
+    try:
+        cache.load(keys[:T - 1], values[:T - 1], T - 1)
+        ctx.attention_step(bufs[0], hq, bufs[1], bufs[2], cache, bufs[3])
+        got = bufs[3].download(np.float32, hq * d).reshape(hq, d)
+        check_attention(got, want, attention_bar(q, k16, v16, T), f"T={T}")
+        assert len(cache) == T
+        k_dev, v_dev = cache.download(hkv, d, d)
+        assert np.array_equal(k_dev[:T], k16) and np.array_equal(v_dev[:T], v16)
+        assert not np.any(k_dev[T:]) and not np.any(v_dev[T:])
+    finally:
+        for b in bufs:
+            b.free()
+        cache.release()
+
+
+def test_kv_cache_f16_rounding_and_errors(ctx):
+    """Loaded rows round to nearest even, ties included, subnormal and overflowing values too;
+    reset zeroes the binary16 arrays; an element type other than F32 / F16 is refused."""
+    vals = np.array([0.0, -0.0, 1.0, 65504.0, 65519.0, 65520.0, -70000.0, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -25,
+                     2.0 ** -14, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 0.1, -1e-7, 1234.5678], np.float32)
+    rows = np.tile(vals, 8).reshape(2, 1, 64)
+    cache = ctx.kv_cache(4, 1, 64, 64, dtype="f16")
+    try:
+        cache.load(rows, -rows, 2)
+        k, v = cache.download(1, 64, 64)
+        assert np.array_equal(k[:2].view(np.uint32), f16(rows).view(np.uint32))
+        assert np.array_equal(v[:2].view(np.uint32), f16(-rows).view(np.uint32))
+        cache.reset()
+        k, v = cache.download(1, 64, 64)
+        assert len(cache) == 0 and not np.any(k) and not np.any(v)
+    finally:
+        cache.release()
+    h = C.c_void_p()
+    rc = ctx.lib.oq_kv_cache_create_typed(ctx.h, 4, 1, 64, 64, 8, C.byref(h))
+    assert rc == -1 and b"KV cache element type must be F32 or F16" in ctx.lib.oq_last_error(ctx.h)
+    with pytest.raises(oracle_amd.InvalidArgument):
+        ctx.kv_cache(4, 1, 64, 64, dtype="q8_0")
+
+
 def test_attention_step_errors(ctx):
     cache = ctx.kv_cache(2, 2, 64, 64)
     q, k, v, o = ctx.alloc(6 * 64 * 4), ctx.alloc(2 * 64 * 4), ctx.alloc(2 * 64 * 4), ctx.alloc(6 * 64 * 4)
@@ -233,11 +300,11 @@ def test_attention_step_errors(ctx):
 
 # ---------------------------------------------------------------- the block
 
-def run_block(ctx, d, w, vec, cache_np, positions, xs):
+def run_block(ctx, d, w, vec, cache_np, positions, xs, dtype="f32"):
     """Device steps; per step: y, trace and the cache arrays before the step."""
     blk = oracle_amd.AttentionBlockWeights(ctx, d, w, vec)
     hkv, D = d["kv_heads"], d["head_dim"]
-    cache = ctx.kv_cache(cache_np.capacity, hkv, D, D)
+    cache = ctx.kv_cache(cache_np.capacity, hkv, D, D, dtype=dtype)
     try:
         cache.load(cache_np.keys, cache_np.values, cache_np.length)
         sizes = oracle.attention_trace_sizes(d)
@@ -257,7 +324,8 @@ def run_block(ctx, d, w, vec, cache_np, positions, xs):
                 off += sz
             k1, v1 = cache.download(hkv, D, D)
             steps.append({"x": x, "pos": pos, "y": yb.download(np.float32, d["embedding"]), "trace": tr,
-                          "keys0": k0, "values0": v0, "len0": n0, "keys1": k1, "values1": v1, "len1": len(cache)})
+                          "keys0": k0, "values0": v0, "len0": n0, "keys1": k1, "values1": v1, "len1": len(cache),
+                          "kv16": dtype == "f16"})
             xb.free()
         tb.free()
         yb.free()
@@ -307,7 +375,11 @@ def check_block_stages(d, w, vec, step, proj_tol=None):
     c.values[:] = step["values0"]
     c.length = n0
     q = g["qcur"].reshape(Hq, D)
-    att = oracle.attention_step(q, g["kcur"].reshape(Hkv, D), g["v"].reshape(Hkv, D), c)
+    # the new token's rows as the cache stores them (an F16 cache: rounded to nearest even)
+    knew, vnew = g["kcur"].reshape(Hkv, D), g["v"].reshape(Hkv, D)
+    if step.get("kv16"):
+        knew, vnew = f16(knew), f16(vnew)
+    att = oracle.attention_step(q, knew, vnew, c)
     bar = attention_bar(q, c.keys, c.values, n0 + 1)
     worst["pregate"] = check_attention(g["pregate"].reshape(Hq, D), att, bar, "pregate")
     gs = np.array([oracle.sigmoid(v) for v in qf[:, D:].reshape(-1)], np.float32)
@@ -319,8 +391,8 @@ def check_block_stages(d, w, vec, step, proj_tol=None):
     close("y", step["y"], g["resid"] + g["ffn"], worst)
     # the append: row n0 holds the rotated key and the value; nothing else changed
     assert step["len1"] == n0 + 1
-    assert np.array_equal(step["keys1"][n0].reshape(-1), g["kcur"])
-    assert np.array_equal(step["values1"][n0].reshape(-1), g["v"])
+    assert np.array_equal(step["keys1"][n0].reshape(-1), knew.reshape(-1))
+    assert np.array_equal(step["values1"][n0].reshape(-1), vnew.reshape(-1))
     assert np.array_equal(step["keys1"][:n0], step["keys0"][:n0])
     return worst
 
@@ -394,6 +466,22 @@ def test_attention_block_stages(ctx, name):
         check_block_stages(d, w, vec, st)
         y, _ = oracle.attention_block_step(d, w, vec, own, st["pos"], st["x"], threads=THREADS)
         assert float(np.max(np.abs(st["y"] - y))) <= CHAIN_TOL * float(np.max(np.abs(y)))
+
+
+@pytest.mark.parametrize("name", ["e2048", "rep1_d64", "rep16"])
+def test_attention_block_f16_cache(ctx, name):
+    """The block over an F16 cache: every stage as over an F32 cache, the attention against the
+    oracle over the stored (rounded) rows, the appended key and value rounded to nearest even."""
+    from golden.make_golden import attention_inputs
+    d, types, cached = BLOCKS[name]
+    w, vec, c, xs = attention_inputs(np.random.default_rng(4343), d, types, cached=cached)
+    positions = [(cached + i, cached + i, cached + i) for i in range(2)] + [(cached + 2, 7, 19)]
+    steps = run_block(ctx, d, w, vec, c, positions, xs, dtype="f16")
+    for st in steps:
+        check_block_stages(d, w, vec, st)
+        # the loaded rows, rounded on the device as numpy rounds them
+        assert np.array_equal(st["keys0"][:cached], f16(c.keys[:cached]))
+        assert np.array_equal(st["values0"][:cached], f16(c.values[:cached]))
 
 
 @pytest.mark.parametrize("name", ["e2048", "rep1_d64"])

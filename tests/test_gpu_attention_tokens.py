@@ -15,7 +15,7 @@ import pytest
 
 import oracle
 import oracle_amd
-from test_gpu_attention import BLOCKS, CHAIN_TOL, THREADS, check_block_stages
+from test_gpu_attention import BLOCKS, CHAIN_TOL, THREADS, check_block_stages, f16
 
 pytestmark = pytest.mark.gpu
 
@@ -35,11 +35,11 @@ def inputs(name, m, seed):
     return d, w, vec, cache, xs, positions
 
 
-def run_tokens(ctx, d, w, vec, c, positions, xs, trace=True):
+def run_tokens(ctx, d, w, vec, c, positions, xs, trace=True, dtype="f32"):
     blk = oracle_amd.AttentionBlockWeights(ctx, d, w, vec)
     hkv, D = d["kv_heads"], d["head_dim"]
     m, E = xs.shape
-    cache = ctx.kv_cache(c.capacity, hkv, D, D)
+    cache = ctx.kv_cache(c.capacity, hkv, D, D, dtype=dtype)
     sizes = oracle.attention_trace_sizes(d)
     per = sum(sizes.values())
     bufs = []
@@ -89,6 +89,20 @@ def test_block_tokens_match_oracle(ctx, name, m):
 # The matrix-core products' bound on rows that a few products lead (2^-10 of sum |w xhat| plus
 # binary16-subnormal weights and F32 summation)
 DOMINATED_TOL = 1.5e-3
+
+
+def test_block_tokens_f16_cache(ctx):
+    """m tokens over an F16 cache: each token's stages, its key and value appended rounded, and
+    every later token attending over the rounded rows."""
+    d, w, vec, c, xs, positions = inputs("e2048", 4, 9500)
+    n0 = c.length
+    y, traces, keys, values, length = run_tokens(ctx, d, w, vec, c, positions, xs, dtype="f16")
+    assert length == n0 + 4
+    assert np.array_equal(keys[:n0], f16(c.keys[:n0])) and np.array_equal(values[:n0], f16(c.values[:n0]))
+    for t in range(4):
+        step = {"x": xs[t], "pos": positions[t], "y": y[t], "trace": traces[t], "keys0": keys, "values0": values,
+                "len0": n0 + t, "keys1": keys, "values1": values, "len1": n0 + t + 1, "kv16": True}
+        check_block_stages(d, w, vec, step)
 
 
 @pytest.mark.parametrize("env", [{}, {"OQ_GEMM_MFMA": "0"}], ids=["matrix_cores", "integer_dots"])
