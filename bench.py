@@ -266,10 +266,11 @@ def run_attention(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, kv_dty
             "copies": ncopies, "geometry": g}
 
 
-def run_attention_block(ctx, steps, warmup, cached=4096, copies_min_bytes=MALL_DEFEAT_BYTES):
+def run_attention_block(ctx, steps, warmup, cached=4096, copies_min_bytes=MALL_DEFEAT_BYTES, tokens=1):
     """One full-attention decode block (hidden 4096, 16 query heads over 4 KV heads of 256, FFN
-    12288) over 4096 cached tokens per step (oq_attention_block_step); steps cycle over block
-    copies (weights + cache) totalling >= 512 MiB; the cache is truncated back after each step."""
+    12288) over 4096 cached tokens per step (oq_attention_block_step; with tokens > 1, that many
+    consecutive tokens per step through oq_attention_block_steps); steps cycle over block copies
+    (weights + cache) totalling >= 512 MiB; the cache is truncated back after each step."""
     rng = np.random.default_rng(SEED + 300)
     d, w, vec, keys, values, x = synth.attention_block(rng, cached=cached)
     first = oracle_amd.AttentionBlockWeights(ctx, d, w, vec)
@@ -279,19 +280,23 @@ def run_attention_block(ctx, steps, warmup, cached=4096, copies_min_bytes=MALL_D
     blocks = [first] + [oracle_amd.AttentionBlockWeights(ctx, d, w, vec) for _ in range(ncopies - 1)]
     caches = []
     for _ in range(ncopies):
-        c = ctx.kv_cache(cached + 1, d["kv_heads"], d["head_dim"], d["head_dim"])
+        c = ctx.kv_cache(cached + tokens, d["kv_heads"], d["head_dim"], d["head_dim"])
         c.load(keys, values, cached)
         caches.append(c)
-    xb, yb = ctx.to_device(x), ctx.alloc(d["embedding"] * 4)
+    xs = np.stack([x] + [rng.standard_normal(x.shape).astype(np.float32) for _ in range(tokens - 1)])
+    xb, yb = ctx.to_device(xs), ctx.alloc(tokens * d["embedding"] * 4)
     lib, h = ctx.lib, ctx.h
     descs = [C.byref(b.desc) for b in blocks]
     hs = [c.h for c in caches]
-    pos = (C.c_uint64 * 3)(cached, cached, cached)
+    pos = (C.c_uint64 * (3 * tokens))(*[cached + t for t in range(tokens) for _ in range(3)])
 
     def step(i):
         c = hs[i % ncopies]
-        if lib.oq_attention_block_step(h, descs[i % ncopies], c, pos, xb.ptr, yb.ptr, None) != 0 or \
-                lib.oq_kv_cache_truncate(c, cached) != 0:
+        if tokens == 1:
+            rc = lib.oq_attention_block_step(h, descs[i % ncopies], c, pos, xb.ptr, yb.ptr, None)
+        else:
+            rc = lib.oq_attention_block_steps(h, descs[i % ncopies], c, tokens, pos, xb.ptr, yb.ptr, None)
+        if rc != 0 or lib.oq_kv_cache_truncate(c, cached) != 0:
             raise RuntimeError(f"step {i}: {lib.oq_last_error(h).decode()}")
 
     step(0)  # checked call; sizes the block workspace
@@ -304,8 +309,8 @@ def run_attention_block(ctx, steps, warmup, cached=4096, copies_min_bytes=MALL_D
     for buf in (xb, yb):
         buf.free()
     ms_step = ms / steps
-    return {"workload": "attention_block", "weight_bytes": wb, "kv_bytes": kvb, "copies": ncopies,
-            "ms_per_step": ms_step, "us_per_block": ms_step * 1e3,
+    return {"workload": "attention_block", "weight_bytes": wb, "kv_bytes": kvb, "copies": ncopies, "tokens": tokens,
+            "ms_per_step": ms_step, "us_per_block": ms_step * 1e3, "us_per_token": ms_step * 1e3 / tokens,
             "gbs": (wb + kvb) / (ms_step * 1e-3) / 1e9, "dims": {k: v for k, v in d.items()}, "cached": cached}
 
 
@@ -433,17 +438,20 @@ def main():
             "hbm_frac_weight_bytes": round(r["weight_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
         return
     if args.workload == "attention_block":
-        r = run_attention_block(ctx, args.steps, args.warmup)
+        r = run_attention_block(ctx, args.steps, args.warmup, tokens=args.tokens)
         ctx.close()
         print(json.dumps({
             "metric": "attention decode block GB/s (weights + KV cache)", "value": round(r["gbs"], 2), "unit": "GB/s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8xu4 dot (i32) + f32",
             "data": "synthetic (seeded block weights, keys/values/x ~ N(0,1))",
-            "config": {"workload": "Qwen3.5 full-attention decode block, batch 1", **r["dims"],
+            "config": {"workload": "Qwen3.5 full-attention decode block, batch 1" if r["tokens"] == 1 else
+                       f"Qwen3.5 full-attention block, {r['tokens']} consecutive tokens per step (oq_attention_block_steps)",
+                       **r["dims"],
                        "cached_tokens": r["cached"], "weight_bytes": r["weight_bytes"], "kv_bytes": r["kv_bytes"],
                        "block_copies_cycled": r["copies"]},
-            "us_per_block": round(r["us_per_block"], 2), "hbm_frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
+            "us_per_block": round(r["us_per_block"], 2), "tokens": r["tokens"], "us_per_token": round(r["us_per_token"], 2),
+            "hbm_frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
         return
     if args.workload == "attention_decode":
         r = run_attention(ctx, args.steps, args.warmup, kv_dtype=args.kv)
@@ -461,7 +469,7 @@ def main():
             "us_per_step": round(r["us_per_step"], 2)}), flush=True)
         return
     main_res = run_gpu(ctx, args.workload, args.steps, args.warmup, graph=args.graph)
-    secondary = block = block4 = attn = attn16 = attn_block = None
+    secondary = block = block4 = attn = attn16 = attn_block = attn_block4 = None
     configs = {}
     if not args.no_secondary and args.workload == "q4k_gemv":
         secondary = run_gpu(ctx, "q4k_down_m512", max(5, args.steps // 4), max(2, args.warmup // 5))
@@ -473,6 +481,7 @@ def main():
         attn = run_attention(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
         attn16 = run_attention(ctx, max(5, args.steps // 10), max(2, args.warmup // 5), kv_dtype="f16")
         attn_block = run_attention_block(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
+        attn_block4 = run_attention_block(ctx, max(5, args.steps // 10), max(2, args.warmup // 5), tokens=4)
     ctx.close()
 
     t, n, k, m, desc = WORKLOADS[args.workload]
@@ -543,6 +552,10 @@ def main():
                                   "hbm_frac": round(attn_block["gbs"] / HBM_PEAK_GBS, 4),
                                   "weight_bytes": attn_block["weight_bytes"], "kv_bytes": attn_block["kv_bytes"],
                                   "cached_tokens": attn_block["cached"]}
+    if attn_block4 is not None:
+        out["attention_block_4_tokens"] = {"us": round(attn_block4["us_per_block"], 2),
+                                           "us_per_token": round(attn_block4["us_per_token"], 2),
+                                           "cached_tokens": attn_block4["cached"]}
     if attn is not None:
         out["attention_decode"] = {"us": round(attn["us_per_step"], 2), "kv_gbs": round(attn["gbs"], 1),
                                    "hbm_frac": round(attn["gbs"] / HBM_PEAK_GBS, 4), **attn["geometry"]}

@@ -1509,17 +1509,25 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
         return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer (x 16-byte, others 4-byte)");
     }
     if (cache->capacity - cache->length < m) return fail(ctx, OQ_OVERFLOW, "KV cache capacity exceeded");
-    // the attention launch of every token, and the partial-sum buffer the longest one needs
-    std::vector<oq::AttnLaunch> Ls(m);
-    uint64_t part_floats = 0;
-    for (uint64_t t = 0; t < m; ++t) {
-        if (int rc = attention_shape(ctx, cache, Hq, Ls[t], t)) return rc;
-        part_floats = std::max(part_floats, oq::attention_partial_floats(Hkv, Hq / Hkv, D, Ls[t].nchunks));
+    // the attention of all m tokens in one chunk launch, shaped for the last token (its chunks lay
+    // out every token's partials); a grid too large for one launch runs the tokens one by one
+    oq::AttnLaunch last{};
+    if (int rc = attention_shape(ctx, cache, Hq, last, m - 1)) return rc;
+    const uint64_t part_last = oq::attention_partial_floats(Hkv, Hq / Hkv, D, last.nchunks);
+    const bool batched = m * Hkv * oq::attention_subgroups((uint32_t)(Hq / Hkv)) * last.nchunks <= 0x7FFFFFFFull;
+    std::vector<oq::AttnLaunch> Ls;
+    uint64_t part_floats = batched ? m * part_last : 0;
+    if (!batched) {
+        Ls.resize(m);
+        for (uint64_t t = 0; t < m; ++t) {
+            if (int rc = attention_shape(ctx, cache, Hq, Ls[t], t)) return rc;
+            part_floats = std::max(part_floats, oq::attention_partial_floats(Hkv, Hq / Hkv, D, Ls[t].nchunks));
+        }
     }
-    // workspace: the 15 trace fields with m rows each, the normalised input, the partial sums and
-    // one Q8_K image (m rows of the widest projection input)
+    // workspace: the 15 trace fields with m rows each, the normalised input, the partial sums, one
+    // Q8_K image (m rows of the widest projection input) and the tokens' positions
     const uint64_t row[16] = {2 * Q, KV, KV, Q, KV, Q, Q, Q, E, E, E, F, F, F, E, E};
-    uint64_t off[18], total = 0;
+    uint64_t off[19], total = 0;
     for (int i = 0; i < 16; ++i) {
         off[i] = total;
         total += (m * row[i] + 63) & ~uint64_t(63);
@@ -1528,6 +1536,8 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
     total += (part_floats + 63) & ~uint64_t(63);
     off[17] = total;
     total += (m * (std::max({E, Q, F}) / oq::kQK) * oq::kQ8KBytes / sizeof(float) + 64) & ~uint64_t(63);
+    off[18] = total;
+    total += (m * 3 * sizeof(uint64_t) / sizeof(float) + 63) & ~uint64_t(63);
     if (int rc = ensure_work(ctx, total * sizeof(float))) return rc;
     uint64_t scratch = 0;
     for (const oq_weight* w : {b->q, b->k, b->v, b->out, b->gate, b->up, b->down}) {
@@ -1542,20 +1552,46 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
           *resid = ws + off[9], *post = ws + off[10], *gate = ws + off[11], *up = ws + off[12], *act = ws + off[13],
           *ffn = ws + off[14], *normed = ws + off[15], *part = ws + off[16];
     uint8_t* q8 = reinterpret_cast<uint8_t*>(ws + off[17]);
+    uint64_t* pos_dev = reinterpret_cast<uint64_t*>(ws + off[18]);
     hipStream_t s = ctx->stream;
     auto quantize = [&](const float* in, uint64_t k, std::initializer_list<const oq_weight*> consumers) {
         for (const oq_weight* w : consumers)
             if (needs_q8(w, m)) return oq::launch_quantize_q8k(in, m, k, q8, s);
         return hipSuccess;
     };
-    hipError_t e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m);
+    hipError_t e = hipSuccess;
+    if (batched) e = hipMemcpyAsync(pos_dev, positions, m * 3 * sizeof(uint64_t), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m);
     if (e == hipSuccess) e = quantize(normed, E, {b->q, b->k, b->v});
     if (e == hipSuccess) e = project_rows(ctx, b->q, m, normed, q8, qfull);
     if (e == hipSuccess) e = project_rows(ctx, b->k, m, normed, q8, kp);
     if (e == hipSuccess) e = project_rows(ctx, b->v, m, normed, q8, vp);
-    // the tokens' attention steps in order: token t appends its key and value at row length + t and
-    // attends over the rows before it and itself (the single step's launch, with its head preparation)
-    for (uint64_t t = 0; t < m && e == hipSuccess; ++t) {
+    // the tokens' heads prepared together (token t's key and value appended at row length + t),
+    // then token t attending over the rows up to its own, all tokens in one chunk and one merge
+    // launch; or, when that grid is too large, the single step's launch token by token
+    if (batched && e == hipSuccess) {
+        oq::AttnTokens tk{};
+        tk.tokens = (uint32_t)m;
+        tk.qfull = qfull;
+        tk.kp = kp;
+        tk.vp = vp;
+        tk.q_norm = b->q_norm;
+        tk.k_norm = b->k_norm;
+        tk.eps = b->eps;
+        tk.rope = rps[0];
+        tk.positions = pos_dev;
+        tk.qcur = qcur;
+        tk.kcur = trace ? kcur : nullptr;
+        tk.gate_tok_stride = 2 * Q;
+        last.part = part;
+        last.out = trace ? pregate : nullptr;
+        last.gate = qfull + D;
+        last.gate_stride = (uint32_t)(2 * D);
+        last.gate_s = trace ? gate_s : nullptr;
+        last.gated = gated;
+        e = oq::launch_attention_tokens(last, tk, s);
+    }
+    for (uint64_t t = 0; !batched && t < m && e == hipSuccess; ++t) {
         oq::AttnPrep prep{};
         prep.qfull = qfull + t * 2 * Q;
         prep.kp = kp + t * KV;

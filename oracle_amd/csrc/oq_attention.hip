@@ -68,6 +68,10 @@ struct ChunkArgs {
     uint32_t T, Hkv, rep, chunk, nchunks;
     uint32_t rep_all;     // query heads per KV head
     uint32_t nsub;        // subgroups per KV head, of rep = rep_all / nsub query heads each
+    // consecutive tokens of one launch: token i attends over T + i rows, its queries at q + i *
+    // q_tok_stride and its partials at part_o / part_ml + i * part_tok_stride (one token: 1, 0, 0)
+    uint32_t tokens;
+    uint64_t q_tok_stride, part_tok_stride;
     float scale;
     float* part_o;        // [Hq][D/64][nchunks][64]: one head slice's chunks contiguous
     float* part_ml;       // [Hq][nchunks][2]
@@ -86,7 +90,11 @@ struct ChunkArgs {
 struct MergeArgs {
     const float* part_o;
     const float* part_ml;
-    uint32_t nchunks;
+    uint32_t nchunks;     // chunks of the partials' layout (the last token's)
+    // consecutive tokens (as ChunkArgs): token i's T0 + i rows in chunks of `chunk`, its partials at
+    // + i * part_tok_stride, out / gate_s / gated at + i * out_tok_stride, gate at + i * gate_tok_stride
+    uint32_t tokens, T0, chunk;
+    uint64_t part_tok_stride, out_tok_stride, gate_tok_stride;
     float* out;           // [Hq][D]
     const float* gate;    // gate of head h at gate + h * gate_stride, or null
     uint32_t gate_stride;
@@ -253,15 +261,23 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
     extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t grp = blockIdx.x / a.nchunks;  // (KV head, subgroup)
-    const uint32_t c = blockIdx.x - grp * a.nchunks;
+    const uint32_t per_tok = a.Hkv * a.nsub * a.nchunks;
+    const uint32_t tok = blockIdx.x / per_tok;
+    const uint32_t bid = blockIdx.x - tok * per_tok;
+    const uint32_t grp = bid / a.nchunks;  // (KV head, subgroup)
+    const uint32_t c = bid - grp * a.nchunks;
     const uint32_t g = grp / a.nsub, sub = grp - g * a.nsub;
     const uint64_t h0 = (uint64_t)g * a.rep_all + (uint64_t)sub * a.rep;  // the subgroup's first query head
+    const uint32_t T = a.T + tok;  // this token's rows
     const uint32_t c0 = c * a.chunk;
-    const uint32_t c1 = min(c0 + a.chunk, a.T);
+    if (c0 >= T) return;  // a chunk past this token's rows (the whole workgroup)
+    const uint32_t c1 = min(c0 + a.chunk, T);
     const uint32_t n = c1 - c0;
     const uint32_t rep = a.rep;
-    const uint32_t last = a.T - 1;
+    const uint32_t last = T - 1;
+    const float* const qtok = a.q + (uint64_t)tok * a.q_tok_stride;
+    float* const part_o = a.part_o + (uint64_t)tok * a.part_tok_stride;
+    float* const part_ml = a.part_ml + (uint64_t)tok * a.part_tok_stride;
     float* sc = lds;  // [rep][chunk] scores, then probabilities
 
     // rows t of the cache; the new token's rows from new_k / new_v when given (an F32 cache only:
@@ -280,7 +296,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
     };
 
     // the append: subgroup 0's chunk holding the new token stores its key and value row
-    if (a.new_k != nullptr && c1 == a.T && sub == 0) {
+    if (a.new_k != nullptr && c1 == T && sub == 0) {
         for (uint32_t i = threadIdx.x; i < (uint32_t)D; i += kAttnThreads) {
             keys[((uint64_t)last * a.Hkv + g) * D + i] = IO::store(a.new_k[(uint64_t)g * D + i]);
             values[((uint64_t)last * a.Hkv + g) * D + i] = IO::store(a.new_v[(uint64_t)g * D + i]);
@@ -295,7 +311,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
     // takes rows w, w + 4, ..  Their loads go out before the key rows, so waiting for them does not
     // wait for the keys.
     constexpr int kPrepRows = PREP ? (REP + kAttnWaves) / kAttnWaves : 1;
-    const bool holds_new = c1 == a.T;
+    const bool holds_new = c1 == T;
     const uint32_t prep_rows = rep + (holds_new ? 1u : 0u);
     float px[kPrepRows][VW], pw[kPrepRows][VW];
     if constexpr (PREP) {
@@ -315,7 +331,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
 #pragma unroll
         for (int h = 0; h < REP; ++h) {
             const uint32_t hh = (uint32_t)h < rep ? (uint32_t)h : 0u;
-            const float4* qp = reinterpret_cast<const float4*>(a.q + (h0 + hh) * D);
+            const float4* qp = reinterpret_cast<const float4*>(qtok + (h0 + hh) * D);
 #pragma unroll
             for (int j = 0; j < NV; ++j) qr[h][j] = qp[j * 16 + l16];
         }
@@ -449,7 +465,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
         }
         l = wave_sum(l);
         if (lane == 0) {
-            float* ml = a.part_ml + ((h0 + h) * a.nchunks + c) * 2;
+            float* ml = part_ml + ((h0 + h) * a.nchunks + c) * 2;
             ml[0] = m;
             ml[1] = l;
         }
@@ -503,7 +519,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
 #pragma unroll
         for (int w = 1; w < kAttnWaves; ++w) s += red[(uint32_t)w * rep * D + i];
         const uint32_t h = i / D, slice = (i % D) / 64;
-        a.part_o[(((h0 + h) * (D / 64) + slice) * a.nchunks + c) * 64 + (i % 64)] = s;
+        part_o[(((h0 + h) * (D / 64) + slice) * a.nchunks + c) * 64 + (i % 64)] = s;
     }
 }
 
@@ -522,16 +538,21 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
     constexpr int SLICES = D / 64;
     __shared__ float4 s_o[kMergeGroups][16];
     __shared__ float s_m[kMergeGroups], s_l[kMergeGroups];
+    const uint32_t tok = blockIdx.y;
     const uint32_t h = blockIdx.x / SLICES, slice = blockIdx.x - h * SLICES;
     const int col = threadIdx.x & 15, grp = threadIdx.x >> 4;
-    const float* mlp = a.part_ml + (uint64_t)h * a.nchunks * 2;                     // [nchunks][2]
-    const float* op = a.part_o + ((uint64_t)h * SLICES + slice) * a.nchunks * 64;  // [nchunks][64]
+    // this token's chunks (its rows T0 + tok in chunks of `chunk`; one token: the layout's)
+    const uint32_t nch = a.tokens > 1 ? (a.T0 + tok + a.chunk - 1) / a.chunk : a.nchunks;
+    const uint64_t ptok = (uint64_t)tok * a.part_tok_stride;
+    const float* mlp = a.part_ml + ptok + (uint64_t)h * a.nchunks * 2;                     // [nchunks][2]
+    const float* op = a.part_o + ptok + ((uint64_t)h * SLICES + slice) * a.nchunks * 64;  // [nchunks][64]
     constexpr uint32_t kPass = kMergeGroups * kMergeUnroll;  // chunks per pass of the workgroup
-    const uint64_t base = (uint64_t)h * D + slice * 64 + (uint64_t)col * 4;
+    const uint64_t base = (uint64_t)tok * a.out_tok_stride + (uint64_t)h * D + slice * 64 + (uint64_t)col * 4;
     // the block's output gate, needed last, requested first
     float4 gv = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.gate != nullptr && grp == 0)
-        gv = *reinterpret_cast<const float4*>(a.gate + (uint64_t)h * a.gate_stride + slice * 64 + col * 4);
+        gv = *reinterpret_cast<const float4*>(a.gate + (uint64_t)tok * a.gate_tok_stride + (uint64_t)h * a.gate_stride +
+                                              slice * 64 + col * 4);
     // the first pass's chunk maxima and sums, then its value slices, all requested before any
     // use (loads complete in order: M waits only for the maxima)
     float2 ml[kMergeUnroll];
@@ -539,13 +560,13 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
 #pragma unroll
     for (int u = 0; u < kMergeUnroll; ++u) {
         uint32_t c = (uint32_t)grp + (uint32_t)u * kMergeGroups;
-        c = c < a.nchunks ? c : a.nchunks - 1;
+        c = c < nch ? c : nch - 1;
         ml[u] = *reinterpret_cast<const float2*>(mlp + (uint64_t)c * 2);
     }
 #pragma unroll
     for (int u = 0; u < kMergeUnroll; ++u) {
         uint32_t c = (uint32_t)grp + (uint32_t)u * kMergeGroups;
-        c = c < a.nchunks ? c : a.nchunks - 1;
+        c = c < nch ? c : nch - 1;
         oc[u] = reinterpret_cast<const float4*>(op + (uint64_t)c * 64)[col];
     }
     // 1. M = the largest chunk maximum (every chunk holds at least one token: m_c is finite);
@@ -553,7 +574,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
     float m = ml[0].x;
 #pragma unroll
     for (int u = 1; u < kMergeUnroll; ++u) m = fmaxf(m, ml[u].x);
-    for (uint32_t c = (uint32_t)grp + kPass; c < a.nchunks; c += kMergeGroups)
+    for (uint32_t c = (uint32_t)grp + kPass; c < nch; c += kMergeGroups)
         m = fmaxf(m, mlp[(uint64_t)c * 2]);
     if (col == 0) s_m[grp] = m;
     __syncthreads();
@@ -566,7 +587,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
     float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < kMergeUnroll; ++u) {
-        const bool in = (uint32_t)grp + (uint32_t)u * kMergeGroups < a.nchunks;
+        const bool in = (uint32_t)grp + (uint32_t)u * kMergeGroups < nch;
         const float wgt = in ? expf(ml[u].x - M) : 0.0f;
         l = fmaf(wgt, ml[u].y, l);
         o.x = fmaf(wgt, oc[u].x, o.x);
@@ -574,7 +595,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
         o.z = fmaf(wgt, oc[u].z, o.z);
         o.w = fmaf(wgt, oc[u].w, o.w);
     }
-    for (uint32_t c = (uint32_t)grp + kPass; c < a.nchunks; c += kMergeGroups) {
+    for (uint32_t c = (uint32_t)grp + kPass; c < nch; c += kMergeGroups) {
         const float2 v = *reinterpret_cast<const float2*>(mlp + (uint64_t)c * 2);
         const float4 ov = reinterpret_cast<const float4*>(op + (uint64_t)c * 64)[col];
         const float wgt = expf(v.x - M);
@@ -609,6 +630,70 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- several tokens
+//
+// The per-head preparation of consecutive tokens in one launch, one wave per (token, row): row r <
+// Hq is query head r, the rest key head r - Hq.  The arithmetic is the chunk kernel's preparation
+// (prep_row_norm, the rotation with rope_cs), so each row gets the same bits; queries go to qcur,
+// keys (and their tokens' value rows) into cache row row0 + token, kcur when given.
+struct TokPrepArgs {
+    const float *qfull, *kp, *vp;
+    uint64_t qfull_tok_stride, kv_tok_stride;
+    const float *q_norm, *k_norm;
+    float eps;
+    RopeParams rope;
+    const uint64_t* positions;  // [tokens][3]
+    uint32_t Hq, Hkv;
+    uint64_t row0;
+    void *keys, *values;
+    float *qcur, *kcur;
+};
+
+template <typename KT, int D>
+__global__ __launch_bounds__(64) void attention_prep_tokens_kernel(TokPrepArgs a) {
+    constexpr int VW = D / 64;
+    __shared__ float row[D];
+    __shared__ float rc[256];
+    const int lane = threadIdx.x;
+    const uint32_t t = blockIdx.y, r = blockIdx.x;
+    const bool is_q = r < a.Hq;
+    const uint32_t h = is_q ? r : r - a.Hq;
+    const float* src = is_q ? a.qfull + (uint64_t)t * a.qfull_tok_stride + (uint64_t)h * 2 * D
+                            : a.kp + (uint64_t)t * a.kv_tok_stride + (uint64_t)h * D;
+    const float* w = is_q ? a.q_norm : a.k_norm;
+    float px[VW], pw[VW];
+    Vec<VW>::unpack(*reinterpret_cast<const typename Vec<VW>::type*>(src + lane * VW), px);
+#pragma unroll
+    for (int e = 0; e < VW; ++e) pw[e] = w[lane * VW + e];
+    RopeParams p = a.rope;
+    p.pos[0] = a.positions[3 * (uint64_t)t];
+    p.pos[1] = a.positions[3 * (uint64_t)t + 1];
+    p.pos[2] = a.positions[3 * (uint64_t)t + 2];
+    const uint32_t half = p.rotary_dim / 2;
+    for (uint32_t f = (uint32_t)lane; f < half; f += 64) rope_cs(f, p, rc[f], rc[128 + f]);
+    prep_row_norm<D>(px, pw, a.eps, lane, row);
+    __syncthreads();
+    for (uint32_t f = (uint32_t)lane; f < half; f += 64) rotate_pair(row, f, half, rc[f], rc[128 + f]);
+    __syncthreads();
+    if (is_q) {
+        float* dst = a.qcur + ((uint64_t)t * a.Hq + h) * D;
+#pragma unroll
+        for (int e = 0; e < VW; ++e) dst[lane * VW + e] = row[lane * VW + e];
+        return;
+    }
+    using IO = KvIo<KT, VW>;
+    KT* krow = static_cast<KT*>(a.keys) + ((a.row0 + t) * a.Hkv + h) * D;
+    KT* vrow = static_cast<KT*>(a.values) + ((a.row0 + t) * a.Hkv + h) * D;
+    const float* vsrc = a.vp + (uint64_t)t * a.kv_tok_stride + (uint64_t)h * D;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+        const uint32_t i = (uint32_t)lane * VW + e;
+        if (a.kcur != nullptr) a.kcur[((uint64_t)t * a.Hkv + h) * D + i] = row[i];
+        krow[i] = IO::store(row[i]);
+        vrow[i] = IO::store(vsrc[i]);
+    }
+}
+
 // ---------------------------------------------------------------- RoPE
 
 OQ_DEVICE void rope_pair(float* x, uint32_t f, uint32_t half, const RopeParams& p) {
@@ -625,7 +710,7 @@ __global__ __launch_bounds__(256) void rope_kernel(float* heads, uint32_t head_d
 
 template <typename KT, int D, int REP, int NB, bool ONE>
 hipError_t launch_nb(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
-    const dim3 grid(a.Hkv * a.nsub * a.nchunks);
+    const dim3 grid(std::max(a.tokens, 1u) * a.Hkv * a.nsub * a.nchunks);
     if (a.qfull != nullptr) {
         hipLaunchKernelGGL((attention_chunk_kernel<KT, D, REP, NB, true, ONE>), grid, dim3(kAttnThreads), lds, s, a);
     } else {
@@ -729,7 +814,88 @@ hipError_t launch_d(const AttnLaunch& L, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <int D>
+hipError_t launch_tokens_d(const AttnLaunch& L, const AttnTokens& tk, hipStream_t s) {
+    const uint32_t T0 = L.T - (tk.tokens - 1);  // rows of the first token
+    TokPrepArgs pa{};
+    pa.qfull = tk.qfull;
+    pa.kp = tk.kp;
+    pa.vp = tk.vp;
+    pa.qfull_tok_stride = (uint64_t)L.Hkv * L.rep * 2 * D;
+    pa.kv_tok_stride = (uint64_t)L.Hkv * D;
+    pa.q_norm = tk.q_norm;
+    pa.k_norm = tk.k_norm;
+    pa.eps = tk.eps;
+    pa.rope = tk.rope;
+    pa.positions = tk.positions;
+    pa.Hq = L.Hkv * L.rep;
+    pa.Hkv = L.Hkv;
+    pa.row0 = T0 - 1;
+    pa.keys = L.keys;
+    pa.values = L.values;
+    pa.qcur = tk.qcur;
+    pa.kcur = tk.kcur;
+    const dim3 pgrid(pa.Hq + pa.Hkv, tk.tokens);
+    if (L.f16) hipLaunchKernelGGL((attention_prep_tokens_kernel<_Float16, D>), pgrid, dim3(64), 0, s, pa);
+    else hipLaunchKernelGGL((attention_prep_tokens_kernel<float, D>), pgrid, dim3(64), 0, s, pa);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+
+    ChunkArgs a{};
+    a.q = tk.qcur;
+    a.keys = L.keys;
+    a.values = L.values;
+    a.T = T0;
+    a.Hkv = L.Hkv;
+    a.rep_all = L.rep;
+    a.nsub = attention_subgroups(L.rep);
+    a.rep = L.rep / a.nsub;
+    a.chunk = L.chunk;
+    a.nchunks = L.nchunks;
+    a.scale = L.scale;
+    a.tokens = tk.tokens;
+    a.q_tok_stride = (uint64_t)L.Hkv * L.rep * D;
+    a.part_tok_stride = attention_partial_floats(L.Hkv, L.rep, D, L.nchunks);
+    a.part_o = L.part;
+    a.part_ml = L.part + (uint64_t)L.Hkv * L.nchunks * L.rep * D;
+    a.stage = std::max(a.rep * L.chunk, (uint32_t)kAttnWaves * a.rep * D);
+    const uint64_t lds = (uint64_t)a.stage * sizeof(float);
+    e = L.f16 ? launch_reps<_Float16, D>(a, lds, s) : launch_reps<float, D>(a, lds, s);
+    if (e != hipSuccess) return e;
+
+    MergeArgs m{};
+    m.part_o = a.part_o;
+    m.part_ml = a.part_ml;
+    m.nchunks = L.nchunks;
+    m.tokens = tk.tokens;
+    m.T0 = T0;
+    m.chunk = L.chunk;
+    m.part_tok_stride = a.part_tok_stride;
+    m.out_tok_stride = (uint64_t)L.Hkv * L.rep * D;
+    m.gate_tok_stride = tk.gate_tok_stride;
+    m.out = L.out;
+    m.gate = L.gate;
+    m.gate_stride = L.gate_stride;
+    m.gate_s = L.gate_s;
+    m.gated = L.gated;
+    const dim3 mgrid(L.Hkv * L.rep * (D / 64), tk.tokens);
+    if (L.nchunks <= 2 * kMergeGroups) hipLaunchKernelGGL((attention_merge_kernel<D, 2>), mgrid, dim3(256), 0, s, m);
+    else if (L.nchunks <= 4 * kMergeGroups) hipLaunchKernelGGL((attention_merge_kernel<D, 4>), mgrid, dim3(256), 0, s, m);
+    else hipLaunchKernelGGL((attention_merge_kernel<D, 8>), mgrid, dim3(256), 0, s, m);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_attention_tokens(const AttnLaunch& L, const AttnTokens& tk, hipStream_t s) {
+    if (tk.tokens == 0 || tk.tokens > L.T) return hipErrorInvalidValue;
+    switch (L.D) {
+        case 64: return launch_tokens_d<64>(L, tk, s);
+        case 128: return launch_tokens_d<128>(L, tk, s);
+        case 256: return launch_tokens_d<256>(L, tk, s);
+        default: return hipErrorInvalidValue;
+    }
+}
 
 bool attention_dims_supported(uint64_t head_dim, uint64_t rep) {
     return (head_dim == 64 || head_dim == 128 || head_dim == 256) && rep >= 1 && rep <= kAttnMaxRep;

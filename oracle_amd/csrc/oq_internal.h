@@ -201,6 +201,23 @@ void attention_plan(uint64_t T, uint64_t Hkv, uint64_t rep, uint32_t& chunk, uin
 uint64_t attention_partial_floats(uint64_t Hkv, uint64_t rep, uint64_t head_dim, uint32_t nchunks);
 constexpr uint32_t kAttnMaxChunks = 8192;
 hipError_t launch_attention(const AttnLaunch& a, hipStream_t s);
+// Several consecutive tokens of the decoder block (L shaped for the last token: T = its rows, the
+// partials `tokens` times attention_partial_floats(...) floats, out / gate / gate_s / gated for
+// token 0).  Three launches: the per-head preparation of every token (queries to qcur, keys and
+// values into cache rows T - tokens .. T - 1, kcur when given), one chunk launch and one merge
+// launch over all tokens; token i attends over the rows up to its own.
+struct AttnTokens {
+    uint32_t tokens;
+    const float *qfull, *kp, *vp;  // [tokens][Hq][2D], [tokens][Hkv][D], [tokens][Hkv][D]
+    const float *q_norm, *k_norm;
+    float eps;
+    RopeParams rope;               // rotary_dim, sections and base (positions from `positions`)
+    const uint64_t* positions;     // device [tokens][3]
+    float* qcur;                   // [tokens][Hq][D]: the prepared queries
+    float* kcur;                   // [tokens][Hkv][D] or null
+    uint64_t gate_tok_stride;      // floats between the tokens' output gates
+};
+hipError_t launch_attention_tokens(const AttnLaunch& L, const AttnTokens& tk, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* src, void* dst, uint64_t n, hipStream_t s);  // round to nearest even
 hipError_t launch_rope(float* heads, uint64_t n_heads, uint64_t head_dim, const RopeParams& p, hipStream_t s);
 

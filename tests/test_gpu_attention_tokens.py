@@ -6,7 +6,9 @@ tokens through one block, against the oracle's restatement of the reference bloc
 Per token, every traced stage is checked as tests/test_gpu_attention.py checks the single step,
 from the device's own inputs to it: the cache before token t is the cache before the call with the
 device's appended rows of the earlier tokens (the appended rows are checked bit for bit against the
-token's traced key and value).  Below 16 tokens the call gives m single steps' bits
+token's traced key and value).  The call prepares every token's heads in one launch and attends for
+all tokens in one launch, in chunks laid out for the last token; below 16 tokens its appended rows
+are m single steps' bits and its outputs agree with theirs as the attention bar allows
 (test_block_steps_equal_single_steps).
 """
 
@@ -125,8 +127,10 @@ def test_block_tokens_full_block_matrix_cores(ctx, env):
 
 
 def test_block_steps_equal_single_steps(ctx):
-    """Below 16 tokens the call's kernels per token are the single step's per-stage schedule
-    (OQ_BLOCK_FUSED=0): m single steps give the same bits, outputs and cache."""
+    """Below 16 tokens the projections are the single step's per-stage kernels (OQ_BLOCK_FUSED=0)
+    and the head preparation is the single step's arithmetic: the appended cache rows equal m single
+    steps' bit for bit.  Attention sums over other chunk boundaries (the call's chunks are laid out
+    for its last token), so the outputs agree within the wiring bound."""
     d, w, vec, c, xs, positions = inputs("rep1_d64", 4, 9300)
     y, _, keys, values, _ = run_tokens(ctx, d, w, vec, c, positions, xs, trace=False)
     hkv, D = d["kv_heads"], d["head_dim"]
@@ -143,7 +147,8 @@ def test_block_steps_equal_single_steps(ctx):
                 ctx.sync()
                 ys.append(yb.download(np.float32, d["embedding"]))
                 xb.free()
-        assert np.array_equal(np.stack(ys).view(np.uint32), y.view(np.uint32))
+        single = np.stack(ys)
+        assert float(np.max(np.abs(single - y))) <= CHAIN_TOL * float(np.max(np.abs(single)))
         k1, v1 = cache.download(hkv, D, D)
         assert np.array_equal(k1, keys) and np.array_equal(v1, values)
         yb.free()
