@@ -396,8 +396,11 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* block, oq
    m rows to the cache; y_dev [m][E].  Replaces the per-token loop of the reference's multi-token
    evaluation (src/runtime/qwen35_target_multi.cpp:14-25).  The projections stream their weights
    once for all m tokens (m >= 16: the matrix-core path of oq_matmul, with its precision contract;
-   below 16: the small-batch integer-dot products); token t's attention step appends its key and
-   value at row size + t and attends over every row up to it, as the single step does.  trace_dev,
+   below 16: the small-batch integer-dot products).  Every token's heads are prepared in one launch
+   with the single step's arithmetic (token t's key and value appended at row size + t, bit for bit
+   the single step's), then one attention launch over all tokens, token t attending over every row
+   up to its own; its chunks are laid out for the last token, so attention outputs agree with m
+   single steps within the attention bound, not bit for bit.  trace_dev,
    if not NULL, receives m traces of oq_attention_block_step's layout, one after the other.
    Checks as oq_attention_block_step, every position, m in 1..65535, and size + m <= capacity
    (OQ_OVERFLOW, "KV cache capacity exceeded"), all before any device work. */
