@@ -32,7 +32,7 @@ constexpr const char* kKnobNames[kKnobCount] = {
     "OQ_GEMV_WG_PER_CU", "OQ_STREAM_WG_PER_CU",  "OQ_GEMV_STREAM", "OQ_STREAM_WAVES",  "OQ_GEMV_STREAM_MT",
     "OQ_GEMV_ROWS",     "OQ_GEMV_WAVES",         "OQ_GEMV_ROWS_MT", "OQ_BLOCK_STREAM", "OQ_BLOCK_FUSED",
     "OQ_GEMM_MFMA",     "OQ_FUSED_QUANT",        "OQ_GEMM_INT8",   "OQ_ATTN_WG_PER_CU", "OQ_ATTN_MIN_CHUNK",
-    "OQ_GEMM_MIN_K",
+    "OQ_GEMM_MIN_K",    "OQ_ATTN_SHARE_MIN",
 };
 
 struct KnobTable {

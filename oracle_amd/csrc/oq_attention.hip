@@ -72,6 +72,9 @@ struct ChunkArgs {
     // q_tok_stride and its partials at part_o / part_ml + i * part_tok_stride (one token: 1, 0, 0)
     uint32_t tokens;
     uint64_t q_tok_stride, part_tok_stride;
+    // a workgroup serves tpw consecutive tokens with `heads` query heads each: its query rows are
+    // (token i, head j) in order, row i * heads + j, rep = tpw * heads of them (one token: 1, rep)
+    uint32_t tpw, heads;
     float scale;
     float* part_o;        // [Hq][D/64][nchunks][64]: one head slice's chunks contiguous
     float* part_ml;       // [Hq][nchunks][2]
@@ -261,23 +264,29 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
     extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t per_tok = a.Hkv * a.nsub * a.nchunks;
-    const uint32_t tok = blockIdx.x / per_tok;
-    const uint32_t bid = blockIdx.x - tok * per_tok;
+    const uint32_t tpw = a.tpw > 0 ? a.tpw : 1u;
+    const uint32_t heads = a.tpw > 0 ? a.heads : a.rep;
+    const uint32_t per_tg = a.Hkv * a.nsub * a.nchunks;
+    const uint32_t tg = blockIdx.x / per_tg;  // the workgroup's group of tokens
+    const uint32_t bid = blockIdx.x - tg * per_tg;
     const uint32_t grp = bid / a.nchunks;  // (KV head, subgroup)
     const uint32_t c = bid - grp * a.nchunks;
     const uint32_t g = grp / a.nsub, sub = grp - g * a.nsub;
-    const uint64_t h0 = (uint64_t)g * a.rep_all + (uint64_t)sub * a.rep;  // the subgroup's first query head
-    const uint32_t T = a.T + tok;  // this token's rows
+    const uint64_t h0 = (uint64_t)g * a.rep_all + (uint64_t)sub * heads;  // the subgroup's first query head
+    const uint32_t t0 = tg * tpw;                                        // the group's first token
+    const uint32_t ntok = min(tpw, max(a.tokens, 1u) - t0);
+    const uint32_t T = a.T + t0 + ntok - 1;  // the rows of the group's last token
     const uint32_t c0 = c * a.chunk;
-    if (c0 >= T) return;  // a chunk past this token's rows (the whole workgroup)
+    if (c0 >= T) return;  // a chunk past every token's rows (the whole workgroup)
     const uint32_t c1 = min(c0 + a.chunk, T);
     const uint32_t n = c1 - c0;
-    const uint32_t rep = a.rep;
+    const uint32_t rep = ntok * heads;  // query rows
     const uint32_t last = T - 1;
-    const float* const qtok = a.q + (uint64_t)tok * a.q_tok_stride;
-    float* const part_o = a.part_o + (uint64_t)tok * a.part_tok_stride;
-    float* const part_ml = a.part_ml + (uint64_t)tok * a.part_tok_stride;
+    // row r: token t0 + r / heads (rows a.T + that token), query head h0 + r % heads.  A row whose
+    // token's rows end before c1 scores -inf past them; a chunk past them all yields partials its
+    // token's merge never reads (it reads the chunks up to its rows only).
+    auto row_tok = [&](uint32_t r) { return t0 + r / heads; };
+    auto row_head = [&](uint32_t r) { return h0 + (r % heads); };
     float* sc = lds;  // [rep][chunk] scores, then probabilities
 
     // rows t of the cache; the new token's rows from new_k / new_v when given (an F32 cache only:
@@ -331,7 +340,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
 #pragma unroll
         for (int h = 0; h < REP; ++h) {
             const uint32_t hh = (uint32_t)h < rep ? (uint32_t)h : 0u;
-            const float4* qp = reinterpret_cast<const float4*>(qtok + (h0 + hh) * D);
+            const float4* qp = reinterpret_cast<const float4*>(a.q + (uint64_t)row_tok(hh) * a.q_tok_stride + row_head(hh) * D);
 #pragma unroll
             for (int j = 0; j < NV; ++j) qr[h][j] = qp[j * 16 + l16];
         }
@@ -412,7 +421,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                     float v = acc[0];
 #pragma unroll
                     for (int h = 1; h < REP; ++h) v = l16 == h ? acc[h] : v;
-                    sc[(uint32_t)l16 * a.chunk + (t - c0)] = v * a.scale;
+                    const uint32_t lim = a.T + row_tok((uint32_t)l16);  // rows of the row's token
+                    sc[(uint32_t)l16 * a.chunk + (t - c0)] = t < lim ? v * a.scale : -INFINITY;
                 }
                 if constexpr (decltype(reload)::value) load_keys(kb[b], pb + NB * kTokStep);
             }
@@ -465,7 +475,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
         }
         l = wave_sum(l);
         if (lane == 0) {
-            float* ml = part_ml + ((h0 + h) * a.nchunks + c) * 2;
+            float* ml = a.part_ml + (uint64_t)row_tok(h) * a.part_tok_stride + (row_head(h) * a.nchunks + c) * 2;
             ml[0] = m;
             ml[1] = l;
         }
@@ -519,7 +529,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
 #pragma unroll
         for (int w = 1; w < kAttnWaves; ++w) s += red[(uint32_t)w * rep * D + i];
         const uint32_t h = i / D, slice = (i % D) / 64;
-        part_o[(((h0 + h) * (D / 64) + slice) * a.nchunks + c) * 64 + (i % 64)] = s;
+        a.part_o[(uint64_t)row_tok(h) * a.part_tok_stride + ((row_head(h) * (D / 64) + slice) * a.nchunks + c) * 64 +
+                 (i % 64)] = s;
     }
 }
 
@@ -710,7 +721,9 @@ __global__ __launch_bounds__(256) void rope_kernel(float* heads, uint32_t head_d
 
 template <typename KT, int D, int REP, int NB, bool ONE>
 hipError_t launch_nb(const ChunkArgs& a, uint64_t lds, hipStream_t s) {
-    const dim3 grid(std::max(a.tokens, 1u) * a.Hkv * a.nsub * a.nchunks);
+    const uint32_t tpw = std::max(a.tpw, 1u);
+    const uint32_t groups = (std::max(a.tokens, 1u) + tpw - 1) / tpw;  // token groups
+    const dim3 grid(groups * a.Hkv * a.nsub * a.nchunks);
     if (a.qfull != nullptr) {
         hipLaunchKernelGGL((attention_chunk_kernel<KT, D, REP, NB, true, ONE>), grid, dim3(kAttnThreads), lds, s, a);
     } else {
@@ -755,6 +768,8 @@ hipError_t launch_d(const AttnLaunch& L, hipStream_t s) {
     a.rep_all = L.rep;
     a.nsub = attention_subgroups(L.rep);
     a.rep = L.rep / a.nsub;
+    a.tpw = 1;
+    a.heads = a.rep;
     a.chunk = L.chunk;
     a.nchunks = L.nchunks;
     a.scale = L.scale;
@@ -849,7 +864,12 @@ hipError_t launch_tokens_d(const AttnLaunch& L, const AttnTokens& tk, hipStream_
     a.Hkv = L.Hkv;
     a.rep_all = L.rep;
     a.nsub = attention_subgroups(L.rep);
-    a.rep = L.rep / a.nsub;
+    // over long caches, as many tokens per workgroup as its 8 query rows hold: each key and value row
+    // read once for them (shorter caches keep one token per workgroup: twice the workgroups)
+    a.heads = L.rep / a.nsub;
+    const bool share = L.T >= (uint32_t)std::max(0, knob(kAttnShareMin, 8192));
+    a.tpw = share ? std::min<uint32_t>(tk.tokens, std::max<uint32_t>(1, 8 / a.heads)) : 1u;
+    a.rep = a.tpw * a.heads;
     a.chunk = L.chunk;
     a.nchunks = L.nchunks;
     a.scale = L.scale;

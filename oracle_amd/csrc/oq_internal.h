@@ -60,6 +60,7 @@ enum Knob : int {
     kAttnWgPerCu,  // OQ_ATTN_WG_PER_CU
     kAttnMinChunk,  // OQ_ATTN_MIN_CHUNK
     kGemmMinK,  // OQ_GEMM_MIN_K: shortest rows (K) of the matrix-core path (default 4096; measurement only)
+    kAttnShareMin,  // OQ_ATTN_SHARE_MIN: cached rows from which a multi-token attention workgroup serves several tokens
     kKnobCount
 };
 int knob(Knob k, int fallback);  // the option's value, or fallback when it is unset

@@ -72,11 +72,19 @@ def run_tokens(ctx, d, w, vec, c, positions, xs, trace=True, dtype="f32"):
         blk.release()
 
 
+# OQ_ATTN_SHARE_MIN=0: workgroups serve as many tokens as their 8 query rows hold at any cache
+# length (by default only from 8192 cached rows): 4 tokens per workgroup with 1 query head per KV
+# head, 3 with 2, 2 with 4, 1 with 8 or 16
+SHARE = [{}, {"OQ_ATTN_SHARE_MIN": "0"}]
+
+
+@pytest.mark.parametrize("env", SHARE, ids=["default", "shared_rows"])
 @pytest.mark.parametrize("name,m", [("rep1_d64", 4), ("mixed", 3), ("empty_rep8", 5), ("e2048", 2), ("rep16", 3)])
-def test_block_tokens_match_oracle(ctx, name, m):
+def test_block_tokens_match_oracle(ctx, name, m, env):
     d, w, vec, c, xs, positions = inputs(name, m, 9100 + m)
     n0 = c.length
-    y, traces, keys, values, length = run_tokens(ctx, d, w, vec, c, positions, xs)
+    with oracle_amd.launch_options(env):
+        y, traces, keys, values, length = run_tokens(ctx, d, w, vec, c, positions, xs)
     assert length == n0 + m
     assert np.array_equal(keys[:n0], c.keys[:n0]) and np.array_equal(values[:n0], c.values[:n0])
     own = c.copy()
@@ -93,12 +101,14 @@ def test_block_tokens_match_oracle(ctx, name, m):
 DOMINATED_TOL = 1.5e-3
 
 
-def test_block_tokens_f16_cache(ctx):
+@pytest.mark.parametrize("env", SHARE, ids=["default", "shared_rows"])
+def test_block_tokens_f16_cache(ctx, env):
     """m tokens over an F16 cache: each token's stages, its key and value appended rounded, and
     every later token attending over the rounded rows."""
     d, w, vec, c, xs, positions = inputs("e2048", 4, 9500)
     n0 = c.length
-    y, traces, keys, values, length = run_tokens(ctx, d, w, vec, c, positions, xs, dtype="f16")
+    with oracle_amd.launch_options(env):
+        y, traces, keys, values, length = run_tokens(ctx, d, w, vec, c, positions, xs, dtype="f16")
     assert length == n0 + 4
     assert np.array_equal(keys[:n0], f16(c.keys[:n0])) and np.array_equal(values[:n0], f16(c.values[:n0]))
     for t in range(4):
