@@ -472,16 +472,17 @@ def main():
     secondary = block = block4 = attn = attn16 = attn_block = attn_block4 = None
     configs = {}
     if not args.no_secondary and args.workload == "q4k_gemv":
-        secondary = run_gpu(ctx, "q4k_down_m512", max(5, args.steps // 4), max(2, args.warmup // 5))
-        # the other single-GPU configurations, each with its own roofline
+        # the other single-GPU configurations, each with its own roofline; steps of a few to a few
+        # hundred microseconds, so at least 10-50 of them (a millisecond or two of GPU time each)
+        secondary = run_gpu(ctx, "q4k_down_m512", max(10, args.steps // 2), max(3, args.warmup))
         for name in ("q8_0_gemv", "q6k_head", "q4k_down_m4"):
-            configs[name] = run_gpu(ctx, name, max(5, args.steps // 4), max(2, args.warmup // 5))
-        block = run_deltanet(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
-        block4 = run_deltanet(ctx, max(5, args.steps // 10), max(2, args.warmup // 5), tokens=4)
-        attn = run_attention(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
-        attn16 = run_attention(ctx, max(5, args.steps // 10), max(2, args.warmup // 5), kv_dtype="f16")
-        attn_block = run_attention_block(ctx, max(5, args.steps // 10), max(2, args.warmup // 5))
-        attn_block4 = run_attention_block(ctx, max(5, args.steps // 10), max(2, args.warmup // 5), tokens=4)
+            configs[name] = run_gpu(ctx, name, max(50, args.steps), max(5, args.warmup))
+        block = run_deltanet(ctx, max(20, args.steps), max(5, args.warmup))
+        block4 = run_deltanet(ctx, max(20, args.steps), max(5, args.warmup), tokens=4)
+        attn = run_attention(ctx, max(20, args.steps), max(5, args.warmup))
+        attn16 = run_attention(ctx, max(20, args.steps), max(5, args.warmup), kv_dtype="f16")
+        attn_block = run_attention_block(ctx, max(20, args.steps), max(5, args.warmup))
+        attn_block4 = run_attention_block(ctx, max(20, args.steps), max(5, args.warmup), tokens=4)
     ctx.close()
 
     t, n, k, m, desc = WORKLOADS[args.workload]
