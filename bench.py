@@ -266,7 +266,7 @@ def run_attention(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, kv_dty
             "copies": ncopies, "geometry": g}
 
 
-def run_attention_block(ctx, steps, warmup, cached=4096, copies_min_bytes=MALL_DEFEAT_BYTES, tokens=1):
+def run_attention_block(ctx, steps, warmup, cached=4096, copies_min_bytes=MALL_DEFEAT_BYTES, tokens=1, kv_dtype="f32"):
     """One full-attention decode block (hidden 4096, 16 query heads over 4 KV heads of 256, FFN
     12288) over 4096 cached tokens per step (oq_attention_block_step; with tokens > 1, that many
     consecutive tokens per step through oq_attention_block_steps); steps cycle over block copies
@@ -275,12 +275,12 @@ def run_attention_block(ctx, steps, warmup, cached=4096, copies_min_bytes=MALL_D
     d, w, vec, keys, values, x = synth.attention_block(rng, cached=cached)
     first = oracle_amd.AttentionBlockWeights(ctx, d, w, vec)
     wb = first.weight_bytes()
-    kvb = keys.nbytes + values.nbytes
+    kvb = (keys.nbytes + values.nbytes) // (2 if kv_dtype == "f16" else 1)
     ncopies = max(1, math.ceil(copies_min_bytes / (wb + kvb)))
     blocks = [first] + [oracle_amd.AttentionBlockWeights(ctx, d, w, vec) for _ in range(ncopies - 1)]
     caches = []
     for _ in range(ncopies):
-        c = ctx.kv_cache(cached + tokens, d["kv_heads"], d["head_dim"], d["head_dim"])
+        c = ctx.kv_cache(cached + tokens, d["kv_heads"], d["head_dim"], d["head_dim"], dtype=kv_dtype)
         c.load(keys, values, cached)
         caches.append(c)
     xs = np.stack([x] + [rng.standard_normal(x.shape).astype(np.float32) for _ in range(tokens - 1)])
@@ -438,7 +438,7 @@ def main():
             "hbm_frac_weight_bytes": round(r["weight_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
         return
     if args.workload == "attention_block":
-        r = run_attention_block(ctx, args.steps, args.warmup, tokens=args.tokens)
+        r = run_attention_block(ctx, args.steps, args.warmup, tokens=args.tokens, kv_dtype=args.kv)
         ctx.close()
         print(json.dumps({
             "metric": "attention decode block GB/s (weights + KV cache)", "value": round(r["gbs"], 2), "unit": "GB/s",

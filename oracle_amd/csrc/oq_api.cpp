@@ -1439,6 +1439,11 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_
     const bool fused_tail = knob_flag(oq::kBlockFused, true) && even && oq::gemv_block_supported(outp) &&
                             oq::gemv_block_supported(ffn_in) && oq::gemv_block_supported(down);
     if (fused_in) {
+        if (cache->type == OQ_TYPE_F16) {
+            // the projection stores the new value row of an F16 cache itself (no append launch)
+            in.v16 = static_cast<_Float16*>(cache->values) + cache->length * Hkv * D;
+            prep.v_stored = true;
+        }
         e = oq::launch_gemv_block(oq::kBlockIn, in, s);
     } else {
         e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s);

@@ -797,10 +797,11 @@ hipError_t launch_d(const AttnLaunch& L, hipStream_t s) {
     if (L.f16) {
         // the new token's rows (with the preparation folded in, its value row only: the key is
         // prepared and stored by the chunk kernel) rounded into the cache before the chunk kernel
-        if (a.new_k != nullptr || a.new_v != nullptr) {
+        const float* nv = L.prep != nullptr && L.prep->v_stored ? nullptr : a.new_v;  // stored by the projection
+        if (a.new_k != nullptr || nv != nullptr) {
             const uint32_t n = L.Hkv * (uint32_t)D;
             const uint64_t row = (uint64_t)(L.T - 1) * L.Hkv * D;
-            hipLaunchKernelGGL(kv_append_f16_kernel, dim3((n + 255) / 256), dim3(256), 0, s, a.new_k, a.new_v,
+            hipLaunchKernelGGL(kv_append_f16_kernel, dim3((n + 255) / 256), dim3(256), 0, s, a.new_k, nv,
                                static_cast<_Float16*>(L.keys) + row, static_cast<_Float16*>(L.values) + row, n);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }

@@ -149,6 +149,7 @@ OQ_DEVICE void blk_epilogue(const BlockGemv& a, uint64_t grp, int lane, float v0
             blk_in_row(a, row, mi, l);
             const float v = r == 0 ? v0 : v1;
             if (lane == r && a.raw[mi] != nullptr) a.raw[mi][l] = v;
+            if (lane == r && mi == 2 && a.v16 != nullptr) a.v16[l] = (_Float16)v;
             if (mi == 0 && a.conv_w != nullptr) {
                 // causal depthwise convolution step of channel l (reference_kernels.cpp:197-225) +
                 // SiLU: the history shifts by one (tap i takes value i + 1, the last tap the new
@@ -523,6 +524,7 @@ __global__ __launch_bounds__(1024) void gemv_block_in_stream_kernel(BlockGemv a)
         const uint32_t local = row - (mi ? a.row_end[mi - 1] : 0u);
         float* dst = mi == 0 ? a.raw[0] : mi == 1 ? a.raw[1] : mi == 2 ? a.raw[2] : a.raw[3];
         dst[local] = v;
+        if (mi == 2 && a.v16 != nullptr) a.v16[local] = (_Float16)v;
     };
     const int q = lane & 3;
     const ScaleSel ss = scale_sel(q);

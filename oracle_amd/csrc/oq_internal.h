@@ -177,6 +177,7 @@ struct AttnPrep {
     float eps;
     RopeParams rope;
     float *qcur, *kcur;           // [Hq][D], [Hkv][D], or null (not stored)
+    bool v_stored;                // an F16 cache's new value row already stored (by the projection)
 };
 struct AttnLaunch {
     const float* q;            // [Hkv * rep][D]
@@ -233,6 +234,8 @@ struct BlockGemv {
     float eps;
     float* norm_out;       // the normalised activation (written by workgroup 0) or null
     float* raw[4];         // per-matrix outputs (or null: not stored; the attention block's IN needs them)
+    _Float16* v16;         // IN: when not null, matrix 2's outputs also stored rounded to binary16 here
+                           // (the new value row of an F16 KV cache)
     const float* conv_w;   // IN: convolution taps [rows of mat[0]][conv_kernel]
     float* history;        // IN: convolution history, same shape, updated in place
     uint32_t conv_kernel;
