@@ -156,33 +156,59 @@ struct HalfVec<4> {
     }
 };
 
-// Loads of cache rows of element type KT: K4 holds a lane's 4 consecutive key elements, V its VW
-// value elements, both as loaded; k4 / unpack_v convert at the point of use.  round gives the
-// value a cache element holds for an F32 value, store the element itself.
+// Loads of cache rows of element type KT.  A lane of a 16-lane key group holds NV = D / 64 pieces
+// of 4 key elements, piece j being the row's 4-element piece q_index(j, l16) (the query slices
+// in registers follow the same map); the pieces arrive in NK loads of type K, kept raw until
+// unpack_k converts them.  V holds a lane's VW value elements as loaded, unpack_v converts them.
+// round gives the value a cache element holds for an F32 value, store the element itself.
 template <typename KT, int VW>
 struct KvIo;
 template <int VW>
 struct KvIo<float, VW> {
-    using K4 = float4;
+    static constexpr int NV = VW, NK = VW;  // one 16-byte load per piece
+    using K = float4;
     using V = typename Vec<VW>::type;
-    OQ_DEVICE static K4 load_k(const float* row, uint32_t i4) { return load_stream(reinterpret_cast<const float4*>(row) + i4); }
-    OQ_DEVICE static float4 k4(K4 v) { return v; }
+    OQ_DEVICE static uint32_t q_index(int j, int l16) { return 16u * (uint32_t)j + (uint32_t)l16; }
+    OQ_DEVICE static K load_k(const float* row, int j, int l16) {
+        return load_stream(reinterpret_cast<const float4*>(row) + q_index(j, l16));
+    }
+    OQ_DEVICE static void unpack_k(const K (&k)[NK], float4 (&f)[NV]) {
+#pragma unroll
+        for (int j = 0; j < NK; ++j) f[j] = k[j];
+    }
     OQ_DEVICE static V load_v(const float* row, int lane) { return load_stream(reinterpret_cast<const V*>(row) + lane); }
     OQ_DEVICE static void unpack_v(V v, float* o) { Vec<VW>::unpack(v, o); }
     OQ_DEVICE static float round(float x) { return x; }
     OQ_DEVICE static float store(float x) { return x; }
 };
+// binary16: rows of 128 elements or more load 8 halves (16 bytes) per lane, two pieces per load
+// (pieces 2i and 2i + 1 = 4-element pieces 2 (16 i + l16) and + 1); rows of 64, 4 halves
 template <int VW>
 struct KvIo<_Float16, VW> {
-    using K4 = uint2;
+    static constexpr bool kWide = VW >= 2;
+    static constexpr int NV = VW, NK = kWide ? VW / 2 : VW;
+    using K = std::conditional_t<kWide, uint4, uint2>;
     using V = typename HalfVec<VW>::type;
-    OQ_DEVICE static K4 load_k(const _Float16* row, uint32_t i4) {
-        return load_stream(reinterpret_cast<const uint2*>(row) + i4);
+    OQ_DEVICE static uint32_t q_index(int j, int l16) {
+        return kWide ? 2u * (16u * (uint32_t)(j >> 1) + (uint32_t)l16) + (uint32_t)(j & 1) : 16u * (uint32_t)j + (uint32_t)l16;
     }
-    OQ_DEVICE static float4 k4(K4 v) {
-        float o[4];
-        HalfVec<4>::unpack(v, o);
-        return make_float4(o[0], o[1], o[2], o[3]);
+    OQ_DEVICE static K load_k(const _Float16* row, int i, int l16) {
+        return load_stream(reinterpret_cast<const K*>(row) + 16 * i + l16);
+    }
+    OQ_DEVICE static void unpack_k(const K (&k)[NK], float4 (&f)[NV]) {
+#pragma unroll
+        for (int i = 0; i < NK; ++i) {
+            float o[8];
+            if constexpr (kWide) {
+                HalfVec<4>::unpack(make_uint2(k[i].x, k[i].y), o);
+                HalfVec<4>::unpack(make_uint2(k[i].z, k[i].w), o + 4);
+                f[2 * i] = make_float4(o[0], o[1], o[2], o[3]);
+                f[2 * i + 1] = make_float4(o[4], o[5], o[6], o[7]);
+            } else {
+                HalfVec<4>::unpack(k[i], o);
+                f[i] = make_float4(o[0], o[1], o[2], o[3]);
+            }
+        }
     }
     OQ_DEVICE static V load_v(const _Float16* row, int lane) { return load_stream(reinterpret_cast<const V*>(row) + lane); }
     OQ_DEVICE static void unpack_v(V v, float* o) { HalfVec<VW>::unpack(v, o); }
@@ -342,18 +368,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
             const uint32_t hh = (uint32_t)h < rep ? (uint32_t)h : 0u;
             const float4* qp = reinterpret_cast<const float4*>(a.q + (uint64_t)row_tok(hh) * a.q_tok_stride + row_head(hh) * D);
 #pragma unroll
-            for (int j = 0; j < NV; ++j) qr[h][j] = qp[j * 16 + l16];
+            for (int j = 0; j < NV; ++j) qr[h][j] = qp[IO::q_index(j, l16)];
         }
     }
     const uint32_t first = c0 + (uint32_t)wave * 4u;  // this wave's first pass (wave-uniform)
-    auto load_keys = [&](typename IO::K4 (&dst)[NV], uint32_t pass_base) {
+    auto load_keys = [&](typename IO::K (&dst)[IO::NK], uint32_t pass_base) {
         const uint32_t t = pass_base + (uint32_t)(lane >> 4);
         const KT* kp = key_row(t < c1 ? t : c1 - 1);
 #pragma unroll
-        for (int j = 0; j < NV; ++j) dst[j] = IO::load_k(kp, (uint32_t)(j * 16 + l16));
+        for (int j = 0; j < IO::NK; ++j) dst[j] = IO::load_k(kp, j, l16);
     };
     {
-        typename IO::K4 kb[NB][NV];
+        typename IO::K kb[NB][IO::NK];
 #pragma unroll
         for (int b = 0; b < NB; ++b) load_keys(kb[b], first + (uint32_t)b * kTokStep);
         if constexpr (PREP) {
@@ -378,7 +404,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
             for (int h = 0; h < REP; ++h) {
                 const uint32_t hh = (uint32_t)h < rep ? (uint32_t)h : 0u;
 #pragma unroll
-                for (int j = 0; j < NV; ++j) qr[h][j] = *reinterpret_cast<const float4*>(stage + hh * D + 4 * (j * 16 + l16));
+                for (int j = 0; j < NV; ++j) qr[h][j] = *reinterpret_cast<const float4*>(stage + hh * D + 4 * IO::q_index(j, l16));
             }
             // the trace's copies, and the append of the new key and value rows
             if (c == 0 && a.qcur != nullptr) {
@@ -401,8 +427,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
                 const uint32_t t = pb + (uint32_t)(lane >> 4);
                 float acc[REP];
                 float4 kf[NV];
-#pragma unroll
-                for (int j = 0; j < NV; ++j) kf[j] = IO::k4(kb[b][j]);
+                IO::unpack_k(kb[b], kf);
 #pragma unroll
                 for (int h = 0; h < REP; ++h) {
                     float sum = 0.0f;
