@@ -558,6 +558,34 @@ hipError_t project_rows(oq_context* ctx, const oq_weight* w, uint64_t m, const f
     return oq::launch_gemv_f32act(w->m, (int)m, x, y, ctx->stream);
 }
 
+// The same m rows through several matrices: one small-batch launch for matrices it can take
+// together (K-quant, one type, K and pitch, none on matrix cores; 2 <= m <= 15), else one product
+// each.  Each output row has the same bits either way.
+hipError_t project_set(oq_context* ctx, std::initializer_list<std::pair<const oq_weight*, float*>> ps, uint64_t m,
+                       const float* x, const uint8_t* q8) {
+    if (m >= 2 && m <= 15 && ps.size() >= 2 && ps.size() <= 4 && knob_flag(oq::kBlockFused, true)) {
+        oq::DeviceMatrix mats[4];
+        float* ys[4];
+        uint32_t n = 0;
+        bool together = true;
+        for (const auto& p : ps) {
+            together = together && is_kquant(p.first->m.type) && !on_matrix_cores(p.first, m, true);
+            mats[n] = p.first->m;
+            ys[n] = p.second;
+            ++n;
+        }
+        if (together) {
+            const hipError_t e = oq::launch_gemv_kquant_set(mats, n, (int)m, q8, ys, ctx->stream);
+            if (e != hipErrorNotSupported) return e;
+        }
+    }
+    for (const auto& p : ps) {
+        const hipError_t e = project_rows(ctx, p.first, m, x, q8, p.second);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 bool needs_q8(const oq_weight* w, uint64_t m, bool mfma = true) {
     return is_kquant(w->m.type) && !on_matrix_cores(w, m, mfma);
 }
@@ -623,10 +651,7 @@ int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, floa
     };
     hipError_t e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m);
     if (e == hipSuccess) e = quantize(normed, E, {b->qkv, b->z, b->beta, b->alpha});
-    if (e == hipSuccess) e = project_rows(ctx, b->qkv, m, normed, q8, qkv);
-    if (e == hipSuccess) e = project_rows(ctx, b->z, m, normed, q8, z);
-    if (e == hipSuccess) e = project_rows(ctx, b->beta, m, normed, q8, beta);
-    if (e == hipSuccess) e = project_rows(ctx, b->alpha, m, normed, q8, alpha);
+    if (e == hipSuccess) e = project_set(ctx, {{b->qkv, qkv}, {b->z, z}, {b->beta, beta}, {b->alpha, alpha}}, m, normed, q8);
     if (e == hipSuccess)
         e = oq::launch_conv_gates_tokens(qkv, b->conv_weight, hist, C, K, beta, alpha, b->dt_bias, b->decay, Hv, m,
                                          conv, beta_s, log_decay, s);
@@ -642,8 +667,7 @@ int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, floa
     if (e == hipSuccess) e = project_rows(ctx, b->out, m, gated, q8, branch, false);
     if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m);
     if (e == hipSuccess) e = quantize(post, E, {b->gate, b->up});
-    if (e == hipSuccess) e = project_rows(ctx, b->gate, m, post, q8, gate);
-    if (e == hipSuccess) e = project_rows(ctx, b->up, m, post, q8, up);
+    if (e == hipSuccess) e = project_set(ctx, {{b->gate, gate}, {b->up, up}}, m, post, q8);
     if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s);
     if (e == hipSuccess) e = quantize(act, F, {b->down});
     if (e == hipSuccess) e = project_rows(ctx, b->down, m, act, q8, ffn);
@@ -1568,9 +1592,7 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
     if (batched) e = hipMemcpyAsync(pos_dev, positions, m * 3 * sizeof(uint64_t), hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m);
     if (e == hipSuccess) e = quantize(normed, E, {b->q, b->k, b->v});
-    if (e == hipSuccess) e = project_rows(ctx, b->q, m, normed, q8, qfull);
-    if (e == hipSuccess) e = project_rows(ctx, b->k, m, normed, q8, kp);
-    if (e == hipSuccess) e = project_rows(ctx, b->v, m, normed, q8, vp);
+    if (e == hipSuccess) e = project_set(ctx, {{b->q, qfull}, {b->k, kp}, {b->v, vp}}, m, normed, q8);
     // the tokens' heads prepared together (token t's key and value appended at row length + t),
     // then token t attending over the rows up to its own, all tokens in one chunk and one merge
     // launch; or, when that grid is too large, the single step's launch token by token
@@ -1621,8 +1643,7 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
     if (e == hipSuccess) e = project_rows(ctx, b->out, m, gated, q8, branch);
     if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m);
     if (e == hipSuccess) e = quantize(post, E, {b->gate, b->up});
-    if (e == hipSuccess) e = project_rows(ctx, b->gate, m, post, q8, gate);
-    if (e == hipSuccess) e = project_rows(ctx, b->up, m, post, q8, up);
+    if (e == hipSuccess) e = project_set(ctx, {{b->gate, gate}, {b->up, up}}, m, post, q8);
     if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s);
     if (e == hipSuccess) e = quantize(act, F, {b->down});
     if (e == hipSuccess) e = project_rows(ctx, b->down, m, act, q8, ffn);

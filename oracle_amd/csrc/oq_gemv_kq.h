@@ -735,23 +735,48 @@ OQ_DEVICE void stage_rows_once(const ActLds& s, int m, const float* x, const uin
 // workgroups stage the m rows' Q8_K blocks in LDS once, a wave walks its weight rows one pass at
 // a time with one pass in flight, decodes each pass once and multiplies it with the m activation
 // slices read from LDS.  Per-lane sums in the order of gemv_kq_kernel (pass, then row mi) and the
-// same row reductions: the same bits.
+// same row reductions: the same bits.  With set.nmat > 0 the rows are those of up to four
+// matrices of w's type, K and pitch, concatenated (MtSet), each writing its own outputs: the same
+// bits per row as one launch per matrix.
 template <uint32_t TYPE, int ITERS, int MT, bool FUSED, bool FULL>
 __global__ __launch_bounds__(1024) void gemv_stream_mt_kernel(DeviceMatrix w, int m, const float* x, const uint8_t* q8k,
-                                                              float* __restrict__ y) {
+                                                              float* __restrict__ y, MtSet set) {
     constexpr int WAVES = 16;
     using WR = typename WRegs<TYPE>::type;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave_in_wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nw = gridDim.x * WAVES;
-    const uint32_t n = (uint32_t)w.n;
+    const uint32_t n = set.nmat > 0 ? set.row_end[set.nmat - 1] : (uint32_t)w.n;
     const uint32_t nsb = (uint32_t)(w.k / kQK);
     const ActLds s{smem, w.k};
     const uint32_t first = blockIdx.x * WAVES + (uint32_t)wave_in_wg;
+    // matrix of row r in a set (selects, not an indexed kernel-argument array)
+    auto set_mat = [&](uint32_t r) {
+        uint32_t i = 0;
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            if ((uint32_t)j + 1 < set.nmat && r >= set.row_end[j]) i = (uint32_t)j + 1;
+        return i;
+    };
+    auto set_start = [&](uint32_t i) { return i == 0 ? 0u : i == 1 ? set.row_end[0] : i == 2 ? set.row_end[1] : set.row_end[2]; };
     auto row_base = [&](uint32_t row) {
         row = row < n ? row : n - 1;
-        return w.base + (uint64_t)__builtin_amdgcn_readfirstlane(row) * w.pitch;
+        row = __builtin_amdgcn_readfirstlane(row);
+        if (set.nmat == 0) return w.base + (uint64_t)row * w.pitch;
+        const uint32_t i = set_mat(row);
+        const uint8_t* b = i == 0 ? set.base[0] : i == 1 ? set.base[1] : i == 2 ? set.base[2] : set.base[3];
+        return b + (uint64_t)(row - set_start(i)) * w.pitch;
+    };
+    auto store = [&](uint32_t r, int mi, float v) {
+        if (set.nmat == 0) {
+            y[(uint64_t)mi * n + r] = v;
+            return;
+        }
+        const uint32_t i = set_mat(r), start = set_start(i);
+        const uint32_t rows = (i == 0 ? set.row_end[0] : i == 1 ? set.row_end[1] : i == 2 ? set.row_end[2] : set.row_end[3]) - start;
+        float* yi = i == 0 ? set.y[0] : i == 1 ? set.y[1] : i == 2 ? set.y[2] : set.y[3];
+        yi[(uint64_t)mi * rows + (r - start)] = v;
     };
 
     WR buf[2];
@@ -813,7 +838,7 @@ __global__ __launch_bounds__(1024) void gemv_stream_mt_kernel(DeviceMatrix w, in
                 if ((done & 63u) == 0u) {
 #pragma unroll
                     for (int mi = 0; mi < MT; ++mi)
-                        if (mi < m) y[(uint64_t)mi * n + out_row] = out[mi];
+                        if (mi < m) store(out_row, mi, out[mi]);
                 }
             }
             row = nrow;
@@ -824,7 +849,7 @@ __global__ __launch_bounds__(1024) void gemv_stream_mt_kernel(DeviceMatrix w, in
     if ((uint32_t)lane < (done & 63u)) {
 #pragma unroll
         for (int mi = 0; mi < MT; ++mi)
-            if (mi < m) y[(uint64_t)mi * n + out_row] = out[mi];
+            if (mi < m) store(out_row, mi, out[mi]);
     }
 }
 
@@ -1074,14 +1099,48 @@ hipError_t launch_argmax_iters(const DeviceMatrix& w, const float* x, const uint
 }
 
 template <uint32_t TYPE, int ITERS, int MT, bool FUSED, bool FULL>
-hipError_t launch_stream_mt(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s) {
+hipError_t launch_stream_mt(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s,
+                            const MtSet& set = MtSet{}) {
     const uint64_t lds = act_lds_bytes(w.k, MT);
     uint64_t wgs = (uint64_t)cu_count();
-    const uint64_t need = (w.n + 15) / 16;
+    const uint64_t rows = set.nmat > 0 ? set.row_end[set.nmat - 1] : w.n;
+    const uint64_t need = (rows + 15) / 16;
     if (wgs > need) wgs = need;
     hipLaunchKernelGGL((gemv_stream_mt_kernel<TYPE, ITERS, MT, FUSED, FULL>), dim3((unsigned)wgs), dim3(1024), lds, s,
-                       w, m, x, q8k, y);
+                       w, m, x, q8k, y, set);
     return hipGetLastError();
+}
+
+// A set of matrices through the streamed small-batch kernel (Q8_K activations): hipErrorNotSupported
+// where that kernel is not the one launch_rows would choose for this m, K and type
+template <uint32_t TYPE, int ITERS, int MT>
+hipError_t launch_set_rows(const DeviceMatrix& w, int m, const uint8_t* q8k, const MtSet& set, hipStream_t s) {
+    if constexpr (MT > 1 && !(TYPE == 13 && MT == 8)) {
+        if (act_lds_bytes(w.k, MT) <= kLdsBudget && knob(kGemvStreamMt, 1) != 0) {
+            return (w.k / kQK) % 16 == 0 ? launch_stream_mt<TYPE, ITERS, MT, false, true>(w, m, nullptr, q8k, nullptr, s, set)
+                                         : launch_stream_mt<TYPE, ITERS, MT, false, false>(w, m, nullptr, q8k, nullptr, s, set);
+        }
+    }
+    return hipErrorNotSupported;
+}
+
+template <uint32_t TYPE, int MT>
+hipError_t launch_set_iters(const DeviceMatrix& w, int m, const uint8_t* q8k, const MtSet& set, hipStream_t s) {
+    switch ((w.k / kQK + 15) / 16) {
+        case 1: return launch_set_rows<TYPE, 1, MT>(w, m, q8k, set, s);
+        case 2: return launch_set_rows<TYPE, 2, MT>(w, m, q8k, set, s);
+        case 3: return launch_set_rows<TYPE, 3, MT>(w, m, q8k, set, s);
+        case 4: return launch_set_rows<TYPE, 4, MT>(w, m, q8k, set, s);
+        default: return hipErrorNotSupported;
+    }
+}
+
+template <uint32_t TYPE>
+hipError_t launch_set_m(const DeviceMatrix& w, int m, const uint8_t* q8k, const MtSet& set, hipStream_t s) {
+    if (m <= 1) return hipErrorNotSupported;
+    if (m <= 2) return launch_set_iters<TYPE, 2>(w, m, q8k, set, s);
+    if (m <= 4) return launch_set_iters<TYPE, 4>(w, m, q8k, set, s);
+    return launch_set_iters<TYPE, 8>(w, m, q8k, set, s);
 }
 
 template <uint32_t TYPE, int ITERS, int MT, bool FUSED>

@@ -67,6 +67,54 @@ hipError_t launch_gemv_kquant_argmax(const DeviceMatrix& w, const float* x, cons
     }
 }
 
+hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m, const uint8_t* q8k, float* const* ys,
+                                  hipStream_t s) {
+    if (nmat < 1 || nmat > 4 || m < 2 || m > 15) return hipErrorNotSupported;
+    const DeviceMatrix& w = mats[0];
+    if (!gemv_kquant_supported(w) || !short_rows(w)) return hipErrorNotSupported;
+    uint64_t rows = 0;
+    for (uint32_t i = 0; i < nmat; ++i) {
+        if (mats[i].type != w.type || mats[i].k != w.k || mats[i].pitch != w.pitch) return hipErrorNotSupported;
+        rows += mats[i].n;
+    }
+    if (rows > 0xFFFFFFFFull) return hipErrorNotSupported;
+    const uint64_t nsb = w.k / kQK;
+    // activation rows per launch, as launch_gemv_kquant: what fits the LDS budget, at most 8
+    int chunk = 8;
+    while (chunk > 1 && kq::act_lds_bytes(w.k, chunk) > kq::kLdsBudget) chunk >>= 1;
+    for (int m0 = 0; m0 < m; m0 += chunk) {
+        const int mc = m - m0 < chunk ? m - m0 : chunk;
+        MtSet set{};
+        set.nmat = nmat;
+        uint32_t end = 0;
+        for (uint32_t i = 0; i < nmat; ++i) {
+            set.base[i] = mats[i].base;
+            set.y[i] = ys[i] + (uint64_t)m0 * mats[i].n;
+            end += (uint32_t)mats[i].n;
+            set.row_end[i] = end;
+        }
+        const uint8_t* q = q8k + (uint64_t)m0 * nsb * kQ8KBytes;
+        hipError_t e;
+        switch (w.type) {
+            case 12: e = kq::launch_set_m<12>(w, mc, q, set, s); break;
+            case 13: e = kq::launch_set_m<13>(w, mc, q, set, s); break;
+            case 14: e = kq::launch_set_m<14>(w, mc, q, set, s); break;
+            default: e = hipErrorNotSupported;
+        }
+        // the first chunk refused: nothing launched, the caller multiplies the matrices one by one;
+        // a later chunk the set kernel does not cover (one row left) runs matrix by matrix here
+        if (e == hipErrorNotSupported && m0 > 0) {
+            for (uint32_t i = 0; i < nmat; ++i) {
+                e = launch_gemv_kquant(mats[i], mc, nullptr, q, ys[i] + (uint64_t)m0 * mats[i].n, s);
+                if (e != hipSuccess) return e;
+            }
+            continue;
+        }
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
                               hipStream_t s) {
     if (!gemv_kquant_supported(w)) return hipErrorNotSupported;

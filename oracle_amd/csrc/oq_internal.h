@@ -80,6 +80,20 @@ hipError_t launch_quantize_q8k(const float* x, uint64_t m, uint64_t k, uint8_t* 
 // Q8_K activations given as blocks (q8k) or as F32 (x, quantized by every workgroup into LDS;
 // bit-identical to launch_quantize_q8k).
 bool gemv_kquant_supported(const DeviceMatrix& w);
+// Up to four matrices of one type, K and pitch multiplied by the same activation rows in one launch
+// of the small-batch kernel: their rows concatenated (matrix i holds rows [row_end[i - 1],
+// row_end[i])), matrix i's outputs at y[i][mi * rows_i + local row].  nmat == 0: a single matrix.
+struct MtSet {
+    const uint8_t* base[4];
+    float* y[4];
+    uint32_t row_end[4];
+    uint32_t nmat;
+};
+// mats[0 .. nmat) from m (2 .. 15) rows of Q8_K blocks, in one launch per 8 activation rows:
+// hipErrorNotSupported when the streamed small-batch kernel does not apply (the caller multiplies
+// the matrices one by one; each row's bits are the same either way)
+hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m, const uint8_t* q8k, float* const* ys,
+                                  hipStream_t s);
 hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k,
                               float* y, hipStream_t s);
 int gemv_max_m();

@@ -25,20 +25,27 @@ RAW="$OUT/raw_$WL$TAG"
 COPY_BYTES=28311552
 SECONDARY=""
 [ "$WL" = "q4k_gemv" ] && SECONDARY="--no-secondary"
+# workloads that are a bench workload with options
+BWL=$WL
+case "$WL" in
+    attention_decode_f16) BWL="attention_decode --kv f16" ;;
+    attention_block_4_tokens) BWL="attention_block --tokens 4" ;;
+    deltanet_block_4_tokens) BWL="deltanet_block --tokens 4" ;;
+esac
 
 # the headline workload is traced in the shape the default run times it (20 steps after 5 warmup
 # steps, every secondary workload after it); the others in 200 steps after 20
 if [ "$WL" = "q4k_gemv" ]; then
     TRACE_CMD="rocprofv3 --kernel-trace --stats --output-format csv -d $RAW/trace -o run -- python3 bench.py --workload $WL --steps 20 --warmup 5 --no-cpu"
 else
-    TRACE_CMD="rocprofv3 --kernel-trace --stats --output-format csv -d $RAW/trace -o run -- python3 bench.py --workload $WL --steps 200 --warmup 20 --no-cpu $SECONDARY"
+    TRACE_CMD="rocprofv3 --kernel-trace --stats --output-format csv -d $RAW/trace -o run -- python3 bench.py --workload $BWL --steps 200 --warmup 20 --no-cpu $SECONDARY"
 fi
 echo "trace: $TRACE_CMD"
 timeout -k 10 300 $TRACE_CMD > "$RAW.trace.log" 2>&1
 for C in FETCH_SIZE WRITE_SIZE; do
     echo "pmc $C"
     timeout -s KILL 60 rocprofv3 --pmc $C --output-format csv -d "$RAW/$C" -o run -- \
-        python3 bench.py --workload "$WL" --steps 20 --warmup 2 --no-cpu $SECONDARY > "$RAW.$C.log" 2>&1
+        python3 bench.py --workload $BWL --steps 20 --warmup 2 --no-cpu $SECONDARY > "$RAW.$C.log" 2>&1
     timeout -s KILL 60 rocprofv3 --pmc $C --output-format csv -d "$RAW/copy_$C" -o run -- \
         python3 bench.py --workload copy_calibration --steps 20 > "$RAW.copy_$C.log" 2>&1
 done
@@ -85,7 +92,7 @@ if [ "${4:-}" = "mfma" ]; then
         if [ $PASS = 1 ]; then C=$P1; else C=$P2; fi
         echo "pmc pass $PASS"
         timeout -s KILL 90 rocprofv3 --pmc $C --output-format csv -d "$RAW/mfma$PASS" -o run -- \
-            python3 bench.py --workload "$WL" --steps 10 --warmup 2 --no-cpu $SECONDARY > "$RAW.mfma$PASS.log" 2>&1
+            python3 bench.py --workload $BWL --steps 10 --warmup 2 --no-cpu $SECONDARY > "$RAW.mfma$PASS.log" 2>&1
     done
     python3 -m oracle_amd.profsum counters --kernel "$KERN" "$RAW/mfma1" "$RAW/mfma2" > "$OUT/${WL}${TAG}_counters.json"
     echo "wrote $OUT/${WL}${TAG}_counters.json"
