@@ -643,14 +643,15 @@ int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, floa
     double* head_ss = reinterpret_cast<double*>(ws + off[17]);
     uint8_t* q8 = reinterpret_cast<uint8_t*>(ws + lay.q8_off);
     hipStream_t s = ctx->stream;
-    // the Q8_K image of one projection input, when a projection of it takes the small-batch GEMV
-    auto quantize = [&](const float* in, uint64_t k, std::initializer_list<const oq_weight*> ws_of_input) {
-        for (const oq_weight* w : ws_of_input)
-            if (needs_q8(w, m)) return oq::launch_quantize_q8k(in, m, k, q8, s);
-        return hipSuccess;
+    // the Q8_K image an input's producer writes beside it, when a projection of it takes the
+    // small-batch GEMV (null: none does)
+    auto q8_for = [&](std::initializer_list<const oq_weight*> consumers) -> uint8_t* {
+        for (const oq_weight* w : consumers)
+            if (needs_q8(w, m)) return q8;
+        return nullptr;
     };
-    hipError_t e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m);
-    if (e == hipSuccess) e = quantize(normed, E, {b->qkv, b->z, b->beta, b->alpha});
+    hipError_t e =
+        oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m, q8_for({b->qkv, b->z, b->beta, b->alpha}));
     if (e == hipSuccess) e = project_set(ctx, {{b->qkv, qkv}, {b->z, z}, {b->beta, beta}, {b->alpha, alpha}}, m, normed, q8);
     if (e == hipSuccess)
         e = oq::launch_conv_gates_tokens(qkv, b->conv_weight, hist, C, K, beta, alpha, b->dt_bias, b->decay, Hv, m,
@@ -665,11 +666,9 @@ int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, floa
     // it keeps the integer-dot products at every m
     if (e == hipSuccess && is_kquant(b->out->m.type)) e = oq::launch_quantize_q8k(gated, m, V, q8, s);
     if (e == hipSuccess) e = project_rows(ctx, b->out, m, gated, q8, branch, false);
-    if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m);
-    if (e == hipSuccess) e = quantize(post, E, {b->gate, b->up});
+    if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m, q8_for({b->gate, b->up}));
     if (e == hipSuccess) e = project_set(ctx, {{b->gate, gate}, {b->up, up}}, m, post, q8);
-    if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s);
-    if (e == hipSuccess) e = quantize(act, F, {b->down});
+    if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s, q8_for({b->down}));
     if (e == hipSuccess) e = project_rows(ctx, b->down, m, act, q8, ffn);
     if (e == hipSuccess) e = oq::launch_add(resid, ffn, m * E, y, s);
     if (e == hipSuccess && trace) {
@@ -1588,10 +1587,16 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
             if (needs_q8(w, m)) return oq::launch_quantize_q8k(in, m, k, q8, s);
         return hipSuccess;
     };
+    // the Q8_K image an input's producer writes beside it, when a projection of it takes the
+    // small-batch GEMV (null: none does)
+    auto q8_for = [&](std::initializer_list<const oq_weight*> consumers) -> uint8_t* {
+        for (const oq_weight* w : consumers)
+            if (needs_q8(w, m)) return q8;
+        return nullptr;
+    };
     hipError_t e = hipSuccess;
     if (batched) e = hipMemcpyAsync(pos_dev, positions, m * 3 * sizeof(uint64_t), hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m);
-    if (e == hipSuccess) e = quantize(normed, E, {b->q, b->k, b->v});
+    if (e == hipSuccess) e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m, q8_for({b->q, b->k, b->v}));
     if (e == hipSuccess) e = project_set(ctx, {{b->q, qfull}, {b->k, kp}, {b->v, vp}}, m, normed, q8);
     // the tokens' heads prepared together (token t's key and value appended at row length + t),
     // then token t attending over the rows up to its own, all tokens in one chunk and one merge
@@ -1641,11 +1646,9 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
     }
     if (e == hipSuccess) e = quantize(gated, Q, {b->out});
     if (e == hipSuccess) e = project_rows(ctx, b->out, m, gated, q8, branch);
-    if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m);
-    if (e == hipSuccess) e = quantize(post, E, {b->gate, b->up});
+    if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m, q8_for({b->gate, b->up}));
     if (e == hipSuccess) e = project_set(ctx, {{b->gate, gate}, {b->up, up}}, m, post, q8);
-    if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s);
-    if (e == hipSuccess) e = quantize(act, F, {b->down});
+    if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s, q8_for({b->down}));
     if (e == hipSuccess) e = project_rows(ctx, b->down, m, act, q8, ffn);
     if (e == hipSuccess) e = oq::launch_add(resid, ffn, m * E, y, s);
     if (e == hipSuccess && trace) {

@@ -247,11 +247,7 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
     const uint64_t blk = blockIdx.x * 4ull + (threadIdx.x >> 6);
     if (blk >= nblocks) return;
     const float4 v = reinterpret_cast<const float4*>(x + blk * kQK)[lane];
-    const Q8KLane r = quantize_q8k_block_wave(v, lane);
-    uint8_t* ob = q8k + blk * kQ8KBytes;
-    *reinterpret_cast<uint32_t*>(ob + 4 + 4 * lane) = r.qword;
-    if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(ob + 260 + 2 * (lane >> 2)) = (int16_t)r.quad_bsum;
-    if (lane == 0) *reinterpret_cast<float*>(ob) = r.d;
+    store_q8k_block(q8k + blk * kQ8KBytes, quantize_q8k_block_wave(v, lane), lane);
 }
 
 hipError_t launch_quantize_q8k(const float* x, uint64_t m, uint64_t k, uint8_t* q8k,

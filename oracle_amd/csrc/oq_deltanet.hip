@@ -60,7 +60,8 @@ OQ_DEVICE double block_sum_f64(double v, double* lds) {
 // sum a + b is also stored to sum_out (the block's residual, qwen35_block.cpp:334).
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                                                const float* __restrict__ w, uint32_t n, float eps,
-                                                               float* __restrict__ sum_out, float* __restrict__ out) {
+                                                               float* __restrict__ sum_out, float* __restrict__ out,
+                                                               uint8_t* __restrict__ q8) {
     __shared__ double red[16];
     // workgroup r normalises row r (rows of n values, consecutive)
     const uint64_t row = (uint64_t)blockIdx.x * n;
@@ -84,6 +85,17 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
         const float v = b ? sum_out[i] : a[i];
         out[i] = v * inv * w[i];
+    }
+    if (q8 != nullptr) {
+        // the row's Q8_K blocks (n a multiple of 256), one wave per block, from the values just
+        // stored: quantize_q8k_kernel's quantization of the same values
+        __syncthreads();
+        const int lane = threadIdx.x & 63;
+        const uint32_t nb = n / kQK;
+        for (uint32_t blk = threadIdx.x >> 6; blk < nb; blk += kNormThreads / 64) {
+            const float4 v = reinterpret_cast<const float4*>(out + (uint64_t)blk * kQK)[lane];
+            store_q8k_block(q8 + ((uint64_t)blockIdx.x * nb + blk) * kQ8KBytes, quantize_q8k_block_wave(v, lane), lane);
+        }
     }
 }
 
@@ -292,6 +304,20 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
     act[i] = silu_ref(gate[i]) * up[i];
 }
 
+// swiglu_kernel's values, and their Q8_K blocks (quantize_q8k_kernel's layout over the n values,
+// n a multiple of 256): one wave per block
+__global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                                         uint64_t nblocks, float* __restrict__ act, uint8_t* __restrict__ q8) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t blk = blockIdx.x * 4ull + (threadIdx.x >> 6);
+    if (blk >= nblocks) return;
+    const uint64_t i = blk * kQK + 4u * (uint32_t)lane;
+    const float4 g = *reinterpret_cast<const float4*>(gate + i), u = *reinterpret_cast<const float4*>(up + i);
+    const float4 v = make_float4(silu_ref(g.x) * u.x, silu_ref(g.y) * u.y, silu_ref(g.z) * u.z, silu_ref(g.w) * u.w);
+    *reinterpret_cast<float4*>(act + i) = v;
+    store_q8k_block(q8 + blk * kQ8KBytes, quantize_q8k_block_wave(v, lane), lane);
+}
+
 // out = a + b (qwen35_block.cpp:188-198)
 __global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ a, const float* __restrict__ b, uint32_t n,
                                                   float* __restrict__ out) {
@@ -310,9 +336,10 @@ bool deltanet_dims_supported(uint64_t key_dim, uint64_t value_dim, uint64_t conv
 }
 
 hipError_t launch_rmsnorm(const float* a, const float* b, const float* w, uint64_t n, float eps, float* sum_out,
-                          float* out, hipStream_t s, uint64_t rows) {
+                          float* out, hipStream_t s, uint64_t rows, uint8_t* q8) {
+    if (q8 != nullptr && n % kQK != 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, s, a, b, w, (uint32_t)n, eps, sum_out,
-                       out);
+                       out, q8);
     return hipGetLastError();
 }
 
@@ -375,7 +402,13 @@ hipError_t launch_gated_norm(const float* rec, const double* head_ss, const floa
 
 uint64_t delta_chunks(uint64_t dv) { return dv / kDeltaCols; }
 
-hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s) {
+hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s, uint8_t* q8) {
+    if (q8 != nullptr) {
+        if (n % kQK != 0) return hipErrorInvalidValue;
+        const uint64_t nblocks = n / kQK;
+        hipLaunchKernelGGL(swiglu_q8k_kernel, dim3(blocks_of(nblocks, 4)), dim3(256), 0, s, gate, up, nblocks, act, q8);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_of(n, 256)), dim3(256), 0, s, gate, up, (uint32_t)n, act);
     return hipGetLastError();
 }

@@ -152,8 +152,9 @@ hipError_t launch_gemm_q4k_i8(const DeviceMatrix& w, int m, const float* x, cons
 // ---- oq_deltanet.hip  (Gated DeltaNet decode block: kernels between the projections)
 bool deltanet_dims_supported(uint64_t key_dim, uint64_t value_dim, uint64_t conv_kernel);
 // rows consecutive rows of n values (one workgroup each)
+// q8, when not null, also receives the rows' Q8_K blocks (n a multiple of 256)
 hipError_t launch_rmsnorm(const float* a, const float* b, const float* w, uint64_t n, float eps, float* sum_out,
-                          float* out, hipStream_t s, uint64_t rows = 1);
+                          float* out, hipStream_t s, uint64_t rows = 1, uint8_t* q8 = nullptr);
 hipError_t launch_conv_gates(const float* qkv, const float* conv_w, float* history, uint64_t channels,
                              uint64_t kernel, const float* beta, const float* alpha, const float* dt_bias,
                              const float* decay, uint64_t heads, float* conv_out, float* beta_s, float* log_decay,
@@ -173,7 +174,8 @@ hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_he
 hipError_t launch_gated_norm(const float* rec, const double* head_ss, const float* z, const float* out_norm,
                              uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s, uint64_t tokens = 1);
 uint64_t delta_chunks(uint64_t dv);  // head_ss entries per head
-hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s);
+// q8, when not null, also receives act's Q8_K blocks (n a multiple of 256)
+hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s, uint8_t* q8 = nullptr);
 hipError_t launch_add(const float* a, const float* b, uint64_t n, float* out, hipStream_t s);
 
 // ---- oq_attention.hip  (full-attention decode: RoPE, the block's head preparation, attention)
