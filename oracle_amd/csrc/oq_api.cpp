@@ -586,6 +586,19 @@ hipError_t project_set(oq_context* ctx, std::initializer_list<std::pair<const oq
     return hipSuccess;
 }
 
+// y = add + w x over m rows: the residual added in the small-batch launch's stores where it takes
+// w (the same bits as a separate sum), else the product into `product` and one add launch
+hipError_t project_add(oq_context* ctx, const oq_weight* w, uint64_t m, const float* x, const uint8_t* q8,
+                       const float* add, float* product, float* y) {
+    if (m >= 2 && m <= 15 && is_kquant(w->m.type) && !on_matrix_cores(w, m, true) && knob_flag(oq::kBlockFused, true)) {
+        const hipError_t e = oq::launch_gemv_kquant_set(&w->m, 1, (int)m, q8, &y, ctx->stream, &add);
+        if (e != hipErrorNotSupported) return e;
+    }
+    hipError_t e = project_rows(ctx, w, m, x, q8, product);
+    if (e == hipSuccess) e = oq::launch_add(add, product, m * w->m.n, y, ctx->stream);
+    return e;
+}
+
 bool needs_q8(const oq_weight* w, uint64_t m, bool mfma = true) {
     return is_kquant(w->m.type) && !on_matrix_cores(w, m, mfma);
 }
@@ -659,18 +672,23 @@ int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, floa
     if (e == hipSuccess)
         e = oq::launch_delta(conv, Hk, Hv, dk, dv, beta_s, log_decay, b->eps, state, rec, head_ss, nullptr, nullptr, s,
                              m);
-    if (e == hipSuccess) e = oq::launch_gated_norm(rec, head_ss, z, b->out_norm, Hv, dv, b->eps, gated, s, m);
     // the out projection's input (RMSNorm(rec) * out_norm * SiLU(z), a product of two near-Gaussian
     // rows) is heavy-tailed -- kurtosis 68 on the hidden-4096 block, one product up to 13 % of
     // sum |w xhat| -- so f16 operands would reach the product bar (2.3e-4 measured at 16 tokens):
-    // it keeps the integer-dot products at every m
-    if (e == hipSuccess && is_kquant(b->out->m.type)) e = oq::launch_quantize_q8k(gated, m, V, q8, s);
+    // it keeps the integer-dot products at every m, from the Q8_K blocks the gated norm writes
+    if (e == hipSuccess)
+        e = oq::launch_gated_norm(rec, head_ss, z, b->out_norm, Hv, dv, b->eps, gated, s, m,
+                                  is_kquant(b->out->m.type) ? q8 : nullptr);
     if (e == hipSuccess) e = project_rows(ctx, b->out, m, gated, q8, branch, false);
     if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m, q8_for({b->gate, b->up}));
     if (e == hipSuccess) e = project_set(ctx, {{b->gate, gate}, {b->up, up}}, m, post, q8);
     if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s, q8_for({b->down}));
-    if (e == hipSuccess) e = project_rows(ctx, b->down, m, act, q8, ffn);
-    if (e == hipSuccess) e = oq::launch_add(resid, ffn, m * E, y, s);
+    if (e == hipSuccess && trace) {
+        e = project_rows(ctx, b->down, m, act, q8, ffn);  // the trace keeps the down projection
+        if (e == hipSuccess) e = oq::launch_add(resid, ffn, m * E, y, s);
+    } else if (e == hipSuccess) {
+        e = project_add(ctx, b->down, m, act, q8, resid, ffn, y);
+    }
     if (e == hipSuccess && trace) {
         // token t's trace (the 16 fields of oq_deltanet_step's trace, in order) at trace + t * size
         uint64_t per_token = 0;
@@ -1595,7 +1613,9 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
         return nullptr;
     };
     hipError_t e = hipSuccess;
-    if (batched) e = hipMemcpyAsync(pos_dev, positions, m * 3 * sizeof(uint64_t), hipMemcpyHostToDevice, s);
+    // the tokens' positions: launch arguments for a few tokens, else a copy to the device
+    const bool pos_inline = m <= oq::kInlineTokenPositions;
+    if (batched && !pos_inline) e = hipMemcpyAsync(pos_dev, positions, m * 3 * sizeof(uint64_t), hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m, q8_for({b->q, b->k, b->v}));
     if (e == hipSuccess) e = project_set(ctx, {{b->q, qfull}, {b->k, kp}, {b->v, vp}}, m, normed, q8);
     // the tokens' heads prepared together (token t's key and value appended at row length + t),
@@ -1611,7 +1631,8 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
         tk.k_norm = b->k_norm;
         tk.eps = b->eps;
         tk.rope = rps[0];
-        tk.positions = pos_dev;
+        tk.positions = pos_inline ? nullptr : pos_dev;
+        tk.positions_host = pos_inline ? positions : nullptr;
         tk.qcur = qcur;
         tk.kcur = trace ? kcur : nullptr;
         tk.gate_tok_stride = 2 * Q;
@@ -1649,8 +1670,12 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
     if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m, q8_for({b->gate, b->up}));
     if (e == hipSuccess) e = project_set(ctx, {{b->gate, gate}, {b->up, up}}, m, post, q8);
     if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s, q8_for({b->down}));
-    if (e == hipSuccess) e = project_rows(ctx, b->down, m, act, q8, ffn);
-    if (e == hipSuccess) e = oq::launch_add(resid, ffn, m * E, y, s);
+    if (e == hipSuccess && trace) {
+        e = project_rows(ctx, b->down, m, act, q8, ffn);  // the trace keeps the down projection
+        if (e == hipSuccess) e = oq::launch_add(resid, ffn, m * E, y, s);
+    } else if (e == hipSuccess) {
+        e = project_add(ctx, b->down, m, act, q8, resid, ffn, y);
+    }
     if (e == hipSuccess && trace) {
         // token t's trace (oq_attention_block_step's 15 fields, in order) at trace + t * size
         uint64_t per_token = 0;

@@ -678,11 +678,12 @@ struct TokPrepArgs {
     const float *q_norm, *k_norm;
     float eps;
     RopeParams rope;
-    const uint64_t* positions;  // [tokens][3]
+    const uint64_t* positions;  // [tokens][3] in device memory, or null: pos below
     uint32_t Hq, Hkv;
     uint64_t row0;
     void *keys, *values;
     float *qcur, *kcur;
+    uint64_t pos[3 * kInlineTokenPositions];  // up to kInlineTokenPositions tokens' positions, by value
 };
 
 template <typename KT, int D>
@@ -702,9 +703,10 @@ __global__ __launch_bounds__(64) void attention_prep_tokens_kernel(TokPrepArgs a
 #pragma unroll
     for (int e = 0; e < VW; ++e) pw[e] = w[lane * VW + e];
     RopeParams p = a.rope;
-    p.pos[0] = a.positions[3 * (uint64_t)t];
-    p.pos[1] = a.positions[3 * (uint64_t)t + 1];
-    p.pos[2] = a.positions[3 * (uint64_t)t + 2];
+    const uint64_t* tp = a.positions != nullptr ? a.positions + 3 * (uint64_t)t : a.pos + 3 * t;
+    p.pos[0] = tp[0];
+    p.pos[1] = tp[1];
+    p.pos[2] = tp[2];
     const uint32_t half = p.rotary_dim / 2;
     for (uint32_t f = (uint32_t)lane; f < half; f += 64) rope_cs(f, p, rc[f], rc[128 + f]);
     prep_row_norm<D>(px, pw, a.eps, lane, row);
@@ -868,7 +870,13 @@ hipError_t launch_tokens_d(const AttnLaunch& L, const AttnTokens& tk, hipStream_
     pa.k_norm = tk.k_norm;
     pa.eps = tk.eps;
     pa.rope = tk.rope;
-    pa.positions = tk.positions;
+    if (tk.positions_host != nullptr && tk.tokens <= kInlineTokenPositions) {
+        for (uint32_t i = 0; i < 3 * tk.tokens; ++i) pa.pos[i] = tk.positions_host[i];
+        pa.positions = nullptr;
+    } else {
+        if (tk.positions == nullptr) return hipErrorInvalidValue;
+        pa.positions = tk.positions;
+    }
     pa.Hq = L.Hkv * L.rep;
     pa.Hkv = L.Hkv;
     pa.row0 = T0 - 1;

@@ -296,6 +296,29 @@ __global__ __launch_bounds__(256) void gated_norm_kernel(const float* __restrict
     gated[i] = rec[i] * inv * out_norm[v] * silu_ref(z[i]);
 }
 
+// gated_norm_kernel's values and their Q8_K blocks (quantize_q8k_kernel's layout; dv a multiple of
+// 64, so a lane's four values lie in one head): one wave per 256 values
+__global__ __launch_bounds__(256) void gated_norm_q8k_kernel(const float* __restrict__ rec, const double* __restrict__ head_ss,
+                                                             const float* __restrict__ z, const float* __restrict__ out_norm,
+                                                             uint64_t nblocks, uint32_t dv, uint32_t chunks, float eps,
+                                                             float* __restrict__ gated, uint8_t* __restrict__ q8) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t blk = blockIdx.x * 4ull + (threadIdx.x >> 6);
+    if (blk >= nblocks) return;
+    const uint64_t i = blk * kQK + 4u * (uint32_t)lane;
+    const uint64_t hv = i / dv;
+    const uint32_t v = (uint32_t)(i % dv);
+    double ss = 0.0;
+    for (uint32_t c = 0; c < chunks; ++c) ss += head_ss[hv * chunks + c];
+    const float inv = (float)(1.0 / sqrt(ss / (double)dv + (double)eps));
+    const float4 r = *reinterpret_cast<const float4*>(rec + i), zz = *reinterpret_cast<const float4*>(z + i);
+    const float* w = out_norm + v;  // a caller's vector: 4-byte alignment only
+    const float4 g = make_float4(r.x * inv * w[0] * silu_ref(zz.x), r.y * inv * w[1] * silu_ref(zz.y),
+                                 r.z * inv * w[2] * silu_ref(zz.z), r.w * inv * w[3] * silu_ref(zz.w));
+    *reinterpret_cast<float4*>(gated + i) = g;
+    store_q8k_block(q8 + blk * kQ8KBytes, quantize_q8k_block_wave(g, lane), lane);
+}
+
 // act = silu(gate) * up (qwen35_block.cpp:313-316)
 __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ gate, const float* __restrict__ up,
                                                      uint32_t n, float* __restrict__ act) {
@@ -393,8 +416,16 @@ hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_he
 }
 
 hipError_t launch_gated_norm(const float* rec, const double* head_ss, const float* z, const float* out_norm,
-                             uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s, uint64_t tokens) {
+                             uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s, uint64_t tokens,
+                             uint8_t* q8) {
     const uint64_t total = tokens * heads * dv;
+    if (q8 != nullptr) {
+        if ((heads * dv) % kQK != 0 || dv % 64 != 0) return hipErrorInvalidValue;
+        const uint64_t nblocks = total / kQK;
+        hipLaunchKernelGGL(gated_norm_q8k_kernel, dim3(blocks_of(nblocks, 4)), dim3(256), 0, s, rec, head_ss, z,
+                           out_norm, nblocks, (uint32_t)dv, (uint32_t)delta_chunks(dv), eps, gated, q8);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(gated_norm_kernel, dim3(blocks_of(total, 256)), dim3(256), 0, s, rec, head_ss, z, out_norm,
                        (uint32_t)total, (uint32_t)dv, (uint32_t)delta_chunks(dv), eps, gated);
     return hipGetLastError();

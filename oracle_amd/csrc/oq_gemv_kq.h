@@ -776,7 +776,9 @@ __global__ __launch_bounds__(1024) void gemv_stream_mt_kernel(DeviceMatrix w, in
         const uint32_t i = set_mat(r), start = set_start(i);
         const uint32_t rows = (i == 0 ? set.row_end[0] : i == 1 ? set.row_end[1] : i == 2 ? set.row_end[2] : set.row_end[3]) - start;
         float* yi = i == 0 ? set.y[0] : i == 1 ? set.y[1] : i == 2 ? set.y[2] : set.y[3];
-        yi[(uint64_t)mi * rows + (r - start)] = v;
+        const float* ai = i == 0 ? set.add[0] : i == 1 ? set.add[1] : i == 2 ? set.add[2] : set.add[3];
+        const uint64_t at = (uint64_t)mi * rows + (r - start);
+        yi[at] = ai != nullptr ? ai[at] + v : v;
     };
 
     WR buf[2];

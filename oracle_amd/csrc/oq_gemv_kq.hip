@@ -68,7 +68,7 @@ hipError_t launch_gemv_kquant_argmax(const DeviceMatrix& w, const float* x, cons
 }
 
 hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m, const uint8_t* q8k, float* const* ys,
-                                  hipStream_t s) {
+                                  hipStream_t s, const float* const* adds) {
     if (nmat < 1 || nmat > 4 || m < 2 || m > 15) return hipErrorNotSupported;
     const DeviceMatrix& w = mats[0];
     if (!gemv_kquant_supported(w) || !short_rows(w)) return hipErrorNotSupported;
@@ -90,6 +90,7 @@ hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m
         for (uint32_t i = 0; i < nmat; ++i) {
             set.base[i] = mats[i].base;
             set.y[i] = ys[i] + (uint64_t)m0 * mats[i].n;
+            set.add[i] = adds != nullptr && adds[i] != nullptr ? adds[i] + (uint64_t)m0 * mats[i].n : nullptr;
             end += (uint32_t)mats[i].n;
             set.row_end[i] = end;
         }
@@ -105,7 +106,9 @@ hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m
         // a later chunk the set kernel does not cover (one row left) runs matrix by matrix here
         if (e == hipErrorNotSupported && m0 > 0) {
             for (uint32_t i = 0; i < nmat; ++i) {
-                e = launch_gemv_kquant(mats[i], mc, nullptr, q, ys[i] + (uint64_t)m0 * mats[i].n, s);
+                float* yi = ys[i] + (uint64_t)m0 * mats[i].n;
+                e = launch_gemv_kquant(mats[i], mc, nullptr, q, yi, s);
+                if (e == hipSuccess && set.add[i] != nullptr) e = launch_add(set.add[i], yi, (uint64_t)mc * mats[i].n, yi, s);
                 if (e != hipSuccess) return e;
             }
             continue;

@@ -86,14 +86,16 @@ bool gemv_kquant_supported(const DeviceMatrix& w);
 struct MtSet {
     const uint8_t* base[4];
     float* y[4];
+    const float* add[4];  // null, or rows laid out like y's: y = add + the product
     uint32_t row_end[4];
     uint32_t nmat;
 };
 // mats[0 .. nmat) from m (2 .. 15) rows of Q8_K blocks, in one launch per 8 activation rows:
 // hipErrorNotSupported when the streamed small-batch kernel does not apply (the caller multiplies
-// the matrices one by one; each row's bits are the same either way)
+// the matrices one by one; each row's bits are the same either way).  With adds, matrix i's
+// outputs are adds[i] + its product (adds[i] null: the product), each sum rounded once.
 hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m, const uint8_t* q8k, float* const* ys,
-                                  hipStream_t s);
+                                  hipStream_t s, const float* const* adds = nullptr);
 hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k,
                               float* y, hipStream_t s);
 int gemv_max_m();
@@ -171,8 +173,10 @@ hipError_t launch_conv_gates_tokens(const float* qkv, const float* conv_w, float
 hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_heads, uint64_t dk, uint64_t dv,
                         const float* beta_s, const float* log_decay, float eps, float* state, float* rec_out,
                         double* head_ss, const float* z, float* z_silu, hipStream_t s, uint64_t tokens = 1);
+// q8, when not null, also receives each token's gated row as Q8_K blocks (heads * dv a multiple of 256)
 hipError_t launch_gated_norm(const float* rec, const double* head_ss, const float* z, const float* out_norm,
-                             uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s, uint64_t tokens = 1);
+                             uint64_t heads, uint64_t dv, float eps, float* gated, hipStream_t s, uint64_t tokens = 1,
+                             uint8_t* q8 = nullptr);
 uint64_t delta_chunks(uint64_t dv);  // head_ss entries per head
 // q8, when not null, also receives act's Q8_K blocks (n a multiple of 256)
 hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s, uint8_t* q8 = nullptr);
@@ -230,11 +234,13 @@ struct AttnTokens {
     const float *q_norm, *k_norm;
     float eps;
     RopeParams rope;               // rotary_dim, sections and base (positions from `positions`)
-    const uint64_t* positions;     // device [tokens][3]
+    const uint64_t* positions;     // device [tokens][3]; or null with positions_host and at most
+    const uint64_t* positions_host;  // kInlineTokenPositions tokens: passed as launch arguments
     float* qcur;                   // [tokens][Hq][D]: the prepared queries
     float* kcur;                   // [tokens][Hkv][D] or null
     uint64_t gate_tok_stride;      // floats between the tokens' output gates
 };
+constexpr uint32_t kInlineTokenPositions = 32;
 hipError_t launch_attention_tokens(const AttnLaunch& L, const AttnTokens& tk, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* src, void* dst, uint64_t n, hipStream_t s);  // round to nearest even
 hipError_t launch_rope(float* heads, uint64_t n_heads, uint64_t head_dim, const RopeParams& p, hipStream_t s);

@@ -96,6 +96,22 @@ def test_block_tokens_match_oracle(ctx, name, m, env):
         assert float(np.max(np.abs(y[t] - y_o))) <= CHAIN_TOL * float(np.max(np.abs(y_o))), t
 
 
+def test_block_tokens_positions_in_device_memory(ctx):
+    """Up to 32 tokens' positions travel in the preparation launch's arguments; beyond that they
+    are copied to the device: 34 tokens, two of them at multimodal positions, the last one's past
+    the first 32."""
+    m = 34
+    d, w, vec, c, xs, positions = inputs("rep1_d64", m, 9300)
+    positions[33] = (c.length + 33, 5, 11)
+    n0 = c.length
+    y, traces, keys, values, length = run_tokens(ctx, d, w, vec, c, positions, xs)
+    assert length == n0 + m
+    for t in (0, 2, 31, 32, 33):
+        step = {"x": xs[t], "pos": positions[t], "y": y[t], "trace": traces[t], "keys0": keys, "values0": values,
+                "len0": n0 + t, "keys1": keys, "values1": values, "len1": n0 + t + 1}
+        check_block_stages(d, w, vec, step)
+
+
 # The matrix-core products' bound on rows that a few products lead (2^-10 of sum |w xhat| plus
 # binary16-subnormal weights and F32 summation)
 DOMINATED_TOL = 1.5e-3

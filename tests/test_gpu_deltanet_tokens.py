@@ -142,6 +142,18 @@ def test_tokens_full_block_matrix_cores(ctx):
     assert np.all(np.isfinite(y))
 
 
+@pytest.mark.parametrize("m", [4, 9])
+def test_tokens_trace_does_not_change_results(ctx, m):
+    """Untraced, the down projection adds the residual in its own stores and the gated norm writes
+    the out projection's Q8_K blocks; traced, both stay separate launches: the same bits."""
+    d, w, vec, hist, st, _ = synth.deltanet_block(np.random.default_rng(85), SMALL)
+    xs = np.random.default_rng(86).standard_normal((m, d["embedding"])).astype(np.float32)
+    y0, _, h0, s0 = run_tokens(ctx, d, w, vec, hist, st, xs, trace=False)
+    y1, _, h1, s1 = run_tokens(ctx, d, w, vec, hist, st, xs, trace=True)
+    assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
+    assert np.array_equal(h0, h1) and np.array_equal(s0.view(np.uint32), s1.view(np.uint32))
+
+
 def test_steps_equal_single_steps(ctx):
     """Below 16 tokens the call's kernels per token are those of the single step's per-stage
     schedule (OQ_BLOCK_FUSED=0: RMSNorm, the same small-batch products from one Q8_K image,
