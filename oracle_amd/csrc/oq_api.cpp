@@ -560,9 +560,11 @@ hipError_t project_rows(oq_context* ctx, const oq_weight* w, uint64_t m, const f
 
 // The same m rows through several matrices: one small-batch launch for matrices it can take
 // together (K-quant, one type, K and pitch, none on matrix cores; 2 <= m <= 15), else one product
-// each.  Each output row has the same bits either way.
+// each.  Each output row has the same bits either way.  With conv (the DeltaNet in-projection's
+// four matrices) *conv_done tells whether the launch also ran the convolution and gates.
 hipError_t project_set(oq_context* ctx, std::initializer_list<std::pair<const oq_weight*, float*>> ps, uint64_t m,
-                       const float* x, const uint8_t* q8) {
+                       const float* x, const uint8_t* q8, const oq::MtConv* conv = nullptr, bool* conv_done = nullptr) {
+    if (conv_done != nullptr) *conv_done = false;
     if (m >= 2 && m <= 15 && ps.size() >= 2 && ps.size() <= 4 && knob_flag(oq::kBlockFused, true)) {
         oq::DeviceMatrix mats[4];
         float* ys[4];
@@ -575,7 +577,12 @@ hipError_t project_set(oq_context* ctx, std::initializer_list<std::pair<const oq
             ++n;
         }
         if (together) {
-            const hipError_t e = oq::launch_gemv_kquant_set(mats, n, (int)m, q8, ys, ctx->stream);
+            hipError_t e = hipErrorNotSupported;
+            if (conv != nullptr && knob_flag(oq::kBlockFused, true)) {
+                e = oq::launch_gemv_kquant_set(mats, n, (int)m, q8, ys, ctx->stream, nullptr, conv);
+                if (e == hipSuccess && conv_done != nullptr) *conv_done = true;
+            }
+            if (e == hipErrorNotSupported) e = oq::launch_gemv_kquant_set(mats, n, (int)m, q8, ys, ctx->stream);
             if (e != hipErrorNotSupported) return e;
         }
     }
@@ -665,8 +672,14 @@ int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, floa
     };
     hipError_t e =
         oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m, q8_for({b->qkv, b->z, b->beta, b->alpha}));
-    if (e == hipSuccess) e = project_set(ctx, {{b->qkv, qkv}, {b->z, z}, {b->beta, beta}, {b->alpha, alpha}}, m, normed, q8);
+    // the convolution and gates in the in-projection's launch where it takes the four matrices
+    // together, else their own launch
+    oq::MtConv epi{b->conv_weight, hist, conv, (uint32_t)K, beta_s, log_decay, b->dt_bias, b->decay};
+    bool conv_done = false;
     if (e == hipSuccess)
+        e = project_set(ctx, {{b->qkv, qkv}, {b->z, z}, {b->beta, beta}, {b->alpha, alpha}}, m, normed, q8, &epi,
+                        &conv_done);
+    if (e == hipSuccess && !conv_done)
         e = oq::launch_conv_gates_tokens(qkv, b->conv_weight, hist, C, K, beta, alpha, b->dt_bias, b->decay, Hv, m,
                                          conv, beta_s, log_decay, s);
     if (e == hipSuccess)

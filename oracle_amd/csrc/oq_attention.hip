@@ -559,16 +559,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
     }
 }
 
-OQ_DEVICE float sigmoid_ref(float v) {
-#pragma clang fp contract(off)
-    if (v >= 0.0f) {
-        const float e = expf(-v);
-        return 1.0f / (1.0f + e);
-    }
-    const float e = expf(v);
-    return e / (1.0f + e);
-}
-
 template <int D, int kMergeUnroll>
 __global__ __launch_bounds__(256) void attention_merge_kernel(MergeArgs a) {
     constexpr int SLICES = D / 64;

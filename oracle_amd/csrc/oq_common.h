@@ -230,6 +230,36 @@ OQ_DEVICE Q8KLane quantize_q8k_block_wave(float4 v, int lane) {
 
 // One quantized block stored in GGML's block_q8_K layout (f32 d, 256 int8 quants, 16 int16 bsums)
 // by the wave that quantized it
+// sum over the wave, butterfly order (every lane gets it)
+OQ_DEVICE double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// The block's scalar activations as the reference evaluates them in F32 (qwen35_block.cpp:138-155):
+// sigmoid from exp of the non-positive argument, softplus with its +-20 cut-offs, SiLU = v * sigmoid(v).
+OQ_DEVICE float sigmoid_ref(float v) {
+#pragma clang fp contract(off)
+    if (v >= 0.0f) {
+        const float e = expf(-v);
+        return 1.0f / (1.0f + e);
+    }
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+
+OQ_DEVICE float softplus_ref(float v) {
+    if (v > 20.0f) return v;
+    if (v < -20.0f) return expf(v);
+    return log1pf(expf(v));
+}
+
+OQ_DEVICE float silu_ref(float v) {
+#pragma clang fp contract(off)
+    return v * sigmoid_ref(v);
+}
+
 OQ_DEVICE void store_q8k_block(uint8_t* ob, const Q8KLane& r, int lane) {
     *reinterpret_cast<uint32_t*>(ob + 4 + 4 * lane) = r.qword;
     if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(ob + 260 + 2 * (lane >> 2)) = (int16_t)r.quad_bsum;

@@ -19,31 +19,6 @@ namespace {
 constexpr int kNormThreads = 1024;
 constexpr int kMaxConvKernel = 16;
 
-// qwen35_block.cpp:138-145
-OQ_DEVICE float sigmoid_ref(float v) {
-    if (v >= 0.0f) {
-        const float e = expf(-v);
-        return 1.0f / (1.0f + e);
-    }
-    const float e = expf(v);
-    return e / (1.0f + e);
-}
-
-// qwen35_block.cpp:147-155
-OQ_DEVICE float softplus_ref(float v) {
-    if (v > 20.0f) return v;
-    if (v < -20.0f) return expf(v);
-    return log1pf(expf(v));
-}
-
-OQ_DEVICE float silu_ref(float v) { return v * sigmoid_ref(v); }
-
-OQ_DEVICE double wave_sum_f64(double v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
 // sum over the workgroup (blockDim.x a multiple of 64, at most 1024); every thread gets it
 OQ_DEVICE double block_sum_f64(double v, double* lds) {
     v = wave_sum_f64(v);

@@ -22,36 +22,6 @@ using namespace kq;
 //             sigmoid, rows of mat[3] (alpha) softplus(a + dt_bias) * decay -- each only when its
 //             output is given (the attention block's q / k / v projections take raw outputs
 //             only); ADD: sum_out[n] = add[n] + y[n]; FFN: act[g] = SiLU(gate) * up.
-namespace blk {
-
-OQ_DEVICE float sigmoid_ref(float v) {
-#pragma clang fp contract(off)
-    if (v >= 0.0f) {
-        const float e = expf(-v);
-        return 1.0f / (1.0f + e);
-    }
-    const float e = expf(v);
-    return e / (1.0f + e);
-}
-
-OQ_DEVICE float softplus_ref(float v) {
-    if (v > 20.0f) return v;
-    if (v < -20.0f) return expf(v);
-    return log1pf(expf(v));
-}
-
-OQ_DEVICE float silu_ref(float v) {
-#pragma clang fp contract(off)
-    return v * sigmoid_ref(v);
-}
-
-OQ_DEVICE double wave_sum_f64(double v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-}  // namespace blk
 
 // IN: matrix index and local row of row `row` of the concatenation (wave-uniform)
 OQ_DEVICE void blk_in_row(const BlockGemv& a, uint32_t row, uint32_t& mi, uint32_t& local) {
@@ -128,7 +98,7 @@ OQ_DEVICE void blk_epilogue(const BlockGemv& a, uint64_t grp, int lane, float v0
         if (lane == 0) {
 #pragma clang fp contract(off)
             if (a.raw[0] != nullptr) a.raw[0][grp] = v0;
-            a.act[grp] = blk::silu_ref(v0) * v1;
+            a.act[grp] = silu_ref(v0) * v1;
         } else if (lane == 1 && a.raw[1] != nullptr) {
             a.raw[1][grp] = v1;
         }
@@ -167,13 +137,13 @@ OQ_DEVICE void blk_epilogue(const BlockGemv& a, uint64_t grp, int lane, float v0
 #pragma clang fp contract(off)
                     sum += readlane_f64(p, 16 * r + (int)j);
                 }
-                if (lane == r) a.conv_out[l] = blk::silu_ref((float)sum);
+                if (lane == r) a.conv_out[l] = silu_ref((float)sum);
             } else if (mi == 2 && a.beta_s != nullptr) {
-                if (lane == r) a.beta_s[l] = blk::sigmoid_ref(v);
+                if (lane == r) a.beta_s[l] = sigmoid_ref(v);
             } else if (mi == 3 && a.log_decay != nullptr) {
                 if (lane == 16 * r) {
 #pragma clang fp contract(off)
-                    a.log_decay[l] = blk::softplus_ref(v + pf.v[0]) * pf.v[1];
+                    a.log_decay[l] = softplus_ref(v + pf.v[0]) * pf.v[1];
                 }
             }
         }
@@ -225,7 +195,7 @@ __global__ __launch_bounds__(512) void gemv_block_kernel(BlockGemv a) {
                       (double)xv[j].z * (double)xv[j].z + (double)xv[j].w * (double)xv[j].w;
             }
         }
-        ss = blk::wave_sum_f64(ss);
+        ss = wave_sum_f64(ss);
         if (lane == 0) red[wave_in_wg] = ss;
         __syncthreads();
         double tot = 0.0;
@@ -485,7 +455,7 @@ __global__ __launch_bounds__(1024) void gemv_block_in_stream_kernel(BlockGemv a)
                       (double)xv[j].z * (double)xv[j].z + (double)xv[j].w * (double)xv[j].w;
             }
         }
-        ss = blk::wave_sum_f64(ss);
+        ss = wave_sum_f64(ss);
         if (lane == 0) red[wave_in_wg] = ss;
     }
     __syncthreads();

@@ -737,7 +737,10 @@ OQ_DEVICE void stage_rows_once(const ActLds& s, int m, const float* x, const uin
 // slices read from LDS.  Per-lane sums in the order of gemv_kq_kernel (pass, then row mi) and the
 // same row reductions: the same bits.  With set.nmat > 0 the rows are those of up to four
 // matrices of w's type, K and pitch, concatenated (MtSet), each writing its own outputs: the same
-// bits per row as one launch per matrix.
+// bits per row as one launch per matrix.  With set.conv the lane that stores a row of the DeltaNet
+// in-projection also runs its epilogue over the m tokens (every wave then has fewer than 64 rows,
+// so each row's outputs are still in the lane's registers at the end): the arithmetic of
+// conv_gates_tokens_kernel, the same bits.
 template <uint32_t TYPE, int ITERS, int MT, bool FUSED, bool FULL>
 __global__ __launch_bounds__(1024) void gemv_stream_mt_kernel(DeviceMatrix w, int m, const float* x, const uint8_t* q8k,
                                                               float* __restrict__ y, MtSet set) {
@@ -779,6 +782,65 @@ __global__ __launch_bounds__(1024) void gemv_stream_mt_kernel(DeviceMatrix w, in
         const float* ai = i == 0 ? set.add[0] : i == 1 ? set.add[1] : i == 2 ? set.add[2] : set.add[3];
         const uint64_t at = (uint64_t)mi * rows + (r - start);
         yi[at] = ai != nullptr ? ai[at] + v : v;
+    };
+    // The DeltaNet in-projection epilogue, run by the whole wave after its last row: lane j < done
+    // holds the m outputs of the wave's j-th row (row first + j * nw).  Every (row, token) pair gets
+    // a lane: a channel row's token t sums the taps i in tap order in double (exact products) over
+    // the values the history holds after t + 1 shifts -- history[t + 1 + i] while inside it, else
+    // output t + 1 + i - K -- then SiLU; beta rows take the sigmoid, alpha rows softplus(a +
+    // dt_bias) * decay.  Then each channel row's new history: its last K values of (history,
+    // outputs).
+    auto conv_epilogue = [&](uint32_t done, const float (&out)[MT]) {
+        const MtConv& c = set.conv;
+        const uint32_t K = c.kernel, C = set.row_end[0], H = set.row_end[2] - set.row_end[1];
+        const uint32_t um = (uint32_t)m, pairs = done * um;
+        auto pick = [&](const float (&v)[MT], uint32_t idx) {
+            float r = 0.0f;
+#pragma unroll
+            for (int q = 0; q < MT; ++q) r = idx == (uint32_t)q ? v[q] : r;
+            return r;
+        };
+        for (uint32_t p0 = 0; p0 < pairs; p0 += 64) {
+            const uint32_t p = p0 + (uint32_t)lane;
+            const uint32_t j = p < pairs ? p / um : 0, t = p < pairs ? p % um : 0;
+            float xs[MT];  // row j's outputs, from lane j
+#pragma unroll
+            for (int q = 0; q < MT; ++q) xs[q] = __shfl(out[q], (int)j, 64);
+            if (p >= pairs) continue;
+            const uint32_t r = first + j * nw, i = set_mat(r), local = r - set_start(i);
+            if (i == 0) {
+                const float* hst = c.history + (uint64_t)local * K;
+                const float* wc = c.conv_w + (uint64_t)local * K;
+                double sum = 0.0;
+                for (uint32_t tap = 0; tap < K; ++tap) {
+                    const uint32_t u = t + 1 + tap;
+                    const float v = u < K ? hst[u] : pick(xs, u - K);
+                    sum += (double)v * (double)wc[tap];
+                }
+                c.conv_out[(uint64_t)t * C + local] = silu_ref((float)sum);
+            } else if (i == 2) {
+                c.beta_s[(uint64_t)t * H + local] = sigmoid_ref(pick(xs, t));
+            } else if (i == 3) {
+#pragma clang fp contract(off)
+                c.log_decay[(uint64_t)t * H + local] = softplus_ref(pick(xs, t) + c.dt_bias[local]) * c.decay[local];
+            }
+        }
+        // the new history, once every read of the old one above has returned
+        if ((uint32_t)lane < done) {
+            const uint32_t r = first + (uint32_t)lane * nw;  // matrix 0 starts the set: local row r
+            if (set_mat(r) == 0) {
+                float* hst = c.history + (uint64_t)r * K;
+                float nv[kMtConvTaps];
+#pragma unroll
+                for (uint32_t tap = 0; tap < kMtConvTaps; ++tap) {
+                    const uint32_t u = um + tap;
+                    nv[tap] = tap < K ? (u < K ? hst[u] : pick(out, u - K)) : 0.0f;
+                }
+#pragma unroll
+                for (uint32_t tap = 0; tap < kMtConvTaps; ++tap)
+                    if (tap < K) hst[tap] = nv[tap];
+            }
+        }
     };
 
     WR buf[2];
@@ -853,6 +915,7 @@ __global__ __launch_bounds__(1024) void gemv_stream_mt_kernel(DeviceMatrix w, in
         for (int mi = 0; mi < MT; ++mi)
             if (mi < m) store(out_row, mi, out[mi]);
     }
+    if (set.conv.conv_w != nullptr) conv_epilogue(done, out);
 }
 
 // Long rows (K beyond the compile-time kernels), any m <= MT: a window of passes
@@ -1108,6 +1171,8 @@ hipError_t launch_stream_mt(const DeviceMatrix& w, int m, const float* x, const 
     const uint64_t rows = set.nmat > 0 ? set.row_end[set.nmat - 1] : w.n;
     const uint64_t need = (rows + 15) / 16;
     if (wgs > need) wgs = need;
+    // the epilogue runs at the end, on the rows still held: fewer than 64 per wave
+    if (set.conv.conv_w != nullptr && (rows + wgs * 16 - 1) / (wgs * 16) >= 64) return hipErrorNotSupported;
     hipLaunchKernelGGL((gemv_stream_mt_kernel<TYPE, ITERS, MT, FUSED, FULL>), dim3((unsigned)wgs), dim3(1024), lds, s,
                        w, m, x, q8k, y, set);
     return hipGetLastError();

@@ -68,8 +68,12 @@ hipError_t launch_gemv_kquant_argmax(const DeviceMatrix& w, const float* x, cons
 }
 
 hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m, const uint8_t* q8k, float* const* ys,
-                                  hipStream_t s, const float* const* adds) {
+                                  hipStream_t s, const float* const* adds, const MtConv* conv) {
     if (nmat < 1 || nmat > 4 || m < 2 || m > 15) return hipErrorNotSupported;
+    if (conv != nullptr && (nmat != 4 || conv->kernel < 1 || conv->kernel > kMtConvTaps ||
+                            mats[2].n != mats[3].n)) {
+        return hipErrorNotSupported;
+    }
     const DeviceMatrix& w = mats[0];
     if (!gemv_kquant_supported(w) || !short_rows(w)) return hipErrorNotSupported;
     uint64_t rows = 0;
@@ -94,6 +98,12 @@ hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m
             end += (uint32_t)mats[i].n;
             set.row_end[i] = end;
         }
+        if (conv != nullptr) {
+            set.conv = *conv;
+            set.conv.conv_out = conv->conv_out + (uint64_t)m0 * mats[0].n;
+            set.conv.beta_s = conv->beta_s + (uint64_t)m0 * mats[2].n;
+            set.conv.log_decay = conv->log_decay + (uint64_t)m0 * mats[3].n;
+        }
         const uint8_t* q = q8k + (uint64_t)m0 * nsb * kQ8KBytes;
         hipError_t e;
         switch (w.type) {
@@ -109,6 +119,15 @@ hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m
                 float* yi = ys[i] + (uint64_t)m0 * mats[i].n;
                 e = launch_gemv_kquant(mats[i], mc, nullptr, q, yi, s);
                 if (e == hipSuccess && set.add[i] != nullptr) e = launch_add(set.add[i], yi, (uint64_t)mc * mats[i].n, yi, s);
+                if (e != hipSuccess) return e;
+            }
+            if (conv != nullptr) {
+                // this chunk's tokens through the separate epilogue launch, in token order after the
+                // earlier chunks'
+                e = launch_conv_gates_tokens(ys[0] + (uint64_t)m0 * mats[0].n, conv->conv_w, conv->history, mats[0].n,
+                                             conv->kernel, ys[2] + (uint64_t)m0 * mats[2].n,
+                                             ys[3] + (uint64_t)m0 * mats[3].n, conv->dt_bias, conv->decay, mats[2].n,
+                                             (uint64_t)mc, set.conv.conv_out, set.conv.beta_s, set.conv.log_decay, s);
                 if (e != hipSuccess) return e;
             }
             continue;

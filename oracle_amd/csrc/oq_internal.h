@@ -83,19 +83,36 @@ bool gemv_kquant_supported(const DeviceMatrix& w);
 // Up to four matrices of one type, K and pitch multiplied by the same activation rows in one launch
 // of the small-batch kernel: their rows concatenated (matrix i holds rows [row_end[i - 1],
 // row_end[i])), matrix i's outputs at y[i][mi * rows_i + local row].  nmat == 0: a single matrix.
+// The Gated DeltaNet in-projection's epilogue over several tokens (conv_gates_tokens_kernel's
+// results): matrix 0's rows are the channels of the causal convolution (history [C][kernel],
+// weights, outputs [tokens][C]), matrix 2's rows the beta gates (beta_s [tokens][Hv]), matrix 3's
+// the alpha gates (log_decay [tokens][Hv], with dt_bias and decay)
+struct MtConv {
+    const float* conv_w;
+    float* history;
+    float* conv_out;
+    uint32_t kernel;
+    float *beta_s, *log_decay;
+    const float *dt_bias, *decay;
+};
+constexpr uint32_t kMtConvTaps = 16;  // the longest convolution the epilogue takes
 struct MtSet {
     const uint8_t* base[4];
     float* y[4];
     const float* add[4];  // null, or rows laid out like y's: y = add + the product
     uint32_t row_end[4];
     uint32_t nmat;
+    MtConv conv;          // conv.conv_w null: no epilogue
 };
 // mats[0 .. nmat) from m (2 .. 15) rows of Q8_K blocks, in one launch per 8 activation rows:
 // hipErrorNotSupported when the streamed small-batch kernel does not apply (the caller multiplies
 // the matrices one by one; each row's bits are the same either way).  With adds, matrix i's
 // outputs are adds[i] + its product (adds[i] null: the product), each sum rounded once.
+// With conv (nmat 4: q/k/v channels, z, beta, alpha) the launches also run the DeltaNet epilogue
+// over the m tokens in order, or nothing is launched (hipErrorNotSupported: a convolution longer
+// than kMtConvTaps, or a wave with 64 rows or more).
 hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m, const uint8_t* q8k, float* const* ys,
-                                  hipStream_t s, const float* const* adds = nullptr);
+                                  hipStream_t s, const float* const* adds = nullptr, const MtConv* conv = nullptr);
 hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k,
                               float* y, hipStream_t s);
 int gemv_max_m();

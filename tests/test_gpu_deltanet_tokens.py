@@ -108,9 +108,15 @@ def shifted(hist, qkv):
     (dict(SMALL, key_dim=32, value_dim=192, value_heads=4, key_heads=4, conv_kernel=2), 5),
     (dict(SMALL, value_dim=256, value_heads=2, key_heads=1), 2),
     (SMALL, 1),
-], ids=["hk2_hv4_m4", "dk64_dv64_k3_m3", "dk32_dv192_k2_m5", "dv256_m2", "m1"])
+    (SMALL, 9),
+    (SMALL, 11),
+    (dict(SMALL, conv_kernel=6), 3),
+], ids=["hk2_hv4_m4", "dk64_dv64_k3_m3", "dk32_dv192_k2_m5", "dv256_m2", "m1", "m9", "m11", "k6_m3"])
 def test_tokens_match_oracle(ctx, dims, m):
-    """Every token's stages, the history (exact) and the carried state after the call."""
+    """Every token's stages, the history (exact) and the carried state after the call.  Up to 8
+    tokens one in-projection launch also runs the convolution and gates (taps <= 4); 9 tokens add
+    a one-token launch and the separate convolution launch for it, 11 a second three-token launch,
+    six taps the separate launch for all."""
     d, w, vec, hist, st, _ = synth.deltanet_block(np.random.default_rng(61), dims)
     xs = np.random.default_rng(62).standard_normal((m, d["embedding"])).astype(np.float32)
     y, traces, hist_g, st_g = run_tokens(ctx, d, w, vec, hist, st, xs)
