@@ -610,6 +610,47 @@ bool needs_q8(const oq_weight* w, uint64_t m, bool mfma = true) {
     return is_kquant(w->m.type) && !on_matrix_cores(w, m, mfma);
 }
 
+// RMSNorm of m rows a [+ b] (n values each) feeding a set of projections.  Where the set's
+// small-batch launch takes the matrices together and its staging holds the rows (m = 2,
+// n <= 8192) the launch normalises them itself (sum_out and, with keep_normed, normed stored by
+// its first workgroup); else the RMSNorm launch (sum_out, normed and the Q8_K image when a
+// projection takes it) and project_set.  Each output has the same value either way (the
+// same formula; the double sums of squares are added in another order, which changes the F32
+// inverse RMS only when the sums fall within about 1e-16 of a rounding boundary).
+hipError_t norm_project_set(oq_context* ctx, std::initializer_list<std::pair<const oq_weight*, float*>> ps, uint64_t m,
+                            const float* a, const float* b, const float* w, float eps, uint64_t n, float* sum_out,
+                            float* normed, bool keep_normed, uint8_t* q8, const oq::MtConv* conv = nullptr,
+                            bool* conv_done = nullptr) {
+    if (conv_done != nullptr) *conv_done = false;
+    if (m == 2 && ps.size() >= 2 && ps.size() <= 4 && knob_flag(oq::kBlockFused, true)) {
+        oq::DeviceMatrix mats[4];
+        float* ys[4];
+        uint32_t cnt = 0;
+        bool together = true;
+        for (const auto& p : ps) {
+            together = together && is_kquant(p.first->m.type) && !on_matrix_cores(p.first, m, true);
+            mats[cnt] = p.first->m;
+            ys[cnt] = p.second;
+            ++cnt;
+        }
+        if (together) {
+            const oq::MtNorm nm{b, w, eps, sum_out, keep_normed ? normed : nullptr};
+            hipError_t e = hipErrorNotSupported;
+            if (conv != nullptr) {
+                e = oq::launch_gemv_kquant_set_norm(mats, cnt, (int)m, a, nm, ys, ctx->stream, conv);
+                if (e == hipSuccess && conv_done != nullptr) *conv_done = true;
+            }
+            if (e == hipErrorNotSupported) e = oq::launch_gemv_kquant_set_norm(mats, cnt, (int)m, a, nm, ys, ctx->stream);
+            if (e != hipErrorNotSupported) return e;
+        }
+    }
+    bool q8_needed = false;
+    for (const auto& p : ps) q8_needed = q8_needed || needs_q8(p.first, m);
+    hipError_t e = oq::launch_rmsnorm(a, b, w, n, eps, sum_out, normed, ctx->stream, m, q8_needed ? q8 : nullptr);
+    if (e == hipSuccess) e = project_set(ctx, ps, m, normed, q8, conv, conv_done);
+    return e;
+}
+
 int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, float* hist, float* state, const float* x,
                    float* y, float* trace) {
     if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
@@ -670,15 +711,14 @@ int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, floa
             if (needs_q8(w, m)) return q8;
         return nullptr;
     };
-    hipError_t e =
-        oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m, q8_for({b->qkv, b->z, b->beta, b->alpha}));
+    hipError_t e = hipSuccess;
     // the convolution and gates in the in-projection's launch where it takes the four matrices
     // together, else their own launch
     oq::MtConv epi{b->conv_weight, hist, conv, (uint32_t)K, beta_s, log_decay, b->dt_bias, b->decay};
     bool conv_done = false;
     if (e == hipSuccess)
-        e = project_set(ctx, {{b->qkv, qkv}, {b->z, z}, {b->beta, beta}, {b->alpha, alpha}}, m, normed, q8, &epi,
-                        &conv_done);
+        e = norm_project_set(ctx, {{b->qkv, qkv}, {b->z, z}, {b->beta, beta}, {b->alpha, alpha}}, m, x, nullptr,
+                             b->input_norm, b->eps, E, nullptr, normed, false, q8, &epi, &conv_done);
     if (e == hipSuccess && !conv_done)
         e = oq::launch_conv_gates_tokens(qkv, b->conv_weight, hist, C, K, beta, alpha, b->dt_bias, b->decay, Hv, m,
                                          conv, beta_s, log_decay, s);
@@ -693,8 +733,9 @@ int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, floa
         e = oq::launch_gated_norm(rec, head_ss, z, b->out_norm, Hv, dv, b->eps, gated, s, m,
                                   is_kquant(b->out->m.type) ? q8 : nullptr);
     if (e == hipSuccess) e = project_rows(ctx, b->out, m, gated, q8, branch, false);
-    if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m, q8_for({b->gate, b->up}));
-    if (e == hipSuccess) e = project_set(ctx, {{b->gate, gate}, {b->up, up}}, m, post, q8);
+    if (e == hipSuccess)
+        e = norm_project_set(ctx, {{b->gate, gate}, {b->up, up}}, m, x, branch, b->post_norm, b->eps, E, resid, post,
+                             trace != nullptr, q8);
     if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s, q8_for({b->down}));
     if (e == hipSuccess && trace) {
         e = project_rows(ctx, b->down, m, act, q8, ffn);  // the trace keeps the down projection
@@ -1629,8 +1670,9 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
     // the tokens' positions: launch arguments for a few tokens, else a copy to the device
     const bool pos_inline = m <= oq::kInlineTokenPositions;
     if (batched && !pos_inline) e = hipMemcpyAsync(pos_dev, positions, m * 3 * sizeof(uint64_t), hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = oq::launch_rmsnorm(x, nullptr, b->input_norm, E, b->eps, nullptr, normed, s, m, q8_for({b->q, b->k, b->v}));
-    if (e == hipSuccess) e = project_set(ctx, {{b->q, qfull}, {b->k, kp}, {b->v, vp}}, m, normed, q8);
+    if (e == hipSuccess)
+        e = norm_project_set(ctx, {{b->q, qfull}, {b->k, kp}, {b->v, vp}}, m, x, nullptr, b->input_norm, b->eps, E,
+                             nullptr, normed, false, q8);
     // the tokens' heads prepared together (token t's key and value appended at row length + t),
     // then token t attending over the rows up to its own, all tokens in one chunk and one merge
     // launch; or, when that grid is too large, the single step's launch token by token
@@ -1680,8 +1722,9 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
     }
     if (e == hipSuccess) e = quantize(gated, Q, {b->out});
     if (e == hipSuccess) e = project_rows(ctx, b->out, m, gated, q8, branch);
-    if (e == hipSuccess) e = oq::launch_rmsnorm(x, branch, b->post_norm, E, b->eps, resid, post, s, m, q8_for({b->gate, b->up}));
-    if (e == hipSuccess) e = project_set(ctx, {{b->gate, gate}, {b->up, up}}, m, post, q8);
+    if (e == hipSuccess)
+        e = norm_project_set(ctx, {{b->gate, gate}, {b->up, up}}, m, x, branch, b->post_norm, b->eps, E, resid, post,
+                             trace != nullptr, q8);
     if (e == hipSuccess) e = oq::launch_swiglu(gate, up, m * F, act, s, q8_for({b->down}));
     if (e == hipSuccess && trace) {
         e = project_rows(ctx, b->down, m, act, q8, ffn);  // the trace keeps the down projection

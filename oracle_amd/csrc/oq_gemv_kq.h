@@ -686,6 +686,70 @@ OQ_DEVICE void stage_rows(const ActLds& s, int m, const float* x, const uint8_t*
     }
 }
 
+// The m F32 rows x [+ b] of K values, RMS-normalised and staged as Q8_K in one round (every
+// block of a wave requested before the first store, then `issue`): per block the wave's double sum
+// of squares (each lane's four squares in order, then the butterfly), per row the blocks' sums in
+// block order, inv = 1 / sqrt(sum / K + eps) rounded to F32, values (v * inv) * w
+// (rmsnorm_kernel's formula); workgroup 0 also stores the sums and the normalised rows.
+template <uint32_t TYPE, int SBW, int WAVES, typename Issue>
+OQ_DEVICE void stage_rows_norm(const ActLds& s, int m, const float* x, const MtNorm& nm, uint64_t nsb, uint64_t k,
+                               int wave_in_wg, int lane, Issue&& issue) {
+#pragma clang fp contract(off)
+    __shared__ double red[kMtNormBlocks * WAVES];
+    const uint64_t nblk = (uint64_t)m * nsb;
+    float4 xv[SBW], bv[SBW], wv[SBW];
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        b = b < nblk ? b : nblk - 1;
+        const uint64_t mi = b / nsb, sb = b % nsb;
+        xv[j] = reinterpret_cast<const float4*>(x + mi * k + sb * kQK)[lane];
+        if (nm.b != nullptr) bv[j] = reinterpret_cast<const float4*>(nm.b + mi * k + sb * kQK)[lane];
+        wv[j] = reinterpret_cast<const float4*>(nm.w + sb * kQK)[lane];
+    }
+    asm volatile("" ::: "memory");
+    issue();
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        if (b >= nblk) break;
+        if (nm.b != nullptr) {
+            xv[j].x = xv[j].x + bv[j].x;
+            xv[j].y = xv[j].y + bv[j].y;
+            xv[j].z = xv[j].z + bv[j].z;
+            xv[j].w = xv[j].w + bv[j].w;
+        }
+        const double sq = (double)xv[j].x * (double)xv[j].x + (double)xv[j].y * (double)xv[j].y +
+                          (double)xv[j].z * (double)xv[j].z + (double)xv[j].w * (double)xv[j].w;
+        const double bs = wave_sum_f64(sq);
+        if (lane == 0) red[b] = bs;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < SBW; ++j) {
+        const uint64_t b = (uint64_t)wave_in_wg + (uint64_t)WAVES * j;
+        if (b >= nblk) break;
+        const uint64_t mi = b / nsb, sb = b % nsb;
+        double tot = 0.0;
+        for (uint64_t c = 0; c < nsb; ++c) tot += red[mi * nsb + c];
+        const float inv = (float)(1.0 / sqrt(tot / (double)k + (double)nm.eps));
+        float4 v;
+        v.x = xv[j].x * inv * wv[j].x;
+        v.y = xv[j].y * inv * wv[j].y;
+        v.z = xv[j].z * inv * wv[j].z;
+        v.w = xv[j].w * inv * wv[j].w;
+        if (blockIdx.x == 0) {
+            if (nm.sum_out != nullptr) reinterpret_cast<float4*>(nm.sum_out + mi * k + sb * kQK)[lane] = xv[j];
+            if (nm.norm_out != nullptr) reinterpret_cast<float4*>(nm.norm_out + mi * k + sb * kQK)[lane] = v;
+        }
+        uint32_t qw;
+        int bsum;
+        float d;
+        quantize_block(v, lane, qw, bsum, d);
+        store_block<TYPE>(s, (int)mi, sb, lane, qw, bsum, d);
+    }
+}
+
 // The m activation rows staged in one round: every block a wave stages (at most MT * ITERS * 16 /
 // WAVES of them) is requested before the first store, then `issue` (the first weight loads), then
 // the stores.  (A loop over rounds of a few blocks costs one memory round trip per round.)
@@ -847,7 +911,16 @@ __global__ __launch_bounds__(1024) void gemv_stream_mt_kernel(DeviceMatrix w, in
     // one staging round (the first pass's weights requested between its loads and its stores)
     // while the per-wave block count stays small; several rounds beyond
     constexpr bool kOnce = (MT * ITERS * 16 + WAVES - 1) / WAVES <= (FUSED ? 8 : 12);
-    if constexpr (kOnce) {
+    constexpr int kSbw = (MT * ITERS * 16 + WAVES - 1) / WAVES;
+    if constexpr (FUSED && kSbw <= kMtNormBlocks) {
+        if (set.norm.w != nullptr) {
+            stage_rows_norm<TYPE, kSbw, WAVES>(s, m, x, set.norm, nsb, w.k, wave_in_wg, lane,
+                                               [&] { load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane); });
+        } else {
+            stage_rows_once<TYPE, ITERS, MT, FUSED, WAVES>(s, m, x, q8k, nsb, w.k, wave_in_wg, lane,
+                                                           [&] { load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane); });
+        }
+    } else if constexpr (kOnce) {
         stage_rows_once<TYPE, ITERS, MT, FUSED, WAVES>(s, m, x, q8k, nsb, w.k, wave_in_wg, lane,
                                                        [&] { load_w<TYPE>(buf[0], row_base(first), nsb, 0, lane); });
     } else {
@@ -1200,6 +1273,32 @@ hipError_t launch_set_iters(const DeviceMatrix& w, int m, const uint8_t* q8k, co
         case 4: return launch_set_rows<TYPE, 4, MT>(w, m, q8k, set, s);
         default: return hipErrorNotSupported;
     }
+}
+
+// The normalising set launch (F32 rows x, set.norm): the kernels whose staging holds a wave's
+// blocks in one round, m * K <= kMtNormBlocks * 4096; hipErrorNotSupported otherwise
+template <uint32_t TYPE, int ITERS, int MT>
+hipError_t launch_set_norm_rows(const DeviceMatrix& w, int m, const float* x, const MtSet& set, hipStream_t s) {
+    if constexpr (MT > 1 && !(TYPE == 13 && MT == 8) && MT * ITERS <= kMtNormBlocks) {
+        if (act_lds_bytes(w.k, MT) <= kLdsBudget && knob(kGemvStreamMt, 1) != 0) {
+            return (w.k / kQK) % 16 == 0 ? launch_stream_mt<TYPE, ITERS, MT, true, true>(w, m, x, nullptr, nullptr, s, set)
+                                         : launch_stream_mt<TYPE, ITERS, MT, true, false>(w, m, x, nullptr, nullptr, s, set);
+        }
+    }
+    return hipErrorNotSupported;
+}
+
+// Two rows only: every workgroup normalises the rows itself, which at four rows of 4096 (and the
+// post-attention norm's addend rows) cost more than the separate RMSNorm launch it saves
+// (DeltaNet block 90.2 -> 93.4 us, attention block 108.6 -> 113.8 us at 4 tokens; 2 tokens
+// 67.3 -> 63.9 and 80.8 -> 77.6 us)
+template <uint32_t TYPE>
+hipError_t launch_set_norm_m(const DeviceMatrix& w, int m, const float* x, const MtSet& set, hipStream_t s) {
+    const uint64_t iters = (w.k / kQK + 15) / 16;
+    if (m != 2) return hipErrorNotSupported;
+    if (iters == 1) return launch_set_norm_rows<TYPE, 1, 2>(w, m, x, set, s);
+    if (iters == 2) return launch_set_norm_rows<TYPE, 2, 2>(w, m, x, set, s);
+    return hipErrorNotSupported;
 }
 
 template <uint32_t TYPE>

@@ -137,6 +137,35 @@ hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m
     return hipSuccess;
 }
 
+hipError_t launch_gemv_kquant_set_norm(const DeviceMatrix* mats, uint32_t nmat, int m, const float* x, const MtNorm& norm,
+                                       float* const* ys, hipStream_t s, const MtConv* conv) {
+    if (nmat < 1 || nmat > 4 || m != 2 || norm.w == nullptr) return hipErrorNotSupported;
+    if (conv != nullptr && (nmat != 4 || conv->kernel < 1 || conv->kernel > kMtConvTaps || mats[2].n != mats[3].n)) {
+        return hipErrorNotSupported;
+    }
+    const DeviceMatrix& w = mats[0];
+    if (!gemv_kquant_supported(w) || !short_rows(w)) return hipErrorNotSupported;
+    uint64_t rows = 0;
+    MtSet set{};
+    set.nmat = nmat;
+    for (uint32_t i = 0; i < nmat; ++i) {
+        if (mats[i].type != w.type || mats[i].k != w.k || mats[i].pitch != w.pitch) return hipErrorNotSupported;
+        rows += mats[i].n;
+        set.base[i] = mats[i].base;
+        set.y[i] = ys[i];
+        set.row_end[i] = (uint32_t)rows;
+    }
+    if (rows > 0xFFFFFFFFull) return hipErrorNotSupported;
+    if (conv != nullptr) set.conv = *conv;
+    set.norm = norm;
+    switch (w.type) {
+        case 12: return kq::launch_set_norm_m<12>(w, m, x, set, s);
+        case 13: return kq::launch_set_norm_m<13>(w, m, x, set, s);
+        case 14: return kq::launch_set_norm_m<14>(w, m, x, set, s);
+        default: return hipErrorNotSupported;
+    }
+}
+
 hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y,
                               hipStream_t s) {
     if (!gemv_kquant_supported(w)) return hipErrorNotSupported;

@@ -96,6 +96,15 @@ struct MtConv {
     const float *dt_bias, *decay;
 };
 constexpr uint32_t kMtConvTaps = 16;  // the longest convolution the epilogue takes
+// RMSNorm of the activation rows in the small-batch kernel's staging (rmsnorm_kernel's values):
+// rows x [+ b] (F32, K each), weights w; workgroup 0 stores x + b to sum_out and the normalised
+// rows to norm_out when given
+struct MtNorm {
+    const float *b, *w;
+    float eps;
+    float *sum_out, *norm_out;
+};
+constexpr int kMtNormBlocks = 4;  // 256-blocks per wave the normalising staging holds (2 rows of 8192)
 struct MtSet {
     const uint8_t* base[4];
     float* y[4];
@@ -103,6 +112,7 @@ struct MtSet {
     uint32_t row_end[4];
     uint32_t nmat;
     MtConv conv;          // conv.conv_w null: no epilogue
+    MtNorm norm;          // norm.w null: the activations are Q8_K blocks
 };
 // mats[0 .. nmat) from m (2 .. 15) rows of Q8_K blocks, in one launch per 8 activation rows:
 // hipErrorNotSupported when the streamed small-batch kernel does not apply (the caller multiplies
@@ -113,6 +123,10 @@ struct MtSet {
 // than kMtConvTaps, or a wave with 64 rows or more).
 hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m, const uint8_t* q8k, float* const* ys,
                                   hipStream_t s, const float* const* adds = nullptr, const MtConv* conv = nullptr);
+// The same from two F32 rows x [+ norm.b] normalised in the kernel's staging (one launch, K <=
+// 8192), or hipErrorNotSupported with nothing launched
+hipError_t launch_gemv_kquant_set_norm(const DeviceMatrix* mats, uint32_t nmat, int m, const float* x, const MtNorm& norm,
+                                       float* const* ys, hipStream_t s, const MtConv* conv = nullptr);
 hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k,
                               float* y, hipStream_t s);
 int gemv_max_m();

@@ -153,13 +153,14 @@ def test_block_tokens_full_block_matrix_cores(ctx, env):
 
 
 @pytest.mark.parametrize("env", SHARE, ids=["default", "shared_rows"])
-def test_block_tokens_trace_does_not_change_results(ctx, env):
+@pytest.mark.parametrize("m", [2, 4])
+def test_block_tokens_trace_does_not_change_results(ctx, env, m):
     """The trace only adds stores: outputs and cache equal bit for bit with and without it."""
-    d, w, vec, c, xs, positions = inputs("e2048", 4, 9600)
+    d, w, vec, c, xs, positions = inputs("e2048", m, 9600)
     with oracle_amd.launch_options(env):
         y0, _, k0, v0, n0 = run_tokens(ctx, d, w, vec, c, positions, xs, trace=False)
         y1, _, k1, v1, n1 = run_tokens(ctx, d, w, vec, c, positions, xs, trace=True)
-    assert n0 == n1 == c.length + 4
+    assert n0 == n1 == c.length + m
     assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
     assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
 

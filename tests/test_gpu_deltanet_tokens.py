@@ -148,10 +148,11 @@ def test_tokens_full_block_matrix_cores(ctx):
     assert np.all(np.isfinite(y))
 
 
-@pytest.mark.parametrize("m", [4, 9])
+@pytest.mark.parametrize("m", [2, 4, 9])
 def test_tokens_trace_does_not_change_results(ctx, m):
     """Untraced, the down projection adds the residual in its own stores and the gated norm writes
-    the out projection's Q8_K blocks; traced, both stay separate launches: the same bits."""
+    the out projection's Q8_K blocks; traced, both stay separate launches; at two tokens the post
+    norm's rows are stored only when traced: the same bits."""
     d, w, vec, hist, st, _ = synth.deltanet_block(np.random.default_rng(85), SMALL)
     xs = np.random.default_rng(86).standard_normal((m, d["embedding"])).astype(np.float32)
     y0, _, h0, s0 = run_tokens(ctx, d, w, vec, hist, st, xs, trace=False)
