@@ -3,7 +3,9 @@
 // loads ("_nt": the form the library's weight and KV loads take), as steady-state back-to-back launches
 // (200 launches captured in a HIP graph over distinct copies that together exceed the 256 MB
 // Infinity Cache; best of three replays after a first one).  It bounds every bandwidth-bound kernel of this library: a
-// decode GEMV over a weight of N bytes cannot take less than the read of N bytes.
+// decode GEMV over a weight of N bytes cannot take less than the read of N bytes.  Then the launch
+// floor: the time per launch of a dependent chain of eager launches that do no memory work to speak
+// of, by launch shape (waves in the grid), the fixed cost of each launch of a chained block step.
 //
 //   build: oracle_amd/build.py (calibration/read_floor)   run: oracle_amd/calibration/read_floor
 #include <hip/hip_runtime.h>
@@ -53,6 +55,13 @@ __global__ __launch_bounds__(256) void read_chunk(const uint4* __restrict__ p, u
 #pragma unroll
     for (int c = 0; c < CH; ++c) acc ^= v[c].x ^ v[c].y ^ v[c].z ^ v[c].w;
     if (acc == 0x12345678u) out[0] = acc;
+}
+
+// one element per thread from the previous launch's output: a dependent chain of launches that do
+// (almost) no memory work
+__global__ __launch_bounds__(1024) void chain_step(const unsigned* __restrict__ in, unsigned* __restrict__ out, unsigned n) {
+    const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = in[(i * 7u) % n] + 1u;
 }
 
 int main() {
@@ -130,6 +139,33 @@ int main() {
         CK(hipEventRecord(e0, s)); CK(hipGraphLaunch(ge, s)); CK(hipEventRecord(e1, s)); CK(hipEventSynchronize(e1));
         float ms; CK(hipEventElapsedTime(&ms, e0, e1));
         printf("{\"kernel\": \"empty_256wg\", \"us\": %.3f}\n", ms * 1e3 / steps);
+    }
+    // Launch floor: 200 dependent launches issued eagerly on one stream (the library's calls), each
+    // workgroup shape with no memory work to speak of; per launch, best of three
+    {
+        const unsigned shapes[][2] = {{1, 64}, {256, 256}, {256, 1024}, {512, 512}, {1024, 256}, {4096, 64},
+                                      {512, 1024}, {2048, 256}};
+        unsigned *a, *b;
+        const unsigned nmax = 512u * 1024u;
+        CK(hipMalloc(&a, nmax * 4)); CK(hipMalloc(&b, nmax * 4));
+        CK(hipMemset(a, 0, nmax * 4)); CK(hipMemset(b, 0, nmax * 4));
+        for (auto& sh : shapes) {
+            const unsigned wgs = sh[0], th = sh[1], n = wgs * th;
+            float best = 1e9;
+            for (int r = 0; r < 3; ++r) {
+                CK(hipStreamSynchronize(s));
+                CK(hipEventRecord(e0, s));
+                for (int i = 0; i < 200; ++i)
+                    hipLaunchKernelGGL(chain_step, dim3(wgs), dim3(th), 0, s, (i & 1) ? b : a, (i & 1) ? a : b, n);
+                CK(hipEventRecord(e1, s)); CK(hipEventSynchronize(e1));
+                float ms; CK(hipEventElapsedTime(&ms, e0, e1)); if (ms < best) best = ms;
+            }
+            CK(hipGetLastError());
+            printf("{\"kernel\": \"chain_%ux%u\", \"waves\": %u, \"us\": %.3f}\n", wgs, th, wgs * ((th + 63) / 64),
+                   best * 1e3 / 200);
+            fflush(stdout);
+        }
+        CK(hipFree(a)); CK(hipFree(b));
     }
     printf("# best per size, any load form | ordinary loads only (%% of 8 TB/s)\n");
     for (int i = 0; i < 7; ++i) {
