@@ -1720,8 +1720,14 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
         L.gated = gated + t * Q;
         e = oq::launch_attention(L, s);
     }
-    if (e == hipSuccess) e = quantize(gated, Q, {b->out});
-    if (e == hipSuccess) e = project_rows(ctx, b->out, m, gated, q8, branch);
+    // the out projection: at two tokens its staging quantizes the gated rows itself (each
+    // workgroup, 32 KB of rows), cheaper than the quantization launch it replaces; same bits
+    if (e == hipSuccess && m == 2 && needs_q8(b->out, m) && knob_flag(oq::kBlockFused, true)) {
+        e = oq::launch_gemv_kquant(b->out->m, (int)m, gated, nullptr, branch, s);
+    } else {
+        if (e == hipSuccess) e = quantize(gated, Q, {b->out});
+        if (e == hipSuccess) e = project_rows(ctx, b->out, m, gated, q8, branch);
+    }
     if (e == hipSuccess)
         e = norm_project_set(ctx, {{b->gate, gate}, {b->up, up}}, m, x, branch, b->post_norm, b->eps, E, resid, post,
                              trace != nullptr, q8);
