@@ -469,7 +469,7 @@ def main():
             "us_per_step": round(r["us_per_step"], 2)}), flush=True)
         return
     main_res = run_gpu(ctx, args.workload, args.steps, args.warmup, graph=args.graph)
-    secondary = block = block4 = attn = attn16 = attn_block = attn_block4 = None
+    secondary = block = block2 = block4 = attn = attn16 = attn_block = attn_block2 = attn_block4 = None
     configs = {}
     if not args.no_secondary and args.workload == "q4k_gemv":
         # the other single-GPU configurations, each with its own roofline; steps of a few to a few
@@ -478,10 +478,12 @@ def main():
         for name in ("q8_0_gemv", "q6k_head", "q4k_down_m4"):
             configs[name] = run_gpu(ctx, name, max(50, args.steps), max(5, args.warmup))
         block = run_deltanet(ctx, max(20, args.steps), max(5, args.warmup))
+        block2 = run_deltanet(ctx, max(20, args.steps), max(5, args.warmup), tokens=2)
         block4 = run_deltanet(ctx, max(20, args.steps), max(5, args.warmup), tokens=4)
         attn = run_attention(ctx, max(20, args.steps), max(5, args.warmup))
         attn16 = run_attention(ctx, max(20, args.steps), max(5, args.warmup), kv_dtype="f16")
         attn_block = run_attention_block(ctx, max(20, args.steps), max(5, args.warmup))
+        attn_block2 = run_attention_block(ctx, max(20, args.steps), max(5, args.warmup), tokens=2)
         attn_block4 = run_attention_block(ctx, max(20, args.steps), max(5, args.warmup), tokens=4)
     ctx.close()
 
@@ -544,6 +546,10 @@ def main():
         out["deltanet_block"] = {"us": round(block["us_per_block"], 2), "weight_gbs": round(block["weight_gbs"], 1),
                                  "hbm_frac": round(block["weight_gbs"] / HBM_PEAK_GBS, 4),
                                  "weight_bytes": block["weight_bytes"]}
+    if block2 is not None:
+        out["deltanet_block_2_tokens"] = {"us": round(block2["us_per_block"], 2),
+                                          "us_per_token": round(block2["us_per_token"], 2),
+                                          "weight_gbs": round(block2["weight_gbs"], 1)}
     if block4 is not None:
         out["deltanet_block_4_tokens"] = {"us": round(block4["us_per_block"], 2),
                                           "us_per_token": round(block4["us_per_token"], 2),
@@ -553,6 +559,10 @@ def main():
                                   "hbm_frac": round(attn_block["gbs"] / HBM_PEAK_GBS, 4),
                                   "weight_bytes": attn_block["weight_bytes"], "kv_bytes": attn_block["kv_bytes"],
                                   "cached_tokens": attn_block["cached"]}
+    if attn_block2 is not None:
+        out["attention_block_2_tokens"] = {"us": round(attn_block2["us_per_block"], 2),
+                                           "us_per_token": round(attn_block2["us_per_token"], 2),
+                                           "cached_tokens": attn_block2["cached"]}
     if attn_block4 is not None:
         out["attention_block_4_tokens"] = {"us": round(attn_block4["us_per_block"], 2),
                                            "us_per_token": round(attn_block4["us_per_token"], 2),
