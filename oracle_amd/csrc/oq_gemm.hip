@@ -1767,36 +1767,30 @@ uint64_t gemm_scratch_bytes(const DeviceMatrix& w, int m) {
 
 template <uint32_t TYPE, bool FAST>
 void launch_kq(const DeviceMatrix& w, int m, const _Float16* a16, const Plan& p, float* dst, hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_kq_kernel<TYPE, FAST>),
+    // once per process (a function-local static: thread-safe)
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_kq_kernel<TYPE, FAST>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kKqLds);
-        attr = true;
-    }
+    (void)attr;
     hipLaunchKernelGGL((gemm_kq_kernel<TYPE, FAST>), dim3(p.tiles_n * p.tiles_m * p.splits), dim3(kKqThreads), kKqLds, s,
                        w, m, a16, p.tiles_n, p.tiles_m, p.splits, dst);
 }
 
 template <uint32_t TYPE, bool FAST>
 void launch_ws(const DeviceMatrix& w, int m, const _Float16* a16, const Plan& p, float* dst, hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_ws_kernel<TYPE, FAST>),
+    // once per process (a function-local static: thread-safe)
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_ws_kernel<TYPE, FAST>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)ws_lds_bytes<TYPE>());
-        attr = true;
-    }
+    (void)attr;
     hipLaunchKernelGGL((gemm_ws_kernel<TYPE, FAST>), dim3(p.tiles_n * p.tiles_m * p.splits), dim3(kWsThreads),
                        ws_lds_bytes<TYPE>(), s, w, m, a16, p.tiles_n, p.tiles_m, p.splits, dst);
 }
 
 template <bool FAST>
 void launch_ws6(const DeviceMatrix& w, int m, const _Float16* a16, const Plan& p, float* dst, hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_ws6_kernel<FAST>),
+    // once per process (a function-local static: thread-safe)
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_ws6_kernel<FAST>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ6Lds);
-        attr = true;
-    }
+    (void)attr;
     hipLaunchKernelGGL((gemm_ws6_kernel<FAST>), dim3(p.tiles_n * p.tiles_m * p.splits), dim3(kWsThreads), kQ6Lds, s,
                        w, m, a16, p.tiles_n, p.tiles_m, p.splits, dst);
 }

@@ -585,15 +585,14 @@ hipError_t launch_block_full(const BlockGemv& a, hipStream_t s) {
     }
     const uint64_t groups = MODE == kBlockFfn ? a.mat[0].n : ((uint64_t)a.row_end[a.nmat - 1] + 1) / 2;
     const uint64_t lds = act_lds_bytes(a.mat[0].k, 1);
-    static int resident = 0;
-    if (resident == 0) {
+    static const int resident = [lds] {
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_block_kernel<TYPE, ITERS, MODE, FULL>, 512, lds) !=
                 hipSuccess || n < 1) {
             n = 1;
         }
-        resident = n;
-    }
+        return n;
+    }();
     uint64_t wgs = (uint64_t)cu_count() * (uint64_t)(resident < 2 ? resident : 2);
     const uint64_t need = (groups + 7) / 8;
     if (wgs > need) wgs = need;

@@ -1150,18 +1150,18 @@ hipError_t launch_window(const DeviceMatrix& w, int m, const float* x, const uin
 
 // ---------------------------------------------------------------- launch
 
-// Workgroups resident per CU for this instantiation (register and LDS limits), cached.
+// Workgroups resident per CU for this instantiation (register and LDS limits), from the first
+// call's LDS size (a function-local static: initialised once, thread-safe)
 template <uint32_t TYPE, int ITERS, int R, int MT, bool FUSED, int WAVES, bool FULL>
 int resident_per_cu(uint64_t lds_bytes) {
-    static int cached = 0;
-    if (cached == 0) {
+    static const int cached = [lds_bytes] {
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_kq_kernel<TYPE, ITERS, R, MT, FUSED, WAVES, FULL>,
                                                          64 * WAVES, lds_bytes) != hipSuccess || n < 1) {
             n = 1;
         }
-        cached = n;
-    }
+        return n;
+    }();
     return cached;
 }
 
@@ -1192,15 +1192,14 @@ template <uint32_t TYPE, int ITERS, bool FUSED, int WAVES, bool FULL>
 hipError_t launch_stream(const DeviceMatrix& w, const float* x, const uint8_t* q8k, float* y, hipStream_t s,
                          ArgmaxPart* amax = nullptr, uint32_t max_parts = 0, uint32_t* nparts = nullptr) {
     const uint64_t lds = act_lds_bytes(w.k, 1);
-    static int resident = 0;
-    if (resident == 0) {
+    static const int resident = [lds] {
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_stream_kernel<TYPE, ITERS, FUSED, WAVES, FULL>,
                                                          64 * WAVES, lds) != hipSuccess || n < 1) {
             n = 1;
         }
-        resident = n;
-    }
+        return n;
+    }();
     // sixteen waves per CU: ~37 KiB of weights in flight per CU, and each CU stages the
     // activation row once per sixteen waves
     int wg_per_cu = knob(kStreamWgPerCu, 16 / WAVES);
