@@ -79,7 +79,8 @@ SHARE = [{}, {"OQ_ATTN_SHARE_MIN": "0"}]
 
 
 @pytest.mark.parametrize("env", SHARE, ids=["default", "shared_rows"])
-@pytest.mark.parametrize("name,m", [("rep1_d64", 4), ("mixed", 3), ("empty_rep8", 5), ("e2048", 2), ("rep16", 3)])
+@pytest.mark.parametrize("name,m", [("rep1_d64", 4), ("mixed", 3), ("empty_rep8", 5), ("e2048", 2), ("rep16", 3),
+                                    ("e8192", 2), ("e8448", 2), ("e4096", 2)])
 def test_block_tokens_match_oracle(ctx, name, m, env):
     d, w, vec, c, xs, positions = inputs(name, m, 9100 + m)
     n0 = c.length
