@@ -74,6 +74,60 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
     }
 }
 
+// rmsnorm_kernel's values for rows of n = 256 * nb values (nb <= kNormWaves * NBW), one workgroup
+// per row with every value in registers: wave w holds the 256-blocks w, w + kNormWaves, ... (lane
+// l: values 4l..4l+3 of each), so the row is read once and its Q8_K blocks come from the same
+// registers.  The sum of squares is the small-batch kernels' staging order (each lane's four
+// squares in order, the wave's butterfly per block, the blocks' sums in block order), so a row
+// normalised here and one normalised in that staging have the same bits.
+constexpr int kNormWaves = 8;
+template <int NBW>
+__global__ __launch_bounds__(64 * kNormWaves) void rmsnorm_blocks_kernel(
+    const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ w, uint32_t nb, float eps,
+    float* __restrict__ sum_out, float* __restrict__ out, uint8_t* __restrict__ q8) {
+#pragma clang fp contract(off)
+    __shared__ double red[kNormWaves * NBW];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t n = (uint64_t)nb * kQK, row = (uint64_t)blockIdx.x * n;
+    float4 v[NBW], wv[NBW];
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+        uint32_t blk = (uint32_t)wave + kNormWaves * j;
+        blk = blk < nb ? blk : nb - 1;
+        const uint64_t i = row + (uint64_t)blk * kQK + 4u * (uint32_t)lane;
+        v[j] = *reinterpret_cast<const float4*>(a + i);
+        if (b != nullptr) {
+            const float4 u = *reinterpret_cast<const float4*>(b + i);
+            v[j] = make_float4(v[j].x + u.x, v[j].y + u.y, v[j].z + u.z, v[j].w + u.w);
+        }
+        wv[j] = *reinterpret_cast<const float4*>(w + (uint64_t)blk * kQK + 4u * (uint32_t)lane);
+    }
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+        const uint32_t blk = (uint32_t)wave + kNormWaves * j;
+        if (blk >= nb) break;
+        if (b != nullptr) *reinterpret_cast<float4*>(sum_out + row + (uint64_t)blk * kQK + 4u * (uint32_t)lane) = v[j];
+        const double sq = (double)v[j].x * (double)v[j].x + (double)v[j].y * (double)v[j].y +
+                          (double)v[j].z * (double)v[j].z + (double)v[j].w * (double)v[j].w;
+        const double bs = wave_sum_f64(sq);
+        if (lane == 0) red[blk] = bs;
+    }
+    __syncthreads();
+    double tot = 0.0;
+    for (uint32_t c = 0; c < nb; ++c) tot += red[c];
+    const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+        const uint32_t blk = (uint32_t)wave + kNormWaves * j;
+        if (blk >= nb) break;
+        const float4 o = make_float4(v[j].x * inv * wv[j].x, v[j].y * inv * wv[j].y, v[j].z * inv * wv[j].z,
+                                     v[j].w * inv * wv[j].w);
+        *reinterpret_cast<float4*>(out + row + (uint64_t)blk * kQK + 4u * (uint32_t)lane) = o;
+        if (q8 != nullptr)
+            store_q8k_block(q8 + ((uint64_t)blockIdx.x * nb + blk) * kQ8KBytes, quantize_q8k_block_wave(o, lane), lane);
+    }
+}
+
 // Causal depthwise convolution step with SiLU (reference_kernels.cpp:197-225 with
 // qwen35_block.cpp:500-503) over `channels` channels of `kernel` taps; the first workgroup
 // also forms the per-head gates: beta_s = sigmoid(beta), log_decay = softplus(alpha + dt_bias)
@@ -336,6 +390,23 @@ bool deltanet_dims_supported(uint64_t key_dim, uint64_t value_dim, uint64_t conv
 hipError_t launch_rmsnorm(const float* a, const float* b, const float* w, uint64_t n, float eps, float* sum_out,
                           float* out, hipStream_t s, uint64_t rows, uint8_t* q8) {
     if (q8 != nullptr && n % kQK != 0) return hipErrorInvalidValue;
+    // rows of whole 256-blocks, up to 16384 values: every value in registers, read once
+    const uint64_t nb = n / kQK;
+    if (n % kQK == 0 && nb >= 1 && nb <= (uint64_t)kNormWaves * 8) {
+        const bool aligned16 = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                                 reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(sum_out) |
+                                 reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
+        if (aligned16) {
+            if (nb <= (uint64_t)kNormWaves * 2) {
+                hipLaunchKernelGGL(rmsnorm_blocks_kernel<2>, dim3((unsigned)rows), dim3(64 * kNormWaves), 0, s, a, b, w,
+                                   (uint32_t)nb, eps, sum_out, out, q8);
+            } else {
+                hipLaunchKernelGGL(rmsnorm_blocks_kernel<8>, dim3((unsigned)rows), dim3(64 * kNormWaves), 0, s, a, b, w,
+                                   (uint32_t)nb, eps, sum_out, out, q8);
+            }
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, s, a, b, w, (uint32_t)n, eps, sum_out,
                        out, q8);
     return hipGetLastError();
