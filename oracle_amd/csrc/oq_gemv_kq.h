@@ -37,6 +37,14 @@ namespace {
 
 constexpr int kMaxIters = 4;  // passes of 16 super-blocks held by the compile-time kernels (K <= 16384)
 constexpr uint64_t kLdsBudget = 64 * 1024;
+// The small-batch streamed kernel runs one 16-wave workgroup per CU, so its activation image may
+// take most of the CU's 160 KB: eight rows of 12288 (124 KB) in one launch.  q5_K, and every type
+// with OQ_GEMV_STREAM_MT=0, keep the general budget (those rows run the batched kernel, whose
+// workgroups share a CU).
+constexpr uint64_t kMtLdsBudget = 128 * 1024;
+uint64_t mt_lds_budget(uint32_t type) {
+    return type == 13 || knob(kGemvStreamMt, 1) == 0 ? kLdsBudget : kMtLdsBudget;
+}
 
 OQ_DEVICE uint4 ldg128(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
 OQ_DEVICE uint32_t ldg32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
@@ -1239,6 +1247,13 @@ template <uint32_t TYPE, int ITERS, int MT, bool FUSED, bool FULL>
 hipError_t launch_stream_mt(const DeviceMatrix& w, int m, const float* x, const uint8_t* q8k, float* y, hipStream_t s,
                             const MtSet& set = MtSet{}) {
     const uint64_t lds = act_lds_bytes(w.k, MT);
+    if (lds > kLdsBudget) {
+        // beyond the default dynamic LDS limit (once per instantiation; a function-local static)
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(gemv_stream_mt_kernel<TYPE, ITERS, MT, FUSED, FULL>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMtLdsBudget);
+        if (attr != hipSuccess) return attr;
+    }
     uint64_t wgs = (uint64_t)cu_count();
     const uint64_t rows = set.nmat > 0 ? set.row_end[set.nmat - 1] : w.n;
     const uint64_t need = (rows + 15) / 16;
@@ -1255,7 +1270,7 @@ hipError_t launch_stream_mt(const DeviceMatrix& w, int m, const float* x, const 
 template <uint32_t TYPE, int ITERS, int MT>
 hipError_t launch_set_rows(const DeviceMatrix& w, int m, const uint8_t* q8k, const MtSet& set, hipStream_t s) {
     if constexpr (MT > 1 && !(TYPE == 13 && MT == 8)) {
-        if (act_lds_bytes(w.k, MT) <= kLdsBudget && knob(kGemvStreamMt, 1) != 0) {
+        if (act_lds_bytes(w.k, MT) <= mt_lds_budget(TYPE) && knob(kGemvStreamMt, 1) != 0) {
             return (w.k / kQK) % 16 == 0 ? launch_stream_mt<TYPE, ITERS, MT, false, true>(w, m, nullptr, q8k, nullptr, s, set)
                                          : launch_stream_mt<TYPE, ITERS, MT, false, false>(w, m, nullptr, q8k, nullptr, s, set);
         }
@@ -1279,7 +1294,7 @@ hipError_t launch_set_iters(const DeviceMatrix& w, int m, const uint8_t* q8k, co
 template <uint32_t TYPE, int ITERS, int MT>
 hipError_t launch_set_norm_rows(const DeviceMatrix& w, int m, const float* x, const MtSet& set, hipStream_t s) {
     if constexpr (MT > 1 && !(TYPE == 13 && MT == 8) && MT * ITERS <= kMtNormBlocks) {
-        if (act_lds_bytes(w.k, MT) <= kLdsBudget && knob(kGemvStreamMt, 1) != 0) {
+        if (act_lds_bytes(w.k, MT) <= mt_lds_budget(TYPE) && knob(kGemvStreamMt, 1) != 0) {
             return (w.k / kQK) % 16 == 0 ? launch_stream_mt<TYPE, ITERS, MT, true, true>(w, m, x, nullptr, nullptr, s, set)
                                          : launch_stream_mt<TYPE, ITERS, MT, true, false>(w, m, x, nullptr, nullptr, s, set);
         }
@@ -1328,7 +1343,7 @@ hipError_t launch_rows(const DeviceMatrix& w, int m, const float* x, const uint8
         // small batches (from Q8_K blocks, or F32 rows quantized in the staging): streamed, one
         // pass in flight
         // (q5_K with eight rows would spill within the 128 registers of a 16-wave workgroup)
-        if (act_lds_bytes(w.k, MT) <= kLdsBudget && knob(kGemvStreamMt, 1) != 0) {
+        if (act_lds_bytes(w.k, MT) <= mt_lds_budget(TYPE) && knob(kGemvStreamMt, 1) != 0) {
             return (w.k / kQK) % 16 == 0 ? launch_stream_mt<TYPE, ITERS, MT, FUSED, true>(w, m, x, q8k, y, s)
                                          : launch_stream_mt<TYPE, ITERS, MT, FUSED, false>(w, m, x, q8k, y, s);
         }

@@ -85,7 +85,7 @@ hipError_t launch_gemv_kquant_set(const DeviceMatrix* mats, uint32_t nmat, int m
     const uint64_t nsb = w.k / kQK;
     // activation rows per launch, as launch_gemv_kquant: what fits the LDS budget, at most 8
     int chunk = 8;
-    while (chunk > 1 && kq::act_lds_bytes(w.k, chunk) > kq::kLdsBudget) chunk >>= 1;
+    while (chunk > 1 && kq::act_lds_bytes(w.k, chunk) > kq::mt_lds_budget(w.type)) chunk >>= 1;
     for (int m0 = 0; m0 < m; m0 += chunk) {
         const int mc = m - m0 < chunk ? m - m0 : chunk;
         MtSet set{};
@@ -173,7 +173,7 @@ hipError_t launch_gemv_kquant(const DeviceMatrix& w, int m, const float* x, cons
     if (short_rows(w)) {
         // activation rows per launch: what fits the LDS budget, at most 8
         int chunk = 8;
-        while (chunk > 1 && kq::act_lds_bytes(w.k, chunk) > kq::kLdsBudget) chunk >>= 1;
+        while (chunk > 1 && kq::act_lds_bytes(w.k, chunk) > kq::mt_lds_budget(w.type)) chunk >>= 1;
         for (int m0 = 0; m0 < m; m0 += chunk) {
             const int mc = m - m0 < chunk ? m - m0 : chunk;
             hipError_t e;

@@ -113,8 +113,9 @@ def shifted(hist, qkv):
     (dict(SMALL, conv_kernel=6), 3),
     (dict(SMALL, embedding=8192), 2),
     (dict(SMALL, embedding=4096), 2),
+    (synth.DELTANET_DIMS, 6),
 ], ids=["hk2_hv4_m4", "dk64_dv64_k3_m3", "dk32_dv192_k2_m5", "dv256_m2", "m1", "m9", "m11", "k6_m3", "e8192_m2",
-        "e4096_m2"])
+        "e4096_m2", "full_m6"])
 def test_tokens_match_oracle(ctx, dims, m):
     """Every token's stages, the history (exact) and the carried state after the call.  Up to 8
     tokens one in-projection launch also runs the convolution and gates (taps <= 4); 9 tokens add

@@ -554,7 +554,8 @@ def test_q8_0_decode_gemv(ctx, rows, cols):
 
 
 @pytest.mark.parametrize("t,rows,cols,m", [(12, 4096, 12288, 4), (12, 5000, 1280, 3), (13, 700, 4096, 2),
-                                           (14, 8269, 512, 8), (14, 300, 8192, 5), (12, 9000, 4096, 7)])
+                                           (14, 8269, 512, 8), (14, 300, 8192, 5), (12, 9000, 4096, 7),
+                                           (12, 4096, 12288, 8), (14, 2000, 12288, 6), (13, 900, 12288, 7)])
 def test_small_batch_streamed_kernel(ctx, t, rows, cols, m):
     """Small batches run the streamed kernel (one weight pass in flight per wave, m activation
     rows in LDS); it gives the batched kernel's bits (OQ_GEMV_STREAM_MT=0), also when it
