@@ -1200,7 +1200,8 @@ int check_cache(oq_context* ctx, const oq_kv_cache* c) {
 
 // the attention launch over a cache whose new token (index T - 1 = cache->length) is given by
 // new_k / new_v, or already stored (both null); the partials go to `part`
-int attention_shape(oq_context* ctx, const oq_kv_cache* c, uint64_t q_heads, oq::AttnLaunch& L, uint64_t ahead = 0) {
+int attention_shape(oq_context* ctx, const oq_kv_cache* c, uint64_t q_heads, oq::AttnLaunch& L, uint64_t ahead = 0,
+                    uint64_t token_groups = 1) {
     const uint64_t rep = q_heads / c->kv_heads;
     if (c->key_dim != c->value_dim || !oq::attention_dims_supported(c->key_dim, rep)) {
         return fail(ctx, OQ_INVALID_ARGUMENT,
@@ -1209,7 +1210,7 @@ int attention_shape(oq_context* ctx, const oq_kv_cache* c, uint64_t q_heads, oq:
     }
     const uint64_t T = c->length + 1 + ahead;  // the token `ahead` places after the next one to append
     uint32_t chunk = 0, nchunks = 0;
-    oq::attention_plan(T, c->kv_heads, rep, chunk, nchunks);
+    oq::attention_plan(T, c->kv_heads, rep, chunk, nchunks, token_groups);
     if (nchunks > oq::kAttnMaxChunks || T > 0xFFFFFFFFull || c->kv_heads > 0xFFFF) {
         return fail(ctx, OQ_INVALID_ARGUMENT, "attention device path supports at most 8388608 cached tokens");
     }
@@ -1611,8 +1612,11 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
     if (cache->capacity - cache->length < m) return fail(ctx, OQ_OVERFLOW, "KV cache capacity exceeded");
     // the attention of all m tokens in one chunk launch, shaped for the last token (its chunks lay
     // out every token's partials); a grid too large for one launch runs the tokens one by one
+    // the chunks sized so that the launch's workgroups over all token groups fill the GPU about as
+    // one token's do
     oq::AttnLaunch last{};
-    if (int rc = attention_shape(ctx, cache, Hq, last, m - 1)) return rc;
+    const uint64_t tpw = oq::attention_tokens_per_workgroup(cache->length + m, Hq / Hkv, m);
+    if (int rc = attention_shape(ctx, cache, Hq, last, m - 1, (m + tpw - 1) / tpw)) return rc;
     const uint64_t part_last = oq::attention_partial_floats(Hkv, Hq / Hkv, D, last.nchunks);
     const bool batched = m * Hkv * oq::attention_subgroups((uint32_t)(Hq / Hkv)) * last.nchunks <= 0x7FFFFFFFull;
     std::vector<oq::AttnLaunch> Ls;

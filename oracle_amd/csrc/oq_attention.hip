@@ -891,8 +891,7 @@ hipError_t launch_tokens_d(const AttnLaunch& L, const AttnTokens& tk, hipStream_
     // over long caches, as many tokens per workgroup as its 8 query rows hold: each key and value row
     // read once for them (shorter caches keep one token per workgroup: twice the workgroups)
     a.heads = L.rep / a.nsub;
-    const bool share = L.T >= (uint32_t)std::max(0, knob(kAttnShareMin, 8192));
-    a.tpw = share ? std::min<uint32_t>(tk.tokens, std::max<uint32_t>(1, 8 / a.heads)) : 1u;
+    a.tpw = attention_tokens_per_workgroup(L.T, L.rep, tk.tokens);
     a.rep = a.tpw * a.heads;
     a.chunk = L.chunk;
     a.nchunks = L.nchunks;
@@ -945,6 +944,12 @@ bool attention_dims_supported(uint64_t head_dim, uint64_t rep) {
     return (head_dim == 64 || head_dim == 128 || head_dim == 256) && rep >= 1 && rep <= kAttnMaxRep;
 }
 
+uint32_t attention_tokens_per_workgroup(uint64_t T, uint64_t rep, uint64_t tokens) {
+    const bool share = T >= (uint64_t)std::max(0, knob(kAttnShareMin, 8192));
+    const uint32_t heads = (uint32_t)rep / attention_subgroups((uint32_t)rep);
+    return share ? (uint32_t)std::min<uint64_t>(tokens, std::max<uint32_t>(1, 8 / heads)) : 1u;
+}
+
 uint32_t attention_subgroups(uint32_t rep) {
     // the fewest equal subgroups of at most 8 query heads (a prime group above 8 becomes single heads)
     for (uint32_t n = (rep + 7) / 8; n < rep; ++n)
@@ -952,11 +957,12 @@ uint32_t attention_subgroups(uint32_t rep) {
     return rep;
 }
 
-void attention_plan(uint64_t T, uint64_t Hkv, uint64_t rep, uint32_t& chunk, uint32_t& nchunks) {
+void attention_plan(uint64_t T, uint64_t Hkv, uint64_t rep, uint32_t& chunk, uint32_t& nchunks, uint64_t token_groups) {
     // about two chunk workgroups per compute unit (OQ_ATTN_WG_PER_CU) over the (KV head, subgroup)
-    // pairs, chunks a multiple of the score pass
+    // pairs and the token groups, chunks a multiple of the score pass
     const uint64_t per_cu = (uint64_t)std::max(1, knob(kAttnWgPerCu, 2));
-    const uint64_t groups = std::max<uint64_t>(Hkv, 1) * attention_subgroups((uint32_t)std::max<uint64_t>(rep, 1));
+    const uint64_t groups = std::max<uint64_t>(Hkv, 1) * attention_subgroups((uint32_t)std::max<uint64_t>(rep, 1)) *
+                            std::max<uint64_t>(token_groups, 1);
     const uint64_t target = std::max<uint64_t>(1, (per_cu * (uint64_t)cu_count()) / groups);
     uint64_t c = (T + target - 1) / target;
     const uint64_t min_chunk = (uint64_t)std::max(1, knob(kAttnMinChunk, (int)kTokStep));

@@ -250,7 +250,12 @@ struct AttnLaunch {
 constexpr uint64_t kAttnMaxRep = 256;  // query heads per KV head
 bool attention_dims_supported(uint64_t head_dim, uint64_t rep);
 uint32_t attention_subgroups(uint32_t rep);  // chunk workgroups per (KV head, chunk): rep / subgroups <= 8 heads each
-void attention_plan(uint64_t T, uint64_t Hkv, uint64_t rep, uint32_t& chunk, uint32_t& nchunks);
+// token_groups: launches of that many tokens' workgroups share the grid (several tokens per call)
+void attention_plan(uint64_t T, uint64_t Hkv, uint64_t rep, uint32_t& chunk, uint32_t& nchunks,
+                    uint64_t token_groups = 1);
+// tokens each chunk workgroup of a several-token launch serves (over long caches, as many as its 8
+// query rows hold; otherwise one)
+uint32_t attention_tokens_per_workgroup(uint64_t T, uint64_t rep, uint64_t tokens);
 uint64_t attention_partial_floats(uint64_t Hkv, uint64_t rep, uint64_t head_dim, uint32_t nchunks);
 constexpr uint32_t kAttnMaxChunks = 8192;
 hipError_t launch_attention(const AttnLaunch& a, hipStream_t s);
