@@ -254,8 +254,10 @@ int oq_matmul_q8k(oq_context* ctx, const oq_weight* w, uint64_t m, const void* q
      qkv[C] z[Hv*dv] beta[Hv] alpha[Hv] conv[C] out[Hv*dv] gated[Hv*dv] branch[E] resid[E]
      post[E] gate[F] up[F] act[F] ffn[E] beta_s[Hv] log_decay[Hv]      with C = 2*Hk*dk + Hv*dv,
      beta_s = sigmoid(beta), log_decay = softplus(alpha + dt_bias) * decay.
-   Device path limits: dk in {32, 64, 128}, dv in {64, 128, 192, 256}, conv_kernel <= 16; otherwise
-   OQ_INVALID_ARGUMENT.  Weight shape mismatches -> OQ_INVALID_ARGUMENT. */
+   Shapes: dk in {32, 64, 128}, dv in {64, 128, 192, 256} and conv_kernel <= 16 take the fused
+   launches; any other shape (dk <= 4096; wider keys -> OQ_INVALID_ARGUMENT) runs one launch per
+   stage with the delta rule's state in HBM, in the same arithmetic order (the register-resident
+   kernel's bits where both apply).  Weight shape mismatches -> OQ_INVALID_ARGUMENT. */
 typedef struct oq_deltanet_block {
     uint64_t embedding;   /* E */
     uint64_t key_heads;   /* Hk */
@@ -349,10 +351,13 @@ int oq_rope(oq_context* ctx, float* heads_dev, uint64_t n_heads, uint64_t head_d
    exceeded", OQ_OVERFLOW), both before any device work.  F32 arithmetic split over token chunks
    and merged with the usual max rescaling: outputs agree with the reference within 1e-4 of
    sum_t p_t |v_t| (the reference sums doubles for the dot products and the denominator).  A
-   non-finite score yields non-finite outputs where the reference throws.  Device path limits:
-   key_dim == value_dim in {64, 128, 256}, q_heads / kv_heads <= 256; else OQ_INVALID_ARGUMENT.
-   Up to 8 query heads per KV head read each cached row once per step; a larger group runs as
-   equal subgroups of at most 8 heads (16: two of 8), each reading the group's rows.
+   non-finite score yields non-finite outputs where the reference throws.  key_dim == value_dim in
+   {64, 128, 256} with q_heads / kv_heads <= 256 takes the chunked kernels: up to 8 query heads per
+   KV head read each cached row once per step; a larger group runs as equal subgroups of at most 8
+   heads (16: two of 8), each reading the group's rows.  Any other shape (key_dim <= 8192; wider
+   keys -> OQ_INVALID_ARGUMENT) runs one workgroup per query head in the reference's order (double
+   dot products and denominator, F32 value sums in token order), the cached rows read once per
+   query head.
    The cache must belong to ctx, and the step is refused while ctx's stream is being captured
    (OQ_INVALID_ARGUMENT; both apply to oq_attention_block_step too). */
 int oq_attention_step(oq_context* ctx, const float* q_dev, uint64_t q_heads, const float* k_dev,

@@ -32,7 +32,7 @@ constexpr const char* kKnobNames[kKnobCount] = {
     "OQ_GEMV_WG_PER_CU", "OQ_STREAM_WG_PER_CU",  "OQ_GEMV_STREAM", "OQ_STREAM_WAVES",  "OQ_GEMV_STREAM_MT",
     "OQ_GEMV_ROWS",     "OQ_GEMV_WAVES",         "OQ_GEMV_ROWS_MT", "OQ_BLOCK_STREAM", "OQ_BLOCK_FUSED",
     "OQ_GEMM_MFMA",     "OQ_FUSED_QUANT",        "OQ_GEMM_INT8",   "OQ_ATTN_WG_PER_CU", "OQ_ATTN_MIN_CHUNK",
-    "OQ_GEMM_MIN_K",    "OQ_ATTN_SHARE_MIN",
+    "OQ_GEMM_MIN_K",    "OQ_ATTN_SHARE_MIN",     "OQ_ANY_SHAPE",
 };
 
 struct KnobTable {
@@ -364,11 +364,13 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
     if (!(b->eps > 0.0f) || !std::isfinite(b->eps)) {
         return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 RMSNorm epsilon must be positive and finite");
     }
-    if (!oq::deltanet_dims_supported(dk, dv, K)) {
-        return fail(ctx, OQ_INVALID_ARGUMENT,
-                    "DeltaNet block device path needs key_dim in {32,64,128}, value_dim in {64,128,192,256}, conv_kernel <= 16");
+    if (!oq::deltanet_dims_any(dk, dv, K)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "DeltaNet block device path needs key_dim <= 4096");
     }
-    if (E > 0x7FFFFFFF || F > 0x7FFFFFFF || Hv * dv > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "block too large");
+    if (E > 0x7FFFFFFF || F > 0x7FFFFFFF || Hv * dv > 0x7FFFFFFF || 2 * Hk * dk + Hv * dv > 0x7FFFFFFF ||
+        Hv * oq::delta_chunks(dv) > 0x7FFFFFFF) {
+        return fail(ctx, OQ_OVERFLOW, "block too large");
+    }
     const uint64_t V = Hv * dv, C = 2 * Hk * dk + V;
     const BlockLayout lay = block_layout(b);
     if (ext_ws != nullptr && lay.total_floats * sizeof(float) > ext_ws_bytes) {
@@ -475,7 +477,9 @@ int deltanet_step(oq_context* ctx, const oq_deltanet_block* b, float* hist, floa
     down.add = resid;
     down.sum_out = y;
     const bool even = C % 2 == 0 && V % 2 == 0 && Hv % 2 == 0 && E % 2 == 0;
-    const bool fused = knob_flag(oq::kBlockFused, true) && even && aligned(x, 16) && oq::gemv_block_supported(in) &&
+    // other shapes: one launch per stage, the delta rule on its any-shape kernel
+    const bool fused = knob_flag(oq::kBlockFused, true) && even && aligned(x, 16) &&
+                       oq::deltanet_dims_supported(dk, dv, K) && oq::gemv_block_supported(in) &&
                        oq::gemv_block_supported(outp) && oq::gemv_block_supported(ffn_in) &&
                        oq::gemv_block_supported(down);
     if (fused) {
@@ -665,12 +669,13 @@ int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, floa
     if (!(b->eps > 0.0f) || !std::isfinite(b->eps)) {
         return fail(ctx, OQ_INVALID_ARGUMENT, "Qwen3.5 RMSNorm epsilon must be positive and finite");
     }
-    if (!oq::deltanet_dims_supported(dk, dv, K)) {
-        return fail(ctx, OQ_INVALID_ARGUMENT,
-                    "DeltaNet block device path needs key_dim in {32,64,128}, value_dim in {64,128,192,256}, conv_kernel <= 16");
+    if (!oq::deltanet_dims_any(dk, dv, K)) {
+        return fail(ctx, OQ_INVALID_ARGUMENT, "DeltaNet block device path needs key_dim <= 4096");
     }
     const uint64_t V = Hv * dv, C = 2 * Hk * dk + V;
-    if (m * std::max({E, F, C}) > 0x7FFFFFFF) return fail(ctx, OQ_OVERFLOW, "block too large");
+    if (m * std::max({E, F, C}) > 0x7FFFFFFF || Hv * oq::delta_chunks(dv) > 0x7FFFFFFF) {
+        return fail(ctx, OQ_OVERFLOW, "block too large");
+    }
     if (int rc = check_block_weight(ctx, b->qkv, E, C, "qkv")) return rc;
     if (int rc = check_block_weight(ctx, b->z, E, V, "z")) return rc;
     if (int rc = check_block_weight(ctx, b->beta, E, Hv, "beta")) return rc;
@@ -684,6 +689,19 @@ int deltanet_steps(oq_context* ctx, const oq_deltanet_block* b, uint64_t m, floa
     }
     if (!aligned(x, 16) || !aligned(y, 4) || !aligned(hist, 4) || !aligned(state, 4) || (trace && !aligned(trace, 4))) {
         return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer (x 16-byte, others 4-byte)");
+    }
+    if (!oq::deltanet_dims_supported(dk, dv, K)) {
+        // shapes outside the token-batched kernels: the single step's per-stage launches, token by
+        // token (token t's trace at trace + t * the single step's trace size, as below)
+        const BlockLayout one = block_layout(b);
+        uint64_t per_token = 0;
+        for (int i = 0; i < 16; ++i) per_token += one.sizes[i];
+        for (uint64_t t = 0; t < m; ++t) {
+            if (int rc = deltanet_step(ctx, b, hist, state, x + t * E, y + t * E, trace ? trace + t * per_token : nullptr,
+                                       nullptr, 0))
+                return rc;
+        }
+        return OQ_OK;
     }
     const StepsLayout lay = steps_layout(b, m);
     if (int rc = ensure_work(ctx, lay.total_floats * sizeof(float))) return rc;
@@ -1200,15 +1218,35 @@ int check_cache(oq_context* ctx, const oq_kv_cache* c) {
 
 // the attention launch over a cache whose new token (index T - 1 = cache->length) is given by
 // new_k / new_v, or already stored (both null); the partials go to `part`
+// the chunked kernels' shapes; every other one takes the any-shape kernels
+bool attention_fast(const oq_kv_cache* c, uint64_t q_heads) {
+    return c->key_dim == c->value_dim && oq::attention_dims_supported(c->key_dim, q_heads / c->kv_heads) &&
+           !knob_flag(oq::kAnyShape, false);
+}
+
 int attention_shape(oq_context* ctx, const oq_kv_cache* c, uint64_t q_heads, oq::AttnLaunch& L, uint64_t ahead = 0,
                     uint64_t token_groups = 1) {
     const uint64_t rep = q_heads / c->kv_heads;
-    if (c->key_dim != c->value_dim || !oq::attention_dims_supported(c->key_dim, rep)) {
-        return fail(ctx, OQ_INVALID_ARGUMENT,
-                    "attention device path needs key_dim == value_dim in {64, 128, 256} and at most 256 query heads per "
-                    "KV head");
-    }
     const uint64_t T = c->length + 1 + ahead;  // the token `ahead` places after the next one to append
+    if (!attention_fast(c, q_heads)) {
+        if (c->key_dim > oq::kAttnAnyMaxDim) {
+            return fail(ctx, OQ_INVALID_ARGUMENT, "attention device path needs key_dim <= 8192");
+        }
+        if (T > 0xFFFFFFFFull || c->kv_heads > 0xFFFF || q_heads > 0x7FFFFFFF || c->value_dim > 0xFFFFFFFFull) {
+            return fail(ctx, OQ_INVALID_ARGUMENT, "attention device path supports at most 4294967295 cached tokens");
+        }
+        L.any = true;
+        L.T = (uint32_t)T;
+        L.Hkv = (uint32_t)c->kv_heads;
+        L.rep = (uint32_t)rep;
+        L.D = (uint32_t)c->key_dim;
+        L.Dv = (uint32_t)c->value_dim;
+        L.scale = 1.0f / std::sqrt((float)c->key_dim);  // reference_kernels.cpp:158
+        L.keys = c->keys;
+        L.values = c->values;
+        L.f16 = c->type == OQ_TYPE_F16;
+        return OQ_OK;
+    }
     uint32_t chunk = 0, nchunks = 0;
     oq::attention_plan(T, c->kv_heads, rep, chunk, nchunks, token_groups);
     if (nchunks > oq::kAttnMaxChunks || T > 0xFFFFFFFFull || c->kv_heads > 0xFFFF) {
@@ -1227,17 +1265,22 @@ int attention_shape(oq_context* ctx, const oq_kv_cache* c, uint64_t q_heads, oq:
     return OQ_OK;
 }
 
+// The attention launch's scratch: the chunks' partial sums, or the any-shape kernels' scores
+uint64_t attention_scratch_floats(const oq::AttnLaunch& L) {
+    return L.any ? oq::attention_any_floats((uint64_t)L.Hkv * L.rep, L.T)
+                 : oq::attention_partial_floats(L.Hkv, L.rep, L.D, L.nchunks);
+}
+
 // Workspace of one attention block step: the 15 trace fields, the normalised input and the
-// attention partials, each padded to 64 floats.
+// attention scratch (P floats), each padded to 64 floats.
 struct AttnLayout {
     uint64_t sizes[17];
     uint64_t off[17];
     uint64_t total_floats;
 };
 
-AttnLayout attn_layout(const oq_attention_block* b, uint32_t nchunks) {
+AttnLayout attn_layout(const oq_attention_block* b, uint64_t P) {
     const uint64_t E = b->embedding, D = b->head_dim, F = b->ffn, Q = b->q_heads * D, KV = b->kv_heads * D;
-    const uint64_t P = oq::attention_partial_floats(b->kv_heads, b->q_heads / b->kv_heads, D, nchunks);
     AttnLayout l{{2 * Q, KV, KV, Q, KV, Q, Q, Q, E, E, E, F, F, F, E, E, P}, {}, 0};
     for (int i = 0; i < 17; ++i) {
         l.off[i] = l.total_floats;
@@ -1414,7 +1457,7 @@ int oq_attention_step(oq_context* ctx, const float* q, uint64_t q_heads, const f
     if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16)) {
         return fail(ctx, OQ_INVALID_ARGUMENT, "attention buffers must be 16-byte aligned");
     }
-    const uint64_t pf = oq::attention_partial_floats(L.Hkv, L.rep, L.D, L.nchunks);
+    const uint64_t pf = attention_scratch_floats(L);
     if (int rc = ensure_scratch(ctx, pf * sizeof(float))) return rc;
     L.q = q;
     L.new_k = k;
@@ -1426,8 +1469,11 @@ int oq_attention_step(oq_context* ctx, const float* q, uint64_t q_heads, const f
     return rc;
 }
 
-int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_cache* cache,
-                            const uint64_t position[3], const float* x, float* y, float* trace) {
+// oq_attention_block_step with x aligned to x_align bytes (16 through the C ABI; 4 for the token rows
+// of a several-token call on the any-shape kernels, whose embedding need not be a multiple of 4)
+static int attention_block_step_core(oq_context* ctx, const oq_attention_block* b, oq_kv_cache* cache,
+                                     const uint64_t position[3], const float* x, float* y, float* trace,
+                                     uint64_t x_align) {
     if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
     if (!b || !x || !y) return fail(ctx, OQ_INVALID_ARGUMENT, "null argument");
     if (int rc = check_cache(ctx, cache)) return rc;
@@ -1456,11 +1502,11 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_
     if (!b->input_norm || !b->q_norm || !b->k_norm || !b->post_norm) {
         return fail(ctx, OQ_INVALID_ARGUMENT, "null block vector");
     }
-    if (!aligned(x, 16) || !aligned(y, 4)) return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer");
+    if (!aligned(x, x_align) || !aligned(y, 4)) return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer");
     if (cache->length >= cache->capacity) return fail(ctx, OQ_OVERFLOW, "KV cache capacity exceeded");
     oq::AttnLaunch L{};
     if (int rc = attention_shape(ctx, cache, Hq, L)) return rc;
-    const AttnLayout lay = attn_layout(b, L.nchunks);
+    const AttnLayout lay = attn_layout(b, attention_scratch_floats(L));
     if (int rc = ensure_work(ctx, lay.total_floats * sizeof(float))) return rc;
     float* ws = static_cast<float*>(ctx->work.ptr);
     const uint64_t* off = lay.off;
@@ -1520,7 +1566,7 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_
     prep.k_norm = b->k_norm;
     prep.eps = b->eps;
     prep.rope = rp;
-    prep.qcur = trace ? qcur : nullptr;
+    prep.qcur = trace || L.any ? qcur : nullptr;  // the any-shape attention reads the rotated queries from there
     prep.kcur = trace ? kcur : nullptr;
     L.prep = &prep;
     L.part = part;
@@ -1531,7 +1577,7 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_
     L.gated = gated;
 
     const bool even = E % 2 == 0 && F % 2 == 0;
-    const bool fused_in = knob_flag(oq::kBlockFused, true) && even && oq::gemv_block_supported(in);
+    const bool fused_in = knob_flag(oq::kBlockFused, true) && even && aligned(x, 16) && oq::gemv_block_supported(in);
     const bool fused_tail = knob_flag(oq::kBlockFused, true) && even && oq::gemv_block_supported(outp) &&
                             oq::gemv_block_supported(ffn_in) && oq::gemv_block_supported(down);
     if (fused_in) {
@@ -1573,6 +1619,11 @@ int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_
     return rc;
 }
 
+int oq_attention_block_step(oq_context* ctx, const oq_attention_block* b, oq_kv_cache* cache,
+                            const uint64_t position[3], const float* x, float* y, float* trace) {
+    return attention_block_step_core(ctx, b, cache, position, x, y, trace, 16);
+}
+
 int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv_cache* cache, uint64_t m,
                              const uint64_t* positions, const float* x, float* y, float* trace) {
     if (!ctx) return fail(nullptr, OQ_INVALID_ARGUMENT, "null context");
@@ -1610,6 +1661,17 @@ int oq_attention_block_steps(oq_context* ctx, const oq_attention_block* b, oq_kv
         return fail(ctx, OQ_INVALID_ARGUMENT, "misaligned buffer (x 16-byte, others 4-byte)");
     }
     if (cache->capacity - cache->length < m) return fail(ctx, OQ_OVERFLOW, "KV cache capacity exceeded");
+    if (!attention_fast(cache, Hq)) {
+        // shapes outside the chunked kernels: the single step token by token (token t's trace at
+        // trace + t * the single step's trace size, as below)
+        const uint64_t per_token = 2 * Q + KV + KV + Q + KV + Q + Q + Q + E + E + E + F + F + F + E;
+        for (uint64_t t = 0; t < m; ++t) {
+            if (int rc = attention_block_step_core(ctx, b, cache, positions + 3 * t, x + t * E, y + t * E,
+                                                   trace ? trace + t * per_token : nullptr, 4))
+                return rc;
+        }
+        return OQ_OK;
+    }
     // the attention of all m tokens in one chunk launch, shaped for the last token (its chunks lay
     // out every token's partials); a grid too large for one launch runs the tokens one by one
     // the chunks sized so that the launch's workgroups over all token groups fill the GPU about as

@@ -254,12 +254,6 @@ OQ_DEVICE void rotate_pair(float* x, uint32_t f, uint32_t half, float c, float s
     x[half + f] = b * c + a * s;
 }
 
-OQ_DEVICE double wave_sum_f64(double v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 // One row of the block's preparation in wave registers (lane i holding elements i*VW ..): the
 // RMSNorm of rms_norm_rows (qwen35_block.cpp:161-189, sum of squares in double; called at :691-698)
 // with weight w, written to LDS row y for the rotation
@@ -928,6 +922,162 @@ hipError_t launch_tokens_d(const AttnLaunch& L, const AttnTokens& tk, hipStream_
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- any shape
+//
+// Key and value widths outside {64, 128, 256}, a key width different from the value width, or more
+// than 256 query heads per KV head (the reference's causal_attention_step and block take any
+// shape): plain kernels in the reference's order, one workgroup per head.
+
+// The block's per-head preparation for one token: workgroup r < Hq normalises query head r with
+// q_norm and rotates it into qcur; workgroup Hq + g normalises key head g with k_norm, rotates it
+// into cache row `row` (and kcur when given) and stores value head g beside it (unless an F16
+// cache's value row is already stored).  The row sits in dynamic LDS (D floats); its sum of squares
+// is in double (rms_norm_rows, qwen35_block.cpp:161-189), the rotation rope_cs / rotate_pair's.
+template <typename KT>
+__global__ __launch_bounds__(256) void attention_prep_any_kernel(AttnPrep p, uint32_t Hq, uint32_t Hkv, uint32_t D,
+                                                                 uint64_t row, KT* __restrict__ keys,
+                                                                 KT* __restrict__ values) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(16) float xrow[];  // [D]
+    __shared__ double red[4];
+    const uint32_t r = blockIdx.x;
+    const bool is_q = r < Hq;
+    const uint32_t h = is_q ? r : r - Hq;
+    const float* src = is_q ? p.qfull + (uint64_t)h * 2 * D : p.kp + (uint64_t)h * D;
+    const float* w = is_q ? p.q_norm : p.k_norm;
+    double ss = 0.0;
+    for (uint32_t i = threadIdx.x; i < D; i += 256) {
+        const float v = src[i];
+        xrow[i] = v;
+        ss += (double)v * (double)v;
+    }
+    ss = wave_sum_f64(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = red[0] + red[1] + red[2] + red[3];
+    const float inv = (float)(1.0 / sqrt(ss / (double)D + (double)p.eps));
+    for (uint32_t i = threadIdx.x; i < D; i += 256) xrow[i] = xrow[i] * inv * w[i];
+    __syncthreads();
+    const uint32_t half = p.rope.rotary_dim / 2;
+    for (uint32_t f = threadIdx.x; f < half; f += 256) {
+        float c, sn;
+        rope_cs(f, p.rope, c, sn);
+        rotate_pair(xrow, f, half, c, sn);
+    }
+    __syncthreads();
+    if (is_q) {
+        float* dst = p.qcur + (uint64_t)h * D;
+        for (uint32_t i = threadIdx.x; i < D; i += 256) dst[i] = xrow[i];
+        return;
+    }
+    KT* krow = keys + (row * Hkv + h) * D;
+    KT* vrow = values + (row * Hkv + h) * D;
+    const float* vsrc = p.vp + (uint64_t)h * D;
+    for (uint32_t i = threadIdx.x; i < D; i += 256) {
+        if (p.kcur != nullptr) p.kcur[(uint64_t)h * D + i] = xrow[i];
+        krow[i] = (KT)xrow[i];
+        if (!p.v_stored) vrow[i] = (KT)vsrc[i];
+    }
+}
+
+// The new token's key rows [Hkv][Dk] and value rows [Hkv][Dv] stored into cache row `row`
+// (KvCache::append, hybrid_cache.cpp:154-169; an F16 cache rounds to nearest even)
+template <typename KT>
+__global__ __launch_bounds__(256) void kv_append_any_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                            KT* __restrict__ keys, KT* __restrict__ values, uint64_t row,
+                                                            uint64_t nk, uint64_t nv) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (k != nullptr && i < nk) keys[row * nk + i] = (KT)k[i];
+    if (v != nullptr && i < nv) values[row * nv + i] = (KT)v[i];
+}
+
+// Query head h over the T cached rows of KV head h / rep (causal_attention_step,
+// reference_kernels.cpp:152-193): each score a double dot product in dimension order, rounded to
+// F32 and scaled; p = exp(s - max) in F32, the denominator in double (per thread over its tokens,
+// then over the threads), p / denominator in double rounded to F32; each output column the F32 sum
+// of p_t * v_t in token order, as the reference adds it.  Scores and then probabilities are kept
+// in scores [T]; the query in dynamic LDS (Dk floats).  With a gate: gate_s = sigmoid(gate),
+// gated = out * gate_s (qwen35_block.cpp:734-741).
+template <typename KT>
+__global__ __launch_bounds__(256) void attention_any_kernel(const float* __restrict__ q, const KT* __restrict__ keys,
+                                                            const KT* __restrict__ values, uint32_t T, uint32_t Hkv,
+                                                            uint32_t rep, uint32_t Dk, uint32_t Dv, float scale,
+                                                            float* __restrict__ scores, float* __restrict__ out,
+                                                            const float* __restrict__ gate, uint32_t gate_stride,
+                                                            float* __restrict__ gate_s, float* __restrict__ gated) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(16) float qs[];  // [Dk]
+    __shared__ float redf[4];
+    __shared__ double redd[4];
+    const uint32_t h = blockIdx.x, g = h / rep;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (uint32_t i = threadIdx.x; i < Dk; i += 256) qs[i] = q[(uint64_t)h * Dk + i];
+    __syncthreads();
+    float* sc = scores + (uint64_t)h * T;
+    float mx = -INFINITY;
+    for (uint32_t t = threadIdx.x; t < T; t += 256) {
+        const KT* k = keys + ((uint64_t)t * Hkv + g) * Dk;
+        double dot = 0.0;
+        for (uint32_t d = 0; d < Dk; ++d) dot += (double)qs[d] * (double)(float)k[d];
+        const float s = (float)dot * scale;
+        sc[t] = s;
+        mx = fmaxf(mx, s);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0) redf[wave] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+    double l = 0.0;
+    for (uint32_t t = threadIdx.x; t < T; t += 256) {
+        const float e = expf(sc[t] - M);
+        sc[t] = e;
+        l += (double)e;
+    }
+    l = wave_sum_f64(l);
+    if (lane == 0) redd[wave] = l;
+    __syncthreads();
+    const double den = redd[0] + redd[1] + redd[2] + redd[3];
+    for (uint32_t t = threadIdx.x; t < T; t += 256) sc[t] = (float)((double)sc[t] / den);
+    __syncthreads();  // every probability stored before any column reads them
+    for (uint32_t d = threadIdx.x; d < Dv; d += 256) {
+        float acc = 0.0f;
+        for (uint32_t t = 0; t < T; ++t) acc += sc[t] * (float)values[((uint64_t)t * Hkv + g) * Dv + d];
+        const uint64_t o = (uint64_t)h * Dv + d;
+        if (out != nullptr) out[o] = acc;
+        if (gate != nullptr) {
+            const float gs = sigmoid_ref(gate[(uint64_t)h * gate_stride + d]);
+            if (gate_s != nullptr) gate_s[o] = gs;
+            gated[o] = acc * gs;
+        }
+    }
+}
+
+template <typename KT>
+hipError_t launch_any(const AttnLaunch& L, hipStream_t s) {
+    const uint32_t Hq = L.Hkv * L.rep;
+    KT* keys = static_cast<KT*>(L.keys);
+    KT* values = static_cast<KT*>(L.values);
+    const uint64_t row = (uint64_t)L.T - 1;
+    const float* q = L.q;
+    if (L.prep != nullptr) {
+        const AttnPrep& p = *L.prep;
+        if (p.qcur == nullptr || L.D != L.Dv) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(attention_prep_any_kernel<KT>, dim3(Hq + L.Hkv), dim3(256), (uint64_t)L.D * sizeof(float), s,
+                           p, Hq, L.Hkv, L.D, row, keys, values);
+        q = p.qcur;
+    } else if (L.new_k != nullptr || L.new_v != nullptr) {
+        const uint64_t nk = (uint64_t)L.Hkv * L.D, nv = (uint64_t)L.Hkv * L.Dv;
+        const uint64_t n = nk > nv ? nk : nv;
+        hipLaunchKernelGGL(kv_append_any_kernel<KT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, L.new_k, L.new_v,
+                           keys, values, row, nk, nv);
+    }
+    if (L.gate != nullptr && L.gated == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(attention_any_kernel<KT>, dim3(Hq), dim3(256), (uint64_t)L.D * sizeof(float), s, q, keys, values,
+                       L.T, L.Hkv, L.rep, L.D, L.Dv, L.scale, L.part, L.out, L.gate, L.gate_stride, L.gate_s, L.gated);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_attention_tokens(const AttnLaunch& L, const AttnTokens& tk, hipStream_t s) {
@@ -984,7 +1134,15 @@ hipError_t launch_f32_to_f16(const float* src, void* dst, uint64_t n, hipStream_
     return hipGetLastError();
 }
 
+uint64_t attention_any_floats(uint64_t q_heads, uint64_t T) { return q_heads * T; }
+
 hipError_t launch_attention(const AttnLaunch& L, hipStream_t s) {
+    if (L.any) {
+        if (L.T == 0 || L.D == 0 || L.Dv == 0 || L.D > kAttnAnyMaxDim || L.Hkv == 0 || L.rep == 0 ||
+            (uint64_t)L.Hkv * L.rep > 0x7FFFFFFFull)
+            return hipErrorInvalidValue;
+        return L.f16 ? launch_any<_Float16>(L, s) : launch_any<float>(L, s);
+    }
     switch (L.D) {
         case 64: return launch_d<64>(L, s);
         case 128: return launch_d<128>(L, s);

@@ -228,8 +228,6 @@ OQ_DEVICE Q8KLane quantize_q8k_block_wave(float4 v, int lane) {
     return r;
 }
 
-// One quantized block stored in GGML's block_q8_K layout (f32 d, 256 int8 quants, 16 int16 bsums)
-// by the wave that quantized it
 // sum over the wave, butterfly order (every lane gets it)
 OQ_DEVICE double wave_sum_f64(double v) {
 #pragma unroll
@@ -260,6 +258,8 @@ OQ_DEVICE float silu_ref(float v) {
     return v * sigmoid_ref(v);
 }
 
+// One quantized block stored in GGML's block_q8_K layout (f32 d, 256 int8 quants, 16 int16 bsums)
+// by the wave that quantized it
 OQ_DEVICE void store_q8k_block(uint8_t* ob, const Q8KLane& r, int lane) {
     *reinterpret_cast<uint32_t*>(ob + 4 + 4 * lane) = r.qword;
     if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(ob + 260 + 2 * (lane >> 2)) = (int16_t)r.quad_bsum;

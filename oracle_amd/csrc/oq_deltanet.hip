@@ -308,6 +308,98 @@ __global__ __launch_bounds__(256) void delta_kernel(const float* __restrict__ co
     for (int i = 0; i < KS; ++i) scol[(uint64_t)i * dv] = s[i];
 }
 
+// Any key and value width (the reference's gated_delta_step, reference_kernels.cpp:227-335, takes any
+// shape): delta_kernel's workgroups (one per (value head, chunk of COLS value columns), the last chunk
+// of a head possibly partial; 256 threads = 8 key slices x 32 columns, slice j owning keys
+// [j ks, min(dk, (j + 1) ks)) with ks = ceil(dk / 8)) and its arithmetic in the same order, with the
+// state in HBM instead of registers: a thread reads its entries for the memory sum and rewrites them
+// with the update, every token.  At the widths delta_kernel takes, the two give the same bits.  The
+// normalised query and key sit in dynamic LDS (2 dk floats).  query_scale = 1/sqrt(dk), rounded on
+// the host as the register kernel's compile-time constant is.
+__global__ __launch_bounds__(256) void delta_any_kernel(const float* __restrict__ conv, uint32_t key_heads, uint32_t dk,
+                                                        uint32_t dv, const float* __restrict__ beta_s,
+                                                        const float* __restrict__ log_decay, float eps, float query_scale,
+                                                        float* __restrict__ state, float* __restrict__ rec_out,
+                                                        double* __restrict__ head_ss, uint32_t tokens,
+                                                        uint32_t value_heads) {
+    constexpr int COLS = kDeltaCols, SLICES = 256 / COLS;
+    extern __shared__ __align__(16) float nqk[];  // nq[dk], then nk[dk]
+    float* nq = nqk;
+    float* nk = nqk + dk;
+    __shared__ float mem_part[SLICES][COLS];
+    __shared__ double out_part[SLICES][COLS];
+    const uint32_t chunks = (dv + COLS - 1) / COLS;
+    const uint32_t h = blockIdx.x / chunks, chunk = blockIdx.x % chunks;
+    const uint32_t col = threadIdx.x % COLS, slice = threadIdx.x / COLS;
+    const uint32_t v = chunk * COLS + col;
+    const bool vok = v < dv;
+    const uint32_t ks = (dk + SLICES - 1) / SLICES;
+    const uint32_t d0 = min(dk, slice * ks), d1 = min(dk, d0 + ks);
+    float* scol = state + (uint64_t)h * dk * dv + v;  // key d's entry at scol[d * dv]
+    const uint32_t kw = key_heads * dk;
+    const uint64_t cstride = 2ull * kw + (uint64_t)value_heads * dv;  // one token's conv row
+    for (uint32_t t = 0; t < tokens; ++t) {
+        if (t > 0) __syncthreads();  // the previous token's reads of nq / nk and the partial sums are done
+        const float* q = conv + t * cstride + (uint64_t)(h % key_heads) * dk;
+        const float* k = conv + t * cstride + kw + (uint64_t)(h % key_heads) * dk;
+        const float vv = vok ? conv[t * cstride + 2ull * kw + (uint64_t)h * dv + v] : 0.0f;
+        const float ldh = log_decay[(uint64_t)t * value_heads + h];
+        const float beta = beta_s[(uint64_t)t * value_heads + h];
+        if (threadIdx.x < 64) {
+            // the first wave: L2 norms of the head's query and key, lane i summing elements i, i + 64, ...
+            const uint32_t lane = threadIdx.x;
+            double qs = 0.0, kss = 0.0;
+            for (uint32_t e = lane; e < dk; e += 64) {
+                qs = qs + (double)q[e] * (double)q[e];
+                kss = kss + (double)k[e] * (double)k[e];
+            }
+            qs = wave_sum_f64(qs);
+            kss = wave_sum_f64(kss);
+            const double ql = sqrt(qs), kl = sqrt(kss);
+            const float iq = (float)(1.0 / (ql > (double)eps ? ql : (double)eps));
+            const float ik = (float)(1.0 / (kl > (double)eps ? kl : (double)eps));
+            for (uint32_t e = lane; e < dk; e += 64) {
+                nq[e] = q[e] * iq * query_scale;
+                nk[e] = k[e] * ik;
+            }
+        }
+        __syncthreads();
+        const float decay = expf(ldh);
+        float mem = 0.0f;
+        if (vok) {
+            for (uint32_t d = d0; d < d1; ++d) mem = mem + (scol[(uint64_t)d * dv] * decay) * nk[d];
+        }
+        mem_part[slice][col] = mem;
+        __syncthreads();
+        float memory = 0.0f;
+#pragma unroll
+        for (int j = 0; j < SLICES; ++j) memory = memory + mem_part[j][col];
+        const float delta = (vv - memory) * beta;
+        double o = 0.0;
+        if (vok) {
+            for (uint32_t d = d0; d < d1; ++d) {
+                float sv = scol[(uint64_t)d * dv] * decay;
+                sv = sv + nk[d] * delta;
+                scol[(uint64_t)d * dv] = sv;
+                o = o + (double)sv * (double)nq[d];
+            }
+        }
+        out_part[slice][col] = o;
+        __syncthreads();
+        if (slice == 0) {
+            double out = 0.0;
+#pragma unroll
+            for (int j = 0; j < SLICES; ++j) out = out + out_part[j][col];
+            const float of = (float)out;
+            if (vok) rec_out[(uint64_t)t * value_heads * dv + (uint64_t)h * dv + v] = of;
+            double sq = vok ? (double)of * (double)of : 0.0;
+#pragma unroll
+            for (int off = COLS / 2; off >= 1; off >>= 1) sq += __shfl_xor(sq, off, 64);
+            if (col == 0) head_ss[(uint64_t)t * value_heads * chunks + (uint64_t)h * chunks + chunk] = sq;
+        }
+    }
+}
+
 // gated[h][v] = RMSNorm(rec[h])[v] * out_norm[v] * SiLU(z[h][v]) (qwen35_block.cpp:579-588), the
 // head's sum of squares taken from the delta kernel's per-chunk partials (added in chunk order).
 __global__ __launch_bounds__(256) void gated_norm_kernel(const float* __restrict__ rec, const double* __restrict__ head_ss,
@@ -383,8 +475,12 @@ unsigned blocks_of(uint64_t n, unsigned t) { return (unsigned)((n + t - 1) / t);
 
 bool deltanet_dims_supported(uint64_t key_dim, uint64_t value_dim, uint64_t conv_kernel) {
     return (key_dim == 32 || key_dim == 64 || key_dim == 128) && value_dim >= 64 && value_dim <= 256 &&
-           value_dim % 64 == 0 &&
-           conv_kernel >= 1 && conv_kernel <= kMaxConvKernel;
+           value_dim % 64 == 0 && conv_kernel >= 1 && conv_kernel <= kMaxConvKernel && knob(kAnyShape, 0) == 0;
+}
+
+bool deltanet_dims_any(uint64_t key_dim, uint64_t value_dim, uint64_t conv_kernel) {
+    return key_dim >= 1 && key_dim <= kDeltaMaxKeyDim && value_dim >= 1 && value_dim <= 0xFFFFFFFFull &&
+           conv_kernel >= 1 && conv_kernel <= 0xFFFFFFFFull;
 }
 
 hipError_t launch_rmsnorm(const float* a, const float* b, const float* w, uint64_t n, float eps, float* sum_out,
@@ -437,7 +533,18 @@ hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_he
                         double* head_ss, const float* z, float* z_silu, hipStream_t s, uint64_t tokens) {
     if (tokens > 1 && z_silu != nullptr) return hipErrorInvalidValue;  // SiLU(z) is a single-token epilogue
     if ((z == nullptr) != (z_silu == nullptr)) return hipErrorInvalidValue;
-    if (dv % kDeltaCols != 0) return hipErrorInvalidValue;
+    const bool regs = (dk == 32 || dk == 64 || dk == 128) && dv % kDeltaCols == 0 && knob(kAnyShape, 0) == 0;
+    if (!regs) {
+        if (z_silu != nullptr || dk == 0 || dk > kDeltaMaxKeyDim || dv == 0 || value_heads == 0 || key_heads == 0)
+            return hipErrorInvalidValue;
+        const uint64_t grid = value_heads * delta_chunks(dv);
+        if (grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
+        const float query_scale = 1.0f / std::sqrt((float)dk);
+        hipLaunchKernelGGL(delta_any_kernel, dim3((unsigned)grid), dim3(256), 2 * dk * sizeof(float), s, conv,
+                           (uint32_t)key_heads, (uint32_t)dk, (uint32_t)dv, beta_s, log_decay, eps, query_scale, state,
+                           rec_out, head_ss, (uint32_t)tokens, (uint32_t)value_heads);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)(value_heads * (dv / kDeltaCols))), block(256);
     switch (dk) {
         case 32:
@@ -477,7 +584,7 @@ hipError_t launch_gated_norm(const float* rec, const double* head_ss, const floa
     return hipGetLastError();
 }
 
-uint64_t delta_chunks(uint64_t dv) { return dv / kDeltaCols; }
+uint64_t delta_chunks(uint64_t dv) { return (dv + kDeltaCols - 1) / kDeltaCols; }
 
 hipError_t launch_swiglu(const float* gate, const float* up, uint64_t n, float* act, hipStream_t s, uint8_t* q8) {
     if (q8 != nullptr) {

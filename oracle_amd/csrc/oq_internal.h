@@ -61,6 +61,7 @@ enum Knob : int {
     kAttnMinChunk,  // OQ_ATTN_MIN_CHUNK
     kGemmMinK,  // OQ_GEMM_MIN_K: shortest rows (K) of the matrix-core path (default 4096; measurement only)
     kAttnShareMin,  // OQ_ATTN_SHARE_MIN: cached rows from which a multi-token attention workgroup serves several tokens
+    kAnyShape,  // OQ_ANY_SHAPE: 1 runs the delta rule and attention on the any-shape kernels at every shape (testing)
     kKnobCount
 };
 int knob(Knob k, int fallback);  // the option's value, or fallback when it is unset
@@ -183,7 +184,11 @@ hipError_t launch_gemm_q4k_i8(const DeviceMatrix& w, int m, const float* x, cons
                               void* scratch, hipStream_t s);
 
 // ---- oq_deltanet.hip  (Gated DeltaNet decode block: kernels between the projections)
+// the shapes of the fused block launches and the register-resident delta rule; every other shape
+// takes the per-stage launches with the any-shape delta rule (deltanet_dims_any)
 bool deltanet_dims_supported(uint64_t key_dim, uint64_t value_dim, uint64_t conv_kernel);
+constexpr uint64_t kDeltaMaxKeyDim = 4096;  // the any-shape delta rule's normalised q / k in LDS
+bool deltanet_dims_any(uint64_t key_dim, uint64_t value_dim, uint64_t conv_kernel);
 // rows consecutive rows of n values (one workgroup each)
 // q8, when not null, also receives the rows' Q8_K blocks (n a multiple of 256)
 hipError_t launch_rmsnorm(const float* a, const float* b, const float* w, uint64_t n, float eps, float* sum_out,
@@ -197,10 +202,12 @@ hipError_t launch_conv_gates_tokens(const float* qkv, const float* conv_w, float
                                     uint64_t kernel, const float* beta, const float* alpha, const float* dt_bias,
                                     const float* decay, uint64_t heads, uint64_t tokens, float* conv_out,
                                     float* beta_s, float* log_decay, hipStream_t s);
-// the delta rule over Hv * dv/32 workgroups: rec_out[Hv][dv] and head_ss[Hv][dv/32], the per-chunk double
-// sums of rec_out^2 that the head's gated RMSNorm takes (launch_gated_norm, or the out projection's staging)
-// z / z_silu: when not null, the launch also stores SiLU(z) of the block's gate row (the value
-// heads' columns, [Hv][dv]) for the out projection's staging
+// the delta rule over Hv * ceil(dv/32) workgroups: rec_out[Hv][dv] and head_ss[Hv][delta_chunks(dv)], the
+// per-chunk double sums of rec_out^2 that the head's gated RMSNorm takes (launch_gated_norm, or the out
+// projection's staging).  Key widths 32, 64, 128 with dv a multiple of 32 keep the state in registers; any
+// other shape (or OQ_ANY_SHAPE=1) runs the any-shape kernel.
+// z / z_silu: when not null (register-resident shapes only), the launch also stores SiLU(z) of the
+// block's gate row (the value heads' columns, [Hv][dv]) for the out projection's staging
 hipError_t launch_delta(const float* conv, uint64_t key_heads, uint64_t value_heads, uint64_t dk, uint64_t dv,
                         const float* beta_s, const float* log_decay, float eps, float* state, float* rec_out,
                         double* head_ss, const float* z, float* z_silu, hipStream_t s, uint64_t tokens = 1);
@@ -246,9 +253,17 @@ struct AttnLaunch {
     float* gate_s;             // sigmoid(gate) [Hq][D] (or null: not stored) and out * sigmoid(gate), when gate is given
     float* gated;
     const AttnPrep* prep;      // or null; when given, q and new_k / new_v are not read
+    // the any-shape kernels (widths outside {64, 128, 256}, key width != value width, or
+    // OQ_ANY_SHAPE=1): D is the key width, Dv the value width (out / gate_s / gated rows of Dv),
+    // chunk / nchunks unused, part holds attention_any_floats(Hkv * rep, T) floats; with a prep,
+    // prep->qcur must be given (the rotated queries the attention reads)
+    bool any;
+    uint32_t Dv;
 };
 constexpr uint64_t kAttnMaxRep = 256;  // query heads per KV head
 bool attention_dims_supported(uint64_t head_dim, uint64_t rep);
+constexpr uint64_t kAttnAnyMaxDim = 8192;  // the any-shape kernels' widest key / head row (LDS)
+uint64_t attention_any_floats(uint64_t q_heads, uint64_t T);
 uint32_t attention_subgroups(uint32_t rep);  // chunk workgroups per (KV head, chunk): rep / subgroups <= 8 heads each
 // token_groups: launches of that many tokens' workgroups share the grid (several tokens per call)
 void attention_plan(uint64_t T, uint64_t Hkv, uint64_t rep, uint32_t& chunk, uint32_t& nchunks,

@@ -211,8 +211,12 @@ def test_deltanet_rejects_bad_shapes(ctx):
     blk = oracle_amd.DeltaNetBlockWeights(ctx, d, w, vec)
     try:
         hb, sb, xb, yb = ctx.to_device(hist), ctx.to_device(st), ctx.to_device(x), ctx.alloc(d["embedding"] * 4)
-        blk.desc.value_dim = 96  # unsupported on the device path
-        with pytest.raises(oracle_amd.InvalidArgument):
+        blk.desc.key_dim = 4097  # wider than the any-shape delta rule's LDS rows
+        with pytest.raises(oracle_amd.InvalidArgument, match="key_dim <= 4096"):
+            ctx.deltanet_step(blk, hb, sb, xb, yb)
+        blk.desc.key_dim = d["key_dim"]
+        blk.desc.value_dim = 96  # the projections no longer match
+        with pytest.raises(oracle_amd.InvalidArgument, match="has shape"):
             ctx.deltanet_step(blk, hb, sb, xb, yb)
         blk.desc.value_dim = d["value_dim"]
         blk.desc.ffn = d["ffn"] + 256  # gate/up/down no longer match
