@@ -466,13 +466,29 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
         }
     }
     // this wave's first value rows go out before the softmax (they do not depend on it): NB groups
-    // of four rows, rotated like the keys
-    VT vb[NB][4];
-    auto load_values = [&](VT (&dst)[4], uint32_t i0) {
+    // of four rows, rotated like the keys.  Over chunks longer than the passes in flight, a binary16
+    // row of 128 or 256 values is loaded 8 values (16 bytes) per lane: D / 8 lanes per row,
+    // TPI = 512 / D of the group's rows per load (lane slot s takes row 4 (v TPI + s) of the group
+    // in load v), the slots' sums added at the end (32768 cached rows: 36.5 -> 31.8 us per step);
+    // other rows one per load, VW values per lane (short chunks measured 0.25 us faster so).
+    constexpr bool kWideV = std::is_same_v<KT, _Float16> && D >= 128 && !ONE;
+    constexpr int TPI = kWideV ? 512 / D : 1;  // rows per value load
+    constexpr int VL = 4 / TPI;                // value loads per group of four rows
+    constexpr int VE = kWideV ? 8 : VW;        // value columns per lane
+    using VLT = std::conditional_t<kWideV, uint4, VT>;
+    const uint32_t vslot = kWideV ? (uint32_t)lane / (uint32_t)(D / 8) : 0u;
+    const uint32_t vcol = kWideV ? ((uint32_t)lane % (uint32_t)(D / 8)) * 8u : (uint32_t)lane * VW;
+    VLT vb[NB][VL];
+    auto load_values = [&](VLT (&dst)[VL], uint32_t i0) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t i = i0 + (uint32_t)u * kAttnWaves;
-            dst[u] = IO::load_v(value_row(c0 + (i < n ? i : n - 1)), lane);
+        for (int v = 0; v < VL; ++v) {
+            const uint32_t i = i0 + ((uint32_t)v * TPI + vslot) * kAttnWaves;
+            const KT* row = value_row(c0 + (i < n ? i : n - 1));
+            if constexpr (kWideV) {
+                dst[v] = load_stream(reinterpret_cast<const uint4*>(row + vcol));
+            } else {
+                dst[v] = IO::load_v(row, lane);
+            }
         }
     };
     constexpr uint32_t kGroup = 4u * kAttnWaves;  // tokens per value group of the workgroup
@@ -502,28 +518,33 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
     __syncthreads();
 
     // ---- weighted values: wave w takes tokens c0 + w, c0 + w + 4, ...
-    float o[REP][VW];
+    float o[REP][VE];
 #pragma unroll
     for (int h = 0; h < REP; ++h)
 #pragma unroll
-        for (int e = 0; e < VW; ++e) o[h][e] = 0.0f;
+        for (int e = 0; e < VE; ++e) o[h][e] = 0.0f;
     auto value_block = [&](uint32_t i0, auto reload) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const uint32_t ib = i0 + (uint32_t)b * kGroup;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t i = ib + (uint32_t)u * kAttnWaves;
+            for (int u = 0; u < VL; ++u) {
+                const uint32_t i = ib + ((uint32_t)u * TPI + vslot) * kAttnWaves;
                 // rows past the chunk are clamped loads with weight 0
                 const uint32_t ic = i < n ? i : n - 1;
-                float v[VW];
-                IO::unpack_v(vb[b][u], v);
+                float v[VE];
+                if constexpr (kWideV) {
+                    HalfVec<4>::unpack(make_uint2(vb[b][u].x, vb[b][u].y), v);
+                    HalfVec<4>::unpack(make_uint2(vb[b][u].z, vb[b][u].w), v + 4);
+                } else {
+                    IO::unpack_v(vb[b][u], v);
+                }
 #pragma unroll
                 for (int h = 0; h < REP; ++h) {
                     if ((uint32_t)h >= rep) break;
                     const float p = i < n ? sc[(uint32_t)h * a.chunk + ic] : 0.0f;
 #pragma unroll
-                    for (int e = 0; e < VW; ++e) o[h][e] += p * v[e];
+                    for (int e = 0; e < VE; ++e) o[h][e] += p * v[e];
                 }
             }
             if constexpr (decltype(reload)::value) load_values(vb[b], ib + NB * kGroup);
@@ -534,13 +555,23 @@ __global__ __launch_bounds__(kAttnThreads) void attention_chunk_kernel(ChunkArgs
         for (; i0 + NB * kGroup < n; i0 += NB * kGroup) value_block(i0, std::true_type{});
     }
     if (i0 < n) value_block(i0, std::false_type{});
+    if constexpr (kWideV) {
+        // the slots' sums of each column, added across the lanes D / 8 apart
+#pragma unroll
+        for (int h = 0; h < REP; ++h)
+#pragma unroll
+            for (int e = 0; e < VE; ++e)
+#pragma unroll
+                for (int off = D / 8; off < 64; off <<= 1) o[h][e] += __shfl_xor(o[h][e], off, 64);
+    }
     __syncthreads();  // the probabilities are no longer read: reuse the LDS for the wave sums
     float* red = lds;  // [wave][rep][D]
 #pragma unroll
     for (int h = 0; h < REP; ++h) {
         if ((uint32_t)h >= rep) break;
+        if (vslot != 0) break;
 #pragma unroll
-        for (int e = 0; e < VW; ++e) red[((uint32_t)wave * rep + (uint32_t)h) * D + (uint32_t)lane * VW + e] = o[h][e];
+        for (int e = 0; e < VE; ++e) red[((uint32_t)wave * rep + (uint32_t)h) * D + vcol + e] = o[h][e];
     }
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < rep * (uint32_t)D; i += kAttnThreads) {
