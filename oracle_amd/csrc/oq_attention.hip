@@ -749,16 +749,24 @@ __global__ __launch_bounds__(64) void attention_prep_tokens_kernel(TokPrepArgs a
 
 // ---------------------------------------------------------------- RoPE
 
-OQ_DEVICE void rope_pair(float* x, uint32_t f, uint32_t half, const RopeParams& p) {
-    float c, s;
-    rope_cs(f, p, c, s);
-    rotate_pair(x, f, half, c, s);
+// frequency f's cos / sin: from the host's table when it has one, else computed here
+OQ_DEVICE void rope_cs_at(uint32_t f, const RopeParams& p, const RopeTable& t, float& c, float& s) {
+    if (t.pairs != 0) {
+        c = t.cs[0][f];
+        s = t.cs[1][f];
+    } else {
+        rope_cs(f, p, c, s);
+    }
 }
 
-__global__ __launch_bounds__(256) void rope_kernel(float* heads, uint32_t head_dim, RopeParams p) {
+__global__ __launch_bounds__(256) void rope_kernel(float* heads, uint32_t head_dim, RopeParams p, RopeTable t) {
     float* x = heads + (uint64_t)blockIdx.x * head_dim;
     const uint32_t half = p.rotary_dim / 2;
-    for (uint32_t f = threadIdx.x; f < half; f += blockDim.x) rope_pair(x, f, half, p);
+    for (uint32_t f = threadIdx.x; f < half; f += blockDim.x) {
+        float c, s;
+        rope_cs_at(f, p, t, c, s);
+        rotate_pair(x, f, half, c, s);
+    }
 }
 
 template <typename KT, int D, int REP, int NB, bool ONE>
@@ -992,7 +1000,7 @@ __global__ __launch_bounds__(256) void attention_prep_any_kernel(AttnPrep p, uin
     const uint32_t half = p.rope.rotary_dim / 2;
     for (uint32_t f = threadIdx.x; f < half; f += 256) {
         float c, sn;
-        rope_cs(f, p.rope, c, sn);
+        rope_cs_at(f, p.rope, p.table, c, sn);
         rotate_pair(xrow, f, half, c, sn);
     }
     __syncthreads();
@@ -1182,10 +1190,11 @@ hipError_t launch_attention(const AttnLaunch& L, hipStream_t s) {
     }
 }
 
-hipError_t launch_rope(float* heads, uint64_t n_heads, uint64_t head_dim, const RopeParams& p, hipStream_t s) {
+hipError_t launch_rope(float* heads, uint64_t n_heads, uint64_t head_dim, const RopeParams& p, const RopeTable& t,
+                       hipStream_t s) {
     if (n_heads == 0) return hipSuccess;
     hipLaunchKernelGGL(rope_kernel, dim3((unsigned)n_heads), dim3(std::min<uint32_t>(256u, std::max(64u, p.rotary_dim / 2))),
-                       0, s, heads, (uint32_t)head_dim, p);
+                       0, s, heads, (uint32_t)head_dim, p, t);
     return hipGetLastError();
 }
 

@@ -226,6 +226,17 @@ struct RopeParams {
     float base;
     uint64_t pos[3];  // temporal, height, width
 };
+// cos and sin of each frequency's angle at one position, computed on the host exactly as
+// apply_qwen35_rope does (reference_kernels.cpp:105-115: double pow, cos and sin of the host's
+// libm, rounded to F32), so a single-position rotation uses the reference's own values; pairs = 0
+// when absent (rotary_dim / 2 above kRopeTablePairs, or positions that differ per token): then the
+// device computes them in double (rope_cs)
+constexpr uint32_t kRopeTablePairs = 128;
+struct RopeTable {
+    uint32_t pairs;
+    float cs[2][kRopeTablePairs];
+};
+void rope_table(const RopeParams& p, RopeTable& t);
 // The decoder block's per-head preparation (qwen35_block.cpp:671-711), done by the attention
 // chunk kernel: RMSNorm of the query heads (q_norm) and of the new key (k_norm), rotation, the
 // append of the new key and value rows, and the trace's copies qcur / kcur.
@@ -234,6 +245,7 @@ struct AttnPrep {
     const float *q_norm, *k_norm;
     float eps;
     RopeParams rope;
+    RopeTable table;              // the any-shape preparation's cos / sin at rope.pos (pairs = 0: computed on the device)
     float *qcur, *kcur;           // [Hq][D], [Hkv][D], or null (not stored)
     bool v_stored;                // an F16 cache's new value row already stored (by the projection)
 };
@@ -294,7 +306,8 @@ struct AttnTokens {
 constexpr uint32_t kInlineTokenPositions = 32;
 hipError_t launch_attention_tokens(const AttnLaunch& L, const AttnTokens& tk, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* src, void* dst, uint64_t n, hipStream_t s);  // round to nearest even
-hipError_t launch_rope(float* heads, uint64_t n_heads, uint64_t head_dim, const RopeParams& p, hipStream_t s);
+hipError_t launch_rope(float* heads, uint64_t n_heads, uint64_t head_dim, const RopeParams& p, const RopeTable& t,
+                       hipStream_t s);
 
 // ---- oq_gemv_block.hip  (fused m = 1 GEMV of the DeltaNet decode block; see the kernel comment)
 enum : int { kBlockIn = 0, kBlockAdd = 1, kBlockFfn = 2 };

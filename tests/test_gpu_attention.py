@@ -76,6 +76,9 @@ def rope_close(got, want, x, half):
 
 
 def test_rope_matches_reference_fixture(ctx, attn_golden):
+    """Bit for bit: a single-position rotation of up to 128 frequency pairs takes its cos / sin
+    from the host, computed as apply_qwen35_rope computes them (reference_kernels.cpp:105-115),
+    and rotates in the reference's F32 operations."""
     g = attn_golden
     x = g["rope_in"]
     buf = ctx.alloc(x.nbytes)
@@ -84,8 +87,7 @@ def test_rope_matches_reference_fixture(ctx, attn_golden):
             buf.upload(x)
             ctx.rope(buf, x.shape[0], x.shape[1], 64, [11, 11, 10, 0], 1e7, tuple(int(v) for v in g[f"rope_{name}_pos"]))
             got = buf.download(np.float32, x.size).reshape(x.shape)
-            exact = rope_close(got, g[f"rope_{name}_bits"].view(np.float32), x, 32)
-            assert exact >= 0.99, f"{name}: only {exact:.4f} of the elements bit-exact"
+            assert np.array_equal(got.view(np.uint32), g[f"rope_{name}_bits"]), name
     finally:
         buf.free()
 
@@ -101,15 +103,21 @@ def test_rope_known_answers_and_sizes(ctx, kat):
         want = oracle.rope(x, spec["rotary_dim"], spec["sections"], spec["base"], spec["position"])[0]
         assert np.allclose(got, want, atol=spec["tol"], rtol=0)
     rng = np.random.default_rng(3)
+    # up to 128 frequency pairs: the host's table, bit-exact; 256 pairs (rotary dimension 512): the
+    # device's double-precision angles, within 2^-21 of the pair (>= 99 % bit-exact)
     for n, hd, rd, sec in ((3, 128, 128, [22, 21, 21, 0]), (40, 256, 64, [11, 11, 10, 0]), (1, 2, 2, [1, 0, 0, 0]),
-                           (7, 96, 48, [8, 8, 8, 0])):
+                           (7, 96, 48, [8, 8, 8, 0]), (2, 512, 512, [86, 85, 85, 0])):
         x = rng.standard_normal((n, hd)).astype(np.float32)
         pos = (int(rng.integers(0, 300000)), int(rng.integers(0, 64)), int(rng.integers(0, 64)))
         buf = ctx.to_device(x)
         ctx.rope(buf, n, hd, rd, sec, 1e6, pos)
         got = buf.download(np.float32, x.size).reshape(x.shape)
         buf.free()
-        rope_close(got, oracle.rope(x, rd, sec, 1e6, pos), x, rd // 2)
+        want = oracle.rope(x, rd, sec, 1e6, pos)
+        if rd // 2 <= 128:
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, hd, rd)
+        else:
+            assert rope_close(got, want, x, rd // 2) >= 0.99
 
 
 def test_rope_errors(ctx):
