@@ -178,11 +178,12 @@ def run_gpu(ctx, name, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, graph=
     return res
 
 
-def run_deltanet(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, tokens=1):
+def run_deltanet(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, tokens=1, graph=False):
     """One Gated DeltaNet decode block (hidden 4096, 32 heads of dk = dv = 128, FFN 12288) per
     step, chained on the device (oq_deltanet_step; with tokens > 1, oq_deltanet_steps over that
     many consecutive tokens); steps cycle over block copies whose weights total >= 512 MiB, so every
-    step streams its projections from HBM."""
+    step streams its projections from HBM.  graph: the K steps captured into one HIP graph and
+    timed as one launch (timed_graph), as a decode loop replaying captured blocks runs them."""
     rng = np.random.default_rng(SEED + 100)
     d, w, vec, hist, st, x = synth.deltanet_block(rng)
     if tokens > 1:
@@ -206,7 +207,7 @@ def run_deltanet(ctx, steps, warmup, copies_min_bytes=MALL_DEFEAT_BYTES, tokens=
 
     step(0)  # checked call; sizes the block workspace
     ctx.sync()
-    ms = timed_steps(ctx, step, steps, warmup, first=1)
+    ms = timed_graph(ctx, step, steps, warmup, 1, wb) if graph else timed_steps(ctx, step, steps, warmup, first=1)
     for b in blocks:
         b.release()
     for buf in (hb, sb, xb, yb):
@@ -424,7 +425,7 @@ def main():
         ctx.close()
         return
     if args.workload == "deltanet_block":
-        r = run_deltanet(ctx, args.steps, args.warmup, tokens=args.tokens)
+        r = run_deltanet(ctx, args.steps, args.warmup, tokens=args.tokens, graph=args.graph)
         ctx.close()
         print(json.dumps({
             "metric": "DeltaNet decode block weight GB/s", "value": round(r["weight_gbs"], 2), "unit": "GB/s",
@@ -433,7 +434,8 @@ def main():
             "data": "synthetic (seeded block weights, state ~ N(0, 0.01), x ~ N(0,1))",
             "config": {"workload": "Gated DeltaNet decode block, batch 1" if r["tokens"] == 1 else
                        f"Gated DeltaNet block, {r['tokens']} consecutive tokens per step (oq_deltanet_steps)", **r["dims"],
-                       "weight_bytes": r["weight_bytes"], "block_copies_cycled": r["copies"]},
+                       "weight_bytes": r["weight_bytes"], "block_copies_cycled": r["copies"],
+                       "launch": "one HIP graph of the timed steps" if args.graph else "eager C-ABI calls"},
             "us_per_block": round(r["us_per_block"], 2), "tokens": r["tokens"], "us_per_token": round(r["us_per_token"], 2),
             "hbm_frac_weight_bytes": round(r["weight_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
         return
