@@ -203,8 +203,10 @@ def f16(a):
     return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
 
 
+# long chunks of rows of 128 and 256 load several value rows per instruction (4 and 2): 65537 and
+# 4097 rows over 4 KV heads, 20000 over 2 and 30001 over one (16 query heads: two subgroups)
 F16_CASES = [(8, 2, 256, 1), (16, 4, 256, 4097), (8, 1, 128, 777), (4, 4, 64, 300), (6, 2, 128, 301),
-             (32, 2, 256, 4097), (16, 4, 256, 65537)]
+             (32, 2, 256, 4097), (16, 4, 256, 65537), (8, 2, 128, 20000), (16, 1, 128, 30001)]
 
 
 @pytest.mark.parametrize("hq,hkv,d,T", F16_CASES, ids=[f"h{a}_{b}_d{c}_T{t}" for a, b, c, t in F16_CASES])

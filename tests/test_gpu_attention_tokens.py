@@ -22,9 +22,16 @@ from test_gpu_attention import BLOCKS, CHAIN_TOL, THREADS, check_block_stages, f
 pytestmark = pytest.mark.gpu
 
 
+# heads of 128 over 12000 cached rows: long chunks (an F16 cache's value rows four per load), and
+# from 8192 rows several tokens per chunk workgroup
+LONG = {"long128": (dict(embedding=512, q_heads=8, kv_heads=2, head_dim=128, ffn=512, rope_dim=64,
+                         rope_sections=[11, 11, 10, 0], rope_base=1e6, eps=1e-6),
+                    dict(q=12, k=12, v=12, out=12, gate=12, up=12, down=12), 12000)}
+
+
 def inputs(name, m, seed):
     from golden.make_golden import attention_inputs
-    d, types, cached = BLOCKS[name]
+    d, types, cached = BLOCKS[name] if name in BLOCKS else LONG[name]
     w, vec, c, _ = attention_inputs(np.random.default_rng(seed), d, types, cached=cached)
     cache = oracle.KvCache(cached + m, d["kv_heads"], d["head_dim"], d["head_dim"])
     cache.keys[:cached] = c.keys[:cached]
@@ -119,10 +126,12 @@ DOMINATED_TOL = 1.5e-3
 
 
 @pytest.mark.parametrize("env", SHARE, ids=["default", "shared_rows"])
-def test_block_tokens_f16_cache(ctx, env):
+@pytest.mark.parametrize("name", ["e2048", "long128"])
+def test_block_tokens_f16_cache(ctx, env, name):
     """m tokens over an F16 cache: each token's stages, its key and value appended rounded, and
-    every later token attending over the rounded rows."""
-    d, w, vec, c, xs, positions = inputs("e2048", 4, 9500)
+    every later token attending over the rounded rows (e2048: heads of 256 over 1000 cached rows,
+    with OQ_ATTN_SHARE_MIN=0 several tokens per workgroup; long128: heads of 128 over 12000)."""
+    d, w, vec, c, xs, positions = inputs(name, 4, 9500)
     n0 = c.length
     with oracle_amd.launch_options(env):
         y, traces, keys, values, length = run_tokens(ctx, d, w, vec, c, positions, xs, dtype="f16")
