@@ -31,6 +31,8 @@ case "$WL" in
     attention_decode_f16) BWL="attention_decode --kv f16" ;;
     attention_block_4_tokens) BWL="attention_block --tokens 4" ;;
     deltanet_block_4_tokens) BWL="deltanet_block --tokens 4" ;;
+    attention_block_2_tokens) BWL="attention_block --tokens 2" ;;
+    deltanet_block_2_tokens) BWL="deltanet_block --tokens 2" ;;
 esac
 
 # the headline workload is traced in the shape the default run times it (20 steps after 5 warmup
