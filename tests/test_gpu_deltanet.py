@@ -130,7 +130,8 @@ SMALL = dict(synth.DELTANET_DIMS, embedding=1024, key_heads=2, value_heads=4, ff
     dict(SMALL, value_dim=256, value_heads=2, key_heads=1),
     dict(SMALL, key_dim=32, value_dim=192, value_heads=4, key_heads=4, conv_kernel=2),
     dict(SMALL, ffn=17408),
-], ids=["hk2_hv4", "dk64_dv64_k3", "dv256", "dk32_dv192_k2", "ffn17408"])
+    dict(SMALL, conv_kernel=8),
+], ids=["hk2_hv4", "dk64_dv64_k3", "dv256", "dk32_dv192_k2", "ffn17408", "k8"])
 @pytest.mark.parametrize("env", [{"OQ_BLOCK_FUSED": "1"}, {"OQ_BLOCK_FUSED": "1", "OQ_BLOCK_STREAM": "0"},
                                  {"OQ_BLOCK_FUSED": "0"}], ids=["fused", "fused_batched", "separate"])
 def test_deltanet_steps_match_oracle(ctx, dims, env):
