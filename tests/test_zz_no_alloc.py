@@ -54,6 +54,11 @@ def test_noalloc_matches_step_two_calls(ctx):
     step_both(ctx, SMALL, 72)
 
 
+def test_noalloc_matches_step_any_shape(ctx):
+    # key heads of 16 and value heads of 32: the per-stage launches with the any-shape delta rule
+    step_both(ctx, dict(SMALL, key_dim=16, value_dim=32, value_heads=8, conv_kernel=3), 74)
+
+
 def test_noalloc_rejects_block_beyond_capacity(ctx):
     cap = int(ctx.lib.oq_deltanet_noalloc_capacity())
     assert cap == 4 << 20
