@@ -66,8 +66,9 @@ def timed_steps(ctx, step, steps, warmup, first=0):
     Steps are launched eagerly through the C ABI (about 3 us of host time per launch, less than
     a step, so the GPU never waits for the host).  After a host synchronization the W warmup
     steps are launched and, right behind them on the same stream, the HIP event pair around the
-    K timed steps: the events measure the K steps back to back.  A host synchronization closes
-    the timed region.  (HIP graphs were measured too: a graph's first launch adds ~15-20 us of
+    K timed steps: the events measure the K steps back to back (they are recorded without a
+    system-scope fence, so no cache write-back of the event itself falls inside the interval).
+    A host synchronization closes the timed region.  (HIP graphs were measured too: a graph's first launch adds ~15-20 us of
     host set-up that the GPU waits for, 0.7-1 us per step at K = 20.)
 
     Step indices run on from the warmup into the timed steps (first, first + 1, ...), so with

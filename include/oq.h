@@ -425,9 +425,12 @@ uint64_t oq_deltanet_noalloc_capacity(void);
 
 /* ------------------------------------------------------------------ timing / graphs */
 
-/* HIP events on the context's stream, for timing the kernels launched there. */
+/* HIP events on the context's stream, for timing the kernels launched there.  They are recorded
+   without a system-scope fence (hipEventDisableSystemFence: no cache write-back inside the timed
+   interval); oq_timer_stop then synchronizes the stream, so the timed work is complete and visible
+   to the host when it returns. */
 int oq_timer_start(oq_context* ctx);
-int oq_timer_stop(oq_context* ctx, float* elapsed_ms); /* waits for the stop event */
+int oq_timer_stop(oq_context* ctx, float* elapsed_ms); /* waits for the stop event and the stream */
 
 /* Capture every oq_* launch on ctx between begin and end into a replayable HIP graph.  Run each
    captured call once eagerly first: a call that would have to grow the context's workspace

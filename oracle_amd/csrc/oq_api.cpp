@@ -848,8 +848,8 @@ int oq_context_create(int device, oq_context** out) {
     oq_context* ctx = new oq_context;
     ctx->device = device;
     e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipEventCreate(&ctx->t0);
-    if (e == hipSuccess) e = hipEventCreate(&ctx->t1);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->t0, hipEventDisableSystemFence);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->t1, hipEventDisableSystemFence);
     if (e == hipSuccess) e = hipMalloc(&ctx->argmax_parts, oq::kArgmaxParts * sizeof(oq::ArgmaxPart));
     if (e != hipSuccess) {
         const int rc = hip_fail(nullptr, e, "context creation");
@@ -1097,6 +1097,7 @@ int oq_timer_stop(oq_context* ctx, float* ms) {
     OQ_HIP(ctx, hipEventRecord(ctx->t1, ctx->stream), "hipEventRecord");
     OQ_HIP(ctx, hipEventSynchronize(ctx->t1), "hipEventSynchronize");
     OQ_HIP(ctx, hipEventElapsedTime(ms, ctx->t0, ctx->t1), "hipEventElapsedTime");
+    OQ_HIP(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     return OQ_OK;
 }
 
