@@ -583,7 +583,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_stream_kernel(DeviceMatrix w,
             // The wave whose data has arrived requests its next unit ahead of the other waves'
             // arithmetic on the SIMD: raised priority from the wait until those loads are issued
             // (the same bits; 12288 x 4096 6.95 -> 6.86 us, the 151936 x 4096 head 82.8 -> 80.8 us;
-            // in the small-batch and block kernels no faster or slower, so not there).
+            // slower in the small-batch kernels and no faster in the block kernels, so not there).
             __builtin_amdgcn_s_setprio(2);
             uint32_t nrow = row, nit = it + 1;
             if (nit == ITERS) {
